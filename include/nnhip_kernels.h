@@ -1,0 +1,138 @@
+/* nnhip_kernels.h — C-ABI of the gfx950 kernel library (libnnhip.so).
+ *
+ * Plays the role of the reference's CUDA kernel ABI
+ * (/root/reference/cuda/cuda_kernels.h:15-169): flat extern "C" entry points,
+ * plain device pointers and sizes, op codes as unsigned, scalars as float, a
+ * HIP stream as void* (NULL = default stream), return 0 on success or a
+ * hipError_t / negative status. Entry points marked "no CUDA counterpart"
+ * cover primitives the CUDA engine leaves unimplemented
+ * (/root/reference/include/neuralnet.cpp/cuda_engine.hpp:212-260,461-469);
+ * their semantics are those of the CPU engine at the cited lines of
+ * /root/reference/include/neuralnet.cpp/cpu_engine.hpp.
+ *
+ * All tensors are row-major float32 in device memory. Index tensors hold
+ * integers as floats (exact up to 2^24). Nothing here allocates device
+ * memory: entry points that need scratch take a workspace pointer whose size
+ * comes from the matching *_workspace_bytes function.
+ */
+#ifndef NNHIP_KERNELS_H
+#define NNHIP_KERNELS_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ── GEMM (fp32 MFMA) ────────────────────────────────────────────────────
+ * C (M,N) = alpha * op(A) op(B); A stored (A_rows, A_cols), B stored (B_rows, B_cols).
+ * Replaces cuda_matmul / cuda_matmul_with_handle (cuda_kernels.h:24-43). */
+int nnhip_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
+                 size_t B_cols, int transA, int transB, void* stream);
+
+/* Per batch b: C_b = alpha * op(A_b) op(B_b); A/B split into `batch` row blocks, C stacked (batch*M, N).
+ * Replaces cuda_batched_matmul (cuda_kernels.h:49-54); alpha as in ComputeEngine::batched_matmul
+ * (compute_engine.hpp:195-199, cpu_engine.hpp:335-419). */
+int nnhip_batched_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
+                         size_t B_cols, size_t batch, int transA, int transB, float alpha, void* stream);
+
+/* ── elementwise (cuda_kernels.h:60-92) ──────────────────────────────────── */
+int nnhip_elementwise_unary(const float* A, float* out, size_t count, unsigned op, void* stream);
+int nnhip_elementwise_binary(const float* A, const float* B, float* out, size_t count, unsigned op, void* stream);
+int nnhip_elementwise_binary_scalar(const float* A, float* out, size_t count, unsigned op, float scalar,
+                                    int scalar_first, void* stream);
+/* out = A + scalar * B (cuda_axpy, cuda_kernels.h:83-86). */
+int nnhip_axpy(const float* A, const float* B, float* out, size_t count, float scalar, void* stream);
+int nnhip_elementwise_select_scalar_cond(const float* A, const float* then_v, float* out, size_t count,
+                                         unsigned cmp, float scalar_b, float scalar_else, void* stream);
+/* out[i] = value (used for ComputeEngine::zero; no CUDA counterpart, CUDA uses cudaMemset). */
+int nnhip_fill(float* out, size_t count, float value, void* stream);
+
+/* ── reductions (cuda_kernels.h:98-109); mode 0 = sum, 1 = max (init lowest()) ── */
+int nnhip_reduce_row(const float* A, float* out, size_t rows, size_t cols, unsigned mode, void* stream);
+/* Column reduction over row chunks combined in chunk order; workspace from nnhip_reduce_col_workspace_bytes. */
+size_t nnhip_reduce_col_workspace_bytes(size_t rows, size_t cols);
+int nnhip_reduce_col(const float* A, float* out, size_t rows, size_t cols, unsigned mode, void* workspace,
+                     void* stream);
+
+/* ── broadcast (cuda_kernels.h:115-125) ───────────────────────────────────── */
+int nnhip_broadcast_row(const float* A, const float* vec, float* out, size_t rows, size_t cols, unsigned op,
+                        void* stream);
+int nnhip_broadcast_col(const float* A, const float* vec, float* out, size_t rows, size_t cols, unsigned op,
+                        void* stream);
+
+/* ── layout (cuda_kernels.h:131-143) ──────────────────────────────────────── */
+int nnhip_transpose(const float* A, float* out, size_t R, size_t C, void* stream);
+int nnhip_rearrange_3d(const float* A, float* out, size_t M, size_t B, size_t N, unsigned inverse, void* stream);
+
+/* ── gather / scatter (cuda_kernels.h:151-163) ───────────────────────────
+ * gather: out[i] = table[idx[i]] or a zero row when idx[i] is out of range (cpu_engine.hpp:125-179).
+ * scatter_add: dst[idx[i]] += grad[i] in increasing i per destination row, bit-identical to the
+ * CPU engine's serial loop (cpu_engine.hpp:184-216); the CUDA version uses unordered atomics. */
+int nnhip_gather(const float* table, const float* indices, float* out, size_t vocab, size_t D, size_t num,
+                 void* stream);
+size_t nnhip_scatter_add_workspace_bytes(size_t num);
+int nnhip_scatter_add(float* dst, const float* indices, const float* grad, size_t vocab, size_t D, size_t num,
+                      void* workspace, void* stream);
+
+/* ── fused attention primitives (no CUDA counterpart) ────────────────────
+ * Shapes as ComputeEngine (compute_engine.hpp:217-276): per batch A_b is (M,K), or stored (K,M) when
+ * transA; B_b is (K,N), or stored (N,K) when transB; mask (M,N) shared by all batches (-inf excludes,
+ * finite values add) or NULL. */
+/* cpu_engine.hpp:426-532: out[b*M+i] = reduce_j(alpha*dot + mask) (reduce_cols), or out[b*N+j] over i. */
+int nnhip_bmm_reduce(const float* A, const float* B, const float* mask, float* out, size_t batch, size_t M,
+                     size_t N, size_t K, int transA, int transB, unsigned op, float alpha, int reduce_cols,
+                     void* stream);
+/* cpu_engine.hpp:535-604: l[b*M+i] = sum_j exp(alpha*dot + mask - row_max[b*M+i]). */
+int nnhip_bmm_softmax_denom(const float* A, const float* B, const float* row_max, const float* mask, float* out,
+                            size_t batch, size_t M, size_t N, size_t K, int transA, int transB, float alpha,
+                            void* stream);
+/* cpu_engine.hpp:607-699: O[(b*M+i)*D+k] = sum_j W_ij V[(b*N+j)*D+k]. */
+int nnhip_bmm_softmax_apply(const float* A, const float* B, const float* V, const float* row_max,
+                            const float* denom, const float* mask, float* out, size_t batch, size_t M, size_t N,
+                            size_t K, size_t D, int transA, int transB, float alpha, void* stream);
+/* cpu_engine.hpp:702-801: R[b*M+i] = sum_j W P; dQ[(b*K+k)*M+i] = alpha sum_j W (P-R) B_b[k][j]. */
+int nnhip_bmm_softmax_backward_q(const float* A, const float* B, const float* P, const float* row_max,
+                                 const float* denom, const float* mask, float* dQ, float* R, size_t batch,
+                                 size_t M, size_t N, size_t K, int transA, int transB, float alpha, void* stream);
+/* cpu_engine.hpp:804-915: dK[(b*K+k)*N+j] = alpha sum_i W (P-R) A_b[:,i]_k; dV = sum_i W G[b*M+i][k]
+ * (G has D >= K columns). */
+int nnhip_bmm_softmax_backward_kv(const float* A, const float* B, const float* P, const float* G, const float* R,
+                                  const float* row_max, const float* denom, const float* mask, float* dK,
+                                  float* dV, size_t batch, size_t M, size_t N, size_t K, size_t D, int transA,
+                                  int transB, float alpha, void* stream);
+
+/* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
+ * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */
+size_t nnhip_col_softmax_workspace_bytes(size_t C, size_t N);
+int nnhip_col_softmax_denom(const float* logits, const float* col_max, float* out, size_t C, size_t N,
+                            void* workspace, void* stream);
+int nnhip_col_softmax_sparse_forward(const float* logits, const float* labels, const float* mask, float* grad,
+                                     float* loss_vec, size_t C, size_t N, size_t vocab_size, float inv_num_valid,
+                                     void* workspace, void* stream);
+
+/* ── row softmax (eval_expr fast path of the Softmax layer, compute_layer.hpp:832-862) ──
+ * forward: out = exp(x - rowmax) / sum(exp(x - rowmax)); backward: dx = y * (g - sum(y*g)). */
+int nnhip_row_softmax(const float* X, float* out, size_t rows, size_t cols, void* stream);
+int nnhip_row_softmax_backward(const float* Y, const float* G, float* out, size_t rows, size_t cols, void* stream);
+
+/* ── ExprSpec interpreter (no CUDA counterpart; cpu_engine.hpp:1298-1659) ──
+ * The program is the ExprSpec in serialised form (see nnhip_engine.h); inputs[k] are device pointers
+ * shaped per view. Workspace from nnhip_eval_expr_workspace_bytes. */
+typedef struct nnhip_expr_program {
+    unsigned char instrs[64][8]; /* {op, dst, a.kind, a.idx, b.kind, b.idx, c.kind, c.idx} */
+    unsigned char view_kind[8];
+    unsigned char view_negate[8];
+    unsigned int view_param[8];
+    float consts[16];
+    unsigned int n_instrs, n_views, n_consts, num_regs;
+} nnhip_expr_program;
+size_t nnhip_eval_expr_workspace_bytes(const nnhip_expr_program* prog, size_t rows, size_t cols);
+int nnhip_eval_expr(const nnhip_expr_program* prog, const float* const* inputs, float* out, size_t rows,
+                    size_t cols, int vector_out, void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NNHIP_KERNELS_H */

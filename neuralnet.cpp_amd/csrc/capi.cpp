@@ -1,0 +1,42 @@
+// capi.cpp — the engine C-ABI (include/nnhip_engine.h) over HipEngine.
+#include "nn/engine_capi.hpp"
+#include "nn/hip_engine.hpp"
+
+namespace
+{
+std::unique_ptr<nn::ComputeEngine> make_hip_engine(std::string& err)
+{
+    auto e = std::make_unique<nn::HipEngine>();
+    if (!e->ok())
+    {
+        err = e->error();
+        return nullptr;
+    }
+    return e;
+}
+} // namespace
+
+NN_DEFINE_ENGINE_CAPI(nnhip_, make_hip_engine(err))
+
+// Measurement hooks (no reference counterpart): GEMM kernel time by HIP events.
+extern "C" int nnhip_engine_profile_gemm(void* e, int enable)
+{
+    auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
+    if (!h) return nn::capi::set_error("profile: not a HIP engine");
+    h->set_gemm_profile(enable != 0);
+    return 0;
+}
+
+extern "C" int nnhip_engine_profile_gemm_read(void* e, double* launches, double* flops, double* ms)
+{
+    auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
+    if (!h) return nn::capi::set_error("profile: not a HIP engine");
+    auto r = h->read_gemm_profile(*launches, *flops, *ms);
+    return r ? 0 : nn::capi::set_error(r.error().message);
+}
+
+extern "C" void* nnhip_engine_stream(void* e)
+{
+    auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
+    return h ? h->stream() : nullptr;
+}

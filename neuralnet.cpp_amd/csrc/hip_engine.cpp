@@ -1,0 +1,818 @@
+// hip_engine.cpp — HipEngine: ComputeEngine primitives over the gfx950 kernel library.
+//
+// Each method mirrors the CPU engine's validation (cpu_engine.hpp, lines cited
+// per method) and then enqueues the matching nnhip_* kernel on the engine's
+// stream. The primitive semantics live in the kernels (include/nnhip_kernels.h).
+#include "nn/hip_engine.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <limits>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "nn/expr_dsl.hpp"
+#include "nnhip_kernels.h"
+
+namespace nn
+{
+
+// ── stream-ordered caching pool ────────────────────────────────────────────
+// Blocks are rounded to size classes (powers of two up to 64 MiB, then 16 MiB
+// multiples) and recycled by exact class. Every user of a pool enqueues on the
+// same stream, so a block returned here may be handed out again right away:
+// the kernels that read the old contents run before the ones that write it.
+class DevicePool
+{
+public:
+    explicit DevicePool(int device) : device_(device) {}
+    ~DevicePool() { trim(); }
+
+    static std::size_t round(std::size_t bytes)
+    {
+        if (bytes <= 256) return 256;
+        constexpr std::size_t big = std::size_t{64} << 20, step = std::size_t{16} << 20;
+        if (bytes >= big) return (bytes + step - 1) / step * step;
+        std::size_t p = 256;
+        while (p < bytes) p <<= 1;
+        return p;
+    }
+
+    void* alloc(std::size_t bytes, std::size_t& rounded)
+    {
+        rounded = round(bytes);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            auto it = free_.find(rounded);
+            if (it != free_.end() && !it->second.empty())
+            {
+                void* p = it->second.back();
+                it->second.pop_back();
+                cached_ -= rounded;
+                live_ += rounded;
+                return p;
+            }
+        }
+        void* p = nullptr;
+        (void)hipSetDevice(device_);
+        if (hipMalloc(&p, rounded) != hipSuccess)
+        {
+            (void)hipGetLastError();
+            (void)hipDeviceSynchronize();
+            trim();
+            if (hipMalloc(&p, rounded) != hipSuccess)
+            {
+                (void)hipGetLastError();
+                return nullptr;
+            }
+        }
+        std::lock_guard<std::mutex> lk(mu_);
+        live_ += rounded;
+        return p;
+    }
+
+    void release(void* p, std::size_t rounded)
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        free_[rounded].push_back(p);
+        live_ -= rounded;
+        cached_ += rounded;
+    }
+
+    void trim()
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        for (auto& [sz, v] : free_)
+            for (void* p : v) (void)hipFree(p);
+        free_.clear();
+        cached_ = 0;
+    }
+
+    std::size_t cached() const
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        return cached_;
+    }
+    std::size_t live() const
+    {
+        std::lock_guard<std::mutex> lk(mu_);
+        return live_;
+    }
+
+private:
+    int device_;
+    mutable std::mutex mu_;
+    std::map<std::size_t, std::vector<void*>> free_;
+    std::size_t cached_ = 0, live_ = 0;
+};
+
+namespace
+{
+
+class HipBuffer final : public DeviceBuffer
+{
+public:
+    HipBuffer(std::shared_ptr<DevicePool> pool, float* p, std::size_t floats, std::size_t rounded)
+        : pool_(std::move(pool)), p_(p), floats_(floats), rounded_(rounded)
+    {
+    }
+    ~HipBuffer() override
+    {
+        if (p_) pool_->release(p_, rounded_);
+    }
+    float* data() noexcept override { return p_; }
+    std::size_t capacity() const noexcept override { return floats_; }
+
+private:
+    std::shared_ptr<DevicePool> pool_;
+    float* p_;
+    std::size_t floats_, rounded_;
+};
+
+const float* D(const Tensor& t) { return t.dev_ptr(); }
+float* W(Tensor& t) { return t.dev_ptr(); }
+
+struct BDims
+{
+    std::size_t M, K, N;
+};
+Result<BDims> bdims(const Tensor& A, const Tensor& B, std::size_t batch, bool tA, bool tB, const char* who)
+{
+    if (batch == 0) return fail(std::string(who) + ": batch must be > 0");
+    if (A.rows() % batch != 0 || B.rows() % batch != 0) return fail(std::string(who) + ": rows not divisible by batch");
+    const std::size_t ar = A.rows() / batch, br = B.rows() / batch;
+    BDims d{tA ? A.cols() : ar, tA ? ar : A.cols(), tB ? br : B.cols()};
+    if (d.K != (tB ? B.cols() : br)) return fail(std::string(who) + ": K dimension mismatch");
+    return d;
+}
+Result<void> mask_ok(const Tensor* mask, std::size_t M, std::size_t N, const char* who)
+{
+    if (mask && (mask->rows() != M || mask->cols() != N)) return fail(std::string(who) + ": mask shape mismatch");
+    return {};
+}
+Result<void> vec_ok(const Tensor& t, std::size_t rows, const char* who, const char* what)
+{
+    if (t.rows() != rows || t.cols() != 1) return fail(std::string(who) + ": " + what + " shape mismatch");
+    return {};
+}
+
+// Canonical Softmax::forward / ::backward programs (compute_layer.hpp:832-862),
+// built with the same DSL the layer uses, for structural comparison.
+const ExprSpec& softmax_fwd_spec()
+{
+    static const ExprSpec s = [] {
+        Tensor t = Tensor::cpu(1, 1);
+        return dsl::to_expr_spec(dsl::exp(dsl::leaf(t) - dsl::row_reduce_max(t)) /
+                                 dsl::row_reduce_sum(dsl::exp(dsl::leaf(t) - dsl::row_reduce_max(t))))
+            .first;
+    }();
+    return s;
+}
+const ExprSpec& softmax_bwd_spec()
+{
+    static const ExprSpec s = [] {
+        Tensor t = Tensor::cpu(1, 1);
+        return dsl::to_expr_spec(dsl::leaf(t) * (dsl::leaf(t) - dsl::row_reduce_sum(dsl::leaf(t) * dsl::leaf(t))))
+            .first;
+    }();
+    return s;
+}
+
+} // namespace
+
+HipEngine::HipEngine()
+{
+    if (hipGetDevice(&device_) != hipSuccess)
+    {
+        init_error_ = "HipEngine: no HIP device";
+        (void)hipGetLastError();
+        return;
+    }
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess)
+    {
+        init_error_ = "HipEngine: hipStreamCreate failed";
+        (void)hipGetLastError();
+        return;
+    }
+    stream_ = s;
+    pool_ = std::make_shared<DevicePool>(device_);
+    ok_ = true;
+}
+
+HipEngine::~HipEngine()
+{
+    if (stream_)
+    {
+        (void)hipStreamSynchronize(static_cast<hipStream_t>(stream_));
+        (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+    }
+    for (auto& r : prof_)
+    {
+        (void)hipEventDestroy(static_cast<hipEvent_t>(r.start));
+        (void)hipEventDestroy(static_cast<hipEvent_t>(r.stop));
+    }
+    for (void* e : event_pool_) (void)hipEventDestroy(static_cast<hipEvent_t>(e));
+}
+
+// ── GEMM event profile ──────────────────────────────────────────────────────
+void HipEngine::set_gemm_profile(bool on) { profile_ = on; }
+
+void HipEngine::prof_begin_()
+{
+    if (!profile_) return;
+    auto take = [this]() -> void* {
+        if (!event_pool_.empty())
+        {
+            void* e = event_pool_.back();
+            event_pool_.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        (void)hipEventCreate(&e);
+        return e;
+    };
+    ProfRecord r{take(), take(), 0.0};
+    (void)hipEventRecord(static_cast<hipEvent_t>(r.start), static_cast<hipStream_t>(stream_));
+    prof_.push_back(r);
+}
+
+void HipEngine::prof_end_(double flops)
+{
+    if (!profile_ || prof_.empty()) return;
+    prof_.back().flops = flops;
+    (void)hipEventRecord(static_cast<hipEvent_t>(prof_.back().stop), static_cast<hipStream_t>(stream_));
+}
+
+Result<void> HipEngine::read_gemm_profile(double& launches, double& flops, double& ms)
+{
+    NN_CHECK(end_batch());
+    launches = static_cast<double>(prof_.size());
+    flops = 0.0;
+    ms = 0.0;
+    for (auto& r : prof_)
+    {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, static_cast<hipEvent_t>(r.start), static_cast<hipEvent_t>(r.stop)) != hipSuccess)
+            return fail("read_gemm_profile: event timing failed");
+        ms += t;
+        flops += r.flops;
+        event_pool_.push_back(r.start);
+        event_pool_.push_back(r.stop);
+    }
+    prof_.clear();
+    return {};
+}
+
+std::size_t HipEngine::pool_cached_bytes() const { return pool_ ? pool_->cached() : 0; }
+std::size_t HipEngine::pool_live_bytes() const { return pool_ ? pool_->live() : 0; }
+
+Result<void> HipEngine::kernel_(int rc, const char* what)
+{
+    if (rc == 0) return {};
+    if (rc > 0)
+        return fail(std::string(what) + ": HIP error " + hipGetErrorString(static_cast<hipError_t>(rc)));
+    if (rc == -3) return fail(std::string(what) + ": shape outside this kernel's supported range");
+    return fail(std::string(what) + ": invalid arguments (status " + std::to_string(rc) + ")");
+}
+
+Result<void> HipEngine::need_gpu_(std::initializer_list<const Tensor*> ts, const char* what) const
+{
+    for (const Tensor* t : ts)
+        if (t && (!t->is_gpu() || (t->size() > 0 && !t->dev_ptr())))
+            return fail(std::string(what) + ": tensor is not on this GPU engine");
+    return {};
+}
+
+Result<Tensor> HipEngine::alloc_(std::size_t rows, std::size_t cols)
+{
+    const std::size_t n = rows * cols;
+    if (n == 0) return Tensor(std::shared_ptr<DeviceBuffer>(), rows, cols);
+    std::size_t rounded = 0;
+    void* p = pool_->alloc(n * sizeof(float), rounded);
+    if (!p) return fail("HipEngine: out of device memory allocating " + std::to_string(n * 4) + " bytes");
+    return Tensor(std::make_shared<HipBuffer>(pool_, static_cast<float*>(p), n, rounded), rows, cols);
+}
+
+Result<std::shared_ptr<DeviceBuffer>> HipEngine::scratch_(std::size_t bytes)
+{
+    std::size_t rounded = 0;
+    void* p = pool_->alloc(bytes < 256 ? 256 : bytes, rounded);
+    if (!p) return fail("HipEngine: out of device memory for workspace");
+    return std::shared_ptr<DeviceBuffer>(
+        std::make_shared<HipBuffer>(pool_, static_cast<float*>(p), rounded / sizeof(float), rounded));
+}
+
+Result<void> HipEngine::begin_batch() { return {}; }
+
+Result<void> HipEngine::end_batch()
+{
+    const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream_));
+    if (e != hipSuccess) return fail(std::string("HipEngine: stream error: ") + hipGetErrorString(e));
+    const hipError_t l = hipGetLastError();
+    if (l != hipSuccess) return fail(std::string("HipEngine: launch error: ") + hipGetErrorString(l));
+    return {};
+}
+
+Result<void> HipEngine::flush_batch() { return end_batch(); }
+
+// ── factories and transfers (cpu_engine.hpp:40-72) ─────────────────────────
+Tensor HipEngine::create_tensor(std::size_t rows, std::size_t cols)
+{
+    auto t = alloc_(rows, cols);
+    if (!t)
+    {
+        std::fprintf(stderr, "%s\n", t.error().message.c_str());
+        return Tensor(std::shared_ptr<DeviceBuffer>(), 0, 0);
+    }
+    return *t;
+}
+
+Result<Tensor> HipEngine::from_matrix(const Matrix& m)
+{
+    NN_TRY(t, alloc_(m.rows(), m.cols()));
+    if (m.size())
+    {
+        auto s = static_cast<hipStream_t>(stream_);
+        if (hipMemcpyAsync(W(t), m.data(), m.size() * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess)
+            return fail("from_matrix: host to device copy failed");
+        NN_CHECK(end_batch());
+    }
+    return t;
+}
+
+Result<Matrix> HipEngine::to_matrix(const Tensor& t)
+{
+    if (!t.is_gpu()) return fail("to_matrix: tensor is not GPU");
+    Matrix m(t.rows(), t.cols());
+    if (m.size())
+    {
+        auto s = static_cast<hipStream_t>(stream_);
+        if (hipMemcpyAsync(m.data(), D(t), m.size() * sizeof(float), hipMemcpyDeviceToHost, s) != hipSuccess)
+            return fail("to_matrix: device to host copy failed");
+    }
+    NN_CHECK(end_batch());
+    return m;
+}
+
+Result<void> HipEngine::copy_from(Tensor& dst, const Matrix& src)
+{
+    if (!dst.is_gpu()) return fail("copy_from: dst tensor is not GPU");
+    if (dst.rows() != src.rows() || dst.cols() != src.cols()) return fail("copy_from: shape mismatch");
+    if (src.size())
+    {
+        auto s = static_cast<hipStream_t>(stream_);
+        if (hipMemcpyAsync(W(dst), src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess)
+            return fail("copy_from: host to device copy failed");
+        NN_CHECK(end_batch());
+    }
+    return {};
+}
+
+Result<Tensor> HipEngine::clone(const Tensor& src)
+{
+    NN_CHECK(need_gpu_({&src}, "clone"));
+    NN_TRY(t, alloc_(src.rows(), src.cols()));
+    if (src.size() &&
+        hipMemcpyAsync(W(t), D(src), src.size() * sizeof(float), hipMemcpyDeviceToDevice,
+                       static_cast<hipStream_t>(stream_)) != hipSuccess)
+        return fail("clone: device copy failed");
+    return t;
+}
+
+// ── row slices (cpu_engine.hpp:75-114) ──────────────────────────────────────
+Result<Tensor> HipEngine::slice_rows(const Tensor& src, std::size_t start, std::size_t count)
+{
+    NN_CHECK(need_gpu_({&src}, "slice_rows"));
+    if (start + count > src.rows()) return fail("slice_rows: range out of bounds");
+    NN_TRY(t, alloc_(count, src.cols()));
+    const std::size_t n = count * src.cols();
+    if (n && hipMemcpyAsync(W(t), D(src) + start * src.cols(), n * sizeof(float), hipMemcpyDeviceToDevice,
+                            static_cast<hipStream_t>(stream_)) != hipSuccess)
+        return fail("slice_rows: device copy failed");
+    return t;
+}
+
+Result<void> HipEngine::insert_rows(Tensor& dst, std::size_t start, const Tensor& src)
+{
+    NN_CHECK(need_gpu_({&dst, &src}, "insert_rows"));
+    if (dst.cols() != src.cols()) return fail("insert_rows: column count mismatch");
+    if (start + src.rows() > dst.rows()) return fail("insert_rows: range out of bounds");
+    if (src.size() && hipMemcpyAsync(W(dst) + start * dst.cols(), D(src), src.size() * sizeof(float),
+                                     hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream_)) != hipSuccess)
+        return fail("insert_rows: device copy failed");
+    return {};
+}
+
+// ── gather / scatter (cpu_engine.hpp:125-216) ───────────────────────────────
+Result<Tensor> HipEngine::gather_rows(const Tensor& table, const Tensor& indices)
+{
+    NN_CHECK(need_gpu_({&table, &indices}, "gather_rows"));
+    const std::size_t n = indices.size(), D_ = table.cols();
+    NN_TRY(out, alloc_(n, D_));
+    NN_CHECK(kernel_(nnhip_gather(D(table), D(indices), W(out), table.rows(), D_, n, stream_), "gather_rows"));
+    return out;
+}
+
+Result<void> HipEngine::scatter_add_rows(Tensor& dst, const Tensor& indices, const Tensor& grad)
+{
+    NN_CHECK(need_gpu_({&dst, &indices, &grad}, "scatter_add_rows"));
+    if (dst.cols() != grad.cols()) return fail("scatter_add_rows: column count mismatch");
+    const std::size_t n = indices.size();
+    if (grad.rows() < n) return fail("scatter_add_rows: grad has fewer rows than indices");
+    if (n == 0 || dst.cols() == 0) return {};
+    NN_TRY(ws, scratch_(nnhip_scatter_add_workspace_bytes(n)));
+    return kernel_(nnhip_scatter_add(W(dst), D(indices), D(grad), dst.rows(), dst.cols(), n, ws->data(), stream_),
+                   "scatter_add_rows");
+}
+
+// ── layout (cpu_engine.hpp:226-287) ─────────────────────────────────────────
+Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size_t B, std::size_t N, bool inverse)
+{
+    NN_CHECK(need_gpu_({&x}, "rearrange_3d"));
+    if (x.size() != M * B * N) return fail("rearrange_3d: element count mismatch");
+    NN_TRY(out, alloc_(inverse ? M : B * M, inverse ? B * N : N));
+    NN_CHECK(kernel_(nnhip_rearrange_3d(D(x), W(out), M, B, N, inverse ? 1u : 0u, stream_), "rearrange_3d"));
+    return out;
+}
+
+Result<Tensor> HipEngine::transpose(const Tensor& A)
+{
+    NN_CHECK(need_gpu_({&A}, "transpose"));
+    NN_TRY(out, alloc_(A.cols(), A.rows()));
+    NN_CHECK(kernel_(nnhip_transpose(D(A), W(out), A.rows(), A.cols(), stream_), "transpose"));
+    return out;
+}
+
+// ── GEMM (cpu_engine.hpp:293-419) ───────────────────────────────────────────
+Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool tB)
+{
+    NN_CHECK(need_gpu_({&A, &B}, "matmul"));
+    const std::size_t M = tA ? A.cols() : A.rows(), K = tA ? A.rows() : A.cols();
+    const std::size_t K2 = tB ? B.cols() : B.rows(), N = tB ? B.rows() : B.cols();
+    if (K != K2)
+        return fail("matmul: dimension mismatch A=" + std::to_string(A.rows()) + "x" + std::to_string(A.cols()) +
+                    " B=" + std::to_string(B.rows()) + "x" + std::to_string(B.cols()));
+    NN_TRY(C, alloc_(M, N));
+    prof_begin_();
+    const int rc = nnhip_matmul(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), tA, tB, stream_);
+    prof_end_(2.0 * double(M) * double(N) * double(K));
+    NN_CHECK(kernel_(rc, "matmul"));
+    return C;
+}
+
+Result<Tensor> HipEngine::batched_matmul(const Tensor& A, const Tensor& B, std::size_t batch, bool tA, bool tB,
+                                         Scalar alpha)
+{
+    NN_CHECK(need_gpu_({&A, &B}, "batched_matmul"));
+    NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul"));
+    NN_TRY(C, alloc_(batch * d.M, d.N));
+    prof_begin_();
+    const int rc = nnhip_batched_matmul(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), batch, tA, tB,
+                                        alpha, stream_);
+    prof_end_(2.0 * double(batch) * double(d.M) * double(d.N) * double(d.K));
+    NN_CHECK(kernel_(rc, "batched_matmul"));
+    return C;
+}
+
+// ── fused attention (cpu_engine.hpp:426-915) ────────────────────────────────
+Result<Tensor> HipEngine::batched_matmul_reduce(const Tensor& A, const Tensor& B, std::size_t batch, ReduceOp op,
+                                                bool tA, bool tB, Scalar alpha, bool reduce_cols, const Tensor* mask)
+{
+    NN_CHECK(need_gpu_({&A, &B, mask}, "batched_matmul_reduce"));
+    NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_reduce"));
+    NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_reduce"));
+    NN_TRY(out, alloc_(reduce_cols ? batch * d.M : batch, reduce_cols ? 1 : d.N));
+    NN_CHECK(kernel_(nnhip_bmm_reduce(D(A), D(B), mask ? D(*mask) : nullptr, W(out), batch, d.M, d.N, d.K, tA, tB,
+                                      static_cast<unsigned>(op), alpha, reduce_cols, stream_),
+                     "batched_matmul_reduce"));
+    return out;
+}
+
+Result<Tensor> HipEngine::batched_matmul_softmax_denom(const Tensor& A, const Tensor& B, const Tensor& row_max,
+                                                       std::size_t batch, bool tA, bool tB, Scalar alpha,
+                                                       const Tensor* mask)
+{
+    NN_CHECK(need_gpu_({&A, &B, &row_max, mask}, "batched_matmul_softmax_denom"));
+    NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_softmax_denom"));
+    NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_denom", "row_max"));
+    NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_denom"));
+    NN_TRY(out, alloc_(batch * d.M, 1));
+    NN_CHECK(kernel_(nnhip_bmm_softmax_denom(D(A), D(B), D(row_max), mask ? D(*mask) : nullptr, W(out), batch, d.M,
+                                             d.N, d.K, tA, tB, alpha, stream_),
+                     "batched_matmul_softmax_denom"));
+    return out;
+}
+
+Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Tensor& B, const Tensor& V,
+                                                       const Tensor& row_max, const Tensor& denom, std::size_t batch,
+                                                       bool tA, bool tB, Scalar alpha, const Tensor* mask)
+{
+    NN_CHECK(need_gpu_({&A, &B, &V, &row_max, &denom, mask}, "batched_matmul_softmax_apply"));
+    if (batch != 0 && V.rows() % batch != 0) return fail("batched_matmul_softmax_apply: rows not divisible by batch");
+    NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_softmax_apply"));
+    if (V.rows() / batch != d.N) return fail("batched_matmul_softmax_apply: V rows per batch != N");
+    NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_apply", "row_max"));
+    NN_CHECK(vec_ok(denom, batch * d.M, "batched_matmul_softmax_apply", "denom"));
+    NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_apply"));
+    NN_TRY(out, alloc_(batch * d.M, V.cols()));
+    NN_CHECK(kernel_(nnhip_bmm_softmax_apply(D(A), D(B), D(V), D(row_max), D(denom), mask ? D(*mask) : nullptr,
+                                             W(out), batch, d.M, d.N, d.K, V.cols(), tA, tB, alpha, stream_),
+                     "batched_matmul_softmax_apply"));
+    return out;
+}
+
+Result<Tensor> HipEngine::batched_matmul_softmax_backward_q(const Tensor& A, const Tensor& B, const Tensor& P,
+                                                            const Tensor& row_max, const Tensor& denom,
+                                                            std::size_t batch, bool tA, bool tB, Scalar alpha,
+                                                            Tensor& r_out, const Tensor* mask)
+{
+    NN_CHECK(need_gpu_({&A, &B, &P, &row_max, &denom, mask}, "batched_matmul_softmax_backward_q"));
+    NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_softmax_backward_q"));
+    if (P.rows() != batch * d.M || P.cols() != d.N) return fail("batched_matmul_softmax_backward_q: P shape mismatch");
+    NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_backward_q", "row_max"));
+    NN_CHECK(vec_ok(denom, batch * d.M, "batched_matmul_softmax_backward_q", "denom"));
+    NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_backward_q"));
+    NN_TRY(dq, alloc_(batch * d.K, d.M));
+    NN_TRY(r, alloc_(batch * d.M, 1));
+    NN_CHECK(kernel_(nnhip_bmm_softmax_backward_q(D(A), D(B), D(P), D(row_max), D(denom), mask ? D(*mask) : nullptr,
+                                                  W(dq), W(r), batch, d.M, d.N, d.K, tA, tB, alpha, stream_),
+                     "batched_matmul_softmax_backward_q"));
+    r_out = r;
+    return dq;
+}
+
+Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, const Tensor& B, const Tensor& P,
+                                                             const Tensor& G, const Tensor& R, const Tensor& row_max,
+                                                             const Tensor& denom, std::size_t batch, bool tA, bool tB,
+                                                             Scalar alpha, Tensor& grad_v_out, const Tensor* mask)
+{
+    NN_CHECK(need_gpu_({&A, &B, &P, &G, &R, &row_max, &denom, mask}, "batched_matmul_softmax_backward_kv"));
+    NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_softmax_backward_kv"));
+    if (P.rows() != batch * d.M || P.cols() != d.N)
+        return fail("batched_matmul_softmax_backward_kv: P shape mismatch");
+    if (G.rows() != batch * d.M) return fail("batched_matmul_softmax_backward_kv: G rows != batch*M");
+    NN_CHECK(vec_ok(R, batch * d.M, "batched_matmul_softmax_backward_kv", "R"));
+    NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_backward_kv", "row_max"));
+    NN_CHECK(vec_ok(denom, batch * d.M, "batched_matmul_softmax_backward_kv", "denom"));
+    NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_backward_kv"));
+    if (G.cols() < d.K) return fail("batched_matmul_softmax_backward_kv: G cols < K");
+    NN_TRY(dk, alloc_(batch * d.K, d.N));
+    NN_TRY(dv, alloc_(batch * d.K, d.N));
+    NN_CHECK(kernel_(nnhip_bmm_softmax_backward_kv(D(A), D(B), D(P), D(G), D(R), D(row_max), D(denom),
+                                                   mask ? D(*mask) : nullptr, W(dk), W(dv), batch, d.M, d.N, d.K,
+                                                   G.cols(), tA, tB, alpha, stream_),
+                     "batched_matmul_softmax_backward_kv"));
+    grad_v_out = dv;
+    return dk;
+}
+
+// ── column softmax / cross-entropy (cpu_engine.hpp:922-1006) ─────────────────
+Result<Tensor> HipEngine::col_softmax_denom(const Tensor& logits, const Tensor& col_max)
+{
+    NN_CHECK(need_gpu_({&logits, &col_max}, "col_softmax_denom"));
+    const std::size_t C = logits.rows(), N = logits.cols();
+    if (col_max.rows() != 1 || col_max.cols() != N) return fail("col_softmax_denom: col_max shape mismatch");
+    NN_TRY(out, alloc_(1, N));
+    NN_TRY(ws, scratch_(nnhip_col_softmax_workspace_bytes(C, N)));
+    NN_CHECK(kernel_(nnhip_col_softmax_denom(D(logits), D(col_max), W(out), C, N, ws->data(), stream_),
+                     "col_softmax_denom"));
+    return out;
+}
+
+Result<Tensor> HipEngine::col_softmax_sparse_forward(const Tensor& logits, const Tensor& labels, const Tensor* mask,
+                                                     std::size_t vocab, Scalar inv, Tensor& loss_vec_out)
+{
+    NN_CHECK(need_gpu_({&logits, &labels, mask}, "col_softmax_sparse_forward"));
+    if (vocab > (std::size_t{1} << 24))
+        return fail("col_softmax_sparse_forward: vocab_size exceeds 2^24 (float labels not exactly representable)");
+    const std::size_t C = logits.rows(), N = logits.cols();
+    if (labels.rows() != 1 || labels.cols() != N) return fail("col_softmax_sparse_forward: labels shape mismatch");
+    if (vocab > C) return fail("col_softmax_sparse_forward: vocab_size > classes");
+    if (mask && (mask->rows() != 1 || mask->cols() != N)) return fail("col_softmax_sparse_forward: mask shape mismatch");
+    NN_TRY(grad, alloc_(C, N));
+    NN_TRY(lv, alloc_(1, N));
+    NN_TRY(ws, scratch_(nnhip_col_softmax_workspace_bytes(C, N)));
+    NN_CHECK(kernel_(nnhip_col_softmax_sparse_forward(D(logits), D(labels), mask ? D(*mask) : nullptr, W(grad), W(lv),
+                                                      C, N, vocab, inv, ws->data(), stream_),
+                     "col_softmax_sparse_forward"));
+    loss_vec_out = lv;
+    return grad;
+}
+
+// ── in-place ops (cpu_engine.hpp:1008-1044) ─────────────────────────────────
+Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
+{
+    NN_CHECK(need_gpu_({&A, &B}, "add_inplace"));
+    if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("add_inplace: shape mismatch");
+    return kernel_(nnhip_elementwise_binary(D(A), D(B), W(A), A.size(), 0u, stream_), "add_inplace");
+}
+
+Result<void> HipEngine::scale_inplace(Tensor& A, Scalar s)
+{
+    NN_CHECK(need_gpu_({&A}, "scale_inplace"));
+    return kernel_(nnhip_elementwise_binary_scalar(D(A), W(A), A.size(), 2u, s, 0, stream_), "scale_inplace");
+}
+
+Result<void> HipEngine::axpy_inplace(Tensor& A, Scalar s, const Tensor& B)
+{
+    NN_CHECK(need_gpu_({&A, &B}, "axpy_inplace"));
+    if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("axpy_inplace: shape mismatch");
+    return kernel_(nnhip_axpy(D(A), D(B), W(A), A.size(), s, stream_), "axpy_inplace");
+}
+
+Result<void> HipEngine::zero(Tensor& A)
+{
+    NN_CHECK(need_gpu_({&A}, "zero"));
+    return kernel_(nnhip_fill(W(A), A.size(), 0.0f, stream_), "zero");
+}
+
+// ── reductions (cpu_engine.hpp:1050-1086) ───────────────────────────────────
+Result<Tensor> HipEngine::row_reduce_sum(const Tensor& A)
+{
+    NN_CHECK(need_gpu_({&A}, "row_reduce_sum"));
+    NN_TRY(o, alloc_(A.rows(), 1));
+    NN_CHECK(kernel_(nnhip_reduce_row(D(A), W(o), A.rows(), A.cols(), 0u, stream_), "row_reduce_sum"));
+    return o;
+}
+Result<Tensor> HipEngine::row_reduce_max(const Tensor& A)
+{
+    NN_CHECK(need_gpu_({&A}, "row_reduce_max"));
+    NN_TRY(o, alloc_(A.rows(), 1));
+    NN_CHECK(kernel_(nnhip_reduce_row(D(A), W(o), A.rows(), A.cols(), 1u, stream_), "row_reduce_max"));
+    return o;
+}
+Result<Tensor> HipEngine::col_reduce_sum(const Tensor& A)
+{
+    NN_CHECK(need_gpu_({&A}, "col_reduce_sum"));
+    NN_TRY(o, alloc_(1, A.cols()));
+    NN_TRY(ws, scratch_(nnhip_reduce_col_workspace_bytes(A.rows(), A.cols())));
+    NN_CHECK(kernel_(nnhip_reduce_col(D(A), W(o), A.rows(), A.cols(), 0u, ws->data(), stream_), "col_reduce_sum"));
+    return o;
+}
+Result<Tensor> HipEngine::col_reduce_max(const Tensor& A)
+{
+    NN_CHECK(need_gpu_({&A}, "col_reduce_max"));
+    NN_TRY(o, alloc_(1, A.cols()));
+    NN_TRY(ws, scratch_(nnhip_reduce_col_workspace_bytes(A.rows(), A.cols())));
+    NN_CHECK(kernel_(nnhip_reduce_col(D(A), W(o), A.rows(), A.cols(), 1u, ws->data(), stream_), "col_reduce_max"));
+    return o;
+}
+
+// ── broadcasts (cpu_engine.hpp:1092-1125) ───────────────────────────────────
+Result<void> HipEngine::broadcast_row_inplace(Tensor& A, const Tensor& v, BinaryOp op)
+{
+    NN_CHECK(need_gpu_({&A, &v}, "broadcast_row_inplace"));
+    if (v.rows() != A.rows() || v.cols() != 1) return fail("broadcast_row_inplace: row_vec shape mismatch");
+    return kernel_(nnhip_broadcast_row(D(A), D(v), W(A), A.rows(), A.cols(), static_cast<unsigned>(op), stream_),
+                   "broadcast_row_inplace");
+}
+Result<void> HipEngine::broadcast_col_inplace(Tensor& A, const Tensor& v, BinaryOp op)
+{
+    NN_CHECK(need_gpu_({&A, &v}, "broadcast_col_inplace"));
+    if (v.rows() != 1 || v.cols() != A.cols()) return fail("broadcast_col_inplace: col_vec shape mismatch");
+    return kernel_(nnhip_broadcast_col(D(A), D(v), W(A), A.rows(), A.cols(), static_cast<unsigned>(op), stream_),
+                   "broadcast_col_inplace");
+}
+
+// ── elementwise (cpu_engine.hpp:1131-1266) ──────────────────────────────────
+Result<Tensor> HipEngine::elementwise_unary(UnaryOp op, const Tensor& A)
+{
+    NN_CHECK(need_gpu_({&A}, "elementwise_unary"));
+    NN_TRY(o, alloc_(A.rows(), A.cols()));
+    NN_CHECK(kernel_(nnhip_elementwise_unary(D(A), W(o), A.size(), static_cast<unsigned>(op), stream_),
+                     "elementwise_unary"));
+    return o;
+}
+Result<Tensor> HipEngine::elementwise_binary(BinaryOp op, const Tensor& A, const Tensor& B)
+{
+    NN_CHECK(need_gpu_({&A, &B}, "elementwise_binary"));
+    if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("elementwise_binary: shape mismatch");
+    NN_TRY(o, alloc_(A.rows(), A.cols()));
+    NN_CHECK(kernel_(nnhip_elementwise_binary(D(A), D(B), W(o), A.size(), static_cast<unsigned>(op), stream_),
+                     "elementwise_binary"));
+    return o;
+}
+Result<Tensor> HipEngine::elementwise_binary_scalar(BinaryOp op, const Tensor& A, Scalar s, bool first)
+{
+    NN_CHECK(need_gpu_({&A}, "elementwise_binary_scalar"));
+    NN_TRY(o, alloc_(A.rows(), A.cols()));
+    NN_CHECK(kernel_(nnhip_elementwise_binary_scalar(D(A), W(o), A.size(), static_cast<unsigned>(op), s, first ? 1 : 0,
+                                                     stream_),
+                     "elementwise_binary_scalar"));
+    return o;
+}
+Result<Tensor> HipEngine::elementwise_select_scalar_cond(CompareOp cmp, const Tensor& A, Scalar sb,
+                                                         const Tensor& then_t, Scalar se)
+{
+    NN_CHECK(need_gpu_({&A, &then_t}, "elementwise_select_scalar_cond"));
+    if (A.rows() != then_t.rows() || A.cols() != then_t.cols())
+        return fail("elementwise_select: A and then shape mismatch");
+    NN_TRY(o, alloc_(A.rows(), A.cols()));
+    NN_CHECK(kernel_(nnhip_elementwise_select_scalar_cond(D(A), D(then_t), W(o), A.size(), static_cast<unsigned>(cmp),
+                                                          sb, se, stream_),
+                     "elementwise_select_scalar_cond"));
+    return o;
+}
+
+// ── eval_expr (cpu_engine.hpp:1276-1659) ────────────────────────────────────
+Result<Tensor> HipEngine::eval_expr(const ExprSpec& spec, std::span<const Tensor> inputs, std::size_t rows,
+                                    std::size_t cols)
+{
+    return eval_impl_(spec, inputs, rows, cols, false);
+}
+Result<Tensor> HipEngine::eval_expr_reduce(const ExprSpec& spec, std::span<const Tensor> inputs, std::size_t rows,
+                                           std::size_t cols)
+{
+    return eval_impl_(spec, inputs, rows, cols, true);
+}
+
+Result<Tensor> HipEngine::eval_impl_(const ExprSpec& spec, std::span<const Tensor> inputs, std::size_t rows,
+                                     std::size_t cols, bool vector_out)
+{
+    NN_CHECK(validate_expr_spec(spec, inputs.size()));
+    const int raxis = vector_out ? expr_spec_reduce_axis(spec) : -1;
+    if (vector_out && raxis != 0 && raxis != 1)
+        return fail("eval_expr_reduce: expression must reduce along rows or along columns");
+    for (std::size_t k = 0; k < inputs.size(); ++k)
+    {
+        const Tensor& t = inputs[k];
+        if (!t.is_gpu()) return fail("eval_expr: input not GPU");
+        const ExprView& v = spec.views[k];
+        switch (static_cast<ExprViewKind>(v.kind))
+        {
+        case ExprViewKind::RotateHalf:
+            if (t.rows() != rows || t.cols() != cols || v.param == 0 || rows % v.param != 0 || v.param % 2 != 0)
+                return fail("eval_expr: RotateHalf shape/param invalid");
+            break;
+        case ExprViewKind::RowMod:
+            if (t.rows() != v.param || t.cols() != cols || v.param == 0 || rows % v.param != 0)
+                return fail("eval_expr: RowMod shape/param invalid");
+            break;
+        case ExprViewKind::RowBroadcast:
+            if (t.rows() != rows || t.cols() != 1) return fail("eval_expr: RowBroadcast input must be (rows,1)");
+            break;
+        case ExprViewKind::ColBroadcast:
+            if (t.rows() != 1 || t.cols() != cols) return fail("eval_expr: ColBroadcast input must be (1,cols)");
+            break;
+        default:
+            if (t.rows() != rows || t.cols() != cols) return fail("eval_expr: Linear/reduce input shape mismatch");
+            break;
+        }
+    }
+    if (rows * cols == 0) return alloc_(rows, cols);   // the reference returns the (rows, cols) shape here
+
+    // Fast paths: the Softmax layer's forward / backward programs on one row tensor.
+    if (!vector_out && expr_spec_equal(spec, softmax_fwd_spec()) && inputs[0].dev_ptr() == inputs[1].dev_ptr() &&
+        inputs[0].dev_ptr() == inputs[2].dev_ptr() && inputs[0].dev_ptr() == inputs[3].dev_ptr())
+    {
+        NN_TRY(o, alloc_(rows, cols));
+        NN_CHECK(kernel_(nnhip_row_softmax(D(inputs[0]), W(o), rows, cols, stream_), "eval_expr(softmax)"));
+        return o;
+    }
+    if (!vector_out && expr_spec_equal(spec, softmax_bwd_spec()) && inputs[0].dev_ptr() == inputs[2].dev_ptr() &&
+        inputs[1].dev_ptr() == inputs[3].dev_ptr())
+    {
+        NN_TRY(o, alloc_(rows, cols));
+        NN_CHECK(kernel_(nnhip_row_softmax_backward(D(inputs[0]), D(inputs[1]), W(o), rows, cols, stream_),
+                         "eval_expr(softmax backward)"));
+        return o;
+    }
+
+    nnhip_expr_program p;
+    std::memset(&p, 0, sizeof p);
+    p.n_instrs = static_cast<unsigned>(spec.instrs.size());
+    p.n_views = static_cast<unsigned>(spec.views.size());
+    p.n_consts = static_cast<unsigned>(spec.consts.size());
+    p.num_regs = spec.num_regs;
+    for (std::size_t i = 0; i < spec.instrs.size(); ++i)
+    {
+        const ExprInstr& in = spec.instrs[i];
+        const unsigned char b[8] = {in.op, in.dst, in.a.kind, in.a.idx, in.b.kind, in.b.idx, in.c.kind, in.c.idx};
+        std::memcpy(p.instrs[i], b, 8);
+    }
+    for (std::size_t k = 0; k < spec.views.size(); ++k)
+    {
+        p.view_kind[k] = spec.views[k].kind;
+        p.view_negate[k] = spec.views[k].negate_first_half;
+        p.view_param[k] = spec.views[k].param;
+    }
+    for (std::size_t c = 0; c < spec.consts.size(); ++c) p.consts[c] = spec.consts[c];
+    const float* ptrs[8] = {};
+    for (std::size_t k = 0; k < inputs.size(); ++k) ptrs[k] = D(inputs[k]);
+
+    const std::size_t orow = vector_out ? (raxis == 0 ? rows : 1) : rows;
+    const std::size_t ocol = vector_out ? (raxis == 0 ? 1 : cols) : cols;
+    NN_TRY(o, alloc_(orow, ocol));
+    NN_TRY(ws, scratch_(nnhip_eval_expr_workspace_bytes(&p, rows, cols)));
+    const int rc = nnhip_eval_expr(&p, ptrs, W(o), rows, cols, vector_out ? 1 : 0, ws->data(), stream_);
+    if (rc == -4)
+        return fail("eval_expr_reduce: output chain reads an input directly; the output is not constant along "
+                    "the reduced axis");
+    NN_CHECK(kernel_(rc, "eval_expr"));
+    return o;
+}
+
+} // namespace nn

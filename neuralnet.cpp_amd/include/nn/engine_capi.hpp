@@ -1,0 +1,524 @@
+// engine_capi.hpp — implementation of the flat C-ABI (include/nnhip_engine.h)
+// over any nn::ComputeEngine. A library instantiates it once with its
+// engine type and symbol prefix via NN_DEFINE_ENGINE_CAPI(prefix, make_engine).
+#pragma once
+
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "compute_engine.hpp"
+#include "compute_loss.hpp"
+#include "compute_optimizer.hpp"
+#include "model.hpp"
+
+namespace nn::capi
+{
+
+inline std::string& last_error()
+{
+    static thread_local std::string e;
+    return e;
+}
+inline int set_error(const std::string& m)
+{
+    last_error() = m;
+    return 1;
+}
+
+struct EngineHandle
+{
+    std::unique_ptr<ComputeEngine> eng;
+};
+
+inline Tensor* T(void* h) { return static_cast<Tensor*>(h); }
+inline const Tensor* T(const void* h) { return static_cast<const Tensor*>(h); }
+
+inline void* new_tensor(Tensor t) { return new Tensor(std::move(t)); }
+
+inline void* tensor_create(EngineHandle* e, std::size_t r, std::size_t c)
+{
+    return new_tensor(e->eng->create_tensor(r, c));
+}
+
+inline void* tensor_from_host(EngineHandle* e, const float* data, std::size_t r, std::size_t c)
+{
+    Matrix m(r, c);
+    if (r * c != 0) std::memcpy(m.data(), data, r * c * sizeof(float));
+    auto t = e->eng->from_matrix(m);
+    if (!t)
+    {
+        set_error(t.error().message);
+        return nullptr;
+    }
+    return new_tensor(*t);
+}
+
+inline int tensor_to_host(EngineHandle* e, const void* h, float* out)
+{
+    auto m = e->eng->to_matrix(*T(h));
+    if (!m) return set_error(m.error().message);
+    if (m->size()) std::memcpy(out, m->data(), m->size() * sizeof(float));
+    return 0;
+}
+
+inline int tensor_copy_from_host(EngineHandle* e, void* h, const float* data)
+{
+    Tensor* t = T(h);
+    Matrix m(t->rows(), t->cols());
+    if (m.size()) std::memcpy(m.data(), data, m.size() * sizeof(float));
+    auto r = e->eng->copy_from(*t, m);
+    return r ? 0 : set_error(r.error().message);
+}
+
+inline void* tensor_data_ptr(const void* h)
+{
+    const Tensor* t = T(h);
+    if (t->is_cpu()) return const_cast<float*>(t->cpu_matrix().data());
+    return t->dev_ptr();
+}
+
+inline int engine_op(EngineHandle* e, int op, void* const* in, std::size_t n_in, void** out, std::size_t n_out,
+                     const double* a, std::size_t n_args)
+{
+    ComputeEngine& E = *e->eng;
+    auto need = [&](std::size_t ni, std::size_t no, std::size_t na) -> bool {
+        if (n_in < ni || n_out < no || n_args < na)
+        {
+            set_error("engine_op: too few inputs/outputs/args for op " + std::to_string(op));
+            return false;
+        }
+        return true;
+    };
+    auto in_t = [&](std::size_t i) -> Tensor& { return *T(in[i]); };
+    auto flag = [&](std::size_t i) { return a[i] != 0.0; };
+    auto sz = [&](std::size_t i) { return static_cast<std::size_t>(a[i]); };
+    auto sc = [&](std::size_t i) { return static_cast<Scalar>(a[i]); };
+    auto put = [&](std::size_t i, Result<Tensor>& r) -> int {
+        if (!r) return set_error(r.error().message);
+        out[i] = new_tensor(*r);
+        return 0;
+    };
+    auto done = [&](const Result<void>& r) -> int { return r ? 0 : set_error(r.error().message); };
+    auto opt_mask = [&](std::size_t idx) -> const Tensor* { return n_in > idx ? T(in[idx]) : nullptr; };
+
+    switch (op)
+    {
+    case 1: { if (!need(1, 1, 0)) return 1; auto r = E.clone(in_t(0)); return put(0, r); }
+    case 2: { if (!need(1, 1, 2)) return 1; auto r = E.slice_rows(in_t(0), sz(0), sz(1)); return put(0, r); }
+    case 3: { if (!need(2, 0, 1)) return 1; return done(E.insert_rows(in_t(0), sz(0), in_t(1))); }
+    case 4: { if (!need(2, 1, 0)) return 1; auto r = E.gather_rows(in_t(0), in_t(1)); return put(0, r); }
+    case 5: { if (!need(3, 0, 0)) return 1; return done(E.scatter_add_rows(in_t(0), in_t(1), in_t(2))); }
+    case 6: { if (!need(1, 1, 4)) return 1; auto r = E.rearrange_3d(in_t(0), sz(0), sz(1), sz(2), flag(3)); return put(0, r); }
+    case 7: { if (!need(1, 1, 0)) return 1; auto r = E.transpose(in_t(0)); return put(0, r); }
+    case 8: { if (!need(2, 1, 2)) return 1; auto r = E.matmul(in_t(0), in_t(1), flag(0), flag(1)); return put(0, r); }
+    case 9: { if (!need(2, 1, 4)) return 1; auto r = E.batched_matmul(in_t(0), in_t(1), sz(0), flag(1), flag(2), sc(3)); return put(0, r); }
+    case 10:
+    {
+        if (!need(2, 1, 6)) return 1;
+        auto r = E.batched_matmul_reduce(in_t(0), in_t(1), sz(0), static_cast<ReduceOp>(sz(1)), flag(2), flag(3), sc(4),
+                                         flag(5), opt_mask(2));
+        return put(0, r);
+    }
+    case 11:
+    {
+        if (!need(3, 1, 4)) return 1;
+        auto r = E.batched_matmul_softmax_denom(in_t(0), in_t(1), in_t(2), sz(0), flag(1), flag(2), sc(3), opt_mask(3));
+        return put(0, r);
+    }
+    case 12:
+    {
+        if (!need(5, 1, 4)) return 1;
+        auto r = E.batched_matmul_softmax_apply(in_t(0), in_t(1), in_t(2), in_t(3), in_t(4), sz(0), flag(1), flag(2),
+                                                sc(3), opt_mask(5));
+        return put(0, r);
+    }
+    case 13:
+    {
+        if (!need(5, 2, 4)) return 1;
+        Tensor R;
+        auto r = E.batched_matmul_softmax_backward_q(in_t(0), in_t(1), in_t(2), in_t(3), in_t(4), sz(0), flag(1),
+                                                     flag(2), sc(3), R, opt_mask(5));
+        if (put(0, r)) return 1;
+        out[1] = new_tensor(R);
+        return 0;
+    }
+    case 14:
+    {
+        if (!need(7, 2, 4)) return 1;
+        Tensor gv;
+        auto r = E.batched_matmul_softmax_backward_kv(in_t(0), in_t(1), in_t(2), in_t(3), in_t(4), in_t(5), in_t(6),
+                                                      sz(0), flag(1), flag(2), sc(3), gv, opt_mask(7));
+        if (put(0, r)) return 1;
+        out[1] = new_tensor(gv);
+        return 0;
+    }
+    case 15: { if (!need(2, 1, 0)) return 1; auto r = E.col_softmax_denom(in_t(0), in_t(1)); return put(0, r); }
+    case 16:
+    {
+        if (!need(2, 2, 2)) return 1;
+        Tensor lv;
+        auto r = E.col_softmax_sparse_forward(in_t(0), in_t(1), opt_mask(2), sz(0), sc(1), lv);
+        if (put(0, r)) return 1;
+        out[1] = new_tensor(lv);
+        return 0;
+    }
+    case 17: { if (!need(2, 0, 0)) return 1; return done(E.add_inplace(in_t(0), in_t(1))); }
+    case 18: { if (!need(1, 0, 1)) return 1; return done(E.scale_inplace(in_t(0), sc(0))); }
+    case 19: { if (!need(2, 0, 1)) return 1; return done(E.axpy_inplace(in_t(0), sc(0), in_t(1))); }
+    case 20: { if (!need(1, 0, 0)) return 1; return done(E.zero(in_t(0))); }
+    case 21: { if (!need(1, 1, 0)) return 1; auto r = E.row_reduce_sum(in_t(0)); return put(0, r); }
+    case 22: { if (!need(1, 1, 0)) return 1; auto r = E.col_reduce_sum(in_t(0)); return put(0, r); }
+    case 23: { if (!need(1, 1, 0)) return 1; auto r = E.row_reduce_max(in_t(0)); return put(0, r); }
+    case 24: { if (!need(1, 1, 0)) return 1; auto r = E.col_reduce_max(in_t(0)); return put(0, r); }
+    case 25: { if (!need(2, 0, 1)) return 1; return done(E.broadcast_row_inplace(in_t(0), in_t(1), static_cast<BinaryOp>(sz(0)))); }
+    case 26: { if (!need(2, 0, 1)) return 1; return done(E.broadcast_col_inplace(in_t(0), in_t(1), static_cast<BinaryOp>(sz(0)))); }
+    case 27: { if (!need(1, 1, 1)) return 1; auto r = E.elementwise_unary(static_cast<UnaryOp>(sz(0)), in_t(0)); return put(0, r); }
+    case 28: { if (!need(2, 1, 1)) return 1; auto r = E.elementwise_binary(static_cast<BinaryOp>(sz(0)), in_t(0), in_t(1)); return put(0, r); }
+    case 29:
+    {
+        if (!need(1, 1, 3)) return 1;
+        auto r = E.elementwise_binary_scalar(static_cast<BinaryOp>(sz(0)), in_t(0), sc(1), flag(2));
+        return put(0, r);
+    }
+    case 30:
+    {
+        if (!need(2, 1, 3)) return 1;
+        auto r = E.elementwise_select_scalar_cond(static_cast<CompareOp>(sz(0)), in_t(0), sc(1), in_t(1), sc(2));
+        return put(0, r);
+    }
+    default:
+        return set_error("engine_op: unknown op " + std::to_string(op));
+    }
+}
+
+inline int eval_expr(EngineHandle* e, const std::uint8_t* instrs, std::size_t n_instrs, const std::uint8_t* vk,
+                     const std::uint32_t* vp, std::size_t n_views, const float* consts, std::size_t n_consts,
+                     std::uint32_t num_regs, void* const* inputs, std::size_t n_inputs, std::size_t rows,
+                     std::size_t cols, int vector_out, void** out)
+{
+    ExprSpec s;
+    for (std::size_t i = 0; i < n_instrs; ++i)
+    {
+        const std::uint8_t* p = instrs + 8 * i;
+        ExprInstr in;
+        in.op = p[0];
+        in.dst = p[1];
+        in.a = {p[2], p[3]};
+        in.b = {p[4], p[5]};
+        in.c = {p[6], p[7]};
+        s.instrs.push_back(in);
+    }
+    for (std::size_t i = 0; i < n_views; ++i)
+        s.views.push_back(ExprView{vk[2 * i], vk[2 * i + 1], vp[i]});
+    s.consts.assign(consts, consts + n_consts);
+    s.num_regs = num_regs;
+    std::vector<Tensor> ins;
+    for (std::size_t i = 0; i < n_inputs; ++i)
+        ins.push_back(*T(inputs[i]));
+    auto r = vector_out ? e->eng->eval_expr_reduce(s, ins, rows, cols) : e->eng->eval_expr(s, ins, rows, cols);
+    if (!r) return set_error(r.error().message);
+    *out = new_tensor(*r);
+    return 0;
+}
+
+struct GptConfigC
+{
+    std::size_t vocab_size, d_model, seq_len, num_heads, d_ff, num_layers;
+    std::uint32_t pos_enc;
+    float lr, beta1, beta2, eps, weight_decay;
+};
+
+// One training session: GPTModel + CrossEntropyLoss + AdamW on one engine,
+// issuing the reference train-step sequence (src/text_train.cpp:1181-1330):
+// begin_batch, forward, sparse CE (loss download), backward, end_batch,
+// begin_batch, AdamW step, zero_grad, end_batch.
+struct GptSession
+{
+    ComputeEngine* eng = nullptr;
+    Model model;
+    std::vector<TensorRef> params, grads;
+    std::unique_ptr<AdamW> opt;
+    CrossEntropyLoss ce;
+    std::size_t vocab = 0, seq = 0, batch = 0, num_valid = 0;
+    Tensor tokens, labels, mask, logits;
+    bool has_batch = false, has_mask = false;
+};
+
+inline int gpt_create(EngineHandle* e, const GptConfigC* c, GptSession** out)
+{
+    GptConfig cfg;
+    cfg.vocab_size = c->vocab_size;
+    cfg.d_model = c->d_model;
+    cfg.seq_len = c->seq_len;
+    cfg.num_heads = c->num_heads;
+    cfg.d_ff = c->d_ff;
+    cfg.num_layers = c->num_layers;
+    cfg.pos_enc = static_cast<PosEncodingType>(c->pos_enc);
+    auto m = build_gpt_model(*e->eng, cfg);
+    if (!m) return set_error(m.error().message);
+    auto s = std::make_unique<GptSession>();
+    s->eng = e->eng.get();
+    s->model = std::move(*m);
+    s->params = s->model.parameters();
+    s->grads = s->model.param_gradients();
+    s->opt = std::make_unique<AdamW>(*s->eng, s->params, s->grads, c->lr, c->beta1, c->beta2, c->eps, c->weight_decay);
+    s->vocab = c->vocab_size;
+    if (auto r = s->eng->end_batch(); !r) return set_error(r.error().message);
+    *out = s.release();
+    return 0;
+}
+
+inline int gpt_param_shape(const GptSession* g, std::size_t i, std::size_t* r, std::size_t* c)
+{
+    if (i >= g->params.size()) return set_error("gpt: parameter index out of range");
+    *r = g->params[i].get().rows();
+    *c = g->params[i].get().cols();
+    return 0;
+}
+
+inline int gpt_set_param(GptSession* g, std::size_t i, const float* data)
+{
+    if (i >= g->params.size()) return set_error("gpt: parameter index out of range");
+    Tensor& p = g->params[i].get();
+    Matrix m(p.rows(), p.cols());
+    std::memcpy(m.data(), data, m.size() * sizeof(float));
+    auto r = g->eng->copy_from(p, m);
+    return r ? 0 : set_error(r.error().message);
+}
+
+inline int gpt_read(GptSession* g, const Tensor& t, float* out)
+{
+    auto m = g->eng->to_matrix(t);
+    if (!m) return set_error(m.error().message);
+    std::memcpy(out, m->data(), m->size() * sizeof(float));
+    return 0;
+}
+
+inline int gpt_set_doc_ids(GptSession* g, const std::uint64_t* ids, std::size_t n)
+{
+    std::vector<std::size_t> v(ids, ids + n);
+    g->model.set_doc_ids(v);
+    return 0;
+}
+
+inline int gpt_load_batch(GptSession* g, const float* tokens, std::size_t seq, std::size_t batch,
+                          const std::uint64_t* labels, const float* loss_mask)
+{
+    const std::size_t n = seq * batch;
+    Matrix tk(seq, batch);
+    std::memcpy(tk.data(), tokens, n * sizeof(float));
+    auto t = g->eng->from_matrix(tk);
+    if (!t) return set_error(t.error().message);
+    Matrix lb(1, n);
+    std::vector<std::size_t> lab(labels, labels + n);
+    for (std::size_t i = 0; i < n; ++i) lb.data()[i] = static_cast<Scalar>(lab[i]);
+    auto l = g->eng->from_matrix(lb);
+    if (!l) return set_error(l.error().message);
+    std::vector<Scalar> mvec;
+    g->has_mask = loss_mask != nullptr;
+    if (g->has_mask)
+    {
+        mvec.assign(loss_mask, loss_mask + n);
+        Matrix mm(1, n);
+        for (std::size_t i = 0; i < n; ++i) mm.data()[i] = loss_mask[i] >= 0.5f ? 1.0f : 0.0f;
+        auto mt = g->eng->from_matrix(mm);
+        if (!mt) return set_error(mt.error().message);
+        g->mask = *mt;
+    }
+    g->tokens = *t;
+    g->labels = *l;
+    g->num_valid = CrossEntropyLoss::count_valid(lab, mvec, g->vocab);
+    g->seq = seq;
+    g->batch = batch;
+    g->has_batch = true;
+    return 0;
+}
+
+inline int gpt_forward_loss(GptSession* g, float* loss)
+{
+    if (!g->has_batch) return set_error("gpt: no batch loaded");
+    if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
+    auto lg = g->model.forward(g->tokens);
+    if (!lg) return set_error(lg.error().message);
+    g->logits = *lg;
+    auto l = g->ce.forward_sparse_resident(*g->eng, g->logits, g->labels, g->has_mask ? &g->mask : nullptr, g->vocab,
+                                           g->num_valid);
+    if (!l) return set_error(l.error().message);
+    *loss = *l;
+    if (auto r = g->eng->flush_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
+inline int gpt_backward(GptSession* g)
+{
+    auto gr = g->ce.backward();
+    if (!gr) return set_error(gr.error().message);
+    auto b = g->model.backward(*gr);
+    if (!b) return set_error(b.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
+inline int gpt_step(GptSession* g)
+{
+    if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
+    if (auto r = g->opt->step(); !r) return set_error(r.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
+inline int gpt_zero_grad(GptSession* g)
+{
+    if (auto r = g->opt->zero_grad(); !r) return set_error(r.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
+inline int gpt_train_step(GptSession* g, float* loss)
+{
+    if (int rc = gpt_forward_loss(g, loss)) return rc;
+    if (int rc = gpt_backward(g)) return rc;
+    if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
+    if (auto r = g->opt->step(); !r) return set_error(r.error().message);
+    if (auto r = g->opt->zero_grad(); !r) return set_error(r.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
+inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads, int alibi, const float* slopes,
+                          const std::uint64_t* doc_ids, std::size_t n_doc, float* out)
+{
+    if (n_doc != 0 && n_doc < batch * seq) return set_error("build_attention_mask: doc_ids too small for batch*seq");
+    std::vector<Scalar> sl;
+    if (alibi) sl.assign(slopes, slopes + heads);
+    std::vector<std::size_t> d(doc_ids, doc_ids + n_doc);
+    Matrix m = build_attention_mask(batch, seq, heads, alibi != 0, sl, d);
+    std::memcpy(out, m.data(), m.size() * sizeof(float));
+    return 0;
+}
+
+} // namespace nn::capi
+
+// Defines every symbol of include/nnhip_engine.h with the given prefix.
+// MAKE_ENGINE must be an expression yielding std::unique_ptr<nn::ComputeEngine>
+// or returning an error string through `err` (a std::string).
+#define NN_CAPI_CAT2(a, b) a##b
+#define NN_CAPI_CAT(a, b) NN_CAPI_CAT2(a, b)
+#define NN_DEFINE_ENGINE_CAPI(P, MAKE_ENGINE)                                                                       \
+    extern "C" {                                                                                                    \
+    const char* NN_CAPI_CAT(P, last_error)(void) { return nn::capi::last_error().c_str(); }                        \
+    int NN_CAPI_CAT(P, engine_create)(void** out)                                                                  \
+    {                                                                                                               \
+        std::string err;                                                                                            \
+        std::unique_ptr<nn::ComputeEngine> eng = MAKE_ENGINE;                                                       \
+        if (!eng) return nn::capi::set_error(err.empty() ? "engine creation failed" : err);                        \
+        *out = new nn::capi::EngineHandle{std::move(eng)};                                                          \
+        return 0;                                                                                                   \
+    }                                                                                                               \
+    void NN_CAPI_CAT(P, engine_destroy)(void* e) { delete static_cast<nn::capi::EngineHandle*>(e); }             \
+    int NN_CAPI_CAT(P, engine_sync)(void* e)                                                                       \
+    {                                                                                                               \
+        auto r = static_cast<nn::capi::EngineHandle*>(e)->eng->end_batch();                                        \
+        return r ? 0 : nn::capi::set_error(r.error().message);                                                      \
+    }                                                                                                               \
+    void* NN_CAPI_CAT(P, tensor_create)(void* e, size_t r, size_t c)                                               \
+    {                                                                                                               \
+        return nn::capi::tensor_create(static_cast<nn::capi::EngineHandle*>(e), r, c);                             \
+    }                                                                                                               \
+    void* NN_CAPI_CAT(P, tensor_from_host)(void* e, const float* d, size_t r, size_t c)                            \
+    {                                                                                                               \
+        return nn::capi::tensor_from_host(static_cast<nn::capi::EngineHandle*>(e), d, r, c);                       \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, tensor_to_host)(void* e, const void* t, float* out)                                        \
+    {                                                                                                               \
+        return nn::capi::tensor_to_host(static_cast<nn::capi::EngineHandle*>(e), t, out);                          \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, tensor_copy_from_host)(void* e, void* t, const float* d)                                    \
+    {                                                                                                               \
+        return nn::capi::tensor_copy_from_host(static_cast<nn::capi::EngineHandle*>(e), t, d);                     \
+    }                                                                                                               \
+    size_t NN_CAPI_CAT(P, tensor_rows)(const void* t) { return nn::capi::T(t)->rows(); }                          \
+    size_t NN_CAPI_CAT(P, tensor_cols)(const void* t) { return nn::capi::T(t)->cols(); }                          \
+    void* NN_CAPI_CAT(P, tensor_data_ptr)(const void* t) { return nn::capi::tensor_data_ptr(t); }                 \
+    void NN_CAPI_CAT(P, tensor_release)(void* t) { delete nn::capi::T(t); }                                        \
+    int NN_CAPI_CAT(P, engine_op)(void* e, int op, void* const* in, size_t n_in, void** out, size_t n_out,        \
+                                  const double* args, size_t n_args)                                                \
+    {                                                                                                               \
+        return nn::capi::engine_op(static_cast<nn::capi::EngineHandle*>(e), op, in, n_in, out, n_out, args,       \
+                                   n_args);                                                                         \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, engine_eval_expr)(void* e, const uint8_t* ins, size_t ni, const uint8_t* vk,               \
+                                         const uint32_t* vp, size_t nv, const float* cs, size_t nc, uint32_t nr,   \
+                                         void* const* inputs, size_t nin, size_t rows, size_t cols, int vec,       \
+                                         void** out)                                                                \
+    {                                                                                                               \
+        return nn::capi::eval_expr(static_cast<nn::capi::EngineHandle*>(e), ins, ni, vk, vp, nv, cs, nc, nr,      \
+                                   inputs, nin, rows, cols, vec, out);                                              \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_create)(void* e, const void* cfg, void** out)                                           \
+    {                                                                                                               \
+        nn::capi::GptSession* s = nullptr;                                                                          \
+        int rc = nn::capi::gpt_create(static_cast<nn::capi::EngineHandle*>(e),                                     \
+                                      static_cast<const nn::capi::GptConfigC*>(cfg), &s);                          \
+        *out = s;                                                                                                   \
+        return rc;                                                                                                  \
+    }                                                                                                               \
+    void NN_CAPI_CAT(P, gpt_destroy)(void* g) { delete static_cast<nn::capi::GptSession*>(g); }                   \
+    size_t NN_CAPI_CAT(P, gpt_num_params)(const void* g)                                                           \
+    {                                                                                                               \
+        return static_cast<const nn::capi::GptSession*>(g)->params.size();                                        \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_param_shape)(const void* g, size_t i, size_t* r, size_t* c)                             \
+    {                                                                                                               \
+        return nn::capi::gpt_param_shape(static_cast<const nn::capi::GptSession*>(g), i, r, c);                    \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_set_param)(void* g, size_t i, const float* d)                                           \
+    {                                                                                                               \
+        return nn::capi::gpt_set_param(static_cast<nn::capi::GptSession*>(g), i, d);                               \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_get_param)(void* g, size_t i, float* out)                                               \
+    {                                                                                                               \
+        auto* s = static_cast<nn::capi::GptSession*>(g);                                                            \
+        if (i >= s->params.size()) return nn::capi::set_error("gpt: parameter index out of range");                \
+        return nn::capi::gpt_read(s, s->params[i].get(), out);                                                      \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_get_grad)(void* g, size_t i, float* out)                                                \
+    {                                                                                                               \
+        auto* s = static_cast<nn::capi::GptSession*>(g);                                                            \
+        if (i >= s->grads.size()) return nn::capi::set_error("gpt: parameter index out of range");                 \
+        return nn::capi::gpt_read(s, s->grads[i].get(), out);                                                       \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_set_doc_ids)(void* g, const uint64_t* ids, size_t n)                                    \
+    {                                                                                                               \
+        return nn::capi::gpt_set_doc_ids(static_cast<nn::capi::GptSession*>(g), ids, n);                           \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_load_batch)(void* g, const float* tk, size_t seq, size_t batch, const uint64_t* lb,    \
+                                       const float* mask)                                                           \
+    {                                                                                                               \
+        return nn::capi::gpt_load_batch(static_cast<nn::capi::GptSession*>(g), tk, seq, batch, lb, mask);          \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_forward_loss)(void* g, float* loss)                                                     \
+    {                                                                                                               \
+        return nn::capi::gpt_forward_loss(static_cast<nn::capi::GptSession*>(g), loss);                            \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_logits)(void* g, float* out)                                                            \
+    {                                                                                                               \
+        auto* s = static_cast<nn::capi::GptSession*>(g);                                                            \
+        if (!s->logits.valid()) return nn::capi::set_error("gpt: no forward pass yet");                            \
+        return nn::capi::gpt_read(s, s->logits, out);                                                               \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_backward)(void* g) { return nn::capi::gpt_backward(static_cast<nn::capi::GptSession*>(g)); } \
+    int NN_CAPI_CAT(P, gpt_optimizer_step)(void* g) { return nn::capi::gpt_step(static_cast<nn::capi::GptSession*>(g)); } \
+    int NN_CAPI_CAT(P, gpt_zero_grad)(void* g) { return nn::capi::gpt_zero_grad(static_cast<nn::capi::GptSession*>(g)); } \
+    int NN_CAPI_CAT(P, build_attention_mask)(size_t batch, size_t seq, size_t heads, int alibi, const float* slopes, \
+                                             const uint64_t* doc_ids, size_t n_doc, float* out)                     \
+    {                                                                                                               \
+        return nn::capi::attention_mask(batch, seq, heads, alibi, slopes, doc_ids, n_doc, out);                    \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_train_step)(void* g, float* loss)                                                       \
+    {                                                                                                               \
+        return nn::capi::gpt_train_step(static_cast<nn::capi::GptSession*>(g), loss);                              \
+    }                                                                                                               \
+    }

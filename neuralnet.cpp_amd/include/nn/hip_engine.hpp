@@ -1,0 +1,153 @@
+// hip_engine.hpp — nn::ComputeEngine on one MI355X (gfx950) GPU.
+//
+// Drop-in replacement for the reference's GPU engines (GpuEngine, Vulkan,
+// include/neuralnet.cpp/gpu_engine.hpp:49-961; CudaEngine,
+// include/neuralnet.cpp/cuda_engine.hpp) behind the unchanged ComputeEngine
+// interface. Every primitive validates shapes on the host exactly as the
+// CPU engine does, allocates its outputs from a per-engine caching pool and
+// enqueues hand-written HIP kernels (include/nnhip_kernels.h) on the engine's
+// own stream. Nothing falls back to the CPU: an unsupported shape is an Error.
+//
+// Ordering: all work goes to one in-order stream, so a buffer released by a
+// Tensor can be handed to the next allocation immediately (stream-ordered
+// reuse). to_matrix / from_matrix / copy_from and end_batch / flush_batch
+// synchronise the stream, matching the reference's batch semantics
+// (compute_engine.hpp:93-118).
+#pragma once
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "compute_engine.hpp"
+
+namespace nn
+{
+
+class DevicePool;
+
+class HipEngine final : public ComputeEngine
+{
+public:
+    // Engine on the current HIP device. Check ok() / error() after construction.
+    HipEngine();
+    ~HipEngine() override;
+    HipEngine(const HipEngine&) = delete;
+    HipEngine& operator=(const HipEngine&) = delete;
+
+    [[nodiscard]] bool ok() const noexcept { return ok_; }
+    [[nodiscard]] const std::string& error() const noexcept { return init_error_; }
+    [[nodiscard]] void* stream() const noexcept { return stream_; }
+
+    Device device() const noexcept override { return Device::GPU; }
+    Result<void> begin_batch() override;
+    Result<void> end_batch() override;
+    Result<void> flush_batch() override;
+    Result<void> begin_expr() override { return {}; }
+    Result<void> end_expr() override { return {}; }
+
+    Tensor create_tensor(std::size_t rows, std::size_t cols) override;
+    Result<Tensor> from_matrix(const Matrix& m) override;
+    Result<Matrix> to_matrix(const Tensor& t) override;
+    Result<void> copy_from(Tensor& dst, const Matrix& src) override;
+    Result<Tensor> clone(const Tensor& src) override;
+
+    Result<Tensor> slice_rows(const Tensor& src, std::size_t start_row, std::size_t count) override;
+    Result<void> insert_rows(Tensor& dst, std::size_t dst_start_row, const Tensor& src) override;
+    Result<Tensor> gather_rows(const Tensor& table, const Tensor& indices) override;
+    Result<void> scatter_add_rows(Tensor& dst, const Tensor& indices, const Tensor& grad) override;
+    Result<Tensor> rearrange_3d(const Tensor& x, std::size_t M, std::size_t B, std::size_t N, bool inverse) override;
+    Result<Tensor> transpose(const Tensor& A) override;
+
+    Result<Tensor> matmul(const Tensor& A, const Tensor& B, bool transA, bool transB) override;
+    Result<Tensor> batched_matmul(const Tensor& A, const Tensor& B, std::size_t batch, bool transA, bool transB,
+                                  Scalar alpha) override;
+    Result<Tensor> batched_matmul_reduce(const Tensor& A, const Tensor& B, std::size_t batch, ReduceOp op,
+                                         bool transA, bool transB, Scalar alpha, bool reduce_cols,
+                                         const Tensor* mask) override;
+    Result<Tensor> batched_matmul_softmax_denom(const Tensor& A, const Tensor& B, const Tensor& row_max,
+                                                std::size_t batch, bool transA, bool transB, Scalar alpha,
+                                                const Tensor* mask) override;
+    Result<Tensor> batched_matmul_softmax_apply(const Tensor& A, const Tensor& B, const Tensor& V,
+                                                const Tensor& row_max, const Tensor& denom, std::size_t batch,
+                                                bool transA, bool transB, Scalar alpha, const Tensor* mask) override;
+    Result<Tensor> batched_matmul_softmax_backward_q(const Tensor& A, const Tensor& B, const Tensor& P,
+                                                     const Tensor& row_max, const Tensor& denom, std::size_t batch,
+                                                     bool transA, bool transB, Scalar alpha, Tensor& r_out,
+                                                     const Tensor* mask) override;
+    Result<Tensor> batched_matmul_softmax_backward_kv(const Tensor& A, const Tensor& B, const Tensor& P,
+                                                      const Tensor& G, const Tensor& R, const Tensor& row_max,
+                                                      const Tensor& denom, std::size_t batch, bool transA,
+                                                      bool transB, Scalar alpha, Tensor& grad_v_out,
+                                                      const Tensor* mask) override;
+
+    Result<Tensor> col_softmax_denom(const Tensor& logits, const Tensor& col_max) override;
+    Result<Tensor> col_softmax_sparse_forward(const Tensor& logits, const Tensor& labels, const Tensor* mask,
+                                              std::size_t vocab_size, Scalar inv_num_valid,
+                                              Tensor& loss_vec_out) override;
+
+    Result<void> add_inplace(Tensor& A, const Tensor& B) override;
+    Result<void> scale_inplace(Tensor& A, Scalar s) override;
+    Result<void> axpy_inplace(Tensor& A, Scalar scalar, const Tensor& B) override;
+    Result<void> zero(Tensor& A) override;
+
+    Result<Tensor> row_reduce_sum(const Tensor& A) override;
+    Result<Tensor> col_reduce_sum(const Tensor& A) override;
+    Result<Tensor> row_reduce_max(const Tensor& A) override;
+    Result<Tensor> col_reduce_max(const Tensor& A) override;
+
+    Result<void> broadcast_row_inplace(Tensor& A, const Tensor& row_vec, BinaryOp op) override;
+    Result<void> broadcast_col_inplace(Tensor& A, const Tensor& col_vec, BinaryOp op) override;
+
+    Result<Tensor> elementwise_unary(UnaryOp op, const Tensor& A) override;
+    Result<Tensor> elementwise_binary(BinaryOp op, const Tensor& A, const Tensor& B) override;
+    Result<Tensor> elementwise_binary_scalar(BinaryOp op, const Tensor& A, Scalar s, bool scalar_first) override;
+    Result<Tensor> elementwise_select_scalar_cond(CompareOp cmp, const Tensor& A, Scalar scalar_b,
+                                                  const Tensor& then_t, Scalar scalar_else) override;
+
+    Result<Tensor> eval_expr(const ExprSpec& spec, std::span<const Tensor> inputs, std::size_t rows,
+                             std::size_t cols) override;
+    Result<Tensor> eval_expr_reduce(const ExprSpec& spec, std::span<const Tensor> inputs, std::size_t rows,
+                                    std::size_t cols) override;
+
+    // Bytes currently cached (free) and held by live tensors in the pool.
+    [[nodiscard]] std::size_t pool_cached_bytes() const;
+    [[nodiscard]] std::size_t pool_live_bytes() const;
+
+    // Measurement hook: while enabled, every GEMM launch (matmul and
+    // batched_matmul) is bracketed by HIP events on the engine's stream.
+    // read_gemm_profile() waits for the stream and returns the number of
+    // launches, their algorithmic FLOPs (2*M*N*K per batch) and the summed
+    // kernel time in milliseconds, then clears the record.
+    void set_gemm_profile(bool on);
+    Result<void> read_gemm_profile(double& launches, double& flops, double& ms);
+
+private:
+    Result<Tensor> alloc_(std::size_t rows, std::size_t cols);
+    Result<std::shared_ptr<DeviceBuffer>> scratch_(std::size_t bytes);
+    Result<void> kernel_(int rc, const char* what);
+    Result<void> need_gpu_(std::initializer_list<const Tensor*> ts, const char* what) const;
+    Result<Tensor> eval_impl_(const ExprSpec& spec, std::span<const Tensor> inputs, std::size_t rows,
+                              std::size_t cols, bool vector_out);
+
+    void prof_begin_();
+    void prof_end_(double flops);
+
+    struct ProfRecord
+    {
+        void* start;
+        void* stop;
+        double flops;
+    };
+    bool profile_ = false;
+    std::vector<ProfRecord> prof_;
+    std::vector<void*> event_pool_;
+
+    bool ok_ = false;
+    std::string init_error_;
+    int device_ = 0;
+    void* stream_ = nullptr;
+    std::shared_ptr<DevicePool> pool_;
+};
+
+} // namespace nn

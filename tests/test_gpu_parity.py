@@ -1,0 +1,366 @@
+"""HIP engine vs the CPU oracle, primitive by primitive, through the C-ABI.
+
+Every test builds seeded inputs, runs the same ComputeEngine primitive on the
+HIP engine (libnnhip.so) and on the CPU restatement (libnnoracle.so), and
+compares. Bars: bit-exact for index / layout / gather / scatter / max work;
+normwise max|d|/max|ref| for floating point, with the tolerance in each test.
+"""
+import numpy as np
+import pytest
+
+from helpers import causal_mask, doc_ids_from_lengths, doc_lengths, doc_mask, grad_errs, normal, nrm_err, uniform
+
+pytestmark = pytest.mark.gpu
+
+
+def both(hip, cpu, fn):
+    """Run fn(engine) on both engines; return (hip_result, cpu_result) as numpy."""
+    def to_np(x):
+        if isinstance(x, (list, tuple)):
+            return [to_np(y) for y in x]
+        return x.numpy() if hasattr(x, "numpy") else x
+    return to_np(fn(hip)), to_np(fn(cpu))
+
+
+# ── GEMM ────────────────────────────────────────────────────────────────────
+@pytest.mark.parametrize("tA", [False, True])
+@pytest.mark.parametrize("tB", [False, True])
+@pytest.mark.parametrize("M,N,K", [(4, 6, 4), (37, 53, 29), (128, 128, 16), (64, 256, 48), (300, 70, 130),
+                                   (256, 384, 256)])
+def test_matmul(hip, cpu, M, N, K, tA, tB):
+    rng = np.random.default_rng(M * 1000 + N * 10 + K)
+    A = uniform(rng, (K, M) if tA else (M, K))
+    B = uniform(rng, (N, K) if tB else (K, N))
+    h, c = both(hip, cpu, lambda e: e.matmul(e.tensor(A), e.tensor(B), tA, tB))
+    ref = (A.T if tA else A).astype(np.float64) @ (B.T if tB else B).astype(np.float64)
+    assert h.shape == (M, N)
+    assert nrm_err(h, ref) <= 1e-5
+    assert nrm_err(h, c) <= 1e-5
+    # elementwise a-priori bound |dC| <= 2K * 2^-24 * (|A||B|)_ij
+    absprod = np.abs(A.T if tA else A).astype(np.float64) @ np.abs(B.T if tB else B).astype(np.float64)
+    assert np.all(np.abs(h - ref) <= 2 * K * 2.0 ** -24 * absprod + 1e-30)
+
+
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+def test_batched_matmul_alpha(hip, cpu, tA, tB):
+    rng = np.random.default_rng(7)
+    batch, M, N, K = 3, 20, 36, 12
+    A = uniform(rng, (batch * (K if tA else M), M if tA else K))
+    B = uniform(rng, (batch * (N if tB else K), K if tB else N))
+    h, c = both(hip, cpu, lambda e: e.batched_matmul(e.tensor(A), e.tensor(B), batch, tA, tB, 0.35))
+    assert h.shape == (batch * M, N)
+    assert nrm_err(h, c) <= 1e-5
+
+
+def test_batched_matmul_attention_shapes(hip, cpu):
+    """The materialised-attention products: S = a*Q^T K (K=64), PV (M=64), dV, dQ."""
+    rng = np.random.default_rng(11)
+    BH, d, T = 4, 64, 256
+    Q, Kt, V = normal(rng, (BH * d, T)), normal(rng, (BH * d, T)), normal(rng, (BH * d, T))
+    A = np.abs(normal(rng, (BH * T, T)))
+    for args in [(Q, Kt, True, False, 0.125), (V, A, False, True, 1.0), (V, A, False, False, 1.0),
+                 (Kt, A, False, True, 0.125)]:
+        X, Y, ta, tb, al = args
+        h, c = both(hip, cpu, lambda e: e.batched_matmul(e.tensor(X), e.tensor(Y), BH, ta, tb, al))
+        assert nrm_err(h, c) <= 1e-5
+
+
+# ── elementwise / in-place / broadcast / reductions ─────────────────────────
+UNARY = ["Neg", "Exp", "Log", "Sqrt", "Rsqrt", "Abs", "Tanh"]
+BINARY = ["Add", "Sub", "Mul", "Div", "Max", "Min"]
+
+
+@pytest.mark.parametrize("op", UNARY)
+def test_unary(hip, cpu, op):
+    rng = np.random.default_rng(3)
+    A = uniform(rng, (33, 77), 0.05, 4.0) if op in ("Log", "Sqrt", "Rsqrt") else uniform(rng, (33, 77), -4, 4)
+    h, c = both(hip, cpu, lambda e: e.elementwise_unary(op, e.tensor(A)))
+    exact = op in ("Neg", "Abs")
+    assert (np.array_equal(h, c) if exact else nrm_err(h, c) <= 2e-7 * 8)
+
+
+@pytest.mark.parametrize("op", BINARY)
+def test_binary_and_scalar(hip, cpu, op):
+    rng = np.random.default_rng(4)
+    A, B = uniform(rng, (129, 65)), uniform(rng, (129, 65), 0.5, 2.0)
+    h, c = both(hip, cpu, lambda e: e.elementwise_binary(op, e.tensor(A), e.tensor(B)))
+    assert np.array_equal(h, c)
+    for first in (False, True):
+        h, c = both(hip, cpu, lambda e: e.elementwise_binary_scalar(op, e.tensor(B), 0.75, first))
+        assert np.array_equal(h, c)
+
+
+@pytest.mark.parametrize("cmp", ["Lt", "Le", "Gt", "Ge", "Eq", "Ne"])
+def test_select(hip, cpu, cmp):
+    rng = np.random.default_rng(5)
+    A = np.round(uniform(rng, (40, 50), -2, 2))
+    T = uniform(rng, (40, 50))
+    h, c = both(hip, cpu, lambda e: e.elementwise_select_scalar_cond(cmp, e.tensor(A), 0.0, e.tensor(T), -7.5))
+    assert np.array_equal(h, c)
+
+
+def test_inplace_ops(hip, cpu):
+    rng = np.random.default_rng(6)
+    A, B = uniform(rng, (301, 17)), uniform(rng, (301, 17))
+
+    def run(e):
+        a, b = e.tensor(A), e.tensor(B)
+        e.add_inplace(a, b)
+        e.scale_inplace(a, 0.9)
+        e.axpy_inplace(a, 0.1, b)
+        z = e.clone(a)
+        e.zero(z)
+        return [a, z]
+    (ha, hz), (ca, cz) = both(hip, cpu, run)
+    assert nrm_err(ha, ca) <= 1e-6
+    assert not hz.any() and not cz.any()
+
+
+@pytest.mark.parametrize("shape", [(1, 8192), (768, 8192), (97, 3), (5, 5000), (3000, 40)])
+def test_reductions(hip, cpu, shape):
+    rng = np.random.default_rng(8)
+    A = uniform(rng, shape)
+    for name in ("row_reduce_max", "col_reduce_max"):
+        h, c = both(hip, cpu, lambda e: getattr(e, name)(e.tensor(A)))
+        assert np.array_equal(h, c), name
+    for name in ("row_reduce_sum", "col_reduce_sum"):
+        h, c = both(hip, cpu, lambda e: getattr(e, name)(e.tensor(A)))
+        assert nrm_err(h, c) <= 1e-5, name
+
+
+@pytest.mark.parametrize("op", BINARY)
+def test_broadcast(hip, cpu, op):
+    rng = np.random.default_rng(9)
+    A = uniform(rng, (48, 36))
+    r, cvec = uniform(rng, (48, 1), 0.5, 2), uniform(rng, (1, 36), 0.5, 2)
+
+    def run(e):
+        a, b = e.tensor(A), e.tensor(A)
+        e.broadcast_row_inplace(a, e.tensor(r), op)
+        e.broadcast_col_inplace(b, e.tensor(cvec), op)
+        return [a, b]
+    (h1, h2), (c1, c2) = both(hip, cpu, run)
+    assert np.array_equal(h1, c1) and np.array_equal(h2, c2)
+
+
+# ── layout / gather / scatter (bit-exact) ───────────────────────────────────
+@pytest.mark.parametrize("shape", [(1, 1), (3, 1000), (8192, 768), (65, 130)])
+def test_transpose(hip, cpu, shape):
+    A = uniform(np.random.default_rng(1), shape)
+    h, c = both(hip, cpu, lambda e: e.transpose(e.tensor(A)))
+    assert np.array_equal(h, c) and np.array_equal(h, A.T)
+
+
+@pytest.mark.parametrize("M,B,N", [(768, 8, 64), (5, 3, 7), (64, 12, 1024)])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_rearrange_3d(hip, cpu, M, B, N, inverse):
+    X = uniform(np.random.default_rng(2), (B * M, N) if inverse else (M, B * N))
+    h, c = both(hip, cpu, lambda e: e.rearrange_3d(e.tensor(X), M, B, N, inverse))
+    assert np.array_equal(h, c)
+
+
+def test_slice_insert(hip, cpu):
+    A = uniform(np.random.default_rng(3), (20, 9))
+
+    def run(e):
+        a = e.tensor(A)
+        s = e.slice_rows(a, 5, 7)
+        d = e.create_tensor(30, 9)
+        e.zero(d)
+        e.insert_rows(d, 11, s)
+        return [s, d]
+    (hs, hd), (cs, cd) = both(hip, cpu, run)
+    assert np.array_equal(hs, cs) and np.array_equal(hd, cd)
+
+
+def test_gather_bit_exact(hip, cpu):
+    rng = np.random.default_rng(10)
+    table = normal(rng, (1000, 96))
+    idx = rng.integers(0, 1000, size=(8, 64)).astype(np.float32)
+    idx.flat[[0, 5, 77]] = [1000.0, -3.0, 5000.0]   # out of range -> zero rows
+    idx.flat[9] = -0.5                             # truncates to row 0
+    h, c = both(hip, cpu, lambda e: e.gather_rows(e.tensor(table), e.tensor(idx)))
+    assert np.array_equal(h, c)
+    assert not h[0].any() and np.array_equal(h[9], table[0])
+
+
+@pytest.mark.parametrize("num,vocab,D", [(8192, 32000, 768), (1024, 50, 33), (3, 4, 5), (5000, 7, 64)])
+def test_scatter_add_bit_exact(hip, cpu, num, vocab, D):
+    rng = np.random.default_rng(num + vocab)
+    dst = normal(rng, (vocab, D))
+    grad = normal(rng, (num, D))
+    idx = rng.integers(0, vocab, size=num).astype(np.float32)
+    idx[::17] = vocab + 3   # ignored
+
+    def run(e):
+        d = e.tensor(dst)
+        e.scatter_add_rows(d, e.tensor(idx.reshape(-1, 1)), e.tensor(grad))
+        return d
+    h, c = both(hip, cpu, run)
+    assert np.array_equal(h, c)
+
+
+# ── fused attention primitives ──────────────────────────────────────────────
+def _attn_inputs(rng, batch, M, N, K, tA, tB):
+    A = uniform(rng, (batch * (K if tA else M), M if tA else K))
+    B = uniform(rng, (batch * (N if tB else K), K if tB else N))
+    return A, B
+
+
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_fused_attention_small(hip, cpu, tA, tB, masked):
+    """matmul_fusion_test shapes: batch 2, M 4, N 6, K 4, D 5, alpha 0.35 (src/matmul_fusion_test.cpp:257-281)."""
+    rng = np.random.default_rng(2026)
+    batch, M, N, K, D, alpha = 2, 4, 6, 4, 5, 0.35
+    A, B = _attn_inputs(rng, batch, M, N, K, tA, tB)
+    mask = np.where(np.arange(N)[None, :] > np.arange(M)[:, None], -np.inf, 0.0).astype(np.float32) if masked else None
+    V = uniform(rng, (batch * N, D))
+    P = uniform(rng, (batch * M, N))
+    G = uniform(rng, (batch * M, K))
+
+    def run(e):
+        a, b = e.tensor(A), e.tensor(B)
+        mk = e.tensor(mask) if masked else None
+        outs = [e.batched_matmul_reduce(a, b, batch, op, tA, tB, alpha, True, mk) for op in ("Max", "Sum", "Min")]
+        outs += [e.batched_matmul_reduce(a, b, batch, "Max", tA, tB, alpha, False, mk)]
+        m = outs[0]
+        l = e.batched_matmul_softmax_denom(a, b, m, batch, tA, tB, alpha, mk)
+        o = e.batched_matmul_softmax_apply(a, b, e.tensor(V), m, l, batch, tA, tB, alpha, mk)
+        dq, r = e.batched_matmul_softmax_backward_q(a, b, e.tensor(P), m, l, batch, tA, tB, alpha, mk)
+        dk, dv = e.batched_matmul_softmax_backward_kv(a, b, e.tensor(P), e.tensor(G), r, m, l, batch, tA, tB, alpha,
+                                                      mk)
+        return outs + [l, o, dq, r, dk, dv]
+    h, c = both(hip, cpu, run)
+    for i, (x, y) in enumerate(zip(h, c)):
+        assert nrm_err(x, y) <= 1e-5, i
+
+
+def test_causal_attention_c2_shape(hip, cpu):
+    """Config-2 layout at reduced size (the oracle is serial): BH 8, T 256, d 64, causal, alpha 1/8."""
+    rng = np.random.default_rng(22)
+    BH, T, d = 8, 256, 64
+    Q, K = normal(rng, (BH * d, T)), normal(rng, (BH * d, T))
+    Vt = normal(rng, (BH * T, d))
+    mask = causal_mask(T)
+
+    def run(e):
+        q, k, mk = e.tensor(Q), e.tensor(K), e.tensor(mask)
+        m = e.batched_matmul_reduce(q, k, BH, "Max", True, False, 0.125, True, mk)
+        l = e.batched_matmul_softmax_denom(q, k, m, BH, True, False, 0.125, mk)
+        o = e.batched_matmul_softmax_apply(q, k, e.tensor(Vt), m, l, BH, True, False, 0.125, mk)
+        return [m, l, o]
+    (hm, hl, ho), (cm, cl, co) = both(hip, cpu, run)
+    assert nrm_err(hm, cm) <= 1e-5
+    assert nrm_err(hl, cl) <= 1e-5
+    assert nrm_err(ho, co) <= 1e-4
+
+
+def test_doc_masked_attention_backward(hip, cpu):
+    """Config-5 primitives on one packed row at reduced size: H 4, T 256, d 64, docs U[16,96]."""
+    rng = np.random.default_rng(5)
+    H, T, d = 4, 256, 64
+    ids = doc_ids_from_lengths(doc_lengths(rng, T, 16, 96))
+    mask = doc_mask(ids)
+    Q, K, V, dO = (normal(rng, (H * d, T)) for _ in range(4))
+
+    def run(e):
+        q, k, v, g, mk = e.tensor(Q), e.tensor(K), e.tensor(V), e.tensor(dO), e.tensor(mask)
+        m = e.batched_matmul_reduce(q, k, H, "Max", True, False, 0.125, True, mk)
+        l = e.batched_matmul_softmax_denom(q, k, m, H, True, False, 0.125, mk)
+        P = e.batched_matmul(g, v, H, True, False)
+        G = e.rearrange_3d(e.transpose(g), T, H, d)
+        dq, r = e.batched_matmul_softmax_backward_q(q, k, P, m, l, H, True, False, 0.125, mk)
+        dk, dv = e.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, l, H, True, False, 0.125, mk)
+        return [dq, r, dk, dv]
+    h, c = both(hip, cpu, run)
+    for x, y in zip(h, c):
+        assert nrm_err(x, y) <= 1e-3
+
+
+# ── column softmax / sparse cross-entropy ───────────────────────────────────
+@pytest.mark.parametrize("C,N", [(1024, 1024), (37, 11), (5000, 300)])
+def test_col_softmax(hip, cpu, C, N):
+    rng = np.random.default_rng(C + N)
+    L = normal(rng, (C, N), 3.0)
+    labels = rng.integers(0, C, size=N).astype(np.float32)
+    labels[::7] = C + 5     # invalid -> zero column
+    labels[3] = -2.0        # negative labels read as class 0 (cpu_engine.hpp:979-981)
+    mask = (rng.random(N) > 0.2).astype(np.float32)
+    colmax = L.max(axis=0, keepdims=True)
+
+    def run(e):
+        lg = e.tensor(L)
+        den = e.col_softmax_denom(lg, e.tensor(colmax))
+        g1, lv1 = e.col_softmax_sparse_forward(lg, e.tensor(labels), None, C, 1.0 / N)
+        g2, lv2 = e.col_softmax_sparse_forward(lg, e.tensor(labels), e.tensor(mask), C - 1, 0.01)
+        return [den, g1, lv1, g2, lv2]
+    h, c = both(hip, cpu, run)
+    for x, y in zip(h, c):
+        assert nrm_err(x, y) <= 1e-5
+
+
+# ── GPT end to end ──────────────────────────────────────────────────────────
+def _gpt_case(e, cfg, seed, B, doc=None):
+    g = e.gpt(**cfg)
+    rng = np.random.default_rng(seed)
+    g.set_params([rng.normal(0, 0.02, s).astype(np.float32) for s in g.param_shapes()])
+    T = cfg["seq_len"]
+    toks = rng.integers(0, cfg["vocab_size"], size=(T + 1, B))
+    if doc is not None:
+        g.set_doc_ids(doc)
+    g.load_batch(toks[:T].astype(np.float32), toks[1:].T.reshape(-1))
+    loss = g.forward_loss()
+    logits = g.logits()
+    g.backward()
+    grads = g.grads()
+    g.optimizer_step()
+    params = g.params()
+    return loss, logits, grads, params
+
+
+@pytest.mark.parametrize("pos", ["learned", "alibi", "sinusoidal"])
+def test_gpt_step_small(hip, cpu, pos):
+    cfg = dict(vocab_size=256, d_model=64, seq_len=32, num_heads=4, d_ff=128, num_layers=2, pos_enc=pos)
+    h, c = _gpt_case(hip, cfg, 1, 3), _gpt_case(cpu, cfg, 1, 3)
+    assert abs(h[0] - c[0]) <= 1e-5 * abs(c[0])
+    assert nrm_err(h[1], c[1]) <= 1e-4
+    errs = grad_errs(h[2], c[2])
+    assert max(errs) <= 1e-3, errs
+    check_adam_params(h[3], c[3], c[2], lr=1e-3)
+
+
+def check_adam_params(got, ref, ref_grads, lr):
+    """Updated weights within 1e-5 of max|w|, except where the first AdamW step
+    (~ -lr*sign(g)) flips sign on a near-zero gradient: such entries may differ
+    by up to 2*lr and must be rare."""
+    flips = 0
+    total = 0
+    for i, (a, b, g) in enumerate(zip(got, ref, ref_grads)):
+        d = np.abs(a.astype(np.float64) - b)
+        bad = d > 1e-5 * max(np.abs(b).max(), 1e-6)
+        assert np.all(d[bad] <= 2.0 * lr * 1.01), i
+        assert np.all(np.abs(g[bad]) <= 1e-4 * max(np.abs(g).max(), 1e-30) + 1e-12), i
+        flips += int(bad.sum())
+        total += b.size
+    assert flips <= max(3, total // 1000), (flips, total)
+
+
+def test_gpt_doc_ids(hip, cpu):
+    cfg = dict(vocab_size=128, d_model=32, seq_len=24, num_heads=2, d_ff=64, num_layers=2, pos_enc="learned")
+    doc = np.array([1] * 10 + [2] * 14 + [1] * 5 + [2] * 19, dtype=np.uint64)
+    h, c = _gpt_case(hip, cfg, 2, 2, doc), _gpt_case(cpu, cfg, 2, 2, doc)
+    assert abs(h[0] - c[0]) <= 1e-5 * abs(c[0])
+    assert nrm_err(h[1], c[1]) <= 1e-4
+    errs = grad_errs(h[2], c[2])
+    assert max(errs) <= 1e-3, errs
+
+
+def test_gpt_config1(hip, cpu):
+    """2L, d128, H4, SwiGLU 512, RMSNorm, learned pos, V1024, T128, B8."""
+    cfg = dict(vocab_size=1024, d_model=128, seq_len=128, num_heads=4, d_ff=512, num_layers=2, pos_enc="learned")
+    h, c = _gpt_case(hip, cfg, 42, 8), _gpt_case(cpu, cfg, 42, 8)
+    assert abs(h[0] - c[0]) <= 1e-5 * abs(c[0])
+    assert nrm_err(h[1], c[1]) <= 1e-4
+    errs = grad_errs(h[2], c[2])
+    assert max(errs) <= 1e-3, errs

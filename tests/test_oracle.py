@@ -1,0 +1,487 @@
+"""Pins the CPU oracle (oracle/, the restatement of the reference CpuEngine).
+
+Each check is an independent computation: float64 numpy closed forms, dense
+formulations of the fused primitives, torch float64 autograd, brute-force
+loops for the index primitives, the reference's own known-answer mask rows
+(src/doc_mask_test.cpp:49-104), its finite-difference gradcheck method
+(src/gpt_gradcheck.cpp:124-261) and its document-invariance test
+(src/doc_attn_test.cpp:75-152). The reference ships no stored vectors; its
+sources need <expected>, which this image's libstdc++ lacks, so it cannot be
+compiled here and every pin below is reference-free.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import torch_gpt
+from helpers import causal_mask, doc_mask, grad_errs, normal, nrm_err, uniform
+from nnengine import EngineError, ExprSpec, cst, inp, red, reg
+
+
+def np64(x):
+    return np.asarray(x, dtype=np.float64)
+
+
+# ── GEMM ────────────────────────────────────────────────────────────────────
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (5, 7, 3), (64, 64, 64), (65, 130, 129), (200, 33, 300)])
+def test_matmul_vs_float64(cpu, M, N, K, tA, tB):
+    rng = np.random.default_rng(M + 7 * N + 13 * K)
+    A = uniform(rng, (K, M) if tA else (M, K))
+    B = uniform(rng, (N, K) if tB else (K, N))
+    C = cpu.matmul(cpu.tensor(A), cpu.tensor(B), tA, tB).numpy()
+    Ae, Be = np64(A.T if tA else A), np64(B.T if tB else B)
+    ref = Ae @ Be
+    assert np.all(np.abs(C - ref) <= 2 * K * 2.0 ** -24 * (np.abs(Ae) @ np.abs(Be)) + 1e-30)
+
+
+def test_matmul_shape_error(cpu):
+    with pytest.raises(EngineError, match="dimension mismatch"):
+        cpu.matmul(cpu.tensor(np.zeros((3, 4))), cpu.tensor(np.zeros((5, 6))))
+
+
+def test_batched_matmul_alpha_and_errors(cpu):
+    rng = np.random.default_rng(1)
+    A, B = uniform(rng, (3 * 4, 5)), uniform(rng, (3 * 5, 6))
+    C = cpu.batched_matmul(cpu.tensor(A), cpu.tensor(B), 3, False, False, 0.5).numpy()
+    ref = np.concatenate([0.5 * (np64(A[4 * b:4 * b + 4]) @ np64(B[5 * b:5 * b + 5])) for b in range(3)])
+    assert nrm_err(C, ref) <= 1e-6
+    with pytest.raises(EngineError, match="divisible"):
+        cpu.batched_matmul(cpu.tensor(A), cpu.tensor(B), 5)
+    with pytest.raises(EngineError, match="batch must be > 0"):
+        cpu.batched_matmul(cpu.tensor(A), cpu.tensor(B), 0)
+
+
+# ── fused attention primitives vs dense float64 / torch autograd ───────────
+def _dense_scores(A, B, batch, tA, tB, alpha, mask):
+    """(batch, M, N) alpha*op(A_b)op(B_b) + mask, float64."""
+    out = []
+    ar, br = A.shape[0] // batch, B.shape[0] // batch
+    for b in range(batch):
+        Ab, Bb = np64(A[b * ar:(b + 1) * ar]), np64(B[b * br:(b + 1) * br])
+        S = alpha * ((Ab.T if tA else Ab) @ (Bb.T if tB else Bb))
+        out.append(S + (np64(mask) if mask is not None else 0.0))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_fused_forward_vs_dense(cpu, tA, tB, masked):
+    rng = np.random.default_rng(2026)
+    batch, M, N, K, D, alpha = 2, 4, 6, 4, 5, 0.35
+    A = uniform(rng, (batch * (K if tA else M), M if tA else K))
+    B = uniform(rng, (batch * (N if tB else K), K if tB else N))
+    V = uniform(rng, (batch * N, D))
+    mask = causal_mask(max(M, N))[:M, :N] if masked else None
+    S = _dense_scores(A, B, batch, tA, tB, alpha, mask)
+    a, b = cpu.tensor(A), cpu.tensor(B)
+    mk = cpu.tensor(mask) if masked else None
+    m = cpu.batched_matmul_reduce(a, b, batch, "Max", tA, tB, alpha, True, mk).numpy().reshape(batch, M)
+    assert nrm_err(m, S.max(axis=2)) <= 1e-6
+    fin = np.isfinite(S)
+    ssum = cpu.batched_matmul_reduce(a, b, batch, "Sum", tA, tB, alpha, True, mk).numpy().reshape(batch, M)
+    assert nrm_err(ssum, np.where(fin, S, 0).sum(axis=2)) <= 1e-6
+    smin = cpu.batched_matmul_reduce(a, b, batch, "Min", tA, tB, alpha, True, mk).numpy().reshape(batch, M)
+    assert nrm_err(smin, np.where(fin, S, np.inf).min(axis=2)) <= 1e-6
+    mcol = cpu.batched_matmul_reduce(a, b, batch, "Max", tA, tB, alpha, False, mk).numpy()
+    # a fully masked column keeps the initial lowest() (max(lowest, -inf) = lowest)
+    ref_col = S.max(axis=1)
+    empty = ~np.isfinite(ref_col)
+    assert np.all(mcol[empty] == np.finfo(np.float32).min)
+    assert nrm_err(np.where(empty, 0, mcol), np.where(empty, 0, ref_col)) <= 1e-6
+    l = cpu.batched_matmul_softmax_denom(a, b, cpu.tensor(m.reshape(-1, 1)), batch, tA, tB, alpha, mk).numpy()
+    W = np.exp(S - S.max(axis=2, keepdims=True))
+    assert nrm_err(l.reshape(batch, M), W.sum(axis=2)) <= 1e-6
+    O = cpu.batched_matmul_softmax_apply(a, b, cpu.tensor(V), cpu.tensor(m.reshape(-1, 1)), cpu.tensor(l), batch, tA,
+                                         tB, alpha, mk).numpy()
+    P = W / W.sum(axis=2, keepdims=True)
+    ref = np.concatenate([P[bb] @ np64(V[bb * N:(bb + 1) * N]) for bb in range(batch)])
+    assert nrm_err(O, ref) <= 1e-6
+    # identity: softmax rows sum to one -> applying to a ones V gives ones
+    O1 = cpu.batched_matmul_softmax_apply(a, b, cpu.tensor(np.ones((batch * N, 3))),
+                                          cpu.tensor(m.reshape(-1, 1)), cpu.tensor(l), batch, tA, tB, alpha,
+                                          mk).numpy()
+    assert np.abs(O1 - 1).max() <= 1e-6
+
+
+def test_fully_masked_row_max_is_lowest(cpu):
+    """Max reduction starts at lowest(): an all -inf row stays lowest (cpu_engine.hpp:466-470)."""
+    A = np.ones((2, 2), dtype=np.float32)
+    mask = np.array([[-np.inf, -np.inf], [0, -np.inf]], dtype=np.float32)
+    m = cpu.batched_matmul_reduce(cpu.tensor(A), cpu.tensor(A), 1, "Max", True, False, 1.0, True,
+                                  cpu.tensor(mask)).numpy()
+    assert m[0, 0] == np.finfo(np.float32).min and m[1, 0] == 2.0
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_fused_backward_vs_autograd(cpu, masked):
+    """backward_q / backward_kv equal torch autograd of L1 = sum P*W (dQ, dK) and
+    L2 = sum G*(W V) (dV) in the attention layout transA=1, transB=0."""
+    rng = np.random.default_rng(7)
+    batch, T, d, alpha = 3, 9, 5, 0.4
+    Q, K = uniform(rng, (batch * d, T)), uniform(rng, (batch * d, T))
+    Pm, G = uniform(rng, (batch * T, T)), uniform(rng, (batch * T, d))
+    mask = causal_mask(T) if masked else None
+    q = torch.tensor(np64(Q), requires_grad=True)
+    k = torch.tensor(np64(K), requires_grad=True)
+    v = torch.zeros(batch * T, d, dtype=torch.float64, requires_grad=True)
+    L1 = 0
+    L2 = 0
+    for b in range(batch):
+        S = alpha * q[b * d:(b + 1) * d].T @ k[b * d:(b + 1) * d]
+        if masked:
+            S = S + torch.tensor(np64(mask))
+        W = torch.softmax(S, dim=1)
+        L1 = L1 + (torch.tensor(np64(Pm[b * T:(b + 1) * T])) * W).sum()
+        L2 = L2 + (torch.tensor(np64(G[b * T:(b + 1) * T])) * (W.detach() @ v[b * T:(b + 1) * T])).sum()
+    L1.backward()
+    L2.backward()
+    a, kk = cpu.tensor(Q), cpu.tensor(K)
+    mk = cpu.tensor(mask) if masked else None
+    m = cpu.batched_matmul_reduce(a, kk, batch, "Max", True, False, alpha, True, mk)
+    l = cpu.batched_matmul_softmax_denom(a, kk, m, batch, True, False, alpha, mk)
+    dq, r = cpu.batched_matmul_softmax_backward_q(a, kk, cpu.tensor(Pm), m, l, batch, True, False, alpha, mk)
+    dk, dv = cpu.batched_matmul_softmax_backward_kv(a, kk, cpu.tensor(Pm), cpu.tensor(G), r, m, l, batch, True,
+                                                    False, alpha, mk)
+    assert nrm_err(dq.numpy(), q.grad.numpy()) <= 1e-5
+    assert nrm_err(dk.numpy(), k.grad.numpy()) <= 1e-5
+    # dV is returned transposed per batch: (batch*K, N) with element [k][j]
+    dv_ref = np.concatenate([v.grad.numpy()[b * T:(b + 1) * T].T for b in range(batch)])
+    assert nrm_err(dv.numpy(), dv_ref) <= 1e-5
+    # R_i = sum_j W_ij P_ij
+    S = _dense_scores(Q, K, batch, True, False, alpha, mask)
+    W = np.exp(S - S.max(axis=2, keepdims=True))
+    W /= W.sum(axis=2, keepdims=True)
+    assert nrm_err(r.numpy().reshape(batch, T), (W * np64(Pm).reshape(batch, T, T)).sum(axis=2)) <= 1e-6
+
+
+# ── column softmax / sparse cross-entropy ───────────────────────────────────
+def test_sparse_ce_closed_form(cpu):
+    rng = np.random.default_rng(3)
+    C, N, vocab = 50, 40, 45
+    L = normal(rng, (C, N), 2.0)
+    labels = rng.integers(0, vocab, size=N).astype(np.float32)
+    labels[[1, 5]] = [vocab, vocab + 100]   # invalid
+    labels[7] = -1.0                        # reads as class 0
+    mask = np.ones(N, dtype=np.float32)
+    mask[[2, 3]] = [0.0, 0.49]
+    inv = 1.0 / 33
+    g, lv = cpu.col_softmax_sparse_forward(cpu.tensor(L), cpu.tensor(labels), cpu.tensor(mask), vocab, inv)
+    g, lv = g.numpy(), lv.numpy()[0]
+    Ld = np64(L)
+    logp = Ld - Ld.max(0) - np.log(np.exp(Ld - Ld.max(0)).sum(0))
+    lab = np.where(labels >= 0, labels, 0).astype(np.int64)
+    valid = (mask >= 0.5) & (lab < vocab)
+    for i in range(N):
+        if not valid[i]:
+            assert not g[:, i].any() and lv[i] == 0
+            continue
+        onehot = np.zeros(C)
+        onehot[lab[i]] = 1
+        assert np.abs(g[:, i] - inv * (np.exp(logp[:, i]) - onehot)).max() <= 1e-7
+        assert abs(g[:, i].sum()) <= 1e-7
+        assert abs(lv[i] - logp[lab[i], i]) <= 1e-5
+    den = cpu.col_softmax_denom(cpu.tensor(L), cpu.tensor(L.max(0, keepdims=True))).numpy()[0]
+    assert nrm_err(den, np.exp(Ld - Ld.max(0)).sum(0)) <= 1e-6
+    with pytest.raises(EngineError, match="2\\^24"):
+        cpu.col_softmax_sparse_forward(cpu.tensor(np.zeros((2, 2))), cpu.tensor(np.zeros((1, 2))), None,
+                                       (1 << 24) + 1, 1.0)
+
+
+# ── index / layout primitives: brute force, bit-exact ──────────────────────
+def test_gather_scatter_brute_force(cpu):
+    rng = np.random.default_rng(4)
+    V, D, n = 30, 7, 200
+    table = normal(rng, (V, D))
+    idx = rng.integers(-2, V + 3, size=n).astype(np.float32)
+    idx[:3] = [-0.5, 29.9, 1e30]
+    out = cpu.gather_rows(cpu.tensor(table), cpu.tensor(idx)).numpy()
+    grad = normal(rng, (n, D))
+    dst = cpu.tensor(table)
+    cpu.scatter_add_rows(dst, cpu.tensor(idx), cpu.tensor(grad))
+    exp_g = np.zeros((n, D), dtype=np.float32)
+    exp_s = table.copy()
+    for i in range(n):
+        f = float(idx[i])
+        if f > -1 and f < 2 ** 64 and int(f) < V:
+            r = int(f)
+            exp_g[i] = table[r]
+            for c in range(D):   # serial float32 accumulation in i order
+                exp_s[r, c] = np.float32(exp_s[r, c] + grad[i, c])
+    assert np.array_equal(out, exp_g)
+    assert np.array_equal(dst.numpy(), exp_s)
+
+
+def test_layout_primitives(cpu):
+    rng = np.random.default_rng(5)
+    M, B, N = 6, 4, 5
+    X = uniform(rng, (M, B * N))
+    Y = cpu.rearrange_3d(cpu.tensor(X), M, B, N).numpy()
+    assert np.array_equal(Y, X.reshape(M, B, N).transpose(1, 0, 2).reshape(B * M, N))
+    Z = cpu.rearrange_3d(cpu.tensor(Y), M, B, N, True).numpy()
+    assert np.array_equal(Z, X)
+    A = uniform(rng, (130, 70))
+    assert np.array_equal(cpu.transpose(cpu.tensor(A)).numpy(), A.T)
+    s = cpu.slice_rows(cpu.tensor(A), 3, 4).numpy()
+    assert np.array_equal(s, A[3:7])
+    with pytest.raises(EngineError, match="out of bounds"):
+        cpu.slice_rows(cpu.tensor(A), 128, 4)
+
+
+def test_elementwise_and_reductions(cpu):
+    rng = np.random.default_rng(6)
+    A, B = uniform(rng, (33, 44), 0.1, 3), uniform(rng, (33, 44), 0.1, 3)
+    f = {"Neg": np.negative, "Exp": np.exp, "Log": np.log, "Sqrt": np.sqrt, "Rsqrt": lambda x: 1 / np.sqrt(x),
+         "Abs": np.abs, "Tanh": np.tanh}
+    for op, fn in f.items():
+        assert nrm_err(cpu.elementwise_unary(op, cpu.tensor(A)).numpy(), fn(np64(A))) <= 2e-7
+    g = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply, "Div": np.divide, "Max": np.maximum,
+         "Min": np.minimum}
+    for op, fn in g.items():
+        assert np.array_equal(cpu.elementwise_binary(op, cpu.tensor(A), cpu.tensor(B)).numpy(), fn(A, B))
+        assert np.array_equal(cpu.elementwise_binary_scalar(op, cpu.tensor(A), 1.5, True).numpy(),
+                              fn(np.float32(1.5), A))
+    assert nrm_err(cpu.row_reduce_sum(cpu.tensor(A)).numpy()[:, 0], np64(A).sum(1)) <= 1e-6
+    assert nrm_err(cpu.col_reduce_sum(cpu.tensor(A)).numpy()[0], np64(A).sum(0)) <= 1e-6
+    assert np.array_equal(cpu.col_reduce_max(cpu.tensor(A)).numpy()[0], A.max(0))
+    big = uniform(rng, (2048, 300))   # parallel row-block path of col_reduce
+    assert nrm_err(cpu.col_reduce_sum(cpu.tensor(big)).numpy()[0], np64(big).sum(0)) <= 1e-6
+
+
+# ── eval_expr programs of the GPT path ─────────────────
+def _softmax_fwd_spec():
+    s = ExprSpec()
+    for v in ("Linear", "RowReduceMax", "Linear", "RowReduceMax"):
+        s.view(v)
+    r0 = s.ins("Sub", inp(0), inp(1))
+    r1 = s.ins("Exp", reg(r0))
+    r2 = s.ins("Sub", inp(2), inp(3))
+    r3 = s.ins("Exp", reg(r2))
+    r4 = s.ins("RowSum", reg(r3))
+    s.ins("Div", reg(r1), red(r4))
+    return s
+
+
+def _softmax_bwd_spec():
+    s = ExprSpec()
+    for _ in range(4):
+        s.view("Linear")
+    r0 = s.ins("Mul", inp(2), inp(3))
+    r1 = s.ins("RowSum", reg(r0))
+    r2 = s.ins("Sub", inp(1), red(r1))
+    s.ins("Mul", inp(0), reg(r2))
+    return s
+
+
+def test_expr_softmax_programs(cpu):
+    rng = np.random.default_rng(8)
+    X, Gr = normal(rng, (17, 23), 3), normal(rng, (17, 23))
+    y = cpu.eval_expr(_softmax_fwd_spec(), [cpu.tensor(X)] * 4, 17, 23).numpy()
+    e = np.exp(np64(X) - np64(X).max(1, keepdims=True))
+    ref = e / e.sum(1, keepdims=True)
+    assert nrm_err(y, ref) <= 1e-6
+    dx = cpu.eval_expr(_softmax_bwd_spec(), [cpu.tensor(y), cpu.tensor(Gr), cpu.tensor(y), cpu.tensor(Gr)],
+                       17, 23).numpy()
+    ref_dx = ref * (np64(Gr) - (ref * np64(Gr)).sum(1, keepdims=True))
+    assert nrm_err(dx, ref_dx) <= 1e-5
+
+
+def test_expr_rmsnorm_programs(cpu):
+    rng = np.random.default_rng(9)
+    F, N = 24, 10
+    x, g, gamma = normal(rng, (F, N)), normal(rng, (F, N)), uniform(rng, (F, 1), 0.5, 1.5)
+    # A.1: ColSum(x*x) as a reduced vector
+    s = ExprSpec()
+    s.view("Linear"), s.view("Linear")
+    r0 = s.ins("Mul", inp(0), inp(1))
+    s.ins("ColSum", reg(r0))
+    ss = cpu.eval_expr_reduce(s, [cpu.tensor(x)] * 2, F, N).numpy()
+    assert ss.shape == (1, N) and nrm_err(ss[0], (np64(x) ** 2).sum(0)) <= 1e-6
+    rms_inv = (1 / np.sqrt(ss / F + 1e-5)).astype(np.float32)
+    normed = x * rms_inv
+    # A.3(c): RowSum(g*gamma*normed) -> (F,1)
+    s = ExprSpec()
+    s.view("Linear"), s.view("RowBroadcast"), s.view("Linear")
+    r0 = s.ins("Mul", inp(0), inp(1))
+    r1 = s.ins("Mul", reg(r0), inp(2))
+    s.ins("RowSum", reg(r1))
+    gg = cpu.eval_expr_reduce(s, [cpu.tensor(g), cpu.tensor(gamma), cpu.tensor(normed)], F, N).numpy()
+    assert gg.shape == (F, 1) and nrm_err(gg[:, 0], (np64(g) * gamma * normed).sum(1)) <= 1e-6
+    # A.3(b): (g*gamma - colbcast(m)*normed) * colbcast(rms_inv)
+    m = ((g * gamma * normed).sum(0, keepdims=True) / F).astype(np.float32)
+    s = ExprSpec()
+    for v in ("Linear", "RowBroadcast", "ColBroadcast", "Linear", "ColBroadcast"):
+        s.view(v)
+    r0 = s.ins("Mul", inp(0), inp(1))
+    r1 = s.ins("Mul", inp(2), inp(3))
+    r2 = s.ins("Sub", reg(r0), reg(r1))
+    s.ins("Mul", reg(r2), inp(4))
+    dx = cpu.eval_expr(s, [cpu.tensor(a) for a in (g, gamma, m, normed, rms_inv)], F, N).numpy()
+    assert nrm_err(dx, (np64(g) * gamma - m * normed) * rms_inv) <= 1e-6
+
+
+def test_expr_views_and_select(cpu):
+    rng = np.random.default_rng(10)
+    R, C, blk = 8, 5, 4
+    x = normal(rng, (R, C))
+    tab = normal(rng, (blk, C))
+    s = ExprSpec()
+    s.view("RotateHalf", blk, 1), s.view("RowMod", blk), s.view("Linear")
+    c0 = s.const(0.0)
+    r0 = s.ins("Mul", inp(0), inp(1))
+    r1 = s.ins("Gt", inp(2), cst(c0))
+    s.ins("Select", reg(r1), reg(r0), inp(2))
+    y = cpu.eval_expr(s, [cpu.tensor(x), cpu.tensor(tab), cpu.tensor(x)], R, C).numpy()
+    rot = np.empty_like(x)
+    for r in range(R):
+        rl = r % blk
+        src = (r // blk) * blk + (rl + blk // 2 if rl < blk // 2 else rl - blk // 2)
+        rot[r] = -x[src] if rl < blk // 2 else x[src]
+    ref = np.where(x > 0, rot * np.tile(tab, (R // blk, 1)), x)
+    assert np.array_equal(y, ref)
+
+
+def test_expr_validation_errors(cpu):
+    t = cpu.tensor(np.ones((2, 2)))
+    s = ExprSpec()
+    s.view("Linear")
+    r0 = s.ins("ColSum", inp(0))
+    s.ins("Add", reg(r0), inp(0))          # register read of a reduce result
+    with pytest.raises(EngineError, match="reduce dst"):
+        cpu.eval_expr(s, [t], 2, 2)
+    s = ExprSpec()
+    s.view("Linear")
+    s.ins("Exp", inp(0))
+    s.ins("Add", red(0), inp(0))           # Reduce operand on an elementwise result
+    with pytest.raises(EngineError, match="prior reduce"):
+        cpu.eval_expr(s, [t], 2, 2)
+    s = ExprSpec()
+    s.view("Linear")
+    r0 = s.ins("ColSum", inp(0))
+    s.ins("Add", red(r0), inp(0))          # reads a Linear input after the reduction
+    with pytest.raises(EngineError, match="not constant"):
+        cpu.eval_expr_reduce(s, [t], 2, 2)
+    s = ExprSpec()
+    s.view("Linear")
+    s.ins("Exp", inp(0))
+    with pytest.raises(EngineError, match="rows or along columns"):
+        cpu.eval_expr_reduce(s, [t], 2, 2)
+
+
+# ── attention mask: the reference's known-answer rows ──────────────────────
+def test_build_attention_mask_known_rows(cpu):
+    """src/doc_mask_test.cpp:49-104."""
+    ninf = -np.inf
+    m = cpu.build_attention_mask(2, 4, 2, False)
+    for row in range(16):
+        i = row % 4
+        assert np.array_equal(m[row], [0 if j <= i else ninf for j in range(4)])
+    doc = [0, 0, 1, 1, 1, 2]
+    m = cpu.build_attention_mask(1, 6, 1, False, doc_ids=doc)
+    for i in range(6):
+        assert np.array_equal(m[i], [0 if (j <= i and doc[i] == doc[j]) else ninf for j in range(6)])
+    m = cpu.build_attention_mask(1, 3, 2, True, slopes=[1.0, 0.5])
+    for h, sl in enumerate([1.0, 0.5]):
+        for i in range(3):
+            exp = [-sl * (i - j) if j <= i else ninf for j in range(3)]
+            assert np.allclose(m[h * 3 + i], exp, atol=1e-6, rtol=0) and np.array_equal(np.isinf(m[h * 3 + i]),
+                                                                                        np.isinf(exp))
+    doc = [0, 0, 1, 1]
+    m = cpu.build_attention_mask(1, 4, 1, True, slopes=[0.25], doc_ids=doc)
+    for i in range(4):
+        exp = [-0.25 * (i - j) if (j <= i and doc[i] == doc[j]) else ninf for j in range(4)]
+        assert np.allclose(np.nan_to_num(m[i], neginf=-9), np.nan_to_num(np.array(exp), neginf=-9))
+
+
+# ── whole GPT: oracle vs independent float64 torch restatement ─────────────
+def _run_gpt(eng, cfg, params, toks, doc=None, mask=None):
+    g = eng.gpt(**cfg)
+    assert g.param_shapes() == torch_gpt.param_shapes(cfg)
+    g.set_params(params)
+    if doc is not None:
+        g.set_doc_ids(doc)
+    T = cfg["seq_len"]
+    g.load_batch(toks[:T].astype(np.float32), toks[1:].T.reshape(-1), mask)
+    loss = g.forward_loss()
+    logits = g.logits()
+    g.backward()
+    grads = g.grads()
+    g.optimizer_step()
+    return loss, logits, grads, g.params()
+
+
+@pytest.mark.parametrize("pos", ["learned", "alibi", "sinusoidal"])
+@pytest.mark.parametrize("with_doc", [False, True])
+def test_gpt_vs_torch_float64(cpu, pos, with_doc):
+    cfg = dict(vocab_size=40, d_model=16, seq_len=8, num_heads=2, d_ff=24, num_layers=2, pos_enc=pos)
+    rng = np.random.default_rng(123)
+    B = 3
+    params = [rng.normal(0, 0.2, s).astype(np.float32) for s in torch_gpt.param_shapes(cfg)]
+    toks = rng.integers(0, 40, size=(9, B))
+    doc = np.repeat(np.arange(6), 4).astype(np.uint64) if with_doc else None
+    loss_mask = (rng.random(B * 8) > 0.2).astype(np.float32)
+    loss, logits, grads, new_params = _run_gpt(cpu, cfg, params, toks, doc, loss_mask)
+    rloss, rlogits, rgrads = torch_gpt.loss_and_grads(params, toks[:8], toks[1:].T.reshape(-1), cfg,
+                                                      doc_ids=doc, loss_mask=loss_mask)
+    assert abs(loss - rloss) <= 1e-5 * abs(rloss)
+    assert nrm_err(logits, rlogits) <= 1e-5
+    errs = grad_errs(grads, torch_gpt.reference_gamma_grads(params, rgrads, cfg))
+    assert max(errs) <= 1e-4, errs
+    # one AdamW step, closed form from the oracle's own gradients
+    for a, b in zip(new_params, torch_gpt.adamw_step(params, [np64(g) for g in grads])):
+        assert np.abs(a - b).max() <= 1e-6 * max(1.0, np.abs(b).max())
+
+
+def test_gpt_gradcheck_finite_differences(cpu):
+    """The reference's gpt_gradcheck method (src/gpt_gradcheck.cpp:124-261): central differences,
+    eps 1e-3, |num - ana| <= 5e-2 (1 + |num| + |ana|)."""
+    cfg = dict(vocab_size=32, d_model=16, seq_len=8, num_heads=2, d_ff=32, num_layers=2, pos_enc="alibi")
+    rng = np.random.default_rng(7)
+    params = [rng.normal(0, 0.3, s).astype(np.float32) for s in torch_gpt.param_shapes(cfg)]
+    for i in torch_gpt.gamma_indices(cfg):   # gains at 1, as the reference's gradcheck model has them
+        params[i] = np.ones_like(params[i])
+    toks = rng.integers(0, 32, size=(9, 2))
+    g = cpu.gpt(**cfg)
+    g.set_params(params)
+    g.load_batch(toks[:8].astype(np.float32), toks[1:].T.reshape(-1))
+    g.forward_loss()
+    g.backward()
+    grads = g.grads()
+    eps = 1e-3
+    for pi in range(len(params)):
+        flat = params[pi].reshape(-1)
+        for e in rng.choice(flat.size, size=min(3, flat.size), replace=False):
+            vals = []
+            for sgn in (1, -1):
+                p2 = [p.copy() for p in params]
+                p2[pi].reshape(-1)[e] += sgn * eps
+                g.set_params(p2)
+                vals.append(g.forward_loss())
+            num = (vals[0] - vals[1]) / (2 * eps)
+            ana = float(grads[pi].reshape(-1)[e])
+            assert abs(num - ana) <= 5e-2 * (1 + abs(num) + abs(ana)), (pi, e, num, ana)
+
+
+def test_doc_invariance(cpu):
+    """src/doc_attn_test.cpp:75-152: with document ids, logits of document B do not
+    depend on document A's tokens; without them they do."""
+    cfg = dict(vocab_size=64, d_model=16, seq_len=8, num_heads=2, d_ff=32, num_layers=2, pos_enc="learned")
+    rng = np.random.default_rng(9)
+    params = [rng.normal(0, 0.3, s).astype(np.float32) for s in torch_gpt.param_shapes(cfg)]
+    toks = rng.integers(0, 64, size=(8, 1))
+    toks2 = toks.copy()
+    toks2[:4] = (toks2[:4] + 7) % 64        # change document A (positions 0..3)
+    doc = np.array([1, 1, 1, 1, 2, 2, 2, 2], dtype=np.uint64)
+
+    def logits(tk, with_doc):
+        g = cpu.gpt(**cfg)
+        g.set_params(params)
+        if with_doc:
+            g.set_doc_ids(doc)
+        g.load_batch(tk.astype(np.float32), np.zeros(8, dtype=np.uint64))
+        g.forward_loss()
+        return g.logits()
+    assert np.abs(logits(toks, True)[:, 4:] - logits(toks2, True)[:, 4:]).max() <= 1e-4
+    assert np.abs(logits(toks, False)[:, 4:] - logits(toks2, False)[:, 4:]).max() > 1e-2
