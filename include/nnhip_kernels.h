@@ -30,6 +30,15 @@ extern "C" {
 int nnhip_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
                  size_t B_cols, int transA, int transB, void* stream);
 
+/* General form used by the engine: per batch b, C_b = alpha * op(A_b) op(B_b). With a workspace of
+ * nnhip_gemm_workspace_bytes(M, N, K, batch) bytes, output grids too small to fill the GPU split K
+ * over workgroups and sum the partial tiles in slice order (deterministic); with workspace NULL the
+ * product is computed without splitting. */
+size_t nnhip_gemm_workspace_bytes(size_t M, size_t N, size_t K, size_t batch);
+int nnhip_gemm(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows, size_t B_cols,
+               size_t batch, int transA, int transB, float alpha, void* workspace, size_t workspace_bytes,
+               void* stream);
+
 /* Per batch b: C_b = alpha * op(A_b) op(B_b); A/B split into `batch` row blocks, C stacked (batch*M, N).
  * Replaces cuda_batched_matmul (cuda_kernels.h:49-54); alpha as in ComputeEngine::batched_matmul
  * (compute_engine.hpp:195-199, cpu_engine.hpp:335-419). */

@@ -456,8 +456,16 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
         return fail("matmul: dimension mismatch A=" + std::to_string(A.rows()) + "x" + std::to_string(A.cols()) +
                     " B=" + std::to_string(B.rows()) + "x" + std::to_string(B.cols()));
     NN_TRY(C, alloc_(M, N));
+    const std::size_t wsb = nnhip_gemm_workspace_bytes(M, N, K, 1);
+    std::shared_ptr<DeviceBuffer> ws;
+    if (wsb)
+    {
+        NN_TRY(w, scratch_(wsb));
+        ws = w;
+    }
     prof_begin_();
-    const int rc = nnhip_matmul(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), tA, tB, stream_);
+    const int rc = nnhip_gemm(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), 1, tA, tB, 1.0f,
+                              ws ? ws->data() : nullptr, wsb, stream_);
     prof_end_(2.0 * double(M) * double(N) * double(K));
     NN_CHECK(kernel_(rc, "matmul"));
     return C;
@@ -469,9 +477,16 @@ Result<Tensor> HipEngine::batched_matmul(const Tensor& A, const Tensor& B, std::
     NN_CHECK(need_gpu_({&A, &B}, "batched_matmul"));
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul"));
     NN_TRY(C, alloc_(batch * d.M, d.N));
+    const std::size_t wsb = nnhip_gemm_workspace_bytes(d.M, d.N, d.K, batch);
+    std::shared_ptr<DeviceBuffer> ws;
+    if (wsb)
+    {
+        NN_TRY(w, scratch_(wsb));
+        ws = w;
+    }
     prof_begin_();
-    const int rc = nnhip_batched_matmul(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), batch, tA, tB,
-                                        alpha, stream_);
+    const int rc = nnhip_gemm(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), batch, tA, tB, alpha,
+                              ws ? ws->data() : nullptr, wsb, stream_);
     prof_end_(2.0 * double(batch) * double(d.M) * double(d.N) * double(d.K));
     NN_CHECK(kernel_(rc, "batched_matmul"));
     return C;

@@ -7,11 +7,14 @@
 // global->LDS staging step: both operands are kept k-major in LDS
 // (As[k][m], Bs[k][n]) so every MFMA fragment read is 32 consecutive floats.
 //
-// Tiling: a workgroup of 4 waves owns a (64*WM) x (64*WN) tile of C
-// (WM*WN = 4); each wave owns 64x64 = 2x2 MFMA 32x32 blocks (64 accumulators
-// per lane). K advances 16 at a time through two LDS buffers: the next
-// stage's global loads are issued into registers before the current stage's
-// MFMAs and written to the other buffer afterwards (one barrier per stage).
+// Tiling: a workgroup of WM x WN waves owns a (64*WM) x (64*WN) tile of C;
+// each wave owns 64x64 = 2x2 MFMA 32x32 blocks (64 accumulators per lane).
+// K advances 16 at a time through two LDS buffers: the next stage's global
+// loads are issued into registers before the current stage's MFMAs and
+// written to the other buffer afterwards (one barrier per stage). Tile ids are
+// remapped so that each XCD (own L2) works on a contiguous, row-grouped slab.
+// Small output grids with long K (weight gradients) split K across
+// workgroups; the partial tiles are summed in order (deterministic).
 //
 // MFMA 32x32x2 f32 operand layout (per lane l, k-step of 2):
 //   A: A[i = l%32][k = l/32],  B: B[k = l/32][j = l%32],
@@ -26,30 +29,56 @@ namespace
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BK = 16;
 constexpr int PAD = 4;
 
-template <int WM, int WN, bool TA, bool TB, bool GUARD>
-__global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
-                                              float* __restrict__ C, int M, int N, int K, long lda, long ldb,
-                                              long strideA, long strideB, long strideC, float alpha, int tiles_n)
+// Tile id for workgroup `bid` of `nt` tiles (tiles_m x tiles_n). Workgroups are
+// dispatched round-robin over the 8 XCDs, each with its own L2: the remap
+// gives every XCD a contiguous slab of tile ids, and the slab is walked in
+// groups of kGroupM tile rows so that neighbours share A and B panels.
+constexpr int kGroupM = 8;
+__device__ __forceinline__ void tile_coords(int bid, int nt, int tiles_m, int tiles_n, int& tm, int& tn)
 {
-    constexpr int BM = 64 * WM, BN = 64 * WN;
+    int t = bid;
+    if ((nt & 7) == 0) t = (bid & 7) * (nt >> 3) + (bid >> 3);
+    const int per_group = kGroupM * tiles_n;
+    const int g = t / per_group, first_m = g * kGroupM;
+    const int gsize = min(tiles_m - first_m, kGroupM);
+    const int r = t - g * per_group;
+    tm = first_m + r % gsize;
+    tn = r / gsize;
+}
+
+// WM x WN waves; each wave owns (32*FM) x (32*FN) of C as FM x FN MFMA 32x32 blocks.
+template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ C, int M, int N, int K, long lda, long ldb,
+                                                       long strideA, long strideB, long strideC, float alpha,
+                                                       int tiles_m, int tiles_n, int k_split, float* __restrict__ part)
+{
+    constexpr int NT = 64 * WM * WN;
+    constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
     constexpr int LDA_S = BM + PAD, LDB_S = BN + PAD;
-    constexpr int LA = BM * BK / 4 / 256;   // float4 per thread per stage for A
-    constexpr int LB = BN * BK / 4 / 256;
+    constexpr int LA = BM * BK / 4 / NT;   // float4 per thread per stage for A
+    constexpr int LB = BN * BK / 4 / NT;
+    static_assert(LA * 4 * NT == BM * BK && LB * 4 * NT == BN * BK, "tile not divisible by the workgroup");
     __shared__ __attribute__((aligned(16))) float As[2][BK][LDA_S];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK][LDB_S];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
-    const int tile = blockIdx.x;
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    int tmi, tni;
+    tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tmi, tni);
+    const int m0 = tmi * BM, n0 = tni * BN;
     const long bz = blockIdx.z;
     A += bz * strideA;
     B += bz * strideB;
     C += bz * strideC;
+    // Split-K: workgroup row y covers k in [y*k_split, min(K, (y+1)*k_split)) and,
+    // when there are several, writes its partial tile to part[y][batch][M][N].
+    const int k_lo = blockIdx.y * k_split;
+    const int k_hi = min(K, k_lo + k_split);
+    if (gridDim.y > 1) C = part + ((long)blockIdx.y * gridDim.z + bz) * strideC;
 
     float4 ra[LA], rb[LB];
 
@@ -58,7 +87,7 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
 #pragma unroll
         for (int s = 0; s < LA; ++s)
         {
-            const int idx = tid + 256 * s;
+            const int idx = tid + NT * s;
             int m, k;
             if constexpr (TA) { k = idx / (BM / 4); m = (idx % (BM / 4)) * 4; }
             else { m = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
@@ -75,7 +104,7 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
                 for (int q = 0; q < 4; ++q)
                 {
                     const int mm = TA ? gm + q : gm, kk = TA ? gk : gk + q;
-                    v[q] = (mm < M && kk < K) ? (TA ? A[(long)kk * lda + mm] : A[(long)mm * lda + kk]) : 0.0f;
+                    v[q] = (mm < M && kk < k_hi) ? (TA ? A[(long)kk * lda + mm] : A[(long)mm * lda + kk]) : 0.0f;
                 }
                 ra[s] = make_float4(v[0], v[1], v[2], v[3]);
             }
@@ -86,7 +115,7 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
 #pragma unroll
         for (int s = 0; s < LB; ++s)
         {
-            const int idx = tid + 256 * s;
+            const int idx = tid + NT * s;
             int n, k;
             if constexpr (!TB) { k = idx / (BN / 4); n = (idx % (BN / 4)) * 4; }
             else { n = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
@@ -103,7 +132,7 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
                 for (int q = 0; q < 4; ++q)
                 {
                     const int nn = !TB ? gn + q : gn, kk = !TB ? gk : gk + q;
-                    v[q] = (nn < N && kk < K) ? (!TB ? B[(long)kk * ldb + nn] : B[(long)nn * ldb + kk]) : 0.0f;
+                    v[q] = (nn < N && kk < k_hi) ? (!TB ? B[(long)kk * ldb + nn] : B[(long)nn * ldb + kk]) : 0.0f;
                 }
                 rb[s] = make_float4(v[0], v[1], v[2], v[3]);
             }
@@ -113,7 +142,7 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
 #pragma unroll
         for (int s = 0; s < LA; ++s)
         {
-            const int idx = tid + 256 * s;
+            const int idx = tid + NT * s;
             if constexpr (TA)
             {
                 const int k = idx / (BM / 4), m = (idx % (BM / 4)) * 4;
@@ -133,7 +162,7 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
 #pragma unroll
         for (int s = 0; s < LB; ++s)
         {
-            const int idx = tid + 256 * s;
+            const int idx = tid + NT * s;
             if constexpr (!TB)
             {
                 const int k = idx / (BN / 4), n = (idx % (BN / 4)) * 4;
@@ -150,42 +179,46 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
         }
     };
 
-    floatx16 acc[2][2];
+    floatx16 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int kt_n = (K + BK - 1) / BK;
+    const int kt_n = (k_hi - k_lo + BK - 1) / BK;
     if (kt_n > 0)
     {
-        load_a(0);
-        load_b(0);
+        load_a(k_lo);
+        load_b(k_lo);
         store_a(0);
         store_b(0);
         __syncthreads();
     }
-    const int am = wm * 64 + (lane & 31), bn = wn * 64 + (lane & 31), kl = lane >> 5;
+    const int am = wm * 32 * FM + (lane & 31), bn = wn * 32 * FN + (lane & 31), kl = lane >> 5;
     for (int kt = 0; kt < kt_n; ++kt)
     {
         const int buf = kt & 1;
         const bool more = kt + 1 < kt_n;
         if (more)
         {
-            load_a((kt + 1) * BK);
-            load_b((kt + 1) * BK);
+            load_a(k_lo + (kt + 1) * BK);
+            load_b(k_lo + (kt + 1) * BK);
         }
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2)
         {
-            const float a0 = As[buf][kk + kl][am], a1 = As[buf][kk + kl][am + 32];
-            const float b0 = Bs[buf][kk + kl][bn], b1 = Bs[buf][kk + kl][bn + 32];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+            float a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) a[i] = As[buf][kk + kl][am + 32 * i];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[j] = Bs[buf][kk + kl][bn + 32 * j];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         if (more)
         {
@@ -198,69 +231,170 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
     // Epilogue: C = alpha * acc.
     const int col_l = lane & 31, row_l = 4 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN; ++j)
         {
-            const int gn = n0 + wn * 64 + j * 32 + col_l;
+            const int gn = n0 + wn * 32 * FN + j * 32 + col_l;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
-                const int gm = m0 + wm * 64 + i * 32 + 8 * (r / 4) + row_l + (r % 4);
-                if (!GUARD || (gm < M && gn < N)) C[(long)gm * N + gn] = alpha * acc[i][j][r];
+                const int gm = m0 + wm * 32 * FM + i * 32 + 8 * (r / 4) + row_l + (r % 4);
+                if (!GUARD || (gm < M && gn < N)) C[(long)gm * N + gn] = (gridDim.y > 1 ? 1.0f : alpha) * acc[i][j][r];
             }
         }
 }
 
-template <int WM, int WN, bool TA, bool TB>
-void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, long lda, long ldb, long sA, long sB,
-                long sC, float alpha, int batch, bool guard, hipStream_t s)
+// C = alpha * sum_s part[s], summed in split order (deterministic).
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, float* __restrict__ C,
+                                                       long n, int splits, float alpha)
 {
-    constexpr int BM = 64 * WM, BN = 64 * WN;
-    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-    const dim3 grid(static_cast<unsigned>(tm * tn), 1, static_cast<unsigned>(batch));
-    if (guard)
-        hipLaunchKernelGGL((k_gemm<WM, WN, TA, TB, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, sA, sB,
-                           sC, alpha, tn);
+    const long stride = (long)gridDim.x * 256;
+    if ((n & 3) == 0)
+    {
+        const long n4 = n / 4;
+        const float4* p4 = reinterpret_cast<const float4*>(part);
+        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride)
+        {
+            float4 a = p4[i];
+            for (int s = 1; s < splits; ++s)
+            {
+                const float4 b = p4[(long)s * n4 + i];
+                a.x += b.x;
+                a.y += b.y;
+                a.z += b.z;
+                a.w += b.w;
+            }
+            reinterpret_cast<float4*>(C)[i] = make_float4(alpha * a.x, alpha * a.y, alpha * a.z, alpha * a.w);
+        }
+    }
     else
-        hipLaunchKernelGGL((k_gemm<WM, WN, TA, TB, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, sA,
-                           sB, sC, alpha, tn);
+    {
+        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        {
+            float a = part[i];
+            for (int s = 1; s < splits; ++s) a += part[(long)s * n + i];
+            C[i] = alpha * a;
+        }
+    }
+}
+
+// Launch plan for one GEMM: tile configuration and split-K factor.
+enum Cfg { kTall = 0, kSquare = 1, kSkinnyM = 2, kSkinnyN = 3 };
+struct Plan
+{
+    Cfg cfg;
+    int bm, bn, splits, k_split;
+};
+
+// Tile choice, from a sweep of the config-4 shapes on MI355X:
+//   * M <= 64 (attention PV / dV / dQ / dK): 64 x 256 tiles;
+//   * N <= 64: 256 x 64;
+//   * M >= 256: 256 x 128 tiles over 8 waves (best on every large shape);
+//   * otherwise 128 x 128.
+// When the tile grid cannot fill the 256 CUs and K is long (the weight
+// gradients dW = G X^T, K = tokens), K is split into slices whose partial
+// tiles are summed in order by k_splitk_reduce.
+Plan plan_gemm(size_t M, size_t N, size_t K, size_t batch, bool allow_split)
+{
+    Plan p;
+    if (M <= 64) { p.cfg = kSkinnyM; p.bm = 64; p.bn = 256; }
+    else if (N <= 64) { p.cfg = kSkinnyN; p.bm = 256; p.bn = 64; }
+    else if (M >= 256) { p.cfg = kTall; p.bm = 256; p.bn = 128; }
+    else { p.cfg = kSquare; p.bm = 128; p.bn = 128; }
+    p.splits = 1;
+    p.k_split = static_cast<int>(K);
+    const size_t tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn) * batch;
+    if (allow_split && tiles < 256 && K >= 1024)
+    {
+        if (p.cfg == kTall && tiles < 128)
+        {
+            p.cfg = kSquare;
+            p.bm = 128;
+            p.bn = 128;
+        }
+        const size_t t2 = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn) * batch;
+        size_t want = (768 + t2 - 1) / t2;                 // aim for ~3 workgroups per CU
+        const size_t max_splits = K / 256;                 // keep >= 256 k per slice
+        if (want > max_splits) want = max_splits;
+        if (want > 64) want = 64;
+        if (want > 1)
+        {
+            size_t ks = (K + want - 1) / want;
+            ks = (ks + 15) / 16 * 16;                      // whole BK stages per slice
+            p.k_split = static_cast<int>(ks);
+            p.splits = static_cast<int>((K + ks - 1) / ks);
+        }
+    }
+    return p;
+}
+
+template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB>
+void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, long lda, long ldb, long sA, long sB,
+                long sC, float alpha, int batch, bool vec_ok, int splits, int k_split, float* part, hipStream_t s)
+{
+    constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
+    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+    const bool guard = !vec_ok || (M % BM) || (N % BN) || (K % BK) || (k_split % BK);
+    const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits), static_cast<unsigned>(batch));
+    const dim3 block(64 * WM * WN);
+    if (guard)
+        hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, true>), grid, block, 0, s, A, B, C, M, N, K, lda, ldb,
+                           sA, sB, sC, alpha, tm, tn, k_split, part);
+    else
+        hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false>), grid, block, 0, s, A, B, C, M, N, K, lda, ldb,
+                           sA, sB, sC, alpha, tm, tn, k_split, part);
 }
 
 template <bool TA, bool TB>
-void launch_trans(const float* A, const float* B, float* C, int M, int N, int K, long lda, long ldb, long sA, long sB,
-                  long sC, float alpha, int batch, hipStream_t s)
+void launch_trans(const Plan& p, const float* A, const float* B, float* C, int M, int N, int K, long lda, long ldb,
+                  long sA, long sB, long sC, float alpha, int batch, float* part, hipStream_t s)
 {
     const bool vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && (sA % 4 == 0) && (sB % 4 == 0) && aligned16(A) &&
                         aligned16(B);
-    if (M <= 64)
+    switch (p.cfg)
     {
-        const bool guard = !vec_ok || (M % 64) || (N % 256) || (K % BK);
-        launch_cfg<1, 4, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, guard, s);
-    }
-    else if (N <= 64)
-    {
-        const bool guard = !vec_ok || (M % 256) || (N % 64) || (K % BK);
-        launch_cfg<4, 1, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, guard, s);
-    }
-    else
-    {
-        const bool guard = !vec_ok || (M % 128) || (N % 128) || (K % BK);
-        launch_cfg<2, 2, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, guard, s);
+    case kSkinnyM:
+        launch_cfg<1, 4, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
+                                           p.k_split, part, s);
+        break;
+    case kSkinnyN:
+        launch_cfg<4, 1, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
+                                           p.k_split, part, s);
+        break;
+    case kTall:
+        launch_cfg<4, 2, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
+                                           p.k_split, part, s);
+        break;
+    default:
+        launch_cfg<2, 2, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
+                                           p.k_split, part, s);
+        break;
     }
 }
 
 int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, size_t K, size_t lda, size_t ldb,
-                  size_t sA, size_t sB, size_t sC, bool tA, bool tB, float alpha, size_t batch, void* stream)
+                  size_t sA, size_t sB, size_t sC, bool tA, bool tB, float alpha, size_t batch, void* workspace,
+                  size_t ws_bytes, void* stream)
 {
     if (M == 0 || N == 0 || batch == 0) return 0;
     if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || batch > 65535) return -1;
     auto s = static_cast<hipStream_t>(stream);
+    Plan p = plan_gemm(M, N, K, batch, workspace != nullptr);
+    if (p.splits > 1 && static_cast<size_t>(p.splits) * batch * M * N * sizeof(float) > ws_bytes)
+        p = plan_gemm(M, N, K, batch, false);
+    float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K, b = (int)batch;
-    if (!tA && !tB) launch_trans<false, false>(A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, s);
-    else if (!tA && tB) launch_trans<false, true>(A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, s);
-    else if (tA && !tB) launch_trans<true, false>(A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, s);
-    else launch_trans<true, true>(A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, s);
+    if (!tA && !tB) launch_trans<false, false>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s);
+    else if (!tA && tB) launch_trans<false, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s);
+    else if (tA && !tB) launch_trans<true, false>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s);
+    else launch_trans<true, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s);
+    if (p.splits > 1)
+    {
+        const long total = (long)batch * (long)M * (long)N;
+        hipLaunchKernelGGL(k_splitk_reduce, dim3(grid_for(static_cast<size_t>(total / 4 + 1), 256, 256 * 16)),
+                           dim3(256), 0, s, part, C, total, p.splits, alpha);
+    }
     return launch_status();
 }
 
@@ -269,18 +403,15 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
 
 using namespace nnhip;
 
-extern "C" int nnhip_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
-                            size_t B_cols, int transA, int transB, void* stream)
+extern "C" size_t nnhip_gemm_workspace_bytes(size_t M, size_t N, size_t K, size_t batch)
 {
-    const size_t M = transA ? A_cols : A_rows, K = transA ? A_rows : A_cols;
-    const size_t K2 = transB ? B_cols : B_rows, N = transB ? B_rows : B_cols;
-    if (K != K2) return -2;
-    return gemm_dispatch(A, B, C, M, N, K, A_cols, B_cols, 0, 0, 0, transA != 0, transB != 0, 1.0f, 1, stream);
+    const Plan p = plan_gemm(M, N, K, batch, true);
+    return p.splits > 1 ? static_cast<size_t>(p.splits) * batch * M * N * sizeof(float) : 0;
 }
 
-extern "C" int nnhip_batched_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols,
-                                    size_t B_rows, size_t B_cols, size_t batch, int transA, int transB, float alpha,
-                                    void* stream)
+extern "C" int nnhip_gemm(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
+                          size_t B_cols, size_t batch, int transA, int transB, float alpha, void* workspace,
+                          size_t workspace_bytes, void* stream)
 {
     if (batch == 0 || A_rows % batch || B_rows % batch) return -2;
     const size_t ar = A_rows / batch, br = B_rows / batch;
@@ -288,5 +419,18 @@ extern "C" int nnhip_batched_matmul(const float* A, const float* B, float* C, si
     const size_t K2 = transB ? B_cols : br, N = transB ? br : B_cols;
     if (K != K2) return -2;
     return gemm_dispatch(A, B, C, M, N, K, A_cols, B_cols, ar * A_cols, br * B_cols, M * N, transA != 0, transB != 0,
-                         alpha, batch, stream);
+                         alpha, batch, workspace, workspace_bytes, stream);
+}
+
+extern "C" int nnhip_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
+                            size_t B_cols, int transA, int transB, void* stream)
+{
+    return nnhip_gemm(A, B, C, A_rows, A_cols, B_rows, B_cols, 1, transA, transB, 1.0f, nullptr, 0, stream);
+}
+
+extern "C" int nnhip_batched_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols,
+                                    size_t B_rows, size_t B_cols, size_t batch, int transA, int transB, float alpha,
+                                    void* stream)
+{
+    return nnhip_gemm(A, B, C, A_rows, A_cols, B_rows, B_cols, batch, transA, transB, alpha, nullptr, 0, stream);
 }

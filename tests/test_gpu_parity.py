@@ -41,6 +41,24 @@ def test_matmul(hip, cpu, M, N, K, tA, tB):
     assert np.all(np.abs(h - ref) <= 2 * K * 2.0 ** -24 * absprod + 1e-30)
 
 
+@pytest.mark.parametrize("tA,tB", [(False, True), (True, False), (False, False)])
+@pytest.mark.parametrize("M,N,K,batch", [(96, 128, 4096, 1), (768, 768, 2048, 1), (50, 70, 3001, 1),
+                                         (100, 100, 2048, 2), (300, 200, 1500, 1)])
+def test_matmul_split_k(hip, cpu, M, N, K, batch, tA, tB):
+    """Small output grids with long K take the split-K path (partials summed in slice order)."""
+    rng = np.random.default_rng(M + N + K)
+    A = uniform(rng, (batch * (K if tA else M), M if tA else K))
+    B = uniform(rng, (batch * (N if tB else K), K if tB else N))
+    h, c = both(hip, cpu, lambda e: e.batched_matmul(e.tensor(A), e.tensor(B), batch, tA, tB, 0.5))
+    assert nrm_err(h, c) <= 1e-5
+    Ae = A.reshape(batch, -1, A.shape[1]).astype(np.float64)
+    Be = B.reshape(batch, -1, B.shape[1]).astype(np.float64)
+    ref = 0.5 * np.concatenate([(Ae[b].T if tA else Ae[b]) @ (Be[b].T if tB else Be[b]) for b in range(batch)])
+    absprod = 0.5 * np.concatenate([np.abs(Ae[b].T if tA else Ae[b]) @ np.abs(Be[b].T if tB else Be[b])
+                                    for b in range(batch)])
+    assert np.all(np.abs(h - ref) <= 2 * K * 2.0 ** -24 * absprod + 1e-30)
+
+
 @pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
 def test_batched_matmul_alpha(hip, cpu, tA, tB):
     rng = np.random.default_rng(7)
