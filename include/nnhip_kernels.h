@@ -23,6 +23,9 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+#if defined(__GNUC__)
+#pragma GCC visibility push(default) /* the library is built with hidden visibility */
+#endif
 
 /* ── GEMM (fp32 MFMA) ────────────────────────────────────────────────────
  * C (M,N) = alpha * op(A) op(B); A stored (A_rows, A_cols), B stored (B_rows, B_cols).
@@ -140,6 +143,9 @@ size_t nnhip_eval_expr_workspace_bytes(const nnhip_expr_program* prog, size_t ro
 int nnhip_eval_expr(const nnhip_expr_program* prog, const float* const* inputs, float* out, size_t rows,
                     size_t cols, int vector_out, void* workspace, void* stream);
 
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
 #ifdef __cplusplus
 }
 #endif

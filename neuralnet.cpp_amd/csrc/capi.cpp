@@ -19,7 +19,7 @@ std::unique_ptr<nn::ComputeEngine> make_hip_engine(std::string& err)
 NN_DEFINE_ENGINE_CAPI(nnhip_, make_hip_engine(err))
 
 // Measurement hooks (no reference counterpart): GEMM kernel time by HIP events.
-extern "C" int nnhip_engine_profile_gemm(void* e, int enable)
+extern "C" NN_CAPI_EXPORT int nnhip_engine_profile_gemm(void* e, int enable)
 {
     auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
     if (!h) return nn::capi::set_error("profile: not a HIP engine");
@@ -27,7 +27,7 @@ extern "C" int nnhip_engine_profile_gemm(void* e, int enable)
     return 0;
 }
 
-extern "C" int nnhip_engine_profile_gemm_read(void* e, double* launches, double* flops, double* ms)
+extern "C" NN_CAPI_EXPORT int nnhip_engine_profile_gemm_read(void* e, double* launches, double* flops, double* ms)
 {
     auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
     if (!h) return nn::capi::set_error("profile: not a HIP engine");
@@ -35,7 +35,7 @@ extern "C" int nnhip_engine_profile_gemm_read(void* e, double* launches, double*
     return r ? 0 : nn::capi::set_error(r.error().message);
 }
 
-extern "C" void* nnhip_engine_stream(void* e)
+extern "C" NN_CAPI_EXPORT void* nnhip_engine_stream(void* e)
 {
     auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
     return h ? h->stream() : nullptr;

@@ -404,9 +404,14 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
 // Defines every symbol of include/nnhip_engine.h with the given prefix.
 // MAKE_ENGINE must be an expression yielding std::unique_ptr<nn::ComputeEngine>
 // or returning an error string through `err` (a std::string).
+// Libraries are built with hidden visibility; only these entry points are
+// exported, so two libraries defining the same inline C++ code (the product
+// and the test oracle) never bind to each other's copies in one process.
+#define NN_CAPI_EXPORT __attribute__((visibility("default")))
 #define NN_CAPI_CAT2(a, b) a##b
 #define NN_CAPI_CAT(a, b) NN_CAPI_CAT2(a, b)
 #define NN_DEFINE_ENGINE_CAPI(P, MAKE_ENGINE)                                                                       \
+    _Pragma("GCC visibility push(default)")                                                                         \
     extern "C" {                                                                                                    \
     const char* NN_CAPI_CAT(P, last_error)(void) { return nn::capi::last_error().c_str(); }                        \
     int NN_CAPI_CAT(P, engine_create)(void** out)                                                                  \
@@ -521,4 +526,5 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
     {                                                                                                               \
         return nn::capi::gpt_train_step(static_cast<nn::capi::GptSession*>(g), loss);                              \
     }                                                                                                               \
-    }
+    }                                                                                                               \
+    _Pragma("GCC visibility pop")

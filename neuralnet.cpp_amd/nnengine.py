@@ -49,7 +49,7 @@ def hip_library() -> ctypes.CDLL:
     if not os.path.exists(HIP_LIB_PATH):
         raise EngineError(f"{HIP_LIB_PATH} is missing: run __graft_entry__.build() first "
                           "(there is no CPU fallback)")
-    return ctypes.CDLL(HIP_LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+    return ctypes.CDLL(HIP_LIB_PATH)
 
 
 class _GptConfig(ctypes.Structure):
@@ -269,14 +269,7 @@ class Engine:
         return self._op("SELECT_SCALAR_COND", [A, then_t], 1, [COMPARE[cmp], scalar_b, scalar_else])[0]
 
     def eval_expr(self, spec: "ExprSpec", inputs: Sequence[Tensor], rows: int, cols: int, vector_out=False):
-        ins = np.zeros(max(1, len(spec.instrs)) * 8, dtype=np.uint8)
-        for i, t in enumerate(spec.instrs):
-            ins[8 * i:8 * i + 8] = t
-        vk = np.zeros(max(1, 2 * len(spec.views)), dtype=np.uint8)
-        vp = np.zeros(max(1, len(spec.views)), dtype=np.uint32)
-        for i, (k, neg, p) in enumerate(spec.views):
-            vk[2 * i], vk[2 * i + 1], vp[i] = k, neg, p
-        cs = np.asarray(spec.consts if spec.consts else [0.0], dtype=np.float32)
+        ins, vk, vp, cs = spec.serialise()
         inh = (ctypes.c_void_p * max(1, len(inputs)))(*[t._h.value for t in inputs])
         out = ctypes.c_void_p()
         self._check(self._f["engine_eval_expr"](
@@ -340,6 +333,19 @@ class ExprSpec:
     def const(self, v):
         self.consts.append(float(v))
         return len(self.consts) - 1
+
+    def serialise(self):
+        """Arrays in the layout of nnhip_engine_eval_expr: instrs (n,8) u8, view kinds
+        {kind, negate} pairs u8, view params u32, consts f32 (each at least one entry long)."""
+        ins = np.zeros((max(1, len(self.instrs)), 8), dtype=np.uint8)
+        for i, t in enumerate(self.instrs):
+            ins[i] = t
+        vk = np.zeros(max(1, 2 * len(self.views)), dtype=np.uint8)
+        vp = np.zeros(max(1, len(self.views)), dtype=np.uint32)
+        for i, (k, neg, p) in enumerate(self.views):
+            vk[2 * i], vk[2 * i + 1], vp[i] = k, neg, p
+        cs = np.asarray(self.consts if self.consts else [0.0], dtype=np.float32)
+        return ins, vk, vp, cs
 
 
 def reg(i): return (OPND["Reg"], i)

@@ -9,4 +9,4 @@
 
 NN_DEFINE_ENGINE_CAPI(nnoracle_, std::unique_ptr<nn::ComputeEngine>(new nn::oracle::CpuEngine()))
 
-extern "C" size_t nnoracle_thread_count(void) { return nn::oracle::pool().size(); }
+extern "C" NN_CAPI_EXPORT size_t nnoracle_thread_count(void) { return nn::oracle::pool().size(); }
