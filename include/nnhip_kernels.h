@@ -128,6 +128,30 @@ int nnhip_col_softmax_sparse_forward(const float* logits, const float* labels, c
 int nnhip_row_softmax(const float* X, float* out, size_t rows, size_t cols, void* stream);
 int nnhip_row_softmax_backward(const float* Y, const float* G, float* out, size_t rows, size_t cols, void* stream);
 
+/* ── fused GPT-layer programs (eval_expr fast paths) ─────────────────────
+ * One kernel per ExprSpec program the layers issue, the role of the reference's ahead-of-time fused
+ * shaders (tools/scan_exprs.cpp, tools/gen_fused.cpp; no CUDA counterpart). Matrices are (F, N) with
+ * N % 4 == 0 and 16-byte aligned pointers, else -5 is returned and nothing runs. vectors: gamma and
+ * row results (F); m, rinv and column results (N).
+ *   RMSNorm forward, compute_layer.hpp:733-754:  sumsq  out[c] = sum_r X[r,c]^2;
+ *     colbcast_mul  out = X * v[c];  rowbcast_mul  out = X * v[r].
+ *   RMSNorm backward, compute_layer.hpp:772-795:  bwd_colsum  out[c] = sum_r G*gamma[r]*Nrm;
+ *     bwd_dx  out = (G*gamma[r] - m[c]*Nrm) * rinv[c];  bwd_rowsum  out[r] = sum_c G*gamma[r]*Nrm.
+ *   SwiGLU backward, compute_layer.hpp:436-444 (count % 4 == 0):
+ *     grad_gate = G*up*(s*(1 + gate*(1 - s)));  grad_up = G*gate*s. */
+int nnhip_rmsnorm_sumsq(const float* X, float* out, size_t F, size_t N, void* stream);
+int nnhip_colbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream);
+int nnhip_rowbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream);
+int nnhip_rmsnorm_bwd_colsum(const float* G, const float* gamma, const float* Nrm, float* out, size_t F, size_t N,
+                             void* stream);
+int nnhip_rmsnorm_bwd_dx(const float* G, const float* gamma, const float* m, const float* Nrm, const float* rinv,
+                         float* out, size_t F, size_t N, void* stream);
+int nnhip_rmsnorm_bwd_rowsum(const float* G, const float* gamma, const float* Nrm, float* out, size_t F, size_t N,
+                             void* stream);
+int nnhip_swiglu_grad_gate(const float* G, const float* up, const float* s, const float* gate, float* out,
+                           size_t count, void* stream);
+int nnhip_swiglu_grad_up(const float* G, const float* gate, const float* s, float* out, size_t count, void* stream);
+
 /* ── ExprSpec interpreter (no CUDA counterpart; cpu_engine.hpp:1298-1659) ──
  * The program is the ExprSpec in serialised form (see nnhip_engine.h); inputs[k] are device pointers
  * shaped per view. Workspace from nnhip_eval_expr_workspace_bytes. */

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "nn/expr_dsl.hpp"
+#include "nn/layer_exprs.hpp"
 #include "nnhip_kernels.h"
 
 namespace nn
@@ -158,26 +159,67 @@ Result<void> vec_ok(const Tensor& t, std::size_t rows, const char* who, const ch
     return {};
 }
 
-// Canonical Softmax::forward / ::backward programs (compute_layer.hpp:832-862),
-// built with the same DSL the layer uses, for structural comparison.
-const ExprSpec& softmax_fwd_spec()
+// A layer program (include/nn/layer_exprs.hpp) in canonical form, with the
+// argument each input slot of the folded spec reads.
+struct Canon
 {
-    static const ExprSpec s = [] {
-        Tensor t = Tensor::cpu(1, 1);
-        return dsl::to_expr_spec(dsl::exp(dsl::leaf(t) - dsl::row_reduce_max(t)) /
-                                 dsl::row_reduce_sum(dsl::exp(dsl::leaf(t) - dsl::row_reduce_max(t))))
-            .first;
-    }();
-    return s;
+    ExprSpec spec;
+    std::vector<int> arg_of_slot;
+    int nargs = 0;
+};
+
+template <class Build>
+Canon make_canon(int nargs, Build build)
+{
+    std::vector<Tensor> a;
+    for (int i = 0; i < nargs; ++i) a.push_back(Tensor::cpu(static_cast<std::size_t>(i) + 1, 1));
+    auto [spec, ins] = dsl::to_expr_spec(build(a));
+    Canon c{std::move(spec), {}, nargs};
+    for (const Tensor& t : ins) c.arg_of_slot.push_back(static_cast<int>(t.rows()) - 1);
+    return c;
 }
-const ExprSpec& softmax_bwd_spec()
+
+// True when `spec` is the canonical program and all slots of one argument
+// hold the same device tensor; args[] then receives one pointer per argument.
+bool bind(const Canon& c, const ExprSpec& spec, std::span<const Tensor> inputs, const float** args)
 {
-    static const ExprSpec s = [] {
-        Tensor t = Tensor::cpu(1, 1);
-        return dsl::to_expr_spec(dsl::leaf(t) * (dsl::leaf(t) - dsl::row_reduce_sum(dsl::leaf(t) * dsl::leaf(t))))
-            .first;
-    }();
-    return s;
+    if (inputs.size() != c.arg_of_slot.size() || !expr_spec_equal(spec, c.spec)) return false;
+    for (int i = 0; i < c.nargs; ++i) args[i] = nullptr;
+    for (std::size_t k = 0; k < inputs.size(); ++k)
+    {
+        const float*& a = args[c.arg_of_slot[k]];
+        const float* p = inputs[k].dev_ptr();
+        if (a == nullptr)
+            a = p;
+        else if (a != p)
+            return false;
+    }
+    return true;
+}
+
+enum class LayerProg
+{
+    SoftmaxFwd, SoftmaxBwd, RmsSumSq, RmsNormalize, RmsScale, RmsBwdColSum, RmsBwdDx, RmsBwdRowSum, SwigluGate,
+    SwigluUp, Count
+};
+
+const Canon& canon(LayerProg p)
+{
+    namespace le = layer_exprs;
+    static const Canon table[] = {
+        make_canon(1, [](auto& a) { return le::softmax_rows(a[0]); }),
+        make_canon(2, [](auto& a) { return le::softmax_rows_backward(a[0], a[1]); }),
+        make_canon(1, [](auto& a) { return le::rms_sum_sq(a[0]); }),
+        make_canon(2, [](auto& a) { return le::rms_normalize(a[0], a[1]); }),
+        make_canon(2, [](auto& a) { return le::rms_scale(a[0], a[1]); }),
+        make_canon(3, [](auto& a) { return le::rms_bwd_colsum(a[0], a[1], a[2]); }),
+        make_canon(5, [](auto& a) { return le::rms_bwd_dx(a[0], a[1], a[2], a[3], a[4]); }),
+        make_canon(3, [](auto& a) { return le::rms_bwd_rowsum(a[0], a[1], a[2]); }),
+        make_canon(4, [](auto& a) { return le::swiglu_grad_gate(a[0], a[1], a[2], a[3]); }),
+        make_canon(3, [](auto& a) { return le::swiglu_grad_up(a[0], a[1], a[2]); }),
+    };
+    static_assert(sizeof table / sizeof table[0] == static_cast<std::size_t>(LayerProg::Count));
+    return table[static_cast<int>(p)];
 }
 
 } // namespace
@@ -779,22 +821,7 @@ Result<Tensor> HipEngine::eval_impl_(const ExprSpec& spec, std::span<const Tenso
     }
     if (rows * cols == 0) return alloc_(rows, cols);   // the reference returns the (rows, cols) shape here
 
-    // Fast paths: the Softmax layer's forward / backward programs on one row tensor.
-    if (!vector_out && expr_spec_equal(spec, softmax_fwd_spec()) && inputs[0].dev_ptr() == inputs[1].dev_ptr() &&
-        inputs[0].dev_ptr() == inputs[2].dev_ptr() && inputs[0].dev_ptr() == inputs[3].dev_ptr())
-    {
-        NN_TRY(o, alloc_(rows, cols));
-        NN_CHECK(kernel_(nnhip_row_softmax(D(inputs[0]), W(o), rows, cols, stream_), "eval_expr(softmax)"));
-        return o;
-    }
-    if (!vector_out && expr_spec_equal(spec, softmax_bwd_spec()) && inputs[0].dev_ptr() == inputs[2].dev_ptr() &&
-        inputs[1].dev_ptr() == inputs[3].dev_ptr())
-    {
-        NN_TRY(o, alloc_(rows, cols));
-        NN_CHECK(kernel_(nnhip_row_softmax_backward(D(inputs[0]), D(inputs[1]), W(o), rows, cols, stream_),
-                         "eval_expr(softmax backward)"));
-        return o;
-    }
+    if (auto fused = fused_layer_program_(spec, inputs, rows, cols, vector_out)) return std::move(*fused);
 
     nnhip_expr_program p;
     std::memset(&p, 0, sizeof p);
@@ -828,6 +855,67 @@ Result<Tensor> HipEngine::eval_impl_(const ExprSpec& spec, std::span<const Tenso
                     "the reduced axis");
     NN_CHECK(kernel_(rc, "eval_expr"));
     return o;
+}
+
+// Fused kernels for the layer programs (k_fused.hip, k_softmax.hip). Returns
+// nullopt when the program, its bindings or its shape are not one of those;
+// the generic interpreter then evaluates it.
+std::optional<Result<Tensor>> HipEngine::fused_layer_program_(const ExprSpec& spec, std::span<const Tensor> inputs,
+                                                              std::size_t rows, std::size_t cols, bool vector_out)
+{
+    const float* a[5] = {};
+    auto is = [&](LayerProg p) { return bind(canon(p), spec, inputs, a); };
+    const bool vec4 = cols % 4 == 0;
+    auto run = [&](std::size_t orow, std::size_t ocol, auto&& launch, const char* what) -> Result<Tensor> {
+        NN_TRY(o, alloc_(orow, ocol));
+        NN_CHECK(kernel_(launch(W(o)), what));
+        return o;
+    };
+    if (!vector_out)
+    {
+        if (is(LayerProg::SoftmaxFwd))
+            return run(rows, cols, [&](float* o) { return nnhip_row_softmax(a[0], o, rows, cols, stream_); },
+                       "eval_expr(softmax)");
+        if (is(LayerProg::SoftmaxBwd))
+            return run(rows, cols,
+                       [&](float* o) { return nnhip_row_softmax_backward(a[0], a[1], o, rows, cols, stream_); },
+                       "eval_expr(softmax backward)");
+        if (!vec4) return std::nullopt;
+        if (is(LayerProg::RmsNormalize))
+            return run(rows, cols, [&](float* o) { return nnhip_colbcast_mul(a[0], a[1], o, rows, cols, stream_); },
+                       "eval_expr(rmsnorm normalize)");
+        if (is(LayerProg::RmsScale))
+            return run(rows, cols, [&](float* o) { return nnhip_rowbcast_mul(a[0], a[1], o, rows, cols, stream_); },
+                       "eval_expr(rmsnorm scale)");
+        if (is(LayerProg::RmsBwdDx))
+            return run(rows, cols,
+                       [&](float* o) {
+                           return nnhip_rmsnorm_bwd_dx(a[0], a[1], a[2], a[3], a[4], o, rows, cols, stream_);
+                       },
+                       "eval_expr(rmsnorm backward dx)");
+        if (is(LayerProg::SwigluGate))
+            return run(rows, cols,
+                       [&](float* o) { return nnhip_swiglu_grad_gate(a[0], a[1], a[2], a[3], o, rows * cols, stream_); },
+                       "eval_expr(swiglu grad gate)");
+        if (is(LayerProg::SwigluUp))
+            return run(rows, cols,
+                       [&](float* o) { return nnhip_swiglu_grad_up(a[0], a[1], a[2], o, rows * cols, stream_); },
+                       "eval_expr(swiglu grad up)");
+        return std::nullopt;
+    }
+    if (!vec4) return std::nullopt;
+    if (is(LayerProg::RmsSumSq))
+        return run(1, cols, [&](float* o) { return nnhip_rmsnorm_sumsq(a[0], o, rows, cols, stream_); },
+                   "eval_expr_reduce(rmsnorm sum of squares)");
+    if (is(LayerProg::RmsBwdColSum))
+        return run(1, cols,
+                   [&](float* o) { return nnhip_rmsnorm_bwd_colsum(a[0], a[1], a[2], o, rows, cols, stream_); },
+                   "eval_expr_reduce(rmsnorm backward column sum)");
+    if (is(LayerProg::RmsBwdRowSum))
+        return run(rows, 1,
+                   [&](float* o) { return nnhip_rmsnorm_bwd_rowsum(a[0], a[1], a[2], o, rows, cols, stream_); },
+                   "eval_expr_reduce(rmsnorm backward row sum)");
+    return std::nullopt;
 }
 
 } // namespace nn

@@ -1,0 +1,320 @@
+// k_fused.hip — one kernel per ExprSpec program of the GPT layers.
+//
+// The HIP engine recognises the RMSNorm and SwiGLU programs structurally
+// (include/nn/layer_exprs.hpp) and runs them here instead of in the generic
+// interpreter, which is what the reference's ahead-of-time fused shaders do
+// for their GPU engine (tools/scan_exprs.cpp, tools/gen_fused.cpp). Each
+// kernel evaluates its program with the same operation order as the program
+// (left operand before right); reductions sum in a fixed order.
+//
+// All tensors are row-major (F, N) fp32 with N % 4 == 0 and 16-byte aligned
+// base pointers (the entry points reject anything else with -5), so every
+// thread moves float4s. The kernels are HBM-bound: per element they read
+// each (F, N) input once and write each output once.
+#include "common.hpp"
+#include "nnhip_kernels.h"
+
+namespace nnhip
+{
+namespace
+{
+
+constexpr unsigned kT = 256;
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+// ── elementwise over (rows, cols): one float4 of one row per thread ──────────
+template <class Op>
+__global__ __launch_bounds__(kT) void k_fused_ew(Op op, unsigned rows, unsigned cols4)
+{
+    const unsigned q = blockIdx.x * kT + threadIdx.x;
+    if (q >= cols4) return;
+    for (unsigned r = blockIdx.y; r < rows; r += gridDim.y) op(r, q);
+}
+
+// normed = x * colbcast(v)
+struct ColBcastMul
+{
+    const float* x;
+    const float* v;
+    float* o;
+    size_t cols;
+    __device__ void operator()(unsigned r, unsigned q) const
+    {
+        const size_t i = size_t(r) * cols + 4u * q;
+        const float4 a = ld4(x + i), b = ld4(v + 4u * q);
+        st4(o + i, make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w));
+    }
+};
+
+// out = x * rowbcast(v)
+struct RowBcastMul
+{
+    const float* x;
+    const float* v;
+    float* o;
+    size_t cols;
+    __device__ void operator()(unsigned r, unsigned q) const
+    {
+        const size_t i = size_t(r) * cols + 4u * q;
+        const float4 a = ld4(x + i);
+        const float s = v[r];
+        st4(o + i, make_float4(a.x * s, a.y * s, a.z * s, a.w * s));
+    }
+};
+
+// dx = (g * gamma[r] - m[c] * normed) * rinv[c]
+struct RmsDx
+{
+    const float* g;
+    const float* gamma;
+    const float* m;
+    const float* n;
+    const float* rinv;
+    float* o;
+    size_t cols;
+    __device__ static float one(float g, float gr, float m, float n, float ri) { return (g * gr - m * n) * ri; }
+    __device__ void operator()(unsigned r, unsigned q) const
+    {
+        const size_t i = size_t(r) * cols + 4u * q;
+        const float4 a = ld4(g + i), b = ld4(m + 4u * q), c = ld4(n + i), d = ld4(rinv + 4u * q);
+        const float gr = gamma[r];
+        st4(o + i, make_float4(one(a.x, gr, b.x, c.x, d.x), one(a.y, gr, b.y, c.y, d.y), one(a.z, gr, b.z, c.z, d.z),
+                               one(a.w, gr, b.w, c.w, d.w)));
+    }
+};
+
+// ── flat elementwise (SwiGLU backward) ───────────────────────────────────────
+template <class Op>
+__global__ __launch_bounds__(kT) void k_fused_flat(Op op, size_t n4)
+{
+    for (size_t q = size_t(blockIdx.x) * kT + threadIdx.x; q < n4; q += size_t(gridDim.x) * kT) op(4 * q);
+}
+
+// grad_gate = g * up * (s * (1 + gate * (1 - s)))
+struct SwigluGradGate
+{
+    const float* g;
+    const float* up;
+    const float* s;
+    const float* gate;
+    float* o;
+    __device__ static float one(float g, float u, float s, float t) { return (g * u) * (s * (1.0f + t * (1.0f - s))); }
+    __device__ void operator()(size_t i) const
+    {
+        const float4 a = ld4(g + i), b = ld4(up + i), c = ld4(s + i), d = ld4(gate + i);
+        st4(o + i, make_float4(one(a.x, b.x, c.x, d.x), one(a.y, b.y, c.y, d.y), one(a.z, b.z, c.z, d.z),
+                               one(a.w, b.w, c.w, d.w)));
+    }
+};
+
+// grad_up = g * gate * s
+struct SwigluGradUp
+{
+    const float* g;
+    const float* gate;
+    const float* s;
+    float* o;
+    __device__ void operator()(size_t i) const
+    {
+        const float4 a = ld4(g + i), b = ld4(gate + i), c = ld4(s + i);
+        st4(o + i, make_float4((a.x * b.x) * c.x, (a.y * b.y) * c.y, (a.z * b.z) * c.z, (a.w * b.w) * c.w));
+    }
+};
+
+// ── column sums: out[c] = sum_r f(r, c) ──────────────────────────────────────
+// A workgroup owns 32 columns (8 float4s: one 128-byte line per row) and
+// splits the rows over 32 row groups; the 32 partial sums are added in
+// row-group order, so the result does not depend on scheduling.
+constexpr unsigned kColQuads = 8, kRowGroups = kT / kColQuads;
+
+struct SumSq
+{
+    const float* x;
+    size_t cols;
+    __device__ float4 operator()(unsigned r, unsigned q) const
+    {
+        const float4 a = ld4(x + size_t(r) * cols + 4u * q);
+        return make_float4(a.x * a.x, a.y * a.y, a.z * a.z, a.w * a.w);
+    }
+};
+
+// g * gamma[r] * normed
+struct GGammaN
+{
+    const float* g;
+    const float* gamma;
+    const float* n;
+    size_t cols;
+    __device__ float4 operator()(unsigned r, unsigned q) const
+    {
+        const size_t i = size_t(r) * cols + 4u * q;
+        const float4 a = ld4(g + i), c = ld4(n + i);
+        const float gr = gamma[r];
+        return make_float4((a.x * gr) * c.x, (a.y * gr) * c.y, (a.z * gr) * c.z, (a.w * gr) * c.w);
+    }
+};
+
+template <class F>
+__global__ __launch_bounds__(kT) void k_fused_colsum(F f, float* out, unsigned rows, unsigned cols4)
+{
+    __shared__ float4 part[kRowGroups][kColQuads];
+    const unsigned qi = threadIdx.x % kColQuads, rg = threadIdx.x / kColQuads;
+    const unsigned q = blockIdx.x * kColQuads + qi;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < cols4)
+        for (unsigned r = rg; r < rows; r += kRowGroups)
+        {
+            const float4 v = f(r, q);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+    part[rg][qi] = acc;
+    __syncthreads();
+    if (threadIdx.x < kColQuads)
+    {
+        const unsigned qo = blockIdx.x * kColQuads + threadIdx.x;
+        float4 s = part[0][threadIdx.x];
+        for (unsigned k = 1; k < kRowGroups; ++k)
+        {
+            const float4 v = part[k][threadIdx.x];
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+        if (qo < cols4) st4(out + 4u * qo, s);
+    }
+}
+
+// ── row sums: out[r] = sum_c g[r,c] * gamma[r] * normed[r,c], one workgroup per row ──
+__global__ __launch_bounds__(kT) void k_fused_rowsum_ggn(const float* g, const float* gamma, const float* n,
+                                                         float* out, unsigned cols4, size_t cols)
+{
+    __shared__ float wsum[kT / 64];
+    const unsigned r = blockIdx.x;
+    const float gr = gamma[r];
+    const float* gp = g + size_t(r) * cols;
+    const float* np = n + size_t(r) * cols;
+    float acc = 0.f;
+    for (unsigned q = threadIdx.x; q < cols4; q += kT)
+    {
+        const float4 a = ld4(gp + 4u * q), c = ld4(np + 4u * q);
+        acc += (a.x * gr) * c.x;
+        acc += (a.y * gr) * c.y;
+        acc += (a.z * gr) * c.z;
+        acc += (a.w * gr) * c.w;
+    }
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        float s = wsum[0];
+        for (unsigned w = 1; w < kT / 64; ++w) s += wsum[w];
+        out[r] = s;
+    }
+}
+
+constexpr int kBadShape = -5;
+
+bool shape_ok(size_t rows, size_t cols, std::initializer_list<const void*> ptrs)
+{
+    if (cols % 4 != 0 || cols / 4 > 0xffffffffu || rows > 0xffffffffu) return false;
+    for (const void* p : ptrs)
+        if (!aligned16(p)) return false;
+    return true;
+}
+
+template <class Op>
+int launch_ew(Op op, size_t rows, size_t cols, hipStream_t s)
+{
+    if (rows == 0 || cols == 0) return 0;
+    const unsigned cols4 = unsigned(cols / 4);
+    const dim3 grid((cols4 + kT - 1) / kT, unsigned(rows < 65535 ? rows : 65535));
+    hipLaunchKernelGGL(k_fused_ew<Op>, grid, dim3(kT), 0, s, op, unsigned(rows), cols4);
+    return launch_status();
+}
+
+template <class F>
+int launch_colsum(F f, float* out, size_t rows, size_t cols, hipStream_t s)
+{
+    if (cols == 0) return 0;
+    const unsigned cols4 = unsigned(cols / 4);
+    hipLaunchKernelGGL(k_fused_colsum<F>, dim3((cols4 + kColQuads - 1) / kColQuads), dim3(kT), 0, s, f, out,
+                       unsigned(rows), cols4);
+    return launch_status();
+}
+
+template <class Op>
+int launch_flat(Op op, size_t count, hipStream_t s)
+{
+    if (count == 0) return 0;
+    const size_t n4 = count / 4;
+    hipLaunchKernelGGL(k_fused_flat<Op>, dim3(grid_for(n4, kT, 1u << 16)), dim3(kT), 0, s, op, n4);
+    return launch_status();
+}
+
+} // namespace
+} // namespace nnhip
+
+using namespace nnhip;
+
+extern "C" int nnhip_rmsnorm_sumsq(const float* X, float* out, size_t F, size_t N, void* stream)
+{
+    if (!shape_ok(F, N, {X, out})) return kBadShape;
+    return launch_colsum(SumSq{X, N}, out, F, N, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_colbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream)
+{
+    if (!shape_ok(F, N, {X, v, out})) return kBadShape;
+    return launch_ew(ColBcastMul{X, v, out, N}, F, N, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_rowbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream)
+{
+    if (!shape_ok(F, N, {X, out})) return kBadShape;
+    return launch_ew(RowBcastMul{X, v, out, N}, F, N, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_rmsnorm_bwd_colsum(const float* G, const float* gamma, const float* normed, float* out, size_t F,
+                                        size_t N, void* stream)
+{
+    if (!shape_ok(F, N, {G, normed, out})) return kBadShape;
+    return launch_colsum(GGammaN{G, gamma, normed, N}, out, F, N, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_rmsnorm_bwd_dx(const float* G, const float* gamma, const float* m, const float* normed,
+                                    const float* rinv, float* out, size_t F, size_t N, void* stream)
+{
+    if (!shape_ok(F, N, {G, m, normed, rinv, out})) return kBadShape;
+    return launch_ew(RmsDx{G, gamma, m, normed, rinv, out, N}, F, N, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_rmsnorm_bwd_rowsum(const float* G, const float* gamma, const float* normed, float* out, size_t F,
+                                        size_t N, void* stream)
+{
+    if (!shape_ok(F, N, {G, normed})) return kBadShape;
+    if (F == 0) return 0;
+    hipLaunchKernelGGL(k_fused_rowsum_ggn, dim3(unsigned(F)), dim3(kT), 0, static_cast<hipStream_t>(stream), G, gamma,
+                       normed, out, unsigned(N / 4), N);
+    return launch_status();
+}
+
+extern "C" int nnhip_swiglu_grad_gate(const float* G, const float* up, const float* s, const float* gate, float* out,
+                                      size_t count, void* stream)
+{
+    if (!shape_ok(1, count, {G, up, s, gate, out})) return kBadShape;
+    return launch_flat(SwigluGradGate{G, up, s, gate, out}, count, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_swiglu_grad_up(const float* G, const float* gate, const float* s, float* out, size_t count,
+                                    void* stream)
+{
+    if (!shape_ok(1, count, {G, gate, s, out})) return kBadShape;
+    return launch_flat(SwigluGradUp{G, gate, s, out}, count, static_cast<hipStream_t>(stream));
+}

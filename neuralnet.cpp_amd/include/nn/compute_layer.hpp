@@ -24,6 +24,7 @@
 
 #include "compute_engine.hpp"
 #include "expr_dsl.hpp"
+#include "layer_exprs.hpp"
 #include "model_spec.hpp"
 #include "tensor.hpp"
 
@@ -154,14 +155,11 @@ public:
     Result<Tensor> backward(ComputeEngine& engine, const Tensor& grad_output) override
     {
         const std::size_t rows = d_ff_, cols = grad_output.cols();
-        const Scalar one{1};
         NN_TRY(grad_gate, dsl::compute(engine,
-                                       dsl::leaf(grad_output) * dsl::leaf(up_cache_) *
-                                           (dsl::leaf(sigmoid_cache_) *
-                                            (one + dsl::leaf(gate_cache_) * (one - dsl::leaf(sigmoid_cache_)))),
+                                       layer_exprs::swiglu_grad_gate(grad_output, up_cache_, sigmoid_cache_,
+                                                                     gate_cache_),
                                        rows, cols));
-        NN_TRY(grad_up, dsl::compute(engine,
-                                     dsl::leaf(grad_output) * dsl::leaf(gate_cache_) * dsl::leaf(sigmoid_cache_),
+        NN_TRY(grad_up, dsl::compute(engine, layer_exprs::swiglu_grad_up(grad_output, gate_cache_, sigmoid_cache_),
                                      rows, cols));
         Tensor grad_input = engine.create_tensor(2 * d_ff_, cols);
         NN_CHECK(engine.zero(grad_input));
@@ -201,34 +199,27 @@ public:
             return fail("rmsnorm forward: input shape mismatch");
         const Scalar inv_f = Scalar{1} / static_cast<Scalar>(features_);
         const std::size_t F = features_, N = input.cols();
-        NN_TRY(s_raw, dsl::compute_reduce(engine, dsl::col_reduce_sum(dsl::leaf(input) * dsl::leaf(input)), F, N));
+        NN_TRY(s_raw, dsl::compute_reduce(engine, layer_exprs::rms_sum_sq(input), F, N));
         NN_TRY(scaled, engine.elementwise_binary_scalar(BinaryOp::Mul, s_raw, inv_f));
         NN_TRY(var_eps, engine.elementwise_binary_scalar(BinaryOp::Add, scaled, epsilon_));
         NN_TRY(rms_inv, engine.elementwise_unary(UnaryOp::Rsqrt, var_eps));
         rms_inv_cache_ = rms_inv;
-        NN_TRY(normed, dsl::compute(engine, dsl::leaf(input) * dsl::col_broadcast(rms_inv_cache_), F, N));
+        NN_TRY(normed, dsl::compute(engine, layer_exprs::rms_normalize(input, rms_inv_cache_), F, N));
         normed_cache_ = normed;
-        return dsl::compute(engine, dsl::leaf(normed_cache_) * dsl::row_broadcast(gamma_), F, N);
+        return dsl::compute(engine, layer_exprs::rms_scale(normed_cache_, gamma_), F, N);
     }
 
     Result<Tensor> backward(ComputeEngine& engine, const Tensor& grad_output) override
     {
         const Scalar inv_f = Scalar{1} / static_cast<Scalar>(features_);
         const std::size_t F = features_, N = grad_output.cols();
-        NN_TRY(m_raw, dsl::compute_reduce(engine,
-                                          dsl::col_reduce_sum(dsl::leaf(grad_output) * dsl::row_broadcast(gamma_) *
-                                                              dsl::leaf(normed_cache_)),
+        NN_TRY(m_raw, dsl::compute_reduce(engine, layer_exprs::rms_bwd_colsum(grad_output, gamma_, normed_cache_),
                                           F, N));
         NN_TRY(m, engine.elementwise_binary_scalar(BinaryOp::Mul, m_raw, inv_f));
         NN_TRY(grad_x, dsl::compute(engine,
-                                    (dsl::leaf(grad_output) * dsl::row_broadcast(gamma_) -
-                                     dsl::col_broadcast(m) * dsl::leaf(normed_cache_)) *
-                                        dsl::col_broadcast(rms_inv_cache_),
+                                    layer_exprs::rms_bwd_dx(grad_output, gamma_, m, normed_cache_, rms_inv_cache_),
                                     F, N));
-        NN_TRY(gg, dsl::compute_reduce(engine,
-                                       dsl::row_reduce_sum(dsl::leaf(grad_output) * dsl::row_broadcast(gamma_) *
-                                                           dsl::leaf(normed_cache_)),
-                                       F, N));
+        NN_TRY(gg, dsl::compute_reduce(engine, layer_exprs::rms_bwd_rowsum(grad_output, gamma_, normed_cache_), F, N));
         NN_CHECK(engine.add_inplace(grad_gamma_, gg));
         return grad_x;
     }
@@ -247,19 +238,13 @@ class Softmax final : public Layer
 public:
     Result<Tensor> forward(ComputeEngine& engine, const Tensor& input) override
     {
-        NN_TRY(out, dsl::compute(engine,
-                                 dsl::exp(dsl::leaf(input) - dsl::row_reduce_max(input)) /
-                                     dsl::row_reduce_sum(dsl::exp(dsl::leaf(input) - dsl::row_reduce_max(input))),
-                                 input.rows(), input.cols()));
+        NN_TRY(out, dsl::compute(engine, layer_exprs::softmax_rows(input), input.rows(), input.cols()));
         output_cache_ = out;
         return out;
     }
     Result<Tensor> backward(ComputeEngine& engine, const Tensor& grad_output) override
     {
-        return dsl::compute(engine,
-                            dsl::leaf(output_cache_) *
-                                (dsl::leaf(grad_output) -
-                                 dsl::row_reduce_sum(dsl::leaf(output_cache_) * dsl::leaf(grad_output))),
+        return dsl::compute(engine, layer_exprs::softmax_rows_backward(output_cache_, grad_output),
                             output_cache_.rows(), output_cache_.cols());
     }
 

@@ -485,3 +485,18 @@ def test_doc_invariance(cpu):
         return g.logits()
     assert np.abs(logits(toks, True)[:, 4:] - logits(toks2, True)[:, 4:]).max() <= 1e-4
     assert np.abs(logits(toks, False)[:, 4:] - logits(toks2, False)[:, 4:]).max() > 1e-2
+
+
+@pytest.mark.parametrize("name", sorted(__import__("layer_programs").PROGRAMS))
+def test_layer_programs_closed_form(cpu, name):
+    """Every ExprSpec program of the GPT layers, as the DSL folds it, against its closed form."""
+    import layer_programs as lp
+    from test_gpu_layer_programs import make_args
+    build, vec, closed = lp.PROGRAMS[name]
+    spec, slots = build()
+    F, N = 24, 36
+    args = make_args(np.random.default_rng(11), slots, F, N)
+    ts = {k: cpu.tensor(v) for k, v in args.items()}
+    ins = [ts[n] for n in slots]
+    got = (cpu.eval_expr_reduce if vec else cpu.eval_expr)(spec, ins, F, N).numpy()
+    assert nrm_err(got, closed({k: v.astype(np.float64) for k, v in args.items()})) <= 1e-6
