@@ -90,29 +90,33 @@ int nnhip_scatter_add(float* dst, const float* indices, const float* grad, size_
 /* ── fused attention primitives (no CUDA counterpart) ────────────────────
  * Shapes as ComputeEngine (compute_engine.hpp:217-276): per batch A_b is (M,K), or stored (K,M) when
  * transA; B_b is (K,N), or stored (N,K) when transB; mask (M,N) shared by all batches (-inf excludes,
- * finite values add) or NULL. */
+ * finite values add) or NULL. Head dims K <= 128 run on the matrix cores. With a mask, a workspace of
+ * nnhip_bmm_workspace_bytes(M, N) bytes lets the kernels skip fully masked 32x32 cells (causal and
+ * document masks); workspace NULL computes every cell. */
+size_t nnhip_bmm_workspace_bytes(size_t M, size_t N);
 /* cpu_engine.hpp:426-532: out[b*M+i] = reduce_j(alpha*dot + mask) (reduce_cols), or out[b*N+j] over i. */
 int nnhip_bmm_reduce(const float* A, const float* B, const float* mask, float* out, size_t batch, size_t M,
                      size_t N, size_t K, int transA, int transB, unsigned op, float alpha, int reduce_cols,
-                     void* stream);
+                     void* workspace, void* stream);
 /* cpu_engine.hpp:535-604: l[b*M+i] = sum_j exp(alpha*dot + mask - row_max[b*M+i]). */
 int nnhip_bmm_softmax_denom(const float* A, const float* B, const float* row_max, const float* mask, float* out,
                             size_t batch, size_t M, size_t N, size_t K, int transA, int transB, float alpha,
-                            void* stream);
+                            void* workspace, void* stream);
 /* cpu_engine.hpp:607-699: O[(b*M+i)*D+k] = sum_j W_ij V[(b*N+j)*D+k]. */
 int nnhip_bmm_softmax_apply(const float* A, const float* B, const float* V, const float* row_max,
                             const float* denom, const float* mask, float* out, size_t batch, size_t M, size_t N,
-                            size_t K, size_t D, int transA, int transB, float alpha, void* stream);
+                            size_t K, size_t D, int transA, int transB, float alpha, void* workspace, void* stream);
 /* cpu_engine.hpp:702-801: R[b*M+i] = sum_j W P; dQ[(b*K+k)*M+i] = alpha sum_j W (P-R) B_b[k][j]. */
 int nnhip_bmm_softmax_backward_q(const float* A, const float* B, const float* P, const float* row_max,
                                  const float* denom, const float* mask, float* dQ, float* R, size_t batch,
-                                 size_t M, size_t N, size_t K, int transA, int transB, float alpha, void* stream);
+                                 size_t M, size_t N, size_t K, int transA, int transB, float alpha, void* workspace,
+                                 void* stream);
 /* cpu_engine.hpp:804-915: dK[(b*K+k)*N+j] = alpha sum_i W (P-R) A_b[:,i]_k; dV = sum_i W G[b*M+i][k]
  * (G has D >= K columns). */
 int nnhip_bmm_softmax_backward_kv(const float* A, const float* B, const float* P, const float* G, const float* R,
                                   const float* row_max, const float* denom, const float* mask, float* dK,
                                   float* dV, size_t batch, size_t M, size_t N, size_t K, size_t D, int transA,
-                                  int transB, float alpha, void* stream);
+                                  int transB, float alpha, void* workspace, void* stream);
 
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */
