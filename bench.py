@@ -8,9 +8,15 @@ and resident in device memory before timing starts.
 
 Prints one JSON line. `roofline` covers the dominant kernel family (the fp32
 MFMA GEMMs: every matmul / batched_matmul launch of the timed steps, timed with
-HIP events on the engine's stream). `cpu_baseline` runs the CPU restatement
-of the reference CpuEngine (oracle/, loaded only for this leg) on a bounded
-sample of the same workload: one full training step at batch 1 of 8.
+HIP events on the engine's stream). `attention` reports the metric's second
+part: the fused causal-attention primitives on BASELINE config 2 (forward:
+bmm_reduce Max -> softmax_denom -> softmax_apply) and config 5 (document-masked
+forward + backward over the 8 packed rows), as algorithmic TFLOP/s (4*d*P
+forward, 8*d*P backward over the P allowed (query, key) pairs) and as a
+fraction of the fp32 MFMA peak, timed with HIP events on the engine's stream.
+`cpu_baseline` runs the CPU restatement of the reference CpuEngine (oracle/,
+loaded only for this leg) on a bounded sample of the same workload: one full
+training step at batch 1 of 8.
 """
 import argparse
 import ctypes
@@ -100,6 +106,104 @@ def gpu_leg(steps, warmup, seed):
                 losses=losses)
 
 
+class StreamTimer:
+    """HIP events recorded on the engine's stream (the HIP runtime libnnhip.so links)."""
+
+    def __init__(self, lib, eng):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        lib.nnhip_engine_stream.restype = ctypes.c_void_p
+        lib.nnhip_engine_stream.argtypes = [ctypes.c_void_p]
+        self.stream = ctypes.c_void_p(lib.nnhip_engine_stream(eng._e))
+        self.ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+        for e in self.ev:
+            self._ok(self.hip.hipEventCreate(ctypes.byref(e)))
+
+    def _ok(self, rc):
+        if rc != 0:
+            raise RuntimeError(f"HIP error {rc}")
+
+    def start(self):
+        self._ok(self.hip.hipEventRecord(self.ev[0], self.stream))
+
+    def stop_ms(self):
+        self._ok(self.hip.hipEventRecord(self.ev[1], self.stream))
+        self._ok(self.hip.hipEventSynchronize(self.ev[1]))
+        ms = ctypes.c_float()
+        self._ok(self.hip.hipEventElapsedTime(ctypes.byref(ms), self.ev[0], self.ev[1]))
+        return ms.value
+
+
+def attention_leg(seed, reps=5):
+    """BASELINE configs 2 and 5 through the engine's fused attention primitives."""
+    import nnengine
+    lib = nnengine.hip_library()
+    eng = nnengine.Engine(lib)
+    timer = StreamTimer(lib, eng)
+    rng = np.random.default_rng(seed)
+    out = {}
+
+    # config 2: B 16 x H 8 = 128 heads, T 512, d 64, causal, alpha 1/8.
+    BH, T, d = 128, 512, 64
+    q, k = (eng.tensor(rng.standard_normal((BH * d, T), dtype=np.float32)) for _ in range(2))
+    vt = eng.tensor(rng.standard_normal((BH * T, d), dtype=np.float32))
+    mask = eng.tensor(eng.build_attention_mask(1, T, 1, False))
+
+    def fwd():
+        m = eng.batched_matmul_reduce(q, k, BH, "Max", True, False, 0.125, True, mask)
+        l = eng.batched_matmul_softmax_denom(q, k, m, BH, True, False, 0.125, mask)
+        return eng.batched_matmul_softmax_apply(q, k, vt, m, l, BH, True, False, 0.125, mask)
+    fwd()
+    timer.start()
+    for _ in range(reps):
+        fwd()
+    ms = timer.stop_ms() / reps
+    flop = 4 * d * (T * (T + 1) // 2) * BH
+    out["causal_config2_forward"] = {
+        "tflops": flop / (ms * 1e-3) / 1e12, "frac_of_fp32_mfma_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+        "ms": ms, "flop": flop, "dense_equivalent_tflops": 4 * d * T * T * BH / (ms * 1e-3) / 1e12,
+        "workload": "B16 x H8, T512, d64, causal mask, alpha 1/8: bmm_reduce(Max) + softmax_denom + softmax_apply"}
+    del q, k, vt, mask
+
+    # config 5: B 8, H 12, T 2048, d 64; documents U{64..1024} per row, blocked across boundaries.
+    B, H, T = 8, 12, 2048
+    rows = []
+    pairs = 0
+    for _ in range(B):
+        lens, tot = [], 0
+        while tot < T:
+            L = min(int(rng.integers(64, 1025)), T - tot)
+            lens.append(L)
+            tot += L
+        ids = np.concatenate([np.full(L, i + 1, dtype=np.uint64) for i, L in enumerate(lens)])
+        pairs += sum(L * (L + 1) // 2 for L in lens)
+        mk = eng.tensor(eng.build_attention_mask(1, T, 1, False, doc_ids=ids))
+        rows.append([eng.tensor(rng.standard_normal((H * d, T), dtype=np.float32)) for _ in range(4)] + [mk])
+
+    def fwd_bwd():
+        for q, k, v, g, mk in rows:
+            m = eng.batched_matmul_reduce(q, k, H, "Max", True, False, 0.125, True, mk)
+            l = eng.batched_matmul_softmax_denom(q, k, m, H, True, False, 0.125, mk)
+            vt = eng.rearrange_3d(eng.transpose(v), T, H, d)
+            eng.batched_matmul_softmax_apply(q, k, vt, m, l, H, True, False, 0.125, mk)
+            P = eng.batched_matmul(g, v, H, True, False)
+            G = eng.rearrange_3d(eng.transpose(g), T, H, d)
+            dq, r = eng.batched_matmul_softmax_backward_q(q, k, P, m, l, H, True, False, 0.125, mk)
+            eng.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, l, H, True, False, 0.125, mk)
+    fwd_bwd()
+    timer.start()
+    for _ in range(reps):
+        fwd_bwd()
+    ms = timer.stop_ms() / reps
+    flop = 12 * d * pairs * H
+    out["doc_masked_config5_forward_backward"] = {
+        "tflops": flop / (ms * 1e-3) / 1e12, "frac_of_fp32_mfma_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+        "ms": ms, "flop": flop, "allowed_pair_fraction": pairs / (B * T * T),
+        "workload": "B8 x H12, T2048, d64, doc lengths U{64..1024}: forward (reduce, denom, apply) + dP GEMM + "
+                    "backward_q + backward_kv, all 8 rows"}
+    eng.sync()
+    return out
+
+
 def cpu_leg(seed):
     import nnengine
     threads = int(os.environ.get("NNORACLE_THREADS", "0")) or min(os.cpu_count() or 1, 16)
@@ -125,6 +229,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--skip-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-attention", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
@@ -132,6 +237,7 @@ def main():
         sys.exit(2)
 
     gpu = gpu_leg(args.steps, args.warmup, args.seed)
+    attn = None if args.skip_attention else attention_leg(args.seed)
     n_tok = BATCH * CFG["seq_len"]
     ms_per_step = 1000.0 * gpu["elapsed"] / args.steps
     flops = step_flops(CFG, BATCH)
@@ -163,6 +269,8 @@ def main():
                      "flop_per_launch": gemm_flops_per_launch,
                      "share_of_step": gpu["gemm_ms"] / (gpu["elapsed"] * 1000.0)},
     }
+    if attn is not None:
+        out["attention"] = attn
     if not args.skip_cpu_baseline:
         cpu = cpu_leg(args.seed)
         out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}

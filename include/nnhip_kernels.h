@@ -90,10 +90,12 @@ int nnhip_scatter_add(float* dst, const float* indices, const float* grad, size_
 /* ── fused attention primitives (no CUDA counterpart) ────────────────────
  * Shapes as ComputeEngine (compute_engine.hpp:217-276): per batch A_b is (M,K), or stored (K,M) when
  * transA; B_b is (K,N), or stored (N,K) when transB; mask (M,N) shared by all batches (-inf excludes,
- * finite values add) or NULL. Head dims K <= 128 run on the matrix cores. With a mask, a workspace of
- * nnhip_bmm_workspace_bytes(M, N) bytes lets the kernels skip fully masked 32x32 cells (causal and
- * document masks); workspace NULL computes every cell. */
-size_t nnhip_bmm_workspace_bytes(size_t M, size_t N);
+ * finite values add) or NULL. With a workspace of nnhip_bmm_workspace_bytes(batch, M, N, K, D) bytes
+ * (D: value width of softmax_apply, else 1) and head dims K <= 128, the matrix-core kernels run: they
+ * skip fully masked 32x32 cells (causal and document masks) and split long rows over several
+ * workgroups whose partial results are combined in a fixed order (deterministic). With workspace
+ * NULL a general, slower path runs. */
+size_t nnhip_bmm_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D);
 /* cpu_engine.hpp:426-532: out[b*M+i] = reduce_j(alpha*dot + mask) (reduce_cols), or out[b*N+j] over i. */
 int nnhip_bmm_reduce(const float* A, const float* B, const float* mask, float* out, size_t batch, size_t M,
                      size_t N, size_t K, int transA, int transB, unsigned op, float alpha, int reduce_cols,

@@ -535,11 +535,12 @@ Result<Tensor> HipEngine::batched_matmul(const Tensor& A, const Tensor& B, std::
 }
 
 // ── fused attention (cpu_engine.hpp:426-915) ────────────────────────────────
-// Mask-cell table for the attention kernels (null without a mask).
-Result<std::shared_ptr<DeviceBuffer>> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, std::size_t N)
+// Workspace of the attention kernels: mask-cell table, combine counters, partial results.
+Result<std::shared_ptr<DeviceBuffer>> HipEngine::attn_ws_(std::size_t batch, std::size_t M, std::size_t N,
+                                                          std::size_t K, std::size_t D)
 {
-    if (!mask || M == 0 || N == 0) return std::shared_ptr<DeviceBuffer>();
-    return scratch_(nnhip_bmm_workspace_bytes(M, N));
+    if (batch == 0 || M == 0 || N == 0) return std::shared_ptr<DeviceBuffer>();
+    return scratch_(nnhip_bmm_workspace_bytes(batch, M, N, K, D));
 }
 
 Result<Tensor> HipEngine::batched_matmul_reduce(const Tensor& A, const Tensor& B, std::size_t batch, ReduceOp op,
@@ -549,7 +550,7 @@ Result<Tensor> HipEngine::batched_matmul_reduce(const Tensor& A, const Tensor& B
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_reduce"));
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_reduce"));
     NN_TRY(out, alloc_(reduce_cols ? batch * d.M : batch, reduce_cols ? 1 : d.N));
-    NN_TRY(ws, mask_cells_(mask, d.M, d.N));
+    NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, 1));
     NN_CHECK(kernel_(nnhip_bmm_reduce(D(A), D(B), mask ? D(*mask) : nullptr, W(out), batch, d.M, d.N, d.K, tA, tB,
                                       static_cast<unsigned>(op), alpha, reduce_cols, ws ? ws->data() : nullptr,
                                       stream_),
@@ -566,7 +567,7 @@ Result<Tensor> HipEngine::batched_matmul_softmax_denom(const Tensor& A, const Te
     NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_denom", "row_max"));
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_denom"));
     NN_TRY(out, alloc_(batch * d.M, 1));
-    NN_TRY(ws, mask_cells_(mask, d.M, d.N));
+    NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, 1));
     NN_CHECK(kernel_(nnhip_bmm_softmax_denom(D(A), D(B), D(row_max), mask ? D(*mask) : nullptr, W(out), batch, d.M,
                                              d.N, d.K, tA, tB, alpha, ws ? ws->data() : nullptr, stream_),
                      "batched_matmul_softmax_denom"));
@@ -585,7 +586,7 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
     NN_CHECK(vec_ok(denom, batch * d.M, "batched_matmul_softmax_apply", "denom"));
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_apply"));
     NN_TRY(out, alloc_(batch * d.M, V.cols()));
-    NN_TRY(ws, mask_cells_(mask, d.M, d.N));
+    NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, V.cols()));
     NN_CHECK(kernel_(nnhip_bmm_softmax_apply(D(A), D(B), D(V), D(row_max), D(denom), mask ? D(*mask) : nullptr,
                                              W(out), batch, d.M, d.N, d.K, V.cols(), tA, tB, alpha,
                                              ws ? ws->data() : nullptr, stream_),
@@ -606,7 +607,7 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_q(const Tensor& A, con
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_backward_q"));
     NN_TRY(dq, alloc_(batch * d.K, d.M));
     NN_TRY(r, alloc_(batch * d.M, 1));
-    NN_TRY(ws, mask_cells_(mask, d.M, d.N));
+    NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, 1));
     NN_CHECK(kernel_(nnhip_bmm_softmax_backward_q(D(A), D(B), D(P), D(row_max), D(denom), mask ? D(*mask) : nullptr,
                                                   W(dq), W(r), batch, d.M, d.N, d.K, tA, tB, alpha,
                                                   ws ? ws->data() : nullptr, stream_),
@@ -632,7 +633,7 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
     if (G.cols() < d.K) return fail("batched_matmul_softmax_backward_kv: G cols < K");
     NN_TRY(dk, alloc_(batch * d.K, d.N));
     NN_TRY(dv, alloc_(batch * d.K, d.N));
-    NN_TRY(ws, mask_cells_(mask, d.M, d.N));
+    NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, 1));
     NN_CHECK(kernel_(nnhip_bmm_softmax_backward_kv(D(A), D(B), D(P), D(G), D(R), D(row_max), D(denom),
                                                    mask ? D(*mask) : nullptr, W(dk), W(dv), batch, d.M, d.N, d.K,
                                                    G.cols(), tA, tB, alpha, ws ? ws->data() : nullptr, stream_),

@@ -6,10 +6,10 @@
 //   W_ij  = exp(s_ij - row_max_i) / denom_i                     (0 where mask = -inf)
 // with A_b(i,k) = A[b*M*K + (transA ? k*M + i : i*K + k)] and
 // B_b(k,j) = B[b*K*N + (transB ? j*K + k : k*N + j)].
-// The matrix-core kernels (k_attn_mfma.hip) take every case with head dim
-// K <= 128 (value width <= 128) except bmm_reduce with Sum/Min or over
-// columns; this file holds those entry points and the general fallback, in
-// which one workgroup owns one output row (query i, or key j for backward_kv); its
+// The matrix-core kernels (k_attn_mfma.hip) take every call with a workspace
+// and head dim K <= 128 (value width <= 128), except bmm_reduce with Sum/Min
+// or over columns; this file holds the entry points and the general fallback,
+// in which one workgroup owns one output row (query i, or key j for backward_kv); its
 // fixed operand vector is staged in LDS and the lanes sweep the other index.
 // Every sum over j (or i) that produces an output element runs in the CPU's
 // order inside one lane; only the row-level reductions (max / denominators
@@ -307,15 +307,17 @@ size_t lds_bytes(size_t K, bool chunk) { return (K + (chunk ? kChunk : 0)) * siz
 
 using namespace nnhip;
 
-extern "C" size_t nnhip_bmm_workspace_bytes(size_t M, size_t N) { return attn_workspace_bytes(M, N); }
+extern "C" size_t nnhip_bmm_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D)
+{
+    return attn_workspace_bytes(batch, M, N, K, D);
+}
 
 namespace
 {
 AttnArgs attn_args(const float* A, const float* B, const float* mask, size_t M, size_t N, size_t K, int tA, int tB,
                    float alpha)
 {
-    return AttnArgs{A, B, mask, nullptr, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), tA, tB, alpha,
-                    0};
+    return AttnArgs{A, B, mask, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), tA, tB, alpha};
 }
 } // namespace
 
@@ -326,12 +328,9 @@ extern "C" int nnhip_bmm_reduce(const float* A, const float* B, const float* mas
     if (op > R_MIN) return -1;
     if (batch == 0 || (reduce_cols ? M : N) == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
-    if (op == R_MAX && reduce_cols && attn_mfma_supported(batch, M, N, K))
-    {
-        AttnArgs a = attn_args(A, B, mask, M, N, K, transA, transB, alpha);
-        if (int rc = attn_prepare(a, workspace, s)) return rc;
-        return attn_mfma_forward(a, batch, kFwdMax, nullptr, nullptr, nullptr, 0, out, s);
-    }
+    if (op == R_MAX && reduce_cols && workspace && attn_mfma_supported(batch, M, N, K))
+        return attn_mfma_forward(attn_args(A, B, mask, M, N, K, transA, transB, alpha), batch, kFwdMax, nullptr,
+                                 nullptr, nullptr, 0, out, workspace, s);
     if (int rc = check_dims(batch, M, N, K)) return rc;
     Dims d{A, B, mask, M, N, K, transA, transB, alpha};
     if (reduce_cols)
@@ -349,12 +348,9 @@ extern "C" int nnhip_bmm_softmax_denom(const float* A, const float* B, const flo
 {
     if (batch == 0 || M == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
-    if (attn_mfma_supported(batch, M, N, K))
-    {
-        AttnArgs a = attn_args(A, B, mask, M, N, K, transA, transB, alpha);
-        if (int rc = attn_prepare(a, workspace, s)) return rc;
-        return attn_mfma_forward(a, batch, kFwdDenom, row_max, nullptr, nullptr, 0, out, s);
-    }
+    if (workspace && attn_mfma_supported(batch, M, N, K))
+        return attn_mfma_forward(attn_args(A, B, mask, M, N, K, transA, transB, alpha), batch, kFwdDenom, row_max,
+                                 nullptr, nullptr, 0, out, workspace, s);
     if (int rc = check_dims(batch, M, N, K)) return rc;
     Dims d{A, B, mask, M, N, K, transA, transB, alpha};
     hipLaunchKernelGGL(k_bmm_denom, dim3(static_cast<unsigned>(M), static_cast<unsigned>(batch)), dim3(kThreads),
@@ -369,12 +365,9 @@ extern "C" int nnhip_bmm_softmax_apply(const float* A, const float* B, const flo
 {
     if (batch == 0 || M == 0 || D == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
-    if (D <= 128 && attn_mfma_supported(batch, M, N, K))
-    {
-        AttnArgs a = attn_args(A, B, mask, M, N, K, transA, transB, alpha);
-        if (int rc = attn_prepare(a, workspace, s)) return rc;
-        return attn_mfma_forward(a, batch, kFwdApply, row_max, denom, V, D, out, s);
-    }
+    if (D <= 128 && workspace && attn_mfma_supported(batch, M, N, K))
+        return attn_mfma_forward(attn_args(A, B, mask, M, N, K, transA, transB, alpha), batch, kFwdApply, row_max,
+                                 denom, V, D, out, workspace, s);
     if (int rc = check_dims(batch, M, N, K)) return rc;
     if (D > 1024) return -3;
     Dims d{A, B, mask, M, N, K, transA, transB, alpha};
@@ -390,12 +383,9 @@ extern "C" int nnhip_bmm_softmax_backward_q(const float* A, const float* B, cons
 {
     if (batch == 0 || M == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
-    if (attn_mfma_supported(batch, M, N, K))
-    {
-        AttnArgs a = attn_args(A, B, mask, M, N, K, transA, transB, alpha);
-        if (int rc = attn_prepare(a, workspace, s)) return rc;
-        return attn_mfma_backward(a, batch, false, P, nullptr, 0, nullptr, row_max, denom, dQ, R, s);
-    }
+    if (workspace && attn_mfma_supported(batch, M, N, K))
+        return attn_mfma_backward(attn_args(A, B, mask, M, N, K, transA, transB, alpha), batch, false, P, nullptr, 0,
+                                  nullptr, row_max, denom, dQ, R, workspace, s);
     if (int rc = check_dims(batch, M, N, K)) return rc;
     Dims d{A, B, mask, M, N, K, transA, transB, alpha};
     hipLaunchKernelGGL(k_bmm_bwd_q, dim3(static_cast<unsigned>(M), static_cast<unsigned>(batch)), dim3(kThreads),
@@ -412,12 +402,9 @@ extern "C" int nnhip_bmm_softmax_backward_kv(const float* A, const float* B, con
     if (D < K) return -2;
     if (batch == 0 || N == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
-    if (attn_mfma_supported(batch, M, N, K))
-    {
-        AttnArgs a = attn_args(A, B, mask, M, N, K, transA, transB, alpha);
-        if (int rc = attn_prepare(a, workspace, s)) return rc;
-        return attn_mfma_backward(a, batch, true, P, G, D, R, row_max, denom, dK, dV, s);
-    }
+    if (workspace && attn_mfma_supported(batch, M, N, K))
+        return attn_mfma_backward(attn_args(A, B, mask, M, N, K, transA, transB, alpha), batch, true, P, G, D, R,
+                                  row_max, denom, dK, dV, workspace, s);
     if (int rc = check_dims(batch, M, N, K)) return rc;
     Dims d{A, B, mask, M, N, K, transA, transB, alpha};
     hipLaunchKernelGGL(k_bmm_bwd_kv, dim3(static_cast<unsigned>(N), static_cast<unsigned>(batch)), dim3(kThreads),

@@ -1,18 +1,31 @@
 // k_attn_mfma.hip — the fused attention primitives on the fp32 matrix cores.
 //
 // Same semantics as the general path in k_attention.hip (CPU engine,
-// cpu_engine.hpp:426-915), for head dims K <= 128 (and value width D <= 128):
+// cpu_engine.hpp:426-915), for head dims K <= 128 and value widths D <= 128:
 //   s_ij = alpha * dot_k(Q(i,k), Kt(k,j)) + mask(i,j),  W_ij = exp(s_ij - m_i) / l_i  (0 where s_ij = -inf)
 // with Q(i,k) = A_b(i,k) and Kt(k,j) = B_b(k,j) in the transpose conventions of
 // ComputeEngine (compute_engine.hpp:217-276).
 //
-// Every score tile is one v_mfma_f32_32x32x2_f32 chain over k. The forward and
-// backward_q kernels compute it transposed, S^T = Kt^T Q (rows = keys,
-// columns = queries): each lane then owns one query (column l%32), so row
-// statistics need no cross-lane work until the very end, and the score
-// registers are already laid out as the B operand of the next MFMA
-// (O^T = V^T W^T, dQ^T = Kt dS^T). backward_kv computes S = Q Kt (rows =
-// queries) so that W and dS feed dK = Q^T dS and dV = G^T W the same way.
+// Work decomposition. The (M, N) score plane of each batch is cut into 32x32
+// cells. A work item is one wave (64 lanes, no block barriers) that owns a
+// 32-wide line of cells (32 queries; 32 keys for backward_kv) and a range of
+// kCells consecutive cells along it. Items cost at most kCells cells however
+// the mask distributes the allowed pairs, and there are thousands of them, so
+// causal and document masks balance over the 1024 SIMDs by themselves. A line
+// with a single non-empty range writes its output directly; otherwise each
+// item writes a partial result (maxima, sums, output rows) to the workspace and
+// a combine kernel adds a line's partials in range order, so results do not
+// depend on scheduling. (Combining inside the item kernel would need
+// device-scope release/acquire between workgroups, i.e. a write-back of the
+// whole L2 per item on this GPU: far slower than a second launch.)
+//
+// Per cell: one v_mfma_f32_32x32x2_f32 chain over k computes the score tile
+// (transposed, S^T = Kt^T Q, in the query-line kernels: each lane then owns one
+// query, and the score registers are already laid out as the B operand of the
+// next MFMA, O^T = V^T W^T or dQ^T = Kt dS^T). Operands come straight from
+// global memory (L2) into registers; the next cell's score operand is loaded
+// while the current cell computes. The two operands that need a transpose (Kt
+// for dQ, Q for dK) go through a wave-private LDS tile.
 //
 // MFMA 32x32x2 operand layout (lane l, h = l/32, c = l%32), step r of 2 k's:
 //   A[row c][k h], B[k h][col c];  D register r <-> row drow(r,h), col c,
@@ -21,9 +34,8 @@
 // drow(r,0) and drow(r,1): over r = 0..15 each of the 32 is used once, and the
 // A operand is read with the same index map.
 //
-// Masks: a pre-pass classifies every 32x32 (query, key) cell of the shared
-// (M,N) mask as all -inf (skipped), all zero (no mask read) or general, so a
-// causal or document mask costs only the cells that hold allowed pairs.
+// Masks: a pre-pass classifies every cell of the shared (M,N) mask as all
+// -inf (skipped), all zero (no mask read) or general.
 #include "attn_mfma.hpp"
 #include "common.hpp"
 
@@ -35,9 +47,12 @@ namespace
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kNegInf = -__builtin_huge_valf();
-constexpr int JT = 64;   // keys per step (forward, backward_q)
-constexpr int IT = 64;   // queries per step (backward_kv)
-constexpr int LP = 1;    // LDS row padding: rows of 65 floats are bank-conflict free both ways
+constexpr int kCells = 8;         // cells per work item along its line (a range)
+constexpr int kStep = 2;          // cells staged per pipeline step
+constexpr int kSteps = kCells / kStep;
+constexpr int kMaxTiles = 1024;   // 32-wide tiles per axis: M, N <= 32768
+
+enum { kRowMax = 0, kRowDenom = 1, kRowApply = 2, kRowR = 3, kRowDQ = 4 };
 
 __device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c)
 {
@@ -60,15 +75,18 @@ __device__ __forceinline__ float kt_at(const AttnArgs& d, const float* Bb, int k
 {
     return d.tB ? Bb[(long)j * d.K + k] : Bb[(long)k * d.N + j];
 }
-// Class of the 32x32 cell (query block ib, key block jb): 0 skip, 1 no mask add, 2 general.
-__device__ __forceinline__ int cell(const AttnArgs& d, int ib, int jb)
-{
-    if (!d.mask) return 1;
-    if (!d.cls) return 2;
-    return d.cls[(long)ib * d.n_j32 + jb];
-}
 
-__global__ __launch_bounds__(256) void k_mask_classify(const float* __restrict__ mask, int M, int N, int n_j32,
+// Geometry and workspace of one call (identical for every item).
+struct Work
+{
+    int RT, CT;                  // query tiles, key tiles
+    int NR;                      // ranges per line: ceil(tiles along the line / kCells)
+    const unsigned char* cls;    // RT x CT cell classes (unused without a mask: every cell is class 1)
+    float* part;                 // partial results, pw floats per item
+    int pw;
+};
+
+__global__ __launch_bounds__(256) void k_attn_classify(const float* __restrict__ mask, int M, int N, int CT,
                                                        unsigned char* __restrict__ cls)
 {
     const int jb = blockIdx.x, ib = blockIdx.y;
@@ -85,122 +103,293 @@ __global__ __launch_bounds__(256) void k_mask_classify(const float* __restrict__
     }
     finite = __syncthreads_or(finite);
     nonzero = __syncthreads_or(nonzero);
-    if (threadIdx.x == 0) cls[(long)ib * n_j32 + jb] = !finite ? 0 : (nonzero ? 2 : 1);
+    if (threadIdx.x == 0) cls[(long)ib * CT + jb] = !finite ? 0 : (nonzero ? 2 : 1);
 }
 
-// Stages Ks[k][jj] = Kt(k, j0 + jj) for k < KP, jj < JT (zero outside K x N).
-template <int KP, int NT>
-__device__ __forceinline__ void stage_keys(const AttnArgs& d, const float* Bb, int j0, float (*Ks)[JT + LP])
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2.
+// Maps the 1-D workgroup id to a work item so that each XCD runs one
+// contiguous run of items: the items of one batch entry (which re-read its
+// query and key tiles) then share an L2.
+__device__ __forceinline__ int xcd_item(int bid, int nb)
 {
-    for (int e = threadIdx.x; e < KP * JT; e += NT)
+    const int x = bid % 8, k = bid / 8, q = nb / 8, r = nb % 8;
+    return x * q + min(x, r) + k;
+}
+
+__device__ __forceinline__ int cell_class(const AttnArgs& d, const Work& w, int ib, int jb)
+{
+    return !d.mask ? 1 : w.cls[(long)ib * w.CT + jb];
+}
+
+// What an item knows about its line: its own non-empty / general cells (bit t
+// = cell rg*kCells + t) and which ranges of the line are non-empty.
+struct LineInfo
+{
+    unsigned mine_nz = 0, mine_gen = 0;
+    int nne = 0;
+    unsigned long long ranges[kMaxTiles / kCells / 64] = {};
+};
+
+// rows: the line is query tile `line`, cells run along keys; else key tile, cells along queries.
+__device__ LineInfo line_info(const AttnArgs& d, const Work& w, bool rows, int line, int rg)
+{
+    static_assert(kCells == 8, "range packing below assumes 8 cells (one byte) per range");
+    LineInfo li;
+    const int nx = rows ? w.CT : w.RT;
+    const int lane = threadIdx.x & 63;
+    for (int x0 = 0; x0 < nx; x0 += 64)
     {
-        int k, jj;
-        if (d.tB) { jj = e / KP; k = e % KP; }   // consecutive threads walk consecutive addresses
-        else { k = e / JT; jj = e % JT; }
-        const int j = j0 + jj;
-        Ks[k][jj] = (k < d.K && j < d.N) ? kt_at(d, Bb, k, j) : 0.0f;
-    }
-}
-
-// Does any wave of the block need key step [j0, j0+64) for query rows starting at qb0?
-template <int WQ>
-__device__ __forceinline__ bool block_needs_keys(const AttnArgs& d, int qb0, int j0)
-{
-    for (int w = 0; w < WQ; ++w)
-        for (int t = 0; t < 2; ++t)
+        const int x = x0 + lane;
+        const int cl = x < nx ? (rows ? cell_class(d, w, line, x) : cell_class(d, w, x, line)) : 0;
+        const unsigned long long nz = __ballot(cl != 0);
+        const unsigned long long gen = __ballot(cl == 2);
+        unsigned long long packed = 0;   // bit q: range x0/kCells + q is non-empty
+#pragma unroll
+        for (int q = 0; q < 64 / kCells; ++q) packed |= (((nz >> (kCells * q)) & 0xFFull) != 0 ? 1ull : 0ull) << q;
+        li.nne += __popcll(packed);
+        const int rb = x0 / kCells;
+#pragma unroll
+        for (int q = 0; q < kMaxTiles / kCells / 64; ++q)   // constant indices keep the words in registers
+            if (rb / 64 == q) li.ranges[q] |= packed << (rb % 64);
+        const int xb = rg * kCells;
+        if (xb >= x0 && xb < x0 + 64)
         {
-            const int ib = qb0 / 32 + w, jb = j0 / 32 + t;
-            if (ib * 32 < d.M && jb * 32 < d.N && cell(d, ib, jb) != 0) return true;
+            li.mine_nz = static_cast<unsigned>((nz >> (xb - x0)) & 0xFF);
+            li.mine_gen = static_cast<unsigned>((gen >> (xb - x0)) & 0xFF);
         }
-    return false;
+    }
+    return li;
 }
 
-// Scores of one transposed 32x32 tile: sv[r] for key j0 + drow(r,h), query qi.
-__device__ __forceinline__ void scores_t(const AttnArgs& d, const f32x16& s, int qi, int jbase, int h, int cl,
-                                         float* sv)
+// f(range) for each non-empty range of the line, in range order.
+template <class F>
+__device__ __forceinline__ void for_ranges(const LineInfo& li, int nr, F f)
 {
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
+    for (int q = 0; q < kMaxTiles / kCells / 64; ++q)
     {
-        const int j = jbase + drow(r, h);
-        float x = d.alpha * s[r];
-        if (j >= d.N || qi >= d.M)
-            x = kNegInf;
-        else if (cl == 2)
-            x += d.mask[(long)qi * d.N + j];
-        sv[r] = x;
+        if (q * 64 >= nr) break;
+        unsigned long long m = li.ranges[q];
+        while (m)
+        {
+            const int t = __builtin_ctzll(m);
+            m &= m - 1;
+            f(q * 64 + t);
+        }
     }
 }
 
-// ── forward: row max (bmm_reduce Max, reduce_cols), denominators, apply ──────
-template <int KP, int WQ, int MODE>
-__global__ __launch_bounds__(64 * WQ) void k_attn_fwd(AttnArgs d, const float* __restrict__ row_max,
-                                                      const float* __restrict__ denom, const float* __restrict__ V,
-                                                      int D, float* __restrict__ out)
+// Writes a query line's output tiles from the registers' (k = 32u + drow(r,h), query qi) layout:
+// O[(b*M + qi)*D + k] (apply) or dQ[(b*K + k)*M + qi] = alpha * value.
+template <bool APPLY, int NU>
+__device__ __forceinline__ void store_row_tiles(const AttnArgs& d, float* out, int D, int b, int qi, int h,
+                                                const f32x16* acc)
 {
-    constexpr int NT = 64 * WQ;
-    constexpr bool APPLY = MODE == kFwdApply;
-    __shared__ float Ks[KP][JT + LP];
-    __shared__ float Vs[APPLY ? JT : 1][APPLY ? 128 + LP : 1];
+    if (qi >= d.M) return;
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            const int k = 32 * u + drow(r, h);
+            if constexpr (APPLY)
+            {
+                if (k < D) out[((long)b * d.M + qi) * D + k] = acc[u][r];
+            }
+            else if (k < d.K)
+                out[((long)b * d.K + k) * d.M + qi] = d.alpha * acc[u][r];
+        }
+}
+
+// ── query-line kernel: forward row max / denominators / apply, backward R / dQ ──
+// A workgroup is 4 waves = 4 consecutive query lines sharing one key range.
+// The range is walked kStep cells at a time through two LDS buffers: the key
+// (and value) tiles of the next step are loaded into registers while the
+// current step's MFMAs run, then written to the other buffer (one barrier per
+// step, as in the GEMM).
+constexpr int kWaves = 4;
+
+// Which steps of the range any wave of the workgroup has work in.
+__device__ __forceinline__ unsigned steps_needed(unsigned need)
+{
+    unsigned m = 0;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s)
+        if ((need >> (kStep * s)) & ((1u << kStep) - 1)) m |= 1u << s;
+    return m;
+}
+
+template <int KP, int MODE, int DU>
+__global__ __launch_bounds__(64 * kWaves) void k_attn_rows(AttnArgs d, Work w, const float* __restrict__ row_max,
+                                                           const float* __restrict__ denom,
+                                                           const float* __restrict__ V, int D,
+                                                           const float* __restrict__ P,
+                                                           const float* __restrict__ Rin, float* __restrict__ out)
+{
+    constexpr int NT = 64 * kWaves;
+    constexpr bool APPLY = MODE == kRowApply, DQ = MODE == kRowDQ, USE_P = MODE == kRowR || MODE == kRowDQ;
+    constexpr bool SCALAR = MODE == kRowMax || MODE == kRowDenom || MODE == kRowR;
+    constexpr int NU = APPLY ? DU : (DQ ? KP / 32 : 1);   // 32-wide output subtiles held by a wave
+    constexpr int VS = DU * 32 + 8;                       // value row stride: rows 4 apart use disjoint banks
+    constexpr int PK = KP * 32 / NT, PV = APPLY ? 32 * DU * 32 / NT : 1;   // per thread, per staged cell
+    static_assert(PK * NT == KP * 32 && (!APPLY || PV * NT == 32 * DU * 32), "staging covers each tile exactly");
+    __shared__ float Ks[2][kStep][KP][33];                // Ks[buf][t][k][jj] = Kt(k, jbase_t + jj)
+    __shared__ float Vs[APPLY ? 2 : 1][APPLY ? kStep : 1][APPLY ? 32 : 1][APPLY ? VS : 1];
+    __shared__ unsigned need_s;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
-    const int qblk = gridDim.x - 1 - blockIdx.x;   // last query blocks carry the most causal work: start them first
-    const int b = blockIdx.y;
-    const int qb0 = qblk * 32 * WQ, i0 = qb0 + wave * 32, qi = i0 + c;
+    const int per = (w.RT + kWaves - 1) / kWaves * w.NR;
+    const int item = xcd_item(blockIdx.x, gridDim.x), b = item / per, grp = item % per / w.NR, rg = item % w.NR;
+    const int row = grp * kWaves + wave, qi = row * 32 + c;
+    const LineInfo li = row < w.RT ? line_info(d, w, true, row, rg) : LineInfo{};
+    if (threadIdx.x == 0) need_s = 0;
+    __syncthreads();
+    if (lane == 0 && li.mine_nz) atomicOr(&need_s, li.mine_nz);
+    __syncthreads();
+    const unsigned steps = steps_needed(need_s);   // steps of the range any wave computes
+
+    // A line without any allowed pair still has outputs: lowest() maxima, zero sums and rows.
+    auto write_empty_line = [&]() {
+        if (li.nne != 0 || rg != 0 || row >= w.RT || qi >= d.M) return;
+        if constexpr (SCALAR)
+        {
+            if (h == 0) out[(long)b * d.M + qi] = MODE == kRowMax ? kLowest : 0.0f;
+        }
+        else
+        {
+            const int width = APPLY ? D : d.K;
+            for (int k = h; k < width; k += 2)
+                out[APPLY ? ((long)b * d.M + qi) * D + k : ((long)b * d.K + k) * d.M + qi] = 0.0f;
+        }
+    };
+    if (steps == 0)
+    {
+        write_empty_line();
+        return;
+    }
+
     const float* Ab = d.A + (long)b * d.M * d.K;
     const float* Bb = d.B + (long)b * d.K * d.N;
+    const float* Vb = APPLY ? V + (long)b * d.N * D : nullptr;
+    // Register staging of one step's tiles (clamped addresses; out-of-range values are zeroed when stored).
+    float kr[kStep][PK], vr[kStep][PV];
+    auto load_step = [&](int st) {
+#pragma unroll
+        for (int t = 0; t < kStep; ++t)
+        {
+            const int jbase = 32 * (rg * kCells + st * kStep + t);
+#pragma unroll
+            for (int u = 0; u < PK; ++u)
+            {
+                const int e = threadIdx.x + u * NT;
+                const int k = d.tB ? e % KP : e / 32, jj = d.tB ? e / KP : e % 32;
+                kr[t][u] = kt_at(d, Bb, min(k, d.K - 1), min(jbase + jj, d.N - 1));
+            }
+            if constexpr (APPLY)
+            {
+#pragma unroll
+                for (int u = 0; u < PV; ++u)
+                {
+                    const int e = threadIdx.x + u * NT, jj = e / (DU * 32), k = e % (DU * 32);
+                    vr[t][u] = Vb[(long)min(jbase + jj, d.N - 1) * D + min(k, D - 1)];
+                }
+            }
+        }
+    };
+    auto store_step = [&](int st, int buf) {
+#pragma unroll
+        for (int t = 0; t < kStep; ++t)
+        {
+            const int jbase = 32 * (rg * kCells + st * kStep + t);
+#pragma unroll
+            for (int u = 0; u < PK; ++u)
+            {
+                const int e = threadIdx.x + u * NT;
+                const int k = d.tB ? e % KP : e / 32, jj = d.tB ? e / KP : e % 32;
+                Ks[buf][t][k][jj] = (k < d.K && jbase + jj < d.N) ? kr[t][u] : 0.0f;
+            }
+            if constexpr (APPLY)
+            {
+#pragma unroll
+                for (int u = 0; u < PV; ++u)
+                {
+                    const int e = threadIdx.x + u * NT, jj = e / (DU * 32), k = e % (DU * 32);
+                    Vs[buf][t][jj][k] = (k < D && jbase + jj < d.N) ? vr[t][u] : 0.0f;
+                }
+            }
+        }
+    };
+    auto next_step = [&](int st) {
+        while (st < kSteps && !((steps >> st) & 1u)) ++st;
+        return st;
+    };
+    int st = next_step(0);
+    load_step(st);
 
-    float qf[KP / 2];   // B operand of S^T: Q(qi, 2kk + h)
+    // This wave's queries: B operand of S^T, Q(qi, 2kk + h).
+    const int qc = min(qi, d.M - 1);
+    float qf[KP / 2];
 #pragma unroll
     for (int kk = 0; kk < KP / 2; ++kk)
     {
         const int k = 2 * kk + h;
-        qf[kk] = (qi < d.M && k < d.K) ? q_at(d, Ab, qi, k) : 0.0f;
+        const float x = q_at(d, Ab, qc, min(k, d.K - 1));
+        qf[kk] = (qi < d.M && k < d.K) ? x : 0.0f;
     }
-    float m_i = 0.0f, inv_l = 0.0f;
-    if (MODE != kFwdMax && qi < d.M) m_i = row_max[(long)b * d.M + qi];
-    if (APPLY && qi < d.M) inv_l = 1.0f / denom[(long)b * d.M + qi];
-    float red = MODE == kFwdMax ? kLowest : 0.0f;
-    const int DU = (D + 31) / 32;
-    f32x16 acc_o[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc_o[u] = zero16();
+    float m_i = 0.0f, inv_l = 0.0f, r_i = 0.0f;
+    if constexpr (MODE != kRowMax) m_i = row_max[(long)b * d.M + qc];
+    if constexpr (MODE != kRowMax && MODE != kRowDenom) inv_l = 1.0f / denom[(long)b * d.M + qc];
+    if constexpr (DQ) r_i = Rin[(long)b * d.M + qc];
+    const float* prow = USE_P ? P + ((long)b * d.M + qc) * d.N : nullptr;
+    const float* mrow = d.mask ? d.mask + (long)qc * d.N : nullptr;
 
-    const int steps = (d.N + JT - 1) / JT;
-    for (int st = 0; st < steps; ++st)
+    float red = MODE == kRowMax ? kLowest : 0.0f;
+    f32x16 acc[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) acc[u] = zero16();
+
+    int buf = 0;
+    store_step(st, buf);
+    __syncthreads();
+    while (true)
     {
-        const int j0 = st * JT;
-        if (!block_needs_keys<WQ>(d, qb0, j0)) continue;
-        __syncthreads();
-        stage_keys<KP, NT>(d, Bb, j0, Ks);
-        if constexpr (APPLY)
+        const int nxt = next_step(st + 1);
+        if (nxt < kSteps) load_step(nxt);   // in flight during this step's MFMAs
+#pragma unroll
+        for (int t = 0; t < kStep; ++t)
         {
-            const int dw = DU * 32;
-            for (int e = threadIdx.x; e < JT * dw; e += NT)
+            const int cell = st * kStep + t;
+            if (!((li.mine_nz >> cell) & 1u)) continue;
+            const int jbase = 32 * (rg * kCells + cell);
+            // Side operands (consumed after the score chain).
+            float mv[16], pv[USE_P ? 16 : 1];
+            if ((li.mine_gen >> cell) & 1u)
             {
-                const int jj = e / dw, k = e % dw, j = j0 + jj;
-                Vs[jj][k] = (k < D && j < d.N) ? V[((long)b * d.N + j) * D + k] : 0.0f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mv[r] = mrow[min(jbase + drow(r, h), d.N - 1)];
             }
-        }
-        __syncthreads();
-        if (i0 >= d.M) continue;
+            else
+            {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-        {
-            const int jbase = j0 + 32 * t;
-            if (jbase >= d.N) continue;
-            const int cl = cell(d, i0 / 32, jbase / 32);
-            if (cl == 0) continue;
-            f32x16 s = zero16();
+                for (int r = 0; r < 16; ++r) mv[r] = 0.0f;
+            }
+            if constexpr (USE_P)
+            {
 #pragma unroll
-            for (int kk = 0; kk < KP / 2; ++kk) s = mfma(Ks[2 * kk + h][32 * t + c], qf[kk], s);
+                for (int r = 0; r < 16; ++r) pv[r] = prow[min(jbase + drow(r, h), d.N - 1)];
+            }
+            f32x16 sacc = zero16();
+#pragma unroll
+            for (int kk = 0; kk < KP / 2; ++kk) sacc = mfma(Ks[buf][t][2 * kk + h][c], qf[kk], sacc);
             float sv[16];
-            scores_t(d, s, qi, jbase, h, cl, sv);
-            if constexpr (MODE == kFwdMax)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                sv[r] = (jbase + drow(r, h) < d.N && qi < d.M) ? d.alpha * sacc[r] + mv[r] : kNegInf;
+            if constexpr (MODE == kRowMax)
             {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) red = fmax_std(red, sv[r]);
             }
-            else if constexpr (MODE == kFwdDenom)
+            else if constexpr (MODE == kRowDenom)
             {
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
@@ -208,365 +397,504 @@ __global__ __launch_bounds__(64 * WQ) void k_attn_fwd(AttnArgs d, const float* _
             }
             else
             {
-                float w[16];
+                float wv[16];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) w[r] = sv[r] == kNegInf ? 0.0f : expf(sv[r] - m_i) * inv_l;
+                for (int r = 0; r < 16; ++r) wv[r] = sv[r] == kNegInf ? 0.0f : expf(sv[r] - m_i) * inv_l;
+                if constexpr (MODE == kRowR)
+                {
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (u < DU)
-                    {
+                    for (int r = 0; r < 16; ++r)
+                        if (sv[r] != kNegInf) red += wv[r] * pv[r];
+                }
+                else if constexpr (APPLY)
+                {
+#pragma unroll
+                    for (int u = 0; u < DU; ++u)
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
-                            acc_o[u] = mfma(Vs[32 * t + drow(r, h)][32 * u + c], w[r], acc_o[u]);
-                    }
-            }
-        }
-    }
-    if constexpr (!APPLY)
-    {
-        const float o = __shfl_xor(red, 32, 64);
-        red = MODE == kFwdMax ? fmax_std(red, o) : red + o;
-        if (h == 0 && qi < d.M) out[(long)b * d.M + qi] = red;
-    }
-    else if (qi < d.M)
-    {
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (u < DU)
-            {
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                {
-                    const int k = 32 * u + drow(r, h);
-                    if (k < D) out[((long)b * d.M + qi) * D + k] = acc_o[u][r];
+                            acc[u] = mfma(Vs[buf][t][drow(r, h)][32 * u + c], wv[r], acc[u]);
                 }
-            }
-    }
-}
-
-// ── backward_q: pass 0 R_i = sum_j W P; pass 1 dQ^T[k][i] = alpha sum_j Kt(k,j) W (P - R_i) ──
-template <int KP, int WQ>
-__global__ __launch_bounds__(64 * WQ) void k_attn_bwd_q(AttnArgs d, const float* __restrict__ P,
-                                                        const float* __restrict__ row_max,
-                                                        const float* __restrict__ denom, float* __restrict__ dQ,
-                                                        float* __restrict__ R)
-{
-    constexpr int NT = 64 * WQ;
-    __shared__ float Ks[KP][JT + LP];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
-    const int qblk = gridDim.x - 1 - blockIdx.x;
-    const int b = blockIdx.y;
-    const int qb0 = qblk * 32 * WQ, i0 = qb0 + wave * 32, qi = i0 + c;
-    const float* Ab = d.A + (long)b * d.M * d.K;
-    const float* Bb = d.B + (long)b * d.K * d.N;
-    const float* prow = P + ((long)b * d.M + (qi < d.M ? qi : 0)) * d.N;
-
-    float qf[KP / 2];
-#pragma unroll
-    for (int kk = 0; kk < KP / 2; ++kk)
-    {
-        const int k = 2 * kk + h;
-        qf[kk] = (qi < d.M && k < d.K) ? q_at(d, Ab, qi, k) : 0.0f;
-    }
-    const float m_i = qi < d.M ? row_max[(long)b * d.M + qi] : 0.0f;
-    const float inv_l = qi < d.M ? 1.0f / denom[(long)b * d.M + qi] : 0.0f;
-    float r_i = 0.0f, rsum = 0.0f;
-    f32x16 acc[KP / 32];
-#pragma unroll
-    for (int u = 0; u < KP / 32; ++u) acc[u] = zero16();
-
-    const int steps = (d.N + JT - 1) / JT;
-    for (int pass = 0; pass < 2; ++pass)
-    {
-        for (int st = 0; st < steps; ++st)
-        {
-            const int j0 = st * JT;
-            if (!block_needs_keys<WQ>(d, qb0, j0)) continue;
-            __syncthreads();
-            stage_keys<KP, NT>(d, Bb, j0, Ks);
-            __syncthreads();
-            if (i0 >= d.M) continue;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-            {
-                const int jbase = j0 + 32 * t;
-                if (jbase >= d.N) continue;
-                const int cl = cell(d, i0 / 32, jbase / 32);
-                if (cl == 0) continue;
-                f32x16 s = zero16();
-#pragma unroll
-                for (int kk = 0; kk < KP / 2; ++kk) s = mfma(Ks[2 * kk + h][32 * t + c], qf[kk], s);
-                float sv[16];
-                scores_t(d, s, qi, jbase, h, cl, sv);
-                float w[16], p[16];
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                {
-                    const int j = jbase + drow(r, h);
-                    w[r] = sv[r] == kNegInf ? 0.0f : expf(sv[r] - m_i) * inv_l;
-                    p[r] = (qi < d.M && j < d.N) ? prow[j] : 0.0f;
-                }
-                if (pass == 0)
-                {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) rsum += w[r] * p[r];
-                }
-                else
+                else   // dQ: A operand Kt(32u + c, jbase + drow(r,h)) read transposed from the staged tile
                 {
 #pragma unroll
                     for (int u = 0; u < KP / 32; ++u)
-                    {
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
-                            acc[u] = mfma(Ks[32 * u + c][32 * t + drow(r, h)], w[r] * (p[r] - r_i), acc[u]);
-                    }
+                            acc[u] = mfma(Ks[buf][t][32 * u + c][drow(r, h)], wv[r] * (pv[r] - r_i), acc[u]);
                 }
             }
         }
-        if (pass == 0)
-        {
-            r_i = rsum + __shfl_xor(rsum, 32, 64);
-            if (h == 0 && qi < d.M) R[(long)b * d.M + qi] = r_i;
-        }
+        if (nxt >= kSteps) break;
+        store_step(nxt, buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+        st = nxt;
     }
-    if (qi < d.M)
+    if (li.mine_nz == 0)
     {
-#pragma unroll
-        for (int u = 0; u < KP / 32; ++u)
+        write_empty_line();
+        return;
+    }
+
+    // Output: direct when the line has one non-empty range, else a partial for k_attn_combine_rows.
+    const long line = (long)b * w.RT + row;
+    if constexpr (SCALAR)
+    {
+        const float o = __shfl_xor(red, 32, 64);
+        red = MODE == kRowMax ? fmax_std(red, o) : red + o;
+        if (li.nne > 1)
         {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-            {
-                const int k = 32 * u + drow(r, h);
-                if (k < d.K) dQ[((long)b * d.K + k) * d.M + qi] = d.alpha * acc[u][r];
-            }
+            if (h == 0) w.part[(line * w.NR + rg) * w.pw + c] = red;
         }
+        else if (h == 0 && qi < d.M)
+            out[(long)b * d.M + qi] = red;
+    }
+    else
+    {
+        if (li.nne > 1)
+        {
+            float* mine = w.part + (line * w.NR + rg) * w.pw;
+#pragma unroll
+            for (int u = 0; u < NU; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mine[(u * 16 + r) * 64 + lane] = acc[u][r];
+        }
+        else
+            store_row_tiles<APPLY, NU>(d, out, D, b, qi, h, acc);
     }
 }
 
-// ── backward_kv: dK[k][j] = alpha sum_i Q(i,k) W (P - R_i), dV[k][j] = sum_i G(i,k) W ──
-template <int KP, int WQ>
-__global__ __launch_bounds__(64 * WQ) void k_attn_bwd_kv(AttnArgs d, const float* __restrict__ P,
-                                                         const float* __restrict__ G, int D,
-                                                         const float* __restrict__ R,
-                                                         const float* __restrict__ row_max,
-                                                         const float* __restrict__ denom, float* __restrict__ dK,
-                                                         float* __restrict__ dV)
+// Sums (the row max: maxima of) the partials of every line with several non-empty ranges, in range order.
+template <int MODE, int NU>
+__global__ __launch_bounds__(64) void k_attn_combine_rows(AttnArgs d, Work w, int D, float* __restrict__ out)
 {
-    constexpr int NT = 64 * WQ;
-    __shared__ float Qs[IT][KP + LP];
-    __shared__ float Gs[IT][KP + LP];
-    __shared__ float ms[IT], ls[IT], rs[IT];
+    constexpr bool SCALAR = MODE == kRowMax || MODE == kRowDenom || MODE == kRowR;
+    const int lane = threadIdx.x, h = lane >> 5, c = lane & 31;
+    const int item = xcd_item(blockIdx.x, gridDim.x), row = item % w.RT, b = item / w.RT, qi = row * 32 + c;
+    const LineInfo li = line_info(d, w, true, row, 0);
+    if (li.nne <= 1) return;
+    const long line = (long)b * w.RT + row;
+    if constexpr (SCALAR)
+    {
+        float red = MODE == kRowMax ? kLowest : 0.0f;
+        for_ranges(li, w.NR, [&](int q) {
+            const float v = w.part[(line * w.NR + q) * w.pw + c];
+            red = MODE == kRowMax ? fmax_std(red, v) : red + v;
+        });
+        if (h == 0 && qi < d.M) out[(long)b * d.M + qi] = red;
+    }
+    else
+    {
+        f32x16 acc[NU];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) acc[u] = zero16();
+        for_ranges(li, w.NR, [&](int q) {
+            const float* pp = w.part + (line * w.NR + q) * w.pw;
+#pragma unroll
+            for (int u = 0; u < NU; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[u][r] += pp[(u * 16 + r) * 64 + lane];
+        });
+        store_row_tiles<MODE == kRowApply, NU>(d, out, D, b, qi, h, acc);
+    }
+}
+
+// Writes a key line's dK / dV from the registers' (k = 32u + drow(r,h), key kj) layout.
+template <int NU>
+__device__ __forceinline__ void store_col_tiles(const AttnArgs& d, float* dK, float* dV, int b, int kj, int h,
+                                                const f32x16* acck, const f32x16* accv)
+{
+    if (kj >= d.N) return;
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            const int k = 32 * u + drow(r, h);
+            if (k < d.K)
+            {
+                dK[((long)b * d.K + k) * d.N + kj] = d.alpha * acck[u][r];
+                dV[((long)b * d.K + k) * d.N + kj] = accv[u][r];
+            }
+        }
+}
+
+// ── key-line kernel: backward_kv ─────────────────────────────────────────────
+//   dK[k][j] = alpha sum_i Q(i,k) W (P - R_i),  dV[k][j] = sum_i G(i,k) W
+// A workgroup is 4 waves = 4 consecutive key lines sharing one query range,
+// walked kStep query cells at a time through two LDS buffers (as k_attn_rows).
+template <int KP>
+__global__ __launch_bounds__(64 * kWaves) void k_attn_cols(AttnArgs d, Work w, const float* __restrict__ P,
+                                                           const float* __restrict__ G, int D,
+                                                           const float* __restrict__ R,
+                                                           const float* __restrict__ row_max,
+                                                           const float* __restrict__ denom, float* __restrict__ dK,
+                                                           float* __restrict__ dV)
+{
+    constexpr int NT = 64 * kWaves;
+    constexpr int NU = KP / 32;
+    constexpr int GS = KP + 8;   // G row stride: rows 4 apart use disjoint banks
+    constexpr int PQ = 32 * KP / NT;   // per thread, per staged cell
+    static_assert(PQ * NT == 32 * KP, "staging covers each tile exactly");
+    __shared__ float Qs[2][kStep][32][KP + 1];   // Qs[buf][t][ii][k] = Q(ibase_t + ii, k)
+    __shared__ float Gs[2][kStep][32][GS];       // Gs[buf][t][ii][k] = G(ibase_t + ii, k)
+    __shared__ float St[2][kStep][3][32];        // row max, denominator, R of the staged queries
+    __shared__ unsigned need_s;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
-    const int b = blockIdx.y;
-    const int kb0 = blockIdx.x * 32 * WQ, j0w = kb0 + wave * 32, kj = j0w + c;
+    const int per = (w.CT + kWaves - 1) / kWaves * w.NR;
+    const int item = xcd_item(blockIdx.x, gridDim.x), b = item / per, grp = item % per / w.NR, rg = item % w.NR;
+    const int col = grp * kWaves + wave, kj = col * 32 + c;
+    const LineInfo li = col < w.CT ? line_info(d, w, false, col, rg) : LineInfo{};
+    if (threadIdx.x == 0) need_s = 0;
+    __syncthreads();
+    if (lane == 0 && li.mine_nz) atomicOr(&need_s, li.mine_nz);
+    __syncthreads();
+    const unsigned steps = steps_needed(need_s);
+    auto write_empty_line = [&]() {   // a key line without any allowed pair: zero gradients
+        if (li.nne != 0 || rg != 0 || col >= w.CT || kj >= d.N) return;
+        for (int k = h; k < d.K; k += 2)
+        {
+            dK[((long)b * d.K + k) * d.N + kj] = 0.0f;
+            dV[((long)b * d.K + k) * d.N + kj] = 0.0f;
+        }
+    };
+    if (steps == 0)
+    {
+        write_empty_line();
+        return;
+    }
+
     const float* Ab = d.A + (long)b * d.M * d.K;
     const float* Bb = d.B + (long)b * d.K * d.N;
+    const float* Gb = G + (long)b * d.M * D;
+    float qr[kStep][PQ], gr[kStep][PQ], sr[kStep];
+    auto load_step = [&](int st) {
+#pragma unroll
+        for (int t = 0; t < kStep; ++t)
+        {
+            const int ibase = 32 * (rg * kCells + st * kStep + t);
+#pragma unroll
+            for (int u = 0; u < PQ; ++u)
+            {
+                const int e = threadIdx.x + u * NT;
+                const int ii = d.tA ? e % 32 : e / KP, k = d.tA ? e / 32 : e % KP;
+                qr[t][u] = q_at(d, Ab, min(ibase + ii, d.M - 1), min(k, d.K - 1));
+                const int gi = e / KP, gk = e % KP;
+                gr[t][u] = Gb[(long)min(ibase + gi, d.M - 1) * D + min(gk, d.K - 1)];
+            }
+            const long si = (long)b * d.M + min(ibase + static_cast<int>(threadIdx.x % 32), d.M - 1);
+            const int which = threadIdx.x / 32;   // threads 0-95 load the statistics
+            sr[t] = which == 0 ? row_max[si] : which == 1 ? denom[si] : which == 2 ? R[si] : 0.0f;
+        }
+    };
+    auto store_step = [&](int st, int buf) {
+#pragma unroll
+        for (int t = 0; t < kStep; ++t)
+        {
+            const int ibase = 32 * (rg * kCells + st * kStep + t);
+#pragma unroll
+            for (int u = 0; u < PQ; ++u)
+            {
+                const int e = threadIdx.x + u * NT;
+                const int ii = d.tA ? e % 32 : e / KP, k = d.tA ? e / 32 : e % KP;
+                Qs[buf][t][ii][k] = (ibase + ii < d.M && k < d.K) ? qr[t][u] : 0.0f;
+                const int gi = e / KP, gk = e % KP;
+                Gs[buf][t][gi][gk] = (ibase + gi < d.M && gk < d.K) ? gr[t][u] : 0.0f;
+            }
+            if (threadIdx.x < 96)
+            {
+                const int ii = threadIdx.x % 32, which = threadIdx.x / 32;
+                St[buf][t][which][ii] = ibase + ii < d.M ? sr[t] : (which == 1 ? 1.0f : 0.0f);
+            }
+        }
+    };
+    auto next_step = [&](int st) {
+        while (st < kSteps && !((steps >> st) & 1u)) ++st;
+        return st;
+    };
+    int st = next_step(0);
+    load_step(st);
 
+    const int jc = min(kj, d.N - 1);
     float kf[KP / 2];   // B operand of S = Q Kt: Kt(2kk + h, kj)
 #pragma unroll
     for (int kk = 0; kk < KP / 2; ++kk)
     {
         const int k = 2 * kk + h;
-        kf[kk] = (kj < d.N && k < d.K) ? kt_at(d, Bb, k, kj) : 0.0f;
+        const float x = kt_at(d, Bb, min(k, d.K - 1), jc);
+        kf[kk] = (kj < d.N && k < d.K) ? x : 0.0f;
     }
-    f32x16 acck[KP / 32], accv[KP / 32];
+    f32x16 acck[NU], accv[NU];
 #pragma unroll
-    for (int u = 0; u < KP / 32; ++u)
+    for (int u = 0; u < NU; ++u)
     {
         acck[u] = zero16();
         accv[u] = zero16();
     }
-
-    const int steps = (d.M + IT - 1) / IT;
-    for (int st = 0; st < steps; ++st)
+    int buf = 0;
+    store_step(st, buf);
+    __syncthreads();
+    while (true)
     {
-        const int i0 = st * IT;
-        bool need = false;
-        for (int w = 0; w < WQ && !need; ++w)
-            for (int t = 0; t < 2; ++t)
+        const int nxt = next_step(st + 1);
+        if (nxt < kSteps) load_step(nxt);
+#pragma unroll
+        for (int t = 0; t < kStep; ++t)
+        {
+            const int cell = st * kStep + t;
+            if (!((li.mine_nz >> cell) & 1u)) continue;
+            const int ibase = 32 * (rg * kCells + cell);
+            float pv[16], mv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pv[r] = P[((long)b * d.M + min(ibase + drow(r, h), d.M - 1)) * d.N + jc];
+            if ((li.mine_gen >> cell) & 1u)
             {
-                const int ib = i0 / 32 + t, jb = kb0 / 32 + w;
-                if (ib * 32 < d.M && jb * 32 < d.N && cell(d, ib, jb) != 0) need = true;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mv[r] = d.mask[(long)min(ibase + drow(r, h), d.M - 1) * d.N + jc];
             }
-        if (!need) continue;
-        __syncthreads();
-        for (int e = threadIdx.x; e < IT * KP; e += NT)
-        {
-            int ii, k;
-            if (d.tA) { k = e / IT; ii = e % IT; }
-            else { ii = e / KP; k = e % KP; }
-            const int i = i0 + ii;
-            Qs[ii][k] = (i < d.M && k < d.K) ? q_at(d, Ab, i, k) : 0.0f;
-        }
-        for (int e = threadIdx.x; e < IT * KP; e += NT)
-        {
-            const int ii = e / KP, k = e % KP, i = i0 + ii;
-            Gs[ii][k] = (i < d.M && k < d.K) ? G[((long)b * d.M + i) * D + k] : 0.0f;
-        }
-        for (int ii = threadIdx.x; ii < IT; ii += NT)
-        {
-            const int i = i0 + ii;
-            const bool ok = i < d.M;
-            ms[ii] = ok ? row_max[(long)b * d.M + i] : 0.0f;
-            ls[ii] = ok ? denom[(long)b * d.M + i] : 1.0f;
-            rs[ii] = ok ? R[(long)b * d.M + i] : 0.0f;
-        }
-        __syncthreads();
-        if (j0w >= d.N) continue;
+            else
+            {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-        {
-            const int ibase = i0 + 32 * t;
-            if (ibase >= d.M) continue;
-            const int cl = cell(d, ibase / 32, j0w / 32);
-            if (cl == 0) continue;
-            f32x16 s = zero16();
+                for (int r = 0; r < 16; ++r) mv[r] = 0.0f;
+            }
+            f32x16 sacc = zero16();
 #pragma unroll
-            for (int kk = 0; kk < KP / 2; ++kk) s = mfma(Qs[32 * t + c][2 * kk + h], kf[kk], s);
-            float w[16], ds[16];
+            for (int kk = 0; kk < KP / 2; ++kk) sacc = mfma(Qs[buf][t][c][2 * kk + h], kf[kk], sacc);
+            float wv[16], ds[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
-                const int ii = 32 * t + drow(r, h), i = i0 + ii;
-                float x = d.alpha * s[r];
-                float p = 0.0f;
-                if (i >= d.M || kj >= d.N)
-                    x = kNegInf;
-                else
-                {
-                    if (cl == 2) x += d.mask[(long)i * d.N + kj];
-                    p = P[((long)b * d.M + i) * d.N + kj];
-                }
-                w[r] = x == kNegInf ? 0.0f : expf(x - ms[ii]) / ls[ii];
-                ds[r] = w[r] * (p - rs[ii]);
+                const int ii = drow(r, h);
+                const bool ok = ibase + ii < d.M && kj < d.N;
+                const float xs = ok ? d.alpha * sacc[r] + mv[r] : kNegInf;
+                wv[r] = xs == kNegInf ? 0.0f : expf(xs - St[buf][t][0][ii]) / St[buf][t][1][ii];
+                ds[r] = wv[r] * ((ok ? pv[r] : 0.0f) - St[buf][t][2][ii]);
             }
 #pragma unroll
-            for (int u = 0; u < KP / 32; ++u)
-            {
+            for (int u = 0; u < NU; ++u)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                 {
-                    const int ii = 32 * t + drow(r, h);
-                    acck[u] = mfma(Qs[ii][32 * u + c], ds[r], acck[u]);
-                    accv[u] = mfma(Gs[ii][32 * u + c], w[r], accv[u]);
+                    acck[u] = mfma(Qs[buf][t][drow(r, h)][32 * u + c], ds[r], acck[u]);
+                    accv[u] = mfma(Gs[buf][t][drow(r, h)][32 * u + c], wv[r], accv[u]);
                 }
-            }
         }
+        if (nxt >= kSteps) break;
+        store_step(nxt, buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+        st = nxt;
     }
-    if (kj < d.N)
+    if (li.mine_nz == 0)
     {
+        write_empty_line();
+        return;
+    }
+
+    const long line = (long)b * w.CT + col;
+    if (li.nne > 1)   // partial for k_attn_combine_cols
+    {
+        float* mine = w.part + (line * w.NR + rg) * w.pw;
 #pragma unroll
-        for (int u = 0; u < KP / 32; ++u)
-        {
+        for (int u = 0; u < NU; ++u)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
-                const int k = 32 * u + drow(r, h);
-                if (k < d.K)
-                {
-                    dK[((long)b * d.K + k) * d.N + kj] = d.alpha * acck[u][r];
-                    dV[((long)b * d.K + k) * d.N + kj] = accv[u][r];
-                }
+                mine[(u * 16 + r) * 64 + lane] = acck[u][r];
+                mine[((NU + u) * 16 + r) * 64 + lane] = accv[u][r];
             }
-        }
-    }
-}
-
-// Queries (or keys) per workgroup: 4 waves when that still gives the GPU
-// enough workgroups, else 2.
-int waves_for(size_t rows, size_t batch)
-{
-    const size_t blocks4 = (rows + 127) / 128 * batch;
-    return blocks4 >= 512 ? 4 : 2;
-}
-
-template <int KP, int WQ, int MODE>
-int launch_fwd(const AttnArgs& d, size_t batch, const float* row_max, const float* denom, const float* V, int D,
-               float* out, hipStream_t s)
-{
-    const unsigned gx = static_cast<unsigned>((d.M + 32 * WQ - 1) / (32 * WQ));
-    hipLaunchKernelGGL((k_attn_fwd<KP, WQ, MODE>), dim3(gx, static_cast<unsigned>(batch)), dim3(64 * WQ), 0, s, d,
-                       row_max, denom, V, D, out);
-    return launch_status();
-}
-
-template <int KP, int WQ>
-int launch_bwd(const AttnArgs& d, size_t batch, bool kv, const float* P, const float* G, int D, const float* R_in,
-               const float* row_max, const float* denom, float* o1, float* o2, hipStream_t s)
-{
-    if (!kv)
-    {
-        const unsigned gx = static_cast<unsigned>((d.M + 32 * WQ - 1) / (32 * WQ));
-        hipLaunchKernelGGL((k_attn_bwd_q<KP, WQ>), dim3(gx, static_cast<unsigned>(batch)), dim3(64 * WQ), 0, s, d,
-                           P, row_max, denom, o1, o2);
     }
     else
+        store_col_tiles<NU>(d, dK, dV, b, kj, h, acck, accv);
+}
+
+template <int NU>
+__global__ __launch_bounds__(64) void k_attn_combine_cols(AttnArgs d, Work w, float* __restrict__ dK,
+                                                          float* __restrict__ dV)
+{
+    const int lane = threadIdx.x, h = lane >> 5, c = lane & 31;
+    const int item = xcd_item(blockIdx.x, gridDim.x), col = item % w.CT, b = item / w.CT, kj = col * 32 + c;
+    const LineInfo li = line_info(d, w, false, col, 0);
+    if (li.nne <= 1) return;
+    const long line = (long)b * w.CT + col;
+    f32x16 acck[NU], accv[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
     {
-        const unsigned gx = static_cast<unsigned>((d.N + 32 * WQ - 1) / (32 * WQ));
-        hipLaunchKernelGGL((k_attn_bwd_kv<KP, WQ>), dim3(gx, static_cast<unsigned>(batch)), dim3(64 * WQ), 0, s,
-                           d, P, G, D, R_in, row_max, denom, o1, o2);
+        acck[u] = zero16();
+        accv[u] = zero16();
     }
+    for_ranges(li, w.NR, [&](int q) {
+        const float* pp = w.part + (line * w.NR + q) * w.pw;
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+            {
+                acck[u][r] += pp[(u * 16 + r) * 64 + lane];
+                accv[u][r] += pp[((NU + u) * 16 + r) * 64 + lane];
+            }
+    });
+    store_col_tiles<NU>(d, dK, dV, b, kj, h, acck, accv);
+}
+
+// ── host side ────────────────────────────────────────────────────────────────
+struct Layout
+{
+    int RT, CT, NRr, NRc, KP, DP;
+    size_t cls_off, part_off, bytes;
+};
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+Layout layout(size_t batch, size_t M, size_t N, size_t K, size_t D)
+{
+    Layout L{};
+    L.RT = static_cast<int>((M + 31) / 32);
+    L.CT = static_cast<int>((N + 31) / 32);
+    L.NRr = (L.CT + kCells - 1) / kCells;
+    L.NRc = (L.RT + kCells - 1) / kCells;
+    L.KP = K <= 64 ? 64 : 128;
+    L.DP = static_cast<int>((D + 31) / 32 * 32);
+    if (L.DP > 128) L.DP = 128;
+    L.cls_off = 0;
+    L.part_off = align256(static_cast<size_t>(L.RT) * L.CT);
+    const size_t pw_rows = static_cast<size_t>(L.KP > L.DP ? L.KP : L.DP) * 32;
+    const size_t pw_cols = static_cast<size_t>(2 * L.KP) * 32;
+    const size_t rows = batch * L.RT * L.NRr * pw_rows, cols = batch * L.CT * L.NRc * pw_cols;
+    L.bytes = L.part_off + align256((rows > cols ? rows : cols) * sizeof(float));
+    return L;
+}
+
+int prep(const AttnArgs& d, const Layout& L, void* ws, hipStream_t s)
+{
+    if (!d.mask) return 0;
+    hipLaunchKernelGGL(k_attn_classify, dim3(L.CT, L.RT), dim3(256), 0, s, d.mask, d.M, d.N, L.CT,
+                       static_cast<unsigned char*>(ws) + L.cls_off);
     return launch_status();
+}
+
+Work work_of(const Layout& L, void* ws, bool rows, int pw)
+{
+    auto* base = static_cast<unsigned char*>(ws);
+    Work w{};
+    w.RT = L.RT;
+    w.CT = L.CT;
+    w.NR = rows ? L.NRr : L.NRc;
+    w.cls = base + L.cls_off;
+    w.part = reinterpret_cast<float*>(base + L.part_off);
+    w.pw = pw;
+    return w;
+}
+
+template <int KP, int MODE, int DU>
+int launch_rows(const AttnArgs& d, const Work& w, size_t batch, const float* row_max, const float* denom,
+                const float* V, int D, const float* P, const float* Rin, float* out, hipStream_t s)
+{
+    const unsigned groups = static_cast<unsigned>((w.RT + kWaves - 1) / kWaves);
+    hipLaunchKernelGGL((k_attn_rows<KP, MODE, DU>), dim3(groups * w.NR * static_cast<unsigned>(batch)),
+                       dim3(64 * kWaves), 0, s, d, w, row_max, denom, V, D, P, Rin, out);
+    if (int rc = launch_status()) return rc;
+    if (w.NR == 1) return 0;   // every line wrote its output directly
+    constexpr int NU = MODE == kRowApply ? DU : (MODE == kRowDQ ? KP / 32 : 1);
+    hipLaunchKernelGGL((k_attn_combine_rows<MODE, NU>), dim3(static_cast<unsigned>(w.RT) * static_cast<unsigned>(batch)),
+                       dim3(64), 0, s, d, w, D, out);
+    return launch_status();
+}
+
+template <int KP, int MODE>
+int rows_by_width(const AttnArgs& d, const Work& w, size_t batch, const float* row_max, const float* denom,
+                  const float* V, int D, const float* P, const float* Rin, float* out, hipStream_t s)
+{
+    if constexpr (MODE == kRowApply)
+    {
+        switch ((D + 31) / 32)
+        {
+        case 1: return launch_rows<KP, MODE, 1>(d, w, batch, row_max, denom, V, D, P, Rin, out, s);
+        case 2: return launch_rows<KP, MODE, 2>(d, w, batch, row_max, denom, V, D, P, Rin, out, s);
+        case 3: return launch_rows<KP, MODE, 3>(d, w, batch, row_max, denom, V, D, P, Rin, out, s);
+        default: return launch_rows<KP, MODE, 4>(d, w, batch, row_max, denom, V, D, P, Rin, out, s);
+        }
+    }
+    else
+        return launch_rows<KP, MODE, 1>(d, w, batch, row_max, denom, V, D, P, Rin, out, s);
+}
+
+template <int MODE>
+int rows_kernel(const AttnArgs& d, const Work& w, size_t batch, const float* row_max, const float* denom,
+                const float* V, int D, const float* P, const float* Rin, float* out, hipStream_t s)
+{
+    return d.K <= 64 ? rows_by_width<64, MODE>(d, w, batch, row_max, denom, V, D, P, Rin, out, s)
+                     : rows_by_width<128, MODE>(d, w, batch, row_max, denom, V, D, P, Rin, out, s);
 }
 
 } // namespace
 
-size_t attn_workspace_bytes(size_t M, size_t N)
+size_t attn_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D)
 {
-    const size_t cells = ((M + 31) / 32) * ((N + 31) / 32);
-    return (cells + 255) / 256 * 256;
+    return layout(batch, M, N, K, D).bytes;
 }
 
 bool attn_mfma_supported(size_t batch, size_t M, size_t N, size_t K)
 {
-    return K >= 1 && K <= 128 && batch >= 1 && batch <= 65535 && M <= (1u << 30) && N <= (1u << 30);
-}
-
-int attn_prepare(AttnArgs& d, void* workspace, hipStream_t s)
-{
-    d.n_j32 = static_cast<int>((static_cast<size_t>(d.N) + 31) / 32);
-    d.cls = nullptr;
-    if (!d.mask || !workspace || d.M == 0 || d.N == 0 || (d.M + 31) / 32 > 65535) return 0;
-    auto* cls = static_cast<unsigned char*>(workspace);
-    hipLaunchKernelGGL(k_mask_classify, dim3(static_cast<unsigned>(d.n_j32), static_cast<unsigned>((d.M + 31) / 32)),
-                       dim3(256), 0, s, d.mask, d.M, d.N, d.n_j32, cls);
-    d.cls = cls;
-    return launch_status();
+    constexpr size_t span = 32 * kMaxTiles;
+    const size_t cells = ((M + 31) / 32) * ((N + 31) / 32);   // bounds the 1-D grids of work items
+    return K >= 1 && K <= 128 && batch >= 1 && batch <= 65535 && M >= 1 && N >= 1 && M <= span && N <= span &&
+           cells * batch <= (size_t{1} << 30);
 }
 
 int attn_mfma_forward(const AttnArgs& d, size_t batch, int mode, const float* row_max, const float* denom,
-                      const float* V, size_t D, float* out, hipStream_t s)
+                      const float* V, size_t D, float* out, void* workspace, hipStream_t s)
 {
     if (mode == kFwdApply && (D == 0 || D > 128)) return -3;
-    const bool big = d.K > 64;
-    const int wq = waves_for(static_cast<size_t>(d.M), batch);
+    const Layout L = layout(batch, d.M, d.N, d.K, mode == kFwdApply ? D : 1);
+    if (int rc = prep(d, L, workspace, s)) return rc;
     const int Di = static_cast<int>(D);
-#define NNHIP_FWD(KP, WQ)                                                                                          \
-    switch (mode)                                                                                                  \
-    {                                                                                                              \
-    case kFwdMax: return launch_fwd<KP, WQ, kFwdMax>(d, batch, row_max, denom, V, Di, out, s);                    \
-    case kFwdDenom: return launch_fwd<KP, WQ, kFwdDenom>(d, batch, row_max, denom, V, Di, out, s);                \
-    default: return launch_fwd<KP, WQ, kFwdApply>(d, batch, row_max, denom, V, Di, out, s);                       \
+    switch (mode)
+    {
+    case kFwdMax:
+        return rows_kernel<kRowMax>(d, work_of(L, workspace, true, 32), batch, nullptr, nullptr, nullptr, 0,
+                                    nullptr, nullptr, out, s);
+    case kFwdDenom:
+        return rows_kernel<kRowDenom>(d, work_of(L, workspace, true, 32), batch, row_max, nullptr, nullptr,
+                                      0, nullptr, nullptr, out, s);
+    default:
+        return rows_kernel<kRowApply>(d, work_of(L, workspace, true, 32 * L.DP), batch, row_max, denom, V,
+                                      Di, nullptr, nullptr, out, s);
     }
-    if (!big && wq == 4) { NNHIP_FWD(64, 4) }
-    if (!big) { NNHIP_FWD(64, 2) }
-    if (wq == 4) { NNHIP_FWD(128, 4) }
-    NNHIP_FWD(128, 2)
-#undef NNHIP_FWD
 }
 
 int attn_mfma_backward(const AttnArgs& d, size_t batch, bool kv, const float* P, const float* G, size_t D,
                        const float* R_in, const float* row_max, const float* denom, float* o1, float* o2,
-                       hipStream_t s)
+                       void* workspace, hipStream_t s)
 {
-    const bool big = d.K > 64;
-    const int wq = waves_for(static_cast<size_t>(kv ? d.N : d.M), batch);
-    const int Di = static_cast<int>(D);
-    if (!big && wq == 4) return launch_bwd<64, 4>(d, batch, kv, P, G, Di, R_in, row_max, denom, o1, o2, s);
-    if (!big) return launch_bwd<64, 2>(d, batch, kv, P, G, Di, R_in, row_max, denom, o1, o2, s);
-    if (wq == 4) return launch_bwd<128, 4>(d, batch, kv, P, G, Di, R_in, row_max, denom, o1, o2, s);
-    return launch_bwd<128, 2>(d, batch, kv, P, G, Di, R_in, row_max, denom, o1, o2, s);
+    const Layout L = layout(batch, d.M, d.N, d.K, 1);
+    if (int rc = prep(d, L, workspace, s)) return rc;
+    if (!kv)
+    {
+        // R first (into o2), then dQ (o1).
+        if (int rc = rows_kernel<kRowR>(d, work_of(L, workspace, true, 32), batch, row_max, denom, nullptr,
+                                        0, P, nullptr, o2, s))
+            return rc;
+        return rows_kernel<kRowDQ>(d, work_of(L, workspace, true, 32 * L.KP), batch, row_max, denom, nullptr,
+                                   0, P, o2, o1, s);
+    }
+    const Work w = work_of(L, workspace, false, 2 * 32 * L.KP);
+    const dim3 grid(static_cast<unsigned>((L.CT + kWaves - 1) / kWaves * L.NRc) * static_cast<unsigned>(batch));
+    const dim3 lines(static_cast<unsigned>(L.CT) * static_cast<unsigned>(batch));
+    if (d.K <= 64)
+        hipLaunchKernelGGL(k_attn_cols<64>, grid, dim3(64 * kWaves), 0, s, d, w, P, G, static_cast<int>(D), R_in, row_max,
+                           denom, o1, o2);
+    else
+        hipLaunchKernelGGL(k_attn_cols<128>, grid, dim3(64 * kWaves), 0, s, d, w, P, G, static_cast<int>(D), R_in,
+                           row_max, denom, o1, o2);
+    if (int rc = launch_status()) return rc;
+    if (w.NR == 1) return 0;
+    if (d.K <= 64)
+        hipLaunchKernelGGL(k_attn_combine_cols<2>, lines, dim3(64), 0, s, d, w, o1, o2);
+    else
+        hipLaunchKernelGGL(k_attn_combine_cols<4>, lines, dim3(64), 0, s, d, w, o1, o2);
+    return launch_status();
 }
 
 } // namespace nnhip

@@ -128,7 +128,8 @@ private:
     Result<std::shared_ptr<DeviceBuffer>> scratch_(std::size_t bytes);
     Result<void> kernel_(int rc, const char* what);
     Result<void> need_gpu_(std::initializer_list<const Tensor*> ts, const char* what) const;
-    Result<std::shared_ptr<DeviceBuffer>> mask_cells_(const Tensor* mask, std::size_t M, std::size_t N);
+    Result<std::shared_ptr<DeviceBuffer>> attn_ws_(std::size_t batch, std::size_t M, std::size_t N, std::size_t K,
+                                                   std::size_t D);
     std::optional<Result<Tensor>> fused_layer_program_(const ExprSpec& spec, std::span<const Tensor> inputs,
                                                        std::size_t rows, std::size_t cols, bool vector_out);
     Result<Tensor> eval_impl_(const ExprSpec& spec, std::span<const Tensor> inputs, std::size_t rows,

@@ -144,3 +144,22 @@ def test_doc_masked_attention_config5_row(hip):
     assert nrm_err(o.numpy(), ref["O"].reshape(H * T, d)) <= 1e-4
     for name, t in (("dQ", dq), ("dK", dk), ("dV", dv)):
         assert nrm_err(t.numpy(), ref[name].reshape(H * d, T)) <= 1e-3, name
+
+
+def test_fully_masked_tiles(hip, cpu):
+    """Whole 32-row query tiles and 32-column key tiles without an allowed pair: their outputs
+    (lowest() maxima, zero sums, rows and gradients) are still written."""
+    rng = np.random.default_rng(6)
+    batch, M, N, K, D = 3, 100, 130, 64, 64
+    mask = np.zeros((M, N), np.float32)
+    mask[:64] = -np.inf            # query tiles 0-1 fully blocked
+    mask[:, 32:64] = -np.inf       # key tile 1 fully blocked
+    mask[80:, 100:] = rng.normal(size=(20, 30)).astype(np.float32)   # general cells
+    A, B = normal(rng, (batch * K, M)), normal(rng, (batch * K, N))
+    V, P, G = normal(rng, (batch * N, D)), normal(rng, (batch * M, N)), normal(rng, (batch * M, D))
+    h, c = both(hip, cpu, lambda e: _run_all(e, A, B, V, P, G, mask, batch, True, False, 0.125))
+    m = h[0][:, 0].reshape(batch, M)
+    assert np.all(m[:, :64] == np.finfo(np.float32).min)
+    for name, x, y in zip(["m", "l", "O", "dQ", "R", "dK", "dV"], h, c):
+        assert nrm_err(x, y) <= 1e-3, name
+        assert np.array_equal(x == 0, y == 0) or name in ("m",), name
