@@ -34,6 +34,7 @@ sys.path.insert(0, os.path.join(ROOT, "neuralnet.cpp_amd"))
 CFG = dict(vocab_size=32000, d_model=768, seq_len=1024, num_heads=12, d_ff=3072, num_layers=12, pos_enc="alibi")
 BATCH = 8
 PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
 
 
 def step_flops(cfg, batch):
@@ -133,6 +134,31 @@ class StreamTimer:
         return ms.value
 
 
+class Busy:
+    """Keeps the GPU busy while the host queues short kernels: two 4096^3 GEMMs
+    (~3 ms) are enqueued before the start event, so the launches that follow run
+    back to back and the event interval measures kernel time, not host
+    submission rate."""
+
+    def __init__(self, eng, rng):
+        self.eng = eng
+        self.a = eng.tensor(rng.uniform(-1, 1, (4096, 4096)).astype(np.float32))
+
+    def __call__(self):
+        for _ in range(2):
+            self.eng.matmul(self.a, self.a)
+
+
+def timed_ms(timer, busy, fn, reps):
+    """Average milliseconds per call of fn over reps back-to-back calls."""
+    fn()
+    busy()
+    timer.start()
+    for _ in range(reps):
+        fn()   # outputs are dropped at once: the pool hands the same block to the next call
+    return timer.stop_ms() / reps
+
+
 def attention_leg(seed, reps=5):
     """BASELINE configs 2 and 5 through the engine's fused attention primitives."""
     import nnengine
@@ -140,6 +166,7 @@ def attention_leg(seed, reps=5):
     eng = nnengine.Engine(lib)
     timer = StreamTimer(lib, eng)
     rng = np.random.default_rng(seed)
+    busy = Busy(eng, rng)
     out = {}
 
     # config 2: B 16 x H 8 = 128 heads, T 512, d 64, causal, alpha 1/8.
@@ -152,11 +179,7 @@ def attention_leg(seed, reps=5):
         m = eng.batched_matmul_reduce(q, k, BH, "Max", True, False, 0.125, True, mask)
         l = eng.batched_matmul_softmax_denom(q, k, m, BH, True, False, 0.125, mask)
         return eng.batched_matmul_softmax_apply(q, k, vt, m, l, BH, True, False, 0.125, mask)
-    fwd()
-    timer.start()
-    for _ in range(reps):
-        fwd()
-    ms = timer.stop_ms() / reps
+    ms = timed_ms(timer, busy, fwd, reps)
     flop = 4 * d * (T * (T + 1) // 2) * BH
     out["causal_config2_forward"] = {
         "tflops": flop / (ms * 1e-3) / 1e12, "frac_of_fp32_mfma_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
@@ -189,11 +212,7 @@ def attention_leg(seed, reps=5):
             G = eng.rearrange_3d(eng.transpose(g), T, H, d)
             dq, r = eng.batched_matmul_softmax_backward_q(q, k, P, m, l, H, True, False, 0.125, mk)
             eng.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, l, H, True, False, 0.125, mk)
-    fwd_bwd()
-    timer.start()
-    for _ in range(reps):
-        fwd_bwd()
-    ms = timer.stop_ms() / reps
+    ms = timed_ms(timer, busy, fwd_bwd, reps)
     flop = 12 * d * pairs * H
     out["doc_masked_config5_forward_backward"] = {
         "tflops": flop / (ms * 1e-3) / 1e12, "frac_of_fp32_mfma_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
@@ -202,6 +221,131 @@ def attention_leg(seed, reps=5):
                     "backward_q + backward_kv, all 8 rows"}
     eng.sync()
     return out
+
+
+# GEMM sweep (A (M,K) x B (K,N), NN) plus the GPT-shaped
+# Linear products of config 4 in the reference's orientation (W (out,in) x X
+# (in, tokens)) and their backward variants (dX = W^T G: TN, dW = G X^T: NT).
+GEMM_SWEEP = [
+    ("square 1024", 1024, 1024, 1024, False, False),
+    ("square 2048", 2048, 2048, 2048, False, False),
+    ("square 4096", 4096, 4096, 4096, False, False),
+    ("QKV [8192x768]x[768x2304]", 8192, 768, 2304, False, False),
+    ("FFN up [8192x768]x[768x3072]", 8192, 768, 3072, False, False),
+    ("FFN down [8192x3072]x[3072x768]", 8192, 3072, 768, False, False),
+    ("Linear fwd fc1 W(6144,768) X(768,8192)", 6144, 768, 8192, False, False),
+    ("Linear fwd fc2 W(768,3072) X(3072,8192)", 768, 3072, 8192, False, False),
+    ("Linear fwd lm_head W(32000,768) X(768,8192)", 32000, 768, 8192, False, False),
+    ("Linear bwd dX fc1 W^T G (TN)", 768, 6144, 8192, True, False),
+    ("Linear bwd dW fc1 G X^T (NT)", 6144, 8192, 768, False, True),
+    ("Linear bwd dX lm_head W^T G (TN)", 768, 32000, 8192, True, False),
+    ("Linear bwd dW lm_head G X^T (NT)", 32000, 8192, 768, False, True),
+]
+
+
+def gemm_leg(seed):
+    import nnengine
+    lib = nnengine.hip_library()
+    eng = nnengine.Engine(lib)
+    timer = StreamTimer(lib, eng)
+    rng = np.random.default_rng(seed)
+    busy = Busy(eng, rng)
+    out = []
+    for name, M, K, N, tA, tB in GEMM_SWEEP:
+        a = eng.tensor(rng.uniform(-1, 1, (K, M) if tA else (M, K)).astype(np.float32))
+        b = eng.tensor(rng.uniform(-1, 1, (N, K) if tB else (K, N)).astype(np.float32))
+        flop = 2.0 * M * N * K
+        reps = max(3, min(50, int(2e12 / flop)))
+        ms = timed_ms(timer, busy, lambda: eng.matmul(a, b, tA, tB), reps)
+        tf = flop / (ms * 1e-3) / 1e12
+        out.append({"shape": name, "M": M, "N": N, "K": K, "transA": tA, "transB": tB, "ms": ms, "tflops": tf,
+                    "frac_of_fp32_mfma_peak": tf / PEAK_FP32_MFMA_TFLOPS})
+        del a, b
+    eng.sync()
+    return out
+
+
+def hbm_leg(seed):
+    """Memory-bound kernels on the config-4 tensors: algorithmic bytes (distinct
+    inputs read + outputs written, fp32) per call / kernel time."""
+    import nnengine
+    import layer_programs as lp
+    lib = nnengine.hip_library()
+    eng = nnengine.Engine(lib)
+    timer = StreamTimer(lib, eng)
+    rng = np.random.default_rng(seed)
+    busy = Busy(eng, rng)
+    F, N, FF, R, C, V = 768, 8192, 3072, 98304, 1024, 32000
+
+    def t(shape, lo=-1.0, hi=1.0):
+        return eng.tensor(rng.uniform(lo, hi, shape).astype(np.float32))
+
+    x, g, normed = t((F, N)), t((F, N)), t((F, N))
+    gamma, rinv, mvec = t((F, 1), 0.5, 1.5), t((1, N), 0.5, 2.0), t((1, N))
+    gate, up, s, gff = t((FF, N)), t((FF, N)), t((FF, N), 0.0, 1.0), t((FF, N))
+    scores, sg = t((R, C), -4.0, 4.0), t((R, C))
+    logits = t((V, N), -3.0, 3.0)
+    labels = eng.tensor(rng.integers(0, V, (1, N)).astype(np.float32))
+    table = t((V, F))
+    idx = eng.tensor(rng.integers(0, V, (N, 1)).astype(np.float32))
+    grad_rows = t((N, F))
+    mask = eng.tensor(np.tile(np.triu(np.full((C, C), -np.inf, np.float32), 1), (R // C, 1)))
+
+    def prog(name, args, rows, cols, vec=False):
+        spec, _ = getattr(lp, name)()
+        return lambda: (eng.eval_expr_reduce if vec else eng.eval_expr)(spec, args, rows, cols)
+
+    fn, fb, bb = F * N * 4, FF * N * 4, R * C * 4
+    cases = [
+        ("RMSNorm fwd sum of squares ColSum(x*x) (768x8192)", prog("rms_sum_sq", [x, x], F, N, True), fn + N * 4),
+        ("RMSNorm fwd x*colbcast(rinv) (768x8192)", prog("rms_normalize", [x, rinv], F, N), 2 * fn + N * 4),
+        ("RMSNorm fwd normed*rowbcast(gamma) (768x8192)", prog("rms_scale", [normed, gamma], F, N), 2 * fn + F * 4),
+        ("RMSNorm bwd ColSum(g*gamma*normed) (768x8192)",
+         prog("rms_bwd_colsum", [g, gamma, normed], F, N, True), 2 * fn + F * 4 + N * 4),
+        ("RMSNorm bwd RowSum(g*gamma*normed) (768x8192)",
+         prog("rms_bwd_rowsum", [g, gamma, normed], F, N, True), 2 * fn + 2 * F * 4),
+        ("RMSNorm bwd dx (768x8192)", prog("rms_bwd_dx", [g, gamma, mvec, normed, rinv], F, N),
+         3 * fn + F * 4 + 2 * N * 4),
+        ("SwiGLU bwd grad_gate (3072x8192)", prog("swiglu_grad_gate", [gff, up, s, gate, s], FF, N), 5 * fb),
+        ("SwiGLU bwd grad_up (3072x8192)", prog("swiglu_grad_up", [gff, gate, s], FF, N), 4 * fb),
+        ("SwiGLU fwd elementwise Mul (3072x8192)", lambda: eng.elementwise_binary("Mul", gate, up), 3 * fb),
+        ("residual Add (768x8192)", lambda: eng.elementwise_binary("Add", x, g), 3 * fn),
+        ("add_inplace (768x8192)", lambda: eng.add_inplace(normed, g), 3 * fn),
+        ("attention mask Add (98304x1024)", lambda: eng.elementwise_binary("Add", scores, mask), 3 * bb),
+        ("Softmax fwd rows (98304x1024)", prog("softmax_rows", [scores] * 4, R, C), 2 * bb),
+        ("Softmax bwd rows (98304x1024)", prog("softmax_rows_backward", [scores, sg, scores, sg], R, C), 3 * bb),
+        ("sparse CE col_softmax_sparse_forward (32000x8192)",
+         lambda: eng.col_softmax_sparse_forward(logits, labels, None, V, 1.0 / N), 2 * V * N * 4 + 2 * N * 4),
+        ("gather_rows token embedding (32000x768, 8192 ids)", lambda: eng.gather_rows(table, idx),
+         2 * N * F * 4 + N * 4),
+        ("transpose (768x8192)", lambda: eng.transpose(x), 2 * fn),
+        ("rearrange_3d (768, 8 x 1024)", lambda: eng.rearrange_3d(x, F, 8, N // 8), 2 * fn),
+    ]
+    out = []
+    for name, fn_call, nbytes in cases:
+        ms = timed_ms(timer, busy, fn_call, 20)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"kernel": name, "bytes": nbytes, "ms": ms, "GB_s": gbs, "frac_of_hbm_peak": gbs / PEAK_HBM_GBS})
+    eng.sync()
+    return out
+
+
+def pmc_sample(seed):
+    """What the rocprofv3 --pmc passes count: one config-4 training step, then a
+    256 MiB element-wise copy (Neg: 256 MiB read + 256 MiB written) as the last
+    dispatch, the calibration for FETCH_SIZE / WRITE_SIZE."""
+    import nnengine
+    lib = nnengine.hip_library()
+    eng = nnengine.Engine(lib)
+    g = init_session(eng, CFG, BATCH, seed)
+    loss = g.train_step()
+    x = eng.create_tensor(8192, 8192)
+    eng.zero(x)
+    eng.sync()
+    y = eng.elementwise_unary("Neg", x)
+    eng.sync()
+    del y
+    print(json.dumps({"pmc_sample": "1 config-4 train step + 256 MiB Neg copy", "loss": loss}), flush=True)
 
 
 def cpu_leg(seed):
@@ -222,6 +366,20 @@ def cpu_leg(seed):
                        f"{dt:.1f} s", seconds=dt)
 
 
+def gemm_traffic_bytes():
+    """HBM bytes per GEMM launch of the training step, measured by the two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) recorded in
+    profiles/gemm_hbm_traffic.txt (key `traffic_bytes_per_launch`); None when
+    that measurement is absent."""
+    path = os.path.join(ROOT, "profiles", "gemm_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split("=")[1])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -230,14 +388,23 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--skip-cpu-baseline", action="store_true")
     ap.add_argument("--skip-attention", action="store_true")
+    ap.add_argument("--skip-gemm-sweep", action="store_true")
+    ap.add_argument("--skip-hbm", action="store_true")
+    ap.add_argument("--pmc-sample", action="store_true",
+                    help="run only the workload the rocprofv3 --pmc passes count (one step + a calibration copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
         sys.exit(2)
 
+    if args.pmc_sample:
+        pmc_sample(args.seed)
+        return
     gpu = gpu_leg(args.steps, args.warmup, args.seed)
     attn = None if args.skip_attention else attention_leg(args.seed)
+    sweep = None if args.skip_gemm_sweep else gemm_leg(args.seed)
+    hbm = None if args.skip_hbm else hbm_leg(args.seed)
     n_tok = BATCH * CFG["seq_len"]
     ms_per_step = 1000.0 * gpu["elapsed"] / args.steps
     flops = step_flops(CFG, BATCH)
@@ -264,13 +431,17 @@ def main():
         "step_tflop": flops / 1e12,
         "roofline": {"bound": "mfma", "kernel": "fp32 MFMA GEMM (all matmul/batched_matmul launches)",
                      "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_FP32_MFMA_TFLOPS, "traffic": None,
+                     "frac": achieved / PEAK_FP32_MFMA_TFLOPS, "traffic": gemm_traffic_bytes(),
                      "launches": gpu["gemm_launches"], "avg_launch_ms": gemm_avg_ms,
                      "flop_per_launch": gemm_flops_per_launch,
                      "share_of_step": gpu["gemm_ms"] / (gpu["elapsed"] * 1000.0)},
     }
     if attn is not None:
         out["attention"] = attn
+    if sweep is not None:
+        out["gemm_sweep_config3"] = sweep
+    if hbm is not None:
+        out["hbm_kernels"] = hbm
     if not args.skip_cpu_baseline:
         cpu = cpu_leg(args.seed)
         out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}

@@ -1,9 +1,11 @@
-"""The ExprSpec programs the GPT layers issue, built the way the expression DSL
+"""The ExprSpec programs the GPT layers issue (compute_layer.hpp:733-795 RMSNorm,
+:436-444 SwiGLU backward, :840-860 Softmax), built the way the expression DSL
 folds them (left operand before right; every leaf or view is a new input
 slot; reduce instructions are referenced through Reduce operands). The HIP
 engine recognises exactly these programs and runs a fused kernel for each,
-so tests built from them exercise those kernels; the generic interpreter
-handles any other program and the shapes the fused kernels do not take.
+so tests and the bench built from them exercise those kernels; the generic
+interpreter handles any other program and the shapes the fused kernels do
+not take.
 
 Each builder returns (spec, slots): `slots` names, per input slot, which
 argument the caller passes there.
