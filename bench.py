@@ -150,12 +150,14 @@ class Busy:
 
 
 def timed_ms(timer, busy, fn, reps):
-    """Average milliseconds per call of fn over reps back-to-back calls."""
+    """Average milliseconds per call of fn over reps back-to-back calls. Work the
+    engine still holds deferred is launched (settle) before the stop event."""
     fn()
     busy()
     timer.start()
     for _ in range(reps):
         fn()   # outputs are dropped at once: the pool hands the same block to the next call
+    busy.eng.settle()
     return timer.stop_ms() / reps
 
 
@@ -202,16 +204,22 @@ def attention_leg(seed, reps=5):
         mk = eng.tensor(eng.build_attention_mask(1, T, 1, False, doc_ids=ids))
         rows.append([eng.tensor(rng.standard_normal((H * d, T), dtype=np.float32)) for _ in range(4)] + [mk])
 
+    def row(q, k, v, g, mk):
+        # The reference's call sequence for one packed row (compute_layer.hpp:1196-1221, :1304-1327);
+        # its temporaries (the dP product among them) end with the call, as in the layer.
+        m = eng.batched_matmul_reduce(q, k, H, "Max", True, False, 0.125, True, mk)
+        l = eng.batched_matmul_softmax_denom(q, k, m, H, True, False, 0.125, mk)
+        vt = eng.rearrange_3d(eng.transpose(v), T, H, d)
+        o = eng.batched_matmul_softmax_apply(q, k, vt, m, l, H, True, False, 0.125, mk)
+        P = eng.batched_matmul(g, v, H, True, False)
+        G = eng.rearrange_3d(eng.transpose(g), T, H, d)
+        dq, r = eng.batched_matmul_softmax_backward_q(q, k, P, m, l, H, True, False, 0.125, mk)
+        dk, dv = eng.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, l, H, True, False, 0.125, mk)
+        return o, dq, dk, dv
+
     def fwd_bwd():
         for q, k, v, g, mk in rows:
-            m = eng.batched_matmul_reduce(q, k, H, "Max", True, False, 0.125, True, mk)
-            l = eng.batched_matmul_softmax_denom(q, k, m, H, True, False, 0.125, mk)
-            vt = eng.rearrange_3d(eng.transpose(v), T, H, d)
-            eng.batched_matmul_softmax_apply(q, k, vt, m, l, H, True, False, 0.125, mk)
-            P = eng.batched_matmul(g, v, H, True, False)
-            G = eng.rearrange_3d(eng.transpose(g), T, H, d)
-            dq, r = eng.batched_matmul_softmax_backward_q(q, k, P, m, l, H, True, False, 0.125, mk)
-            eng.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, l, H, True, False, 0.125, mk)
+            row(q, k, v, g, mk)
     ms = timed_ms(timer, busy, fwd_bwd, reps)
     flop = 12 * d * pairs * H
     out["doc_masked_config5_forward_backward"] = {

@@ -82,7 +82,9 @@ int nnhip_tensor_to_host(nnhip_engine* e, const nnhip_tensor* t, float* out);   
 int nnhip_tensor_copy_from_host(nnhip_engine* e, nnhip_tensor* t, const float* data);
 size_t nnhip_tensor_rows(const nnhip_tensor* t);
 size_t nnhip_tensor_cols(const nnhip_tensor* t);
-void* nnhip_tensor_data_ptr(const nnhip_tensor* t);   /* device pointer (host pointer for the CPU oracle) */
+/* Device pointer (host pointer for the CPU oracle). Results of the deferred attention calls hold their
+ * values only after nnhip_engine_settle (or any engine call that reads them) on the HIP engine. */
+void* nnhip_tensor_data_ptr(const nnhip_tensor* t);
 void nnhip_tensor_release(nnhip_tensor* t);
 
 /* One ComputeEngine primitive; new tensors are returned in out[] and must be released. */
@@ -137,6 +139,9 @@ int nnhip_gpt_train_step(nnhip_gpt* g, float* loss_out);
 int nnhip_engine_profile_gemm(nnhip_engine* e, int enable);
 int nnhip_engine_profile_gemm_read(nnhip_engine* e, double* launches, double* flops, double* ms);
 void* nnhip_engine_stream(nnhip_engine* e);
+/* Launches every deferred attention call (HipEngine defers the reference's two-pass attention chains
+ * and runs each as one fused launch) whose results are still referenced, without waiting. */
+int nnhip_engine_settle(nnhip_engine* e);
 
 #ifdef __cplusplus
 }

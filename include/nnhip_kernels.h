@@ -120,6 +120,28 @@ int nnhip_bmm_softmax_backward_kv(const float* A, const float* B, const float* P
                                   float* dV, size_t batch, size_t M, size_t N, size_t K, size_t D, int transA,
                                   int transB, float alpha, void* workspace, void* stream);
 
+/* ── one-pass attention chains (no CUDA counterpart) ─────────────────────
+ * The reference's two-pass attention issues reduce(Max) -> softmax_denom -> softmax_apply forward and
+ * batched_matmul(dO, V', transA) -> softmax_backward_q -> softmax_backward_kv backward
+ * (compute_layer.hpp:1196-1221, :1304-1327; semantics cpu_engine.hpp:426-915, :335-419). These entry
+ * points compute each chain in one pass, for the operand layouts the attention layer passes:
+ * Q per batch (K,M) (the transA = 1 operand), K per batch (K,N) (transB = 0), V per batch (N,D),
+ * dO per batch (Kd,M) and V' per batch (Kd,N) (P_ij = alpha2 sum_k dO(k,i) V'(k,j), recomputed, never
+ * stored), G per batch (M,ldg). Supported when nnhip_flash_supported(batch, M, N, max(K,Kd), D)
+ * (K, Kd <= 64; D <= 64, D % 4 == 0); the backward also needs K % 4 == 0, ldg % 4 == 0. Fully masked
+ * 32x32 cells are skipped; long rows are split over workgroups and combined in a fixed order. */
+int nnhip_flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D);
+size_t nnhip_flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D, int backward);
+/* m, l (batch*M) as reduce(Max) and softmax_denom; O (batch*M, D) as softmax_apply, or O = V = NULL. */
+int nnhip_flash_forward(const float* Q, const float* Kt, const float* V, const float* mask, float* m, float* l,
+                        float* O, size_t batch, size_t M, size_t N, size_t K, size_t D, float alpha, void* workspace,
+                        void* stream);
+/* R (batch*M), dQ (batch*K, M) as softmax_backward_q; dK, dV (batch*K, N) as softmax_backward_kv. */
+int nnhip_flash_backward(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* G, size_t ldg,
+                         const float* mask, const float* m, const float* l, float* R, float* dQ, float* dK, float* dV,
+                         size_t batch, size_t M, size_t N, size_t K, size_t Kd, float alpha, float alpha2,
+                         void* workspace, void* stream);
+
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */
 size_t nnhip_col_softmax_workspace_bytes(size_t C, size_t N);

@@ -40,3 +40,13 @@ extern "C" NN_CAPI_EXPORT void* nnhip_engine_stream(void* e)
     auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
     return h ? h->stream() : nullptr;
 }
+
+// Launches every deferred attention call whose results are still referenced,
+// without waiting (HipEngine::settle); end_batch does the same and then waits.
+extern "C" NN_CAPI_EXPORT int nnhip_engine_settle(void* e)
+{
+    auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
+    if (!h) return nn::capi::set_error("settle: not a HIP engine");
+    auto r = h->settle();
+    return r ? 0 : nn::capi::set_error(r.error().message);
+}

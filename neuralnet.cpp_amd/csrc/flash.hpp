@@ -1,0 +1,65 @@
+// flash.hpp — host interface of the one-pass attention chains (k_flash.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+
+namespace nnhip
+{
+
+// Geometry of one launch (filled by the host planner in k_flash.hip).
+struct FlashGeo
+{
+    int M, N;        // queries, keys per batch entry
+    int RT, CT;      // 32-wide query tiles, key tiles
+    int R, NR;       // cells per range, ranges per line
+    int G;           // line groups (4 lines each) per batch entry
+    int pw;          // floats per (line, range) partial
+    const unsigned char* cls;   // RT x CT mask cell classes, or nullptr without a mask
+    float* part;
+    int* flag;
+};
+
+// Forward: m, l (batch*M) and, when O is not null, O (batch*M, D).
+struct FlashFwdArgs
+{
+    const float* Q;      // per batch (K, M)
+    const float* Kt;     // per batch (K, N)
+    const float* V;      // per batch (N, D); unused without O
+    const float* mask;   // (M, N) or nullptr
+    float* m;
+    float* l;
+    float* O;
+    int M, N, K, D;
+    float alpha;
+};
+
+// Backward: R (batch*M), dQ (batch*K, M), dK and dV (batch*K, N) from
+// P_ij = alpha2 * sum_k dO(k, i) V'(k, j) (recomputed), G (per batch (M, ldg)).
+struct FlashBwdArgs
+{
+    const float* Q;      // per batch (K, M)
+    const float* Kt;     // per batch (K, N)
+    const float* dO;     // per batch (Kd, M)
+    const float* Vp;     // per batch (Kd, N)
+    const float* G;      // per batch (M, ldg), ldg >= K
+    const float* mask;   // (M, N) or nullptr
+    const float* m;
+    const float* l;
+    float* R;
+    float* dQ;
+    float* dK;
+    float* dV;
+    int M, N, K, Kd, ldg;
+    float alpha, alpha2;
+};
+
+// Shapes the one-pass kernels take: head dims K (and Kd) <= 64, value width
+// D <= 64 with D % 4 == 0. The backward also needs K % 4 == 0 and ldg % 4 == 0.
+bool flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D);
+size_t flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D, bool backward);
+int flash_forward(const FlashFwdArgs& a, size_t batch, void* workspace, hipStream_t s);
+int flash_backward(const FlashBwdArgs& a, size_t batch, void* workspace, hipStream_t s);
+
+} // namespace nnhip

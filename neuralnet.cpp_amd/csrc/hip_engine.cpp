@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <limits>
 #include <map>
@@ -222,7 +223,64 @@ const Canon& canon(LayerProg p)
     return table[static_cast<int>(p)];
 }
 
+// ── deferred attention chains ───────────────────────────────────────────────
+bool same_t(const Tensor& a, const Tensor& b)
+{
+    return a.dev_ptr() && a.dev_ptr() == b.dev_ptr() && a.rows() == b.rows() && a.cols() == b.cols();
+}
+bool same_mask(const Tensor* a, const std::optional<Tensor>& b) { return a ? (b && same_t(*a, *b)) : !b; }
+bool has_buf(const Tensor& t, const float* p) { return p && t.dev_ptr() == p; }
+// True when a tensor held by a deferred record is also referenced elsewhere.
+bool live(const Tensor& t) { return t.device_buffer().use_count() > 1; }
+
 } // namespace
+
+// reduce(Max) [-> softmax_denom]: m (and l) still to be computed.
+struct HipEngine::PendingFwd
+{
+    Tensor Q, K;
+    std::optional<Tensor> mask;
+    std::size_t batch, M, N, Kd;
+    float alpha;
+    Tensor m;
+    std::optional<Tensor> l;
+    bool uses(const float* p) const
+    {
+        return has_buf(Q, p) || has_buf(K, p) || (mask && has_buf(*mask, p)) || has_buf(m, p) ||
+               (l && has_buf(*l, p));
+    }
+    bool yields(const float* p) const { return has_buf(m, p) || (l && has_buf(*l, p)); }
+    bool matches(const Tensor& A, const Tensor& B, std::size_t b, bool tA, bool tB, Scalar a, const Tensor* mk) const
+    {
+        return same_t(A, Q) && same_t(B, K) && b == batch && tA && !tB && a == alpha && same_mask(mk, mask);
+    }
+};
+
+// batched_matmul(A, B, transA, !transB): its product C still to be computed.
+struct HipEngine::PendingGemm
+{
+    Tensor A, B, C;
+    std::size_t batch, M, N, K;
+    float alpha;
+    bool uses(const float* p) const { return has_buf(A, p) || has_buf(B, p) || has_buf(C, p); }
+    bool yields(const float* p) const { return has_buf(C, p); }
+};
+
+// softmax_backward_q on a deferred product P: dQ and R still to be computed.
+struct HipEngine::PendingBwd
+{
+    Tensor Q, K, P, m, l;
+    std::optional<Tensor> mask;
+    std::size_t batch, M, N, Kd;
+    float alpha;
+    Tensor dQ, R;
+    bool uses(const float* p) const
+    {
+        return has_buf(Q, p) || has_buf(K, p) || has_buf(P, p) || has_buf(m, p) || has_buf(l, p) ||
+               (mask && has_buf(*mask, p)) || has_buf(dQ, p) || has_buf(R, p);
+    }
+    bool yields(const float* p) const { return has_buf(dQ, p) || has_buf(R, p); }
+};
 
 HipEngine::HipEngine()
 {
@@ -320,12 +378,98 @@ Result<void> HipEngine::kernel_(int rc, const char* what)
     return fail(std::string(what) + ": invalid arguments (status " + std::to_string(rc) + ")");
 }
 
-Result<void> HipEngine::need_gpu_(std::initializer_list<const Tensor*> ts, const char* what) const
+Result<void> HipEngine::check_gpu_(std::initializer_list<const Tensor*> ts, const char* what) const
 {
     for (const Tensor* t : ts)
         if (t && (!t->is_gpu() || (t->size() > 0 && !t->dev_ptr())))
             return fail(std::string(what) + ": tensor is not on this GPU engine");
     return {};
+}
+
+Result<void> HipEngine::need_gpu_(std::initializer_list<const Tensor*> ts, const char* what)
+{
+    NN_CHECK(check_gpu_(ts, what));
+    return settle_reads_(ts);
+}
+
+// ── deferred work: launch on demand ─────────────────────────────────────────
+Result<void> HipEngine::settle_reads_(std::initializer_list<const Tensor*> ts)
+{
+    for (const Tensor* t : ts)
+    {
+        if (!t) continue;
+        const float* p = t->dev_ptr();
+        if (!p) continue;
+        if (pbwd_ && pbwd_->yields(p)) NN_CHECK(settle_bwd_());
+        if (pgemm_ && pgemm_->yields(p)) NN_CHECK(settle_gemm_());
+        if (pfwd_ && pfwd_->yields(p)) NN_CHECK(settle_fwd_());
+    }
+    return {};
+}
+
+Result<void> HipEngine::settle_write_(const Tensor& t)
+{
+    const float* p = t.dev_ptr();
+    if (!p) return {};
+    if (pbwd_ && pbwd_->uses(p)) NN_CHECK(settle_bwd_());
+    if (pgemm_ && pgemm_->uses(p))
+    {
+        if (pbwd_ && same_t(pbwd_->P, pgemm_->C)) NN_CHECK(settle_bwd_());
+        NN_CHECK(settle_gemm_());
+    }
+    if (pfwd_ && pfwd_->uses(p)) NN_CHECK(settle_fwd_());
+    return {};
+}
+
+Result<void> HipEngine::settle()
+{
+    NN_CHECK(settle_bwd_());
+    NN_CHECK(settle_gemm_());
+    return settle_fwd_();
+}
+
+// m (and l) of a deferred forward chain, in one pass over the scores.
+Result<void> HipEngine::settle_fwd_()
+{
+    if (!pfwd_) return {};
+    std::unique_ptr<PendingFwd> f = std::move(pfwd_);
+    if (!live(f->m) && !(f->l && live(*f->l))) return {};
+    Tensor l;
+    if (f->l)
+        l = *f->l;
+    else
+    {
+        NN_TRY(t, alloc_(f->batch * f->M, 1));
+        l = t;
+    }
+    NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(f->batch, f->M, f->N, f->Kd, 4, 0)));
+    return kernel_(nnhip_flash_forward(D(f->Q), D(f->K), nullptr, f->mask ? D(*f->mask) : nullptr, W(f->m), W(l),
+                                       nullptr, f->batch, f->M, f->N, f->Kd, 4, f->alpha, ws->data(), stream_),
+                   "batched_matmul_reduce");
+}
+
+Result<void> HipEngine::settle_gemm_()
+{
+    if (!pgemm_) return {};
+    if (pbwd_ && same_t(pbwd_->P, pgemm_->C)) NN_CHECK(settle_bwd_());
+    if (!pgemm_) return {};
+    std::unique_ptr<PendingGemm> g = std::move(pgemm_);
+    if (!live(g->C)) return {};
+    return launch_gemm_(g->A, g->B, g->C, g->batch, true, false, g->alpha, g->M, g->N, g->K);
+}
+
+// dQ and R of a deferred backward_q with the general kernels (P computed first).
+Result<void> HipEngine::settle_bwd_()
+{
+    if (!pbwd_) return {};
+    std::unique_ptr<PendingBwd> q = std::move(pbwd_);
+    if (!live(q->dQ) && !live(q->R)) return {};
+    if (pgemm_ && same_t(q->P, pgemm_->C)) NN_CHECK(settle_gemm_());
+    NN_TRY(ws, attn_ws_(q->batch, q->M, q->N, q->Kd, 1));
+    return kernel_(nnhip_bmm_softmax_backward_q(D(q->Q), D(q->K), D(q->P), D(q->m), D(q->l),
+                                                q->mask ? D(*q->mask) : nullptr, W(q->dQ), W(q->R), q->batch, q->M,
+                                                q->N, q->Kd, 1, 0, q->alpha, ws ? ws->data() : nullptr, stream_),
+                   "batched_matmul_softmax_backward_q");
 }
 
 Result<Tensor> HipEngine::alloc_(std::size_t rows, std::size_t cols)
@@ -350,6 +494,12 @@ Result<std::shared_ptr<DeviceBuffer>> HipEngine::scratch_(std::size_t bytes)
 Result<void> HipEngine::begin_batch() { return {}; }
 
 Result<void> HipEngine::end_batch()
+{
+    NN_CHECK(settle());
+    return sync_();
+}
+
+Result<void> HipEngine::sync_()
 {
     const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream_));
     if (e != hipSuccess) return fail(std::string("HipEngine: stream error: ") + hipGetErrorString(e));
@@ -380,7 +530,7 @@ Result<Tensor> HipEngine::from_matrix(const Matrix& m)
         auto s = static_cast<hipStream_t>(stream_);
         if (hipMemcpyAsync(W(t), m.data(), m.size() * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess)
             return fail("from_matrix: host to device copy failed");
-        NN_CHECK(end_batch());
+        NN_CHECK(sync_());
     }
     return t;
 }
@@ -388,6 +538,7 @@ Result<Tensor> HipEngine::from_matrix(const Matrix& m)
 Result<Matrix> HipEngine::to_matrix(const Tensor& t)
 {
     if (!t.is_gpu()) return fail("to_matrix: tensor is not GPU");
+    NN_CHECK(settle_reads_({&t}));
     Matrix m(t.rows(), t.cols());
     if (m.size())
     {
@@ -395,7 +546,7 @@ Result<Matrix> HipEngine::to_matrix(const Tensor& t)
         if (hipMemcpyAsync(m.data(), D(t), m.size() * sizeof(float), hipMemcpyDeviceToHost, s) != hipSuccess)
             return fail("to_matrix: device to host copy failed");
     }
-    NN_CHECK(end_batch());
+    NN_CHECK(sync_());
     return m;
 }
 
@@ -403,12 +554,13 @@ Result<void> HipEngine::copy_from(Tensor& dst, const Matrix& src)
 {
     if (!dst.is_gpu()) return fail("copy_from: dst tensor is not GPU");
     if (dst.rows() != src.rows() || dst.cols() != src.cols()) return fail("copy_from: shape mismatch");
+    NN_CHECK(settle_write_(dst));
     if (src.size())
     {
         auto s = static_cast<hipStream_t>(stream_);
         if (hipMemcpyAsync(W(dst), src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess)
             return fail("copy_from: host to device copy failed");
-        NN_CHECK(end_batch());
+        NN_CHECK(sync_());
     }
     return {};
 }
@@ -440,6 +592,7 @@ Result<Tensor> HipEngine::slice_rows(const Tensor& src, std::size_t start, std::
 Result<void> HipEngine::insert_rows(Tensor& dst, std::size_t start, const Tensor& src)
 {
     NN_CHECK(need_gpu_({&dst, &src}, "insert_rows"));
+    NN_CHECK(settle_write_(dst));
     if (dst.cols() != src.cols()) return fail("insert_rows: column count mismatch");
     if (start + src.rows() > dst.rows()) return fail("insert_rows: range out of bounds");
     if (src.size() && hipMemcpyAsync(W(dst) + start * dst.cols(), D(src), src.size() * sizeof(float),
@@ -461,6 +614,7 @@ Result<Tensor> HipEngine::gather_rows(const Tensor& table, const Tensor& indices
 Result<void> HipEngine::scatter_add_rows(Tensor& dst, const Tensor& indices, const Tensor& grad)
 {
     NN_CHECK(need_gpu_({&dst, &indices, &grad}, "scatter_add_rows"));
+    NN_CHECK(settle_write_(dst));
     if (dst.cols() != grad.cols()) return fail("scatter_add_rows: column count mismatch");
     const std::size_t n = indices.size();
     if (grad.rows() < n) return fail("scatter_add_rows: grad has fewer rows than indices");
@@ -513,13 +667,10 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
     return C;
 }
 
-Result<Tensor> HipEngine::batched_matmul(const Tensor& A, const Tensor& B, std::size_t batch, bool tA, bool tB,
-                                         Scalar alpha)
+Result<void> HipEngine::launch_gemm_(const Tensor& A, const Tensor& B, Tensor& C, std::size_t batch, bool tA, bool tB,
+                                     Scalar alpha, std::size_t M, std::size_t N, std::size_t K)
 {
-    NN_CHECK(need_gpu_({&A, &B}, "batched_matmul"));
-    NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul"));
-    NN_TRY(C, alloc_(batch * d.M, d.N));
-    const std::size_t wsb = nnhip_gemm_workspace_bytes(d.M, d.N, d.K, batch);
+    const std::size_t wsb = nnhip_gemm_workspace_bytes(M, N, K, batch);
     std::shared_ptr<DeviceBuffer> ws;
     if (wsb)
     {
@@ -529,8 +680,26 @@ Result<Tensor> HipEngine::batched_matmul(const Tensor& A, const Tensor& B, std::
     prof_begin_();
     const int rc = nnhip_gemm(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), batch, tA, tB, alpha,
                               ws ? ws->data() : nullptr, wsb, stream_);
-    prof_end_(2.0 * double(batch) * double(d.M) * double(d.N) * double(d.K));
-    NN_CHECK(kernel_(rc, "batched_matmul"));
+    prof_end_(2.0 * double(batch) * double(M) * double(N) * double(K));
+    return kernel_(rc, "batched_matmul");
+}
+
+Result<Tensor> HipEngine::batched_matmul(const Tensor& A, const Tensor& B, std::size_t batch, bool tA, bool tB,
+                                         Scalar alpha)
+{
+    NN_CHECK(need_gpu_({&A, &B}, "batched_matmul"));
+    NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul"));
+    NN_TRY(C, alloc_(batch * d.M, d.N));
+    // The dP product of the attention backward (compute_layer.hpp:1306-1307) is
+    // deferred: backward_q / backward_kv recompute its entries where the mask
+    // allows them; any other reader gets the full product.
+    if (tA && !tB && nnhip_flash_supported(batch, d.M, d.N, d.K, 4) && d.K % 4 == 0)
+    {
+        NN_CHECK(settle_gemm_());
+        pgemm_ = std::make_unique<PendingGemm>(PendingGemm{A, B, C, batch, d.M, d.N, d.K, alpha});
+        return C;
+    }
+    NN_CHECK(launch_gemm_(A, B, C, batch, tA, tB, alpha, d.M, d.N, d.K));
     return C;
 }
 
@@ -550,6 +719,14 @@ Result<Tensor> HipEngine::batched_matmul_reduce(const Tensor& A, const Tensor& B
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_reduce"));
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_reduce"));
     NN_TRY(out, alloc_(reduce_cols ? batch * d.M : batch, reduce_cols ? 1 : d.N));
+    // First call of the forward chain (compute_layer.hpp:1203-1205): deferred.
+    if (op == ReduceOp::Max && reduce_cols && tA && !tB && nnhip_flash_supported(batch, d.M, d.N, d.K, 4))
+    {
+        NN_CHECK(settle_fwd_());
+        pfwd_ = std::make_unique<PendingFwd>(PendingFwd{A, B, mask ? std::optional<Tensor>(*mask) : std::nullopt,
+                                                        batch, d.M, d.N, d.K, alpha, out, std::nullopt});
+        return out;
+    }
     NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, 1));
     NN_CHECK(kernel_(nnhip_bmm_reduce(D(A), D(B), mask ? D(*mask) : nullptr, W(out), batch, d.M, d.N, d.K, tA, tB,
                                       static_cast<unsigned>(op), alpha, reduce_cols, ws ? ws->data() : nullptr,
@@ -562,10 +739,17 @@ Result<Tensor> HipEngine::batched_matmul_softmax_denom(const Tensor& A, const Te
                                                        std::size_t batch, bool tA, bool tB, Scalar alpha,
                                                        const Tensor* mask)
 {
-    NN_CHECK(need_gpu_({&A, &B, &row_max, mask}, "batched_matmul_softmax_denom"));
+    NN_CHECK(check_gpu_({&A, &B, &row_max, mask}, "batched_matmul_softmax_denom"));
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_softmax_denom"));
     NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_denom", "row_max"));
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_denom"));
+    if (pfwd_ && !pfwd_->l && same_t(row_max, pfwd_->m) && pfwd_->matches(A, B, batch, tA, tB, alpha, mask))
+    {
+        NN_TRY(l, alloc_(batch * d.M, 1));
+        pfwd_->l = l;
+        return l;
+    }
+    NN_CHECK(settle_reads_({&A, &B, &row_max, mask}));
     NN_TRY(out, alloc_(batch * d.M, 1));
     NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, 1));
     NN_CHECK(kernel_(nnhip_bmm_softmax_denom(D(A), D(B), D(row_max), mask ? D(*mask) : nullptr, W(out), batch, d.M,
@@ -578,13 +762,28 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
                                                        const Tensor& row_max, const Tensor& denom, std::size_t batch,
                                                        bool tA, bool tB, Scalar alpha, const Tensor* mask)
 {
-    NN_CHECK(need_gpu_({&A, &B, &V, &row_max, &denom, mask}, "batched_matmul_softmax_apply"));
+    NN_CHECK(check_gpu_({&A, &B, &V, &row_max, &denom, mask}, "batched_matmul_softmax_apply"));
     if (batch != 0 && V.rows() % batch != 0) return fail("batched_matmul_softmax_apply: rows not divisible by batch");
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_softmax_apply"));
     if (V.rows() / batch != d.N) return fail("batched_matmul_softmax_apply: V rows per batch != N");
     NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_apply", "row_max"));
     NN_CHECK(vec_ok(denom, batch * d.M, "batched_matmul_softmax_apply", "denom"));
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_apply"));
+    // Last call of the forward chain: m, l and O in one pass.
+    const bool v_from_chain = pfwd_ && pfwd_->yields(V.dev_ptr());
+    if (!v_from_chain) NN_CHECK(settle_reads_({&V}));
+    if (!v_from_chain && pfwd_ && pfwd_->l && same_t(row_max, pfwd_->m) && same_t(denom, *pfwd_->l) &&
+        pfwd_->matches(A, B, batch, tA, tB, alpha, mask) && nnhip_flash_supported(batch, d.M, d.N, d.K, V.cols()))
+    {
+        std::unique_ptr<PendingFwd> f = std::move(pfwd_);
+        NN_TRY(o, alloc_(batch * d.M, V.cols()));
+        NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, d.K, V.cols(), 0)));
+        NN_CHECK(kernel_(nnhip_flash_forward(D(A), D(B), D(V), mask ? D(*mask) : nullptr, W(f->m), W(*f->l), W(o),
+                                             batch, d.M, d.N, d.K, V.cols(), alpha, ws->data(), stream_),
+                         "batched_matmul_softmax_apply"));
+        return o;
+    }
+    NN_CHECK(settle_reads_({&A, &B, &V, &row_max, &denom, mask}));
     NN_TRY(out, alloc_(batch * d.M, V.cols()));
     NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, V.cols()));
     NN_CHECK(kernel_(nnhip_bmm_softmax_apply(D(A), D(B), D(V), D(row_max), D(denom), mask ? D(*mask) : nullptr,
@@ -599,7 +798,7 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_q(const Tensor& A, con
                                                             std::size_t batch, bool tA, bool tB, Scalar alpha,
                                                             Tensor& r_out, const Tensor* mask)
 {
-    NN_CHECK(need_gpu_({&A, &B, &P, &row_max, &denom, mask}, "batched_matmul_softmax_backward_q"));
+    NN_CHECK(check_gpu_({&A, &B, &P, &row_max, &denom, mask}, "batched_matmul_softmax_backward_q"));
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_softmax_backward_q"));
     if (P.rows() != batch * d.M || P.cols() != d.N) return fail("batched_matmul_softmax_backward_q: P shape mismatch");
     NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_backward_q", "row_max"));
@@ -607,6 +806,19 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_q(const Tensor& A, con
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_backward_q"));
     NN_TRY(dq, alloc_(batch * d.K, d.M));
     NN_TRY(r, alloc_(batch * d.M, 1));
+    // Middle call of the backward chain on a deferred dP: deferred until backward_kv.
+    if (pgemm_ && same_t(P, pgemm_->C) && pgemm_->batch == batch && tA && !tB && d.K % 4 == 0 &&
+        nnhip_flash_supported(batch, d.M, d.N, std::max(d.K, pgemm_->K), 4))
+    {
+        NN_CHECK(settle_reads_({&A, &B, &row_max, &denom, mask}));
+        NN_CHECK(settle_bwd_());
+        pbwd_ = std::make_unique<PendingBwd>(PendingBwd{A, B, P, row_max, denom,
+                                                        mask ? std::optional<Tensor>(*mask) : std::nullopt, batch,
+                                                        d.M, d.N, d.K, alpha, dq, r});
+        r_out = r;
+        return dq;
+    }
+    NN_CHECK(settle_reads_({&A, &B, &P, &row_max, &denom, mask}));
     NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, 1));
     NN_CHECK(kernel_(nnhip_bmm_softmax_backward_q(D(A), D(B), D(P), D(row_max), D(denom), mask ? D(*mask) : nullptr,
                                                   W(dq), W(r), batch, d.M, d.N, d.K, tA, tB, alpha,
@@ -621,7 +833,7 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
                                                              const Tensor& denom, std::size_t batch, bool tA, bool tB,
                                                              Scalar alpha, Tensor& grad_v_out, const Tensor* mask)
 {
-    NN_CHECK(need_gpu_({&A, &B, &P, &G, &R, &row_max, &denom, mask}, "batched_matmul_softmax_backward_kv"));
+    NN_CHECK(check_gpu_({&A, &B, &P, &G, &R, &row_max, &denom, mask}, "batched_matmul_softmax_backward_kv"));
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul_softmax_backward_kv"));
     if (P.rows() != batch * d.M || P.cols() != d.N)
         return fail("batched_matmul_softmax_backward_kv: P shape mismatch");
@@ -633,6 +845,25 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
     if (G.cols() < d.K) return fail("batched_matmul_softmax_backward_kv: G cols < K");
     NN_TRY(dk, alloc_(batch * d.K, d.N));
     NN_TRY(dv, alloc_(batch * d.K, d.N));
+    // Last call of the backward chain: R, dQ, dK, dV with dP recomputed, never stored.
+    const bool g_from_chain = (pbwd_ && pbwd_->yields(G.dev_ptr())) || (pgemm_ && pgemm_->yields(G.dev_ptr()));
+    if (!g_from_chain) NN_CHECK(settle_reads_({&G}));
+    if (!g_from_chain && pbwd_ && pgemm_ && same_t(P, pbwd_->P) && same_t(P, pgemm_->C) && same_t(R, pbwd_->R) &&
+        same_t(A, pbwd_->Q) && same_t(B, pbwd_->K) && same_t(row_max, pbwd_->m) && same_t(denom, pbwd_->l) &&
+        same_mask(mask, pbwd_->mask) && batch == pbwd_->batch && tA && !tB && alpha == pbwd_->alpha &&
+        G.cols() % 4 == 0)
+    {
+        std::unique_ptr<PendingBwd> q = std::move(pbwd_);
+        const PendingGemm& g = *pgemm_;
+        NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, std::max(d.K, g.K), 4, 1)));
+        NN_CHECK(kernel_(nnhip_flash_backward(D(A), D(B), D(g.A), D(g.B), D(G), G.cols(), mask ? D(*mask) : nullptr,
+                                              D(row_max), D(denom), W(q->R), W(q->dQ), W(dk), W(dv), batch, d.M, d.N,
+                                              d.K, g.K, alpha, g.alpha, ws->data(), stream_),
+                         "batched_matmul_softmax_backward_kv"));
+        grad_v_out = dv;
+        return dk;
+    }
+    NN_CHECK(settle_reads_({&A, &B, &P, &G, &R, &row_max, &denom, mask}));
     NN_TRY(ws, attn_ws_(batch, d.M, d.N, d.K, 1));
     NN_CHECK(kernel_(nnhip_bmm_softmax_backward_kv(D(A), D(B), D(P), D(G), D(R), D(row_max), D(denom),
                                                    mask ? D(*mask) : nullptr, W(dk), W(dv), batch, d.M, d.N, d.K,
@@ -679,6 +910,7 @@ Result<Tensor> HipEngine::col_softmax_sparse_forward(const Tensor& logits, const
 Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
 {
     NN_CHECK(need_gpu_({&A, &B}, "add_inplace"));
+    NN_CHECK(settle_write_(A));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("add_inplace: shape mismatch");
     return kernel_(nnhip_elementwise_binary(D(A), D(B), W(A), A.size(), 0u, stream_), "add_inplace");
 }
@@ -686,12 +918,14 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
 Result<void> HipEngine::scale_inplace(Tensor& A, Scalar s)
 {
     NN_CHECK(need_gpu_({&A}, "scale_inplace"));
+    NN_CHECK(settle_write_(A));
     return kernel_(nnhip_elementwise_binary_scalar(D(A), W(A), A.size(), 2u, s, 0, stream_), "scale_inplace");
 }
 
 Result<void> HipEngine::axpy_inplace(Tensor& A, Scalar s, const Tensor& B)
 {
     NN_CHECK(need_gpu_({&A, &B}, "axpy_inplace"));
+    NN_CHECK(settle_write_(A));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("axpy_inplace: shape mismatch");
     return kernel_(nnhip_axpy(D(A), D(B), W(A), A.size(), s, stream_), "axpy_inplace");
 }
@@ -699,6 +933,7 @@ Result<void> HipEngine::axpy_inplace(Tensor& A, Scalar s, const Tensor& B)
 Result<void> HipEngine::zero(Tensor& A)
 {
     NN_CHECK(need_gpu_({&A}, "zero"));
+    NN_CHECK(settle_write_(A));
     return kernel_(nnhip_fill(W(A), A.size(), 0.0f, stream_), "zero");
 }
 
@@ -738,6 +973,7 @@ Result<Tensor> HipEngine::col_reduce_max(const Tensor& A)
 Result<void> HipEngine::broadcast_row_inplace(Tensor& A, const Tensor& v, BinaryOp op)
 {
     NN_CHECK(need_gpu_({&A, &v}, "broadcast_row_inplace"));
+    NN_CHECK(settle_write_(A));
     if (v.rows() != A.rows() || v.cols() != 1) return fail("broadcast_row_inplace: row_vec shape mismatch");
     return kernel_(nnhip_broadcast_row(D(A), D(v), W(A), A.rows(), A.cols(), static_cast<unsigned>(op), stream_),
                    "broadcast_row_inplace");
@@ -745,6 +981,7 @@ Result<void> HipEngine::broadcast_row_inplace(Tensor& A, const Tensor& v, Binary
 Result<void> HipEngine::broadcast_col_inplace(Tensor& A, const Tensor& v, BinaryOp op)
 {
     NN_CHECK(need_gpu_({&A, &v}, "broadcast_col_inplace"));
+    NN_CHECK(settle_write_(A));
     if (v.rows() != 1 || v.cols() != A.cols()) return fail("broadcast_col_inplace: col_vec shape mismatch");
     return kernel_(nnhip_broadcast_col(D(A), D(v), W(A), A.rows(), A.cols(), static_cast<unsigned>(op), stream_),
                    "broadcast_col_inplace");
@@ -806,6 +1043,11 @@ Result<Tensor> HipEngine::eval_impl_(const ExprSpec& spec, std::span<const Tenso
                                      std::size_t cols, bool vector_out)
 {
     NN_CHECK(validate_expr_spec(spec, inputs.size()));
+    for (const Tensor& t : inputs)
+    {
+        if (!t.is_gpu()) return fail("eval_expr: input not GPU");
+        NN_CHECK(settle_reads_({&t}));
+    }
     const int raxis = vector_out ? expr_spec_reduce_axis(spec) : -1;
     if (vector_out && raxis != 0 && raxis != 1)
         return fail("eval_expr_reduce: expression must reduce along rows or along columns");

@@ -13,6 +13,17 @@
 // reuse). to_matrix / from_matrix / copy_from and end_batch / flush_batch
 // synchronise the stream, matching the reference's batch semantics
 // (compute_engine.hpp:93-118).
+//
+// Deferred attention chains: the reference's two-pass attention calls
+// (compute_layer.hpp:1196-1221, :1304-1327) are recorded instead of launched
+// when their operands fit the one-pass kernels, and the whole chain runs as
+// one launch when its last call arrives (reduce -> denom -> apply forward;
+// batched_matmul(transA) -> backward_q -> backward_kv backward). The tensors a
+// deferred call returns are real allocations; any other primitive that reads
+// one of them, or writes in place to any tensor a deferred call uses, first
+// launches the deferred work with the general kernels, and end_batch /
+// flush_batch / settle() launch whatever is still deferred. A deferred result
+// that nobody references any more is dropped without being computed.
 #pragma once
 
 #include <memory>
@@ -111,6 +122,9 @@ public:
     Result<Tensor> eval_expr_reduce(const ExprSpec& spec, std::span<const Tensor> inputs, std::size_t rows,
                                     std::size_t cols) override;
 
+    // Launches every deferred call whose results are still referenced (no wait).
+    Result<void> settle();
+
     // Bytes currently cached (free) and held by live tensors in the pool.
     [[nodiscard]] std::size_t pool_cached_bytes() const;
     [[nodiscard]] std::size_t pool_live_bytes() const;
@@ -127,7 +141,25 @@ private:
     Result<Tensor> alloc_(std::size_t rows, std::size_t cols);
     Result<std::shared_ptr<DeviceBuffer>> scratch_(std::size_t bytes);
     Result<void> kernel_(int rc, const char* what);
-    Result<void> need_gpu_(std::initializer_list<const Tensor*> ts, const char* what) const;
+    // Checks that every tensor lives on this engine, then launches deferred
+    // work whose results are among them (the caller is about to read them).
+    Result<void> need_gpu_(std::initializer_list<const Tensor*> ts, const char* what);
+    Result<void> check_gpu_(std::initializer_list<const Tensor*> ts, const char* what) const;
+    Result<void> sync_();   // waits for the stream (no deferred work is launched)
+    Result<void> launch_gemm_(const Tensor& A, const Tensor& B, Tensor& C, std::size_t batch, bool tA, bool tB,
+                              Scalar alpha, std::size_t M, std::size_t N, std::size_t K);
+
+    struct PendingFwd;
+    struct PendingGemm;
+    struct PendingBwd;
+    std::unique_ptr<PendingFwd> pfwd_;
+    std::unique_ptr<PendingGemm> pgemm_;
+    std::unique_ptr<PendingBwd> pbwd_;
+    Result<void> settle_reads_(std::initializer_list<const Tensor*> ts);
+    Result<void> settle_write_(const Tensor& t);
+    Result<void> settle_fwd_();
+    Result<void> settle_gemm_();
+    Result<void> settle_bwd_();
     Result<std::shared_ptr<DeviceBuffer>> attn_ws_(std::size_t batch, std::size_t M, std::size_t N, std::size_t K,
                                                    std::size_t D);
     std::optional<Result<Tensor>> fused_layer_program_(const ExprSpec& spec, std::span<const Tensor> inputs,

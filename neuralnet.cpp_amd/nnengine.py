@@ -177,6 +177,13 @@ class Engine:
     def sync(self) -> None:
         self._check(self._f["engine_sync"](self._e))
 
+    def settle(self) -> None:
+        """Launches deferred attention work still referenced, without waiting (HIP engine only)."""
+        fn = getattr(self._lib, "nnhip_engine_settle", None)
+        if fn is not None:
+            fn.argtypes = [ctypes.c_void_p]
+            self._check(fn(self._e))
+
     def tensor(self, a) -> Tensor:
         a = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
         if a.ndim == 1:
