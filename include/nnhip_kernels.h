@@ -131,16 +131,22 @@ int nnhip_bmm_softmax_backward_kv(const float* A, const float* B, const float* P
  * (K, Kd <= 64; D <= 64, D % 4 == 0); the backward also needs K % 4 == 0, ldg % 4 == 0. Fully masked
  * 32x32 cells are skipped; long rows are split over workgroups and combined in a fixed order. */
 int nnhip_flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D);
+/* Mask cell table: one byte per 32x32 cell of the (M,N) mask (0 all -inf, 1 all zero, 2 general), the
+ * argument `cells` of the calls below when a mask is given. The caller may keep it while the mask is
+ * unchanged. */
+size_t nnhip_flash_cells_bytes(size_t M, size_t N);
+int nnhip_flash_classify(const float* mask, size_t M, size_t N, void* cells, void* stream);
+/* Scratch for the partial results of rows cut into several ranges (0 when none are). */
 size_t nnhip_flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D, int backward);
 /* m, l (batch*M) as reduce(Max) and softmax_denom; O (batch*M, D) as softmax_apply, or O = V = NULL. */
-int nnhip_flash_forward(const float* Q, const float* Kt, const float* V, const float* mask, float* m, float* l,
-                        float* O, size_t batch, size_t M, size_t N, size_t K, size_t D, float alpha, void* workspace,
-                        void* stream);
+int nnhip_flash_forward(const float* Q, const float* Kt, const float* V, const float* mask, const void* cells,
+                        float* m, float* l, float* O, size_t batch, size_t M, size_t N, size_t K, size_t D,
+                        float alpha, void* workspace, void* stream);
 /* R (batch*M), dQ (batch*K, M) as softmax_backward_q; dK, dV (batch*K, N) as softmax_backward_kv. */
 int nnhip_flash_backward(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* G, size_t ldg,
-                         const float* mask, const float* m, const float* l, float* R, float* dQ, float* dK, float* dV,
-                         size_t batch, size_t M, size_t N, size_t K, size_t Kd, float alpha, float alpha2,
-                         void* workspace, void* stream);
+                         const float* mask, const void* cells, const float* m, const float* l, float* R, float* dQ,
+                         float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K, size_t Kd, float alpha,
+                         float alpha2, void* workspace, void* stream);
 
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */

@@ -17,8 +17,7 @@ struct FlashGeo
     int G;           // line groups (4 lines each) per batch entry
     int pw;          // floats per (line, range) partial
     const unsigned char* cls;   // RT x CT mask cell classes, or nullptr without a mask
-    float* part;
-    int* flag;
+    float* part;     // partials of lines cut into several ranges
 };
 
 // Forward: m, l (batch*M) and, when O is not null, O (batch*M, D).
@@ -58,8 +57,11 @@ struct FlashBwdArgs
 // Shapes the one-pass kernels take: head dims K (and Kd) <= 64, value width
 // D <= 64 with D % 4 == 0. The backward also needs K % 4 == 0 and ldg % 4 == 0.
 bool flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D);
+// Mask cell table: one byte per 32x32 cell of the (M, N) mask (0 all -inf, 1 all zero, 2 general).
+size_t flash_cells_bytes(size_t M, size_t N);
+int flash_classify(const float* mask, size_t M, size_t N, void* cells, hipStream_t s);
 size_t flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D, bool backward);
-int flash_forward(const FlashFwdArgs& a, size_t batch, void* workspace, hipStream_t s);
-int flash_backward(const FlashBwdArgs& a, size_t batch, void* workspace, hipStream_t s);
+int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, hipStream_t s);
+int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, hipStream_t s);
 
 } // namespace nnhip

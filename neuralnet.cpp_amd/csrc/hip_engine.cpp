@@ -407,10 +407,31 @@ Result<void> HipEngine::settle_reads_(std::initializer_list<const Tensor*> ts)
     return {};
 }
 
+Result<const void*> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, std::size_t N)
+{
+    if (!mask) return static_cast<const void*>(nullptr);
+    for (std::size_t i = 0; i < cells_.size(); ++i)
+        if (same_t(cells_[i].mask, *mask))
+        {
+            CellTable t = cells_[i];
+            cells_.erase(cells_.begin() + static_cast<std::ptrdiff_t>(i));
+            cells_.push_back(t);
+            return static_cast<const void*>(t.cells->data());
+        }
+    NN_TRY(buf, scratch_(nnhip_flash_cells_bytes(M, N)));
+    NN_CHECK(kernel_(nnhip_flash_classify(D(*mask), M, N, buf->data(), stream_), "attention mask cells"));
+    constexpr std::size_t kKeep = 8;
+    if (cells_.size() == kKeep) cells_.erase(cells_.begin());
+    cells_.push_back({*mask, buf});
+    return static_cast<const void*>(buf->data());
+}
+
 Result<void> HipEngine::settle_write_(const Tensor& t)
 {
     const float* p = t.dev_ptr();
     if (!p) return {};
+    for (std::size_t i = cells_.size(); i-- > 0;)
+        if (has_buf(cells_[i].mask, p)) cells_.erase(cells_.begin() + static_cast<std::ptrdiff_t>(i));
     if (pbwd_ && pbwd_->uses(p)) NN_CHECK(settle_bwd_());
     if (pgemm_ && pgemm_->uses(p))
     {
@@ -442,9 +463,10 @@ Result<void> HipEngine::settle_fwd_()
         NN_TRY(t, alloc_(f->batch * f->M, 1));
         l = t;
     }
+    NN_TRY(cells, mask_cells_(f->mask ? &*f->mask : nullptr, f->M, f->N));
     NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(f->batch, f->M, f->N, f->Kd, 4, 0)));
-    return kernel_(nnhip_flash_forward(D(f->Q), D(f->K), nullptr, f->mask ? D(*f->mask) : nullptr, W(f->m), W(l),
-                                       nullptr, f->batch, f->M, f->N, f->Kd, 4, f->alpha, ws->data(), stream_),
+    return kernel_(nnhip_flash_forward(D(f->Q), D(f->K), nullptr, f->mask ? D(*f->mask) : nullptr, cells, W(f->m),
+                                       W(l), nullptr, f->batch, f->M, f->N, f->Kd, 4, f->alpha, ws->data(), stream_),
                    "batched_matmul_reduce");
 }
 
@@ -777,9 +799,10 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
     {
         std::unique_ptr<PendingFwd> f = std::move(pfwd_);
         NN_TRY(o, alloc_(batch * d.M, V.cols()));
+        NN_TRY(cells, mask_cells_(mask, d.M, d.N));
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, d.K, V.cols(), 0)));
-        NN_CHECK(kernel_(nnhip_flash_forward(D(A), D(B), D(V), mask ? D(*mask) : nullptr, W(f->m), W(*f->l), W(o),
-                                             batch, d.M, d.N, d.K, V.cols(), alpha, ws->data(), stream_),
+        NN_CHECK(kernel_(nnhip_flash_forward(D(A), D(B), D(V), mask ? D(*mask) : nullptr, cells, W(f->m), W(*f->l),
+                                             W(o), batch, d.M, d.N, d.K, V.cols(), alpha, ws->data(), stream_),
                          "batched_matmul_softmax_apply"));
         return o;
     }
@@ -855,10 +878,11 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
     {
         std::unique_ptr<PendingBwd> q = std::move(pbwd_);
         const PendingGemm& g = *pgemm_;
+        NN_TRY(cells, mask_cells_(mask, d.M, d.N));
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, std::max(d.K, g.K), 4, 1)));
         NN_CHECK(kernel_(nnhip_flash_backward(D(A), D(B), D(g.A), D(g.B), D(G), G.cols(), mask ? D(*mask) : nullptr,
-                                              D(row_max), D(denom), W(q->R), W(q->dQ), W(dk), W(dv), batch, d.M, d.N,
-                                              d.K, g.K, alpha, g.alpha, ws->data(), stream_),
+                                              cells, D(row_max), D(denom), W(q->R), W(q->dQ), W(dk), W(dv), batch,
+                                              d.M, d.N, d.K, g.K, alpha, g.alpha, ws->data(), stream_),
                          "batched_matmul_softmax_backward_kv"));
         grad_v_out = dv;
         return dk;

@@ -149,6 +149,16 @@ private:
     Result<void> launch_gemm_(const Tensor& A, const Tensor& B, Tensor& C, std::size_t batch, bool tA, bool tB,
                               Scalar alpha, std::size_t M, std::size_t N, std::size_t K);
 
+    // Mask cell tables of the one-pass attention kernels, kept per mask tensor
+    // (most recent last) until the mask is written in place or evicted.
+    struct CellTable
+    {
+        Tensor mask;
+        std::shared_ptr<DeviceBuffer> cells;
+    };
+    std::vector<CellTable> cells_;
+    Result<const void*> mask_cells_(const Tensor* mask, std::size_t M, std::size_t N);
+
     struct PendingFwd;
     struct PendingGemm;
     struct PendingBwd;
