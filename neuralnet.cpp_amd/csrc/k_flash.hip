@@ -61,7 +61,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr int kWaves = 4;
-constexpr int kMaxRange = 64;   // cells per range: one 64-bit ballot
 
 __device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c)
 {
@@ -112,47 +111,42 @@ __device__ __forceinline__ Item item_of(const FlashGeo& g)
     return r;
 }
 
-// Ballots of the non-empty / general cells of range r of a line (lane x <-> cell r*R + x).
-// rows: the line is a query tile and cells run along keys; else a key tile, cells along queries.
-struct Bits
-{
-    unsigned long long nz, gen;
-};
-__device__ __forceinline__ Bits range_bits(const FlashGeo& g, bool rows, int line, int r)
-{
-    const int lane = threadIdx.x & 63, cells = rows ? g.CT : g.RT, x = r * g.R + lane;
-    const bool in = lane < g.R && x < cells;
-    if (!g.cls) return {__ballot(in), 0ull};
-    int cl = 0;
-    if (in) cl = rows ? g.cls[(long)line * g.CT + x] : g.cls[(long)x * g.CT + line];
-    return {__ballot(cl != 0), __ballot(cl == 2)};
-}
-
-// This range's cells of a line and the number of the line's non-empty ranges.
+// This range's cells of a line (ballots: bit x <-> cell rg*R + x, non-empty /
+// general) and which of the line's ranges are non-empty. R is a power of two
+// <= 64, so every range lies inside one 64-cell ballot; lines are scanned one
+// 64-cell chunk per lane load. rows: the line is a query tile and cells run
+// along keys; else a key tile, cells along queries.
 struct LineWork
 {
-    unsigned long long nz, gen;
+    unsigned long long nz, gen, ranges;
     int nne;
 };
 __device__ __forceinline__ LineWork line_work(const FlashGeo& g, bool rows, int line, int rg)
 {
-    LineWork w{0ull, 0ull, 0};
+    LineWork w{0ull, 0ull, 0ull, 0};
     if (line >= (rows ? g.RT : g.CT)) return w;
-    if (!g.cls)
+    const int cells = rows ? g.CT : g.RT, lane = threadIdx.x & 63;
+    const unsigned long long lowR = g.R >= 64 ? ~0ull : ((1ull << g.R) - 1);
+    for (int x0 = 0; x0 < cells; x0 += 64)
     {
-        const Bits b = range_bits(g, rows, line, rg);
-        return {b.nz, 0ull, g.NR};
-    }
-    for (int r = 0; r < g.NR; ++r)
-    {
-        const Bits b = range_bits(g, rows, line, r);
-        w.nne += b.nz != 0;
-        if (r == rg)
+        const int x = x0 + lane;
+        int cl = 0;
+        if (x < cells) cl = !g.cls ? 1 : (rows ? g.cls[(long)line * g.CT + x] : g.cls[(long)x * g.CT + line]);
+        const unsigned long long nz = __ballot(cl != 0), gen = __ballot(cl == 2);
+        const int r_end = min(g.NR, (x0 + 64) / g.R);
+        for (int r = x0 / g.R; r < r_end; ++r)
         {
-            w.nz = b.nz;
-            w.gen = b.gen;
+            const int sh = r * g.R - x0;
+            const unsigned long long bits = (nz >> sh) & lowR;
+            if (bits) w.ranges |= 1ull << r;
+            if (r == rg)
+            {
+                w.nz = bits;
+                w.gen = (gen >> sh) & lowR;
+            }
         }
     }
+    w.nne = __popcll(w.ranges);
     return w;
 }
 // Who writes a line's outputs: with one non-empty range its workgroup writes
@@ -545,15 +539,15 @@ __global__ __launch_bounds__(64) void k_flash_fwd_combine(FlashFwdArgs a, FlashG
     const int lane = threadIdx.x, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
-    if (line_work(g, true, line, 0).nne <= 1) return;
+    const LineWork lw = line_work(g, true, line, 0);
+    if (lw.nne <= 1) return;
     float m = kLowest, l = 0.0f;
     f32x16 o[DU];
 #pragma unroll
     for (int u = 0; u < DU; ++u) o[u] = zero16();
-    for (int rg = 0; rg < g.NR; ++rg)
+    for (unsigned long long rs = lw.ranges; rs; rs &= rs - 1)
     {
-        if (!range_bits(g, true, line, rg).nz) continue;
-        const float* pp = g.part + (lidx * g.NR + rg) * g.pw;
+        const float* pp = g.part + (lidx * g.NR + __builtin_ctzll(rs)) * g.pw;
         const float mr = pp[c], lr = pp[32 + c];
         const float mn = fmax_f(m, mr);
         const float sa = exp_neg(m - mn), sb = exp_neg(mr - mn);
@@ -567,7 +561,7 @@ __global__ __launch_bounds__(64) void k_flash_fwd_combine(FlashFwdArgs a, FlashG
                 for (int r = 0; r < 16; ++r) o[u][r] = o[u][r] * sa + pp[64 + (u * 16 + r) * 64 + lane] * sb;
         }
     }
-    const LineWork one{1ull, 0ull, 1};
+    const LineWork one{1ull, 0ull, 1ull, 1};
     fwd_store<DP, WITH_O>(a, g, one, b, line, 0, m, l, o);
 }
 
@@ -647,6 +641,7 @@ __device__ __forceinline__ void rows_group(const FlashBwdArgs& a, const FlashGeo
         const long srow = (long)b * g.M + qc;
         const float mi = a.m[srow], li = a.l[srow];
         const float linv = li != 0.0f ? 1.0f / li : 0.0f;
+        const float mb = mi == kLowest ? 0.0f : mi * kLog2e;   // a row without allowed keys has only -inf scores
         const float* mrow = a.mask ? a.mask + (long)qc * g.N : nullptr;
         kt.store(Ks[0], threadIdx.x);
         vt.store(Vs[0], threadIdx.x);
@@ -663,22 +658,22 @@ __device__ __forceinline__ void rows_group(const FlashBwdArgs& a, const FlashGeo
             if ((lw.nz >> cur) & 1ull)
             {
                 const int jbase = 32 * (cell0 + cur);
-                float mv[16];
-                if ((lw.gen >> cur) & 1ull)
-                    mask_row16(mrow, g.N, jbase, h, mv);
-                else
-                {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) mv[r] = 0.0f;
-                }
                 const f32x16 s = score_chain<KP>(Ks[buf], qf, h, c);
                 const f32x16 pp = score_chain<KP>(Vs[buf], of, h, c);
                 float w[16], wp[16];
+                const bool gen = (lw.gen >> cur) & 1ull, full = jbase + 32 <= g.N;
+                if (full && !gen)
+                    cell_scores<true, false>(s, a.alpha, mrow, g.N, jbase, h, w);
+                else if (full)
+                    cell_scores<true, true>(s, a.alpha, mrow, g.N, jbase, h, w);
+                else if (!gen)
+                    cell_scores<false, false>(s, a.alpha, mrow, g.N, jbase, h, w);
+                else
+                    cell_scores<false, true>(s, a.alpha, mrow, g.N, jbase, h, w);
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                 {
-                    const float sc = jbase + drow(r, h) < g.N ? a.alpha * s[r] + mv[r] : kNegInf;
-                    w[r] = sc == kNegInf ? 0.0f : exp_neg(sc - mi) * linv;
+                    w[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(w[r], kLog2e, -mb)) * linv;
                     wp[r] = w[r] * (a.alpha2 * pp[r]);
                     racc += wp[r];
                 }
@@ -714,7 +709,8 @@ __global__ __launch_bounds__(64) void k_flash_bwd_rows_combine(FlashBwdArgs a, F
     const int lane = threadIdx.x, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
-    if (line_work(g, true, line, 0).nne <= 1) return;
+    const LineWork lw = line_work(g, true, line, 0);
+    if (lw.nne <= 1) return;
     float racc = 0.0f;
     f32x16 x[DU], y[DU];
 #pragma unroll
@@ -723,10 +719,9 @@ __global__ __launch_bounds__(64) void k_flash_bwd_rows_combine(FlashBwdArgs a, F
         x[u] = zero16();
         y[u] = zero16();
     }
-    for (int rg = 0; rg < g.NR; ++rg)
+    for (unsigned long long rs = lw.ranges; rs; rs &= rs - 1)
     {
-        if (!range_bits(g, true, line, rg).nz) continue;
-        const float* pp = g.part + (lidx * g.NR + rg) * g.pw;
+        const float* pp = g.part + (lidx * g.NR + __builtin_ctzll(rs)) * g.pw;
         racc += pp[c];
 #pragma unroll
         for (int u = 0; u < DU; ++u)
@@ -737,7 +732,7 @@ __global__ __launch_bounds__(64) void k_flash_bwd_rows_combine(FlashBwdArgs a, F
                 y[u][r] += pp[32 + ((DU + u) * 16 + r) * 64 + lane];
             }
     }
-    const LineWork one{1ull, 0ull, 1};
+    const LineWork one{1ull, 0ull, 1ull, 1};
     rows_store<KP>(a, g, one, b, line, 0, racc, x, y);
 }
 
@@ -756,7 +751,25 @@ __device__ __forceinline__ void stage_cols(TTile<KP>& qt, TTile<KP>& ot, RTile<K
         const int i = i0 + static_cast<int>(threadIdx.x & 31), which = threadIdx.x >> 5;
         float v = 0.0f;
         if (i < M) v = which == 0 ? mb[i] : which == 1 ? lb[i] : Rb[i];
-        st = which == 1 ? (v != 0.0f ? 1.0f / v : 0.0f) : v;
+        // m * log2(e) (0 for a row without allowed keys), 1 / l (0 for l = 0), R.
+        st = which == 0 ? (v == kLowest ? 0.0f : v * kLog2e) : which == 1 ? (v != 0.0f ? 1.0f / v : 0.0f) : v;
+    }
+}
+
+// Scores of one cell of the key-line kernel for this lane's key (16 queries
+// drow(r,h)): alpha * dot + mask, -inf outside the (M, N) plane.
+template <bool FULL, bool MASKED>
+__device__ __forceinline__ void col_scores(const f32x16& s, const FlashBwdArgs& a, int ibase, int jc, int kj, int h,
+                                           int M, int N, float* x)
+{
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+    {
+        const int i = ibase + drow(r, h);
+        float v = a.alpha * s[r];
+        if constexpr (MASKED) v += a.mask[(long)min(i, M - 1) * N + jc];
+        if constexpr (!FULL) v = (i < M && kj < N) ? v : kNegInf;
+        x[r] = v;
     }
 }
 
@@ -853,27 +866,23 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
             if ((lw.nz >> cur) & 1ull)
             {
                 const int ibase = 32 * (cell0 + cur);
-                float mv[16];
-                if ((lw.gen >> cur) & 1ull)
-                {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) mv[r] = a.mask[(long)min(ibase + drow(r, h), g.M - 1) * g.N + jc];
-                }
-                else
-                {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) mv[r] = 0.0f;
-                }
                 const f32x16 s = score_chain<KP>(Qs[buf], kf, h, c);
                 const f32x16 p = score_chain<KP>(Os[buf], vf, h, c);
                 float w[16], ds[16];
+                const bool gen = (lw.gen >> cur) & 1ull, full = ibase + 32 <= g.M && (line + 1) * 32 <= g.N;
+                if (full && !gen)
+                    col_scores<true, false>(s, a, ibase, jc, kj, h, g.M, g.N, w);
+                else if (full)
+                    col_scores<true, true>(s, a, ibase, jc, kj, h, g.M, g.N, w);
+                else if (!gen)
+                    col_scores<false, false>(s, a, ibase, jc, kj, h, g.M, g.N, w);
+                else
+                    col_scores<false, true>(s, a, ibase, jc, kj, h, g.M, g.N, w);
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                 {
                     const int ii = drow(r, h);
-                    const bool ok = ibase + ii < g.M && kj < g.N;
-                    const float sc = ok ? a.alpha * s[r] + mv[r] : kNegInf;
-                    w[r] = sc == kNegInf ? 0.0f : exp_neg(sc - St[buf][0][ii]) * St[buf][1][ii];
+                    w[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(w[r], kLog2e, -St[buf][0][ii])) * St[buf][1][ii];
                     ds[r] = w[r] * (a.alpha2 * p[r] - St[buf][2][ii]);
                 }
                 value_chain<KP>(Gs[buf], w, h, c, dv);
@@ -912,7 +921,8 @@ __global__ __launch_bounds__(64) void k_flash_bwd_cols_combine(FlashBwdArgs a, F
     const int lane = threadIdx.x;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.CT), line = static_cast<int>(lidx % g.CT);
-    if (line_work(g, false, line, 0).nne <= 1) return;
+    const LineWork lw = line_work(g, false, line, 0);
+    if (lw.nne <= 1) return;
     f32x16 dk[DU], dv[DU];
 #pragma unroll
     for (int u = 0; u < DU; ++u)
@@ -920,10 +930,9 @@ __global__ __launch_bounds__(64) void k_flash_bwd_cols_combine(FlashBwdArgs a, F
         dk[u] = zero16();
         dv[u] = zero16();
     }
-    for (int rg = 0; rg < g.NR; ++rg)
+    for (unsigned long long rs = lw.ranges; rs; rs &= rs - 1)
     {
-        if (!range_bits(g, false, line, rg).nz) continue;
-        const float* pp = g.part + (lidx * g.NR + rg) * g.pw;
+        const float* pp = g.part + (lidx * g.NR + __builtin_ctzll(rs)) * g.pw;
 #pragma unroll
         for (int u = 0; u < DU; ++u)
 #pragma unroll
@@ -933,7 +942,7 @@ __global__ __launch_bounds__(64) void k_flash_bwd_cols_combine(FlashBwdArgs a, F
                 dv[u][r] += pp[((DU + u) * 16 + r) * 64 + lane];
             }
     }
-    const LineWork one{1ull, 0ull, 1};
+    const LineWork one{1ull, 0ull, 1ull, 1};
     cols_store<KP>(a, g, one, b, line, 0, dk, dv);
 }
 
@@ -963,19 +972,18 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 int pad32(size_t x) { return x <= 32 ? 32 : 64; }
 
-// Ranges per line: one range when there are enough workgroups to fill the GPU
-// twice over, else lines are cut (at most 64 cells per range, at least 8).
+// Ranges per line: R cells each, R a power of two in [8, 64] and at most 64
+// ranges per line. One range when there are enough workgroups to fill the GPU
+// twice over, else lines are cut until there are about four times as many
+// workgroups as CUs.
 void ranges(size_t items, int cells, int& R, int& NR)
 {
-    int nr = (cells + kMaxRange - 1) / kMaxRange;
+    R = 64;
     if (items < 512)
     {
-        const int want = static_cast<int>((1024 + items - 1) / items);
-        const int cap = (cells + 7) / 8;
-        nr = std::max(nr, std::min(want, cap));
+        const size_t want = (1024 + items - 1) / items;
+        while (R > 8 && static_cast<size_t>((cells + R - 1) / R) < want) R /= 2;
     }
-    nr = std::max(nr, 1);
-    R = (cells + nr - 1) / nr;
     NR = (cells + R - 1) / R;
 }
 
@@ -1047,8 +1055,9 @@ bool flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D)
 {
     // Head dims up to 64 and value widths up to 64 in multiples of 4 (16-byte
     // value rows); sizes that fit int; at most 2^30 cells over all batches.
+    // Lines of at most 64 ranges of 64 cells: M, N <= 131072.
     return batch >= 1 && M >= 1 && N >= 1 && K >= 1 && K <= 64 && D >= 1 && D <= 64 && D % 4 == 0 &&
-           M <= (size_t{1} << 24) && N <= (size_t{1} << 24) && batch <= (size_t{1} << 20) &&
+           M <= (size_t{1} << 17) && N <= (size_t{1} << 17) && batch <= (size_t{1} << 20) &&
            batch * ((M + 31) / 32) * ((N + 31) / 32) <= (size_t{1} << 30);
 }
 

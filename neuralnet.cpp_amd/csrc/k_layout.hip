@@ -38,6 +38,40 @@ __global__ __launch_bounds__(256) void k_transpose(const float* A, float* out, s
     }
 }
 
+// 64x64 tile per workgroup with 16-byte accesses on both sides (R, C multiples
+// of 4, 16-byte aligned): 16 threads cover a 256-byte row segment of A on the
+// way in and of out on the way out; the padded LDS tile turns the tile.
+__global__ __launch_bounds__(256) void k_transpose4(const float* A, float* out, size_t R, size_t C)
+{
+    __shared__ float tile[64][65];
+    const size_t r0 = static_cast<size_t>(blockIdx.y) * 64, c0 = static_cast<size_t>(blockIdx.x) * 64;
+    const unsigned tx = threadIdx.x % 16, ty = threadIdx.x / 16;   // 16 x 16
+#pragma unroll
+    for (unsigned k = 0; k < 4; ++k)
+    {
+        const unsigned rr = ty + 16 * k;
+        const size_t r = r0 + rr, c = c0 + 4 * tx;
+        if (r < R && c < C)
+        {
+            const float4 v = *reinterpret_cast<const float4*>(A + r * C + c);
+            tile[rr][4 * tx + 0] = v.x;
+            tile[rr][4 * tx + 1] = v.y;
+            tile[rr][4 * tx + 2] = v.z;
+            tile[rr][4 * tx + 3] = v.w;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (unsigned k = 0; k < 4; ++k)
+    {
+        const unsigned cc = ty + 16 * k;
+        const size_t c = c0 + cc, r = r0 + 4 * tx;   // out (C, R): row c, columns r .. r+3
+        if (c < C && r < R)
+            *reinterpret_cast<float4*>(out + c * R + r) =
+                make_float4(tile[4 * tx + 0][cc], tile[4 * tx + 1][cc], tile[4 * tx + 2][cc], tile[4 * tx + 3][cc]);
+    }
+}
+
 // ── rearrange_3d: (M, B*N) <-> (B*M, N), contiguous runs of N ─────────────
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void k_rearrange(const float* in, float* out, size_t M, size_t B, size_t N,
@@ -215,8 +249,11 @@ extern "C" int nnhip_transpose(const float* A, float* out, size_t R, size_t C, v
 {
     if (R == 0 || C == 0) return 0;
     if ((C + 63) / 64 > 0x7fffffff || (R + 63) / 64 > 65535) return -1;
-    hipLaunchKernelGGL(k_transpose, dim3(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>((R + 63) / 64)),
-                       dim3(256), 0, static_cast<hipStream_t>(stream), A, out, R, C);
+    const dim3 grid(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>((R + 63) / 64));
+    if (R % 4 == 0 && C % 4 == 0 && aligned16(A) && aligned16(out))
+        hipLaunchKernelGGL(k_transpose4, grid, dim3(256), 0, static_cast<hipStream_t>(stream), A, out, R, C);
+    else
+        hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, static_cast<hipStream_t>(stream), A, out, R, C);
     return launch_status();
 }
 

@@ -166,6 +166,129 @@ __global__ __launch_bounds__(kThreads) void k_ce_grad(const float* L, const floa
     }
 }
 
+// ── float4 column kernels (N % 4 == 0, 16-byte aligned rows) ───────────────
+// A lane owns 4 consecutive columns, so a wave reads 1 KB of one row per load;
+// the 4 waves of a workgroup interleave rows. Per-column state stays in
+// registers for the whole row chunk.
+constexpr unsigned kGroupRows = 4;    // rows folded into the running (max, sum) at once
+
+__device__ __forceinline__ float& at(float4& v, int e) { return reinterpret_cast<float*>(&v)[e]; }
+__device__ __forceinline__ float at(const float4& v, int e) { return reinterpret_cast<const float*>(&v)[e]; }
+
+template <bool GIVEN_MAX>
+__global__ __launch_bounds__(kThreads) void k_col_stats4(const float* L, const float* col_max, float* part_m,
+                                                         float* part_s, size_t C, size_t N, size_t rows_per_chunk)
+{
+    __shared__ float4 sm[kWaves][64], ss[kWaves][64];
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const size_t N4 = N / 4, c4 = static_cast<size_t>(blockIdx.x) * 64 + lane;
+    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
+    const size_t r1 = r0 + rows_per_chunk < C ? r0 + rows_per_chunk : C;
+    const float4* L4 = reinterpret_cast<const float4*>(L);
+    constexpr float kNinf = -__builtin_huge_valf();
+    float4 m = make_float4(kNinf, kNinf, kNinf, kNinf), sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (c4 < N4)
+    {
+        if constexpr (GIVEN_MAX)
+        {
+            const float4 mx = reinterpret_cast<const float4*>(col_max)[c4];
+            for (size_t r = r0 + wave; r < r1; r += kWaves)
+            {
+                const float4 x = L4[r * N4 + c4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) at(sum, e) += expf(at(x, e) - at(mx, e));
+            }
+        }
+        else
+        {
+            // kGroupRows rows at a time: one rescale per group instead of a branch per element.
+            for (size_t r = r0 + wave; r < r1; r += kWaves * kGroupRows)
+            {
+                float4 x[kGroupRows];
+#pragma unroll
+                for (unsigned k = 0; k < kGroupRows; ++k)
+                {
+                    const size_t rr = r + k * kWaves;
+                    x[k] = rr < r1 ? L4[rr * N4 + c4] : make_float4(kNinf, kNinf, kNinf, kNinf);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                {
+                    float gm = at(x[0], e);
+#pragma unroll
+                    for (unsigned k = 1; k < kGroupRows; ++k) gm = fmaxf(gm, at(x[k], e));
+                    if (gm > at(m, e))
+                    {
+                        at(sum, e) *= expf(at(m, e) - gm);
+                        at(m, e) = gm;
+                    }
+                    if (at(m, e) > kNinf)
+                    {
+#pragma unroll
+                        for (unsigned k = 0; k < kGroupRows; ++k) at(sum, e) += expf(at(x[k], e) - at(m, e));
+                    }
+                }
+            }
+        }
+    }
+    sm[wave][lane] = m;
+    ss[wave][lane] = sum;
+    __syncthreads();
+    if (wave == 0 && c4 < N4)
+    {
+        for (unsigned w = 1; w < kWaves; ++w)
+        {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                if constexpr (GIVEN_MAX) at(sum, e) += at(ss[w][lane], e);
+                else merge(at(m, e), at(sum, e), at(sm[w][lane], e), at(ss[w][lane], e));
+            }
+        }
+        reinterpret_cast<float4*>(part_s + static_cast<size_t>(blockIdx.y) * N)[c4] = sum;
+        if (!GIVEN_MAX) reinterpret_cast<float4*>(part_m + static_cast<size_t>(blockIdx.y) * N)[c4] = m;
+    }
+}
+
+// Dense gradient of the sparse cross-entropy, a (rows_per_block x 256)-column
+// strip per workgroup: per-column max, scale and label held in registers.
+__global__ __launch_bounds__(kThreads) void k_ce_grad4(const float* L, const float* labels, const float* col_m,
+                                                       const float* col_s, float* grad, size_t C, size_t N,
+                                                       float inv, size_t rows_per_block)
+{
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const size_t N4 = N / 4, c4 = static_cast<size_t>(blockIdx.x) * 64 + lane;
+    if (c4 >= N4) return;
+    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_block;
+    const size_t r1 = r0 + rows_per_block < C ? r0 + rows_per_block : C;
+    const float4 m = reinterpret_cast<const float4*>(col_m)[c4], sv = reinterpret_cast<const float4*>(col_s)[c4];
+    const float4 lb = reinterpret_cast<const float4*>(labels)[c4];
+    float4 f;
+    size_t lbl[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+    {
+        // s == 0 marks an invalid column (masked or label out of range): all-zero gradient.
+        at(f, e) = at(sv, e) != 0.0f ? inv / at(sv, e) : 0.0f;
+        lbl[e] = at(sv, e) != 0.0f ? label_of(at(lb, e)) : ~size_t{0};
+    }
+    const float4* L4 = reinterpret_cast<const float4*>(L);
+    float4* G4 = reinterpret_cast<float4*>(grad);
+    for (size_t r = r0 + wave; r < r1; r += kWaves)
+    {
+        const float4 x = L4[r * N4 + c4];
+        float4 gv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+        {
+            float gg = at(f, e) * expf(at(x, e) - at(m, e));
+            if (lbl[e] == r) gg -= inv;
+            at(gv, e) = gg;
+        }
+        G4[r * N4 + c4] = gv;
+    }
+}
+
 // ── row softmax ─────────────────────────────────────────────────────────────
 constexpr unsigned kRowPer = 16;   // values per lane kept in registers: rows up to 4096 wide
 
@@ -239,6 +362,54 @@ __global__ __launch_bounds__(kThreads) void k_row_softmax_stream(const float* X,
     for (size_t c = threadIdx.x; c < cols; c += kThreads) o[c] = expf(x[c] - m) / s;
 }
 
+// One wave per row for rows of cols % 4 == 0 (16-byte aligned), cols <= 256 * NV:
+// the row sits in registers as NV float4 per lane, max and sum are wave
+// reductions, 4 rows per workgroup, no barriers.
+template <int NV>
+__global__ __launch_bounds__(kThreads) void k_row_softmax_wave(const float* X, float* out, size_t rows, size_t cols)
+{
+    const size_t row = static_cast<size_t>(blockIdx.x) * kWaves + threadIdx.x / 64;
+    if (row >= rows) return;
+    const unsigned lane = threadIdx.x % 64;
+    const size_t nq = cols / 4;
+    const float4* x = reinterpret_cast<const float4*>(X + row * cols);
+    float4* o = reinterpret_cast<float4*>(out + row * cols);
+    float4 v[NV];
+    float m = kLowest;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+    {
+        const size_t q = lane + 64 * u;
+        if (q < nq)
+        {
+            v[u] = x[q];
+            m = fmax_std(fmax_std(fmax_std(fmax_std(m, v[u].x), v[u].y), v[u].z), v[u].w);
+        }
+    }
+    m = wave_max(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+    {
+        const size_t q = lane + 64 * u;
+        if (q < nq)
+        {
+            v[u].x = expf(v[u].x - m);
+            v[u].y = expf(v[u].y - m);
+            v[u].z = expf(v[u].z - m);
+            v[u].w = expf(v[u].w - m);
+            sum += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+        }
+    }
+    sum = wave_sum(sum);
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+    {
+        const size_t q = lane + 64 * u;
+        if (q < nq) o[q] = make_float4(v[u].x / sum, v[u].y / sum, v[u].z / sum, v[u].w / sum);
+    }
+}
+
 // dx = y * (g - sum(y * g))
 __global__ __launch_bounds__(kThreads) void k_row_softmax_bwd_reg(const float* Y, const float* G, float* out,
                                                                   size_t cols)
@@ -280,10 +451,30 @@ __global__ __launch_bounds__(kThreads) void k_row_softmax_bwd_stream(const float
 
 using namespace nnhip;
 
+namespace
+{
+// Column plan of the float4 kernels: 256 columns per workgroup.
+ColPlan col_plan4(size_t C, size_t N)
+{
+    ColPlan p;
+    p.col_blocks = (N / 4 + 63) / 64;
+    size_t chunks = 2048 / (p.col_blocks ? p.col_blocks : 1);
+    const size_t max_chunks = (C + 63) / 64;   // at least 64 rows per chunk
+    if (chunks > max_chunks) chunks = max_chunks;
+    if (chunks < 1) chunks = 1;
+    p.rows_per_chunk = (C + chunks - 1) / chunks;
+    if (p.rows_per_chunk == 0) p.rows_per_chunk = 1;
+    p.chunks = (C + p.rows_per_chunk - 1) / p.rows_per_chunk;
+    return p;
+}
+bool cols4_ok(const float* L, size_t N) { return N % 4 == 0 && aligned16(L); }
+} // namespace
+
 extern "C" size_t nnhip_col_softmax_workspace_bytes(size_t C, size_t N)
 {
-    const ColPlan p = col_plan(C, N);
-    return (2 * p.chunks + 2) * N * sizeof(float);
+    const ColPlan p = col_plan(C, N), p4 = col_plan4(C, N);
+    const size_t chunks = p.chunks > p4.chunks ? p.chunks : p4.chunks;
+    return (2 * chunks + 2) * N * sizeof(float) + 256;
 }
 
 extern "C" int nnhip_col_softmax_denom(const float* logits, const float* col_max, float* out, size_t C, size_t N,
@@ -292,10 +483,15 @@ extern "C" int nnhip_col_softmax_denom(const float* logits, const float* col_max
     if (N == 0) return 0;
     if (C == 0) return nnhip_fill(out, N, 0.0f, stream);
     auto s = static_cast<hipStream_t>(stream);
-    const ColPlan p = col_plan(C, N);
+    const bool v4 = cols4_ok(logits, N) && aligned16(col_max) && aligned16(workspace) && aligned16(out);
+    const ColPlan p = v4 ? col_plan4(C, N) : col_plan(C, N);
     float* ps = static_cast<float*>(workspace);
-    hipLaunchKernelGGL(k_col_stats<true>, dim3(static_cast<unsigned>(p.col_blocks), static_cast<unsigned>(p.chunks)),
-                       dim3(kThreads), 0, s, logits, col_max, nullptr, ps, C, N, p.rows_per_chunk);
+    if (v4)
+        hipLaunchKernelGGL(k_col_stats4<true>, dim3(static_cast<unsigned>(p.col_blocks), static_cast<unsigned>(p.chunks)),
+                           dim3(kThreads), 0, s, logits, col_max, nullptr, ps, C, N, p.rows_per_chunk);
+    else
+        hipLaunchKernelGGL(k_col_stats<true>, dim3(static_cast<unsigned>(p.col_blocks), static_cast<unsigned>(p.chunks)),
+                           dim3(kThreads), 0, s, logits, col_max, nullptr, ps, C, N, p.rows_per_chunk);
     hipLaunchKernelGGL(k_col_denom_combine, dim3(grid_for(N, kThreads, 1u << 30)), dim3(kThreads), 0, s, ps, out,
                        p.chunks, N);
     return launch_status();
@@ -309,17 +505,31 @@ extern "C" int nnhip_col_softmax_sparse_forward(const float* logits, const float
     if (N == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
     if (C == 0) return nnhip_fill(loss_vec, N, 0.0f, stream);
-    const ColPlan p = col_plan(C, N);
+    const bool v4 = cols4_ok(logits, N) && aligned16(labels) && aligned16(workspace) && aligned16(grad);
+    const ColPlan p = v4 ? col_plan4(C, N) : col_plan(C, N);
     float* pm = static_cast<float*>(workspace);
     float* ps = pm + p.chunks * N;
     float* cm = ps + p.chunks * N;
     float* cs = cm + N;
-    hipLaunchKernelGGL(k_col_stats<false>, dim3(static_cast<unsigned>(p.col_blocks), static_cast<unsigned>(p.chunks)),
-                       dim3(kThreads), 0, s, logits, nullptr, pm, ps, C, N, p.rows_per_chunk);
+    if (v4)
+        hipLaunchKernelGGL(k_col_stats4<false>, dim3(static_cast<unsigned>(p.col_blocks), static_cast<unsigned>(p.chunks)),
+                           dim3(kThreads), 0, s, logits, nullptr, pm, ps, C, N, p.rows_per_chunk);
+    else
+        hipLaunchKernelGGL(k_col_stats<false>, dim3(static_cast<unsigned>(p.col_blocks), static_cast<unsigned>(p.chunks)),
+                           dim3(kThreads), 0, s, logits, nullptr, pm, ps, C, N, p.rows_per_chunk);
     hipLaunchKernelGGL(k_ce_combine, dim3(grid_for(N, kThreads, 1u << 30)), dim3(kThreads), 0, s, logits, labels, mask,
                        pm, ps, cm, cs, loss_vec, p.chunks, C, N, vocab_size);
-    hipLaunchKernelGGL(k_ce_grad, dim3(grid_for(C * N, kThreads, 256 * 64)), dim3(kThreads), 0, s, logits, labels, cm,
-                       cs, grad, C, N, inv_num_valid);
+    if (v4)
+    {
+        const size_t rows_per_block = 64, col_blocks = (N / 4 + 63) / 64;
+        const size_t row_blocks = (C + rows_per_block - 1) / rows_per_block;
+        if (row_blocks > 65535) return -3;
+        hipLaunchKernelGGL(k_ce_grad4, dim3(static_cast<unsigned>(col_blocks), static_cast<unsigned>(row_blocks)),
+                           dim3(kThreads), 0, s, logits, labels, cm, cs, grad, C, N, inv_num_valid, rows_per_block);
+    }
+    else
+        hipLaunchKernelGGL(k_ce_grad, dim3(grid_for(C * N, kThreads, 256 * 64)), dim3(kThreads), 0, s, logits, labels,
+                           cm, cs, grad, C, N, inv_num_valid);
     return launch_status();
 }
 
@@ -328,7 +538,16 @@ extern "C" int nnhip_row_softmax(const float* X, float* out, size_t rows, size_t
     if (rows == 0 || cols == 0) return 0;
     if (rows > 0x7fffffff) return -1;
     auto s = static_cast<hipStream_t>(stream);
-    if (cols <= kRowPer * kThreads)
+    if (cols % 4 == 0 && cols <= 4096 && aligned16(X) && aligned16(out))
+    {
+        const unsigned grid = static_cast<unsigned>((rows + kWaves - 1) / kWaves);
+        if (cols <= 256) hipLaunchKernelGGL(k_row_softmax_wave<1>, dim3(grid), dim3(kThreads), 0, s, X, out, rows, cols);
+        else if (cols <= 512) hipLaunchKernelGGL(k_row_softmax_wave<2>, dim3(grid), dim3(kThreads), 0, s, X, out, rows, cols);
+        else if (cols <= 1024) hipLaunchKernelGGL(k_row_softmax_wave<4>, dim3(grid), dim3(kThreads), 0, s, X, out, rows, cols);
+        else if (cols <= 2048) hipLaunchKernelGGL(k_row_softmax_wave<8>, dim3(grid), dim3(kThreads), 0, s, X, out, rows, cols);
+        else hipLaunchKernelGGL(k_row_softmax_wave<16>, dim3(grid), dim3(kThreads), 0, s, X, out, rows, cols);
+    }
+    else if (cols <= kRowPer * kThreads)
         hipLaunchKernelGGL(k_row_softmax_reg, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, X, out, cols);
     else
         hipLaunchKernelGGL(k_row_softmax_stream, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, X, out, cols);
