@@ -94,17 +94,38 @@ def gpu_leg(steps, warmup, seed):
         losses.append(g.train_step())
     eng.sync()
     elapsed = time.perf_counter() - t0
-    launches, flops, ms = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
-    eng._check(lib.nnhip_engine_profile_gemm_read(eng._e, ctypes.byref(launches), ctypes.byref(flops),
-                                                  ctypes.byref(ms)))
+    lib.nnhip_engine_profile_gemm_records.restype = ctypes.c_long
+    lib.nnhip_engine_profile_gemm_records.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double),
+                                                      ctypes.c_size_t]
+    cap = 1 << 16
+    buf = (ctypes.c_double * (7 * cap))()
+    n = lib.nnhip_engine_profile_gemm_records(eng._e, buf, cap)
+    if n < 0:
+        raise RuntimeError("GEMM profile read failed")
+    rec = np.frombuffer(buf, dtype=np.float64, count=7 * n).reshape(n, 7)
     eng._check(lib.nnhip_engine_profile_gemm(eng._e, 0))
+    by_shape = {}
+    for M, N, K, b, ta, tb, t in rec:
+        key = (int(M), int(N), int(K), int(b), int(ta), int(tb))
+        e = by_shape.setdefault(key, [0, 0.0])
+        e[0] += 1
+        e[1] += t
+    shapes = []
+    for (M, N, K, b, ta, tb), (cnt, t) in sorted(by_shape.items(), key=lambda kv: -kv[1][1]):
+        fl = 2.0 * M * N * K * b
+        shapes.append({"M": M, "N": N, "K": K, "batch": b, "transA": ta, "transB": tb,
+                       "launches_per_step": cnt / steps, "ms_per_step": t / steps,
+                       "tflops": fl / (t / cnt * 1e-3) / 1e12})
+    launches = ctypes.c_double(float(n))
+    flops = ctypes.c_double(float((2.0 * rec[:, 0] * rec[:, 1] * rec[:, 2] * rec[:, 3]).sum()))
+    ms = ctypes.c_double(float(rec[:, 6].sum()))
     print(f"[bench] timed {steps} steps in {elapsed:.3f}s, losses {[round(x, 4) for x in losses]}",
           file=sys.stderr, flush=True)
     for x in losses:
         if not math.isfinite(x):
             raise RuntimeError(f"non-finite loss {x}")
     return dict(elapsed=elapsed, gemm_launches=launches.value, gemm_flops=flops.value, gemm_ms=ms.value,
-                losses=losses)
+                losses=losses, gemm_shapes=shapes)
 
 
 class StreamTimer:
@@ -442,7 +463,8 @@ def main():
                      "frac": achieved / PEAK_FP32_MFMA_TFLOPS, "traffic": gemm_traffic_bytes(),
                      "launches": gpu["gemm_launches"], "avg_launch_ms": gemm_avg_ms,
                      "flop_per_launch": gemm_flops_per_launch,
-                     "share_of_step": gpu["gemm_ms"] / (gpu["elapsed"] * 1000.0)},
+                     "share_of_step": gpu["gemm_ms"] / (gpu["elapsed"] * 1000.0),
+                     "by_shape": gpu["gemm_shapes"]},
     }
     if attn is not None:
         out["attention"] = attn

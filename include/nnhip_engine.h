@@ -138,6 +138,9 @@ int nnhip_gpt_train_step(nnhip_gpt* g, float* loss_out);
  * then clears the record. nnhip_engine_stream returns the engine's hipStream_t. */
 int nnhip_engine_profile_gemm(nnhip_engine* e, int enable);
 int nnhip_engine_profile_gemm_read(nnhip_engine* e, double* launches, double* flops, double* ms);
+/* Per-launch records {M, N, K, batch, transA, transB, ms} (7 doubles each) of the profiled GEMMs,
+ * at most max; returns the number written (-1 on error) and clears the record. */
+long nnhip_engine_profile_gemm_records(nnhip_engine* e, double* out, size_t max);
 void* nnhip_engine_stream(nnhip_engine* e);
 /* Launches every deferred attention call (HipEngine defers the reference's two-pass attention chains
  * and runs each as one fused launch) whose results are still referenced, without waiting. */

@@ -35,6 +35,20 @@ extern "C" NN_CAPI_EXPORT int nnhip_engine_profile_gemm_read(void* e, double* la
     return r ? 0 : nn::capi::set_error(r.error().message);
 }
 
+// Per-launch records {M, N, K, batch, transA, transB, ms} of the profiled GEMMs
+// (7 doubles each); returns the number of records, at most `max`, or -1.
+extern "C" NN_CAPI_EXPORT long nnhip_engine_profile_gemm_records(void* e, double* out, size_t max)
+{
+    auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
+    if (!h) return nn::capi::set_error("profile: not a HIP engine"), -1;
+    std::vector<double> rec;
+    auto r = h->read_gemm_profile_records(rec);
+    if (!r) return nn::capi::set_error(r.error().message), -1;
+    const size_t n = std::min(rec.size() / 7, max);
+    std::copy(rec.begin(), rec.begin() + static_cast<std::ptrdiff_t>(7 * n), out);
+    return static_cast<long>(n);
+}
+
 extern "C" NN_CAPI_EXPORT void* nnhip_engine_stream(void* e)
 {
     auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());

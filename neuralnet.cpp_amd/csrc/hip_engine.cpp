@@ -334,31 +334,47 @@ void HipEngine::prof_begin_()
         (void)hipEventCreate(&e);
         return e;
     };
-    ProfRecord r{take(), take(), 0.0};
+    ProfRecord r{take(), take(), 0.0, {}};
     (void)hipEventRecord(static_cast<hipEvent_t>(r.start), static_cast<hipStream_t>(stream_));
     prof_.push_back(r);
 }
 
-void HipEngine::prof_end_(double flops)
+void HipEngine::prof_end_(std::size_t M, std::size_t N, std::size_t K, std::size_t batch, bool tA, bool tB)
 {
     if (!profile_ || prof_.empty()) return;
-    prof_.back().flops = flops;
-    (void)hipEventRecord(static_cast<hipEvent_t>(prof_.back().stop), static_cast<hipStream_t>(stream_));
+    ProfRecord& r = prof_.back();
+    r.flops = 2.0 * double(batch) * double(M) * double(N) * double(K);
+    const double shape[6] = {double(M), double(N), double(K), double(batch), tA ? 1.0 : 0.0, tB ? 1.0 : 0.0};
+    std::copy(shape, shape + 6, r.shape);
+    (void)hipEventRecord(static_cast<hipEvent_t>(r.stop), static_cast<hipStream_t>(stream_));
 }
 
 Result<void> HipEngine::read_gemm_profile(double& launches, double& flops, double& ms)
 {
-    NN_CHECK(end_batch());
-    launches = static_cast<double>(prof_.size());
+    std::vector<double> rec;
+    NN_CHECK(read_gemm_profile_records(rec));
+    launches = static_cast<double>(rec.size() / 7);
     flops = 0.0;
     ms = 0.0;
+    for (std::size_t i = 0; i + 7 <= rec.size(); i += 7)
+    {
+        flops += 2.0 * rec[i] * rec[i + 1] * rec[i + 2] * rec[i + 3];
+        ms += rec[i + 6];
+    }
+    return {};
+}
+
+Result<void> HipEngine::read_gemm_profile_records(std::vector<double>& records)
+{
+    NN_CHECK(end_batch());
+    records.clear();
     for (auto& r : prof_)
     {
         float t = 0.0f;
         if (hipEventElapsedTime(&t, static_cast<hipEvent_t>(r.start), static_cast<hipEvent_t>(r.stop)) != hipSuccess)
             return fail("read_gemm_profile: event timing failed");
-        ms += t;
-        flops += r.flops;
+        records.insert(records.end(), r.shape, r.shape + 6);
+        records.push_back(t);
         event_pool_.push_back(r.start);
         event_pool_.push_back(r.stop);
     }
@@ -684,7 +700,7 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
     prof_begin_();
     const int rc = nnhip_gemm(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), 1, tA, tB, 1.0f,
                               ws ? ws->data() : nullptr, wsb, stream_);
-    prof_end_(2.0 * double(M) * double(N) * double(K));
+    prof_end_(M, N, K, 1, tA, tB);
     NN_CHECK(kernel_(rc, "matmul"));
     return C;
 }
@@ -702,7 +718,7 @@ Result<void> HipEngine::launch_gemm_(const Tensor& A, const Tensor& B, Tensor& C
     prof_begin_();
     const int rc = nnhip_gemm(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), batch, tA, tB, alpha,
                               ws ? ws->data() : nullptr, wsb, stream_);
-    prof_end_(2.0 * double(batch) * double(M) * double(N) * double(K));
+    prof_end_(M, N, K, batch, tA, tB);
     return kernel_(rc, "batched_matmul");
 }
 

@@ -7,8 +7,8 @@
 // global->LDS staging step: both operands are kept k-major in LDS
 // (As[k][m], Bs[k][n]) so every MFMA fragment read is 32 consecutive floats.
 //
-// Tiling: a workgroup of WM x WN waves owns a (64*WM) x (64*WN) tile of C;
-// each wave owns 64x64 = 2x2 MFMA 32x32 blocks (64 accumulators per lane).
+// Tiling: a workgroup of WM x WN waves owns a (32*FM*WM) x (32*FN*WN) tile of
+// C; each wave owns FM x FN MFMA 32x32 blocks (64 x 64 or 32 x 64).
 // K advances 16 at a time through two LDS buffers: the next stage's global
 // loads are issued into registers before the current stage's MFMAs and
 // written to the other buffer afterwards (one barrier per stage). Tile ids are
@@ -280,52 +280,68 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 }
 
 // Launch plan for one GEMM: tile configuration and split-K factor.
-enum Cfg { kTall = 0, kSquare = 1, kSkinnyM = 2, kSkinnyN = 3 };
+enum Cfg { kTall, kSquare, kSkinnyN, kThinWaves, kThinWavesM64 };
 struct Plan
 {
     Cfg cfg;
     int bm, bn, splits, k_split;
 };
 
-// Tile choice, from a sweep of the config-4 shapes on MI355X:
-//   * M <= 64 (attention PV / dV / dQ / dK): 64 x 256 tiles;
+// Tile choice, from sweeps of the config-3 and config-4 shapes on MI355X.
+// The work is balanced over the 1024 SIMDs first: a 768 x 8192 output makes
+// only 192 tiles of 256 x 128, and any tiling with 64 x 64 per wave leaves
+// either idle CUs or 1.5 waves per SIMD; 32 x 64 per wave (128 x 64 tiles of
+// 4 waves: 768 workgroups, 3 waves on every SIMD) took those products from
+// 69-80 to 87-98 TF/s and the 64-row attention products from 48-61 to 70-85.
+//   * M <= 64: 64 x 128 tiles of 4 waves with 32 x 64 each;
 //   * N <= 64: 256 x 64;
-//   * M >= 256: 256 x 128 tiles over 8 waves (best on every large shape);
-//   * otherwise 128 x 128.
-// When the tile grid cannot fill the 256 CUs and K is long (the weight
-// gradients dW = G X^T, K = tokens), K is split into slices whose partial
-// tiles are summed in order by k_splitk_reduce.
+//   * at least 512 tiles of 256 x 128: 256 x 128 over 8 waves;
+//   * K >= 4096 with a workspace: 256 x 128 (128 x 128 below 128 tiles) with
+//     K split into slices (weight gradients, K = tokens: measured faster than
+//     the thin tiles there);
+//   * otherwise 128 x 64 tiles of 4 waves with 32 x 64 each, K split when the
+//     grid is small and K >= 1024.
+// Split K: slices of >= 256 k for about three workgroups per CU, partial
+// tiles summed in slice order by k_splitk_reduce (deterministic).
 Plan plan_gemm(size_t M, size_t N, size_t K, size_t batch, bool allow_split)
 {
     Plan p;
-    if (M <= 64) { p.cfg = kSkinnyM; p.bm = 64; p.bn = 256; }
-    else if (N <= 64) { p.cfg = kSkinnyN; p.bm = 256; p.bn = 64; }
-    else if (M >= 256) { p.cfg = kTall; p.bm = 256; p.bn = 128; }
-    else { p.cfg = kSquare; p.bm = 128; p.bn = 128; }
     p.splits = 1;
     p.k_split = static_cast<int>(K);
-    const size_t tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn) * batch;
-    if (allow_split && tiles < 256 && K >= 1024)
-    {
-        if (p.cfg == kTall && tiles < 128)
-        {
-            p.cfg = kSquare;
-            p.bm = 128;
-            p.bn = 128;
-        }
-        const size_t t2 = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn) * batch;
-        size_t want = (768 + t2 - 1) / t2;                 // aim for ~3 workgroups per CU
-        const size_t max_splits = K / 256;                 // keep >= 256 k per slice
+    auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+    auto split = [&](size_t t) {
+        size_t want = (768 + t - 1) / t;
+        const size_t max_splits = K / 256;
         if (want > max_splits) want = max_splits;
         if (want > 64) want = 64;
         if (want > 1)
         {
             size_t ks = (K + want - 1) / want;
-            ks = (ks + 15) / 16 * 16;                      // whole BK stages per slice
+            ks = (ks + 15) / 16 * 16;   // whole BK stages per slice
             p.k_split = static_cast<int>(ks);
             p.splits = static_cast<int>((K + ks - 1) / ks);
         }
+    };
+    if (M <= 64) { p.cfg = kThinWavesM64; p.bm = 64; p.bn = 128; }
+    else if (N <= 64) { p.cfg = kSkinnyN; p.bm = 256; p.bn = 64; }
+    else if (tiles(256, 128) >= 512) { p.cfg = kTall; p.bm = 256; p.bn = 128; }
+    else if (allow_split && K >= 4096)
+    {
+        p.cfg = kTall;
+        p.bm = 256;
+        p.bn = 128;
+        if (tiles(256, 128) < 128)
+        {
+            p.cfg = kSquare;
+            p.bm = 128;
+            p.bn = 128;
+        }
+        split(tiles(p.bm, p.bn));
+        return p;
     }
+    else { p.cfg = kThinWaves; p.bm = 128; p.bn = 64; }
+    const size_t t = tiles(p.bm, p.bn);
+    if (allow_split && t < 512 && K >= 1024) split(t);
     return p;
 }
 
@@ -354,12 +370,16 @@ void launch_trans(const Plan& p, const float* A, const float* B, float* C, int M
                         aligned16(B);
     switch (p.cfg)
     {
-    case kSkinnyM:
-        launch_cfg<1, 4, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
-                                           p.k_split, part, s);
-        break;
     case kSkinnyN:
         launch_cfg<4, 1, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
+                                           p.k_split, part, s);
+        break;
+    case kThinWaves:
+        launch_cfg<4, 1, 1, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
+                                           p.k_split, part, s);
+        break;
+    case kThinWavesM64:
+        launch_cfg<2, 2, 1, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
                                            p.k_split, part, s);
         break;
     case kTall:

@@ -136,6 +136,8 @@ public:
     // kernel time in milliseconds, then clears the record.
     void set_gemm_profile(bool on);
     Result<void> read_gemm_profile(double& launches, double& flops, double& ms);
+    // Same, plus one record per launch: {M, N, K, batch, transA, transB, ms}.
+    Result<void> read_gemm_profile_records(std::vector<double>& records);
 
 private:
     Result<Tensor> alloc_(std::size_t rows, std::size_t cols);
@@ -178,13 +180,14 @@ private:
                               std::size_t cols, bool vector_out);
 
     void prof_begin_();
-    void prof_end_(double flops);
+    void prof_end_(std::size_t M, std::size_t N, std::size_t K, std::size_t batch, bool tA, bool tB);
 
     struct ProfRecord
     {
         void* start;
         void* stop;
         double flops;
+        double shape[6];   // M, N, K, batch, transA, transB
     };
     bool profile_ = false;
     std::vector<ProfRecord> prof_;

@@ -41,9 +41,23 @@ def test_matmul(hip, cpu, M, N, K, tA, tB):
     assert np.all(np.abs(h - ref) <= 2 * K * 2.0 ** -24 * absprod + 1e-30)
 
 
+@pytest.mark.parametrize("tA,tB", [(False, False), (True, False), (False, True)])
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 64), (1000, 64, 100), (1024, 48, 200)])
+def test_matmul_large_tiles(hip, cpu, M, N, K, tA, tB):
+    """Output grids of >= 512 tiles of 256 x 128 (the 8-wave configuration) and N <= 64 (256 x 64)."""
+    rng = np.random.default_rng(M + 7 * N + K)
+    A = uniform(rng, (K, M) if tA else (M, K))
+    B = uniform(rng, (N, K) if tB else (K, N))
+    h = hip.matmul(hip.tensor(A), hip.tensor(B), tA, tB).numpy()
+    ref = (A.T if tA else A).astype(np.float64) @ (B.T if tB else B).astype(np.float64)
+    absprod = np.abs(A.T if tA else A).astype(np.float64) @ np.abs(B.T if tB else B).astype(np.float64)
+    assert nrm_err(h, ref) <= 1e-5
+    assert np.all(np.abs(h - ref) <= 2 * K * 2.0 ** -24 * absprod + 1e-30)
+
+
 @pytest.mark.parametrize("tA,tB", [(False, True), (True, False), (False, False)])
 @pytest.mark.parametrize("M,N,K,batch", [(96, 128, 4096, 1), (768, 768, 2048, 1), (50, 70, 3001, 1),
-                                         (100, 100, 2048, 2), (300, 200, 1500, 1)])
+                                         (100, 100, 2048, 2), (300, 200, 1500, 1), (768, 1024, 4096, 1)])
 def test_matmul_split_k(hip, cpu, M, N, K, batch, tA, tB):
     """Small output grids with long K take the split-K path (partials summed in slice order)."""
     rng = np.random.default_rng(M + N + K)
