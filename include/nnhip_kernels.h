@@ -57,6 +57,15 @@ int nnhip_elementwise_binary_scalar(const float* A, float* out, size_t count, un
 int nnhip_axpy(const float* A, const float* B, float* out, size_t count, float scalar, void* stream);
 int nnhip_elementwise_select_scalar_cond(const float* A, const float* then_v, float* out, size_t count,
                                          unsigned cmp, float scalar_b, float scalar_else, void* stream);
+/* One Adam / AdamW update of a parameter tensor in one pass, rounding every step exactly as the
+ * reference's chain of engine primitives does (compute_optimizer.hpp:252-304; AdamW's decay
+ * scale_inplace(p, 1 - lr*wd), :388-412, when has_decay): m = m*beta1; m = fma(1-beta1, g, m);
+ * v = v*beta2 + (g*g)*(1-beta2); p = p*decay + (-lr) * ((m*inv_bc1) / (sqrt(v*inv_bc2) + eps)).
+ * p, m, v updated in place; g read only. The CUDA backend has no counterpart (it runs the
+ * primitive chain); HipEngine issues this when it recognises that chain among deferred calls. */
+int nnhip_adam_update(float* p, float* m, float* v, const float* g, size_t count, int has_decay, float decay,
+                      float beta1, float one_minus_beta1, float beta2, float one_minus_beta2, float inv_bc1,
+                      float inv_bc2, float eps, float neg_lr, void* stream);
 /* out[i] = value (used for ComputeEngine::zero; no CUDA counterpart, CUDA uses cudaMemset). */
 int nnhip_fill(float* out, size_t count, float value, void* stream);
 

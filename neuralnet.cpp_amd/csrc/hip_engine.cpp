@@ -134,7 +134,7 @@ private:
 };
 
 const float* D(const Tensor& t) { return t.dev_ptr(); }
-float* W(Tensor& t) { return t.dev_ptr(); }
+float* W(const Tensor& t) { return t.dev_ptr(); }
 
 struct BDims
 {
@@ -282,6 +282,77 @@ struct HipEngine::PendingBwd
     bool yields(const float* p) const { return has_buf(dQ, p) || has_buf(R, p); }
 };
 
+namespace
+{
+enum EwCode : std::uint8_t { kBin, kScalar, kUnary, kAxpy, kCopy };
+}
+
+// Consecutive same-size elementwise calls (scale / axpy / add in place; unary,
+// binary, scalar and clone into new tensors), recorded in call order. Slots
+// are the distinct buffers the calls touch; every result is a real allocation
+// that the record keeps alive until it runs.
+struct HipEngine::PendingEw
+{
+    struct Op
+    {
+        EwCode code;
+        std::uint8_t op, first;
+        std::uint8_t dst, a, b;   // slots; b is read by kBin and kAxpy only
+        float s;
+    };
+    static constexpr std::size_t kMaxOps = 96, kMaxSlots = 64;
+    std::size_t n = 0;   // elements of every tensor in the record
+    std::vector<Tensor> slots;
+    std::vector<Op> ops;
+
+    std::uint8_t slot(const Tensor& t)
+    {
+        for (std::size_t i = 0; i < slots.size(); ++i)
+            if (slots[i].dev_ptr() == t.dev_ptr()) return static_cast<std::uint8_t>(i);
+        slots.push_back(t);
+        return static_cast<std::uint8_t>(slots.size() - 1);
+    }
+    bool full() const { return ops.size() >= kMaxOps || slots.size() + 3 > kMaxSlots; }
+    static bool reads_b(const Op& o) { return o.code == kBin || o.code == kAxpy; }
+};
+
+namespace
+{
+
+// The Adam update chain of one parameter tensor as the optimizer issues it
+// (reference compute_optimizer.hpp:252-304): the tensors it touches, by role,
+// and its calls in order. AdamW (:388-412) puts scale_inplace(p, decay) first.
+enum AdamRole { rP, rM, rG, rV, rG2, rMH, rVH, rSQ, rDEN, rR, kAdamRoles };
+struct AdamStep
+{
+    EwCode code;
+    unsigned op;
+    int dst, a, b;   // roles; b < 0: not read
+};
+constexpr unsigned kMul = static_cast<unsigned>(BinaryOp::Mul), kAdd = static_cast<unsigned>(BinaryOp::Add),
+                   kDiv = static_cast<unsigned>(BinaryOp::Div), kSqrt = static_cast<unsigned>(UnaryOp::Sqrt);
+constexpr AdamStep kAdamDecay = {kScalar, kMul, rP, rP, -1};
+constexpr AdamStep kAdamSteps[] = {
+    {kScalar, kMul, rM, rM, -1},      // m *= beta1
+    {kAxpy, 0, rM, rM, rG},           // m += (1 - beta1) g
+    {kScalar, kMul, rV, rV, -1},      // v *= beta2
+    {kBin, kMul, rG2, rG, rG},        // g2 = g * g
+    {kScalar, kMul, rG2, rG2, -1},    // g2 *= 1 - beta2
+    {kBin, kAdd, rV, rV, rG2},        // v += g2
+    {kCopy, 0, rMH, rM, -1},          // m_hat = clone(m)
+    {kScalar, kMul, rMH, rMH, -1},    // m_hat *= inv_bc1
+    {kCopy, 0, rVH, rV, -1},          // v_hat = clone(v)
+    {kScalar, kMul, rVH, rVH, -1},    // v_hat *= inv_bc2
+    {kUnary, kSqrt, rSQ, rVH, -1},    // sq = sqrt(v_hat)
+    {kScalar, kAdd, rDEN, rSQ, -1},   // den = sq + eps
+    {kBin, kDiv, rR, rMH, rDEN},      // ratio = m_hat / den
+    {kScalar, kMul, rR, rR, -1},      // ratio *= -lr
+    {kBin, kAdd, rP, rP, rR},         // p += ratio
+};
+constexpr std::size_t kAdamLen = sizeof(kAdamSteps) / sizeof(kAdamSteps[0]);
+
+} // namespace
+
 HipEngine::HipEngine()
 {
     if (hipGetDevice(&device_) != hipSuccess)
@@ -411,6 +482,12 @@ Result<void> HipEngine::need_gpu_(std::initializer_list<const Tensor*> ts, const
 // ── deferred work: launch on demand ─────────────────────────────────────────
 Result<void> HipEngine::settle_reads_(std::initializer_list<const Tensor*> ts)
 {
+    NN_CHECK(settle_ew_());
+    return settle_chain_reads_(ts);
+}
+
+Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*> ts)
+{
     for (const Tensor* t : ts)
     {
         if (!t) continue;
@@ -444,6 +521,12 @@ Result<const void*> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, st
 
 Result<void> HipEngine::settle_write_(const Tensor& t)
 {
+    NN_CHECK(settle_ew_());
+    return settle_chain_write_(t);
+}
+
+Result<void> HipEngine::settle_chain_write_(const Tensor& t)
+{
     const float* p = t.dev_ptr();
     if (!p) return {};
     for (std::size_t i = cells_.size(); i-- > 0;)
@@ -460,6 +543,7 @@ Result<void> HipEngine::settle_write_(const Tensor& t)
 
 Result<void> HipEngine::settle()
 {
+    NN_CHECK(settle_ew_());
     NN_CHECK(settle_bwd_());
     NN_CHECK(settle_gemm_());
     return settle_fwd_();
@@ -508,6 +592,129 @@ Result<void> HipEngine::settle_bwd_()
                                                 q->mask ? D(*q->mask) : nullptr, W(q->dQ), W(q->R), q->batch, q->M,
                                                 q->N, q->Kd, 1, 0, q->alpha, ws ? ws->data() : nullptr, stream_),
                    "batched_matmul_softmax_backward_q");
+}
+
+// ── deferred elementwise runs ───────────────────────────────────────────────
+// Records one call; a record of another size, or a full one, is launched first.
+// The caller has checked shapes and launched deferred attention work that
+// yields or reads the tensors involved.
+Result<void> HipEngine::ew_push_(unsigned code, unsigned op, bool first, const Tensor& dst, const Tensor& a,
+                                 const Tensor* b, float s)
+{
+    const std::size_t n = dst.size();
+    if (pew_ && (pew_->n != n || pew_->full())) NN_CHECK(settle_ew_());
+    if (!pew_)
+    {
+        pew_ = std::make_unique<PendingEw>();
+        pew_->n = n;
+    }
+    PendingEw::Op o{};
+    o.code = static_cast<EwCode>(code);
+    o.op = static_cast<std::uint8_t>(op);
+    o.first = first ? 1 : 0;
+    o.s = s;
+    o.a = pew_->slot(a);
+    o.b = b ? pew_->slot(*b) : o.a;
+    o.dst = pew_->slot(dst);
+    pew_->ops.push_back(o);
+    return {};
+}
+
+// Launches the recorded calls in order: every Adam / AdamW update chain as one
+// nnhip_adam_update pass, any other call with its own kernel. A call is
+// skipped when its result is referenced by nobody and read by no later call.
+Result<void> HipEngine::settle_ew_()
+{
+    if (!pew_) return {};
+    std::unique_ptr<PendingEw> g = std::move(pew_);
+    const auto& ops = g->ops;
+    std::vector<std::ptrdiff_t> last_read(g->slots.size(), -1);
+    for (std::size_t i = 0; i < ops.size(); ++i)
+    {
+        last_read[ops[i].a] = static_cast<std::ptrdiff_t>(i);
+        if (PendingEw::reads_b(ops[i])) last_read[ops[i].b] = static_cast<std::ptrdiff_t>(i);
+    }
+    const auto st = static_cast<hipStream_t>(stream_);
+    const std::size_t n = g->n;
+    for (std::size_t i = 0; i < ops.size();)
+    {
+        NN_TRY(k, adam_run_(*g, i, last_read));
+        if (k)
+        {
+            i += k;
+            continue;
+        }
+        const auto& o = ops[i];
+        const Tensor& dst = g->slots[o.dst];
+        if (live(dst) || last_read[o.dst] > static_cast<std::ptrdiff_t>(i))
+        {
+            const float* a = D(g->slots[o.a]);
+            const float* b = D(g->slots[o.b]);
+            float* out = W(dst);
+            switch (o.code)
+            {
+            case kBin: NN_CHECK(kernel_(nnhip_elementwise_binary(a, b, out, n, o.op, st), "elementwise_binary")); break;
+            case kScalar:
+                NN_CHECK(kernel_(nnhip_elementwise_binary_scalar(a, out, n, o.op, o.s, o.first, st),
+                                 "elementwise_binary_scalar"));
+                break;
+            case kUnary: NN_CHECK(kernel_(nnhip_elementwise_unary(a, out, n, o.op, st), "elementwise_unary")); break;
+            case kAxpy: NN_CHECK(kernel_(nnhip_axpy(a, b, out, n, o.s, st), "axpy_inplace")); break;
+            case kCopy:
+                if (hipMemcpyAsync(out, a, n * sizeof(float), hipMemcpyDeviceToDevice, st) != hipSuccess)
+                    return fail("clone: device copy failed");
+                break;
+            }
+        }
+        ++i;
+    }
+    return {};
+}
+
+// If calls i.. of the record are an Adam(W) update chain whose temporaries
+// nobody keeps, launches it as one pass and returns its length; else 0.
+Result<std::size_t> HipEngine::adam_run_(const PendingEw& g, std::size_t i,
+                                         const std::vector<std::ptrdiff_t>& last_read)
+{
+    const auto& ops = g.ops;
+    for (int decay = 1; decay >= 0; --decay)
+    {
+        const std::size_t len = kAdamLen + static_cast<std::size_t>(decay);
+        if (i + len > ops.size()) continue;
+        int slot_of[kAdamRoles];
+        std::fill(std::begin(slot_of), std::end(slot_of), -1);
+        std::vector<int> role_of(g.slots.size(), -1);
+        auto bind = [&](int role, int slot) {
+            if (slot_of[role] < 0 && role_of[slot] < 0)
+            {
+                slot_of[role] = slot;
+                role_of[slot] = role;
+                return true;
+            }
+            return slot_of[role] == slot;
+        };
+        bool ok = true;
+        for (std::size_t j = 0; ok && j < len; ++j)
+        {
+            const AdamStep& st = decay ? (j == 0 ? kAdamDecay : kAdamSteps[j - 1]) : kAdamSteps[j];
+            const PendingEw::Op& o = ops[i + j];
+            ok = o.code == st.code && o.op == st.op && o.first == 0 && bind(st.a, o.a) &&
+                 (st.b < 0 || bind(st.b, o.b)) && bind(st.dst, o.dst);
+        }
+        if (!ok) continue;
+        for (int r = rG2; ok && r <= rR; ++r)
+            ok = !live(g.slots[slot_of[r]]) && last_read[slot_of[r]] < static_cast<std::ptrdiff_t>(i + len);
+        if (!ok) continue;
+        const PendingEw::Op* c = &ops[i + static_cast<std::size_t>(decay)];   // the first call after the decay
+        const float decay_f = decay ? ops[i].s : 1.0f;
+        NN_CHECK(kernel_(nnhip_adam_update(W(g.slots[slot_of[rP]]), W(g.slots[slot_of[rM]]),
+                                           W(g.slots[slot_of[rV]]), D(g.slots[slot_of[rG]]), g.n, decay, decay_f,
+                                           c[0].s, c[1].s, c[2].s, c[4].s, c[7].s, c[9].s, c[11].s, c[13].s,
+                                           static_cast<hipStream_t>(stream_)),
+                         "adam update"));
+        return len;
+    }
+    return std::size_t{0};
 }
 
 Result<Tensor> HipEngine::alloc_(std::size_t rows, std::size_t cols)
@@ -605,12 +812,10 @@ Result<void> HipEngine::copy_from(Tensor& dst, const Matrix& src)
 
 Result<Tensor> HipEngine::clone(const Tensor& src)
 {
-    NN_CHECK(need_gpu_({&src}, "clone"));
+    NN_CHECK(check_gpu_({&src}, "clone"));
+    NN_CHECK(settle_chain_reads_({&src}));
     NN_TRY(t, alloc_(src.rows(), src.cols()));
-    if (src.size() &&
-        hipMemcpyAsync(W(t), D(src), src.size() * sizeof(float), hipMemcpyDeviceToDevice,
-                       static_cast<hipStream_t>(stream_)) != hipSuccess)
-        return fail("clone: device copy failed");
+    if (src.size()) NN_CHECK(ew_push_(kCopy, 0, false, t, src, nullptr, 0.0f));
     return t;
 }
 
@@ -947,27 +1152,34 @@ Result<Tensor> HipEngine::col_softmax_sparse_forward(const Tensor& logits, const
 }
 
 // ── in-place ops (cpu_engine.hpp:1008-1044) ─────────────────────────────────
+// In-place and elementwise calls are recorded (see PendingEw) and run
+// together when any other kind of call arrives.
 Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
 {
-    NN_CHECK(need_gpu_({&A, &B}, "add_inplace"));
-    NN_CHECK(settle_write_(A));
+    NN_CHECK(check_gpu_({&A, &B}, "add_inplace"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("add_inplace: shape mismatch");
-    return kernel_(nnhip_elementwise_binary(D(A), D(B), W(A), A.size(), 0u, stream_), "add_inplace");
+    if (!A.size()) return {};
+    NN_CHECK(settle_chain_reads_({&B}));
+    NN_CHECK(settle_chain_write_(A));
+    return ew_push_(kBin, static_cast<unsigned>(BinaryOp::Add), false, A, A, &B, 0.0f);
 }
 
 Result<void> HipEngine::scale_inplace(Tensor& A, Scalar s)
 {
-    NN_CHECK(need_gpu_({&A}, "scale_inplace"));
-    NN_CHECK(settle_write_(A));
-    return kernel_(nnhip_elementwise_binary_scalar(D(A), W(A), A.size(), 2u, s, 0, stream_), "scale_inplace");
+    NN_CHECK(check_gpu_({&A}, "scale_inplace"));
+    if (!A.size()) return {};
+    NN_CHECK(settle_chain_write_(A));
+    return ew_push_(kScalar, static_cast<unsigned>(BinaryOp::Mul), false, A, A, nullptr, s);
 }
 
 Result<void> HipEngine::axpy_inplace(Tensor& A, Scalar s, const Tensor& B)
 {
-    NN_CHECK(need_gpu_({&A, &B}, "axpy_inplace"));
-    NN_CHECK(settle_write_(A));
+    NN_CHECK(check_gpu_({&A, &B}, "axpy_inplace"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("axpy_inplace: shape mismatch");
-    return kernel_(nnhip_axpy(D(A), D(B), W(A), A.size(), s, stream_), "axpy_inplace");
+    if (!A.size()) return {};
+    NN_CHECK(settle_chain_reads_({&B}));
+    NN_CHECK(settle_chain_write_(A));
+    return ew_push_(kAxpy, 0, false, A, A, &B, s);
 }
 
 Result<void> HipEngine::zero(Tensor& A)
@@ -1030,28 +1242,31 @@ Result<void> HipEngine::broadcast_col_inplace(Tensor& A, const Tensor& v, Binary
 // ── elementwise (cpu_engine.hpp:1131-1266) ──────────────────────────────────
 Result<Tensor> HipEngine::elementwise_unary(UnaryOp op, const Tensor& A)
 {
-    NN_CHECK(need_gpu_({&A}, "elementwise_unary"));
+    NN_CHECK(check_gpu_({&A}, "elementwise_unary"));
+    if (static_cast<unsigned>(op) > static_cast<unsigned>(UnaryOp::Tanh)) return fail("elementwise_unary: bad op");
+    NN_CHECK(settle_chain_reads_({&A}));
     NN_TRY(o, alloc_(A.rows(), A.cols()));
-    NN_CHECK(kernel_(nnhip_elementwise_unary(D(A), W(o), A.size(), static_cast<unsigned>(op), stream_),
-                     "elementwise_unary"));
+    if (A.size()) NN_CHECK(ew_push_(kUnary, static_cast<unsigned>(op), false, o, A, nullptr, 0.0f));
     return o;
 }
 Result<Tensor> HipEngine::elementwise_binary(BinaryOp op, const Tensor& A, const Tensor& B)
 {
-    NN_CHECK(need_gpu_({&A, &B}, "elementwise_binary"));
+    NN_CHECK(check_gpu_({&A, &B}, "elementwise_binary"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("elementwise_binary: shape mismatch");
+    if (static_cast<unsigned>(op) > static_cast<unsigned>(BinaryOp::Min)) return fail("elementwise_binary: bad op");
+    NN_CHECK(settle_chain_reads_({&A, &B}));
     NN_TRY(o, alloc_(A.rows(), A.cols()));
-    NN_CHECK(kernel_(nnhip_elementwise_binary(D(A), D(B), W(o), A.size(), static_cast<unsigned>(op), stream_),
-                     "elementwise_binary"));
+    if (A.size()) NN_CHECK(ew_push_(kBin, static_cast<unsigned>(op), false, o, A, &B, 0.0f));
     return o;
 }
 Result<Tensor> HipEngine::elementwise_binary_scalar(BinaryOp op, const Tensor& A, Scalar s, bool first)
 {
-    NN_CHECK(need_gpu_({&A}, "elementwise_binary_scalar"));
+    NN_CHECK(check_gpu_({&A}, "elementwise_binary_scalar"));
+    if (static_cast<unsigned>(op) > static_cast<unsigned>(BinaryOp::Min))
+        return fail("elementwise_binary_scalar: bad op");
+    NN_CHECK(settle_chain_reads_({&A}));
     NN_TRY(o, alloc_(A.rows(), A.cols()));
-    NN_CHECK(kernel_(nnhip_elementwise_binary_scalar(D(A), W(o), A.size(), static_cast<unsigned>(op), s, first ? 1 : 0,
-                                                     stream_),
-                     "elementwise_binary_scalar"));
+    if (A.size()) NN_CHECK(ew_push_(kScalar, static_cast<unsigned>(op), first, o, A, nullptr, s));
     return o;
 }
 Result<Tensor> HipEngine::elementwise_select_scalar_cond(CompareOp cmp, const Tensor& A, Scalar sb,

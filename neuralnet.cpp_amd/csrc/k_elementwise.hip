@@ -30,10 +30,12 @@ struct ScalarF
     int first;
     __device__ float operator()(float a, float) const { return first ? binary_op(op, s, a) : binary_op(op, a, s); }
 };
+// One rounding (fused multiply-add), spelled out so that k_adam's axpy step
+// rounds identically.
 struct AxpyF
 {
     float s;
-    __device__ float operator()(float a, float b) const { return a + s * b; }
+    __device__ float operator()(float a, float b) const { return __builtin_fmaf(s, b, a); }
 };
 struct SelectF
 {
@@ -152,10 +154,99 @@ int launch_broadcast(const float* A, const float* v, float* out, size_t rows, si
     return launch_status();
 }
 
+// The Adam(W) per-tensor chain of engine primitives (reference
+// compute_optimizer.hpp:252-304, AdamW decay :388-412) in one pass: p, m, v
+// read and written once, g read once, 28 bytes per element. Every step is
+// rounded exactly as its separate primitive kernel rounds it (k_map with
+// ScalarF / AxpyF / BinaryF / UnaryF), in the same order, so the fused and
+// unfused chains agree bit for bit; contraction into FMAs is switched off for
+// that reason.
+struct AdamArgs
+{
+    float decay, b1, c1, b2, c2, ib1, ib2, eps, neg_lr;
+    int has_decay;
+};
+
+__device__ __forceinline__ void adam_elem(float& p, float& m, float& v, float g, const AdamArgs& a)
+{
+#pragma clang fp contract(off)
+    float pp = a.has_decay ? p * a.decay : p;   // scale_inplace(p, 1 - lr*wd)
+    float mm = m * a.b1;                        // scale_inplace(m, b1)
+    mm = __builtin_fmaf(a.c1, g, mm);           // axpy_inplace(m, 1 - b1, g)
+    float vv = v * a.b2;                        // scale_inplace(v, b2)
+    float g2 = g * g;                           // g2 = g * g
+    g2 = g2 * a.c2;                             // scale_inplace(g2, 1 - b2)
+    vv = vv + g2;                               // add_inplace(v, g2)
+    const float mh = mm * a.ib1;                // m_hat = clone(m) * inv_bc1
+    const float vh = vv * a.ib2;                // v_hat = clone(v) * inv_bc2
+    const float den = sqrtf(vh) + a.eps;        // sqrt(v_hat) + eps
+    float r = mh / den;                         // m_hat / den
+    r = r * a.neg_lr;                           // scale_inplace(ratio, -lr)
+    p = pp + r;                                 // add_inplace(p, ratio)
+    m = mm;
+    v = vv;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void k_adam(float* p, float* m, float* v, const float* g, size_t n, AdamArgs a)
+{
+    const size_t tid = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+    size_t done = 0;
+    if constexpr (VEC)
+    {
+        const size_t n4 = n / 4;
+        float4* p4 = reinterpret_cast<float4*>(p);
+        float4* m4 = reinterpret_cast<float4*>(m);
+        float4* v4 = reinterpret_cast<float4*>(v);
+        const float4* g4 = reinterpret_cast<const float4*>(g);
+        for (size_t i = tid; i < n4; i += stride)
+        {
+            float4 pp = p4[i], mm = m4[i], vv = v4[i];
+            const float4 gg = g4[i];
+            adam_elem(pp.x, mm.x, vv.x, gg.x, a);
+            adam_elem(pp.y, mm.y, vv.y, gg.y, a);
+            adam_elem(pp.z, mm.z, vv.z, gg.z, a);
+            adam_elem(pp.w, mm.w, vv.w, gg.w, a);
+            p4[i] = pp;
+            m4[i] = mm;
+            v4[i] = vv;
+        }
+        done = n4 * 4;
+    }
+    for (size_t i = done + tid; i < n; i += stride)
+    {
+        float pp = p[i], mm = m[i], vv = v[i];
+        adam_elem(pp, mm, vv, g[i], a);
+        p[i] = pp;
+        m[i] = mm;
+        v[i] = vv;
+    }
+}
+
 } // namespace
 } // namespace nnhip
 
 using namespace nnhip;
+
+extern "C" int nnhip_adam_update(float* p, float* m, float* v, const float* g, size_t count, int has_decay,
+                                 float decay, float beta1, float one_minus_beta1, float beta2, float one_minus_beta2,
+                                 float inv_bc1, float inv_bc2, float eps, float neg_lr, void* stream)
+{
+    if (count == 0) return 0;
+    if (!p || !m || !v || !g) return -1;
+    const AdamArgs a{decay, beta1, one_minus_beta1, beta2, one_minus_beta2, inv_bc1, inv_bc2, eps, neg_lr,
+                     has_decay ? 1 : 0};
+    const bool vec = aligned16(p) && aligned16(m) && aligned16(v) && aligned16(g);
+    const size_t work = vec ? (count + 3) / 4 : count;
+    const unsigned grid = grid_for(work, kThreads, 256 * 32);
+    auto s = static_cast<hipStream_t>(stream);
+    if (vec)
+        hipLaunchKernelGGL(k_adam<true>, dim3(grid), dim3(kThreads), 0, s, p, m, v, g, count, a);
+    else
+        hipLaunchKernelGGL(k_adam<false>, dim3(grid), dim3(kThreads), 0, s, p, m, v, g, count, a);
+    return launch_status();
+}
 
 extern "C" int nnhip_elementwise_unary(const float* A, float* out, size_t count, unsigned op, void* stream)
 {

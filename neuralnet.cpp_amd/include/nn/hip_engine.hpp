@@ -24,6 +24,14 @@
 // launches the deferred work with the general kernels, and end_batch /
 // flush_batch / settle() launch whatever is still deferred. A deferred result
 // that nobody references any more is dropped without being computed.
+//
+// Deferred elementwise runs: consecutive in-place (add / scale / axpy) and
+// elementwise (unary / binary / scalar / clone) calls on tensors of one size
+// are recorded too, and run when any other call arrives (or on settle,
+// end_batch, flush_batch, to_matrix). The optimizers' per-tensor Adam / AdamW
+// chain (compute_optimizer.hpp:252-304, :388-412) is recognised among them and
+// runs as one pass over p, m, v and g with the same roundings as the separate
+// calls; everything else runs call by call.
 #pragma once
 
 #include <memory>
@@ -164,11 +172,21 @@ private:
     struct PendingFwd;
     struct PendingGemm;
     struct PendingBwd;
+    struct PendingEw;
     std::unique_ptr<PendingFwd> pfwd_;
     std::unique_ptr<PendingGemm> pgemm_;
     std::unique_ptr<PendingBwd> pbwd_;
+    std::unique_ptr<PendingEw> pew_;
+    // Before reading (writing) tensors: launch deferred work that yields
+    // (yields or reads) them; the plain forms also launch the elementwise run.
     Result<void> settle_reads_(std::initializer_list<const Tensor*> ts);
     Result<void> settle_write_(const Tensor& t);
+    Result<void> settle_chain_reads_(std::initializer_list<const Tensor*> ts);
+    Result<void> settle_chain_write_(const Tensor& t);
+    Result<void> ew_push_(unsigned code, unsigned op, bool first, const Tensor& dst, const Tensor& a, const Tensor* b,
+                          float s);
+    Result<void> settle_ew_();
+    Result<std::size_t> adam_run_(const PendingEw& g, std::size_t i, const std::vector<std::ptrdiff_t>& last_read);
     Result<void> settle_fwd_();
     Result<void> settle_gemm_();
     Result<void> settle_bwd_();

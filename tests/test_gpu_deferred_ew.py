@@ -1,0 +1,141 @@
+"""Deferred elementwise runs of the HIP engine, through the C-ABI.
+
+The engine records consecutive same-size elementwise / in-place calls and runs
+them when another kind of call arrives; the optimizers' Adam / AdamW chain
+(reference compute_optimizer.hpp:252-304, :388-412) runs as one fused pass.
+Bars: the fused chain is bit-exact against the same calls run one by one (an
+engine settle after every call stops any recording from spanning two calls);
+both are within 1e-6 of max|p| of the CPU oracle. Mixed sequences match the
+oracle within 1e-6 normwise and see every in-place update in call order.
+"""
+import numpy as np
+import pytest
+
+from helpers import nrm_err, normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+LR, B1, B2, EPS, WD = 1e-3, 0.9, 0.999, 1e-8, 0.01
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def adam_chain(e, p, m, v, g, t, decay, after=lambda: None, keep=None):
+    """The per-tensor call sequence of the optimizer's adam_update_ (AdamW: decay first)."""
+    ib1 = 1.0 / (1.0 - B1 ** t)
+    ib2 = 1.0 / (1.0 - B2 ** t)
+    if decay:
+        e.scale_inplace(p, 1.0 - LR * WD); after()
+    e.scale_inplace(m, B1); after()
+    e.axpy_inplace(m, 1.0 - B1, g); after()
+    e.scale_inplace(v, B2); after()
+    g2 = e.elementwise_binary("Mul", g, g); after()
+    e.scale_inplace(g2, 1.0 - B2); after()
+    e.add_inplace(v, g2); after()
+    mh = e.clone(m); after()
+    e.scale_inplace(mh, ib1); after()
+    vh = e.clone(v); after()
+    e.scale_inplace(vh, ib2); after()
+    sq = e.elementwise_unary("Sqrt", vh); after()
+    den = e.elementwise_binary_scalar("Add", sq, EPS); after()
+    ratio = e.elementwise_binary("Div", mh, den); after()
+    e.scale_inplace(ratio, -LR); after()
+    e.add_inplace(p, ratio); after()
+    if keep is not None:
+        keep.extend([g2, mh, vh, sq, den, ratio])
+
+
+def adam_state(rng, shapes):
+    out = []
+    for s in shapes:
+        out.append((normal(rng, s, 0.02), normal(rng, s, 1e-3), np.abs(normal(rng, s, 1e-6)), normal(rng, s, 0.05)))
+    return out
+
+
+def run_adam(e, state, steps, decay, settle_each, keep=None):
+    ts = [[e.tensor(a) for a in st] for st in state]
+    after = e.settle if settle_each else (lambda: None)
+    for t in range(1, steps + 1):
+        for p, m, v, g in ts:
+            adam_chain(e, p, m, v, g, t, decay, after, keep)
+    return [[x.numpy() for x in (p, m, v)] for p, m, v, _ in ts]
+
+
+SHAPES = [[(1, 1)], [(1, 7)], [(768, 1)], [(10, 100)], [(768, 768)], [(1, 6144)], [(33, 31)],
+          # two chains of one size in one recording, then sizes that change
+          [(64, 64), (64, 64), (1, 768), (768, 768), (1, 768)]]
+
+
+@pytest.mark.parametrize("decay", [True, False])
+@pytest.mark.parametrize("shapes", SHAPES, ids=lambda s: "+".join(f"{r}x{c}" for r, c in s))
+def test_adam_fused_matches_calls(hip, cpu, shapes, decay):
+    rng = np.random.default_rng(len(shapes) * 1000 + shapes[0][0] + 7 * shapes[0][1] + decay)
+    state = adam_state(rng, shapes)
+    fused = run_adam(hip, state, 3, decay, settle_each=False)
+    calls = run_adam(hip, state, 3, decay, settle_each=True)
+    ref = run_adam(cpu, state, 3, decay, settle_each=False)
+    for f, c, r, st in zip(fused, calls, ref, state):
+        for name, a, b, o in zip("pmv", f, c, r):
+            assert np.array_equal(bits(a), bits(b)), f"{name}: fused chain differs from the calls run one by one"
+            scale = max(float(np.abs(o).max()), 1e-30)
+            assert float(np.abs(a - o).max()) <= 1e-6 * scale, f"{name} vs oracle"
+
+
+def test_adam_kept_temporaries_run_call_by_call(hip):
+    """A temporary of the chain still referenced: the chain must not fuse, and the temporary holds its value."""
+    rng = np.random.default_rng(11)
+    state = adam_state(rng, [(40, 50)])
+    keep = []
+    got = run_adam(hip, state, 1, True, settle_each=False, keep=keep)
+    ref = run_adam(hip, state, 1, True, settle_each=True)
+    for a, b in zip(got[0], ref[0]):
+        assert np.array_equal(bits(a), bits(b))
+    p, m, v, g = state[0]
+    g2, mh, vh, sq, den, ratio = [k.numpy() for k in keep]
+    assert np.array_equal(bits(g2), bits((g * g).astype(np.float32) * np.float32(1 - B2)))
+    assert np.array_equal(bits(sq), bits(np.sqrt(vh)))
+    assert np.array_equal(bits(den), bits(sq + np.float32(EPS)))
+
+
+def test_mixed_sequence_in_call_order(hip, cpu):
+    """In-place updates, aliases and reads by other kinds of call see every earlier call."""
+    rng = np.random.default_rng(5)
+    A, B = uniform(rng, (129, 65)), uniform(rng, (129, 65))
+    V = uniform(rng, (1, 129 * 65 // 5))
+
+    def run(e):
+        a, b = e.tensor(A), e.tensor(B)
+        c = e.clone(a)
+        e.scale_inplace(a, 3.0)
+        d = e.elementwise_binary("Mul", a, c)          # new a times old a
+        e.add_inplace(c, d)
+        e.axpy_inplace(b, -0.5, c)
+        s1 = e.row_reduce_sum(b)                        # another kind of call reads b
+        e.add_inplace(b, b)                             # operand aliasing the destination
+        x = e.elementwise_binary_scalar("Sub", b, 2.0, scalar_first=True)
+        dead = e.elementwise_unary("Exp", x)            # result dropped unread
+        del dead
+        y = e.elementwise_unary("Abs", x)
+        v = e.tensor(V)                                 # another size: starts a new recording
+        e.scale_inplace(v, -1.0)
+        w = e.elementwise_binary("Max", v, v)
+        e.scale_inplace(y, 0.25)
+        return [a, b, c, d, s1, x, y, v, w]
+
+    h, c = run(hip), run(cpu)
+    for i, (a, b) in enumerate(zip(h, c)):
+        assert nrm_err(a.numpy(), b.numpy()) <= 1e-6, f"output {i}"
+
+
+def test_zero_size_and_errors(hip):
+    z = hip.tensor(np.zeros((0, 5), np.float32))
+    hip.scale_inplace(z, 2.0)
+    assert hip.clone(z).shape == (0, 5)
+    a = hip.tensor(np.ones((3, 4), np.float32))
+    b = hip.tensor(np.ones((4, 3), np.float32))
+    with pytest.raises(Exception):
+        hip.add_inplace(a, b)
+    hip.scale_inplace(a, 2.0)
+    assert np.array_equal(a.numpy(), np.full((3, 4), 2.0, np.float32))
