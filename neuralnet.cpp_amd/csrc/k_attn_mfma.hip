@@ -490,10 +490,13 @@ __global__ __launch_bounds__(64) void k_attn_combine_rows(AttnArgs d, Work w, in
         for (int u = 0; u < NU; ++u) acc[u] = zero16();
         for_ranges(li, w.NR, [&](int q) {
             const float* pp = w.part + (line * w.NR + q) * w.pw;
+            float t[NU * 16];   // all loads of a partial in flight before the sums
+#pragma unroll
+            for (int e = 0; e < NU * 16; ++e) t[e] = pp[e * 64 + lane];
 #pragma unroll
             for (int u = 0; u < NU; ++u)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[u][r] += pp[(u * 16 + r) * 64 + lane];
+                for (int r = 0; r < 16; ++r) acc[u][r] += t[u * 16 + r];
         });
         store_row_tiles<MODE == kRowApply, NU>(d, out, D, b, qi, h, acc);
     }
@@ -726,13 +729,16 @@ __global__ __launch_bounds__(64) void k_attn_combine_cols(AttnArgs d, Work w, fl
     }
     for_ranges(li, w.NR, [&](int q) {
         const float* pp = w.part + (line * w.NR + q) * w.pw;
+        float t[2 * NU * 16];   // all loads of a partial in flight before the sums
+#pragma unroll
+        for (int e = 0; e < 2 * NU * 16; ++e) t[e] = pp[e * 64 + lane];
 #pragma unroll
         for (int u = 0; u < NU; ++u)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
-                acck[u][r] += pp[(u * 16 + r) * 64 + lane];
-                accv[u][r] += pp[((NU + u) * 16 + r) * 64 + lane];
+                acck[u][r] += t[u * 16 + r];
+                accv[u][r] += t[(NU + u) * 16 + r];
             }
     });
     store_col_tiles<NU>(d, dK, dV, b, kj, h, acck, accv);

@@ -762,12 +762,19 @@ template <bool FULL, bool MASKED>
 __device__ __forceinline__ void col_scores(const f32x16& s, const FlashBwdArgs& a, int ibase, int jc, int kj, int h,
                                            int M, int N, float* x)
 {
+    // The 16 mask loads are issued together (clamped indices, no branch), then used.
+    float mv[16];
+    if constexpr (MASKED)
+    {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mv[r] = a.mask[(long)min(ibase + drow(r, h), M - 1) * N + jc];
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r)
     {
         const int i = ibase + drow(r, h);
         float v = a.alpha * s[r];
-        if constexpr (MASKED) v += a.mask[(long)min(i, M - 1) * N + jc];
+        if constexpr (MASKED) v += mv[r];
         if constexpr (!FULL) v = (i < M && kj < N) ? v : kNegInf;
         x[r] = v;
     }
@@ -933,13 +940,17 @@ __global__ __launch_bounds__(64) void k_flash_bwd_cols_combine(FlashBwdArgs a, F
     for (unsigned long long rs = lw.ranges; rs; rs &= rs - 1)
     {
         const float* pp = g.part + (lidx * g.NR + __builtin_ctzll(rs)) * g.pw;
+        // All of a partial's loads first, then the sums: keeps them in flight together.
+        float t[2 * DU * 16];
+#pragma unroll
+        for (int q = 0; q < 2 * DU * 16; ++q) t[q] = pp[q * 64 + lane];
 #pragma unroll
         for (int u = 0; u < DU; ++u)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
-                dk[u][r] += pp[(u * 16 + r) * 64 + lane];
-                dv[u][r] += pp[((DU + u) * 16 + r) * 64 + lane];
+                dk[u][r] += t[u * 16 + r];
+                dv[u][r] += t[(DU + u) * 16 + r];
             }
     }
     const LineWork one{1ull, 0ull, 1ull, 1};

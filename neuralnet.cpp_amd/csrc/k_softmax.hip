@@ -327,9 +327,11 @@ __global__ __launch_bounds__(kThreads) void k_row_softmax_reg(const float* X, fl
     for (unsigned u = 0; u < kRowPer; ++u)
     {
         const size_t c = threadIdx.x + u * kThreads;
-        v[u] = c < cols ? x[c] : 0.0f;
-        if (c < cols) m = fmax_std(m, v[u]);
+        v[u] = x[c < cols ? c : cols - 1];
     }
+#pragma unroll
+    for (unsigned u = 0; u < kRowPer; ++u)
+        if (threadIdx.x + u * kThreads < cols) m = fmax_std(m, v[u]);
     m = block_max(m, scratch);
     float s = 0.0f;
 #pragma unroll
@@ -376,16 +378,16 @@ __global__ __launch_bounds__(kThreads) void k_row_softmax_wave(const float* X, f
     float4* o = reinterpret_cast<float4*>(out + row * cols);
     float4 v[NV];
     float m = kLowest;
+    // Unconditional loads (index clamped into the row) so that all NV are in flight at once.
 #pragma unroll
     for (int u = 0; u < NV; ++u)
     {
         const size_t q = lane + 64 * u;
-        if (q < nq)
-        {
-            v[u] = x[q];
-            m = fmax_std(fmax_std(fmax_std(fmax_std(m, v[u].x), v[u].y), v[u].z), v[u].w);
-        }
+        v[u] = x[q < nq ? q : nq - 1];
     }
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+        if (lane + 64 * u < nq) m = fmax_std(fmax_std(fmax_std(fmax_std(m, v[u].x), v[u].y), v[u].z), v[u].w);
     m = wave_max(m);
     float sum = 0.0f;
 #pragma unroll
