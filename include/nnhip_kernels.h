@@ -157,6 +157,31 @@ int nnhip_flash_backward(const float* Q, const float* Kt, const float* dO, const
                          float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K, size_t Kd, float alpha,
                          float alpha2, void* workspace, void* stream);
 
+/* Layout options of the one-pass chains for the reference's materialised attention path
+ * (compute_layer.hpp:1230-1252 forward, :1331-1361 backward: scores = batched_matmul(Q, K, transA),
+ * masked = scores + mask, A = softmax rows, O = batched_matmul(V, A, transB); dV = batched_matmul(dO, A),
+ * P = batched_matmul(dO, V, transA), dS = softmax backward, dQ = batched_matmul(K, dS, transB),
+ * dK = batched_matmul(Q, dS)), which HipEngine runs here without materialising scores or A:
+ *   mask_batch_stride  floats between the batch entries' (M, N) masks (0: one mask for all), e.g. M*N for
+ *                      the (batch*M, N) ALiBi / document mask; cells then come from
+ *                      nnhip_flash_classify_batched over the same masks;
+ *   v_dim_major        V per batch is (D, N) [dim][key] (the layer's (B*H*d, T) heads) instead of (N, D);
+ *   o_dim_major        O per batch is written (D, M) [dim][query] instead of (M, D);
+ *   g_is_do            G_i is dO's column i (dV_j = sum_i W_ij dO_i, the materialised path's
+ *                      batched_matmul(dO, A)); G and ldg are ignored; needs Kd == K.
+ * No CUDA counterpart (cuda_engine.hpp leaves the attention primitives to the CPU). */
+int nnhip_flash_classify_batched(const float* mask, size_t masks, size_t mask_batch_stride, size_t M, size_t N,
+                                 void* cells, void* stream);
+int nnhip_flash_forward_layout(const float* Q, const float* Kt, const float* V, const float* mask, const void* cells,
+                               float* m, float* l, float* O, size_t batch, size_t M, size_t N, size_t K, size_t D,
+                               float alpha, size_t mask_batch_stride, int v_dim_major, int o_dim_major,
+                               void* workspace, void* stream);
+int nnhip_flash_backward_layout(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* G,
+                                size_t ldg, const float* mask, const void* cells, const float* m, const float* l,
+                                float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K,
+                                size_t Kd, float alpha, float alpha2, size_t mask_batch_stride, int g_is_do,
+                                void* workspace, void* stream);
+
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */
 size_t nnhip_col_softmax_workspace_bytes(size_t C, size_t N);

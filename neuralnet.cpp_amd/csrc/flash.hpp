@@ -17,6 +17,7 @@ struct FlashGeo
     int G;           // line groups (4 lines each) per batch entry
     int pw;          // floats per (line, range) partial
     const unsigned char* cls;   // RT x CT mask cell classes, or nullptr without a mask
+    long cls_bs;     // bytes between batch entries' cell tables (0: one table shared)
     float* part;     // partials of lines cut into several ranges
 };
 
@@ -26,12 +27,15 @@ struct FlashFwdArgs
     const float* Q;      // per batch (K, M)
     const float* Kt;     // per batch (K, N)
     const float* V;      // per batch (N, D); unused without O
-    const float* mask;   // (M, N) or nullptr
+    const float* mask;   // (M, N) per batch entry (mask_bs apart), or nullptr
     float* m;
     float* l;
     float* O;
     int M, N, K, D;
     float alpha;
+    long mask_bs;        // floats between batch entries' masks (0: one mask shared)
+    int v_dm;            // V per batch is (D, N) [dim][key] instead of (N, D)
+    int o_dm;            // O per batch is written (D, M) [dim][query] instead of (M, D)
 };
 
 // Backward: R (batch*M), dQ (batch*K, M), dK and dV (batch*K, N) from
@@ -42,8 +46,8 @@ struct FlashBwdArgs
     const float* Kt;     // per batch (K, N)
     const float* dO;     // per batch (Kd, M)
     const float* Vp;     // per batch (Kd, N)
-    const float* G;      // per batch (M, ldg), ldg >= K
-    const float* mask;   // (M, N) or nullptr
+    const float* G;      // per batch (M, ldg), ldg >= K; unused when g_do
+    const float* mask;   // (M, N) per batch entry (mask_bs apart), or nullptr
     const float* m;
     const float* l;
     float* R;
@@ -52,14 +56,17 @@ struct FlashBwdArgs
     float* dV;
     int M, N, K, Kd, ldg;
     float alpha, alpha2;
+    long mask_bs;        // floats between batch entries' masks (0: one mask shared)
+    int g_do;            // G_i is dO's column i (dV_j = sum_i W dO_i; needs Kd == K)
 };
 
 // Shapes the one-pass kernels take: head dims K (and Kd) <= 64, value width
 // D <= 64 with D % 4 == 0. The backward also needs K % 4 == 0 and ldg % 4 == 0.
 bool flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D);
-// Mask cell table: one byte per 32x32 cell of the (M, N) mask (0 all -inf, 1 all zero, 2 general).
+// Mask cell table: one byte per 32x32 cell of each (M, N) mask (0 all -inf, 1 all zero, 2 general);
+// masks batches, mask_bs floats apart, give batches tables of flash_cells_bytes(M, N) each.
 size_t flash_cells_bytes(size_t M, size_t N);
-int flash_classify(const float* mask, size_t M, size_t N, void* cells, hipStream_t s);
+int flash_classify(const float* mask, size_t masks, long mask_bs, size_t M, size_t N, void* cells, hipStream_t s);
 size_t flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D, bool backward);
 int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, hipStream_t s);
 int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, hipStream_t s);

@@ -316,6 +316,66 @@ struct HipEngine::PendingEw
     static bool reads_b(const Op& o) { return o.code == kBin || o.code == kAxpy; }
 };
 
+// The reference's materialised attention (compute_layer.hpp:1230-1252 forward,
+// :1331-1361 backward), recorded call by call and run by the one-pass kernels:
+//   scores = batched_matmul(Q, K, transA) * alpha      PendingGemm
+//   masked = scores + mask                             PendingMaskAdd
+//   A      = softmax rows of masked                    PendingAttn (kept per layer)
+//   O      = batched_matmul(V, A, transB)              fused forward: O, and m, l into the record
+//   dV     = batched_matmul(dO, A)                     PendingDv
+//   P      = batched_matmul(dO, V, transA)             PendingGemm
+//   dS     = softmax backward (A, P)                   PendingDs
+//   dQ     = batched_matmul(K, dS, transB) * alpha     fused backward: dQ, dK, dV (AttnGrads)
+//   dK     = batched_matmul(Q, dS) * alpha
+// Each record can also compute its result with the general kernels, which is
+// what happens when anything else reads it or writes one of its inputs.
+struct HipEngine::PendingMaskAdd
+{
+    Tensor Q, K, mask, out;   // out = alpha * Q^T K (per batch) + mask
+    std::size_t batch, M, N, Kd;
+    float alpha;
+    bool uses(const float* p) const
+    {
+        return has_buf(Q, p) || has_buf(K, p) || has_buf(mask, p) || has_buf(out, p);
+    }
+};
+struct HipEngine::PendingAttn
+{
+    Tensor Q, K, mask, A;     // A: the probabilities handed out; written only when materialised
+    std::size_t batch, M, N, Kd;
+    float alpha;
+    Tensor m, l;              // row max and sum, once the fused forward has run
+    bool stats = false, materialised = false;
+    bool uses(const float* p) const
+    {
+        return has_buf(Q, p) || has_buf(K, p) || has_buf(mask, p) || has_buf(A, p);
+    }
+};
+struct HipEngine::PendingDv
+{
+    std::shared_ptr<PendingAttn> p;
+    Tensor dO, out;           // out = dO A (per batch)
+    bool uses(const float* q) const { return has_buf(dO, q) || has_buf(out, q) || p->uses(q); }
+};
+struct HipEngine::PendingDs
+{
+    std::shared_ptr<PendingAttn> p;
+    Tensor dO, Vp, out;       // out = A * (P - rowsum(A P)), P = alpha2 * dO^T Vp (per batch)
+    std::size_t Kd2;
+    float alpha2;
+    bool uses(const float* q) const
+    {
+        return has_buf(dO, q) || has_buf(Vp, q) || has_buf(out, q) || p->uses(q);
+    }
+};
+// dQ and dK of a fused backward, waiting for their batched_matmul calls.
+struct HipEngine::AttnGrads
+{
+    Tensor dS, Q, K, dQ, dK;
+    float alpha;
+    bool q_taken = false, k_taken = false;
+};
+
 namespace
 {
 
@@ -493,6 +553,11 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
         if (!t) continue;
         const float* p = t->dev_ptr();
         if (!p) continue;
+        if (pmadd_ && has_buf(pmadd_->out, p)) NN_CHECK(settle_madd_());
+        if (pdv_ && has_buf(pdv_->out, p)) NN_CHECK(settle_dv_());
+        if (pds_ && has_buf(pds_->out, p)) NN_CHECK(settle_ds_());
+        for (auto& a : pattn_)
+            if (has_buf(a->A, p)) NN_CHECK(materialise_attn_(*a));
         if (pbwd_ && pbwd_->yields(p)) NN_CHECK(settle_bwd_());
         if (pgemm_ && pgemm_->yields(p)) NN_CHECK(settle_gemm_());
         if (pfwd_ && pfwd_->yields(p)) NN_CHECK(settle_fwd_());
@@ -500,22 +565,26 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
     return {};
 }
 
+// Cell tables of a mask tensor read as rows / M stacked (M, N) masks (one
+// table each), cached per tensor until it is written in place or evicted.
 Result<const void*> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, std::size_t N)
 {
     if (!mask) return static_cast<const void*>(nullptr);
     for (std::size_t i = 0; i < cells_.size(); ++i)
-        if (same_t(cells_[i].mask, *mask))
+        if (same_t(cells_[i].mask, *mask) && cells_[i].M == M)
         {
             CellTable t = cells_[i];
             cells_.erase(cells_.begin() + static_cast<std::ptrdiff_t>(i));
             cells_.push_back(t);
             return static_cast<const void*>(t.cells->data());
         }
-    NN_TRY(buf, scratch_(nnhip_flash_cells_bytes(M, N)));
-    NN_CHECK(kernel_(nnhip_flash_classify(D(*mask), M, N, buf->data(), stream_), "attention mask cells"));
-    constexpr std::size_t kKeep = 8;
+    const std::size_t masks = mask->rows() / M;
+    NN_TRY(buf, scratch_(masks * nnhip_flash_cells_bytes(M, N)));
+    NN_CHECK(kernel_(nnhip_flash_classify_batched(D(*mask), masks, M * N, M, N, buf->data(), stream_),
+                     "attention mask cells"));
+    constexpr std::size_t kKeep = 32;   // one per layer's mask in a 12-32 layer model
     if (cells_.size() == kKeep) cells_.erase(cells_.begin());
-    cells_.push_back({*mask, buf});
+    cells_.push_back({*mask, buf, M});
     return static_cast<const void*>(buf->data());
 }
 
@@ -529,6 +598,16 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t)
 {
     const float* p = t.dev_ptr();
     if (!p) return {};
+    if (pmadd_ && pmadd_->uses(p)) NN_CHECK(settle_madd_());
+    if (pdv_ && pdv_->uses(p)) NN_CHECK(settle_dv_());
+    if (pds_ && pds_->uses(p)) NN_CHECK(settle_ds_());
+    if (pgrads_ && (has_buf(pgrads_->dQ, p) || has_buf(pgrads_->dK, p))) pgrads_.reset();
+    for (std::size_t i = pattn_.size(); i-- > 0;)
+        if (pattn_[i]->uses(p))
+        {
+            if (live(pattn_[i]->A)) NN_CHECK(materialise_attn_(*pattn_[i]));
+            pattn_.erase(pattn_.begin() + static_cast<std::ptrdiff_t>(i));
+        }
     for (std::size_t i = cells_.size(); i-- > 0;)
         if (has_buf(cells_[i].mask, p)) cells_.erase(cells_.begin() + static_cast<std::ptrdiff_t>(i));
     if (pbwd_ && pbwd_->uses(p)) NN_CHECK(settle_bwd_());
@@ -544,6 +623,11 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t)
 Result<void> HipEngine::settle()
 {
     NN_CHECK(settle_ew_());
+    NN_CHECK(settle_madd_());
+    NN_CHECK(settle_dv_());
+    NN_CHECK(settle_ds_());
+    if (pgrads_ && !live(pgrads_->dQ) && !live(pgrads_->dK)) pgrads_.reset();
+    forget_dead_attn_();
     NN_CHECK(settle_bwd_());
     NN_CHECK(settle_gemm_());
     return settle_fwd_();
@@ -592,6 +676,162 @@ Result<void> HipEngine::settle_bwd_()
                                                 q->mask ? D(*q->mask) : nullptr, W(q->dQ), W(q->R), q->batch, q->M,
                                                 q->N, q->Kd, 1, 0, q->alpha, ws ? ws->data() : nullptr, stream_),
                    "batched_matmul_softmax_backward_q");
+}
+
+// ── deferred materialised attention ─────────────────────────────────────────
+void HipEngine::forget_dead_attn_()
+{
+    for (std::size_t i = pattn_.size(); i-- > 0;)
+        if (!live(pattn_[i]->A) && pattn_[i].use_count() == 1) pattn_.erase(pattn_.begin() + static_cast<std::ptrdiff_t>(i));
+}
+
+std::shared_ptr<HipEngine::PendingAttn> HipEngine::attn_of_(const Tensor& A) const
+{
+    for (const auto& a : pattn_)
+        if (same_t(a->A, A)) return a;
+    return nullptr;
+}
+
+// masked = alpha Q^T K + mask into `out` with the general kernels.
+Result<void> HipEngine::scores_masked_(const Tensor& Q, const Tensor& K, const Tensor& mask, std::size_t batch,
+                                       std::size_t M, std::size_t N, std::size_t Kd, float alpha, const Tensor& out)
+{
+    Tensor o = out;
+    NN_CHECK(launch_gemm_(Q, K, o, batch, true, false, alpha, M, N, Kd));
+    return kernel_(nnhip_elementwise_binary(D(out), D(mask), W(out), out.size(), 0u, stream_), "attention mask add");
+}
+
+Result<void> HipEngine::settle_madd_()
+{
+    if (!pmadd_) return {};
+    std::unique_ptr<PendingMaskAdd> r = std::move(pmadd_);
+    if (!live(r->out)) return {};
+    return scores_masked_(r->Q, r->K, r->mask, r->batch, r->M, r->N, r->Kd, r->alpha, r->out);
+}
+
+// A = softmax rows (alpha Q^T K + mask), written into the handed-out tensor.
+Result<void> HipEngine::materialise_attn_(PendingAttn& p)
+{
+    if (p.materialised) return {};
+    NN_TRY(t, alloc_(p.batch * p.M, p.N));
+    NN_CHECK(scores_masked_(p.Q, p.K, p.mask, p.batch, p.M, p.N, p.Kd, p.alpha, t));
+    NN_CHECK(kernel_(nnhip_row_softmax(D(t), W(p.A), p.batch * p.M, p.N, stream_), "attention probabilities"));
+    p.materialised = true;
+    return {};
+}
+
+Result<void> HipEngine::settle_dv_()
+{
+    if (!pdv_) return {};
+    std::unique_ptr<PendingDv> r = std::move(pdv_);
+    if (!live(r->out)) return {};
+    NN_CHECK(materialise_attn_(*r->p));
+    const PendingAttn& p = *r->p;
+    return launch_gemm_(r->dO, p.A, r->out, p.batch, false, false, 1.0f, r->dO.rows() / p.batch, p.N, p.M);
+}
+
+Result<void> HipEngine::settle_ds_()
+{
+    if (!pds_) return {};
+    std::unique_ptr<PendingDs> r = std::move(pds_);
+    if (!live(r->out)) return {};
+    NN_CHECK(materialise_attn_(*r->p));
+    const PendingAttn& p = *r->p;
+    NN_TRY(P, alloc_(p.batch * p.M, p.N));
+    NN_CHECK(launch_gemm_(r->dO, r->Vp, P, p.batch, true, false, r->alpha2, p.M, p.N, r->Kd2));
+    return kernel_(nnhip_row_softmax_backward(D(p.A), D(P), W(r->out), p.batch * p.M, p.N, stream_),
+                   "attention softmax backward");
+}
+
+// The calls of the chain that consume deferred tensors. Each returns nullopt
+// when the call is not the expected next step; the caller then proceeds with
+// the general path (which settles what it reads).
+Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor& B, std::size_t batch, bool tA,
+                                                   bool tB, Scalar alpha)
+{
+    using R = std::optional<Tensor>;
+    // dQ / dK of a fused backward already run.
+    if (pgrads_ && same_t(B, pgrads_->dS) && !tA && alpha == pgrads_->alpha)
+    {
+        if (tB && !pgrads_->q_taken && same_t(A, pgrads_->K))
+        {
+            pgrads_->q_taken = true;
+            R r(pgrads_->dQ);
+            if (pgrads_->k_taken) pgrads_.reset();
+            return r;
+        }
+        if (!tB && !pgrads_->k_taken && same_t(A, pgrads_->Q))
+        {
+            pgrads_->k_taken = true;
+            R r(pgrads_->dK);
+            if (pgrads_->q_taken) pgrads_.reset();
+            return r;
+        }
+    }
+    if (tA) return R();
+    auto p = attn_of_(B);
+    // O = V A^T per batch: the fused forward.
+    if (p && tB && !p->stats && alpha == 1.0f && A.rows() % batch == 0 && batch == p->batch && A.cols() == p->N)
+    {
+        const std::size_t Dv = A.rows() / batch;
+        if (Dv == 0 || !nnhip_flash_supported(batch, p->M, p->N, p->Kd, Dv)) return R();
+        NN_CHECK(settle_reads_({&A}));
+        NN_TRY(out, alloc_(batch * Dv, p->M));
+        NN_TRY(m, alloc_(batch * p->M, 1));
+        NN_TRY(l, alloc_(batch * p->M, 1));
+        NN_TRY(cells, mask_cells_(&p->mask, p->M, p->N));
+        const std::size_t bs = p->mask.rows() == p->M ? 0 : p->M * p->N;
+        NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, p->M, p->N, p->Kd, Dv, 0)));
+        NN_CHECK(kernel_(nnhip_flash_forward_layout(D(p->Q), D(p->K), D(A), D(p->mask), cells, W(m), W(l), W(out),
+                                                    batch, p->M, p->N, p->Kd, Dv, p->alpha, bs, 1, 1, ws->data(),
+                                                    stream_),
+                         "attention forward"));
+        p->m = m;
+        p->l = l;
+        p->stats = true;
+        return R(out);
+    }
+    // dV = dO A per batch: recorded for the fused backward.
+    if (p && !tB && p->stats && alpha == 1.0f && A.rows() == batch * p->Kd && A.cols() == p->M && batch == p->batch)
+    {
+        NN_CHECK(settle_reads_({&A}));
+        NN_CHECK(settle_dv_());
+        NN_TRY(out, alloc_(batch * p->Kd, p->N));
+        pdv_ = std::make_unique<PendingDv>(PendingDv{p, A, out});
+        return R(out);
+    }
+    // dQ = alpha K dS^T or dK = alpha Q dS per batch: run the fused backward.
+    if (pds_ && same_t(B, pds_->out) && alpha == pds_->p->alpha &&
+        ((tB && same_t(A, pds_->p->K)) || (!tB && same_t(A, pds_->p->Q))))
+    {
+        const PendingAttn& q = *pds_->p;
+        NN_CHECK(settle_ew_());
+        const bool dv_here = pdv_ && pdv_->p == pds_->p && same_t(pdv_->dO, pds_->dO);
+        if (!dv_here) NN_CHECK(settle_dv_());
+        NN_TRY(dQ, alloc_(batch * q.Kd, q.M));
+        NN_TRY(dK, alloc_(batch * q.Kd, q.N));
+        Tensor dV;
+        if (dv_here)
+            dV = pdv_->out;
+        else
+        {
+            NN_TRY(t, alloc_(batch * q.Kd, q.N));
+            dV = t;
+        }
+        NN_TRY(Rr, alloc_(batch * q.M, 1));
+        NN_TRY(cells, mask_cells_(&q.mask, q.M, q.N));
+        const std::size_t bs = q.mask.rows() == q.M ? 0 : q.M * q.N;
+        NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, q.M, q.N, q.Kd, 4, 1)));
+        NN_CHECK(kernel_(nnhip_flash_backward_layout(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), nullptr, 0, D(q.mask),
+                                                     cells, D(q.m), D(q.l), W(Rr), W(dQ), W(dK), W(dV), batch, q.M,
+                                                     q.N, q.Kd, pds_->Kd2, q.alpha, pds_->alpha2, bs, 1, ws->data(),
+                                                     stream_),
+                         "attention backward"));
+        if (dv_here) pdv_.reset();
+        pgrads_ = std::make_unique<AttnGrads>(AttnGrads{pds_->out, q.Q, q.K, dQ, dK, q.alpha});
+        return attn_bmm_(A, B, batch, tA, tB, alpha);
+    }
+    return R();
 }
 
 // ── deferred elementwise runs ───────────────────────────────────────────────
@@ -930,6 +1170,11 @@ Result<void> HipEngine::launch_gemm_(const Tensor& A, const Tensor& B, Tensor& C
 Result<Tensor> HipEngine::batched_matmul(const Tensor& A, const Tensor& B, std::size_t batch, bool tA, bool tB,
                                          Scalar alpha)
 {
+    NN_CHECK(check_gpu_({&A, &B}, "batched_matmul"));
+    NN_TRY(d0, bdims(A, B, batch, tA, tB, "batched_matmul"));
+    (void)d0;
+    NN_TRY(chained, attn_bmm_(A, B, batch, tA, tB, alpha));
+    if (chained) return std::move(*chained);
     NN_CHECK(need_gpu_({&A, &B}, "batched_matmul"));
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul"));
     NN_TRY(C, alloc_(batch * d.M, d.N));
@@ -1254,6 +1499,20 @@ Result<Tensor> HipEngine::elementwise_binary(BinaryOp op, const Tensor& A, const
     NN_CHECK(check_gpu_({&A, &B}, "elementwise_binary"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("elementwise_binary: shape mismatch");
     if (static_cast<unsigned>(op) > static_cast<unsigned>(BinaryOp::Min)) return fail("elementwise_binary: bad op");
+    // scores + mask of a deferred scores product (materialised attention): recorded.
+    if (op == BinaryOp::Add && pgemm_ && same_t(A, pgemm_->C) && !has_buf(B, A.dev_ptr()) && A.size() &&
+        pgemm_->N == B.cols() && pgemm_->K <= 64)
+    {
+        NN_CHECK(settle_reads_({&B}));
+        NN_CHECK(settle_madd_());
+        if (pgemm_ && same_t(A, pgemm_->C))
+        {
+            const PendingGemm& g = *pgemm_;
+            NN_TRY(o, alloc_(A.rows(), A.cols()));
+            pmadd_ = std::make_unique<PendingMaskAdd>(PendingMaskAdd{g.A, g.B, B, o, g.batch, g.M, g.N, g.K, g.alpha});
+            return o;
+        }
+    }
     NN_CHECK(settle_chain_reads_({&A, &B}));
     NN_TRY(o, alloc_(A.rows(), A.cols()));
     if (A.size()) NN_CHECK(ew_push_(kBin, static_cast<unsigned>(op), false, o, A, &B, 0.0f));
@@ -1298,6 +1557,11 @@ Result<Tensor> HipEngine::eval_impl_(const ExprSpec& spec, std::span<const Tenso
                                      std::size_t cols, bool vector_out)
 {
     NN_CHECK(validate_expr_spec(spec, inputs.size()));
+    if (!vector_out)
+    {
+        NN_TRY(chained, attn_softmax_(spec, inputs, rows, cols));
+        if (chained) return std::move(*chained);
+    }
     for (const Tensor& t : inputs)
     {
         if (!t.is_gpu()) return fail("eval_expr: input not GPU");
@@ -1368,6 +1632,56 @@ Result<Tensor> HipEngine::eval_impl_(const ExprSpec& spec, std::span<const Tenso
                     "the reduced axis");
     NN_CHECK(kernel_(rc, "eval_expr"));
     return o;
+}
+
+// Softmax rows of a recorded scores + mask (the attention probabilities), and
+// the softmax backward of such probabilities against a deferred dO^T V
+// product: both recorded for the one-pass kernels.
+Result<std::optional<Tensor>> HipEngine::attn_softmax_(const ExprSpec& spec, std::span<const Tensor> inputs,
+                                                       std::size_t rows, std::size_t cols)
+{
+    using R = std::optional<Tensor>;
+    const float* a[5] = {};
+    auto tensor_of = [&](const float* p) -> const Tensor* {
+        for (const Tensor& t : inputs)
+            if (t.dev_ptr() == p) return &t;
+        return nullptr;
+    };
+    if (pmadd_ && inputs.size() >= 1 && same_t(inputs[0], pmadd_->out) && rows == pmadd_->out.rows() &&
+        cols == pmadd_->out.cols() && bind(canon(LayerProg::SoftmaxFwd), spec, inputs, a))
+    {
+        const PendingMaskAdd& r = *pmadd_;
+        if (!nnhip_flash_supported(r.batch, r.M, r.N, r.Kd, 4) || r.Kd % 4 != 0) return R();
+        if (r.mask.rows() != r.batch * r.M && r.mask.rows() != r.M) return R();
+        forget_dead_attn_();
+        NN_TRY(A, alloc_(rows, cols));
+        auto p = std::make_shared<PendingAttn>();
+        p->Q = r.Q;
+        p->K = r.K;
+        p->mask = r.mask;
+        p->A = A;
+        p->batch = r.batch;
+        p->M = r.M;
+        p->N = r.N;
+        p->Kd = r.Kd;
+        p->alpha = r.alpha;
+        pattn_.push_back(std::move(p));
+        return R(A);
+    }
+    if (inputs.size() >= 2 && pgemm_ && bind(canon(LayerProg::SoftmaxBwd), spec, inputs, a))
+    {
+        const Tensor* y = tensor_of(a[0]);
+        const Tensor* g = tensor_of(a[1]);
+        auto p = y ? attn_of_(*y) : nullptr;
+        if (!p || !g || !p->stats || !same_t(*g, pgemm_->C)) return R();
+        const PendingGemm& pg = *pgemm_;
+        if (pg.batch != p->batch || pg.M != p->M || pg.N != p->N || pg.K != p->Kd) return R();
+        NN_CHECK(settle_ds_());
+        NN_TRY(out, alloc_(rows, cols));
+        pds_ = std::make_unique<PendingDs>(PendingDs{p, pg.A, pg.B, out, pg.K, pg.alpha});
+        return R(out);
+    }
+    return R();
 }
 
 // Fused kernels for the layer programs (k_fused.hip, k_softmax.hip). Returns

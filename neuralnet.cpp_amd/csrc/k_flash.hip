@@ -47,6 +47,7 @@
 #include "flash.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "nnhip_kernels.h"
@@ -121,17 +122,18 @@ struct LineWork
     unsigned long long nz, gen, ranges;
     int nne;
 };
-__device__ __forceinline__ LineWork line_work(const FlashGeo& g, bool rows, int line, int rg)
+__device__ __forceinline__ LineWork line_work(const FlashGeo& g, bool rows, int b, int line, int rg)
 {
     LineWork w{0ull, 0ull, 0ull, 0};
     if (line >= (rows ? g.RT : g.CT)) return w;
     const int cells = rows ? g.CT : g.RT, lane = threadIdx.x & 63;
+    const unsigned char* cls = g.cls ? g.cls + (long)b * g.cls_bs : nullptr;
     const unsigned long long lowR = g.R >= 64 ? ~0ull : ((1ull << g.R) - 1);
     for (int x0 = 0; x0 < cells; x0 += 64)
     {
         const int x = x0 + lane;
         int cl = 0;
-        if (x < cells) cl = !g.cls ? 1 : (rows ? g.cls[(long)line * g.CT + x] : g.cls[(long)x * g.CT + line]);
+        if (x < cells) cl = !cls ? 1 : (rows ? cls[(long)line * g.CT + x] : cls[(long)x * g.CT + line]);
         const unsigned long long nz = __ballot(cl != 0), gen = __ballot(cl == 2);
         const int r_end = min(g.NR, (x0 + 64) / g.R);
         for (int r = x0 / g.R; r < r_end; ++r)
@@ -339,6 +341,19 @@ __device__ __forceinline__ void fwd_store(const FlashFwdArgs& a, const FlashGeo&
         if constexpr (WITH_O)
         {
             const float inv = lrun > 0.0f ? 1.0f / lrun : 0.0f;
+            if (a.o_dm)
+            {
+                float* ocol = a.O + (long)b * a.D * g.M + qi;   // O per batch (D, M)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                {
+                    const int d0 = DU * drow(r, h);
+                    if (d0 >= a.D) continue;
+#pragma unroll
+                    for (int u = 0; u < DU; ++u) ocol[(long)(d0 + u) * g.M] = o[u][r] * inv;
+                }
+                return;
+            }
             float* orow = a.O + row * a.D;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
@@ -396,7 +411,7 @@ __device__ __forceinline__ float cell_scores(const f32x16& s, float alpha, const
 // step); each wave computes the scores of its active cells, updates its
 // online max / sum once for both (one cross-lane max, one rescale, skipped
 // when no row maximum moved) and accumulates the weighted values.
-template <int KP, int DP, bool WITH_O>
+template <int KP, int DP, bool WITH_O, bool VDM>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, FlashGeo g)
 {
     constexpr int DU = DP / 32;
@@ -406,7 +421,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const Item it = item_of(g);
     const int line = it.grp * kWaves + wave, qi = line * 32 + c;
-    const LineWork lw = line_work(g, true, line, it.rg);
+    const LineWork lw = line_work(g, true, it.b, line, it.rg);
     if (lane == 0) nz_s[wave] = lw.nz;
     __syncthreads();
     const unsigned long long any = nz_s[0] | nz_s[1] | nz_s[2] | nz_s[3];
@@ -422,7 +437,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
         const float* Kb = a.Kt + (long)it.b * a.K * g.N;
         const float* Vb = WITH_O ? a.V + (long)it.b * g.N * a.D : nullptr;
         TTile<KP> kt[2];
-        RTile<DP> vt[2];
+        std::conditional_t<VDM, TTile<DP>, RTile<DP>> vt[2];   // V (D, N) or (N, D), staged [key][dim]
         unsigned long long rest = any;
         auto pop = [&]() {
             if (!rest) return -1;
@@ -437,7 +452,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
                 if (cc[t] >= 0)
                 {
                     kt[t].load(Kb, a.K, g.N, 32 * (cell0 + cc[t]), threadIdx.x);
-                    if constexpr (WITH_O) vt[t].load(Vb, a.D, a.D, g.N, 32 * (cell0 + cc[t]), threadIdx.x);
+                    if constexpr (WITH_O && VDM) vt[t].load(Vb, a.D, g.N, 32 * (cell0 + cc[t]), threadIdx.x);
+                    if constexpr (WITH_O && !VDM) vt[t].load(Vb, a.D, a.D, g.N, 32 * (cell0 + cc[t]), threadIdx.x);
                 }
         };
         auto store = [&](int buf, int c0, int c1) {
@@ -455,7 +471,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
         float qf[KP / 2];
         line_operand<KP>(Qb, a.K, g.M, qi, h, qf);
         const int qc = min(qi, g.M - 1);
-        const float* mrow = a.mask ? a.mask + (long)qc * g.N : nullptr;
+        const float* mrow = a.mask ? a.mask + it.b * a.mask_bs + (long)qc * g.N : nullptr;
         store(0, c0, c1);
         __syncthreads();
         int buf = 0;
@@ -539,7 +555,7 @@ __global__ __launch_bounds__(64) void k_flash_fwd_combine(FlashFwdArgs a, FlashG
     const int lane = threadIdx.x, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
-    const LineWork lw = line_work(g, true, line, 0);
+    const LineWork lw = line_work(g, true, b, line, 0);
     if (lw.nne <= 1) return;
     float m = kLowest, l = 0.0f;
     f32x16 o[DU];
@@ -609,7 +625,7 @@ __device__ __forceinline__ void rows_group(const FlashBwdArgs& a, const FlashGeo
     constexpr int DU = KP / 32;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const int line = grp * kWaves + wave, qi = line * 32 + c;
-    const LineWork lw = line_work(g, true, line, rg);
+    const LineWork lw = line_work(g, true, b, line, rg);
     if (lane == 0) nz_s[wave] = lw.nz;
     __syncthreads();
     const unsigned long long any = nz_s[0] | nz_s[1] | nz_s[2] | nz_s[3];
@@ -642,7 +658,7 @@ __device__ __forceinline__ void rows_group(const FlashBwdArgs& a, const FlashGeo
         const float mi = a.m[srow], li = a.l[srow];
         const float linv = li != 0.0f ? 1.0f / li : 0.0f;
         const float mb = mi == kLowest ? 0.0f : mi * kLog2e;   // a row without allowed keys has only -inf scores
-        const float* mrow = a.mask ? a.mask + (long)qc * g.N : nullptr;
+        const float* mrow = a.mask ? a.mask + b * a.mask_bs + (long)qc * g.N : nullptr;
         kt.store(Ks[0], threadIdx.x);
         vt.store(Vs[0], threadIdx.x);
         __syncthreads();
@@ -709,7 +725,7 @@ __global__ __launch_bounds__(64) void k_flash_bwd_rows_combine(FlashBwdArgs a, F
     const int lane = threadIdx.x, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
-    const LineWork lw = line_work(g, true, line, 0);
+    const LineWork lw = line_work(g, true, b, line, 0);
     if (lw.nne <= 1) return;
     float racc = 0.0f;
     f32x16 x[DU], y[DU];
@@ -738,14 +754,14 @@ __global__ __launch_bounds__(64) void k_flash_bwd_rows_combine(FlashBwdArgs a, F
 
 // Loads the query-side tiles of one cell of the key-line kernel into registers:
 // Q and dO (transposed), G rows, and m, 1/l, R of the 32 queries (threads 0-95).
-template <int KP>
+template <int KP, bool GDO>
 __device__ __forceinline__ void stage_cols(TTile<KP>& qt, TTile<KP>& ot, RTile<KP>& gt, float& st, const float* Qb,
                                            const float* Ob, const float* Gb, const float* mb, const float* lb,
                                            const float* Rb, const FlashBwdArgs& a, int M, int i0)
 {
     qt.load(Qb, a.K, M, i0, threadIdx.x);
     ot.load(Ob, a.Kd, M, i0, threadIdx.x);
-    gt.load(Gb, a.ldg, a.K, M, i0, threadIdx.x);
+    if constexpr (!GDO) gt.load(Gb, a.ldg, a.K, M, i0, threadIdx.x);
     if (threadIdx.x < 96)
     {
         const int i = i0 + static_cast<int>(threadIdx.x & 31), which = threadIdx.x >> 5;
@@ -759,24 +775,28 @@ __device__ __forceinline__ void stage_cols(TTile<KP>& qt, TTile<KP>& ot, RTile<K
 // Scores of one cell of the key-line kernel for this lane's key (16 queries
 // drow(r,h)): alpha * dot + mask, -inf outside the (M, N) plane.
 template <bool FULL, bool MASKED>
-__device__ __forceinline__ void col_scores(const f32x16& s, const FlashBwdArgs& a, int ibase, int jc, int kj, int h,
-                                           int M, int N, float* x)
+__device__ __forceinline__ void col_scores(const f32x16& s, const FlashBwdArgs& a, const float* mask, int ibase,
+                                           int jc, int kj, int h, int M, int N, float* x)
 {
-    // The 16 mask loads are issued together (clamped indices, no branch), then used.
-    float mv[16];
-    if constexpr (MASKED)
-    {
+    // Mask loads are issued 8 at a time (clamped indices, no branch), then used.
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mv[r] = a.mask[(long)min(ibase + drow(r, h), M - 1) * N + jc];
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
+    for (int r0 = 0; r0 < 16; r0 += 8)
     {
-        const int i = ibase + drow(r, h);
-        float v = a.alpha * s[r];
-        if constexpr (MASKED) v += mv[r];
-        if constexpr (!FULL) v = (i < M && kj < N) ? v : kNegInf;
-        x[r] = v;
+        float mv[8];
+        if constexpr (MASKED)
+        {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) mv[r] = mask[(long)min(ibase + drow(r0 + r, h), M - 1) * N + jc];
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+        {
+            const int i = ibase + drow(r0 + r, h);
+            float v = a.alpha * s[r0 + r];
+            if constexpr (MASKED) v += mv[r];
+            if constexpr (!FULL) v = (i < M && kj < N) ? v : kNegInf;
+            x[r0 + r] = v;
+        }
     }
 }
 
@@ -819,7 +839,7 @@ __device__ __forceinline__ void cols_store(const FlashBwdArgs& a, const FlashGeo
         }
 }
 
-template <int KP>
+template <int KP, bool GDO>
 __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo& g, int b, int grp, int rg,
                                            float (*Qs)[32][KP + 4], float (*Os)[32][KP + 4],
                                            float (*Gs)[32][KP + 4], float (*St)[3][32], unsigned long long* nz_s)
@@ -827,7 +847,7 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
     constexpr int DU = KP / 32;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const int line = grp * kWaves + wave, kj = line * 32 + c;
-    const LineWork lw = line_work(g, false, line, rg);
+    const LineWork lw = line_work(g, false, b, line, rg);
     if (lane == 0) nz_s[wave] = lw.nz;
     __syncthreads();
     const unsigned long long any = nz_s[0] | nz_s[1] | nz_s[2] | nz_s[3];
@@ -855,21 +875,22 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
         float st = 0.0f;
         int cur = __builtin_ctzll(any);
         unsigned long long rest = any & (any - 1);
-        stage_cols(qt, ot, gt, st, Qb, Ob, Gb, mb, lb, Rb, a, g.M, 32 * (cell0 + cur));
+        stage_cols<KP, GDO>(qt, ot, gt, st, Qb, Ob, Gb, mb, lb, Rb, a, g.M, 32 * (cell0 + cur));
         float kf[KP / 2], vf[KP / 2];
         line_operand<KP>(Kb, a.K, g.N, kj, h, kf);
         line_operand<KP>(Vb, a.Kd, g.N, kj, h, vf);
         const int jc = min(kj, g.N - 1);
+        const float* mk = a.mask ? a.mask + b * a.mask_bs : nullptr;
         qt.store(Qs[0], threadIdx.x);
         ot.store(Os[0], threadIdx.x);
-        gt.store(Gs[0], threadIdx.x);
+        if constexpr (!GDO) gt.store(Gs[0], threadIdx.x);
         if (threadIdx.x < 96) St[0][threadIdx.x >> 5][threadIdx.x & 31] = st;
         __syncthreads();
         int buf = 0;
         while (true)
         {
             const int nxt = rest ? __builtin_ctzll(rest) : -1;
-            if (nxt >= 0) stage_cols(qt, ot, gt, st, Qb, Ob, Gb, mb, lb, Rb, a, g.M, 32 * (cell0 + nxt));
+            if (nxt >= 0) stage_cols<KP, GDO>(qt, ot, gt, st, Qb, Ob, Gb, mb, lb, Rb, a, g.M, 32 * (cell0 + nxt));
             if ((lw.nz >> cur) & 1ull)
             {
                 const int ibase = 32 * (cell0 + cur);
@@ -878,13 +899,13 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
                 float w[16], ds[16];
                 const bool gen = (lw.gen >> cur) & 1ull, full = ibase + 32 <= g.M && (line + 1) * 32 <= g.N;
                 if (full && !gen)
-                    col_scores<true, false>(s, a, ibase, jc, kj, h, g.M, g.N, w);
+                    col_scores<true, false>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
                 else if (full)
-                    col_scores<true, true>(s, a, ibase, jc, kj, h, g.M, g.N, w);
+                    col_scores<true, true>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
                 else if (!gen)
-                    col_scores<false, false>(s, a, ibase, jc, kj, h, g.M, g.N, w);
+                    col_scores<false, false>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
                 else
-                    col_scores<false, true>(s, a, ibase, jc, kj, h, g.M, g.N, w);
+                    col_scores<false, true>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                 {
@@ -892,13 +913,16 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
                     w[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(w[r], kLog2e, -St[buf][0][ii])) * St[buf][1][ii];
                     ds[r] = w[r] * (a.alpha2 * p[r] - St[buf][2][ii]);
                 }
-                value_chain<KP>(Gs[buf], w, h, c, dv);
+                if constexpr (GDO)
+                    value_chain<KP>(Os[buf], w, h, c, dv);
+                else
+                    value_chain<KP>(Gs[buf], w, h, c, dv);
                 value_chain<KP>(Qs[buf], ds, h, c, dk);
             }
             if (nxt < 0) break;
             qt.store(Qs[buf ^ 1], threadIdx.x);
             ot.store(Os[buf ^ 1], threadIdx.x);
-            gt.store(Gs[buf ^ 1], threadIdx.x);
+            if constexpr (!GDO) gt.store(Gs[buf ^ 1], threadIdx.x);
             if (threadIdx.x < 96) St[buf ^ 1][threadIdx.x >> 5][threadIdx.x & 31] = st;
             __syncthreads();
             buf ^= 1;
@@ -909,16 +933,16 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
     cols_store<KP>(a, g, lw, b, line, rg, dk, dv);
 }
 
-template <int KP>
+template <int KP, bool GDO>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdArgs a, FlashGeo g)
 {
     __shared__ __align__(16) float Qs[2][32][KP + 4];   // query tile [query][dim]
     __shared__ __align__(16) float Os[2][32][KP + 4];   // dO tile [query][dim]
-    __shared__ __align__(16) float Gs[2][32][KP + 4];   // G tile [query][dim]
+    __shared__ __align__(16) float Gs[GDO ? 1 : 2][32][KP + 4];   // G tile [query][dim] (GDO: the dO tile)
     __shared__ float St[2][3][32];                      // m, 1/l, R of the tile's queries
     __shared__ unsigned long long nz_s[kWaves];
     const Item it = item_of(g);
-    cols_group<KP>(a, g, it.b, it.grp, it.rg, Qs, Os, Gs, St, nz_s);
+    cols_group<KP, GDO>(a, g, it.b, it.grp, it.rg, Qs, Os, Gs, St, nz_s);
 }
 
 template <int KP>
@@ -928,7 +952,7 @@ __global__ __launch_bounds__(64) void k_flash_bwd_cols_combine(FlashBwdArgs a, F
     const int lane = threadIdx.x;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.CT), line = static_cast<int>(lidx % g.CT);
-    const LineWork lw = line_work(g, false, line, 0);
+    const LineWork lw = line_work(g, false, b, line, 0);
     if (lw.nne <= 1) return;
     f32x16 dk[DU], dv[DU];
 #pragma unroll
@@ -957,11 +981,13 @@ __global__ __launch_bounds__(64) void k_flash_bwd_cols_combine(FlashBwdArgs a, F
     cols_store<KP>(a, g, one, b, line, 0, dk, dv);
 }
 
-// Mask cell classes: 0 all -inf, 1 all zero, 2 general.
-__global__ __launch_bounds__(256) void k_flash_classify(const float* __restrict__ mask, int M, int N, int CT,
-                                                        unsigned char* __restrict__ cls)
+// Mask cell classes: 0 all -inf, 1 all zero, 2 general. blockIdx.z: which mask.
+__global__ __launch_bounds__(256) void k_flash_classify(const float* __restrict__ mask, long mask_bs, int M, int N,
+                                                        int CT, unsigned char* __restrict__ cls)
 {
     const int jb = blockIdx.x, ib = blockIdx.y;
+    mask += blockIdx.z * mask_bs;
+    cls += (long)blockIdx.z * gridDim.y * CT;
     int finite = 0, nonzero = 0;
     for (int e = threadIdx.x; e < 1024; e += 256)
     {
@@ -998,8 +1024,10 @@ void ranges(size_t items, int cells, int& R, int& NR)
     NR = (cells + R - 1) / R;
 }
 
-// Geometry of a row kernel (lines = query tiles) or a column kernel (lines = key tiles).
-FlashGeo geo(size_t batch, size_t M, size_t N, bool rows, int pw, const unsigned char* cls, void* ws)
+// Geometry of a row kernel (lines = query tiles) or a column kernel (lines = key tiles);
+// per_batch_cls: every batch entry has its own cell table.
+FlashGeo geo(size_t batch, size_t M, size_t N, bool rows, int pw, const unsigned char* cls, void* ws,
+             bool per_batch_cls = false)
 {
     FlashGeo g{};
     g.M = static_cast<int>(M);
@@ -1011,6 +1039,7 @@ FlashGeo geo(size_t batch, size_t M, size_t N, bool rows, int pw, const unsigned
     ranges(batch * g.G, cells, g.R, g.NR);
     g.pw = pw;
     g.cls = cls;
+    g.cls_bs = per_batch_cls ? static_cast<long>(g.RT) * g.CT : 0;
     g.part = static_cast<float*>(ws);
     return g;
 }
@@ -1033,7 +1062,12 @@ int cols_pw(int KP) { return 64 * KP; }
 template <int KP, int DP, bool WITH_O>
 int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g, size_t batch, hipStream_t s)
 {
-    hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O>), dim3(grid_of(g, batch)), dim3(64 * kWaves), 0, s, a, g);
+    if (WITH_O && a.v_dm)
+        hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true>), dim3(grid_of(g, batch)), dim3(64 * kWaves), 0, s, a,
+                           g);
+    else
+        hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, false>), dim3(grid_of(g, batch)), dim3(64 * kWaves), 0, s, a,
+                           g);
     if (int rc = launch_status()) return rc;
     if (g.NR == 1) return 0;
     hipLaunchKernelGGL((k_flash_fwd_combine<DP, WITH_O>), dim3(static_cast<unsigned>(batch * g.RT)), dim3(64), 0, s,
@@ -1052,7 +1086,10 @@ int launch_bwd(const FlashBwdArgs& a, const FlashGeo& gr, const FlashGeo& gc, si
                            s, a, gr);
         if (int rc = launch_status()) return rc;
     }
-    hipLaunchKernelGGL((k_flash_bwd_cols<KP>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a, gc);
+    if (a.g_do)
+        hipLaunchKernelGGL((k_flash_bwd_cols<KP, true>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a, gc);
+    else
+        hipLaunchKernelGGL((k_flash_bwd_cols<KP, false>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a, gc);
     if (int rc = launch_status()) return rc;
     if (gc.NR == 1) return 0;
     hipLaunchKernelGGL((k_flash_bwd_cols_combine<KP>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(64), 0, s, a,
@@ -1074,11 +1111,12 @@ bool flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D)
 
 size_t flash_cells_bytes(size_t M, size_t N) { return ((M + 31) / 32) * ((N + 31) / 32); }
 
-int flash_classify(const float* mask, size_t M, size_t N, void* cells, hipStream_t s)
+int flash_classify(const float* mask, size_t masks, long mask_bs, size_t M, size_t N, void* cells, hipStream_t s)
 {
     const unsigned RT = static_cast<unsigned>((M + 31) / 32), CT = static_cast<unsigned>((N + 31) / 32);
-    hipLaunchKernelGGL(k_flash_classify, dim3(CT, RT), dim3(256), 0, s, mask, static_cast<int>(M),
-                       static_cast<int>(N), static_cast<int>(CT), static_cast<unsigned char*>(cells));
+    hipLaunchKernelGGL(k_flash_classify, dim3(CT, RT, static_cast<unsigned>(masks)), dim3(256), 0, s, mask, mask_bs,
+                       static_cast<int>(M), static_cast<int>(N), static_cast<int>(CT),
+                       static_cast<unsigned char*>(cells));
     return launch_status();
 }
 
@@ -1094,7 +1132,7 @@ int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batc
 {
     const int KP = pad32(static_cast<size_t>(a.K)), DP = a.O ? pad32(static_cast<size_t>(a.D)) : 32;
     const FlashGeo g = geo(batch, static_cast<size_t>(a.M), static_cast<size_t>(a.N), true, fwd_pw(DP),
-                           a.mask ? cells : nullptr, ws);
+                           a.mask ? cells : nullptr, ws, a.mask && a.mask_bs != 0);
     if (g.NR > 1 && !ws) return -1;
     if (!a.O) return KP == 32 ? launch_fwd<32, 32, false>(a, g, batch, s) : launch_fwd<64, 32, false>(a, g, batch, s);
     if (KP == 32) return DP == 32 ? launch_fwd<32, 32, true>(a, g, batch, s) : launch_fwd<32, 64, true>(a, g, batch, s);
@@ -1105,8 +1143,11 @@ int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t bat
 {
     const int KP = pad32(static_cast<size_t>(std::max(a.K, a.Kd)));
     const unsigned char* cl = a.mask ? cells : nullptr;
-    const FlashGeo gr = geo(batch, static_cast<size_t>(a.M), static_cast<size_t>(a.N), true, rows_pw(KP), cl, ws);
-    const FlashGeo gc = geo(batch, static_cast<size_t>(a.M), static_cast<size_t>(a.N), false, cols_pw(KP), cl, ws);
+    const bool pb = a.mask && a.mask_bs != 0;
+    const FlashGeo gr =
+        geo(batch, static_cast<size_t>(a.M), static_cast<size_t>(a.N), true, rows_pw(KP), cl, ws, pb);
+    const FlashGeo gc =
+        geo(batch, static_cast<size_t>(a.M), static_cast<size_t>(a.N), false, cols_pw(KP), cl, ws, pb);
     if ((gr.NR > 1 || gc.NR > 1) && !ws) return -1;
     return KP == 32 ? launch_bwd<32>(a, gr, gc, batch, s) : launch_bwd<64>(a, gr, gc, batch, s);
 }
@@ -1123,9 +1164,17 @@ extern "C" size_t nnhip_flash_cells_bytes(size_t M, size_t N) { return nnhip::fl
 
 extern "C" int nnhip_flash_classify(const float* mask, size_t M, size_t N, void* cells, void* stream)
 {
-    if (!mask || !cells || M == 0 || N == 0) return -1;
-    if (M > (size_t{1} << 24) || N > (size_t{1} << 24)) return -3;
-    return nnhip::flash_classify(mask, M, N, cells, static_cast<hipStream_t>(stream));
+    return nnhip_flash_classify_batched(mask, 1, 0, M, N, cells, stream);
+}
+
+extern "C" int nnhip_flash_classify_batched(const float* mask, size_t masks, size_t mask_batch_stride, size_t M,
+                                            size_t N, void* cells, void* stream)
+{
+    if (!mask || !cells || M == 0 || N == 0 || masks == 0) return -1;
+    if (masks > 1 && mask_batch_stride < M * N) return -1;
+    if (M > (size_t{1} << 24) || N > (size_t{1} << 24) || masks > 65535) return -3;
+    return nnhip::flash_classify(mask, masks, static_cast<long>(mask_batch_stride), M, N, cells,
+                                 static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t nnhip_flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D, int backward)
@@ -1137,10 +1186,23 @@ extern "C" int nnhip_flash_forward(const float* Q, const float* Kt, const float*
                                    const void* cells, float* m, float* l, float* O, size_t batch, size_t M, size_t N,
                                    size_t K, size_t D, float alpha, void* workspace, void* stream)
 {
+    return nnhip_flash_forward_layout(Q, Kt, V, mask, cells, m, l, O, batch, M, N, K, D, alpha, 0, 0, 0, workspace,
+                                      stream);
+}
+
+extern "C" int nnhip_flash_forward_layout(const float* Q, const float* Kt, const float* V, const float* mask,
+                                          const void* cells, float* m, float* l, float* O, size_t batch, size_t M,
+                                          size_t N, size_t K, size_t D, float alpha, size_t mask_batch_stride,
+                                          int v_dim_major, int o_dim_major, void* workspace, void* stream)
+{
     if (!Q || !Kt || !m || !l || (O && !V) || (mask && !cells)) return -1;
+    if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
     if (!nnhip::flash_supported(batch, M, N, K, O ? D : 4)) return -3;
     nnhip::FlashFwdArgs a{Q, Kt, V, mask, m, l, O, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
                           static_cast<int>(O ? D : 4), alpha};
+    a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
+    a.v_dm = v_dim_major ? 1 : 0;
+    a.o_dm = o_dim_major ? 1 : 0;
     return nnhip::flash_forward(a, static_cast<const unsigned char*>(cells), batch, workspace,
                                 static_cast<hipStream_t>(stream));
 }
@@ -1150,10 +1212,28 @@ extern "C" int nnhip_flash_backward(const float* Q, const float* Kt, const float
                                     float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M, size_t N,
                                     size_t K, size_t Kd, float alpha, float alpha2, void* workspace, void* stream)
 {
-    if (!Q || !Kt || !dO || !Vp || !G || !m || !l || !R || !dQ || !dK || !dV || (mask && !cells)) return -1;
+    if (!G) return -1;
+    return nnhip_flash_backward_layout(Q, Kt, dO, Vp, G, ldg, mask, cells, m, l, R, dQ, dK, dV, batch, M, N, K, Kd,
+                                       alpha, alpha2, 0, 0, workspace, stream);
+}
+
+extern "C" int nnhip_flash_backward_layout(const float* Q, const float* Kt, const float* dO, const float* Vp,
+                                           const float* G, size_t ldg, const float* mask, const void* cells,
+                                           const float* m, const float* l, float* R, float* dQ, float* dK, float* dV,
+                                           size_t batch, size_t M, size_t N, size_t K, size_t Kd, float alpha,
+                                           float alpha2, size_t mask_batch_stride, int g_is_do, void* workspace,
+                                           void* stream)
+{
+    if (!Q || !Kt || !dO || !Vp || (!G && !g_is_do) || !m || !l || !R || !dQ || !dK || !dV || (mask && !cells))
+        return -1;
+    if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
+    if (g_is_do && Kd != K) return -1;
+    if (g_is_do) ldg = K;
     if (!nnhip::flash_supported(batch, M, N, K > Kd ? K : Kd, 4) || K % 4 != 0 || ldg < K || ldg % 4 != 0) return -3;
     nnhip::FlashBwdArgs a{Q, Kt, dO, Vp, G, mask, m, l, R, dQ, dK, dV, static_cast<int>(M), static_cast<int>(N),
                           static_cast<int>(K), static_cast<int>(Kd), static_cast<int>(ldg), alpha, alpha2};
+    a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
+    a.g_do = g_is_do ? 1 : 0;
     return nnhip::flash_backward(a, static_cast<const unsigned char*>(cells), batch, workspace,
                                  static_cast<hipStream_t>(stream));
 }

@@ -165,6 +165,7 @@ private:
     {
         Tensor mask;
         std::shared_ptr<DeviceBuffer> cells;
+        std::size_t M;   // rows of one mask (the tensor holds rows / M of them)
     };
     std::vector<CellTable> cells_;
     Result<const void*> mask_cells_(const Tensor* mask, std::size_t M, std::size_t N);
@@ -173,6 +174,28 @@ private:
     struct PendingGemm;
     struct PendingBwd;
     struct PendingEw;
+    struct PendingMaskAdd;
+    struct PendingAttn;
+    struct PendingDv;
+    struct PendingDs;
+    struct AttnGrads;
+    std::unique_ptr<PendingMaskAdd> pmadd_;
+    std::vector<std::shared_ptr<PendingAttn>> pattn_;   // one per layer between forward and backward
+    std::unique_ptr<PendingDv> pdv_;
+    std::unique_ptr<PendingDs> pds_;
+    std::unique_ptr<AttnGrads> pgrads_;
+    Result<void> settle_madd_();
+    Result<void> settle_dv_();
+    Result<void> settle_ds_();
+    Result<void> materialise_attn_(PendingAttn& p);
+    void forget_dead_attn_();
+    std::shared_ptr<PendingAttn> attn_of_(const Tensor& A) const;
+    Result<void> scores_masked_(const Tensor& Q, const Tensor& K, const Tensor& mask, std::size_t batch, std::size_t M,
+                                std::size_t N, std::size_t Kd, float alpha, const Tensor& out);
+    Result<std::optional<Tensor>> attn_bmm_(const Tensor& A, const Tensor& B, std::size_t batch, bool tA, bool tB,
+                                            Scalar alpha);
+    Result<std::optional<Tensor>> attn_softmax_(const ExprSpec& spec, std::span<const Tensor> inputs,
+                                                std::size_t rows, std::size_t cols);
     std::unique_ptr<PendingFwd> pfwd_;
     std::unique_ptr<PendingGemm> pgemm_;
     std::unique_ptr<PendingBwd> pbwd_;
