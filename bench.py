@@ -421,6 +421,8 @@ def main():
     ap.add_argument("--skip-hbm", action="store_true")
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run only the workload the rocprofv3 --pmc passes count (one step + a calibration copy)")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="run only the attention leg (configs 2 and 5) and print its JSON (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
@@ -429,6 +431,9 @@ def main():
 
     if args.pmc_sample:
         pmc_sample(args.seed)
+        return
+    if args.attention_only:
+        print(json.dumps({"attention": attention_leg(args.seed)}), flush=True)
         return
     gpu = gpu_leg(args.steps, args.warmup, args.seed)
     attn = None if args.skip_attention else attention_leg(args.seed)
