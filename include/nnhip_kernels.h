@@ -66,6 +66,15 @@ int nnhip_elementwise_select_scalar_cond(const float* A, const float* then_v, fl
 int nnhip_adam_update(float* p, float* m, float* v, const float* g, size_t count, int has_decay, float decay,
                       float beta1, float one_minus_beta1, float beta2, float one_minus_beta2, float inv_bc1,
                       float inv_bc2, float eps, float neg_lr, void* stream);
+/* SwiGLU forward (reference compute_layer.hpp, SwiGLU::forward, a chain of six primitives:
+ * Neg, Exp, + c_add, c_div / x, gate * s, * up) in one pass with the same roundings:
+ * s = c_div / (exp(-gate) + c_add) (stored when s_out is not null), out = (gate * s) * up.
+ * No CUDA counterpart; HipEngine issues it when it recognises that chain among deferred calls. */
+int nnhip_swiglu_forward(const float* gate, const float* up, float* s_out, float* out, size_t count, float c_add,
+                         float c_div, void* stream);
+/* Zeroes n device buffers (ptrs[i], counts[i] floats) in as few launches as possible (consecutive
+ * ComputeEngine::zero calls, e.g. Optimizer::zero_grad, compute_optimizer.hpp:142-151). */
+int nnhip_zero_list(float* const* ptrs, const size_t* counts, size_t n, void* stream);
 /* out[i] = value (used for ComputeEngine::zero; no CUDA counterpart, CUDA uses cudaMemset). */
 int nnhip_fill(float* out, size_t count, float value, void* stream);
 

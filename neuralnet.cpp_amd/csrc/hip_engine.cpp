@@ -282,10 +282,17 @@ struct HipEngine::PendingBwd
     bool yields(const float* p) const { return has_buf(dQ, p) || has_buf(R, p); }
 };
 
-namespace
-{
 enum EwCode : std::uint8_t { kBin, kScalar, kUnary, kAxpy, kCopy };
-}
+
+// One call of a recognised chain of deferred elementwise calls: code, op,
+// scalar-first flag and the roles of its destination and operands (b < 0: not read).
+struct RunStep
+{
+    EwCode code;
+    unsigned op;
+    std::uint8_t first;
+    int dst, a, b;
+};
 
 // Consecutive same-size elementwise calls (scale / axpy / add in place; unary,
 // binary, scalar and clone into new tensors), recorded in call order. Slots
@@ -383,33 +390,40 @@ namespace
 // (reference compute_optimizer.hpp:252-304): the tensors it touches, by role,
 // and its calls in order. AdamW (:388-412) puts scale_inplace(p, decay) first.
 enum AdamRole { rP, rM, rG, rV, rG2, rMH, rVH, rSQ, rDEN, rR, kAdamRoles };
-struct AdamStep
-{
-    EwCode code;
-    unsigned op;
-    int dst, a, b;   // roles; b < 0: not read
-};
 constexpr unsigned kMul = static_cast<unsigned>(BinaryOp::Mul), kAdd = static_cast<unsigned>(BinaryOp::Add),
-                   kDiv = static_cast<unsigned>(BinaryOp::Div), kSqrt = static_cast<unsigned>(UnaryOp::Sqrt);
-constexpr AdamStep kAdamDecay = {kScalar, kMul, rP, rP, -1};
-constexpr AdamStep kAdamSteps[] = {
-    {kScalar, kMul, rM, rM, -1},      // m *= beta1
-    {kAxpy, 0, rM, rM, rG},           // m += (1 - beta1) g
-    {kScalar, kMul, rV, rV, -1},      // v *= beta2
-    {kBin, kMul, rG2, rG, rG},        // g2 = g * g
-    {kScalar, kMul, rG2, rG2, -1},    // g2 *= 1 - beta2
-    {kBin, kAdd, rV, rV, rG2},        // v += g2
-    {kCopy, 0, rMH, rM, -1},          // m_hat = clone(m)
-    {kScalar, kMul, rMH, rMH, -1},    // m_hat *= inv_bc1
-    {kCopy, 0, rVH, rV, -1},          // v_hat = clone(v)
-    {kScalar, kMul, rVH, rVH, -1},    // v_hat *= inv_bc2
-    {kUnary, kSqrt, rSQ, rVH, -1},    // sq = sqrt(v_hat)
-    {kScalar, kAdd, rDEN, rSQ, -1},   // den = sq + eps
-    {kBin, kDiv, rR, rMH, rDEN},      // ratio = m_hat / den
-    {kScalar, kMul, rR, rR, -1},      // ratio *= -lr
-    {kBin, kAdd, rP, rP, rR},         // p += ratio
+                   kDiv = static_cast<unsigned>(BinaryOp::Div), kSqrt = static_cast<unsigned>(UnaryOp::Sqrt),
+                   kNeg = static_cast<unsigned>(UnaryOp::Neg), kExp = static_cast<unsigned>(UnaryOp::Exp);
+constexpr RunStep kAdamSteps[] = {
+    {kScalar, kMul, 0, rP, rP, -1},       // p *= 1 - lr * wd (AdamW only)
+    {kScalar, kMul, 0, rM, rM, -1},       // m *= beta1
+    {kAxpy, 0, 0, rM, rM, rG},            // m += (1 - beta1) g
+    {kScalar, kMul, 0, rV, rV, -1},       // v *= beta2
+    {kBin, kMul, 0, rG2, rG, rG},         // g2 = g * g
+    {kScalar, kMul, 0, rG2, rG2, -1},     // g2 *= 1 - beta2
+    {kBin, kAdd, 0, rV, rV, rG2},         // v += g2
+    {kCopy, 0, 0, rMH, rM, -1},           // m_hat = clone(m)
+    {kScalar, kMul, 0, rMH, rMH, -1},     // m_hat *= inv_bc1
+    {kCopy, 0, 0, rVH, rV, -1},           // v_hat = clone(v)
+    {kScalar, kMul, 0, rVH, rVH, -1},     // v_hat *= inv_bc2
+    {kUnary, kSqrt, 0, rSQ, rVH, -1},     // sq = sqrt(v_hat)
+    {kScalar, kAdd, 0, rDEN, rSQ, -1},    // den = sq + eps
+    {kBin, kDiv, 0, rR, rMH, rDEN},       // ratio = m_hat / den
+    {kScalar, kMul, 0, rR, rR, -1},       // ratio *= -lr
+    {kBin, kAdd, 0, rP, rP, rR},          // p += ratio
 };
-constexpr std::size_t kAdamLen = sizeof(kAdamSteps) / sizeof(kAdamSteps[0]);
+constexpr std::size_t kAdamLen = sizeof(kAdamSteps) / sizeof(kAdamSteps[0]) - 1;   // without the decay
+
+// SwiGLU::forward's chain (its sigmoid written out as primitives).
+enum SwigluRole { sG, sU, sT1, sT2, sT3, sS, sSW, sO, kSwigluRoles };
+constexpr RunStep kSwigluSteps[] = {
+    {kUnary, kNeg, 0, sT1, sG, -1},       // t1 = -gate
+    {kUnary, kExp, 0, sT2, sT1, -1},      // t2 = exp(t1)
+    {kScalar, kAdd, 0, sT3, sT2, -1},     // t3 = t2 + 1
+    {kScalar, kDiv, 1, sS, sT3, -1},      // s = 1 / t3
+    {kBin, kMul, 0, sSW, sG, sS},         // sw = gate * s
+    {kBin, kMul, 0, sO, sSW, sU},         // out = sw * up
+};
+constexpr std::size_t kSwigluLen = sizeof(kSwigluSteps) / sizeof(kSwigluSteps[0]);
 
 } // namespace
 
@@ -542,6 +556,7 @@ Result<void> HipEngine::need_gpu_(std::initializer_list<const Tensor*> ts, const
 // ── deferred work: launch on demand ─────────────────────────────────────────
 Result<void> HipEngine::settle_reads_(std::initializer_list<const Tensor*> ts)
 {
+    NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
     return settle_chain_reads_(ts);
 }
@@ -590,6 +605,7 @@ Result<const void*> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, st
 
 Result<void> HipEngine::settle_write_(const Tensor& t)
 {
+    NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
     return settle_chain_write_(t);
 }
@@ -622,6 +638,7 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t)
 
 Result<void> HipEngine::settle()
 {
+    NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
     NN_CHECK(settle_madd_());
     NN_CHECK(settle_dv_());
@@ -841,6 +858,7 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
 Result<void> HipEngine::ew_push_(unsigned code, unsigned op, bool first, const Tensor& dst, const Tensor& a,
                                  const Tensor* b, float s)
 {
+    NN_CHECK(settle_zero_());
     const std::size_t n = dst.size();
     if (pew_ && (pew_->n != n || pew_->full())) NN_CHECK(settle_ew_());
     if (!pew_)
@@ -879,6 +897,11 @@ Result<void> HipEngine::settle_ew_()
     for (std::size_t i = 0; i < ops.size();)
     {
         NN_TRY(k, adam_run_(*g, i, last_read));
+        if (!k)
+        {
+            NN_TRY(k2, swiglu_run_(*g, i, last_read));
+            k = k2;
+        }
         if (k)
         {
             i += k;
@@ -911,6 +934,34 @@ Result<void> HipEngine::settle_ew_()
     return {};
 }
 
+// True when calls i, i+1, ... of the record are `steps` with one distinct
+// buffer per role; slot_of[role] receives the slots.
+bool HipEngine::match_run_(const PendingEw& g, std::size_t i, const RunStep* steps, std::size_t len, int nroles,
+                           int* slot_of)
+{
+    if (i + len > g.ops.size()) return false;
+    for (int r = 0; r < nroles; ++r) slot_of[r] = -1;
+    std::vector<int> role_of(g.slots.size(), -1);
+    auto bind = [&](int role, int slot) {
+        if (slot_of[role] < 0 && role_of[slot] < 0)
+        {
+            slot_of[role] = slot;
+            role_of[slot] = role;
+            return true;
+        }
+        return slot_of[role] == slot;
+    };
+    for (std::size_t j = 0; j < len; ++j)
+    {
+        const RunStep& st = steps[j];
+        const PendingEw::Op& o = g.ops[i + j];
+        if (!(o.code == st.code && o.op == st.op && o.first == st.first && bind(st.a, o.a) &&
+              (st.b < 0 || bind(st.b, o.b)) && bind(st.dst, o.dst)))
+            return false;
+    }
+    return true;
+}
+
 // If calls i.. of the record are an Adam(W) update chain whose temporaries
 // nobody keeps, launches it as one pass and returns its length; else 0.
 Result<std::size_t> HipEngine::adam_run_(const PendingEw& g, std::size_t i,
@@ -920,28 +971,9 @@ Result<std::size_t> HipEngine::adam_run_(const PendingEw& g, std::size_t i,
     for (int decay = 1; decay >= 0; --decay)
     {
         const std::size_t len = kAdamLen + static_cast<std::size_t>(decay);
-        if (i + len > ops.size()) continue;
         int slot_of[kAdamRoles];
-        std::fill(std::begin(slot_of), std::end(slot_of), -1);
-        std::vector<int> role_of(g.slots.size(), -1);
-        auto bind = [&](int role, int slot) {
-            if (slot_of[role] < 0 && role_of[slot] < 0)
-            {
-                slot_of[role] = slot;
-                role_of[slot] = role;
-                return true;
-            }
-            return slot_of[role] == slot;
-        };
+        if (!match_run_(g, i, kAdamSteps + (decay ? 0 : 1), len, kAdamRoles, slot_of)) continue;
         bool ok = true;
-        for (std::size_t j = 0; ok && j < len; ++j)
-        {
-            const AdamStep& st = decay ? (j == 0 ? kAdamDecay : kAdamSteps[j - 1]) : kAdamSteps[j];
-            const PendingEw::Op& o = ops[i + j];
-            ok = o.code == st.code && o.op == st.op && o.first == 0 && bind(st.a, o.a) &&
-                 (st.b < 0 || bind(st.b, o.b)) && bind(st.dst, o.dst);
-        }
-        if (!ok) continue;
         for (int r = rG2; ok && r <= rR; ++r)
             ok = !live(g.slots[slot_of[r]]) && last_read[slot_of[r]] < static_cast<std::ptrdiff_t>(i + len);
         if (!ok) continue;
@@ -955,6 +987,25 @@ Result<std::size_t> HipEngine::adam_run_(const PendingEw& g, std::size_t i,
         return len;
     }
     return std::size_t{0};
+}
+
+// Same for SwiGLU::forward's chain: gate and up read once, s (when kept or
+// read later) and out written once.
+Result<std::size_t> HipEngine::swiglu_run_(const PendingEw& g, std::size_t i,
+                                           const std::vector<std::ptrdiff_t>& last_read)
+{
+    int slot_of[kSwigluRoles];
+    if (!match_run_(g, i, kSwigluSteps, kSwigluLen, kSwigluRoles, slot_of)) return std::size_t{0};
+    const auto end = static_cast<std::ptrdiff_t>(i + kSwigluLen);
+    for (int r : {sT1, sT2, sT3, sSW})
+        if (live(g.slots[slot_of[r]]) || last_read[slot_of[r]] >= end) return std::size_t{0};
+    const Tensor& S = g.slots[slot_of[sS]];
+    const bool keep_s = live(S) || last_read[slot_of[sS]] >= end;
+    NN_CHECK(kernel_(nnhip_swiglu_forward(D(g.slots[slot_of[sG]]), D(g.slots[slot_of[sU]]), keep_s ? W(S) : nullptr,
+                                          W(g.slots[slot_of[sO]]), g.n, g.ops[i + 2].s, g.ops[i + 3].s,
+                                          static_cast<hipStream_t>(stream_)),
+                     "swiglu forward"));
+    return kSwigluLen;
 }
 
 Result<Tensor> HipEngine::alloc_(std::size_t rows, std::size_t cols)
@@ -1427,11 +1478,32 @@ Result<void> HipEngine::axpy_inplace(Tensor& A, Scalar s, const Tensor& B)
     return ew_push_(kAxpy, 0, false, A, A, &B, s);
 }
 
+// Consecutive zero calls (Optimizer::zero_grad over every gradient) are
+// collected and cleared together, a few launches for all of them.
 Result<void> HipEngine::zero(Tensor& A)
 {
-    NN_CHECK(need_gpu_({&A}, "zero"));
-    NN_CHECK(settle_write_(A));
-    return kernel_(nnhip_fill(W(A), A.size(), 0.0f, stream_), "zero");
+    NN_CHECK(check_gpu_({&A}, "zero"));
+    if (!A.size()) return {};
+    NN_CHECK(settle_ew_());
+    NN_CHECK(settle_chain_write_(A));
+    pzero_.push_back(A);
+    if (pzero_.size() >= 512) return settle_zero_();
+    return {};
+}
+
+Result<void> HipEngine::settle_zero_()
+{
+    if (pzero_.empty()) return {};
+    std::vector<Tensor> ts = std::move(pzero_);
+    pzero_.clear();
+    std::vector<float*> ptrs;
+    std::vector<std::size_t> counts;
+    for (const Tensor& t : ts)
+    {
+        ptrs.push_back(W(t));
+        counts.push_back(t.size());
+    }
+    return kernel_(nnhip_zero_list(ptrs.data(), counts.data(), ptrs.size(), stream_), "zero");
 }
 
 // ── reductions (cpu_engine.hpp:1050-1086) ───────────────────────────────────

@@ -224,10 +224,124 @@ __global__ __launch_bounds__(kThreads) void k_adam(float* p, float* m, float* v,
     }
 }
 
+// The SwiGLU forward chain of engine primitives (reference compute_layer.hpp,
+// SwiGLU::forward: t = -gate, t = exp(t), t = t + c_add, s = c_div / t,
+// sw = gate * s, out = sw * up) in one pass with the same roundings: gate and
+// up read once, s (kept by the layer) and out written once.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void k_swiglu_fwd(const float* gate, const float* up, float* s_out,
+                                                         float* out, size_t n, float c_add, float c_div)
+{
+    const size_t tid = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+    auto one = [&](float g, float u, float& sv, float& o) {
+        sv = c_div / (expf(-g) + c_add);
+        o = (g * sv) * u;
+    };
+    size_t done = 0;
+    if constexpr (VEC)
+    {
+        const size_t n4 = n / 4;
+        for (size_t i = tid; i < n4; i += stride)
+        {
+            const float4 g = reinterpret_cast<const float4*>(gate)[i], u = reinterpret_cast<const float4*>(up)[i];
+            float4 sv, o;
+            one(g.x, u.x, sv.x, o.x);
+            one(g.y, u.y, sv.y, o.y);
+            one(g.z, u.z, sv.z, o.z);
+            one(g.w, u.w, sv.w, o.w);
+            if (s_out) reinterpret_cast<float4*>(s_out)[i] = sv;
+            reinterpret_cast<float4*>(out)[i] = o;
+        }
+        done = n4 * 4;
+    }
+    for (size_t i = done + tid; i < n; i += stride)
+    {
+        float sv, o;
+        one(gate[i], up[i], sv, o);
+        if (s_out) s_out[i] = sv;
+        out[i] = o;
+    }
+}
+
+// Zero fill of up to kFillMax tensors in one launch: block ranges per tensor
+// from the prefix sums in `first` (blocks of 256 threads x 4 floats x 4).
+constexpr int kFillMax = 96;
+struct FillList
+{
+    float* p[kFillMax];
+    unsigned long long n[kFillMax];
+    unsigned first[kFillMax + 1];
+    int count;
+};
+__global__ __launch_bounds__(kThreads) void k_fill_list(FillList f)
+{
+    const unsigned b = blockIdx.x;
+    int t = 0;
+    while (t + 1 < f.count && f.first[t + 1] <= b) ++t;
+    const size_t base = static_cast<size_t>(b - f.first[t]) * kThreads * 16, n = f.n[t];
+    float* p = f.p[t];
+    const bool vec = (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+    {
+        const size_t i = base + (static_cast<size_t>(k) * kThreads + threadIdx.x) * 4;
+        if (vec && i + 4 <= n)
+            *reinterpret_cast<float4*>(p + i) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        else
+            for (size_t e = i; e < i + 4 && e < n; ++e) p[e] = 0.0f;
+    }
+}
+
 } // namespace
 } // namespace nnhip
 
 using namespace nnhip;
+
+extern "C" int nnhip_swiglu_forward(const float* gate, const float* up, float* s_out, float* out, size_t count,
+                                    float c_add, float c_div, void* stream)
+{
+    if (count == 0) return 0;
+    if (!gate || !up || !out) return -1;
+    const bool vec = aligned16(gate) && aligned16(up) && aligned16(out) && (!s_out || aligned16(s_out));
+    const unsigned grid = grid_for(vec ? (count + 3) / 4 : count, kThreads, 256 * 32);
+    auto s = static_cast<hipStream_t>(stream);
+    if (vec)
+        hipLaunchKernelGGL(k_swiglu_fwd<true>, dim3(grid), dim3(kThreads), 0, s, gate, up, s_out, out, count, c_add,
+                           c_div);
+    else
+        hipLaunchKernelGGL(k_swiglu_fwd<false>, dim3(grid), dim3(kThreads), 0, s, gate, up, s_out, out, count,
+                           c_add, c_div);
+    return launch_status();
+}
+
+extern "C" int nnhip_zero_list(float* const* ptrs, const size_t* counts, size_t n, void* stream)
+{
+    auto s = static_cast<hipStream_t>(stream);
+    for (size_t i0 = 0; i0 < n; i0 += kFillMax)
+    {
+        FillList f{};
+        unsigned blocks = 0;
+        f.count = 0;
+        for (size_t i = i0; i < n && i < i0 + kFillMax; ++i)
+        {
+            if (counts[i] == 0) continue;
+            if (!ptrs[i]) return -1;
+            const size_t nb = (counts[i] + kThreads * 16 - 1) / (kThreads * 16);
+            if (blocks + nb > 0x7fffffffu) return -3;
+            f.p[f.count] = ptrs[i];
+            f.n[f.count] = counts[i];
+            f.first[f.count] = blocks;
+            blocks += static_cast<unsigned>(nb);
+            ++f.count;
+        }
+        if (f.count == 0) continue;
+        f.first[f.count] = blocks;
+        hipLaunchKernelGGL(k_fill_list, dim3(blocks), dim3(kThreads), 0, s, f);
+        if (int rc = launch_status()) return rc;
+    }
+    return 0;
+}
 
 extern "C" int nnhip_adam_update(float* p, float* m, float* v, const float* g, size_t count, int has_decay,
                                  float decay, float beta1, float one_minus_beta1, float beta2, float one_minus_beta2,

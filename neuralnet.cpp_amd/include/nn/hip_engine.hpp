@@ -45,6 +45,7 @@ namespace nn
 {
 
 class DevicePool;
+struct RunStep;
 
 class HipEngine final : public ComputeEngine
 {
@@ -200,6 +201,8 @@ private:
     std::unique_ptr<PendingGemm> pgemm_;
     std::unique_ptr<PendingBwd> pbwd_;
     std::unique_ptr<PendingEw> pew_;
+    std::vector<Tensor> pzero_;   // zero calls not yet launched
+    Result<void> settle_zero_();
     // Before reading (writing) tensors: launch deferred work that yields
     // (yields or reads) them; the plain forms also launch the elementwise run.
     Result<void> settle_reads_(std::initializer_list<const Tensor*> ts);
@@ -210,6 +213,9 @@ private:
                           float s);
     Result<void> settle_ew_();
     Result<std::size_t> adam_run_(const PendingEw& g, std::size_t i, const std::vector<std::ptrdiff_t>& last_read);
+    Result<std::size_t> swiglu_run_(const PendingEw& g, std::size_t i, const std::vector<std::ptrdiff_t>& last_read);
+    static bool match_run_(const PendingEw& g, std::size_t i, const RunStep* steps, std::size_t len, int nroles,
+                           int* slot_of);
     Result<void> settle_fwd_();
     Result<void> settle_gemm_();
     Result<void> settle_bwd_();

@@ -2,7 +2,9 @@
 
 The engine records consecutive same-size elementwise / in-place calls and runs
 them when another kind of call arrives; the optimizers' Adam / AdamW chain
-(reference compute_optimizer.hpp:252-304, :388-412) runs as one fused pass.
+(reference compute_optimizer.hpp:252-304, :388-412) and SwiGLU::forward's
+sigmoid-gate chain run as one fused pass each. Consecutive zero calls
+(zero_grad) are cleared together.
 Bars: the fused chain is bit-exact against the same calls run one by one (an
 engine settle after every call stops any recording from spanning two calls);
 both are within 1e-6 of max|p| of the CPU oracle. Mixed sequences match the
@@ -139,3 +141,60 @@ def test_zero_size_and_errors(hip):
         hip.add_inplace(a, b)
     hip.scale_inplace(a, 2.0)
     assert np.array_equal(a.numpy(), np.full((3, 4), 2.0, np.float32))
+
+
+def swiglu_chain(e, gate, up, after=lambda: None):
+    """SwiGLU::forward's calls on the gate and up halves (sigmoid written out as primitives)."""
+    t1 = e.elementwise_unary("Neg", gate); after()
+    t2 = e.elementwise_unary("Exp", t1); after()
+    t3 = e.elementwise_binary_scalar("Add", t2, 1.0); after()
+    s = e.elementwise_binary_scalar("Div", t3, 1.0, scalar_first=True); after()
+    sw = e.elementwise_binary("Mul", gate, s); after()
+    out = e.elementwise_binary("Mul", sw, up); after()
+    return s, out
+
+
+@pytest.mark.parametrize("shape", [(3072, 8192), (7, 13), (1, 5), (64, 64)])
+def test_swiglu_forward_fused_matches_calls(hip, cpu, shape):
+    rng = np.random.default_rng(shape[0] * 31 + shape[1])
+    G, U = normal(rng, shape, 3.0), normal(rng, shape)
+
+    def run(e, settle_each):
+        g, u = e.tensor(G), e.tensor(U)
+        s, out = swiglu_chain(e, g, u, e.settle if settle_each else (lambda: None))
+        return s.numpy(), out.numpy()
+
+    fs, fo = run(hip, False)
+    cs, co = run(hip, True)
+    assert np.array_equal(bits(fs), bits(cs)) and np.array_equal(bits(fo), bits(co))
+    rs, ro = run(cpu, False)
+    assert nrm_err(fs, rs) <= 1e-6 and nrm_err(fo, ro) <= 1e-6
+
+
+def test_swiglu_forward_sigmoid_dropped(hip):
+    """The sigmoid dropped before the run is launched: out alone is written."""
+    rng = np.random.default_rng(2)
+    G, U = normal(rng, (40, 64)), normal(rng, (40, 64))
+    g, u = hip.tensor(G), hip.tensor(U)
+    s, out = swiglu_chain(hip, g, u)
+    del s
+    ref = swiglu_chain(hip, hip.tensor(G), hip.tensor(U), hip.settle)[1].numpy()
+    assert np.array_equal(bits(out.numpy()), bits(ref))
+
+
+def test_zero_list(hip):
+    """Consecutive zero calls over tensors of many sizes, then reads and further calls in order."""
+    rng = np.random.default_rng(8)
+    shapes = [(1, 1), (3, 5), (768, 1), (1, 6144), (768, 768), (17, 33), (4096, 5)] * 30
+    arrs = [uniform(rng, s, 1.0, 2.0) for s in shapes]
+    ts = [hip.tensor(a) for a in arrs]
+    keep = hip.tensor(arrs[0])
+    for t in ts:
+        hip.zero(t)
+    hip.add_inplace(ts[3], hip.tensor(arrs[3]))          # an elementwise call after the zeros
+    s = hip.row_reduce_sum(ts[4])                          # another kind of call
+    for i, t in enumerate(ts):
+        got = t.numpy()
+        assert np.array_equal(got, arrs[3] if i == 3 else np.zeros_like(got)), i
+    assert not s.numpy().any()
+    assert np.array_equal(keep.numpy(), arrs[0])
