@@ -167,18 +167,26 @@ class Busy:
 
     def __call__(self):
         for _ in range(2):
-            self.eng.matmul(self.a, self.a)
+            c = self.eng.matmul(self.a, self.a)
+            self.eng.settle()   # matmul is recorded until its result is used: launch it now
+            del c
 
 
 def timed_ms(timer, busy, fn, reps):
-    """Average milliseconds per call of fn over reps back-to-back calls. Work the
-    engine still holds deferred is launched (settle) before the stop event."""
-    fn()
+    """Average milliseconds per call of fn over reps back-to-back calls. The
+    engine records some calls instead of launching them and skips results that
+    nobody references, so each call's outputs are held until settle() has
+    launched what the call recorded, then dropped (the pool hands the same
+    block to the next call)."""
+    keep = fn()
+    busy.eng.settle()
+    del keep
     busy()
     timer.start()
     for _ in range(reps):
-        fn()   # outputs are dropped at once: the pool hands the same block to the next call
-    busy.eng.settle()
+        keep = fn()
+        busy.eng.settle()
+        del keep
     return timer.stop_ms() / reps
 
 

@@ -42,6 +42,15 @@ int nnhip_gemm(const float* A, const float* B, float* C, size_t A_rows, size_t A
                size_t batch, int transA, int transB, float alpha, void* workspace, size_t workspace_bytes,
                void* stream);
 
+/* One product with the epilogue of the call that follows it in the reference's Linear layer
+ * (compute_layer.hpp Linear::forward / backward): C = alpha * op(A) op(B), then C[i][j] += row_bias[i]
+ * (broadcast_row_inplace(C, bias, Add)) when row_bias is not null, and C = C_old + result
+ * (add_inplace(C_old, result)) when accumulate; each addition rounded as the separate call rounds it.
+ * Workspace as nnhip_gemm. No CUDA counterpart. */
+int nnhip_gemm_epilogue(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
+                        size_t B_cols, int transA, int transB, float alpha, const float* row_bias, int accumulate,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* Per batch b: C_b = alpha * op(A_b) op(B_b); A/B split into `batch` row blocks, C stacked (batch*M, N).
  * Replaces cuda_batched_matmul (cuda_kernels.h:49-54); alpha as in ComputeEngine::batched_matmul
  * (compute_engine.hpp:195-199, cpu_engine.hpp:335-419). */

@@ -294,6 +294,17 @@ struct RunStep
     int dst, a, b;
 };
 
+// matmul(A, B) not launched yet (see HipEngine::matmul). `folded`: its product
+// was already added into another tensor; C itself is computed only if read.
+struct HipEngine::PendingMm
+{
+    Tensor A, B, C;
+    bool tA, tB;
+    std::size_t M, N, K;
+    bool folded;
+    bool uses(const float* p) const { return has_buf(A, p) || has_buf(B, p) || has_buf(C, p); }
+};
+
 // Consecutive same-size elementwise calls (scale / axpy / add in place; unary,
 // binary, scalar and clone into new tensors), recorded in call order. Slots
 // are the distinct buffers the calls touch; every result is a real allocation
@@ -568,6 +579,7 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
         if (!t) continue;
         const float* p = t->dev_ptr();
         if (!p) continue;
+        if (pmm_ && has_buf(pmm_->C, p)) NN_CHECK(settle_mm_());
         if (pmadd_ && has_buf(pmadd_->out, p)) NN_CHECK(settle_madd_());
         if (pdv_ && has_buf(pdv_->out, p)) NN_CHECK(settle_dv_());
         if (pds_ && has_buf(pds_->out, p)) NN_CHECK(settle_ds_());
@@ -614,6 +626,7 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t)
 {
     const float* p = t.dev_ptr();
     if (!p) return {};
+    if (pmm_ && pmm_->uses(p)) NN_CHECK(settle_mm_());
     if (pmadd_ && pmadd_->uses(p)) NN_CHECK(settle_madd_());
     if (pdv_ && pdv_->uses(p)) NN_CHECK(settle_dv_());
     if (pds_ && pds_->uses(p)) NN_CHECK(settle_ds_());
@@ -640,6 +653,7 @@ Result<void> HipEngine::settle()
 {
     NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
+    NN_CHECK(settle_mm_());
     NN_CHECK(settle_madd_());
     NN_CHECK(settle_dv_());
     NN_CHECK(settle_ds_());
@@ -1186,7 +1200,19 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
         return fail("matmul: dimension mismatch A=" + std::to_string(A.rows()) + "x" + std::to_string(A.cols()) +
                     " B=" + std::to_string(B.rows()) + "x" + std::to_string(B.cols()));
     NN_TRY(C, alloc_(M, N));
-    const std::size_t wsb = nnhip_gemm_workspace_bytes(M, N, K, 1);
+    if (!C.size()) return C;
+    // Recorded: the Linear layer's next call adds the bias to C or adds C to
+    // the weight gradient (compute_layer.hpp Linear), both folded into the
+    // product's epilogue; any other use launches the plain product.
+    NN_CHECK(settle_mm_());
+    pmm_ = std::make_unique<PendingMm>(PendingMm{A, B, C, tA, tB, M, N, K, false});
+    return C;
+}
+
+// The recorded matmul into `out`: out = A B (+ bias per row) or out += A B.
+Result<void> HipEngine::launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate)
+{
+    const std::size_t wsb = nnhip_gemm_workspace_bytes(r.M, r.N, r.K, 1);
     std::shared_ptr<DeviceBuffer> ws;
     if (wsb)
     {
@@ -1194,11 +1220,19 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
         ws = w;
     }
     prof_begin_();
-    const int rc = nnhip_gemm(D(A), D(B), W(C), A.rows(), A.cols(), B.rows(), B.cols(), 1, tA, tB, 1.0f,
-                              ws ? ws->data() : nullptr, wsb, stream_);
-    prof_end_(M, N, K, 1, tA, tB);
-    NN_CHECK(kernel_(rc, "matmul"));
-    return C;
+    const int rc = nnhip_gemm_epilogue(D(r.A), D(r.B), W(out), r.A.rows(), r.A.cols(), r.B.rows(), r.B.cols(), r.tA,
+                                       r.tB, 1.0f, bias ? D(*bias) : nullptr, accumulate ? 1 : 0,
+                                       ws ? ws->data() : nullptr, wsb, stream_);
+    prof_end_(r.M, r.N, r.K, 1, r.tA, r.tB);
+    return kernel_(rc, "matmul");
+}
+
+Result<void> HipEngine::settle_mm_()
+{
+    if (!pmm_) return {};
+    std::unique_ptr<PendingMm> r = std::move(pmm_);
+    if (!live(r->C)) return {};
+    return launch_mm_(*r, r->C, nullptr, false);
 }
 
 Result<void> HipEngine::launch_gemm_(const Tensor& A, const Tensor& B, Tensor& C, std::size_t batch, bool tA, bool tB,
@@ -1455,6 +1489,18 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
     NN_CHECK(check_gpu_({&A, &B}, "add_inplace"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("add_inplace: shape mismatch");
     if (!A.size()) return {};
+    if (pmm_ && !pmm_->folded && same_t(B, pmm_->C) && !pmm_->uses(A.dev_ptr()))
+    {
+        // Linear backward: the weight-gradient accumulation becomes the
+        // product's epilogue (A += product); B stays recorded.
+        NN_CHECK(settle_write_(A));
+        if (pmm_ && same_t(B, pmm_->C))
+        {
+            NN_CHECK(launch_mm_(*pmm_, A, nullptr, true));
+            pmm_->folded = true;
+            return {};
+        }
+    }
     NN_CHECK(settle_chain_reads_({&B}));
     NN_CHECK(settle_chain_write_(A));
     return ew_push_(kBin, static_cast<unsigned>(BinaryOp::Add), false, A, A, &B, 0.0f);
@@ -1541,6 +1587,18 @@ Result<Tensor> HipEngine::col_reduce_max(const Tensor& A)
 // ── broadcasts (cpu_engine.hpp:1092-1125) ───────────────────────────────────
 Result<void> HipEngine::broadcast_row_inplace(Tensor& A, const Tensor& v, BinaryOp op)
 {
+    NN_CHECK(check_gpu_({&A, &v}, "broadcast_row_inplace"));
+    if (op == BinaryOp::Add && pmm_ && !pmm_->folded && same_t(A, pmm_->C) && v.rows() == A.rows() &&
+        v.cols() == 1 && !pmm_->uses(v.dev_ptr()))
+    {
+        // Linear forward: the bias add becomes the product's epilogue.
+        NN_CHECK(settle_reads_({&v}));
+        if (pmm_ && same_t(A, pmm_->C))
+        {
+            std::unique_ptr<PendingMm> r = std::move(pmm_);
+            return launch_mm_(*r, r->C, &v, false);
+        }
+    }
     NN_CHECK(need_gpu_({&A, &v}, "broadcast_row_inplace"));
     NN_CHECK(settle_write_(A));
     if (v.rows() != A.rows() || v.cols() != 1) return fail("broadcast_row_inplace: row_vec shape mismatch");

@@ -48,12 +48,15 @@ __device__ __forceinline__ void tile_coords(int bid, int nt, int tiles_m, int ti
     tn = r / gsize;
 }
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
 // WM x WN waves; each wave owns (32*FM) x (32*FN) of C as FM x FN MFMA 32x32 blocks.
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K, long lda, long ldb,
                                                        long strideA, long strideB, long strideC, float alpha,
-                                                       int tiles_m, int tiles_n, int k_split, float* __restrict__ part)
+                                                       int tiles_m, int tiles_n, int k_split, float* __restrict__ part,
+                                                       const float* __restrict__ bias, int accum)
 {
     constexpr int NT = 64 * WM * WN;
     constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
@@ -80,7 +83,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     const int k_hi = min(K, k_lo + k_split);
     if (gridDim.y > 1) C = part + ((long)blockIdx.y * gridDim.z + bz) * strideC;
 
-    float4 ra[LA], rb[LB];
+    f4 ra[LA], rb[LB];   // native vectors: HIP's float4 struct kept these arrays in scratch
 
     // A_eff(m, k) = TA ? A[k*lda + m] : A[m*lda + k]
     auto load_a = [&](int k0) {
@@ -94,8 +97,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             const int gm = m0 + m, gk = k0 + k;
             if constexpr (!GUARD)
             {
-                ra[s] = TA ? *reinterpret_cast<const float4*>(A + (long)gk * lda + gm)
-                           : *reinterpret_cast<const float4*>(A + (long)gm * lda + gk);
+                ra[s] = TA ? *reinterpret_cast<const f4*>(A + (long)gk * lda + gm)
+                           : *reinterpret_cast<const f4*>(A + (long)gm * lda + gk);
             }
             else
             {
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
                     const int mm = TA ? gm + q : gm, kk = TA ? gk : gk + q;
                     v[q] = (mm < M && kk < k_hi) ? (TA ? A[(long)kk * lda + mm] : A[(long)mm * lda + kk]) : 0.0f;
                 }
-                ra[s] = make_float4(v[0], v[1], v[2], v[3]);
+                ra[s] = f4{v[0], v[1], v[2], v[3]};
             }
         }
     };
@@ -122,8 +125,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             const int gn = n0 + n, gk = k0 + k;
             if constexpr (!GUARD)
             {
-                rb[s] = !TB ? *reinterpret_cast<const float4*>(B + (long)gk * ldb + gn)
-                            : *reinterpret_cast<const float4*>(B + (long)gn * ldb + gk);
+                rb[s] = !TB ? *reinterpret_cast<const f4*>(B + (long)gk * ldb + gn)
+                            : *reinterpret_cast<const f4*>(B + (long)gn * ldb + gk);
             }
             else
             {
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
                     const int nn = !TB ? gn + q : gn, kk = !TB ? gk : gk + q;
                     v[q] = (nn < N && kk < k_hi) ? (!TB ? B[(long)kk * ldb + nn] : B[(long)nn * ldb + kk]) : 0.0f;
                 }
-                rb[s] = make_float4(v[0], v[1], v[2], v[3]);
+                rb[s] = f4{v[0], v[1], v[2], v[3]};
             }
         }
     };
@@ -146,7 +149,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             if constexpr (TA)
             {
                 const int k = idx / (BM / 4), m = (idx % (BM / 4)) * 4;
-                *reinterpret_cast<float4*>(&As[buf][k][m]) = ra[s];
+                *reinterpret_cast<f4*>(&As[buf][k][m]) = ra[s];
             }
             else
             {
@@ -166,7 +169,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             if constexpr (!TB)
             {
                 const int k = idx / (BN / 4), n = (idx % (BN / 4)) * 4;
-                *reinterpret_cast<float4*>(&Bs[buf][k][n]) = rb[s];
+                *reinterpret_cast<f4*>(&Bs[buf][k][n]) = rb[s];
             }
             else
             {
@@ -228,8 +231,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
         __syncthreads();
     }
 
-    // Epilogue: C = alpha * acc.
+    // Epilogue: C = alpha * acc, then + bias[row] and / or + C (each rounded
+    // as the separate broadcast / add call would round it); a split-K partial
+    // is written unscaled and the reduce applies all of that.
     const int col_l = lane & 31, row_l = 4 * (lane >> 5);
+    const bool plain = gridDim.y > 1 || (!bias && !accum);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -240,17 +246,81 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             for (int r = 0; r < 16; ++r)
             {
                 const int gm = m0 + wm * 32 * FM + i * 32 + 8 * (r / 4) + row_l + (r % 4);
-                if (!GUARD || (gm < M && gn < N)) C[(long)gm * N + gn] = (gridDim.y > 1 ? 1.0f : alpha) * acc[i][j][r];
+                if (GUARD && !(gm < M && gn < N)) continue;
+                float* c = C + (long)gm * N + gn;
+                if (plain)
+                {
+                    *c = (gridDim.y > 1 ? 1.0f : alpha) * acc[i][j][r];
+                    continue;
+                }
+                {
+#pragma clang fp contract(off)
+                    float v = alpha * acc[i][j][r];
+                    if (bias) v = v + bias[gm];
+                    if (accum) v = *c + v;
+                    *c = v;
+                }
             }
         }
 }
 
+// C = alpha * sum_s part[s], summed in split order (deterministic); then
+// + bias[row] (rows of N) and / or + C when given, rounded as the separate calls.
+__global__ __launch_bounds__(256) void k_splitk_reduce_ep(const float* __restrict__ part, float* __restrict__ C,
+                                                          long n, int splits, float alpha, const float* bias, long N,
+                                                          int accum, int vec)
+{
+#pragma clang fp contract(off)
+    const long stride = (long)gridDim.x * 256;
+    if (vec)
+    {
+        // N % 4 == 0 and C 16-byte aligned: four consecutive elements share a row.
+        const long n4 = n / 4;
+        const float4* p4 = reinterpret_cast<const float4*>(part);
+        float4* c4 = reinterpret_cast<float4*>(C);
+        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride)
+        {
+            float4 a = p4[i];
+            for (int s = 1; s < splits; ++s)
+            {
+                const float4 b = p4[(long)s * n4 + i];
+                a.x += b.x;
+                a.y += b.y;
+                a.z += b.z;
+                a.w += b.w;
+            }
+            float4 v = make_float4(alpha * a.x, alpha * a.y, alpha * a.z, alpha * a.w);
+            if (bias)
+            {
+                const float bv = bias[(4 * i) / N];
+                v = make_float4(v.x + bv, v.y + bv, v.z + bv, v.w + bv);
+            }
+            if (accum)
+            {
+                const float4 c = c4[i];
+                v = make_float4(c.x + v.x, c.y + v.y, c.z + v.z, c.w + v.w);
+            }
+            c4[i] = v;
+        }
+        return;
+    }
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+    {
+        float a = part[i];
+        for (int s = 1; s < splits; ++s) a += part[(long)s * n + i];
+        float v = alpha * a;
+        if (bias) v = v + bias[i / N];
+        if (accum) v = C[i] + v;
+        C[i] = v;
+    }
+}
+
 // C = alpha * sum_s part[s], summed in split order (deterministic).
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, float* __restrict__ C,
-                                                       long n, int splits, float alpha)
+                                                       long n, int splits, float alpha, int vec)
 {
     const long stride = (long)gridDim.x * 256;
-    if ((n & 3) == 0)
+    if (vec)
     {
         const long n4 = n / 4;
         const float4* p4 = reinterpret_cast<const float4*>(part);
@@ -345,9 +415,16 @@ Plan plan_gemm(size_t M, size_t N, size_t K, size_t batch, bool allow_split)
     return p;
 }
 
+struct Epi
+{
+    const float* bias;   // per output row, or null
+    int accum;           // C += result
+};
+
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB>
 void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, long lda, long ldb, long sA, long sB,
-                long sC, float alpha, int batch, bool vec_ok, int splits, int k_split, float* part, hipStream_t s)
+                long sC, float alpha, int batch, bool vec_ok, int splits, int k_split, float* part, hipStream_t s,
+                Epi e)
 {
     constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
     const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
@@ -356,15 +433,15 @@ void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, l
     const dim3 block(64 * WM * WN);
     if (guard)
         hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, true>), grid, block, 0, s, A, B, C, M, N, K, lda, ldb,
-                           sA, sB, sC, alpha, tm, tn, k_split, part);
+                           sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum);
     else
         hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false>), grid, block, 0, s, A, B, C, M, N, K, lda, ldb,
-                           sA, sB, sC, alpha, tm, tn, k_split, part);
+                           sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum);
 }
 
 template <bool TA, bool TB>
 void launch_trans(const Plan& p, const float* A, const float* B, float* C, int M, int N, int K, long lda, long ldb,
-                  long sA, long sB, long sC, float alpha, int batch, float* part, hipStream_t s)
+                  long sA, long sB, long sC, float alpha, int batch, float* part, hipStream_t s, Epi e)
 {
     const bool vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && (sA % 4 == 0) && (sB % 4 == 0) && aligned16(A) &&
                         aligned16(B);
@@ -372,30 +449,30 @@ void launch_trans(const Plan& p, const float* A, const float* B, float* C, int M
     {
     case kSkinnyN:
         launch_cfg<4, 1, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
-                                           p.k_split, part, s);
+                                           p.k_split, part, s, e);
         break;
     case kThinWaves:
         launch_cfg<4, 1, 1, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
-                                           p.k_split, part, s);
+                                           p.k_split, part, s, e);
         break;
     case kThinWavesM64:
         launch_cfg<2, 2, 1, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
-                                           p.k_split, part, s);
+                                           p.k_split, part, s, e);
         break;
     case kTall:
         launch_cfg<4, 2, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
-                                           p.k_split, part, s);
+                                           p.k_split, part, s, e);
         break;
     default:
         launch_cfg<2, 2, 2, 2, 16, TA, TB>(A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, batch, vec_ok, p.splits,
-                                           p.k_split, part, s);
+                                           p.k_split, part, s, e);
         break;
     }
 }
 
 int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, size_t K, size_t lda, size_t ldb,
                   size_t sA, size_t sB, size_t sC, bool tA, bool tB, float alpha, size_t batch, void* workspace,
-                  size_t ws_bytes, void* stream)
+                  size_t ws_bytes, void* stream, Epi e = {nullptr, 0})
 {
     if (M == 0 || N == 0 || batch == 0) return 0;
     if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || batch > 65535) return -1;
@@ -405,15 +482,20 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
         p = plan_gemm(M, N, K, batch, false);
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K, b = (int)batch;
-    if (!tA && !tB) launch_trans<false, false>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s);
-    else if (!tA && tB) launch_trans<false, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s);
-    else if (tA && !tB) launch_trans<true, false>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s);
-    else launch_trans<true, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s);
+    if (!tA && !tB) launch_trans<false, false>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
+    else if (!tA && tB) launch_trans<false, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
+    else if (tA && !tB) launch_trans<true, false>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
+    else launch_trans<true, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
     if (p.splits > 1)
     {
         const long total = (long)batch * (long)M * (long)N;
-        hipLaunchKernelGGL(k_splitk_reduce, dim3(grid_for(static_cast<size_t>(total / 4 + 1), 256, 256 * 16)),
-                           dim3(256), 0, s, part, C, total, p.splits, alpha);
+        const int vec = aligned16(C) && (e.bias || e.accum ? N % 4 == 0 : total % 4 == 0) ? 1 : 0;
+        if (e.bias || e.accum)
+            hipLaunchKernelGGL(k_splitk_reduce_ep, dim3(grid_for(static_cast<size_t>(total / 4 + 1), 256, 256 * 16)),
+                               dim3(256), 0, s, part, C, total, p.splits, alpha, e.bias, (long)N, e.accum, vec);
+        else
+            hipLaunchKernelGGL(k_splitk_reduce, dim3(grid_for(static_cast<size_t>(total / 4 + 1), 256, 256 * 16)),
+                               dim3(256), 0, s, part, C, total, p.splits, alpha, vec);
     }
     return launch_status();
 }
@@ -440,6 +522,18 @@ extern "C" int nnhip_gemm(const float* A, const float* B, float* C, size_t A_row
     if (K != K2) return -2;
     return gemm_dispatch(A, B, C, M, N, K, A_cols, B_cols, ar * A_cols, br * B_cols, M * N, transA != 0, transB != 0,
                          alpha, batch, workspace, workspace_bytes, stream);
+}
+
+extern "C" int nnhip_gemm_epilogue(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols,
+                                   size_t B_rows, size_t B_cols, int transA, int transB, float alpha,
+                                   const float* row_bias, int accumulate, void* workspace, size_t workspace_bytes,
+                                   void* stream)
+{
+    const size_t M = transA ? A_cols : A_rows, K = transA ? A_rows : A_cols;
+    const size_t K2 = transB ? B_cols : B_rows, N = transB ? B_rows : B_cols;
+    if (K != K2) return -2;
+    return gemm_dispatch(A, B, C, M, N, K, A_cols, B_cols, A_rows * A_cols, B_rows * B_cols, M * N, transA != 0,
+                         transB != 0, alpha, 1, workspace, workspace_bytes, stream, Epi{row_bias, accumulate ? 1 : 0});
 }
 
 extern "C" int nnhip_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,

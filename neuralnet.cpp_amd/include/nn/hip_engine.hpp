@@ -175,6 +175,10 @@ private:
     struct PendingGemm;
     struct PendingBwd;
     struct PendingEw;
+    struct PendingMm;
+    std::unique_ptr<PendingMm> pmm_;
+    Result<void> settle_mm_();
+    Result<void> launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate);
     struct PendingMaskAdd;
     struct PendingAttn;
     struct PendingDv;

@@ -1,0 +1,107 @@
+"""Linear layer products with their next call folded into the GEMM epilogue.
+
+Linear::forward is matmul(W, x) then broadcast_row_inplace(out, b, Add);
+Linear::backward accumulates the weight gradient with add_inplace(grad_w,
+matmul(g, x, transB)) (reference compute_layer.hpp:99-196). The HIP engine
+records the matmul and, when that next call follows, adds the bias or
+accumulates inside the product's epilogue. Bars: bit-exact against the same
+calls launched one by one (an engine settle between them), the products within
+the GEMM bound of the float64 product, and the recorded product itself correct
+when read afterwards.
+"""
+import numpy as np
+import pytest
+
+from helpers import nrm_err, uniform
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+SHAPES = [(64, 48, 40), (768, 8192, 768), (6144, 768, 8192), (37, 29, 1500), (3, 5, 7)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_bias_epilogue(hip, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    W, X, b = uniform(rng, (M, K)), uniform(rng, (K, N)), uniform(rng, (M, 1))
+
+    def run(settle):
+        w, x, bb = hip.tensor(W), hip.tensor(X), hip.tensor(b)
+        out = hip.matmul(w, x)
+        if settle:
+            hip.settle()
+        hip.broadcast_row_inplace(out, bb, "Add")
+        return out.numpy()
+
+    fused, calls = run(False), run(True)
+    assert np.array_equal(bits(fused), bits(calls))
+    ref = W.astype(np.float64) @ X.astype(np.float64) + b.astype(np.float64)
+    assert nrm_err(fused, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_accumulate_epilogue(hip, M, N, K):
+    rng = np.random.default_rng(3 * M + N + K)
+    G, X, acc0 = uniform(rng, (M, K)), uniform(rng, (N, K)), uniform(rng, (M, N))
+
+    def run(settle):
+        g, x, acc = hip.tensor(G), hip.tensor(X), hip.tensor(acc0)
+        gw = hip.matmul(g, x, False, True)
+        if settle:
+            hip.settle()
+        hip.add_inplace(acc, gw)
+        return acc.numpy(), gw.numpy()
+
+    (fa, fg), (ca, cg) = run(False), run(True)
+    assert np.array_equal(bits(fa), bits(ca))
+    assert np.array_equal(bits(fg), bits(cg)), "the recorded product read after the accumulation"
+    ref = G.astype(np.float64) @ X.astype(np.float64).T
+    assert nrm_err(fg, ref) <= 1e-5
+    assert nrm_err(fa, ref + acc0) <= 1e-5
+
+
+def test_linear_forward_backward_sequence(hip, cpu):
+    """A Linear layer's calls, forward then backward, twice, against the oracle."""
+    rng = np.random.default_rng(1)
+    O, I, N = 96, 80, 256
+    W, b, X, G = uniform(rng, (O, I)), uniform(rng, (O, 1)), uniform(rng, (I, N)), uniform(rng, (O, N))
+
+    def run(e):
+        w, bb, x, g = e.tensor(W), e.tensor(b), e.tensor(X), e.tensor(G)
+        gw_acc = e.tensor(np.zeros((O, I), np.float32))
+        outs = []
+        for _ in range(2):
+            out = e.matmul(w, x)
+            e.broadcast_row_inplace(out, bb, "Add")
+            dx = e.matmul(w, g, True, False)
+            gw = e.matmul(g, x, False, True)
+            e.add_inplace(gw_acc, gw)
+            del gw
+            outs += [out.numpy(), dx.numpy()]
+        outs.append(gw_acc.numpy())
+        return outs
+
+    h, c = run(hip), run(cpu)
+    for i, (a, r) in enumerate(zip(h, c)):
+        assert nrm_err(a, r) <= 1e-5, i
+
+
+def test_other_consumers(hip):
+    """A product followed by a call that is not its epilogue is launched as is."""
+    rng = np.random.default_rng(2)
+    A, B, v = uniform(rng, (40, 30)), uniform(rng, (30, 50)), uniform(rng, (40, 1))
+    a, bm, vv = hip.tensor(A), hip.tensor(B), hip.tensor(v)
+    c = hip.matmul(a, bm)
+    hip.broadcast_row_inplace(c, vv, "Mul")            # not an Add: plain product, then the broadcast
+    ref = (A.astype(np.float64) @ B.astype(np.float64)) * v
+    assert nrm_err(c.numpy(), ref) <= 1e-5
+    c2 = hip.matmul(a, bm)
+    t = hip.transpose(c2)                               # another kind of call reads the product
+    assert nrm_err(t.numpy(), (A.astype(np.float64) @ B.astype(np.float64)).T) <= 1e-5
+    c3 = hip.matmul(a, bm)
+    hip.scale_inplace(a, 2.0)                           # an input written before the product ran
+    assert nrm_err(c3.numpy(), A.astype(np.float64) @ B.astype(np.float64)) <= 1e-5
