@@ -406,17 +406,18 @@ __device__ __forceinline__ float cell_scores(const f32x16& s, float alpha, const
 }
 
 // Forward workgroup: 4 waves on 4 consecutive query lines (32 queries each)
-// walking the non-empty cells of their range two at a time. A step stages the
-// key and value tiles of two cells in LDS (double-buffered, one barrier per
-// step); each wave computes the scores of its active cells, updates its
-// online max / sum once for both (one cross-lane max, one rescale, skipped
-// when no row maximum moved) and accumulates the weighted values.
-template <int KP, int DP, bool WITH_O, bool VDM>
-__global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, FlashGeo g)
+// walking the non-empty cells of their range CPS (1 or 2) at a time. A step
+// stages the key and value tiles of its cells in LDS (double-buffered, one
+// barrier per step); each wave computes the scores of its active cells,
+// updates its online max / sum once per step (one cross-lane max, one
+// rescale, skipped when no row maximum moved) and accumulates the weighted
+// values.
+template <int KP, int DP, bool WITH_O, bool VDM, int CPS>
+__global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(FlashFwdArgs a, FlashGeo g)
 {
     constexpr int DU = DP / 32;
-    __shared__ __align__(16) float Ks[2][2][32][KP + 4];
-    __shared__ __align__(16) float Vs[WITH_O ? 2 : 1][WITH_O ? 2 : 1][WITH_O ? 32 : 1][DP + 4];
+    __shared__ __align__(16) float Ks[2][CPS][32][KP + 4];
+    __shared__ __align__(16) float Vs[WITH_O ? 2 : 1][WITH_O ? CPS : 1][WITH_O ? 32 : 1][DP + 4];
     __shared__ unsigned long long nz_s[kWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const Item it = item_of(g);
@@ -436,8 +437,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
         const float* Qb = a.Q + (long)it.b * a.K * g.M;
         const float* Kb = a.Kt + (long)it.b * a.K * g.N;
         const float* Vb = WITH_O ? a.V + (long)it.b * g.N * a.D : nullptr;
-        TTile<KP> kt[2];
-        std::conditional_t<VDM, TTile<DP>, RTile<DP>> vt[2];   // V (D, N) or (N, D), staged [key][dim]
+        TTile<KP> kt[CPS];
+        std::conditional_t<VDM, TTile<DP>, RTile<DP>> vt[CPS];   // V (D, N) or (N, D), staged [key][dim]
         unsigned long long rest = any;
         auto pop = [&]() {
             if (!rest) return -1;
@@ -448,7 +449,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
         auto load = [&](int c0, int c1) {
             const int cc[2] = {c0, c1};
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < CPS; ++t)
                 if (cc[t] >= 0)
                 {
                     kt[t].load(Kb, a.K, g.N, 32 * (cell0 + cc[t]), threadIdx.x);
@@ -459,14 +460,14 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
         auto store = [&](int buf, int c0, int c1) {
             const int cc[2] = {c0, c1};
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < CPS; ++t)
                 if (cc[t] >= 0)
                 {
                     kt[t].store(Ks[buf][t], threadIdx.x);
                     if constexpr (WITH_O) vt[t].store(Vs[buf][t], threadIdx.x);
                 }
         };
-        int c0 = pop(), c1 = pop();
+        int c0 = pop(), c1 = CPS == 2 ? pop() : -1;
         load(c0, c1);
         float qf[KP / 2];
         line_operand<KP>(Qb, a.K, g.M, qi, h, qf);
@@ -477,14 +478,14 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
         int buf = 0;
         while (true)
         {
-            const int n0 = pop(), n1 = pop();
+            const int n0 = pop(), n1 = CPS == 2 ? pop() : -1;
             if (n0 >= 0) load(n0, n1);
             const bool act0 = (lw.nz >> c0) & 1ull, act1 = c1 >= 0 && ((lw.nz >> c1) & 1ull);
             if (act0 || act1)
             {
-                float x[2][16], cmax = kLowest;
+                float x[CPS][16], cmax = kLowest;
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+                for (int t = 0; t < CPS; ++t)
                 {
                     const int cell = t ? c1 : c0;
                     if (!(t ? act1 : act0))
@@ -523,7 +524,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_fwd(FlashFwdArgs a, Fl
                 // Rows still without an allowed key keep lowest() and only -inf scores.
                 const float mb = mrun == kLowest ? 0.0f : mrun * kLog2e;
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+                for (int t = 0; t < CPS; ++t)
                 {
                     if (!(t ? act1 : act0)) continue;
 #pragma unroll
@@ -1062,12 +1063,23 @@ int cols_pw(int KP) { return 64 * KP; }
 template <int KP, int DP, bool WITH_O>
 int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g, size_t batch, hipStream_t s)
 {
+    // Cells per step: one cell (3 workgroups per CU: 35 KB of LDS, <= 168
+    // VGPRs) when a line range holds >= 32 cells, two (2 per CU) for shorter
+    // ranges, where fewer barriers per cell pay more. Measured: causal
+    // (96 x 1024)^2 58 -> 71 TFLOP/s with one; causal (128 x 512)^2 and the
+    // document-masked rows 3-4 % faster with two.
+    const dim3 grid(grid_of(g, batch)), block(64 * kWaves);
+    const bool one = std::min(g.R, g.CT) >= 32;
     if (WITH_O && a.v_dm)
-        hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true>), dim3(grid_of(g, batch)), dim3(64 * kWaves), 0, s, a,
-                           g);
+    {
+        if (one) hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true, 1>), grid, block, 0, s, a, g);
+        else hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true, 2>), grid, block, 0, s, a, g);
+    }
     else
-        hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, false>), dim3(grid_of(g, batch)), dim3(64 * kWaves), 0, s, a,
-                           g);
+    {
+        if (one) hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, false, 1>), grid, block, 0, s, a, g);
+        else hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, false, 2>), grid, block, 0, s, a, g);
+    }
     if (int rc = launch_status()) return rc;
     if (g.NR == 1) return 0;
     hipLaunchKernelGGL((k_flash_fwd_combine<DP, WITH_O>), dim3(static_cast<unsigned>(batch * g.RT)), dim3(64), 0, s,

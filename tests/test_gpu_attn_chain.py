@@ -181,3 +181,12 @@ def test_dropped_probabilities(hip, cpu):
 
     h, c = go(hip), go(cpu)
     assert nrm_err(h[0], c[0]) <= 1e-4 and nrm_err(h[1], c[1]) <= 1e-4
+
+
+def test_chain_config4_shape(hip, cpu):
+    """The config-4 attention of one layer (B8 x H12, T1024, d64, ALiBi): the forward
+    runs one cell per step here."""
+    B, H, T, dk = 8, 12, 1024, 64
+    mask = attn_mask(B, H, T)
+    arrs = inputs(17, B * H, T, dk)
+    check(run(hip, arrs, mask, B * H, T, 0.125), run(cpu, arrs, mask, B * H, T, 0.125))

@@ -211,3 +211,27 @@ def test_config5_rows_back_to_back(hip, cpu):
 
     for i, (x, y) in enumerate(zip(run(hip), run(cpu))):
         assert nrm_err(x, y) <= 1e-3, i
+
+
+def test_forward_long_lines_float64(hip):
+    """Lines of >= 32 cells in one range (64 heads x 1024 keys: the one-cell-per-step
+    forward), against a float64 softmax attention (the oracle's serial primitives
+    would take minutes at this size)."""
+    B, M, N, K, D = 64, 1024, 1024, 64, 64
+    rng = np.random.default_rng(21)
+    Q, Kt, V = normal(rng, (B * K, M)), normal(rng, (B * K, N)), normal(rng, (B * N, D))
+    mask = _mask("alibi", M, N, rng)
+    alpha = 0.125
+    q, k, mk = hip.tensor(Q), hip.tensor(Kt), hip.tensor(mask)
+    m = hip.batched_matmul_reduce(q, k, B, "Max", True, False, alpha, True, mk)
+    l = hip.batched_matmul_softmax_denom(q, k, m, B, True, False, alpha, mk)
+    o = hip.batched_matmul_softmax_apply(q, k, hip.tensor(V), m, l, B, True, False, alpha, mk).numpy()
+    m, l = m.numpy().reshape(B, M), l.numpy().reshape(B, M)
+    for b in range(0, B, 9):
+        s = alpha * (Q[b * K:(b + 1) * K].astype(np.float64).T @ Kt[b * K:(b + 1) * K].astype(np.float64)) + mask
+        mr = s.max(axis=1)
+        w = np.exp(s - mr[:, None])
+        lr = w.sum(axis=1)
+        orf = (w / lr[:, None]) @ V[b * N:(b + 1) * N].astype(np.float64)
+        assert nrm_err(m[b], mr) <= 1e-5 and nrm_err(l[b], lr) <= 1e-5
+        assert nrm_err(o[b * M:(b + 1) * M], orf) <= 1e-4, b
