@@ -81,6 +81,9 @@ int nnhip_adam_update(float* p, float* m, float* v, const float* g, size_t count
  * No CUDA counterpart; HipEngine issues it when it recognises that chain among deferred calls. */
 int nnhip_swiglu_forward(const float* gate, const float* up, float* s_out, float* out, size_t count, float c_add,
                          float c_div, void* stream);
+/* dst[i] = src[i] for count floats (non-overlapping): slice_rows / insert_rows / clone (cpu_engine.hpp:75-114;
+ * the CUDA engine uses cudaMemcpy). */
+int nnhip_copy(const float* src, float* dst, size_t count, void* stream);
 /* Zeroes n device buffers (ptrs[i], counts[i] floats) in as few launches as possible (consecutive
  * ComputeEngine::zero calls, e.g. Optimizer::zero_grad, compute_optimizer.hpp:142-151). */
 int nnhip_zero_list(float* const* ptrs, const size_t* counts, size_t n, void* stream);

@@ -938,8 +938,7 @@ Result<void> HipEngine::settle_ew_()
             case kUnary: NN_CHECK(kernel_(nnhip_elementwise_unary(a, out, n, o.op, st), "elementwise_unary")); break;
             case kAxpy: NN_CHECK(kernel_(nnhip_axpy(a, b, out, n, o.s, st), "axpy_inplace")); break;
             case kCopy:
-                if (hipMemcpyAsync(out, a, n * sizeof(float), hipMemcpyDeviceToDevice, st) != hipSuccess)
-                    return fail("clone: device copy failed");
+                NN_CHECK(kernel_(nnhip_copy(a, out, n, st), "clone"));
                 break;
             }
         }
@@ -1131,21 +1130,38 @@ Result<Tensor> HipEngine::slice_rows(const Tensor& src, std::size_t start, std::
     if (start + count > src.rows()) return fail("slice_rows: range out of bounds");
     NN_TRY(t, alloc_(count, src.cols()));
     const std::size_t n = count * src.cols();
-    if (n && hipMemcpyAsync(W(t), D(src) + start * src.cols(), n * sizeof(float), hipMemcpyDeviceToDevice,
-                            static_cast<hipStream_t>(stream_)) != hipSuccess)
-        return fail("slice_rows: device copy failed");
+    if (n) NN_CHECK(kernel_(nnhip_copy(D(src) + start * src.cols(), W(t), n, stream_), "slice_rows"));
     return t;
 }
 
+// A row insert into a tensor whose zero call is still pending does not launch
+// the zeroing first: the inserted rows are left out of it (SwiGLU::backward
+// zeroes its (2 d_ff, N) gradient and then inserts both halves).
 Result<void> HipEngine::insert_rows(Tensor& dst, std::size_t start, const Tensor& src)
 {
-    NN_CHECK(need_gpu_({&dst, &src}, "insert_rows"));
-    NN_CHECK(settle_write_(dst));
+    NN_CHECK(check_gpu_({&dst, &src}, "insert_rows"));
     if (dst.cols() != src.cols()) return fail("insert_rows: column count mismatch");
     if (start + src.rows() > dst.rows()) return fail("insert_rows: range out of bounds");
-    if (src.size() && hipMemcpyAsync(W(dst) + start * dst.cols(), D(src), src.size() * sizeof(float),
-                                     hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream_)) != hipSuccess)
-        return fail("insert_rows: device copy failed");
+    PendingZero* z = nullptr;
+    for (auto& e : pzero_)
+        if (same_t(e.t, dst)) z = &e;
+    bool src_zero = false;
+    for (auto& e : pzero_)
+        if (has_buf(e.t, src.dev_ptr())) src_zero = true;
+    if (z && !src_zero && !has_buf(src, dst.dev_ptr()))
+    {
+        NN_CHECK(settle_ew_());
+        NN_CHECK(settle_chain_reads_({&src}));
+        NN_CHECK(settle_chain_write_(dst));
+        z->covered.emplace_back(start, start + src.rows());
+    }
+    else
+    {
+        NN_CHECK(settle_reads_({&dst, &src}));
+        NN_CHECK(settle_write_(dst));
+    }
+    if (src.size())
+        NN_CHECK(kernel_(nnhip_copy(D(src), W(dst) + start * dst.cols(), src.size(), stream_), "insert_rows"));
     return {};
 }
 
@@ -1532,7 +1548,13 @@ Result<void> HipEngine::zero(Tensor& A)
     if (!A.size()) return {};
     NN_CHECK(settle_ew_());
     NN_CHECK(settle_chain_write_(A));
-    pzero_.push_back(A);
+    for (auto& e : pzero_)
+        if (same_t(e.t, A))
+        {
+            e.covered.clear();
+            return {};
+        }
+    pzero_.push_back(PendingZero{A, {}});
     if (pzero_.size() >= 512) return settle_zero_();
     return {};
 }
@@ -1540,15 +1562,32 @@ Result<void> HipEngine::zero(Tensor& A)
 Result<void> HipEngine::settle_zero_()
 {
     if (pzero_.empty()) return {};
-    std::vector<Tensor> ts = std::move(pzero_);
+    std::vector<PendingZero> ts = std::move(pzero_);
     pzero_.clear();
     std::vector<float*> ptrs;
     std::vector<std::size_t> counts;
-    for (const Tensor& t : ts)
+    for (auto& z : ts)
     {
-        ptrs.push_back(W(t));
-        counts.push_back(t.size());
+        // Row ranges not covered by inserts since the zero call.
+        std::sort(z.covered.begin(), z.covered.end());
+        std::size_t row = 0;
+        const std::size_t cols = z.t.cols();
+        for (const auto& [a, b] : z.covered)
+        {
+            if (a > row)
+            {
+                ptrs.push_back(W(z.t) + row * cols);
+                counts.push_back((a - row) * cols);
+            }
+            row = std::max(row, b);
+        }
+        if (row < z.t.rows())
+        {
+            ptrs.push_back(W(z.t) + row * cols);
+            counts.push_back((z.t.rows() - row) * cols);
+        }
     }
+    if (ptrs.empty()) return {};
     return kernel_(nnhip_zero_list(ptrs.data(), counts.data(), ptrs.size(), stream_), "zero");
 }
 

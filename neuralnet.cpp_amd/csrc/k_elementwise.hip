@@ -264,6 +264,25 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_fwd(const float* gate, cons
     }
 }
 
+// Plain copy, float4 per lane and two in flight (slices, row inserts, clones).
+__global__ __launch_bounds__(kThreads) void k_copy4(const float4* __restrict__ src, float4* __restrict__ dst, size_t n4)
+{
+    const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+    size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+    for (; i + stride < n4; i += 2 * stride)
+    {
+        const float4 a = src[i], b = src[i + stride];
+        dst[i] = a;
+        dst[i + stride] = b;
+    }
+    if (i < n4) dst[i] = src[i];
+}
+__global__ __launch_bounds__(kThreads) void k_copy1(const float* __restrict__ src, float* __restrict__ dst, size_t n)
+{
+    const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
 // Zero fill of up to kFillMax tensors in one launch: block ranges per tensor
 // from the prefix sums in `first` (blocks of 256 threads x 4 floats x 4).
 constexpr int kFillMax = 96;
@@ -312,6 +331,19 @@ extern "C" int nnhip_swiglu_forward(const float* gate, const float* up, float* s
     else
         hipLaunchKernelGGL(k_swiglu_fwd<false>, dim3(grid), dim3(kThreads), 0, s, gate, up, s_out, out, count,
                            c_add, c_div);
+    return launch_status();
+}
+
+extern "C" int nnhip_copy(const float* src, float* dst, size_t count, void* stream)
+{
+    if (count == 0) return 0;
+    if (!src || !dst) return -1;
+    auto s = static_cast<hipStream_t>(stream);
+    if (aligned16(src) && aligned16(dst) && count % 4 == 0)
+        hipLaunchKernelGGL(k_copy4, dim3(grid_for(count / 8 + 1, kThreads, 256 * 16)), dim3(kThreads), 0, s,
+                           reinterpret_cast<const float4*>(src), reinterpret_cast<float4*>(dst), count / 4);
+    else
+        hipLaunchKernelGGL(k_copy1, dim3(grid_for(count, kThreads, 256 * 16)), dim3(kThreads), 0, s, src, dst, count);
     return launch_status();
 }
 

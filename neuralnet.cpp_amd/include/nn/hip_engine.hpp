@@ -205,7 +205,12 @@ private:
     std::unique_ptr<PendingGemm> pgemm_;
     std::unique_ptr<PendingBwd> pbwd_;
     std::unique_ptr<PendingEw> pew_;
-    std::vector<Tensor> pzero_;   // zero calls not yet launched
+    struct PendingZero
+    {
+        Tensor t;
+        std::vector<std::pair<std::size_t, std::size_t>> covered;   // rows inserted since the zero call
+    };
+    std::vector<PendingZero> pzero_;   // zero calls not yet launched
     Result<void> settle_zero_();
     // Before reading (writing) tensors: launch deferred work that yields
     // (yields or reads) them; the plain forms also launch the elementwise run.

@@ -198,3 +198,30 @@ def test_zero_list(hip):
         assert np.array_equal(got, arrs[3] if i == 3 else np.zeros_like(got)), i
     assert not s.numpy().any()
     assert np.array_equal(keep.numpy(), arrs[0])
+
+
+def test_zero_then_inserts(hip):
+    """SwiGLU::backward's zero + insert_rows pattern: inserted rows are not zeroed
+    afterwards, rows no insert covers are, and a second zero call wins over earlier inserts."""
+    rng = np.random.default_rng(12)
+    R, C = 70, 36
+    a, b, c = uniform(rng, (30, C)), uniform(rng, (25, C)), uniform(rng, (10, C))
+    dst = hip.tensor(uniform(rng, (R, C), 5.0, 6.0))
+    hip.zero(dst)
+    hip.insert_rows(dst, 0, hip.tensor(a))
+    hip.insert_rows(dst, 40, hip.tensor(b))     # rows 30..39 and 65..69 stay zero
+    ref = np.zeros((R, C), np.float32)
+    ref[0:30], ref[40:65] = a, b
+    assert np.array_equal(dst.numpy(), ref)
+    hip.zero(dst)
+    hip.insert_rows(dst, 5, hip.tensor(c))
+    hip.zero(dst)                                # the later zero clears the insert too
+    hip.insert_rows(dst, 60, hip.tensor(c))
+    ref = np.zeros((R, C), np.float32)
+    ref[60:70] = c
+    assert np.array_equal(dst.numpy(), ref)
+    src = hip.tensor(a)
+    hip.zero(src)                                # a pending zero on the source is applied before it is read
+    hip.insert_rows(dst, 0, src)
+    ref[0:30] = 0
+    assert np.array_equal(dst.numpy(), ref)
