@@ -240,6 +240,10 @@ int nnhip_rmsnorm_bwd_rowsum(const float* G, const float* gamma, const float* Nr
 int nnhip_swiglu_grad_gate(const float* G, const float* up, const float* s, const float* gate, float* out,
                            size_t count, void* stream);
 int nnhip_swiglu_grad_up(const float* G, const float* gate, const float* s, float* out, size_t count, void* stream);
+/* Both of the above in one pass (SwiGLU::backward's two programs, whose results it inserts into one (2 d_ff, N)
+ * gradient): out_gate and out_up may be rows of one tensor. Same roundings as the separate calls. */
+int nnhip_swiglu_grad_both(const float* G, const float* up, const float* s, const float* gate, float* out_gate,
+                           float* out_up, size_t count, void* stream);
 
 /* ── ExprSpec interpreter (no CUDA counterpart; cpu_engine.hpp:1298-1659) ──
  * The program is the ExprSpec in serialised form (see nnhip_engine.h); inputs[k] are device pointers

@@ -230,6 +230,7 @@ bool same_t(const Tensor& a, const Tensor& b)
 }
 bool same_mask(const Tensor* a, const std::optional<Tensor>& b) { return a ? (b && same_t(*a, *b)) : !b; }
 bool has_buf(const Tensor& t, const float* p) { return p && t.dev_ptr() == p; }
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 // True when a tensor held by a deferred record is also referenced elsewhere.
 bool live(const Tensor& t) { return t.device_buffer().use_count() > 1; }
 
@@ -292,6 +293,24 @@ struct RunStep
     unsigned op;
     std::uint8_t first;
     int dst, a, b;
+};
+
+// A SwiGLU gradient program (SwiGLU::backward) not launched yet. The layer
+// inserts each result into its (2 d_ff, N) gradient right away; the program
+// then writes those rows directly (`placed`), both programs in one pass when
+// both are placed.
+struct HipEngine::PendingSwb
+{
+    bool up;                      // grad_up (G, gate, s) or grad_gate (G, up, s, gate)
+    Tensor G, upt, s, gate, out;  // upt: unused by grad_up
+    Tensor dst;
+    std::size_t off = 0;          // floats into dst
+    bool placed = false;
+    bool uses(const float* p) const
+    {
+        return has_buf(G, p) || has_buf(upt, p) || has_buf(s, p) || has_buf(gate, p) || has_buf(out, p) ||
+               (placed && has_buf(dst, p));
+    }
 };
 
 // matmul(A, B) not launched yet (see HipEngine::matmul). `folded`: its product
@@ -580,6 +599,12 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
         const float* p = t->dev_ptr();
         if (!p) continue;
         if (pmm_ && has_buf(pmm_->C, p)) NN_CHECK(settle_mm_());
+        for (const auto& r : pswb_)
+            if (has_buf(r.out, p) || (r.placed && has_buf(r.dst, p)))
+            {
+                NN_CHECK(settle_swb_());
+                break;
+            }
         if (pmadd_ && has_buf(pmadd_->out, p)) NN_CHECK(settle_madd_());
         if (pdv_ && has_buf(pdv_->out, p)) NN_CHECK(settle_dv_());
         if (pds_ && has_buf(pds_->out, p)) NN_CHECK(settle_ds_());
@@ -622,11 +647,17 @@ Result<void> HipEngine::settle_write_(const Tensor& t)
     return settle_chain_write_(t);
 }
 
-Result<void> HipEngine::settle_chain_write_(const Tensor& t)
+Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb)
 {
     const float* p = t.dev_ptr();
     if (!p) return {};
     if (pmm_ && pmm_->uses(p)) NN_CHECK(settle_mm_());
+    for (const auto& r : pswb_)
+        if (!keep_swb && r.uses(p))
+        {
+            NN_CHECK(settle_swb_());
+            break;
+        }
     if (pmadd_ && pmadd_->uses(p)) NN_CHECK(settle_madd_());
     if (pdv_ && pdv_->uses(p)) NN_CHECK(settle_dv_());
     if (pds_ && pds_->uses(p)) NN_CHECK(settle_ds_());
@@ -654,6 +685,7 @@ Result<void> HipEngine::settle()
     NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
     NN_CHECK(settle_mm_());
+    NN_CHECK(settle_swb_());
     NN_CHECK(settle_madd_());
     NN_CHECK(settle_dv_());
     NN_CHECK(settle_ds_());
@@ -1134,6 +1166,39 @@ Result<Tensor> HipEngine::slice_rows(const Tensor& src, std::size_t start, std::
     return t;
 }
 
+// Launches the recorded SwiGLU gradient programs: into their rows of the
+// layer's gradient when placed there, and into their own result while that
+// is still referenced.
+Result<void> HipEngine::settle_swb_()
+{
+    if (pswb_.empty()) return {};
+    std::vector<PendingSwb> rs = std::move(pswb_);
+    pswb_.clear();
+    if (rs.size() == 2 && rs[0].placed && rs[1].placed && rs[0].up != rs[1].up && !live(rs[0].out) &&
+        !live(rs[1].out))
+    {
+        // The layer's two inserts: both gradients in one pass.
+        const PendingSwb& g = rs[0].up ? rs[1] : rs[0];
+        const PendingSwb& u = rs[0].up ? rs[0] : rs[1];
+        if (same_t(g.G, u.G) && same_t(g.s, u.s) && same_t(g.gate, u.gate))
+            return kernel_(nnhip_swiglu_grad_both(D(g.G), D(g.upt), D(g.s), D(g.gate), W(g.dst) + g.off,
+                                                  W(u.dst) + u.off, g.out.size(), stream_),
+                           "swiglu grad");
+    }
+    for (auto& r : rs)
+    {
+        const std::size_t n = r.out.size();
+        auto run = [&](float* o) -> Result<void> {
+            if (r.up) return kernel_(nnhip_swiglu_grad_up(D(r.G), D(r.gate), D(r.s), o, n, stream_), "swiglu grad up");
+            return kernel_(nnhip_swiglu_grad_gate(D(r.G), D(r.upt), D(r.s), D(r.gate), o, n, stream_),
+                           "swiglu grad gate");
+        };
+        if (r.placed) NN_CHECK(run(W(r.dst) + r.off));
+        if (live(r.out)) NN_CHECK(run(W(r.out)));
+    }
+    return {};
+}
+
 // A row insert into a tensor whose zero call is still pending does not launch
 // the zeroing first: the inserted rows are left out of it (SwiGLU::backward
 // zeroes its (2 d_ff, N) gradient and then inserts both halves).
@@ -1142,6 +1207,28 @@ Result<void> HipEngine::insert_rows(Tensor& dst, std::size_t start, const Tensor
     NN_CHECK(check_gpu_({&dst, &src}, "insert_rows"));
     if (dst.cols() != src.cols()) return fail("insert_rows: column count mismatch");
     if (start + src.rows() > dst.rows()) return fail("insert_rows: range out of bounds");
+    // A recorded SwiGLU gradient inserted into another tensor: written there directly.
+    for (std::size_t i = 0; i < pswb_.size(); ++i)
+    {
+        PendingSwb& r = pswb_[i];
+        const std::size_t off = start * dst.cols();
+        if (!same_t(r.out, src) || r.placed || r.uses(dst.dev_ptr()) || !aligned16(W(dst) + off)) continue;
+        // Records already placed into overlapping rows of dst run first.
+        bool overlap = false;
+        for (const auto& q : pswb_)
+            if (q.placed && same_t(q.dst, dst) && q.off < off + src.size() && off < q.off + q.out.size())
+                overlap = true;
+        if (overlap) break;
+        NN_CHECK(settle_ew_());
+        NN_CHECK(settle_chain_write_(dst, true));
+        for (auto& z : pzero_)
+            if (same_t(z.t, dst)) z.covered.emplace_back(start, start + src.rows());
+        PendingSwb& q = pswb_[i];
+        q.dst = dst;
+        q.off = off;
+        q.placed = true;
+        return {};
+    }
     PendingZero* z = nullptr;
     for (auto& e : pzero_)
         if (same_t(e.t, dst)) z = &e;
@@ -1889,14 +1976,41 @@ std::optional<Result<Tensor>> HipEngine::fused_layer_program_(const ExprSpec& sp
                            return nnhip_rmsnorm_bwd_dx(a[0], a[1], a[2], a[3], a[4], o, rows, cols, stream_);
                        },
                        "eval_expr(rmsnorm backward dx)");
-        if (is(LayerProg::SwigluGate))
-            return run(rows, cols,
-                       [&](float* o) { return nnhip_swiglu_grad_gate(a[0], a[1], a[2], a[3], o, rows * cols, stream_); },
-                       "eval_expr(swiglu grad gate)");
-        if (is(LayerProg::SwigluUp))
-            return run(rows, cols,
-                       [&](float* o) { return nnhip_swiglu_grad_up(a[0], a[1], a[2], o, rows * cols, stream_); },
-                       "eval_expr(swiglu grad up)");
+        // The SwiGLU gradients are recorded (PendingSwb) when their operands
+        // allow the float4 kernels; the layer's next calls insert them.
+        auto arg = [&](const float* p) -> Tensor {
+            for (const Tensor& t : inputs)
+                if (t.dev_ptr() == p) return t;
+            return Tensor();
+        };
+        const bool al = aligned16(a[0]) && aligned16(a[1]) && aligned16(a[2]);
+        if (is(LayerProg::SwigluGate) && al && aligned16(a[3]))
+        {
+            if (pswb_.size() >= 2) NN_CHECK(settle_swb_());
+            NN_TRY(o, alloc_(rows, cols));
+            PendingSwb r;
+            r.up = false;
+            r.G = arg(a[0]);
+            r.upt = arg(a[1]);
+            r.s = arg(a[2]);
+            r.gate = arg(a[3]);
+            r.out = o;
+            pswb_.push_back(std::move(r));
+            return Result<Tensor>(o);
+        }
+        if (is(LayerProg::SwigluUp) && al)
+        {
+            if (pswb_.size() >= 2) NN_CHECK(settle_swb_());
+            NN_TRY(o, alloc_(rows, cols));
+            PendingSwb r;
+            r.up = true;
+            r.G = arg(a[0]);
+            r.gate = arg(a[1]);
+            r.s = arg(a[2]);
+            r.out = o;
+            pswb_.push_back(std::move(r));
+            return Result<Tensor>(o);
+        }
         return std::nullopt;
     }
     if (!vec4) return std::nullopt;

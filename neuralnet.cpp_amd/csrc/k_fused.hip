@@ -123,6 +123,25 @@ struct SwigluGradUp
     }
 };
 
+// Both SwiGLU gradients in one pass (G, up, s, gate read once), each rounded as
+// its own program rounds it.
+struct SwigluGradBoth
+{
+    const float* g;
+    const float* up;
+    const float* s;
+    const float* gate;
+    float* og;
+    float* ou;
+    __device__ void operator()(size_t i) const
+    {
+        const float4 a = ld4(g + i), b = ld4(up + i), c = ld4(s + i), d = ld4(gate + i);
+        st4(og + i, make_float4(SwigluGradGate::one(a.x, b.x, c.x, d.x), SwigluGradGate::one(a.y, b.y, c.y, d.y),
+                                SwigluGradGate::one(a.z, b.z, c.z, d.z), SwigluGradGate::one(a.w, b.w, c.w, d.w)));
+        st4(ou + i, make_float4((a.x * d.x) * c.x, (a.y * d.y) * c.y, (a.z * d.z) * c.z, (a.w * d.w) * c.w));
+    }
+};
+
 // ── column sums: out[c] = sum_r f(r, c) ──────────────────────────────────────
 // A workgroup owns 32 columns (8 float4s: one 128-byte line per row) and
 // splits the rows over 32 row groups; the 32 partial sums are added in
@@ -317,4 +336,11 @@ extern "C" int nnhip_swiglu_grad_up(const float* G, const float* gate, const flo
 {
     if (!shape_ok(1, count, {G, gate, s, out})) return kBadShape;
     return launch_flat(SwigluGradUp{G, gate, s, out}, count, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_swiglu_grad_both(const float* G, const float* up, const float* s, const float* gate,
+                                      float* out_gate, float* out_up, size_t count, void* stream)
+{
+    if (!shape_ok(1, count, {G, up, s, gate, out_gate, out_up})) return kBadShape;
+    return launch_flat(SwigluGradBoth{G, up, s, gate, out_gate, out_up}, count, static_cast<hipStream_t>(stream));
 }

@@ -175,6 +175,9 @@ private:
     struct PendingGemm;
     struct PendingBwd;
     struct PendingEw;
+    struct PendingSwb;
+    std::vector<PendingSwb> pswb_;
+    Result<void> settle_swb_();
     struct PendingMm;
     std::unique_ptr<PendingMm> pmm_;
     Result<void> settle_mm_();
@@ -217,7 +220,7 @@ private:
     Result<void> settle_reads_(std::initializer_list<const Tensor*> ts);
     Result<void> settle_write_(const Tensor& t);
     Result<void> settle_chain_reads_(std::initializer_list<const Tensor*> ts);
-    Result<void> settle_chain_write_(const Tensor& t);
+    Result<void> settle_chain_write_(const Tensor& t, bool keep_swb = false);   // keep_swb: placed SwiGLU records stay
     Result<void> ew_push_(unsigned code, unsigned op, bool first, const Tensor& dst, const Tensor& a, const Tensor* b,
                           float s);
     Result<void> settle_ew_();

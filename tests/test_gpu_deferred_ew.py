@@ -225,3 +225,38 @@ def test_zero_then_inserts(hip):
     hip.insert_rows(dst, 0, src)
     ref[0:30] = 0
     assert np.array_equal(dst.numpy(), ref)
+
+
+def swiglu_backward(e, G, U, S, Ga, after=lambda: None, read_parts=False, dst_init=None):
+    """SwiGLU::backward's calls: both gradient programs, then zero + two row inserts."""
+    import layer_programs as lp
+    F, N = G.shape
+    spec_g, slots_g = lp.swiglu_grad_gate()
+    spec_u, slots_u = lp.swiglu_grad_up()
+    t = dict(g=e.tensor(G), up=e.tensor(U), s=e.tensor(S), gate=e.tensor(Ga))
+    gg = e.eval_expr(spec_g, [t[n] for n in slots_g], F, N); after()
+    gu = e.eval_expr(spec_u, [t[n] for n in slots_u], F, N); after()
+    dst = e.tensor(dst_init) if dst_init is not None else e.create_tensor(2 * F, N)
+    if dst_init is None:
+        e.zero(dst); after()
+    e.insert_rows(dst, 0, gg); after()
+    e.insert_rows(dst, F, gu); after()
+    parts = [gg.numpy(), gu.numpy()] if read_parts else []
+    del gg, gu                               # as when SwiGLU::backward returns: one pass for both halves
+    return [dst.numpy()] + parts
+
+
+@pytest.mark.parametrize("F,N,read_parts,init", [(3072, 8192, False, False), (24, 36, True, False),
+                                                 (40, 64, False, True), (8, 12, True, True)])
+def test_swiglu_backward_into_gradient(hip, cpu, F, N, read_parts, init):
+    rng = np.random.default_rng(F + N)
+    G, U, Ga = normal(rng, (F, N)), normal(rng, (F, N)), normal(rng, (F, N))
+    S = uniform(rng, (F, N), 0.0, 1.0)
+    D0 = uniform(rng, (2 * F, N)) if init else None
+    fused = swiglu_backward(hip, G, U, S, Ga, read_parts=read_parts, dst_init=D0)
+    calls = swiglu_backward(hip, G, U, S, Ga, hip.settle, read_parts=read_parts, dst_init=D0)
+    for a, b in zip(fused, calls):
+        assert np.array_equal(bits(a), bits(b))
+    ref = swiglu_backward(cpu, G, U, S, Ga, read_parts=read_parts, dst_init=D0)
+    for a, b in zip(fused, ref):
+        assert nrm_err(a, b) <= 1e-6
