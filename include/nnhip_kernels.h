@@ -202,6 +202,15 @@ int nnhip_flash_backward_layout(const float* Q, const float* Kt, const float* dO
                                 float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K,
                                 size_t Kd, float alpha, float alpha2, size_t mask_batch_stride, int g_is_do,
                                 void* workspace, void* stream);
+/* Backward of the materialised path when the forward output O is at hand (per batch (K, M), dim-major,
+ * computed from the same V as Vp): R_i = alpha2 dO_i . O_i, then one key-line pass for dK, dV and
+ * dS = W (P - R) (stored in the workspace), then dQ = alpha dS K; G is dO's columns (Kd == K). Workspace
+ * from nnhip_flash_ds_workspace_bytes (batch*M*N floats of dS included). No CUDA counterpart. */
+size_t nnhip_flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K);
+int nnhip_flash_backward_ds(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* O,
+                            const float* mask, const void* cells, const float* m, const float* l, float* dQ, float* dK,
+                            float* dV, size_t batch, size_t M, size_t N, size_t K, float alpha, float alpha2,
+                            size_t mask_batch_stride, void* workspace, void* stream);
 
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */

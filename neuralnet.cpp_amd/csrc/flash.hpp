@@ -58,6 +58,7 @@ struct FlashBwdArgs
     float alpha, alpha2;
     long mask_bs;        // floats between batch entries' masks (0: one mask shared)
     int g_do;            // G_i is dO's column i (dV_j = sum_i W dO_i; needs Kd == K)
+    float* dS;           // the key-line pass also stores dS_ij = W (P - R_i) here, (batch*M, N)
 };
 
 // Shapes the one-pass kernels take: head dims K (and Kd) <= 64, value width
@@ -70,5 +71,10 @@ int flash_classify(const float* mask, size_t masks, long mask_bs, size_t M, size
 size_t flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D, bool backward);
 int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, hipStream_t s);
 int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, hipStream_t s);
+// Backward when the forward output O (per batch (Kd, M), dim-major, from the same V as V') is at hand:
+// R_i = alpha2 dO_i . O_i directly, one key-line pass for dK, dV and dS, then dQ = alpha dS K.
+size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K);
+int flash_backward_ds(const FlashBwdArgs& a, const float* O, const unsigned char* cells, size_t batch,
+                      void* workspace, hipStream_t s);
 
 } // namespace nnhip

@@ -382,10 +382,12 @@ struct HipEngine::PendingAttn
     std::size_t batch, M, N, Kd;
     float alpha;
     Tensor m, l;              // row max and sum, once the fused forward has run
+    Tensor V, O;              // the fused forward's values and output (R_i = dO_i . O_i in the backward)
     bool stats = false, materialised = false;
     bool uses(const float* p) const
     {
-        return has_buf(Q, p) || has_buf(K, p) || has_buf(mask, p) || has_buf(A, p);
+        return has_buf(Q, p) || has_buf(K, p) || has_buf(mask, p) || has_buf(A, p) || has_buf(V, p) ||
+               has_buf(O, p);
     }
 };
 struct HipEngine::PendingDv
@@ -851,6 +853,8 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
                          "attention forward"));
         p->m = m;
         p->l = l;
+        p->V = A;
+        p->O = out;
         p->stats = true;
         return R(out);
     }
@@ -881,15 +885,27 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
             NN_TRY(t, alloc_(batch * q.Kd, q.N));
             dV = t;
         }
-        NN_TRY(Rr, alloc_(batch * q.M, 1));
         NN_TRY(cells, mask_cells_(&q.mask, q.M, q.N));
         const std::size_t bs = q.mask.rows() == q.M ? 0 : q.M * q.N;
-        NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, q.M, q.N, q.Kd, 4, 1)));
-        NN_CHECK(kernel_(nnhip_flash_backward_layout(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), nullptr, 0, D(q.mask),
-                                                     cells, D(q.m), D(q.l), W(Rr), W(dQ), W(dK), W(dV), batch, q.M,
-                                                     q.N, q.Kd, pds_->Kd2, q.alpha, pds_->alpha2, bs, 1, ws->data(),
-                                                     stream_),
-                         "attention backward"));
+        if (q.O.dev_ptr() && same_t(pds_->Vp, q.V) && q.V.rows() == batch * q.Kd)
+        {
+            // R from the forward output (same V): one key-line pass plus dQ from the stored dS.
+            NN_TRY(ws, scratch_(nnhip_flash_ds_workspace_bytes(batch, q.M, q.N, q.Kd)));
+            NN_CHECK(kernel_(nnhip_flash_backward_ds(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), D(q.O), D(q.mask),
+                                                     cells, D(q.m), D(q.l), W(dQ), W(dK), W(dV), batch, q.M, q.N,
+                                                     q.Kd, q.alpha, pds_->alpha2, bs, ws->data(), stream_),
+                             "attention backward"));
+        }
+        else
+        {
+            NN_TRY(Rr, alloc_(batch * q.M, 1));
+            NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, q.M, q.N, q.Kd, 4, 1)));
+            NN_CHECK(kernel_(nnhip_flash_backward_layout(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), nullptr, 0,
+                                                         D(q.mask), cells, D(q.m), D(q.l), W(Rr), W(dQ), W(dK), W(dV),
+                                                         batch, q.M, q.N, q.Kd, pds_->Kd2, q.alpha, pds_->alpha2, bs,
+                                                         1, ws->data(), stream_),
+                             "attention backward"));
+        }
         if (dv_here) pdv_.reset();
         pgrads_ = std::make_unique<AttnGrads>(AttnGrads{pds_->out, q.Q, q.K, dQ, dK, q.alpha});
         return attn_bmm_(A, B, batch, tA, tB, alpha);

@@ -840,7 +840,7 @@ __device__ __forceinline__ void cols_store(const FlashBwdArgs& a, const FlashGeo
         }
 }
 
-template <int KP, bool GDO>
+template <int KP, bool GDO, bool WDS>
 __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo& g, int b, int grp, int rg,
                                            float (*Qs)[32][KP + 4], float (*Os)[32][KP + 4],
                                            float (*Gs)[32][KP + 4], float (*St)[3][32], unsigned long long* nz_s)
@@ -914,6 +914,17 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
                     w[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(w[r], kLog2e, -St[buf][0][ii])) * St[buf][1][ii];
                     ds[r] = w[r] * (a.alpha2 * p[r] - St[buf][2][ii]);
                 }
+                if constexpr (WDS)
+                {
+                    // dS of the cell, for the query-line pass (row i, key kj).
+                    float* dsb = a.dS + (long)b * g.M * g.N + kj;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                    {
+                        const int i = ibase + drow(r, h);
+                        if (i < g.M && kj < g.N) dsb[(long)i * g.N] = ds[r];
+                    }
+                }
                 if constexpr (GDO)
                     value_chain<KP>(Os[buf], w, h, c, dv);
                 else
@@ -934,7 +945,7 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
     cols_store<KP>(a, g, lw, b, line, rg, dk, dv);
 }
 
-template <int KP, bool GDO>
+template <int KP, bool GDO, bool WDS>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdArgs a, FlashGeo g)
 {
     __shared__ __align__(16) float Qs[2][32][KP + 4];   // query tile [query][dim]
@@ -943,7 +954,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdArgs 
     __shared__ float St[2][3][32];                      // m, 1/l, R of the tile's queries
     __shared__ unsigned long long nz_s[kWaves];
     const Item it = item_of(g);
-    cols_group<KP, GDO>(a, g, it.b, it.grp, it.rg, Qs, Os, Gs, St, nz_s);
+    cols_group<KP, GDO, WDS>(a, g, it.b, it.grp, it.rg, Qs, Os, Gs, St, nz_s);
 }
 
 template <int KP>
@@ -980,6 +991,77 @@ __global__ __launch_bounds__(64) void k_flash_bwd_cols_combine(FlashBwdArgs a, F
     }
     const LineWork one{1ull, 0ull, 1ull, 1};
     cols_store<KP>(a, g, one, b, line, 0, dk, dv);
+}
+
+// dQ from the stored dS: dQ_i = alpha sum_j dS_ij k_j over the non-empty cells
+// of the line's range, with the rows kernel's lines, ranges, partials and
+// combine (R and Y of the partials are zero).
+template <int KP>
+__global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a, FlashGeo g)
+{
+    constexpr int DU = KP / 32;
+    __shared__ __align__(16) float Ks[2][32][KP + 4];   // key tile [key][dim]
+    __shared__ unsigned long long nz_s[kWaves];
+    const Item it = item_of(g);
+    const int b = it.b, rg = it.rg;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
+    const int line = it.grp * kWaves + wave, qi = line * 32 + c;
+    const LineWork lw = line_work(g, true, b, line, rg);
+    if (lane == 0) nz_s[wave] = lw.nz;
+    __syncthreads();
+    const unsigned long long any = nz_s[0] | nz_s[1] | nz_s[2] | nz_s[3];
+    f32x16 x[DU], y[DU];
+#pragma unroll
+    for (int u = 0; u < DU; ++u)
+    {
+        x[u] = zero16();
+        y[u] = zero16();
+    }
+    if (any)
+    {
+        const int cell0 = rg * g.R;
+        const float* Kb = a.Kt + (long)b * a.K * g.N;
+        const float* dsrow = a.dS + ((long)b * g.M + min(qi, g.M - 1)) * g.N;
+        TTile<KP> kt;
+        int cur = __builtin_ctzll(any);
+        unsigned long long rest = any & (any - 1);
+        kt.load(Kb, a.K, g.N, 32 * (cell0 + cur), threadIdx.x);
+        kt.store(Ks[0], threadIdx.x);
+        __syncthreads();
+        int buf = 0;
+        while (true)
+        {
+            const int nxt = rest ? __builtin_ctzll(rest) : -1;
+            if (nxt >= 0) kt.load(Kb, a.K, g.N, 32 * (cell0 + nxt), threadIdx.x);
+            if ((lw.nz >> cur) & 1ull)
+            {
+                float w[16];
+                mask_row16(dsrow, g.N, 32 * (cell0 + cur), h, w);
+                value_chain<KP>(Ks[buf], w, h, c, x);
+            }
+            if (nxt < 0) break;
+            kt.store(Ks[buf ^ 1], threadIdx.x);
+            __syncthreads();
+            buf ^= 1;
+            cur = nxt;
+            rest &= rest - 1;
+        }
+    }
+    rows_store<KP>(a, g, lw, b, line, rg, 0.0f, x, y);
+}
+
+// R_i = alpha2 sum_d dO(d, i) O(d, i): per batch (Kd, M) dim-major operands.
+__global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ dO, const float* __restrict__ O,
+                                                      float* __restrict__ R, int M, int Kd, long total, float alpha2)
+{
+    const long t = (long)blockIdx.x * 256 + threadIdx.x;
+    if (t >= total) return;
+    const long b = t / M, i = t % M;
+    const float* p = dO + b * Kd * M + i;
+    const float* q = O + b * Kd * M + i;
+    float acc = 0.0f;
+    for (int d = 0; d < Kd; ++d) acc = __builtin_fmaf(p[(long)d * M], q[(long)d * M], acc);
+    R[t] = alpha2 * acc;
 }
 
 // Mask cell classes: 0 all -inf, 1 all zero, 2 general. blockIdx.z: which mask.
@@ -1099,9 +1181,11 @@ int launch_bwd(const FlashBwdArgs& a, const FlashGeo& gr, const FlashGeo& gc, si
         if (int rc = launch_status()) return rc;
     }
     if (a.g_do)
-        hipLaunchKernelGGL((k_flash_bwd_cols<KP, true>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a, gc);
+        hipLaunchKernelGGL((k_flash_bwd_cols<KP, true, false>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a,
+                           gc);
     else
-        hipLaunchKernelGGL((k_flash_bwd_cols<KP, false>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a, gc);
+        hipLaunchKernelGGL((k_flash_bwd_cols<KP, false, false>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a,
+                           gc);
     if (int rc = launch_status()) return rc;
     if (gc.NR == 1) return 0;
     hipLaunchKernelGGL((k_flash_bwd_cols_combine<KP>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(64), 0, s, a,
@@ -1164,9 +1248,84 @@ int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t bat
     return KP == 32 ? launch_bwd<32>(a, gr, gc, batch, s) : launch_bwd<64>(a, gr, gc, batch, s);
 }
 
+size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K)
+{
+    const int KP = pad32(K);
+    const size_t part = std::max(part_bytes(geo(batch, M, N, true, rows_pw(KP), nullptr, nullptr), batch, true),
+                                 part_bytes(geo(batch, M, N, false, cols_pw(KP), nullptr, nullptr), batch, false));
+    return align256(batch * M * N * sizeof(float)) + align256(batch * M * sizeof(float)) + part;
+}
+
+int flash_backward_ds(const FlashBwdArgs& a0, const float* O, const unsigned char* cells, size_t batch, void* ws,
+                      hipStream_t s)
+{
+    if (!ws || a0.K != a0.Kd) return -1;
+    FlashBwdArgs a = a0;
+    char* w = static_cast<char*>(ws);
+    const size_t M = static_cast<size_t>(a.M), N = static_cast<size_t>(a.N);
+    a.dS = reinterpret_cast<float*>(w);
+    w += align256(batch * M * N * sizeof(float));
+    a.R = reinterpret_cast<float*>(w);
+    w += align256(batch * M * sizeof(float));
+    a.g_do = 1;
+    const int KP = pad32(static_cast<size_t>(a.K));
+    const unsigned char* cl = a.mask ? cells : nullptr;
+    const bool pb = a.mask && a.mask_bs != 0;
+    const FlashGeo gr = geo(batch, M, N, true, rows_pw(KP), cl, w, pb);
+    const FlashGeo gc = geo(batch, M, N, false, cols_pw(KP), cl, w, pb);
+    const long total = static_cast<long>(batch * M);
+    hipLaunchKernelGGL(k_flash_rowdot, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, a.dO, O,
+                       a.R, a.M, a.Kd, total, a.alpha2);
+    if (int rc = launch_status()) return rc;
+    auto run = [&](auto kp) -> int {
+        constexpr int P = decltype(kp)::value;
+        hipLaunchKernelGGL((k_flash_bwd_cols<P, true, true>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a,
+                           gc);
+        if (int rc = launch_status()) return rc;
+        if (gc.NR > 1)
+        {
+            hipLaunchKernelGGL((k_flash_bwd_cols_combine<P>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(64),
+                               0, s, a, gc);
+            if (int rc = launch_status()) return rc;
+        }
+        hipLaunchKernelGGL((k_flash_bwd_dq<P>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, a, gr);
+        if (int rc = launch_status()) return rc;
+        if (gr.NR > 1)
+        {
+            hipLaunchKernelGGL((k_flash_bwd_rows_combine<P>), dim3(static_cast<unsigned>(batch * gr.RT)), dim3(64),
+                               0, s, a, gr);
+            if (int rc = launch_status()) return rc;
+        }
+        return 0;
+    };
+    return KP == 32 ? run(std::integral_constant<int, 32>{}) : run(std::integral_constant<int, 64>{});
+}
+
 } // namespace nnhip
 
 // ── C-ABI (include/nnhip_kernels.h) ─────────────────────────────────────────
+extern "C" size_t nnhip_flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K)
+{
+    return nnhip::flash_ds_workspace_bytes(batch, M, N, K);
+}
+
+extern "C" int nnhip_flash_backward_ds(const float* Q, const float* Kt, const float* dO, const float* Vp,
+                                       const float* O, const float* mask, const void* cells, const float* m,
+                                       const float* l, float* dQ, float* dK, float* dV, size_t batch, size_t M,
+                                       size_t N, size_t K, float alpha, float alpha2, size_t mask_batch_stride,
+                                       void* workspace, void* stream)
+{
+    if (!Q || !Kt || !dO || !Vp || !O || !m || !l || !dQ || !dK || !dV || !workspace || (mask && !cells)) return -1;
+    if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
+    if (!nnhip::flash_supported(batch, M, N, K, 4) || K % 4 != 0) return -3;
+    nnhip::FlashBwdArgs a{Q, Kt, dO, Vp, nullptr, mask, m, l, nullptr, dQ, dK, dV, static_cast<int>(M),
+                          static_cast<int>(N), static_cast<int>(K), static_cast<int>(K), static_cast<int>(K), alpha,
+                          alpha2};
+    a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
+    return nnhip::flash_backward_ds(a, O, static_cast<const unsigned char*>(cells), batch, workspace,
+                                    static_cast<hipStream_t>(stream));
+}
+
 extern "C" int nnhip_flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D)
 {
     return nnhip::flash_supported(batch, M, N, K, D) ? 1 : 0;
