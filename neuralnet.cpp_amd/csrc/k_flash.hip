@@ -914,6 +914,12 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
                     w[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(w[r], kLog2e, -St[buf][0][ii])) * St[buf][1][ii];
                     ds[r] = w[r] * (a.alpha2 * p[r] - St[buf][2][ii]);
                 }
+
+                if constexpr (GDO)
+                    value_chain<KP>(Os[buf], w, h, c, dv);
+                else
+                    value_chain<KP>(Gs[buf], w, h, c, dv);
+                value_chain<KP>(Qs[buf], ds, h, c, dk);
                 if constexpr (WDS)
                 {
                     // dS of the cell, for the query-line pass (row i, key kj).
@@ -925,11 +931,6 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
                         if (i < g.M && kj < g.N) dsb[(long)i * g.N] = ds[r];
                     }
                 }
-                if constexpr (GDO)
-                    value_chain<KP>(Os[buf], w, h, c, dv);
-                else
-                    value_chain<KP>(Gs[buf], w, h, c, dv);
-                value_chain<KP>(Qs[buf], ds, h, c, dk);
             }
             if (nxt < 0) break;
             qt.store(Qs[buf ^ 1], threadIdx.x);
@@ -1059,9 +1060,15 @@ __global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ 
     const long b = t / M, i = t % M;
     const float* p = dO + b * Kd * M + i;
     const float* q = O + b * Kd * M + i;
-    float acc = 0.0f;
-    for (int d = 0; d < Kd; ++d) acc = __builtin_fmaf(p[(long)d * M], q[(long)d * M], acc);
-    R[t] = alpha2 * acc;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // four independent chains keep loads in flight
+    int d = 0;
+    for (; d + 4 <= Kd; d += 4)
+    {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(p[(long)(d + e) * M], q[(long)(d + e) * M], acc[e]);
+    }
+    for (; d < Kd; ++d) acc[0] = __builtin_fmaf(p[(long)d * M], q[(long)d * M], acc[0]);
+    R[t] = alpha2 * ((acc[0] + acc[1]) + (acc[2] + acc[3]));
 }
 
 // Mask cell classes: 0 all -inf, 1 all zero, 2 general. blockIdx.z: which mask.
