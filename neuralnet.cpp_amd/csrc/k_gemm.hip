@@ -387,7 +387,7 @@ Plan plan_gemm(size_t M, size_t N, size_t K, size_t batch, bool allow_split)
         if (want > 1)
         {
             size_t ks = (K + want - 1) / want;
-            ks = (ks + 15) / 16 * 16;   // whole BK stages per slice
+            ks = (ks + 31) / 32 * 32;   // whole BK stages per slice
             p.k_split = static_cast<int>(ks);
             p.splits = static_cast<int>((K + ks - 1) / ks);
         }
