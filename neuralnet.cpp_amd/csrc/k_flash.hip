@@ -77,7 +77,30 @@ __device__ __forceinline__ f32x16 zero16()
 __device__ __forceinline__ int drow(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 // exp(x) for x <= 0 (or -inf -> 0) on the hardware exp2.
 __device__ __forceinline__ float exp_neg(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
-__device__ __forceinline__ float fmax_f(float a, float b) { return a < b ? b : a; }
+// v_max_f32; for the finite and -inf scores here the same as (a < b ? b : a).
+__device__ __forceinline__ float fmax_f(float a, float b) { return __builtin_fmaxf(a, b); }
+
+// Buffer loads with the hardware range check: a load whose byte offset is at
+// or past the resource's size returns 0 without touching memory, so padding
+// elements (offset kOob) are zero with no branch around the load. A resource
+// covers one batch entry's array, below 2 GiB (flash_supported). Word 3 sets
+// the 32-bit data format that untyped loads need on gfx9-family parts.
+using Rsrc = __amdgpu_buffer_rsrc_t;
+constexpr unsigned kOob = 0x80000000u;
+__device__ __forceinline__ Rsrc rsrc(const float* base, long floats)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(floats * 4), 0x00020000);
+}
+__device__ __forceinline__ float bload(Rsrc r, unsigned off)
+{
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ float4 bload4(Rsrc r, unsigned off)
+{
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
 
 // Workgroups are dispatched round-robin over the 8 XCDs (one L2 each); this
 // gives each XCD a contiguous run of work items, so the items of one batch
@@ -168,6 +191,7 @@ struct TTile
     float4 r[NQ];
     __device__ __forceinline__ void load(const float* base, int dims, int T, int t0, int tid)
     {
+        const Rsrc rs = rsrc(base, (long)dims * T);
         const int tok = tid & 31, q0 = tid >> 5, t = t0 + tok;
 #pragma unroll
         for (int s = 0; s < NQ; ++s)
@@ -175,7 +199,8 @@ struct TTile
             const int d0 = 4 * (q0 + 8 * s);
             float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = (t < T && d0 + e < dims) ? base[(long)(d0 + e) * T + t] : 0.0f;
+            for (int e = 0; e < 4; ++e)
+                v[e] = bload(rs, (t < T && d0 + e < dims) ? 4u * static_cast<unsigned>((d0 + e) * T + t) : kOob);
             r[s] = make_float4(v[0], v[1], v[2], v[3]);
         }
     }
@@ -196,13 +221,13 @@ struct RTile
     float4 r[NQ];
     __device__ __forceinline__ void load(const float* base, int ld, int ncols, int T, int t0, int tid)
     {
+        const Rsrc rs = rsrc(base, (long)T * ld);
 #pragma unroll
         for (int s = 0; s < NQ; ++s)
         {
             const int idx = tid + 256 * s, tok = idx / QPR, q = idx % QPR;
-            r[s] = (t0 + tok < T && 4 * q < ncols)
-                       ? *reinterpret_cast<const float4*>(base + (long)(t0 + tok) * ld + 4 * q)
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            r[s] = bload4(rs, (t0 + tok < T && 4 * q < ncols) ? 4u * static_cast<unsigned>((t0 + tok) * ld + 4 * q)
+                                                               : kOob);
         }
     }
     __device__ __forceinline__ void store(float (*lds)[DP + 4], int tid) const
@@ -216,8 +241,20 @@ struct RTile
     }
 };
 
-// mask(row, jbase + drow(r, h)) for r = 0..15 (zero past column N).
-__device__ __forceinline__ void mask_row16(const float* mrow, int N, int jbase, int h, float* mv)
+// A row of an (M, N) array of one batch entry: the entry's resource and the
+// row's byte offset.
+struct MRow
+{
+    Rsrc rs;
+    unsigned row;
+};
+__device__ __forceinline__ MRow mrow_of(const float* batch_base, int M, int N, int row)
+{
+    return MRow{rsrc(batch_base, (long)M * N), 4u * static_cast<unsigned>(row) * static_cast<unsigned>(N)};
+}
+
+// X(row, jbase + drow(r, h)) for r = 0..15 (zero past column N).
+__device__ __forceinline__ void mask_row16(const MRow& x, int N, int jbase, int h, float* mv)
 {
     if ((N & 3) == 0)
     {
@@ -225,7 +262,7 @@ __device__ __forceinline__ void mask_row16(const float* mrow, int N, int jbase, 
         for (int g4 = 0; g4 < 4; ++g4)
         {
             const int j = jbase + 8 * g4 + 4 * h;
-            const float4 v = j < N ? *reinterpret_cast<const float4*>(mrow + j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 v = bload4(x.rs, j < N ? x.row + 4u * j : kOob);
             mv[4 * g4 + 0] = v.x;
             mv[4 * g4 + 1] = v.y;
             mv[4 * g4 + 2] = v.z;
@@ -238,7 +275,7 @@ __device__ __forceinline__ void mask_row16(const float* mrow, int N, int jbase, 
         for (int r = 0; r < 16; ++r)
         {
             const int j = jbase + drow(r, h);
-            mv[r] = j < N ? mrow[j] : 0.0f;
+            mv[r] = bload(x.rs, j < N ? x.row + 4u * j : kOob);
         }
     }
 }
@@ -387,12 +424,11 @@ __device__ __forceinline__ void fwd_store(const FlashFwdArgs& a, const FlashGeo&
 // Scores of one cell for this lane's query (16 keys drow(r,h) of the cell):
 // alpha * dot + mask, -inf for keys past N. Returns the cell's row maximum.
 template <bool FULL, bool MASKED>
-__device__ __forceinline__ float cell_scores(const f32x16& s, float alpha, const float* mrow, int N, int jbase, int h,
+__device__ __forceinline__ float cell_scores(const f32x16& s, float alpha, const MRow& mrow, int N, int jbase, int h,
                                              float* x)
 {
     float mv[16];
     if constexpr (MASKED) mask_row16(mrow, N, jbase, h, mv);
-    float cmax = kLowest;
 #pragma unroll
     for (int r = 0; r < 16; ++r)
     {
@@ -400,9 +436,14 @@ __device__ __forceinline__ float cell_scores(const f32x16& s, float alpha, const
         if constexpr (MASKED) v += mv[r];
         if constexpr (!FULL) v = jbase + drow(r, h) < N ? v : kNegInf;
         x[r] = v;
-        cmax = fmax_f(cmax, v);
     }
-    return cmax;
+    // Pairwise tree: 4 levels of independent v_max instead of a 16-long chain.
+    float t8[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) t8[r] = fmax_f(x[r], x[r + 8]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) t8[r] = fmax_f(t8[r], t8[r + 4]);
+    return fmax_f(kLowest, fmax_f(fmax_f(t8[0], t8[2]), fmax_f(t8[1], t8[3])));
 }
 
 // Forward workgroup: 4 waves on 4 consecutive query lines (32 queries each)
@@ -472,7 +513,7 @@ __global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(Fla
         float qf[KP / 2];
         line_operand<KP>(Qb, a.K, g.M, qi, h, qf);
         const int qc = min(qi, g.M - 1);
-        const float* mrow = a.mask ? a.mask + it.b * a.mask_bs + (long)qc * g.N : nullptr;
+        const MRow mrow = mrow_of(a.mask ? a.mask + it.b * a.mask_bs : a.Q, a.mask ? g.M : 0, g.N, qc);
         store(0, c0, c1);
         __syncthreads();
         int buf = 0;
@@ -659,7 +700,7 @@ __device__ __forceinline__ void rows_group(const FlashBwdArgs& a, const FlashGeo
         const float mi = a.m[srow], li = a.l[srow];
         const float linv = li != 0.0f ? 1.0f / li : 0.0f;
         const float mb = mi == kLowest ? 0.0f : mi * kLog2e;   // a row without allowed keys has only -inf scores
-        const float* mrow = a.mask ? a.mask + b * a.mask_bs + (long)qc * g.N : nullptr;
+        const MRow mrow = mrow_of(a.mask ? a.mask + b * a.mask_bs : a.Q, a.mask ? g.M : 0, g.N, qc);
         kt.store(Ks[0], threadIdx.x);
         vt.store(Vs[0], threadIdx.x);
         __syncthreads();
@@ -1022,7 +1063,7 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a,
     {
         const int cell0 = rg * g.R;
         const float* Kb = a.Kt + (long)b * a.K * g.N;
-        const float* dsrow = a.dS + ((long)b * g.M + min(qi, g.M - 1)) * g.N;
+        const MRow dsrow = mrow_of(a.dS + (long)b * g.M * g.N, g.M, g.N, min(qi, g.M - 1));
         TTile<KP> kt;
         int cur = __builtin_ctzll(any);
         unsigned long long rest = any & (any - 1);
@@ -1207,8 +1248,11 @@ bool flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D)
     // Head dims up to 64 and value widths up to 64 in multiples of 4 (16-byte
     // value rows); sizes that fit int; at most 2^30 cells over all batches.
     // Lines of at most 64 ranges of 64 cells: M, N <= 131072.
+    // One batch entry's (M, N) mask or score gradients below 2 GiB (32-bit
+    // buffer offsets).
     return batch >= 1 && M >= 1 && N >= 1 && K >= 1 && K <= 64 && D >= 1 && D <= 64 && D % 4 == 0 &&
            M <= (size_t{1} << 17) && N <= (size_t{1} << 17) && batch <= (size_t{1} << 20) &&
+           M * N < (size_t{1} << 29) &&
            batch * ((M + 31) / 32) * ((N + 31) / 32) <= (size_t{1} << 30);
 }
 
@@ -1407,7 +1451,9 @@ extern "C" int nnhip_flash_backward_layout(const float* Q, const float* Kt, cons
     if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
     if (g_is_do && Kd != K) return -1;
     if (g_is_do) ldg = K;
-    if (!nnhip::flash_supported(batch, M, N, K > Kd ? K : Kd, 4) || K % 4 != 0 || ldg < K || ldg % 4 != 0) return -3;
+    if (!nnhip::flash_supported(batch, M, N, K > Kd ? K : Kd, 4) || K % 4 != 0 || ldg < K || ldg % 4 != 0 ||
+        M * ldg >= (size_t{1} << 29))
+        return -3;
     nnhip::FlashBwdArgs a{Q, Kt, dO, Vp, G, mask, m, l, R, dQ, dK, dV, static_cast<int>(M), static_cast<int>(N),
                           static_cast<int>(K), static_cast<int>(Kd), static_cast<int>(ldg), alpha, alpha2};
     a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
