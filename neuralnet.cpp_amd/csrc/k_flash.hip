@@ -91,6 +91,13 @@ __device__ __forceinline__ Rsrc rsrc(const float* base, long floats)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(floats * 4), 0x00020000);
 }
+// off when sgn >= 0, else an out-of-range offset (bit 31 set; resources are
+// below 2 GiB). Integer arithmetic only: a select here can be turned into a
+// branch around the load, with a wait for every load in flight inside it.
+__device__ __forceinline__ unsigned oob_if_neg(unsigned off, int sgn)
+{
+    return off | (static_cast<unsigned>(sgn) & 0x80000000u);
+}
 __device__ __forceinline__ float bload(Rsrc r, unsigned off)
 {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
@@ -199,8 +206,8 @@ struct TTile
             const int d0 = 4 * (q0 + 8 * s);
             float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                v[e] = bload(rs, (t < T && d0 + e < dims) ? 4u * static_cast<unsigned>((d0 + e) * T + t) : kOob);
+            for (int e = 0; e < 4; ++e)   // dims past the array fall past the resource by themselves
+                v[e] = bload(rs, oob_if_neg(4u * static_cast<unsigned>((d0 + e) * T + t), T - 1 - t));
             r[s] = make_float4(v[0], v[1], v[2], v[3]);
         }
     }
@@ -226,8 +233,8 @@ struct RTile
         for (int s = 0; s < NQ; ++s)
         {
             const int idx = tid + 256 * s, tok = idx / QPR, q = idx % QPR;
-            r[s] = bload4(rs, (t0 + tok < T && 4 * q < ncols) ? 4u * static_cast<unsigned>((t0 + tok) * ld + 4 * q)
-                                                               : kOob);
+            r[s] = bload4(rs, oob_if_neg(4u * static_cast<unsigned>((t0 + tok) * ld + 4 * q),
+                                         (T - 1 - t0 - tok) | (ncols - 1 - 4 * q)));
         }
     }
     __device__ __forceinline__ void store(float (*lds)[DP + 4], int tid) const
@@ -262,7 +269,7 @@ __device__ __forceinline__ void mask_row16(const MRow& x, int N, int jbase, int 
         for (int g4 = 0; g4 < 4; ++g4)
         {
             const int j = jbase + 8 * g4 + 4 * h;
-            const float4 v = bload4(x.rs, j < N ? x.row + 4u * j : kOob);
+            const float4 v = bload4(x.rs, oob_if_neg(x.row + 4u * j, N - 1 - j));
             mv[4 * g4 + 0] = v.x;
             mv[4 * g4 + 1] = v.y;
             mv[4 * g4 + 2] = v.z;
@@ -275,7 +282,7 @@ __device__ __forceinline__ void mask_row16(const MRow& x, int N, int jbase, int 
         for (int r = 0; r < 16; ++r)
         {
             const int j = jbase + drow(r, h);
-            mv[r] = bload(x.rs, j < N ? x.row + 4u * j : kOob);
+            mv[r] = bload(x.rs, oob_if_neg(x.row + 4u * j, N - 1 - j));
         }
     }
 }

@@ -60,12 +60,21 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
 {
     constexpr int NT = 64 * WM * WN;
     constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
-    constexpr int LDA_S = BM + PAD, LDB_S = BN + PAD;
     constexpr int LA = BM * BK / 4 / NT;   // float4 per thread per stage for A
     constexpr int LB = BN * BK / 4 / NT;
     static_assert(LA * 4 * NT == BM * BK && LB * 4 * NT == BN * BK, "tile not divisible by the workgroup");
-    __shared__ __attribute__((aligned(16))) float As[2][BK][LDA_S];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK][LDB_S];
+    // An A contiguous in k (untransposed) is staged as it lies, [m][k] (one
+    // 16-byte LDS write per float4); a transposed A and B are staged k-major.
+    // Within a stage the MFMA steps take k in the order k = 8 * (lane / 32) +
+    // step, so a lane's eight k of one row of A are adjacent (two 16-byte LDS
+    // reads); B uses the same order. Measured on the config-4 products: NN
+    // 101 -> 105 and 113 -> 117 TFLOP/s; staging a transposed B as [n][k] as
+    // well was 3-5 % slower on the weight-gradient (NT) products.
+    constexpr bool AK = !TA;
+    constexpr int KROW = BK + 4;   // [m][k] row stride: 8 rows cover all 32 banks
+    constexpr int A_R = AK ? BM : BK, A_C = AK ? KROW : BM + PAD;
+    __shared__ __attribute__((aligned(16))) float As[2][A_R][A_C];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK][BN + PAD];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -154,10 +163,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             else
             {
                 const int m = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
-                As[buf][k + 0][m] = ra[s].x;
-                As[buf][k + 1][m] = ra[s].y;
-                As[buf][k + 2][m] = ra[s].z;
-                As[buf][k + 3][m] = ra[s].w;
+                *reinterpret_cast<f4*>(&As[buf][m][k]) = ra[s];
             }
         }
     };
@@ -209,14 +215,16 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             load_a(k_lo + (kt + 1) * BK);
             load_b(k_lo + (kt + 1) * BK);
         }
+        static_assert(BK == 16, "k order assumes 8 MFMA steps per stage");
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 2)
+        for (int kk = 0; kk < 8; ++kk)
         {
+            const int k = 8 * kl + kk;
             float a[FM], b[FN];
 #pragma unroll
-            for (int i = 0; i < FM; ++i) a[i] = As[buf][kk + kl][am + 32 * i];
+            for (int i = 0; i < FM; ++i) a[i] = AK ? As[buf][am + 32 * i][k] : As[buf][k][am + 32 * i];
 #pragma unroll
-            for (int j = 0; j < FN; ++j) b[j] = Bs[buf][kk + kl][bn + 32 * j];
+            for (int j = 0; j < FN; ++j) b[j] = Bs[buf][k][bn + 32 * j];
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
