@@ -67,9 +67,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     // 16-byte LDS write per float4); a transposed A and B are staged k-major.
     // Within a stage the MFMA steps take k in the order k = 8 * (lane / 32) +
     // step, so a lane's eight k of one row of A are adjacent (two 16-byte LDS
-    // reads); B uses the same order. Measured on the config-4 products: NN
-    // 101 -> 105 and 113 -> 117 TFLOP/s; staging a transposed B as [n][k] as
-    // well was 3-5 % slower on the weight-gradient (NT) products.
+    // reads); B uses the same order. Measured on the GPT-step products (d 768,
+    // 8192 tokens): NN 101 -> 105 and 113 -> 117 TFLOP/s; staging a transposed
+    // B as [n][k] as well was 3-5 % slower on the weight-gradient (NT) products.
     constexpr bool AK = !TA;
     constexpr int KROW = BK + 4;   // [m][k] row stride: 8 rows cover all 32 banks
     constexpr int A_R = AK ? BM : BK, A_C = AK ? KROW : BM + PAD;
