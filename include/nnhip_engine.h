@@ -131,6 +131,16 @@ int nnhip_gpt_optimizer_step(nnhip_gpt* g);                  /* AdamW */
 int nnhip_gpt_zero_grad(nnhip_gpt* g);
 /* forward + CE + backward + AdamW + zero_grad on the resident batch. */
 int nnhip_gpt_train_step(nnhip_gpt* g, float* loss_out);
+/* Backward with the loss gradient scaled in place by grad_scale first: one micro-batch of
+ * gradient accumulation, 1 / accum_steps in src/text_train.cpp:1242-1253. */
+int nnhip_gpt_backward_scaled(nnhip_gpt* g, float grad_scale);
+/* Optimizer::clip_grad_norm (compute_optimizer.hpp:90-140): scales every gradient by
+ * max_norm / ||g||_2 when the global norm exceeds max_norm; max_norm <= 0 does nothing. */
+int nnhip_gpt_clip_grad_norm(nnhip_gpt* g, float max_norm);
+/* One iteration of the reference training loop (src/text_train.cpp:1181-1330): forward + CE,
+ * backward scaled by 1 / accum_steps (accum_steps >= 1); when do_update != 0 also
+ * clip_grad_norm(max_norm) if max_norm > 0, AdamW step and zero_grad. */
+int nnhip_gpt_train_step_ex(nnhip_gpt* g, size_t accum_steps, float max_norm, int do_update, float* loss_out);
 
 /* Measurement hooks (no reference counterpart). While enabled, every GEMM launch of the
  * engine is bracketed by HIP events on the engine's stream; _read waits for the stream and

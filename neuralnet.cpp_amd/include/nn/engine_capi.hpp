@@ -361,6 +361,51 @@ inline int gpt_backward(GptSession* g)
     return 0;
 }
 
+// Backward of one micro-batch when gradients are accumulated over several
+// (src/text_train.cpp:1242-1253): the loss gradient is scaled in place by
+// grad_scale (1 / accum_steps there) before the model backward, so the
+// accumulated gradients are the mean over the micro-batches.
+inline int gpt_backward_scaled(GptSession* g, float grad_scale)
+{
+    auto gr = g->ce.backward();
+    if (!gr) return set_error(gr.error().message);
+    if (grad_scale != 1.0f)
+        if (auto r = g->eng->scale_inplace(*gr, grad_scale); !r) return set_error(r.error().message);
+    auto b = g->model.backward(*gr);
+    if (!b) return set_error(b.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
+// Global L2-norm gradient clipping (Optimizer::clip_grad_norm,
+// compute_optimizer.hpp:90-140); max_norm <= 0 leaves the gradients alone.
+inline int gpt_clip_grad_norm(GptSession* g, float max_norm)
+{
+    if (auto r = g->opt->clip_grad_norm(max_norm); !r) return set_error(r.error().message);
+    return 0;
+}
+
+// One iteration of the reference training loop (src/text_train.cpp:1181-1330):
+// forward + CE (flush), backward with the loss gradient scaled by
+// 1 / accum_steps when accum_steps > 1 (end_batch); then, when do_update,
+// clip_grad_norm(max_norm) if max_norm > 0, and begin_batch, AdamW step,
+// zero_grad, end_batch.
+inline int gpt_train_step_ex(GptSession* g, std::size_t accum_steps, float max_norm, int do_update, float* loss)
+{
+    if (accum_steps == 0) return set_error("gpt: accum_steps must be at least 1");
+    if (int rc = gpt_forward_loss(g, loss)) return rc;
+    const float scale = accum_steps > 1 ? 1.0f / static_cast<float>(accum_steps) : 1.0f;
+    if (int rc = gpt_backward_scaled(g, scale)) return rc;
+    if (!do_update) return 0;
+    if (max_norm > 0)
+        if (int rc = gpt_clip_grad_norm(g, max_norm)) return rc;
+    if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
+    if (auto r = g->opt->step(); !r) return set_error(r.error().message);
+    if (auto r = g->opt->zero_grad(); !r) return set_error(r.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
 inline int gpt_step(GptSession* g)
 {
     if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
@@ -525,6 +570,19 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
     int NN_CAPI_CAT(P, gpt_train_step)(void* g, float* loss)                                                       \
     {                                                                                                               \
         return nn::capi::gpt_train_step(static_cast<nn::capi::GptSession*>(g), loss);                              \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_backward_scaled)(void* g, float s)                                                      \
+    {                                                                                                               \
+        return nn::capi::gpt_backward_scaled(static_cast<nn::capi::GptSession*>(g), s);                            \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_clip_grad_norm)(void* g, float max_norm)                                                \
+    {                                                                                                               \
+        return nn::capi::gpt_clip_grad_norm(static_cast<nn::capi::GptSession*>(g), max_norm);                      \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_train_step_ex)(void* g, size_t accum_steps, float max_norm, int do_update, float* loss) \
+    {                                                                                                               \
+        return nn::capi::gpt_train_step_ex(static_cast<nn::capi::GptSession*>(g), accum_steps, max_norm,            \
+                                           do_update, loss);                                                        \
     }                                                                                                               \
     }                                                                                                               \
     _Pragma("GCC visibility pop")

@@ -95,6 +95,9 @@ def _bind(lib: ctypes.CDLL, prefix: str):
         "gpt_optimizer_step": (i32, [vp]),
         "gpt_zero_grad": (i32, [vp]),
         "gpt_train_step": (i32, [vp, fp]),
+        "gpt_backward_scaled": (i32, [vp, ctypes.c_float]),
+        "gpt_clip_grad_norm": (i32, [vp, ctypes.c_float]),
+        "gpt_train_step_ex": (i32, [vp, ctypes.c_size_t, ctypes.c_float, ctypes.c_int, fp]),
         "build_attention_mask": (i32, [sz, sz, sz, i32, fp, ctypes.POINTER(ctypes.c_uint64), sz, fp]),
     }
     fns = {}
@@ -439,6 +442,20 @@ class GptSession:
     def train_step(self) -> float:
         v = ctypes.c_float()
         self._eng._check(self._f["gpt_train_step"](self._g, ctypes.byref(v)))
+        return v.value
+
+    def backward_scaled(self, grad_scale: float) -> None:
+        """Backward of one accumulated micro-batch: loss gradient scaled by grad_scale first."""
+        self._eng._check(self._f["gpt_backward_scaled"](self._g, float(grad_scale)))
+
+    def clip_grad_norm(self, max_norm: float) -> None:
+        self._eng._check(self._f["gpt_clip_grad_norm"](self._g, float(max_norm)))
+
+    def train_step_ex(self, accum_steps: int = 1, max_norm: float = 0.0, do_update: bool = True) -> float:
+        """One iteration of the reference training loop (src/text_train.cpp:1181-1330)."""
+        v = ctypes.c_float()
+        self._eng._check(self._f["gpt_train_step_ex"](self._g, int(accum_steps), float(max_norm),
+                                                      1 if do_update else 0, ctypes.byref(v)))
         return v.value
 
     def close(self):
