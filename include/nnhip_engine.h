@@ -104,6 +104,16 @@ int nnhip_engine_eval_expr(nnhip_engine* e, const uint8_t* instrs, size_t n_inst
 int nnhip_build_attention_mask(size_t batch, size_t seq, size_t heads, int alibi, const float* slopes,
                                const uint64_t* doc_ids, size_t n_doc, float* out);
 
+/* One training batch cut from a token flow (src/text_train.cpp:1137-1172). Window b starts at
+ * starts[b] < n_flow and holds win_len = min(seq, n_flow - starts[b]) tokens: x[t] = flow[start+t],
+ * y[t] = flow[start+t+1] inside it, pad_id past it; position t is in the loss iff t+1 < win_len.
+ * tokens (seq, batch) column per window; labels, loss_mask, doc_ids batch-major (b*seq + t);
+ * doc_ids = flow_doc[start+t] inside the window, 0 past it (skipped when flow_doc or doc_ids is
+ * NULL). *valid = positions in the loss. Host-only, no device use. */
+int nnhip_window_batch(const uint64_t* flow, const uint64_t* flow_doc, size_t n_flow, const uint64_t* starts,
+                       size_t batch, size_t seq, uint64_t pad_id, float* tokens, uint64_t* labels, float* loss_mask,
+                       uint64_t* doc_ids, size_t* valid);
+
 /* GPT training session (GPTModel + sparse CE + AdamW; SwiGLU FFN, RMSNorm). */
 typedef struct nnhip_gpt_config {
     size_t vocab_size, d_model, seq_len, num_heads, d_ff, num_layers;

@@ -432,6 +432,42 @@ inline int gpt_train_step(GptSession* g, float* loss)
     return 0;
 }
 
+// One training batch cut from a token flow, as src/text_train.cpp:1137-1172
+// builds it: window b starts at flow offset starts[b] and holds
+// win_len = min(seq, n_flow - start) tokens; x[t] = flow[start + t] and
+// y[t] = flow[start + t + 1] inside the window, pad_id past it; position t
+// takes part in the loss iff t + 1 < win_len. doc_ids (optional; flow_doc
+// null leaves them untouched) are flow_doc[start + t] inside the window and
+// 0 past it. tokens (seq, batch) column per window; labels, loss_mask and
+// doc_ids batch-major (b * seq + t). Returns the participating positions.
+inline int window_batch(const std::uint64_t* flow, const std::uint64_t* flow_doc, std::size_t n_flow,
+                        const std::uint64_t* starts, std::size_t batch, std::size_t seq, std::uint64_t pad_id,
+                        float* tokens, std::uint64_t* labels, float* loss_mask, std::uint64_t* doc_ids,
+                        std::size_t* valid)
+{
+    if (!flow || !starts || !tokens || !labels || !loss_mask || !valid || seq == 0)
+        return set_error("window_batch: null argument or seq 0");
+    std::size_t n_valid = 0;
+    for (std::size_t b = 0; b < batch; ++b)
+    {
+        if (starts[b] >= n_flow) return set_error("window_batch: window start past the flow");
+        const std::size_t pos = starts[b], len = std::min(seq, n_flow - pos);
+        for (std::size_t t = 0; t < seq; ++t)
+        {
+            const std::uint64_t x = t < len ? flow[pos + t] : pad_id;
+            const std::uint64_t y = t + 1 < len ? flow[pos + t + 1] : pad_id;
+            const bool take = t + 1 < len;
+            tokens[t * batch + b] = static_cast<float>(x);
+            labels[b * seq + t] = y;
+            loss_mask[b * seq + t] = take ? 1.0f : 0.0f;
+            n_valid += take ? 1 : 0;
+            if (flow_doc && doc_ids) doc_ids[b * seq + t] = t < len ? flow_doc[pos + t] : 0;
+        }
+    }
+    *valid = n_valid;
+    return 0;
+}
+
 inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads, int alibi, const float* slopes,
                           const std::uint64_t* doc_ids, std::size_t n_doc, float* out)
 {
@@ -570,6 +606,13 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
     int NN_CAPI_CAT(P, gpt_train_step)(void* g, float* loss)                                                       \
     {                                                                                                               \
         return nn::capi::gpt_train_step(static_cast<nn::capi::GptSession*>(g), loss);                              \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, window_batch)(const uint64_t* flow, const uint64_t* flow_doc, size_t n_flow,                 \
+                                     const uint64_t* starts, size_t batch, size_t seq, uint64_t pad_id, float* tokens, \
+                                     uint64_t* labels, float* loss_mask, uint64_t* doc_ids, size_t* valid)          \
+    {                                                                                                               \
+        return nn::capi::window_batch(flow, flow_doc, n_flow, starts, batch, seq, pad_id, tokens, labels, loss_mask, \
+                                      doc_ids, valid);                                                              \
     }                                                                                                               \
     int NN_CAPI_CAT(P, gpt_backward_scaled)(void* g, float s)                                                      \
     {                                                                                                               \

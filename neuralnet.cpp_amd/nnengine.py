@@ -62,6 +62,7 @@ class _GptConfig(ctypes.Structure):
 def _bind(lib: ctypes.CDLL, prefix: str):
     vp, sz, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
     fp = ctypes.POINTER(ctypes.c_float)
+    u64p = ctypes.POINTER(ctypes.c_uint64)
     sig = {
         "last_error": (ctypes.c_char_p, []),
         "engine_create": (i32, [ctypes.POINTER(vp)]),
@@ -96,6 +97,8 @@ def _bind(lib: ctypes.CDLL, prefix: str):
         "gpt_zero_grad": (i32, [vp]),
         "gpt_train_step": (i32, [vp, fp]),
         "gpt_backward_scaled": (i32, [vp, ctypes.c_float]),
+        "window_batch": (i32, [u64p, u64p, sz, u64p, sz, sz, ctypes.c_uint64, fp, u64p, fp, u64p,
+                               ctypes.POINTER(ctypes.c_size_t)]),
         "gpt_clip_grad_norm": (i32, [vp, ctypes.c_float]),
         "gpt_train_step_ex": (i32, [vp, ctypes.c_size_t, ctypes.c_float, ctypes.c_int, fp]),
         "build_attention_mask": (i32, [sz, sz, sz, i32, fp, ctypes.POINTER(ctypes.c_uint64), sz, fp]),
@@ -301,6 +304,26 @@ class Engine:
                                                     di.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)),
                                                     len(doc_ids), _fptr(out)))
         return out
+
+    def window_batch(self, flow, starts, seq, pad_id, flow_doc=None):
+        """One training batch cut from a token flow (src/text_train.cpp:1137-1172): returns
+        tokens (seq, batch) float32, labels and loss_mask (batch*seq,), doc_ids (batch*seq,) or
+        None, and the number of positions in the loss."""
+        u64 = ctypes.POINTER(ctypes.c_uint64)
+        fl = np.ascontiguousarray(np.asarray(flow, dtype=np.uint64))
+        st = np.ascontiguousarray(np.asarray(starts, dtype=np.uint64))
+        fd = None if flow_doc is None else np.ascontiguousarray(np.asarray(flow_doc, dtype=np.uint64))
+        batch = st.size
+        tokens = np.empty((seq, batch), dtype=np.float32)
+        labels = np.empty(batch * seq, dtype=np.uint64)
+        mask = np.empty(batch * seq, dtype=np.float32)
+        docs = None if fd is None else np.empty(batch * seq, dtype=np.uint64)
+        valid = ctypes.c_size_t()
+        self._check(self._f["window_batch"](fl.ctypes.data_as(u64), None if fd is None else fd.ctypes.data_as(u64),
+                                            fl.size, st.ctypes.data_as(u64), batch, seq, int(pad_id), _fptr(tokens),
+                                            labels.ctypes.data_as(u64), _fptr(mask),
+                                            None if docs is None else docs.ctypes.data_as(u64), ctypes.byref(valid)))
+        return tokens, labels, mask, docs, valid.value
 
     def gpt(self, **cfg) -> "GptSession":
         return GptSession(self, **cfg)

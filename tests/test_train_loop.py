@@ -123,3 +123,44 @@ def test_train_step_ex_rejects_zero_accum_steps(cpu):
     g.load_batch(*a)
     with pytest.raises(nnengine.EngineError):
         g.train_step_ex(accum_steps=0)
+
+
+def test_window_batch_hand_cases(cpu):
+    """src/text_train.cpp:1137-1172 on a 7-token flow cut into windows of 4 at stride 3:
+    full windows drop only their last label; the tail window holds one token."""
+    flow = [10, 11, 12, 13, 14, 15, 16]
+    docs = [1, 1, 1, 2, 2, 3, 3]
+    pad = 0
+    tokens, labels, mask, doc_ids, valid = cpu.window_batch(flow, [0, 3, 6], seq=4, pad_id=pad, flow_doc=docs)
+    assert tokens.T.tolist() == [[10, 11, 12, 13], [13, 14, 15, 16], [16, pad, pad, pad]]
+    assert labels.reshape(3, 4).tolist() == [[11, 12, 13, pad], [14, 15, 16, pad], [pad, pad, pad, pad]]
+    assert mask.reshape(3, 4).tolist() == [[1, 1, 1, 0], [1, 1, 1, 0], [0, 0, 0, 0]]
+    assert doc_ids.reshape(3, 4).tolist() == [[1, 1, 1, 2], [2, 2, 3, 3], [3, 0, 0, 0]]
+    assert valid == 6
+    t2, l2, m2, d2, v2 = cpu.window_batch(flow, [0, 3, 6], seq=4, pad_id=pad)
+    assert d2 is None and v2 == valid and np.array_equal(t2, tokens) and np.array_equal(l2, labels)
+    with pytest.raises(nnengine.EngineError):
+        cpu.window_batch(flow, [7], seq=4, pad_id=pad)
+
+
+def test_window_batch_feeds_a_session(cpu):
+    """A flow of documents (one id per document, as the reference's line-per-document
+    tokenisation gives them) through window_batch into the session: every full window
+    contributes seq - 1 positions, and the doc-masked forward and backward run on it."""
+    rng = np.random.default_rng(3)
+    T = CFG["seq_len"]
+    n_flow = 3 * T + 3
+    flow = rng.integers(1, CFG["vocab_size"], size=n_flow)
+    lengths = [5, 9, 4, 7]
+    docs = np.repeat(np.arange(1, len(lengths) + 1), lengths)
+    docs = np.concatenate([docs, np.full(n_flow - docs.size, len(lengths) + 1)])[:n_flow]
+    starts = list(range(0, n_flow, T))[:B]
+    tokens, labels, mask, doc_ids, valid = cpu.window_batch(flow, starts, T, pad_id=0, flow_doc=docs)
+    assert valid == int(mask.sum()) and valid == B * (T - 1)
+    params, _ = _setup(cpu)
+    g = _session(cpu, params)
+    g.set_doc_ids(doc_ids)
+    g.load_batch(tokens, labels, mask)
+    loss = g.forward_loss()
+    g.backward()
+    assert np.isfinite(loss) and loss > 0
