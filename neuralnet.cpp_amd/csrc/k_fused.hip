@@ -182,15 +182,28 @@ __global__ __launch_bounds__(kT) void k_fused_colsum(F f, float* out, unsigned r
     const unsigned qi = threadIdx.x % kColQuads, rg = threadIdx.x / kColQuads;
     const unsigned q = blockIdx.x * kColQuads + qi;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto add = [&](const float4& v) {
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    };
     if (q < cols4)
-        for (unsigned r = rg; r < rows; r += kRowGroups)
+    {
+        // Four rows' loads in flight per trip (one wave per SIMD at the GPT
+        // shapes, so each wave needs several); the sums keep row order.
+        unsigned r = rg;
+        for (; r + 3 * kRowGroups < rows; r += 4 * kRowGroups)
         {
-            const float4 v = f(r, q);
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
+            const float4 v0 = f(r, q), v1 = f(r + kRowGroups, q), v2 = f(r + 2 * kRowGroups, q),
+                         v3 = f(r + 3 * kRowGroups, q);
+            add(v0);
+            add(v1);
+            add(v2);
+            add(v3);
         }
+        for (; r < rows; r += kRowGroups) add(f(r, q));
+    }
     part[rg][qi] = acc;
     __syncthreads();
     if (threadIdx.x < kColQuads)
