@@ -133,6 +133,33 @@ private:
     std::size_t floats_, rounded_;
 };
 
+// A row slice viewing rows of a root buffer (a pool block, or a view that
+// holds a private copy). materialise() gives it its own block holding the
+// same floats and drops the root; after that it is a root itself.
+class HipView final : public DeviceBuffer
+{
+public:
+    HipView(std::shared_ptr<DeviceBuffer> root, std::size_t offset, std::size_t floats)
+        : root_(std::move(root)), off_(offset), floats_(floats)
+    {
+    }
+    float* data() noexcept override { return own_ ? own_->data() : root_->data() + off_; }
+    std::size_t capacity() const noexcept override { return floats_; }
+    bool aliased() const noexcept { return !own_; }
+    const DeviceBuffer* root() const noexcept { return root_.get(); }
+    const std::shared_ptr<DeviceBuffer>& root_ptr() const noexcept { return root_; }
+    std::size_t offset() const noexcept { return off_; }
+    void materialise(std::shared_ptr<DeviceBuffer> own)
+    {
+        own_ = std::move(own);
+        root_.reset();
+    }
+
+private:
+    std::shared_ptr<DeviceBuffer> root_, own_;
+    std::size_t off_, floats_;
+};
+
 const float* D(const Tensor& t) { return t.dev_ptr(); }
 float* W(const Tensor& t) { return t.dev_ptr(); }
 
@@ -651,6 +678,7 @@ Result<void> HipEngine::settle_write_(const Tensor& t)
 
 Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb)
 {
+    NN_CHECK(unshare_(t));
     const float* p = t.dev_ptr();
     if (!p) return {};
     if (pmm_ && pmm_->uses(p)) NN_CHECK(settle_mm_());
@@ -1172,14 +1200,53 @@ Result<Tensor> HipEngine::clone(const Tensor& src)
 }
 
 // ── row slices (cpu_engine.hpp:75-114) ──────────────────────────────────────
+// Returns a view of src's rows (see unshare_); views of views share the root.
 Result<Tensor> HipEngine::slice_rows(const Tensor& src, std::size_t start, std::size_t count)
 {
     NN_CHECK(need_gpu_({&src}, "slice_rows"));
     if (start + count > src.rows()) return fail("slice_rows: range out of bounds");
-    NN_TRY(t, alloc_(count, src.cols()));
     const std::size_t n = count * src.cols();
-    if (n) NN_CHECK(kernel_(nnhip_copy(D(src) + start * src.cols(), W(t), n, stream_), "slice_rows"));
-    return t;
+    if (!n) return alloc_(count, src.cols());
+    std::shared_ptr<DeviceBuffer> root = src.device_buffer();
+    std::size_t off = start * src.cols();
+    if (auto* v = dynamic_cast<HipView*>(root.get()); v && v->aliased())
+    {
+        off += v->offset();
+        root = v->root_ptr();
+    }
+    auto view = std::make_shared<HipView>(std::move(root), off, n);
+    std::erase_if(views_, [](const std::weak_ptr<DeviceBuffer>& w) { return w.expired(); });
+    views_.push_back(view);
+    return Tensor(std::static_pointer_cast<DeviceBuffer>(view), count, src.cols());
+}
+
+// Before t is written in place: a view t takes its private copy, and every
+// live view of t's memory takes one (the copies run before the write on the
+// stream; all earlier writes to that memory were launched when the views
+// were cut or when they unshared).
+Result<void> HipEngine::unshare_(const Tensor& t)
+{
+    if (views_.empty()) return {};
+    const DeviceBuffer* b = t.device_buffer().get();
+    if (!b) return {};
+    auto take_copy = [&](HipView& v) -> Result<void> {
+        const std::size_t n = v.capacity();
+        NN_TRY(own, alloc_(1, n));
+        NN_CHECK(kernel_(nnhip_copy(v.data(), W(own), n, stream_), "slice_rows copy on write"));
+        v.materialise(own.device_buffer());
+        return {};
+    };
+    for (auto& w : views_)
+        if (auto sp = w.lock())
+        {
+            auto* v = static_cast<HipView*>(sp.get());
+            if (v->aliased() && (v == b || v->root() == b)) NN_CHECK(take_copy(*v));
+        }
+    std::erase_if(views_, [](const std::weak_ptr<DeviceBuffer>& w) {
+        auto sp = w.lock();
+        return !sp || !static_cast<HipView*>(sp.get())->aliased();
+    });
+    return {};
 }
 
 // Launches the recorded SwiGLU gradient programs: into their rows of the

@@ -150,6 +150,11 @@ public:
 
 private:
     Result<Tensor> alloc_(std::size_t rows, std::size_t cols);
+    // Row slices are views of their source's memory until the view or the
+    // memory it aliases is written in place; then the view takes a private
+    // copy first (copy semantics as CpuEngine, without copying slices that
+    // are only read, e.g. SwiGLU's gate and up halves).
+    Result<void> unshare_(const Tensor& t);
     Result<std::shared_ptr<DeviceBuffer>> scratch_(std::size_t bytes);
     Result<void> kernel_(int rc, const char* what);
     // Checks that every tensor lives on this engine, then launches deferred
@@ -169,6 +174,7 @@ private:
         std::size_t M;   // rows of one mask (the tensor holds rows / M of them)
     };
     std::vector<CellTable> cells_;
+    std::vector<std::weak_ptr<DeviceBuffer>> views_;   // live row-slice views (HipView)
     Result<const void*> mask_cells_(const Tensor* mask, std::size_t M, std::size_t N);
 
     struct PendingFwd;
