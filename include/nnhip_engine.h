@@ -141,6 +141,13 @@ int nnhip_gpt_optimizer_step(nnhip_gpt* g);                  /* AdamW */
 int nnhip_gpt_zero_grad(nnhip_gpt* g);
 /* forward + CE + backward + AdamW + zero_grad on the resident batch. */
 int nnhip_gpt_train_step(nnhip_gpt* g, float* loss_out);
+/* The reference's model file, format v4 ("NNNN": header, ModelSpec record, parameter matrices
+ * in parameters() order, embedded tokenizer; model_serialization.hpp:36-52,380-503).
+ * _save writes the session's parameters (tokenizer may be NULL with tok_len 0); _load reads a
+ * file whose matrices match this session's shapes, *tok_len = embedded tokenizer length and up
+ * to tok_cap of its bytes are copied to tok_out. */
+int nnhip_gpt_save(nnhip_gpt* g, const char* path, const char* tokenizer, size_t tok_len);
+int nnhip_gpt_load(nnhip_gpt* g, const char* path, char* tok_out, size_t tok_cap, size_t* tok_len);
 /* Backward with the loss gradient scaled in place by grad_scale first: one micro-batch of
  * gradient accumulation, 1 / accum_steps in src/text_train.cpp:1242-1253. */
 int nnhip_gpt_backward_scaled(nnhip_gpt* g, float grad_scale);

@@ -11,6 +11,7 @@
 #include "compute_engine.hpp"
 #include "compute_loss.hpp"
 #include "compute_optimizer.hpp"
+#include "model_file.hpp"
 #include "model.hpp"
 
 namespace nn::capi
@@ -244,6 +245,7 @@ struct GptSession
     std::size_t vocab = 0, seq = 0, batch = 0, num_valid = 0;
     Tensor tokens, labels, mask, logits;
     bool has_batch = false, has_mask = false;
+    GptConfigC cfg{};
 };
 
 inline int gpt_create(EngineHandle* e, const GptConfigC* c, GptSession** out)
@@ -265,6 +267,7 @@ inline int gpt_create(EngineHandle* e, const GptConfigC* c, GptSession** out)
     s->grads = s->model.param_gradients();
     s->opt = std::make_unique<AdamW>(*s->eng, s->params, s->grads, c->lr, c->beta1, c->beta2, c->eps, c->weight_decay);
     s->vocab = c->vocab_size;
+    s->cfg = *c;
     if (auto r = s->eng->end_batch(); !r) return set_error(r.error().message);
     *out = s.release();
     return 0;
@@ -403,6 +406,42 @@ inline int gpt_train_step_ex(GptSession* g, std::size_t accum_steps, float max_n
     if (auto r = g->opt->step(); !r) return set_error(r.error().message);
     if (auto r = g->opt->zero_grad(); !r) return set_error(r.error().message);
     if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
+// The reference's model file (format v4; model_file.hpp): save_model /
+// load_model (model_serialization.hpp:380-503) for this session's GPT.
+inline int gpt_save(GptSession* g, const char* path, const char* tokenizer, std::size_t tok_len)
+{
+    if (!path) return set_error("gpt_save: null path");
+    std::vector<Matrix> ms;
+    for (auto& p : g->params)
+    {
+        auto m = g->eng->to_matrix(p.get());
+        if (!m) return set_error(m.error().message);
+        ms.push_back(std::move(*m));
+    }
+    const model_file::GptSpec spec{g->cfg.d_model,    g->cfg.num_heads, g->cfg.d_ff,   g->cfg.num_layers,
+                                   g->cfg.vocab_size, g->cfg.seq_len,   g->cfg.pos_enc};
+    auto r = model_file::save(path, spec, ms, std::string_view(tokenizer ? tokenizer : "", tokenizer ? tok_len : 0));
+    return r ? 0 : set_error(r.error().message);
+}
+
+// Loads parameters (shapes must match this session's model); the embedded
+// tokenizer's length goes to *tok_len and up to tok_cap of its bytes to tok_out.
+inline int gpt_load(GptSession* g, const char* path, char* tok_out, std::size_t tok_cap, std::size_t* tok_len)
+{
+    if (!path) return set_error("gpt_load: null path");
+    std::vector<Matrix> ms;
+    for (auto& p : g->params) ms.emplace_back(p.get().rows(), p.get().cols());
+    std::string tok;
+    auto spec = model_file::load(path, ms, tok);
+    if (!spec) return set_error(spec.error().message);
+    for (std::size_t i = 0; i < ms.size(); ++i)
+        if (auto r = g->eng->copy_from(g->params[i].get(), ms[i]); !r) return set_error(r.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    if (tok_len) *tok_len = tok.size();
+    if (tok_out && tok_cap) std::memcpy(tok_out, tok.data(), std::min(tok_cap, tok.size()));
     return 0;
 }
 
@@ -613,6 +652,14 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
     {                                                                                                               \
         return nn::capi::window_batch(flow, flow_doc, n_flow, starts, batch, seq, pad_id, tokens, labels, loss_mask, \
                                       doc_ids, valid);                                                              \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_save)(void* g, const char* path, const char* tok, size_t tok_len)                      \
+    {                                                                                                               \
+        return nn::capi::gpt_save(static_cast<nn::capi::GptSession*>(g), path, tok, tok_len);                      \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_load)(void* g, const char* path, char* tok_out, size_t tok_cap, size_t* tok_len)        \
+    {                                                                                                               \
+        return nn::capi::gpt_load(static_cast<nn::capi::GptSession*>(g), path, tok_out, tok_cap, tok_len);         \
     }                                                                                                               \
     int NN_CAPI_CAT(P, gpt_backward_scaled)(void* g, float s)                                                      \
     {                                                                                                               \

@@ -97,6 +97,8 @@ def _bind(lib: ctypes.CDLL, prefix: str):
         "gpt_zero_grad": (i32, [vp]),
         "gpt_train_step": (i32, [vp, fp]),
         "gpt_backward_scaled": (i32, [vp, ctypes.c_float]),
+        "gpt_save": (i32, [vp, ctypes.c_char_p, ctypes.c_char_p, sz]),
+        "gpt_load": (i32, [vp, ctypes.c_char_p, ctypes.c_char_p, sz, ctypes.POINTER(ctypes.c_size_t)]),
         "window_batch": (i32, [u64p, u64p, sz, u64p, sz, sz, ctypes.c_uint64, fp, u64p, fp, u64p,
                                ctypes.POINTER(ctypes.c_size_t)]),
         "gpt_clip_grad_norm": (i32, [vp, ctypes.c_float]),
@@ -466,6 +468,18 @@ class GptSession:
         v = ctypes.c_float()
         self._eng._check(self._f["gpt_train_step"](self._g, ctypes.byref(v)))
         return v.value
+
+    def save(self, path: str, tokenizer: bytes = b"") -> None:
+        """The reference's model file, format v4 (model_serialization.hpp:380-425)."""
+        self._eng._check(self._f["gpt_save"](self._g, path.encode(), tokenizer or None, len(tokenizer)))
+
+    def load(self, path: str) -> bytes:
+        """Loads parameters from a format-v4 model file; returns the embedded tokenizer bytes."""
+        n = ctypes.c_size_t()
+        self._eng._check(self._f["gpt_load"](self._g, path.encode(), None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(max(1, n.value))
+        self._eng._check(self._f["gpt_load"](self._g, path.encode(), buf, n.value, ctypes.byref(n)))
+        return buf.raw[:n.value]
 
     def backward_scaled(self, grad_scale: float) -> None:
         """Backward of one accumulated micro-batch: loss gradient scaled by grad_scale first."""
