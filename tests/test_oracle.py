@@ -500,3 +500,149 @@ def test_layer_programs_closed_form(cpu, name):
     ins = [ts[n] for n in slots]
     got = (cpu.eval_expr_reduce if vec else cpu.eval_expr)(spec, ins, F, N).numpy()
     assert nrm_err(got, closed({k: v.astype(np.float64) for k, v in args.items()})) <= 1e-6
+
+
+# ── pins for the remaining primitives: select, column broadcast, row max ───
+_CMP = {"Lt": np.less, "Le": np.less_equal, "Gt": np.greater, "Ge": np.greater_equal, "Eq": np.equal,
+        "Ne": np.not_equal}
+
+
+@pytest.mark.parametrize("cmp", sorted(_CMP))
+def test_select_scalar_cond_closed_form(cpu, cmp):
+    """elementwise_select_scalar_cond (reference cpu_engine.hpp:1221-1266): out = (A cmp b) ? T : e,
+    with ties (entries equal to b), signed zeros, infinities and NaN (every comparison with NaN is
+    false except Ne)."""
+    rng = np.random.default_rng(21)
+    b = np.float32(0.25)
+    A = rng.choice(np.array([-1.5, -0.0, 0.0, 0.25, 0.2500001, 0.2499999, 3.0, np.inf, -np.inf, np.nan],
+                            dtype=np.float32), size=(13, 17))
+    A[0, :4] = b                                  # ties in every case
+    T = normal(rng, (13, 17))
+    e = np.float32(-7.5)
+    got = cpu.elementwise_select_scalar_cond(cmp, cpu.tensor(A), float(b), cpu.tensor(T), float(e)).numpy()
+    with np.errstate(invalid="ignore"):
+        cond = _CMP[cmp](A, b)
+    assert np.array_equal(got, np.where(cond, T, e))
+    # b = 0 against signed zeros: -0.0 == 0.0
+    got0 = cpu.elementwise_select_scalar_cond(cmp, cpu.tensor(A), 0.0, cpu.tensor(T), float(e)).numpy()
+    with np.errstate(invalid="ignore"):
+        assert np.array_equal(got0, np.where(_CMP[cmp](A, np.float32(0.0)), T, e))
+    with pytest.raises(EngineError, match="shape"):
+        cpu.elementwise_select_scalar_cond(cmp, cpu.tensor(A), 0.0, cpu.tensor(T[:, :3]), 0.0)
+
+
+@pytest.mark.parametrize("op", ["Add", "Sub", "Mul", "Div", "Max", "Min"])
+def test_broadcast_inplace_closed_form(cpu, op):
+    """broadcast_col_inplace / broadcast_row_inplace (reference cpu_engine.hpp:1092-1125): A[r][c] op= v[c]
+    (v is (1, cols)) and A[r][c] op= v[r] (v is (rows, 1)); one float32 operation per element, so the
+    result equals numpy's float32 broadcast bit for bit."""
+    fn = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply, "Div": np.divide, "Max": np.maximum,
+          "Min": np.minimum}[op]
+    rng = np.random.default_rng(22)
+    A = uniform(rng, (9, 14), 0.1, 2.0)
+    A[0, 0] = 1.0
+    vc = uniform(rng, (1, 14), 0.5, 1.5)
+    vc[0, 0] = 1.0                                # ties for Max / Min
+    t = cpu.tensor(A)
+    cpu.broadcast_col_inplace(t, cpu.tensor(vc), op)
+    assert np.array_equal(t.numpy(), fn(A, vc))
+    vr = uniform(rng, (9, 1), 0.5, 1.5)
+    t = cpu.tensor(A)
+    cpu.broadcast_row_inplace(t, cpu.tensor(vr), op)
+    assert np.array_equal(t.numpy(), fn(A, vr))
+    with pytest.raises(EngineError, match="shape mismatch"):
+        cpu.broadcast_col_inplace(cpu.tensor(A), cpu.tensor(vr), op)
+    with pytest.raises(EngineError, match="shape mismatch"):
+        cpu.broadcast_row_inplace(cpu.tensor(A), cpu.tensor(vc), op)
+
+
+def test_row_reduce_max_closed_form(cpu):
+    """row_reduce_max (reference cpu_engine.hpp:1068-1076 over algebra_matrix.hpp:799-821): the
+    maximum over {lowest()} and the row, so a row of -inf (or an empty row) yields lowest(), not -inf."""
+    rng = np.random.default_rng(23)
+    A = normal(rng, (11, 37), 3.0)
+    A[2] = -np.inf
+    A[3, :5] = -np.inf
+    A[4] = np.finfo(np.float32).min
+    A[5, 7] = np.inf
+    got = cpu.row_reduce_max(cpu.tensor(A)).numpy()
+    lowest = np.finfo(np.float32).min
+    assert got.shape == (11, 1)
+    assert np.array_equal(got[:, 0], np.max(A, axis=1, initial=lowest))
+    assert got[2, 0] == lowest and got[5, 0] == np.inf
+    assert np.array_equal(cpu.col_reduce_max(cpu.tensor(A.T.copy())).numpy()[0], got[:, 0])
+    empty = cpu.row_reduce_max(cpu.tensor(np.zeros((3, 0), dtype=np.float32))).numpy()
+    assert np.array_equal(empty[:, 0], np.full(3, lowest, dtype=np.float32))
+
+
+@pytest.mark.parametrize("view", ["RowReduceSum", "RowReduceMax", "ColReduceSum", "ColReduceMax"])
+def test_expr_reduce_views_closed_form(cpu, view):
+    """The reduce views of eval_expr (reference cpu_engine.hpp:1368-1396): each row (Row*) or column
+    (Col*) of the input is summed, or maxed from lowest(), and the scalar is read at every element of
+    that row / column. Checked through out = view(x) - y * 2 against float64 sums and exact maxima."""
+    rng = np.random.default_rng(24)
+    R, C = 19, 29
+    x = normal(rng, (R, C))
+    x[1] = -np.inf                                # a row of -inf: max view yields lowest()
+    x[:, 2] = -np.inf                             # a column of -inf
+    if view.endswith("Sum"):
+        x = np.where(np.isfinite(x), x, 0.5).astype(np.float32)
+    y = normal(rng, (R, C))
+    s = ExprSpec()
+    s.view(view), s.view("Linear")
+    c2 = s.const(2.0)
+    r0 = s.ins("Mul", inp(1), cst(c2))
+    s.ins("Sub", inp(0), reg(r0))
+    got = cpu.eval_expr(s, [cpu.tensor(x), cpu.tensor(y)], R, C).numpy()
+    axis = 1 if view.startswith("Row") else 0
+    if view.endswith("Sum"):
+        red_v = np64(x).sum(axis=axis, keepdims=True)
+        assert nrm_err(got, red_v - 2 * np64(y)) <= 1e-6
+    else:
+        red_v = np.max(x, axis=axis, keepdims=True, initial=np.finfo(np.float32).min)
+        assert np.array_equal(got, (red_v - np.float32(2) * y).astype(np.float32))
+    # as the operand of a reduce instruction along the same axis (eval_expr_reduce requires one
+    # axis for views and instructions): every element of a row / column holds the same scalar
+    # (finite input here: C copies of lowest() would overflow the float32 sum)
+    xf = np.where(np.isfinite(x), x, 0.5).astype(np.float32)
+    s = ExprSpec()
+    s.view(view)
+    s.ins("RowSum" if axis == 1 else "ColSum", inp(0))
+    vec = cpu.eval_expr_reduce(s, [cpu.tensor(xf)], R, C).numpy()
+    if view.endswith("Sum"):
+        ref = np.broadcast_to(np64(xf).sum(axis=axis, keepdims=True), (R, C)).sum(axis=axis)
+    else:
+        ref = np.broadcast_to(np64(xf).max(axis=axis, keepdims=True), (R, C)).sum(axis=axis)
+    assert nrm_err(vec.reshape(-1), ref) <= 1e-6
+
+
+def test_inplace_and_copy_primitives_closed_form(cpu):
+    """add_inplace / scale_inplace / axpy_inplace / zero (reference cpu_engine.hpp:1008-1040), insert_rows
+    and clone (:67-110): one float32 operation per element (bit-exact against numpy float32) and
+    exact copies."""
+    rng = np.random.default_rng(25)
+    A, B = normal(rng, (7, 9)), normal(rng, (7, 9))
+    t = cpu.tensor(A)
+    cpu.add_inplace(t, cpu.tensor(B))
+    assert np.array_equal(t.numpy(), A + B)
+    cpu.scale_inplace(t, 0.3)
+    assert np.array_equal(t.numpy(), (A + B) * np.float32(0.3))
+    # a + s*b is contracted to one fused multiply-add (as clang, the reference's compiler, does by
+    # default): the float64 value rounded once, within half an ulp of the float32 result
+    x = (A + B) * np.float32(0.3)
+    cpu.axpy_inplace(t, -1.25, cpu.tensor(B))
+    ref = np64(x) + -1.25 * np64(B)
+    got = t.numpy()
+    assert np.all(np.abs(got - ref) <= 0.5 * np.spacing(np.abs(got)))
+    c = cpu.clone(t)
+    cpu.zero(t)
+    assert not t.numpy().any() and np.array_equal(c.numpy(), got)
+    dst = cpu.tensor(A)
+    cpu.insert_rows(dst, 2, cpu.tensor(B[:3]))
+    ref = A.copy()
+    ref[2:5] = B[:3]
+    assert np.array_equal(dst.numpy(), ref)
+    with pytest.raises(EngineError):
+        cpu.insert_rows(dst, 6, cpu.tensor(B[:3]))
+    with pytest.raises(EngineError):
+        cpu.add_inplace(cpu.tensor(A), cpu.tensor(B[:3]))
