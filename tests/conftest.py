@@ -21,6 +21,10 @@ import nnengine  # noqa: E402
 
 ORACLE_LIB = os.path.join(ROOT, "oracle", "_build", "libnnoracle.so")
 
+# The oracle's thread pool reads NNORACLE_THREADS once, at first use: size it to
+# the CPUs this process may run on, at most 16 (a GPU box's share of its host).
+os.environ.setdefault("NNORACLE_THREADS", str(max(1, min(len(os.sched_getaffinity(0)), 16))))
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP engine parity / kernels)")

@@ -362,20 +362,37 @@ def test_gpt_step_small(hip, cpu, pos):
     check_adam_params(h[3], c[3], c[2], lr=1e-3)
 
 
-def check_adam_params(got, ref, ref_grads, lr):
+def check_adam_params(got, ref, ref_grads, lr, got_grads=None, params0=None):
     """Updated weights within 1e-5 of max|w|, except where the first AdamW step
-    (~ -lr*sign(g)) flips sign on a near-zero gradient: such entries may differ
-    by up to 2*lr and must be rare."""
+    (~ -lr*sign(g)) flips sign on a gradient the gradient tolerance does not
+    resolve. Without got_grads: |g| <= 1e-3 of the tensor's largest (the bar the
+    gradients are held to, floored at 1e-4 of the model's largest gradient as
+    grad_errs floors it: the key bias's gradient is rounding noise around 0).
+    With got_grads and params0: the engine's weight there equals the closed-form
+    AdamW step from its own gradient (torch_gpt.adamw_step), and its gradient is
+    within that bar of the oracle's, so the two updates differ only because the
+    first step, g / (|g| + eps), is sensitive to small gradients. Such entries
+    may differ by up to 2*lr and must be rare (<= 0.1 %). Returns their number."""
+    import torch_gpt
     flips = 0
     total = 0
+    scale = max(float(np.abs(g).max()) for g in ref_grads if g.size)
     for i, (a, b, g) in enumerate(zip(got, ref, ref_grads)):
         d = np.abs(a.astype(np.float64) - b)
-        bad = d > 1e-5 * max(np.abs(b).max(), 1e-6)
+        tol = 1e-5 * max(np.abs(b).max(), 1e-6)
+        bad = d > tol
         assert np.all(d[bad] <= 2.0 * lr * 1.01), i
-        assert np.all(np.abs(g[bad]) <= 1e-4 * max(np.abs(g).max(), 1e-30) + 1e-12), i
+        if got_grads is None:
+            assert np.all(np.abs(g[bad]) <= 1e-3 * max(np.abs(g).max(), 1e-4 * scale)), i
+        elif bad.any():
+            gh = got_grads[i][bad].astype(np.float64)
+            assert np.all(np.abs(gh - g[bad]) <= 1e-3 * max(np.abs(g).max(), 1e-4 * scale)), i
+            own = torch_gpt.adamw_step([params0[i][bad]], [gh], lr=lr)[0]
+            assert np.all(np.abs(a[bad] - own) <= tol), i
         flips += int(bad.sum())
         total += b.size
     assert flips <= max(3, total // 1000), (flips, total)
+    return flips
 
 
 def test_gpt_doc_ids(hip, cpu):
