@@ -409,6 +409,22 @@ inline int gpt_train_step_ex(GptSession* g, std::size_t accum_steps, float max_n
     return 0;
 }
 
+// The ModelSpec this session's model is built from (model_spec.hpp:58-77).
+inline model_file::GptSpec session_spec(const GptSession& g)
+{
+    model_file::GptSpec s;
+    s.d_model = g.cfg.d_model;
+    s.num_heads = g.cfg.num_heads;
+    s.d_ff = g.cfg.d_ff;
+    s.num_layers = g.cfg.num_layers;
+    s.vocab_size = g.cfg.vocab_size;
+    s.seq_len = g.cfg.seq_len;
+    s.pos_encoding = g.cfg.pos_enc;
+    s.activation = model_file::kActivationSwiGLU;
+    s.norm_type = model_file::kNormRMSNorm;
+    return s;
+}
+
 // The reference's model file (format v4; model_file.hpp): save_model /
 // load_model (model_serialization.hpp:380-503) for this session's GPT.
 inline int gpt_save(GptSession* g, const char* path, const char* tokenizer, std::size_t tok_len)
@@ -421,14 +437,20 @@ inline int gpt_save(GptSession* g, const char* path, const char* tokenizer, std:
         if (!m) return set_error(m.error().message);
         ms.push_back(std::move(*m));
     }
-    const model_file::GptSpec spec{g->cfg.d_model,    g->cfg.num_heads, g->cfg.d_ff,   g->cfg.num_layers,
-                                   g->cfg.vocab_size, g->cfg.seq_len,   g->cfg.pos_enc};
-    auto r = model_file::save(path, spec, ms, std::string_view(tokenizer ? tokenizer : "", tokenizer ? tok_len : 0));
+    auto r = model_file::save(path, session_spec(*g), ms,
+                              std::string_view(tokenizer ? tokenizer : "", tokenizer ? tok_len : 0));
     return r ? 0 : set_error(r.error().message);
 }
 
-// Loads parameters (shapes must match this session's model); the embedded
-// tokenizer's length goes to *tok_len and up to tok_cap of its bytes to tok_out.
+// Loads a model file into this session. The reference builds its model from
+// the file's spec and then creates the optimizer (text_train.cpp:940-966);
+// a session's model already exists, so the file's spec must describe it field
+// for field (a file of another head count, context or position encoding has
+// the same matrix shapes but another model), and the AdamW state (moments and
+// step count) starts afresh, as a newly created optimizer's does. The type
+// check is build_gpt_model_from_spec's (domain_gpt.hpp:87-99). The embedded
+// tokenizer's length goes to *tok_len and up to tok_cap of its bytes to
+// tok_out (a tokenizer is never longer than the file that holds it).
 inline int gpt_load(GptSession* g, const char* path, char* tok_out, std::size_t tok_cap, std::size_t* tok_len)
 {
     if (!path) return set_error("gpt_load: null path");
@@ -437,8 +459,23 @@ inline int gpt_load(GptSession* g, const char* path, char* tok_out, std::size_t 
     std::string tok;
     auto spec = model_file::load(path, ms, tok);
     if (!spec) return set_error(spec.error().message);
+    if (spec->type != model_file::kTypeGpt && spec->pos_encoding != model_file::kPosALiBi)
+        return set_error("Invalid ModelSpec type for GPT: expected GPT or ALiBi_GPT");
+    const model_file::GptSpec want = session_spec(*g);
+    const std::pair<const char*, std::pair<std::uint64_t, std::uint64_t>> fields[] = {
+        {"d_model", {spec->d_model, want.d_model}},          {"num_heads", {spec->num_heads, want.num_heads}},
+        {"d_ff", {spec->d_ff, want.d_ff}},                   {"num_layers", {spec->num_layers, want.num_layers}},
+        {"vocab_size", {spec->vocab_size, want.vocab_size}}, {"seq_len", {spec->seq_len, want.seq_len}},
+        {"pos_encoding", {spec->pos_encoding, want.pos_encoding}},
+        {"activation", {spec->activation, want.activation}}, {"norm_type", {spec->norm_type, want.norm_type}}};
+    for (const auto& [key, v] : fields)
+        if (v.first != v.second)
+            return set_error("gpt_load: the file's " + std::string(key) + " is " + std::to_string(v.first) +
+                             ", this session's model has " + std::to_string(v.second));
     for (std::size_t i = 0; i < ms.size(); ++i)
         if (auto r = g->eng->copy_from(g->params[i].get(), ms[i]); !r) return set_error(r.error().message);
+    g->opt = std::make_unique<AdamW>(*g->eng, g->params, g->grads, g->cfg.lr, g->cfg.beta1, g->cfg.beta2,
+                                     g->cfg.eps, g->cfg.weight_decay);
     if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
     if (tok_len) *tok_len = tok.size();
     if (tok_out && tok_cap) std::memcpy(tok_out, tok.data(), std::min(tok_cap, tok.size()));
@@ -511,6 +548,8 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
                           const std::uint64_t* doc_ids, std::size_t n_doc, float* out)
 {
     if (n_doc != 0 && n_doc < batch * seq) return set_error("build_attention_mask: doc_ids too small for batch*seq");
+    if (!out || (alibi && !slopes) || (n_doc != 0 && !doc_ids))
+        return set_error("build_attention_mask: null output, slopes (ALiBi needs one per head) or doc_ids");
     std::vector<Scalar> sl;
     if (alibi) sl.assign(slopes, slopes + heads);
     std::vector<std::size_t> d(doc_ids, doc_ids + n_doc);

@@ -30,12 +30,15 @@ namespace nn::model_file
 constexpr std::uint32_t kMagic = 0x4E4E4E4Eu, kVersion = 4;
 constexpr std::uint8_t kPrecisionF32 = 0;
 // ModelSpec enum values (reference model_spec.hpp:24-55).
-constexpr std::uint64_t kTypeGpt = 3, kActivationSwiGLU = 1, kNormRMSNorm = 1;
+constexpr std::uint64_t kTypeGpt = 3, kPosALiBi = 2, kActivationSwiGLU = 1, kNormRMSNorm = 1;
 
+// The GPT fields of a ModelSpec. Fields a file leaves out keep ModelSpec's
+// defaults (model_spec.hpp:58-77: pos_encoding Learned, activation GeLU,
+// norm_type LayerNorm), as spec_from_kv leaves them (model_serialization.hpp:238-266).
 struct GptSpec
 {
     std::uint64_t d_model = 0, num_heads = 0, d_ff = 0, num_layers = 0, vocab_size = 0, seq_len = 0,
-                  pos_encoding = 0;
+                  pos_encoding = 0, activation = 0, norm_type = 0, type = kTypeGpt;
 };
 
 inline void put_u32(std::string& o, std::uint32_t v)
@@ -61,8 +64,8 @@ inline std::string encode_spec(const GptSpec& g)
     const std::pair<const char*, std::uint64_t> u[] = {
         {"d_model", g.d_model},       {"num_heads", g.num_heads},   {"d_ff", g.d_ff},
         {"num_layers", g.num_layers}, {"patch_size", 0},            {"vocab_size", g.vocab_size},
-        {"seq_len", g.seq_len},       {"pos_encoding", g.pos_encoding}, {"activation", kActivationSwiGLU},
-        {"norm_type", kNormRMSNorm}};
+        {"seq_len", g.seq_len},       {"pos_encoding", g.pos_encoding}, {"activation", g.activation},
+        {"norm_type", g.norm_type}};
     put_u32(o, 2 + static_cast<std::uint32_t>(std::size(u)));
     auto field = [&](const char* key, std::uint8_t type) {
         put_u32(o, static_cast<std::uint32_t>(std::strlen(key)));
@@ -71,7 +74,7 @@ inline std::string encode_spec(const GptSpec& g)
     };
     field("type", 0);
     put_u32(o, 8);
-    put_u64(o, kTypeGpt);
+    put_u64(o, g.type);
     field("layer_dims", 2);   // empty for a GPT
     put_u32(o, 0);
     for (const auto& [k, v] : u)
@@ -85,7 +88,7 @@ inline std::string encode_spec(const GptSpec& g)
 
 // Reads the u64 fields of a spec record (unknown types are skipped by length,
 // as KeyValueRecord::parse does); type must be present and non-zero.
-inline Result<GptSpec> decode_spec(std::string_view s, std::uint64_t* type_out = nullptr)
+inline Result<GptSpec> decode_spec(std::string_view s)
 {
     std::uint64_t count = 0, type = 0;
     if (!take(s, count, 4)) return fail("model file: spec record has no field count");
@@ -111,9 +114,11 @@ inline Result<GptSpec> decode_spec(std::string_view s, std::uint64_t* type_out =
         else if (key == "vocab_size") g.vocab_size = v;
         else if (key == "seq_len") g.seq_len = v;
         else if (key == "pos_encoding") g.pos_encoding = v;
+        else if (key == "activation") g.activation = v;
+        else if (key == "norm_type") g.norm_type = v;
     }
     if (type == 0) return fail("model file: spec has no valid type field");
-    if (type_out) *type_out = type;
+    g.type = type;
     return g;
 }
 

@@ -299,6 +299,8 @@ class Engine:
 
     # -- pure host helpers ------------------------------------------------------
     def build_attention_mask(self, batch, seq, heads, use_alibi, slopes=(), doc_ids=()):
+        if use_alibi and len(slopes) != heads:
+            raise EngineError(f"build_attention_mask: ALiBi needs one slope per head ({heads}), got {len(slopes)}")
         sl = np.asarray(list(slopes) if len(slopes) else [0.0], dtype=np.float32)
         di = np.asarray(list(doc_ids) if len(doc_ids) else [0], dtype=np.uint64)
         out = np.empty((batch * heads * seq, seq), dtype=np.float32)
@@ -474,11 +476,12 @@ class GptSession:
         self._eng._check(self._f["gpt_save"](self._g, path.encode(), tokenizer or None, len(tokenizer)))
 
     def load(self, path: str) -> bytes:
-        """Loads parameters from a format-v4 model file; returns the embedded tokenizer bytes."""
+        """Loads parameters from a format-v4 model file whose spec matches this session's model
+        (the AdamW state starts afresh); returns the embedded tokenizer bytes. One call: the
+        tokenizer buffer is sized by the file, which holds it."""
         n = ctypes.c_size_t()
-        self._eng._check(self._f["gpt_load"](self._g, path.encode(), None, 0, ctypes.byref(n)))
-        buf = ctypes.create_string_buffer(max(1, n.value))
-        self._eng._check(self._f["gpt_load"](self._g, path.encode(), buf, n.value, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(max(1, os.path.getsize(path)))
+        self._eng._check(self._f["gpt_load"](self._g, path.encode(), buf, len(buf), ctypes.byref(n)))
         return buf.raw[:n.value]
 
     def backward_scaled(self, grad_scale: float) -> None:

@@ -103,3 +103,57 @@ def test_load_errors(cpu, tmp_path):
     other = dict(CFG, d_model=32)
     with pytest.raises(nnengine.EngineError):
         cpu.gpt(**other).load(str(path))                      # shape mismatch
+
+
+def _with_spec_field(raw, key, value):
+    """The file bytes with one u64 spec field replaced (same length, so every offset holds)."""
+    kb = key.encode()
+    i = raw.index(struct.pack("<I", len(kb)) + kb + b"\x00" + struct.pack("<I", 8))
+    j = i + 4 + len(kb) + 1 + 4
+    return raw[:j] + struct.pack("<Q", value) + raw[j + 8:]
+
+
+@pytest.mark.parametrize("key,value", [("num_heads", 4), ("seq_len", 16), ("pos_encoding", 1), ("activation", 0),
+                                       ("norm_type", 0), ("type", 1)])
+def test_load_rejects_another_spec(cpu, tmp_path, key, value):
+    """A file whose spec describes another model with the same matrix shapes (other head count, context,
+    position encoding, activation, norm, model type) does not load: the reference builds the model from
+    the file's spec (text_train.cpp:940-952), a session's model is fixed, so the specs must agree. The
+    type check is build_gpt_model_from_spec's (domain_gpt.hpp:90-92): type GPT, or ALiBi positions."""
+    cfg = dict(CFG, pos_enc="learned") if key == "type" else CFG
+    g = _session(cpu, cfg=cfg)
+    path = tmp_path / "m.nnm"
+    g.save(str(path))
+    p = tmp_path / "other.nnm"
+    p.write_bytes(_with_spec_field(path.read_bytes(), key, value))
+    with pytest.raises(nnengine.EngineError, match="type|" + key):
+        _session(cpu, cfg=cfg).load(str(p))
+    # the unchanged file loads, and an ALiBi file may carry the legacy ALiBi_GPT type (4)
+    _session(cpu, cfg=cfg).load(str(path))
+    if cfg["pos_enc"] == "alibi":
+        q = tmp_path / "legacy.nnm"
+        q.write_bytes(_with_spec_field(path.read_bytes(), "type", 4))
+        _session(cpu).load(str(q))
+
+
+def test_load_restarts_the_optimizer(cpu, tmp_path):
+    """After load the AdamW moments and step count start afresh, as an optimizer created after
+    load_model does (text_train.cpp:952 then 966): one step after loading into a session that has
+    trained equals one step of a fresh session that loaded the same file."""
+    rng = np.random.default_rng(5)
+    toks = rng.integers(0, CFG["vocab_size"], size=(CFG["seq_len"] + 1, 2))
+    batch = (toks[:-1].astype(np.float32), toks[1:].T.reshape(-1))
+    path = str(tmp_path / "m.nnm")
+    _session(cpu, 1).save(path)
+    used = _session(cpu, 2)
+    for _ in range(3):
+        used.load_batch(*batch)
+        used.train_step()
+    used.load(path)
+    fresh = _session(cpu, 3)
+    fresh.load(path)
+    for g in (used, fresh):
+        g.load_batch(*batch)
+        g.train_step()
+    for x, y in zip(used.params(), fresh.params()):
+        assert np.array_equal(x, y)

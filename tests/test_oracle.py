@@ -9,6 +9,7 @@ loops for the index primitives, the reference's own known-answer mask rows
 sources need <expected>, which this image's libstdc++ lacks, so it cannot be
 compiled here and every pin below is reference-free.
 """
+import ctypes
 import math
 
 import numpy as np
@@ -646,3 +647,15 @@ def test_inplace_and_copy_primitives_closed_form(cpu):
         cpu.insert_rows(dst, 6, cpu.tensor(B[:3]))
     with pytest.raises(EngineError):
         cpu.add_inplace(cpu.tensor(A), cpu.tensor(B[:3]))
+
+
+def test_build_attention_mask_rejects_missing_slopes(cpu):
+    """ALiBi reads one slope per head: a slope list of another length is an error, not a read past it."""
+    with pytest.raises(EngineError, match="slope"):
+        cpu.build_attention_mask(1, 4, 2, True, slopes=[1.0])
+    with pytest.raises(EngineError, match="slope"):
+        cpu.build_attention_mask(1, 4, 2, True)
+    # the C-ABI itself rejects a null slope pointer with ALiBi set
+    out = np.empty((8, 4), np.float32)
+    assert cpu._f["build_attention_mask"](1, 4, 2, 1, None, None, 0, out.ctypes.data_as(
+        ctypes.POINTER(ctypes.c_float))) != 0
