@@ -51,6 +51,21 @@ int nnhip_gemm_epilogue(const float* A, const float* B, float* C, size_t A_rows,
                         size_t B_cols, int transA, int transB, float alpha, const float* row_bias, int accumulate,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* nnhip_gemm that allocates nothing and takes no workspace. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory or hand in a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation). Split-K partial tiles go to a scratch array inside
+ * the library, one per GPU, NNHIP_GEMM_NOALLOC_SCRATCH_BYTES (64 MiB) in size and held until the process
+ * ends. Same plan, kernels and summation order as nnhip_gemm given nnhip_gemm_workspace_bytes(M, N, K,
+ * batch) bytes of workspace, so the results are identical. Returns -6, launching nothing, when that
+ * workspace size exceeds NNHIP_GEMM_NOALLOC_SCRATCH_BYTES: products whose output grid fills the GPU need
+ * none; among the config-4 step's, the long-K ones into small outputs (768 x 8192 from K = 6144 or
+ * 32000, the 6144 x 768 weight gradient) need 96-108 MiB and are rejected. All calls on one GPU share its
+ * scratch: calls that may overlap in time on one GPU (other streams, other threads) race and must be
+ * ordered by the caller. */
+#define NNHIP_GEMM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int nnhip_gemm_noalloc(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
+                       size_t B_cols, size_t batch, int transA, int transB, float alpha, void* stream);
+
 /* Per batch b: C_b = alpha * op(A_b) op(B_b); A/B split into `batch` row blocks, C stacked (batch*M, N).
  * Replaces cuda_batched_matmul (cuda_kernels.h:49-54); alpha as in ComputeEngine::batched_matmul
  * (compute_engine.hpp:195-199, cpu_engine.hpp:335-419). */

@@ -19,6 +19,8 @@
 // MFMA 32x32x2 f32 operand layout (per lane l, k-step of 2):
 //   A: A[i = l%32][k = l/32],  B: B[k = l/32][j = l%32],
 //   D: 16 values, value r at row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#include <mutex>
+
 #include "common.hpp"
 #include "nnhip_kernels.h"
 
@@ -542,6 +544,66 @@ extern "C" int nnhip_gemm_epilogue(const float* A, const float* B, float* C, siz
     if (K != K2) return -2;
     return gemm_dispatch(A, B, C, M, N, K, A_cols, B_cols, A_rows * A_cols, B_rows * B_cols, M * N, transA != 0,
                          transB != 0, alpha, 1, workspace, workspace_bytes, stream, Epi{row_bias, accumulate ? 1 : 0});
+}
+
+// ── GEMM without allocation ─────────────────────────────────────────────────
+// Split-K partial tiles of nnhip_gemm_noalloc live in this array. One copy
+// per GPU, held from when the library's code object loads on that GPU until
+// the process ends. Host code never passes `scratch` itself (its host-side
+// name is not a device address): scratch_ptr() resolves the current GPU's
+// copy once with hipGetSymbolAddress and every launch uses that address.
+static __device__ __align__(256) float scratch[NNHIP_GEMM_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace nnhip
+{
+namespace
+{
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+
+// The current GPU's address of `scratch` (resolved on the first call made with
+// that GPU current). Returns 0, a hipError_t, or -1 for a device id past the table.
+int scratch_ptr(float** out)
+{
+    int dev = 0;
+    if (const hipError_t e = hipGetDevice(&dev); e != hipSuccess) return static_cast<int>(e);
+    if (dev < 0 || dev >= kMaxDevices) return -1;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev])
+    {
+        void* p = nullptr;
+        if (const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess)
+            return static_cast<int>(e);
+        if (!p) return -1;
+        g_scratch[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch[dev];
+    return 0;
+}
+} // namespace
+} // namespace nnhip
+
+// nnhip_gemm with the split-K partials in the library's own scratch: the same
+// plan, kernels and summation order as nnhip_gemm given a workspace of
+// nnhip_gemm_workspace_bytes(M, N, K, batch), so the results are identical.
+// Every partial element is written by its slice before the reduction reads
+// it, so nothing in the scratch has to start at zero.
+extern "C" int nnhip_gemm_noalloc(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols,
+                                  size_t B_rows, size_t B_cols, size_t batch, int transA, int transB, float alpha,
+                                  void* stream)
+{
+    if (batch == 0 || A_rows % batch || B_rows % batch) return -2;
+    const size_t ar = A_rows / batch, br = B_rows / batch;
+    const size_t M = transA ? A_cols : ar, K = transA ? ar : A_cols;
+    const size_t K2 = transB ? B_cols : br, N = transB ? br : B_cols;
+    if (K != K2) return -2;
+    if (M == 0 || N == 0) return 0;
+    if (nnhip_gemm_workspace_bytes(M, N, K, batch) > NNHIP_GEMM_NOALLOC_SCRATCH_BYTES) return -6;
+    float* ws = nullptr;
+    if (const int rc = scratch_ptr(&ws)) return rc;
+    return gemm_dispatch(A, B, C, M, N, K, A_cols, B_cols, ar * A_cols, br * B_cols, M * N, transA != 0, transB != 0,
+                         alpha, batch, ws, NNHIP_GEMM_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int nnhip_matmul(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
