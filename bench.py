@@ -15,8 +15,9 @@ forward + backward over the 8 packed rows), as algorithmic TFLOP/s (4*d*P
 forward, 8*d*P backward over the P allowed (query, key) pairs) and as a
 fraction of the fp32 MFMA peak, timed with HIP events on the engine's stream.
 `cpu_baseline` runs the CPU restatement of the reference CpuEngine (oracle/,
-loaded only for this leg) on a bounded sample of the same workload: one full
-training step at batch 1 of 8.
+loaded only for this leg) on a bounded sample of the same workload: the
+config-4 model at batch 1 of 8, one warmup and three timed training steps.
+`--cpu-legs` runs the oracle's legs of configs 2, 3 and 5 instead.
 """
 import argparse
 import ctypes
@@ -385,22 +386,128 @@ def pmc_sample(seed):
     print(json.dumps({"pmc_sample": "1 config-4 train step + 256 MiB Neg copy", "loss": loss}), flush=True)
 
 
-def cpu_leg(seed):
+def host_info(threads):
+    """The host the CPU baseline runs on: CPU model and sockets (lscpu), logical CPUs (nproc), the CPUs
+    this process may use, and the threads the oracle's pool runs."""
+    import subprocess
+    info = {"threads": threads, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() == "Model name":
+                info["cpu_model"] = v.strip()
+            elif k.strip() == "Socket(s)":
+                info["sockets"] = int(v.strip())
+    except (OSError, subprocess.SubprocessError, ValueError):
+        pass
+    return info
+
+
+def _oracle(threads):
+    """The CPU restatement of the reference CpuEngine (oracle/), its pool sized to `threads`."""
     import nnengine
-    threads = int(os.environ.get("NNORACLE_THREADS", "0")) or min(os.cpu_count() or 1, 16)
     os.environ["NNORACLE_THREADS"] = str(threads)
     lib = ctypes.CDLL(os.path.join(ROOT, "oracle", "_build", "libnnoracle.so"))
-    eng = nnengine.Engine(lib, prefix="nnoracle_")
     lib.nnoracle_thread_count.restype = ctypes.c_size_t
+    return nnengine.Engine(lib, prefix="nnoracle_"), lib
+
+
+def _cpu_threads():
+    """hardware_concurrency is the reference's pool size (core_threadpool.hpp:612); a GPU box lends one
+    GPU's job 16 of its host's CPUs, so the pool is capped at 16 (NNORACLE_THREADS overrides)."""
+    return int(os.environ.get("NNORACLE_THREADS", "0")) or min(len(os.sched_getaffinity(0)), 16)
+
+
+def cpu_leg(seed, steps=3, warmup=1):
+    """Config-4 training steps (forward, CE, backward, AdamW) of the oracle at batch 1 of 8, following
+    compute_bench's method (src/compute_bench.cpp:36-61): warmup, then timed steps, min and mean."""
+    eng, lib = _oracle(_cpu_threads())
     g = init_session(eng, CFG, 1, seed)
-    t0 = time.perf_counter()
-    loss = g.train_step()
-    dt = time.perf_counter() - t0
-    print(f"[bench] cpu baseline step {dt:.1f}s loss {loss:.4f}", file=sys.stderr, flush=True)
+    times = []
+    for i in range(warmup + steps):
+        t0 = time.perf_counter()
+        loss = g.train_step()
+        dt = time.perf_counter() - t0
+        print(f"[bench] cpu baseline {'warmup' if i < warmup else 'timed'} step {dt:.1f}s loss {loss:.4f}",
+              file=sys.stderr, flush=True)
+        if i >= warmup:
+            times.append(dt)
     T = CFG["seq_len"]
-    return dict(value=T / dt, unit="tokens/s", cores=int(lib.nnoracle_thread_count()), kind="port",
-                sample=f"1 AdamW train step of the config-4 model on batch 1 of {BATCH} ({T} tokens), "
-                       f"{dt:.1f} s", seconds=dt)
+    mean, best = sum(times) / len(times), min(times)
+    threads = int(lib.nnoracle_thread_count())
+    return dict(value=T / mean, unit="tokens/s", cores=threads, kind="port",
+                sample=f"config-4 model (12L d768 V32000 T1024 ALiBi) at batch 1 of {BATCH} ({T} tokens): "
+                       f"{warmup} warmup + {steps} timed AdamW train steps, mean {mean:.2f} s, min {best:.2f} s; "
+                       f"the oracle (CPU restatement of CpuEngine) on {threads} threads",
+                tflops=step_flops(CFG, 1) / mean / 1e12, min_s=best, mean_s=mean, host=host_info(threads))
+
+
+def cpu_legs_other(seed, iters=5):
+    """CPU legs of configs 2, 3 and 5 on the oracle, compute_bench's method: one warmup, then `iters`
+    timed calls (config 5: one packed row, timed once), min and mean. The fused attention primitives
+    are serial loops in the reference and in the oracle."""
+    eng, lib = _oracle(_cpu_threads())
+    rng = np.random.default_rng(seed)
+    out = {"host": host_info(int(lib.nnoracle_thread_count()))}
+
+    def bench(fn, n):
+        fn()
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return min(ts), sum(ts) / len(ts)
+
+    BH, T, d = 128, 512, 64
+    q, k = (eng.tensor(rng.standard_normal((BH * d, T), dtype=np.float32)) for _ in range(2))
+    vt = eng.tensor(rng.standard_normal((BH * T, d), dtype=np.float32))
+    mask = eng.tensor(eng.build_attention_mask(1, T, 1, False))
+
+    def c2():
+        m = eng.batched_matmul_reduce(q, k, BH, "Max", True, False, 0.125, True, mask)
+        lsum = eng.batched_matmul_softmax_denom(q, k, m, BH, True, False, 0.125, mask)
+        return eng.batched_matmul_softmax_apply(q, k, vt, m, lsum, BH, True, False, 0.125, mask)
+    best, mean = bench(c2, 1)
+    flop = 4 * d * (T * (T + 1) // 2) * BH
+    out["config2_causal_forward"] = {"min_s": best, "mean_s": mean, "tflops": flop / mean / 1e12,
+                                     "iterations": 1, "warmup": 1}
+    del q, k, vt, mask
+    sweep = []
+    for name, M, K, N, tA, tB in GEMM_SWEEP[:6]:
+        a = eng.tensor(rng.uniform(-1, 1, (M, K)).astype(np.float32))
+        b = eng.tensor(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+        best, mean = bench(lambda: eng.matmul(a, b), iters)
+        fl = 2.0 * M * N * K
+        sweep.append({"shape": name, "min_s": best, "mean_s": mean, "gflops": fl / mean / 1e9, "iterations": iters})
+        print(f"[bench] cpu {name}: {fl / mean / 1e9:.1f} GFLOP/s", file=sys.stderr, flush=True)
+    out["config3_gemm"] = sweep
+    H, T = 12, 2048
+    lens, tot = [], 0
+    while tot < T:
+        L = min(int(rng.integers(64, 1025)), T - tot)
+        lens.append(L)
+        tot += L
+    ids = np.concatenate([np.full(L, i + 1, dtype=np.uint64) for i, L in enumerate(lens)])
+    pairs = sum(L * (L + 1) // 2 for L in lens)
+    mk = eng.tensor(eng.build_attention_mask(1, T, 1, False, doc_ids=ids))
+    q, k, v, g = (eng.tensor(rng.standard_normal((H * d, T), dtype=np.float32)) for _ in range(4))
+
+    def c5():
+        m = eng.batched_matmul_reduce(q, k, H, "Max", True, False, 0.125, True, mk)
+        lsum = eng.batched_matmul_softmax_denom(q, k, m, H, True, False, 0.125, mk)
+        P = eng.batched_matmul(g, v, H, True, False)
+        G = eng.rearrange_3d(eng.transpose(g), T, H, d)
+        dq, r = eng.batched_matmul_softmax_backward_q(q, k, P, m, lsum, H, True, False, 0.125, mk)
+        return eng.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, lsum, H, True, False, 0.125, mk)
+    t0 = time.perf_counter()
+    c5()
+    dt = time.perf_counter() - t0
+    flop = 12 * d * pairs * H
+    out["config5_one_row_forward_backward"] = {"s": dt, "tflops": flop / dt / 1e12, "iterations": 1, "warmup": 0,
+                                               "allowed_pair_fraction": pairs / (T * T)}
+    return out
 
 
 def gemm_traffic_bytes():
@@ -429,6 +536,8 @@ def main():
     ap.add_argument("--skip-hbm", action="store_true")
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run only the workload the rocprofv3 --pmc passes count (one step + a calibration copy)")
+    ap.add_argument("--cpu-legs", action="store_true",
+                    help="run only the oracle's CPU legs of configs 2, 3 and 5 and print their JSON")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the attention leg (configs 2 and 5) and print its JSON (for kernel traces)")
     args = ap.parse_args()
@@ -442,6 +551,9 @@ def main():
         return
     if args.attention_only:
         print(json.dumps({"attention": attention_leg(args.seed)}), flush=True)
+        return
+    if args.cpu_legs:
+        print(json.dumps({"cpu_legs": cpu_legs_other(args.seed)}), flush=True)
         return
     gpu = gpu_leg(args.steps, args.warmup, args.seed)
     attn = None if args.skip_attention else attention_leg(args.seed)
@@ -487,7 +599,8 @@ def main():
         out["hbm_kernels"] = hbm
     if not args.skip_cpu_baseline:
         cpu = cpu_leg(args.seed)
-        out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
+        out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "tflops", "min_s",
+                                                   "mean_s", "host")}
     print(json.dumps(out), flush=True)
 
 

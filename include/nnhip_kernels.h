@@ -90,6 +90,13 @@ int nnhip_elementwise_select_scalar_cond(const float* A, const float* then_v, fl
 int nnhip_adam_update(float* p, float* m, float* v, const float* g, size_t count, int has_decay, float decay,
                       float beta1, float one_minus_beta1, float beta2, float one_minus_beta2, float inv_bc1,
                       float inv_bc2, float eps, float neg_lr, void* stream);
+/* The update above for n tensors with one set of scalars (one optimizer step over every parameter,
+ * compute_optimizer.hpp:252-304, :388-412), in as few launches as possible (48 tensors per launch):
+ * tensor i is p[i], m[i], v[i], g[i] of counts[i] floats. Bit-identical to n nnhip_adam_update calls. */
+int nnhip_adam_update_list(float* const* p, float* const* m, float* const* v, const float* const* g,
+                           const size_t* counts, size_t n, int has_decay, float decay, float beta1,
+                           float one_minus_beta1, float beta2, float one_minus_beta2, float inv_bc1, float inv_bc2,
+                           float eps, float neg_lr, void* stream);
 /* SwiGLU forward (reference compute_layer.hpp, SwiGLU::forward, a chain of six primitives:
  * Neg, Exp, + c_add, c_div / x, gate * s, * up) in one pass with the same roundings:
  * s = c_div / (exp(-gate) + c_add) (stored when s_out is not null), out = (gate * s) * up.

@@ -950,7 +950,7 @@ Result<void> HipEngine::ew_push_(unsigned code, unsigned op, bool first, const T
 {
     NN_CHECK(settle_zero_());
     const std::size_t n = dst.size();
-    if (pew_ && (pew_->n != n || pew_->full())) NN_CHECK(settle_ew_());
+    if (pew_ && (pew_->n != n || pew_->full())) NN_CHECK(settle_ew_(true));
     if (!pew_)
     {
         pew_ = std::make_unique<PendingEw>();
@@ -971,9 +971,9 @@ Result<void> HipEngine::ew_push_(unsigned code, unsigned op, bool first, const T
 // Launches the recorded calls in order: every Adam / AdamW update chain as one
 // nnhip_adam_update pass, any other call with its own kernel. A call is
 // skipped when its result is referenced by nobody and read by no later call.
-Result<void> HipEngine::settle_ew_()
+Result<void> HipEngine::settle_ew_(bool keep_adam)
 {
-    if (!pew_) return {};
+    if (!pew_) return keep_adam ? Result<void>{} : flush_adam_();
     std::unique_ptr<PendingEw> g = std::move(pew_);
     const auto& ops = g->ops;
     std::vector<std::ptrdiff_t> last_read(g->slots.size(), -1);
@@ -987,14 +987,16 @@ Result<void> HipEngine::settle_ew_()
     for (std::size_t i = 0; i < ops.size();)
     {
         NN_TRY(k, adam_run_(*g, i, last_read));
-        if (!k)
-        {
-            NN_TRY(k2, swiglu_run_(*g, i, last_read));
-            k = k2;
-        }
         if (k)
         {
             i += k;
+            continue;
+        }
+        NN_CHECK(flush_adam_());   // collected updates precede every other launch
+        NN_TRY(k2, swiglu_run_(*g, i, last_read));
+        if (k2)
+        {
+            i += k2;
             continue;
         }
         const auto& o = ops[i];
@@ -1020,7 +1022,31 @@ Result<void> HipEngine::settle_ew_()
         }
         ++i;
     }
-    return {};
+    return keep_adam ? Result<void>{} : flush_adam_();
+}
+
+// Launches the collected Adam / AdamW updates: one nnhip_adam_update_list call.
+Result<void> HipEngine::flush_adam_()
+{
+    if (padam_.empty()) return {};
+    std::vector<PendingAdam> items = std::move(padam_);
+    padam_.clear();
+    std::vector<float*> p, m, v;
+    std::vector<const float*> g;
+    std::vector<std::size_t> n;
+    for (const auto& a : items)
+    {
+        p.push_back(W(a.p));
+        m.push_back(W(a.m));
+        v.push_back(W(a.v));
+        g.push_back(D(a.g));
+        n.push_back(a.p.size());
+    }
+    const float* c = padam_args_;
+    return kernel_(nnhip_adam_update_list(p.data(), m.data(), v.data(), g.data(), n.data(), items.size(),
+                                          c[0] != 0.0f, c[1], c[2], c[3], c[4], c[5], c[6], c[7], c[8], c[9],
+                                          static_cast<hipStream_t>(stream_)),
+                   "adam update");
 }
 
 // True when calls i, i+1, ... of the record are `steps` with one distinct
@@ -1067,12 +1093,26 @@ Result<std::size_t> HipEngine::adam_run_(const PendingEw& g, std::size_t i,
             ok = !live(g.slots[slot_of[r]]) && last_read[slot_of[r]] < static_cast<std::ptrdiff_t>(i + len);
         if (!ok) continue;
         const PendingEw::Op* c = &ops[i + static_cast<std::size_t>(decay)];   // the first call after the decay
-        const float decay_f = decay ? ops[i].s : 1.0f;
-        NN_CHECK(kernel_(nnhip_adam_update(W(g.slots[slot_of[rP]]), W(g.slots[slot_of[rM]]),
-                                           W(g.slots[slot_of[rV]]), D(g.slots[slot_of[rG]]), g.n, decay, decay_f,
-                                           c[0].s, c[1].s, c[2].s, c[4].s, c[7].s, c[9].s, c[11].s, c[13].s,
-                                           static_cast<hipStream_t>(stream_)),
-                         "adam update"));
+        const float args[10] = {decay ? 1.0f : 0.0f, decay ? ops[i].s : 1.0f, c[0].s, c[1].s, c[2].s, c[4].s,
+                                c[7].s, c[9].s, c[11].s, c[13].s};
+        const Tensor* mine[4] = {&g.slots[slot_of[rP]], &g.slots[slot_of[rM]], &g.slots[slot_of[rV]],
+                                 &g.slots[slot_of[rG]]};
+        auto overlap = [](const Tensor& a, const Tensor& b) {
+            const float *pa = a.dev_ptr(), *pb = b.dev_ptr();
+            return pa && pb && pa < pb + b.size() && pb < pa + a.size();
+        };
+        bool conflict = !padam_.empty() && std::memcmp(args, padam_args_, sizeof(args)) != 0;
+        for (const auto& q : padam_)   // a collected update writing what this one touches, or reading what it writes
+            for (const Tensor* t : mine)
+                if (overlap(*t, q.p) || overlap(*t, q.m) || overlap(*t, q.v) ||
+                    (t != mine[3] && overlap(*t, q.g)))
+                    conflict = true;
+        if (conflict) NN_CHECK(flush_adam_());
+        std::memcpy(padam_args_, args, sizeof(args));
+        // The update is launched later, with others: p, m, v and g are held
+        // (they are distinct buffers, as match_run_ bound one slot per role).
+        padam_.push_back(PendingAdam{g.slots[slot_of[rP]], g.slots[slot_of[rM]], g.slots[slot_of[rV]],
+                                     g.slots[slot_of[rG]]});
         return len;
     }
     return std::size_t{0};

@@ -283,6 +283,68 @@ __global__ __launch_bounds__(kThreads) void k_copy1(const float* __restrict__ sr
     for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
 
+// Adam / AdamW over up to kAdamMax tensors in one launch (the optimizer's
+// per-parameter chains with one set of scalars: Optimizer::step issues them
+// back to back). Blocks of 256 threads x 4 float4 per tensor, block ranges
+// from the prefix sums in `first`; the same per-element steps as k_adam.
+constexpr int kAdamMax = 48;
+constexpr unsigned kAdamBlockFloats = kThreads * 16;
+struct AdamList
+{
+    float* p[kAdamMax];
+    float* m[kAdamMax];
+    float* v[kAdamMax];
+    const float* g[kAdamMax];
+    unsigned long long n[kAdamMax];
+    unsigned first[kAdamMax + 1];
+    int count;
+    AdamArgs a;
+};
+__global__ __launch_bounds__(kThreads) void k_adam_list(AdamList L)
+{
+    const unsigned b = blockIdx.x;
+    int lo = 0, hi = L.count - 1;   // last tensor whose first block is <= b
+    while (lo < hi)
+    {
+        const int mid = (lo + hi + 1) / 2;
+        if (L.first[mid] <= b) lo = mid;
+        else hi = mid - 1;
+    }
+    const int t = lo;
+    const size_t base = static_cast<size_t>(b - L.first[t]) * kAdamBlockFloats, n = L.n[t];
+    float *p = L.p[t], *m = L.m[t], *v = L.v[t];
+    const float* g = L.g[t];
+    const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(m) |
+                       reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(g)) & 15u) == 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+    {
+        const size_t i = base + (static_cast<size_t>(k) * kThreads + threadIdx.x) * 4;
+        if (vec && i + 4 <= n)
+        {
+            float4 pp = *reinterpret_cast<float4*>(p + i), mm = *reinterpret_cast<float4*>(m + i),
+                   vv = *reinterpret_cast<float4*>(v + i);
+            const float4 gg = *reinterpret_cast<const float4*>(g + i);
+            adam_elem(pp.x, mm.x, vv.x, gg.x, L.a);
+            adam_elem(pp.y, mm.y, vv.y, gg.y, L.a);
+            adam_elem(pp.z, mm.z, vv.z, gg.z, L.a);
+            adam_elem(pp.w, mm.w, vv.w, gg.w, L.a);
+            *reinterpret_cast<float4*>(p + i) = pp;
+            *reinterpret_cast<float4*>(m + i) = mm;
+            *reinterpret_cast<float4*>(v + i) = vv;
+        }
+        else
+            for (size_t e = i; e < i + 4 && e < n; ++e)
+            {
+                float pp = p[e], mm = m[e], vv = v[e];
+                adam_elem(pp, mm, vv, g[e], L.a);
+                p[e] = pp;
+                m[e] = mm;
+                v[e] = vv;
+            }
+    }
+}
+
 // Zero fill of up to kFillMax tensors in one launch: block ranges per tensor
 // from the prefix sums in `first` (blocks of 256 threads x 4 floats x 4).
 constexpr int kFillMax = 96;
@@ -392,6 +454,43 @@ extern "C" int nnhip_adam_update(float* p, float* m, float* v, const float* g, s
     else
         hipLaunchKernelGGL(k_adam<false>, dim3(grid), dim3(kThreads), 0, s, p, m, v, g, count, a);
     return launch_status();
+}
+
+extern "C" int nnhip_adam_update_list(float* const* p, float* const* m, float* const* v, const float* const* g,
+                                      const size_t* counts, size_t n, int has_decay, float decay, float beta1,
+                                      float one_minus_beta1, float beta2, float one_minus_beta2, float inv_bc1,
+                                      float inv_bc2, float eps, float neg_lr, void* stream)
+{
+    if (n && (!p || !m || !v || !g || !counts)) return -1;
+    const AdamArgs a{decay, beta1, one_minus_beta1, beta2, one_minus_beta2, inv_bc1, inv_bc2, eps, neg_lr,
+                     has_decay ? 1 : 0};
+    auto s = static_cast<hipStream_t>(stream);
+    for (size_t i0 = 0; i0 < n; i0 += kAdamMax)
+    {
+        AdamList L{};
+        L.a = a;
+        unsigned blocks = 0;
+        for (size_t i = i0; i < n && i < i0 + kAdamMax; ++i)
+        {
+            if (counts[i] == 0) continue;
+            if (!p[i] || !m[i] || !v[i] || !g[i]) return -1;
+            const size_t nb = (counts[i] + kAdamBlockFloats - 1) / kAdamBlockFloats;
+            if (blocks + nb > 0x7fffffffu) return -3;
+            L.p[L.count] = p[i];
+            L.m[L.count] = m[i];
+            L.v[L.count] = v[i];
+            L.g[L.count] = g[i];
+            L.n[L.count] = counts[i];
+            L.first[L.count] = blocks;
+            blocks += static_cast<unsigned>(nb);
+            ++L.count;
+        }
+        if (L.count == 0) continue;
+        L.first[L.count] = blocks;
+        hipLaunchKernelGGL(k_adam_list, dim3(blocks), dim3(kThreads), 0, s, L);
+        if (int rc = launch_status()) return rc;
+    }
+    return 0;
 }
 
 extern "C" int nnhip_elementwise_unary(const float* A, float* out, size_t count, unsigned op, void* stream)

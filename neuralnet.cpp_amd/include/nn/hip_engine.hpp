@@ -229,7 +229,19 @@ private:
     Result<void> settle_chain_write_(const Tensor& t, bool keep_swb = false);   // keep_swb: placed SwiGLU records stay
     Result<void> ew_push_(unsigned code, unsigned op, bool first, const Tensor& dst, const Tensor& a, const Tensor* b,
                           float s);
-    Result<void> settle_ew_();
+    // keep_adam: recognised Adam chains stay collected in padam_ (the record
+    // is being replaced by one of another size; the next call is recorded too).
+    Result<void> settle_ew_(bool keep_adam = false);
+    // Adam / AdamW update chains recognised in elementwise records and not yet
+    // launched: launched together (nnhip_adam_update_list) before any other
+    // kernel, so their order relative to every other call is kept.
+    struct PendingAdam
+    {
+        Tensor p, m, v, g;
+    };
+    std::vector<PendingAdam> padam_;
+    float padam_args_[11] = {};   // has_decay, decay, beta1, 1-beta1, beta2, 1-beta2, ib1, ib2, eps, -lr, (unused)
+    Result<void> flush_adam_();
     Result<std::size_t> adam_run_(const PendingEw& g, std::size_t i, const std::vector<std::ptrdiff_t>& last_read);
     Result<std::size_t> swiglu_run_(const PendingEw& g, std::size_t i, const std::vector<std::ptrdiff_t>& last_read);
     static bool match_run_(const PendingEw& g, std::size_t i, const RunStep* steps, std::size_t len, int nroles,

@@ -2,8 +2,10 @@
 
 The engine records consecutive same-size elementwise / in-place calls and runs
 them when another kind of call arrives; the optimizers' Adam / AdamW chain
-(reference compute_optimizer.hpp:252-304, :388-412) and SwiGLU::forward's
-sigmoid-gate chain run as one fused pass each. Consecutive zero calls
+(reference compute_optimizer.hpp:252-304, :388-412) runs as one fused pass per
+tensor, the chains of consecutive tensors collected into multi-tensor launches
+(a tensor updated again, as in the next step, first launches what is
+collected), and SwiGLU::forward's sigmoid-gate chain as one fused pass. Consecutive zero calls
 (zero_grad) are cleared together.
 Bars: the fused chain is bit-exact against the same calls run one by one (an
 engine settle after every call stops any recording from spanning two calls);
@@ -67,7 +69,9 @@ def run_adam(e, state, steps, decay, settle_each, keep=None):
 
 SHAPES = [[(1, 1)], [(1, 7)], [(768, 1)], [(10, 100)], [(768, 768)], [(1, 6144)], [(33, 31)],
           # two chains of one size in one recording, then sizes that change
-          [(64, 64), (64, 64), (1, 768), (768, 768), (1, 768)]]
+          [(64, 64), (64, 64), (1, 768), (768, 768), (1, 768)],
+          # more tensors than one multi-tensor launch takes (48), ragged sizes
+          [(i % 7 + 1, 3 * i + 1) for i in range(60)]]
 
 
 @pytest.mark.parametrize("decay", [True, False])
