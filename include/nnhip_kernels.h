@@ -243,6 +243,22 @@ int nnhip_col_softmax_sparse_forward(const float* logits, const float* labels, c
                                      float* loss_vec, size_t C, size_t N, size_t vocab_size, float inv_num_valid,
                                      void* workspace, void* stream);
 
+/* The sparse cross-entropy of logits produced by nnhip_gemm_colstats (the GPT's lm_head Linear:
+ * logits = W x + b, compute_layer.hpp Linear::forward, then CrossEntropyLoss::forward_sparse,
+ * compute_loss.hpp:229-309): the product's epilogue leaves, per column and per block of
+ * nnhip_gemm_colstats_tiles(M, N, K, transA, transB) rows, the max and the sum of exp(x - max) in
+ * stats[(tile) * N + col] and stats[(tiles + tile) * N + col] (2 * tiles * N floats; 0 tiles: the
+ * shape has no such epilogue). nnhip_col_softmax_sparse_from_stats merges them in row order and writes
+ * the gradient and loss as nnhip_col_softmax_sparse_forward does, reading the logits once instead of
+ * twice; workspace 2 * N floats. No CUDA counterpart. */
+size_t nnhip_gemm_colstats_tiles(size_t M, size_t N, size_t K, int transA, int transB);
+int nnhip_gemm_colstats(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
+                        size_t B_cols, int transA, int transB, const float* row_bias, float* stats, void* stream);
+int nnhip_col_softmax_sparse_from_stats(const float* logits, const float* labels, const float* mask,
+                                        const float* stats, size_t tiles, float* grad, float* loss_vec, size_t C,
+                                        size_t N, size_t vocab_size, float inv_num_valid, void* workspace,
+                                        void* stream);
+
 /* ── row softmax (eval_expr fast path of the Softmax layer, compute_layer.hpp:832-862) ──
  * forward: out = exp(x - rowmax) / sum(exp(x - rowmax)); backward: dx = y * (g - sum(y*g)). */
 int nnhip_row_softmax(const float* X, float* out, size_t rows, size_t cols, void* stream);

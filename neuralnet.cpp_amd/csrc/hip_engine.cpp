@@ -348,7 +348,8 @@ struct HipEngine::PendingMm
     bool tA, tB;
     std::size_t M, N, K;
     bool folded;
-    bool uses(const float* p) const { return has_buf(A, p) || has_buf(B, p) || has_buf(C, p); }
+    Tensor bias;   // the Linear bias added by the call that followed (broadcast_row_inplace), if any
+    bool uses(const float* p) const { return has_buf(A, p) || has_buf(B, p) || has_buf(C, p) || has_buf(bias, p); }
 };
 
 // Consecutive same-size elementwise calls (scale / axpy / add in place; unary,
@@ -1458,7 +1459,7 @@ Result<void> HipEngine::settle_mm_()
     if (!pmm_) return {};
     std::unique_ptr<PendingMm> r = std::move(pmm_);
     if (!live(r->C)) return {};
-    return launch_mm_(*r, r->C, nullptr, false);
+    return launch_mm_(*r, r->C, r->bias.size() ? &r->bias : nullptr, false);
 }
 
 Result<void> HipEngine::launch_gemm_(const Tensor& A, const Tensor& B, Tensor& C, std::size_t batch, bool tA, bool tB,
@@ -1690,6 +1691,41 @@ Result<Tensor> HipEngine::col_softmax_denom(const Tensor& logits, const Tensor& 
 Result<Tensor> HipEngine::col_softmax_sparse_forward(const Tensor& logits, const Tensor& labels, const Tensor* mask,
                                                      std::size_t vocab, Scalar inv, Tensor& loss_vec_out)
 {
+    NN_CHECK(check_gpu_({&logits, &labels, mask}, "col_softmax_sparse_forward"));
+    // Logits still recorded as a product (the lm_head Linear): the product's
+    // epilogue leaves per-tile column statistics, so the logits are read once.
+    if (pmm_ && !pmm_->folded && same_t(logits, pmm_->C) && !pmm_->uses(labels.dev_ptr()) &&
+        !(mask && pmm_->uses(mask->dev_ptr())) && vocab <= (std::size_t{1} << 24) && vocab <= logits.rows() &&
+        labels.rows() == 1 && labels.cols() == logits.cols() && (!mask || (mask->rows() == 1 && mask->cols() == logits.cols())))
+    {
+        const std::size_t tiles = nnhip_gemm_colstats_tiles(pmm_->M, pmm_->N, pmm_->K, pmm_->tA, pmm_->tB);
+        if (tiles)
+        {
+            NN_CHECK(settle_reads_({&labels, mask}));
+            if (pmm_ && same_t(logits, pmm_->C))
+            {
+                std::unique_ptr<PendingMm> r = std::move(pmm_);
+                const std::size_t C = logits.rows(), N = logits.cols();
+                NN_TRY(stats, scratch_(2 * tiles * N * sizeof(float)));
+                NN_TRY(ws, scratch_(2 * N * sizeof(float)));
+                prof_begin_();
+                const int rc = nnhip_gemm_colstats(D(r->A), D(r->B), W(r->C), r->A.rows(), r->A.cols(), r->B.rows(),
+                                                   r->B.cols(), r->tA, r->tB, r->bias.size() ? D(r->bias) : nullptr,
+                                                   static_cast<float*>(stats->data()), stream_);
+                prof_end_(r->M, r->N, r->K, 1, r->tA, r->tB);
+                NN_CHECK(kernel_(rc, "matmul"));
+                NN_TRY(grad, alloc_(C, N));
+                NN_TRY(lv, alloc_(1, N));
+                NN_CHECK(kernel_(nnhip_col_softmax_sparse_from_stats(D(logits), D(labels), mask ? D(*mask) : nullptr,
+                                                                      static_cast<const float*>(stats->data()), tiles,
+                                                                      W(grad), W(lv), C, N, vocab, inv, ws->data(),
+                                                                      stream_),
+                                 "col_softmax_sparse_forward"));
+                loss_vec_out = lv;
+                return grad;
+            }
+        }
+    }
     NN_CHECK(need_gpu_({&logits, &labels, mask}, "col_softmax_sparse_forward"));
     if (vocab > (std::size_t{1} << 24))
         return fail("col_softmax_sparse_forward: vocab_size exceeds 2^24 (float labels not exactly representable)");
@@ -1715,7 +1751,7 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
     NN_CHECK(check_gpu_({&A, &B}, "add_inplace"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("add_inplace: shape mismatch");
     if (!A.size()) return {};
-    if (pmm_ && !pmm_->folded && same_t(B, pmm_->C) && !pmm_->uses(A.dev_ptr()))
+    if (pmm_ && !pmm_->folded && !pmm_->bias.size() && same_t(B, pmm_->C) && !pmm_->uses(A.dev_ptr()))
     {
         // Linear backward: the weight-gradient accumulation becomes the
         // product's epilogue (A += product); B stays recorded.
@@ -1837,15 +1873,17 @@ Result<Tensor> HipEngine::col_reduce_max(const Tensor& A)
 Result<void> HipEngine::broadcast_row_inplace(Tensor& A, const Tensor& v, BinaryOp op)
 {
     NN_CHECK(check_gpu_({&A, &v}, "broadcast_row_inplace"));
-    if (op == BinaryOp::Add && pmm_ && !pmm_->folded && same_t(A, pmm_->C) && v.rows() == A.rows() &&
-        v.cols() == 1 && !pmm_->uses(v.dev_ptr()))
+    if (op == BinaryOp::Add && pmm_ && !pmm_->folded && !pmm_->bias.size() && same_t(A, pmm_->C) &&
+        v.rows() == A.rows() && v.cols() == 1 && v.size() && !pmm_->uses(v.dev_ptr()))
     {
-        // Linear forward: the bias add becomes the product's epilogue.
+        // Linear forward: the bias add becomes the product's epilogue. The
+        // product stays recorded: when the sparse cross-entropy reads it next
+        // (the lm_head logits), its epilogue also yields the column statistics.
         NN_CHECK(settle_reads_({&v}));
         if (pmm_ && same_t(A, pmm_->C))
         {
-            std::unique_ptr<PendingMm> r = std::move(pmm_);
-            return launch_mm_(*r, r->C, &v, false);
+            pmm_->bias = v;
+            return {};
         }
     }
     NN_CHECK(need_gpu_({&A, &v}, "broadcast_row_inplace"));

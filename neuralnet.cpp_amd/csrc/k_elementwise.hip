@@ -312,10 +312,39 @@ __global__ __launch_bounds__(kThreads) void k_adam_list(AdamList L)
     }
     const int t = lo;
     const size_t base = static_cast<size_t>(b - L.first[t]) * kAdamBlockFloats, n = L.n[t];
-    float *p = L.p[t], *m = L.m[t], *v = L.v[t];
-    const float* g = L.g[t];
+    float* __restrict__ p = L.p[t];
+    float* __restrict__ m = L.m[t];
+    float* __restrict__ v = L.v[t];
+    const float* __restrict__ g = L.g[t];
     const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(m) |
                        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(g)) & 15u) == 0;
+    if (vec && base + kAdamBlockFloats <= n)
+    {
+        // A whole block of float4s: every load issued before any update.
+        float4 pp[4], mm[4], vv[4], gg[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const size_t i = base + (static_cast<size_t>(k) * kThreads + threadIdx.x) * 4;
+            pp[k] = *reinterpret_cast<const float4*>(p + i);
+            mm[k] = *reinterpret_cast<const float4*>(m + i);
+            vv[k] = *reinterpret_cast<const float4*>(v + i);
+            gg[k] = *reinterpret_cast<const float4*>(g + i);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const size_t i = base + (static_cast<size_t>(k) * kThreads + threadIdx.x) * 4;
+            adam_elem(pp[k].x, mm[k].x, vv[k].x, gg[k].x, L.a);
+            adam_elem(pp[k].y, mm[k].y, vv[k].y, gg[k].y, L.a);
+            adam_elem(pp[k].z, mm[k].z, vv[k].z, gg[k].z, L.a);
+            adam_elem(pp[k].w, mm[k].w, vv[k].w, gg[k].w, L.a);
+            *reinterpret_cast<float4*>(p + i) = pp[k];
+            *reinterpret_cast<float4*>(m + i) = mm[k];
+            *reinterpret_cast<float4*>(v + i) = vv[k];
+        }
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k)
     {

@@ -143,10 +143,14 @@ struct SwigluGradBoth
 };
 
 // ── column sums: out[c] = sum_r f(r, c) ──────────────────────────────────────
-// A workgroup owns 32 columns (8 float4s: one 128-byte line per row) and
-// splits the rows over 32 row groups; the 32 partial sums are added in
-// row-group order, so the result does not depend on scheduling.
-constexpr unsigned kColQuads = 8, kRowGroups = kT / kColQuads;
+// A workgroup of 16 waves owns 32 columns (8 float4s: one 128-byte line per
+// row) and splits the rows over 128 row groups (8 per wave); each thread
+// issues the loads of up to 8 of its rows before adding them. The partial
+// sums are combined in a fixed order (inside each wave, then over waves), so
+// the result does not depend on scheduling. At the GPT shapes (768 x 8192)
+// this puts 4 waves on every SIMD with 6 loads each in flight, where the
+// first version (4 waves per workgroup) had one wave per SIMD.
+constexpr unsigned kColT = 1024, kColQuads = 8, kRowGroups = kColT / kColQuads, kColWaves = kColT / 64;
 
 struct SumSq
 {
@@ -176,10 +180,11 @@ struct GGammaN
 };
 
 template <class F>
-__global__ __launch_bounds__(kT) void k_fused_colsum(F f, float* out, unsigned rows, unsigned cols4)
+__global__ __launch_bounds__(kColT) void k_fused_colsum(F f, float* out, unsigned rows, unsigned cols4)
 {
-    __shared__ float4 part[kRowGroups][kColQuads];
-    const unsigned qi = threadIdx.x % kColQuads, rg = threadIdx.x / kColQuads;
+    __shared__ float4 part[kColWaves][kColQuads];
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const unsigned qi = lane % kColQuads, rg = threadIdx.x / kColQuads;
     const unsigned q = blockIdx.x * kColQuads + qi;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     auto add = [&](const float4& v) {
@@ -190,27 +195,35 @@ __global__ __launch_bounds__(kT) void k_fused_colsum(F f, float* out, unsigned r
     };
     if (q < cols4)
     {
-        // Four rows' loads in flight per trip (one wave per SIMD at the GPT
-        // shapes, so each wave needs several); the sums keep row order.
+        constexpr unsigned kBatch = 8;   // rows whose loads are in flight together
         unsigned r = rg;
-        for (; r + 3 * kRowGroups < rows; r += 4 * kRowGroups)
+        for (; r + (kBatch - 1) * kRowGroups < rows; r += kBatch * kRowGroups)
         {
-            const float4 v0 = f(r, q), v1 = f(r + kRowGroups, q), v2 = f(r + 2 * kRowGroups, q),
-                         v3 = f(r + 3 * kRowGroups, q);
-            add(v0);
-            add(v1);
-            add(v2);
-            add(v3);
+            float4 v[kBatch];
+#pragma unroll
+            for (unsigned k = 0; k < kBatch; ++k) v[k] = f(r + k * kRowGroups, q);
+#pragma unroll
+            for (unsigned k = 0; k < kBatch; ++k) add(v[k]);
         }
         for (; r < rows; r += kRowGroups) add(f(r, q));
     }
-    part[rg][qi] = acc;
+    // The wave's 8 row groups of one column quad sit 8 lanes apart: add them
+    // pairwise (lane bits 3, 4, 5), every lane ending with the same sums.
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1)
+    {
+        acc.x += __shfl_xor(acc.x, o, 64);
+        acc.y += __shfl_xor(acc.y, o, 64);
+        acc.z += __shfl_xor(acc.z, o, 64);
+        acc.w += __shfl_xor(acc.w, o, 64);
+    }
+    if (lane < kColQuads) part[wave][lane] = acc;
     __syncthreads();
     if (threadIdx.x < kColQuads)
     {
         const unsigned qo = blockIdx.x * kColQuads + threadIdx.x;
         float4 s = part[0][threadIdx.x];
-        for (unsigned k = 1; k < kRowGroups; ++k)
+        for (unsigned k = 1; k < kColWaves; ++k)
         {
             const float4 v = part[k][threadIdx.x];
             s.x += v.x;
@@ -276,7 +289,7 @@ int launch_colsum(F f, float* out, size_t rows, size_t cols, hipStream_t s)
 {
     if (cols == 0) return 0;
     const unsigned cols4 = unsigned(cols / 4);
-    hipLaunchKernelGGL(k_fused_colsum<F>, dim3((cols4 + kColQuads - 1) / kColQuads), dim3(kT), 0, s, f, out,
+    hipLaunchKernelGGL(k_fused_colsum<F>, dim3((cols4 + kColQuads - 1) / kColQuads), dim3(kColT), 0, s, f, out,
                        unsigned(rows), cols4);
     return launch_status();
 }

@@ -53,7 +53,12 @@ __device__ __forceinline__ void tile_coords(int bid, int nt, int tiles_m, int ti
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // WM x WN waves; each wave owns (32*FM) x (32*FN) of C as FM x FN MFMA 32x32 blocks.
-template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD>
+// STATS: besides C, each workgroup writes the column softmax statistics of its
+// BM rows of C (as stored, bias included): part[tile_m * N + n] = max over the
+// rows, part[(tiles_m + tile_m) * N + n] = sum of exp(c - max) over them. The
+// sparse cross-entropy that follows the product (the GPT's lm_head logits)
+// merges these instead of reading C once more for them. Needs splits == 1.
+template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD, bool STATS = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K, long lda, long ldb,
                                                        long strideA, long strideB, long strideC, float alpha,
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     // when there are several, writes its partial tile to part[y][batch][M][N].
     const int k_lo = blockIdx.y * k_split;
     const int k_hi = min(K, k_lo + k_split);
-    if (gridDim.y > 1) C = part + ((long)blockIdx.y * gridDim.z + bz) * strideC;
+    if (!STATS && gridDim.y > 1) C = part + ((long)blockIdx.y * gridDim.z + bz) * strideC;
 
     f4 ra[LA], rb[LB];   // native vectors: HIP's float4 struct kept these arrays in scratch
 
@@ -245,7 +250,80 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     // as the separate broadcast / add call would round it); a split-K partial
     // is written unscaled and the reduce applies all of that.
     const int col_l = lane & 31, row_l = 4 * (lane >> 5);
-    const bool plain = gridDim.y > 1 || (!bias && !accum);
+    const bool plain = STATS || gridDim.y > 1 || (!bias && !accum);
+    if constexpr (STATS)
+    {
+        // acc becomes C as stored (alpha * acc, + bias[row] rounded as the
+        // separate add); the stores below then write it unchanged.
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+            {
+                const int gm = m0 + wm * 32 * FM + i * 32 + 8 * (r / 4) + row_l + (r % 4);
+                const float bv = (bias && (!GUARD || gm < M)) ? bias[gm] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                {
+#pragma clang fp contract(off)
+                    float v = alpha * acc[i][j][r];
+                    if (bias) v = v + bv;
+                    acc[i][j][r] = v;
+                }
+            }
+        float* sm = &Bs[0][0][0];    // [WM][BN] maxima, then [WM][BN] sums (the stages are done)
+        float* ss = sm + WM * BN;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+        {
+            float mx = -__builtin_huge_valf();
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                {
+                    const int gm = m0 + wm * 32 * FM + i * 32 + 8 * (r / 4) + row_l + (r % 4);
+                    if (!GUARD || gm < M) mx = fmaxf(mx, acc[i][j][r]);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));   // lanes l and l ^ 32 hold one column's other rows
+            float sum = 0.0f;
+            if (mx > -__builtin_huge_valf())
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                    {
+                        const int gm = m0 + wm * 32 * FM + i * 32 + 8 * (r / 4) + row_l + (r % 4);
+                        if (!GUARD || gm < M) sum += __expf(acc[i][j][r] - mx);
+                    }
+            sum += __shfl_xor(sum, 32, 64);
+            if (lane < 32)
+            {
+                sm[wm * BN + wn * 32 * FN + j * 32 + col_l] = mx;
+                ss[wm * BN + wn * 32 * FN + j * 32 + col_l] = sum;
+            }
+        }
+        __syncthreads();
+        for (int c = tid; c < BN; c += NT)
+        {
+            const int gn = n0 + c;
+            if (GUARD && gn >= N) continue;
+            float m = sm[c], t = ss[c];
+            for (int w = 1; w < WM; ++w)   // merge the waves' row bands in row order
+            {
+                const float m2 = sm[w * BN + c], t2 = ss[w * BN + c];
+                if (m2 > m)
+                {
+                    t = t * __expf(m - m2) + t2;
+                    m = m2;
+                }
+                else if (m2 > -__builtin_huge_valf())
+                    t = t + t2 * __expf(m2 - m);
+            }
+            part[(long)tmi * N + gn] = m;
+            part[(long)(tiles_m + tmi) * N + gn] = t;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -260,7 +338,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
                 float* c = C + (long)gm * N + gn;
                 if (plain)
                 {
-                    *c = (gridDim.y > 1 ? 1.0f : alpha) * acc[i][j][r];
+                    *c = STATS ? acc[i][j][r] : (gridDim.y > 1 ? 1.0f : alpha) * acc[i][j][r];
                     continue;
                 }
                 {
@@ -510,10 +588,47 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
     return launch_status();
 }
 
+// The product of nnhip_gemm_colstats: 256 x 128 tiles of 8 waves, no split.
+constexpr int kStatsBM = 256, kStatsBN = 128;
+bool colstats_ok(size_t M, size_t N, size_t K, int tA, int tB)
+{
+    return !tA && !tB && M > 0 && N > 0 && K > 0 && M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff &&
+           plan_gemm(M, N, K, 1, false).cfg == kTall;
+}
+
 } // namespace
 } // namespace nnhip
 
 using namespace nnhip;
+
+extern "C" size_t nnhip_gemm_colstats_tiles(size_t M, size_t N, size_t K, int transA, int transB)
+{
+    return colstats_ok(M, N, K, transA, transB) ? (M + kStatsBM - 1) / kStatsBM : 0;
+}
+
+extern "C" int nnhip_gemm_colstats(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols,
+                                   size_t B_rows, size_t B_cols, int transA, int transB, const float* row_bias,
+                                   float* stats, void* stream)
+{
+    const size_t M = transA ? A_cols : A_rows, K = transA ? A_rows : A_cols;
+    const size_t K2 = transB ? B_cols : B_rows, N = transB ? B_rows : B_cols;
+    if (K != K2) return -2;
+    if (!colstats_ok(M, N, K, transA, transB)) return -3;
+    if (!A || !B || !C || !stats) return -1;
+    const int m = (int)M, n = (int)N, k = (int)K;
+    const int tm = (m + kStatsBM - 1) / kStatsBM, tn = (n + kStatsBN - 1) / kStatsBN;
+    const bool vec = (A_cols % 4 == 0) && (B_cols % 4 == 0) && aligned16(A) && aligned16(B);
+    const bool guard = !vec || (m % kStatsBM) || (n % kStatsBN) || (k % 16);
+    const dim3 grid(static_cast<unsigned>(tm * tn), 1, 1), block(512);
+    auto s = static_cast<hipStream_t>(stream);
+    if (guard)
+        hipLaunchKernelGGL((k_gemm<4, 2, 2, 2, 16, false, false, true, true>), grid, block, 0, s, A, B, C, m, n, k,
+                           (long)A_cols, (long)B_cols, 0L, 0L, 0L, 1.0f, tm, tn, k, stats, row_bias, 0);
+    else
+        hipLaunchKernelGGL((k_gemm<4, 2, 2, 2, 16, false, false, false, true>), grid, block, 0, s, A, B, C, m, n, k,
+                           (long)A_cols, (long)B_cols, 0L, 0L, 0L, 1.0f, tm, tn, k, stats, row_bias, 0);
+    return launch_status();
+}
 
 extern "C" size_t nnhip_gemm_workspace_bytes(size_t M, size_t N, size_t K, size_t batch)
 {

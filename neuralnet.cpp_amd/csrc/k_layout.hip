@@ -73,27 +73,29 @@ __global__ __launch_bounds__(256) void k_transpose4(const float* A, float* out, 
 }
 
 // ── rearrange_3d: (M, B*N) <-> (B*M, N), contiguous runs of N ─────────────
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void k_rearrange(const float* in, float* out, size_t M, size_t B, size_t N,
+// IT: index type, 32-bit when every index fits (integer division by a
+// runtime divisor costs several times more in 64 bits).
+template <bool VEC, class IT>
+__global__ __launch_bounds__(kThreads) void k_rearrange(const float* in, float* out, IT M, IT B, IT N,
                                                         unsigned inverse)
 {
-    const size_t W = VEC ? 4 : 1;
-    const size_t total = M * B * N / W;
-    const size_t Nw = N / W;
-    const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
-    for (size_t o = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; o < total; o += stride)
+    const IT W = VEC ? 4 : 1;
+    const IT total = M * B * N / W;
+    const IT Nw = N / W;
+    const IT stride = static_cast<IT>(gridDim.x) * kThreads;
+    for (IT o = static_cast<IT>(blockIdx.x) * kThreads + threadIdx.x; o < total; o += stride)
     {
-        size_t src;
+        IT src;
         if (!inverse)
         {
             // out[(b*M+m), n] = in[m, b*N+n]
-            const size_t row = o / Nw, n = o % Nw, b = row / M, m = row % M;
+            const IT row = o / Nw, n = o - row * Nw, b = row / M, m = row - b * M;
             src = (m * B + b) * Nw + n;
         }
         else
         {
             // out[m, b*N+n] = in[(b*M+m), n]
-            const size_t m = o / (B * Nw), rem = o % (B * Nw), b = rem / Nw, n = rem % Nw;
+            const IT m = o / (B * Nw), rem = o - m * (B * Nw), b = rem / Nw, n = rem - b * Nw;
             src = (b * M + m) * Nw + n;
         }
         if constexpr (VEC)
@@ -104,22 +106,22 @@ __global__ __launch_bounds__(kThreads) void k_rearrange(const float* in, float* 
 }
 
 // ── gather: out[i, :] = table[idx[i], :] or zeros ─────────────────────────
-template <bool VEC>
+template <bool VEC, class IT>
 __global__ __launch_bounds__(kThreads) void k_gather(const float* table, const float* idx, float* out, size_t vocab,
-                                                     size_t D, size_t num)
+                                                     IT D, IT num)
 {
-    const size_t W = VEC ? 4 : 1, Dw = D / W, total = num * Dw;
-    const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
-    for (size_t o = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; o < total; o += stride)
+    const IT W = VEC ? 4 : 1, Dw = D / W, total = num * Dw;
+    const IT stride = static_cast<IT>(gridDim.x) * kThreads;
+    for (IT o = static_cast<IT>(blockIdx.x) * kThreads + threadIdx.x; o < total; o += stride)
     {
-        const size_t i = o / Dw, d = o % Dw;
+        const IT i = o / Dw, d = o - i * Dw;
         size_t r;
         const bool ok = row_index(idx[i], vocab, r);
         if constexpr (VEC)
             reinterpret_cast<float4*>(out)[o] =
-                ok ? reinterpret_cast<const float4*>(table)[r * Dw + d] : make_float4(0, 0, 0, 0);
+                ok ? reinterpret_cast<const float4*>(table)[r * size_t(Dw) + d] : make_float4(0, 0, 0, 0);
         else
-            out[o] = ok ? table[r * D + d] : 0.0f;
+            out[o] = ok ? table[r * size_t(D) + d] : 0.0f;
     }
 }
 
@@ -263,12 +265,20 @@ extern "C" int nnhip_rearrange_3d(const float* A, float* out, size_t M, size_t B
     const size_t total = M * B * N;
     if (total == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
-    if (N % 4 == 0 && aligned16(A) && aligned16(out))
-        hipLaunchKernelGGL(k_rearrange<true>, dim3(grid_for(total / 4, kThreads, 256 * 32)), dim3(kThreads), 0, s, A,
-                           out, M, B, N, inverse);
+    const bool vec = N % 4 == 0 && aligned16(A) && aligned16(out);
+    const unsigned grid = grid_for(vec ? total / 4 : total, kThreads, 256 * 32);
+    // 32-bit indices when o + stride cannot wrap
+    const bool i32 = total + static_cast<size_t>(grid) * kThreads < (size_t{1} << 32);
+    if (vec && i32)
+        hipLaunchKernelGGL((k_rearrange<true, unsigned>), dim3(grid), dim3(kThreads), 0, s, A, out, unsigned(M),
+                           unsigned(B), unsigned(N), inverse);
+    else if (vec)
+        hipLaunchKernelGGL((k_rearrange<true, size_t>), dim3(grid), dim3(kThreads), 0, s, A, out, M, B, N, inverse);
+    else if (i32)
+        hipLaunchKernelGGL((k_rearrange<false, unsigned>), dim3(grid), dim3(kThreads), 0, s, A, out, unsigned(M),
+                           unsigned(B), unsigned(N), inverse);
     else
-        hipLaunchKernelGGL(k_rearrange<false>, dim3(grid_for(total, kThreads, 256 * 32)), dim3(kThreads), 0, s, A,
-                           out, M, B, N, inverse);
+        hipLaunchKernelGGL((k_rearrange<false, size_t>), dim3(grid), dim3(kThreads), 0, s, A, out, M, B, N, inverse);
     return launch_status();
 }
 
@@ -278,12 +288,21 @@ extern "C" int nnhip_gather(const float* table, const float* indices, float* out
     const size_t total = num * D;
     if (total == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
-    if (D % 4 == 0 && aligned16(table) && aligned16(out))
-        hipLaunchKernelGGL(k_gather<true>, dim3(grid_for(total / 4, kThreads, 256 * 32)), dim3(kThreads), 0, s, table,
-                           indices, out, vocab, D, num);
+    const bool vec = D % 4 == 0 && aligned16(table) && aligned16(out);
+    const unsigned grid = grid_for(vec ? total / 4 : total, kThreads, 256 * 32);
+    const bool i32 = total + static_cast<size_t>(grid) * kThreads < (size_t{1} << 32);
+    if (vec && i32)
+        hipLaunchKernelGGL((k_gather<true, unsigned>), dim3(grid), dim3(kThreads), 0, s, table, indices, out, vocab,
+                           unsigned(D), unsigned(num));
+    else if (vec)
+        hipLaunchKernelGGL((k_gather<true, size_t>), dim3(grid), dim3(kThreads), 0, s, table, indices, out, vocab, D,
+                           num);
+    else if (i32)
+        hipLaunchKernelGGL((k_gather<false, unsigned>), dim3(grid), dim3(kThreads), 0, s, table, indices, out, vocab,
+                           unsigned(D), unsigned(num));
     else
-        hipLaunchKernelGGL(k_gather<false>, dim3(grid_for(total, kThreads, 256 * 32)), dim3(kThreads), 0, s, table,
-                           indices, out, vocab, D, num);
+        hipLaunchKernelGGL((k_gather<false, size_t>), dim3(grid), dim3(kThreads), 0, s, table, indices, out, vocab, D,
+                           num);
     return launch_status();
 }
 

@@ -53,8 +53,27 @@ __global__ __launch_bounds__(kThreads) void k_row_block(const float* A, float* o
     float acc = mode ? kLowest : 0.0f;
     if ((cols % 4) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0)
     {
+        // Eight float4 loads in flight per thread (a 8192-wide row is one
+        // batch), then added in column order.
         const float4* r4 = reinterpret_cast<const float4*>(row);
-        for (size_t c = threadIdx.x; c < cols / 4; c += kThreads)
+        const size_t n4 = cols / 4;
+        constexpr unsigned kBatch = 8;
+        size_t c = threadIdx.x;
+        for (; c + (kBatch - 1) * kThreads < n4; c += kBatch * kThreads)
+        {
+            float4 v[kBatch];
+#pragma unroll
+            for (unsigned k = 0; k < kBatch; ++k) v[k] = r4[c + k * kThreads];
+#pragma unroll
+            for (unsigned k = 0; k < kBatch; ++k)
+            {
+                acc = combine(mode, acc, v[k].x);
+                acc = combine(mode, acc, v[k].y);
+                acc = combine(mode, acc, v[k].z);
+                acc = combine(mode, acc, v[k].w);
+            }
+        }
+        for (; c < n4; c += kThreads)
         {
             const float4 v = r4[c];
             acc = combine(mode, acc, v.x);

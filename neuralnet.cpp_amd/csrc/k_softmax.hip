@@ -146,6 +146,33 @@ __global__ __launch_bounds__(kThreads) void k_ce_combine(const float* L, const f
     loss_vec[c] = valid ? L[lbl * N + c] - m - logf(s) : 0.0f;
 }
 
+// The same over many chunks (one per 256-row block of a product's statistics):
+// a workgroup owns 64 columns, its 4 waves merge a quarter of the chunks each
+// (in chunk order), then wave 0 merges the 4 results in wave order.
+__global__ __launch_bounds__(kThreads) void k_ce_combine_wide(const float* L, const float* labels, const float* mask,
+                                                              const float* part_m, const float* part_s, float* col_m,
+                                                              float* col_s, float* loss_vec, size_t chunks, size_t C,
+                                                              size_t N, size_t vocab)
+{
+    __shared__ float sm[kWaves][64], ss[kWaves][64];
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const size_t c = static_cast<size_t>(blockIdx.x) * 64 + lane;
+    const size_t per = (chunks + kWaves - 1) / kWaves, k0 = wave * per, k1 = k0 + per < chunks ? k0 + per : chunks;
+    float m = -__builtin_huge_valf(), s = 0.0f;
+    if (c < N)
+        for (size_t k = k0; k < k1; ++k) merge(m, s, part_m[k * N + c], part_s[k * N + c]);
+    sm[wave][lane] = m;
+    ss[wave][lane] = s;
+    __syncthreads();
+    if (wave != 0 || c >= N) return;
+    for (unsigned w = 1; w < kWaves; ++w) merge(m, s, sm[w][lane], ss[w][lane]);
+    const size_t lbl = label_of(labels[c]);
+    const bool valid = (!mask || mask[c] >= 0.5f) && lbl < vocab;
+    col_m[c] = m;
+    col_s[c] = valid ? s : 0.0f;   // 0 marks an invalid column for the gradient pass
+    loss_vec[c] = valid ? L[lbl * N + c] - m - logf(s) : 0.0f;
+}
+
 __global__ __launch_bounds__(kThreads) void k_ce_grad(const float* L, const float* labels, const float* col_m,
                                                       const float* col_s, float* grad, size_t C, size_t N,
                                                       float inv)
@@ -272,21 +299,30 @@ __global__ __launch_bounds__(kThreads) void k_ce_grad4(const float* L, const flo
         at(f, e) = at(sv, e) != 0.0f ? inv / at(sv, e) : 0.0f;
         lbl[e] = at(sv, e) != 0.0f ? label_of(at(lb, e)) : ~size_t{0};
     }
-    const float4* L4 = reinterpret_cast<const float4*>(L);
-    float4* G4 = reinterpret_cast<float4*>(grad);
-    for (size_t r = r0 + wave; r < r1; r += kWaves)
-    {
-        const float4 x = L4[r * N4 + c4];
+    const float4* __restrict__ L4 = reinterpret_cast<const float4*>(L);
+    float4* __restrict__ G4 = reinterpret_cast<float4*>(grad);
+    auto one = [&](const float4& x, size_t r) {
         float4 gv;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
         {
-            float gg = at(f, e) * expf(at(x, e) - at(m, e));
+            float gg = at(f, e) * __expf(at(x, e) - at(m, e));
             if (lbl[e] == r) gg -= inv;
             at(gv, e) = gg;
         }
         G4[r * N4 + c4] = gv;
+    };
+    constexpr unsigned kBatch = 4;   // rows whose loads are in flight together
+    size_t r = r0 + wave;
+    for (; r + (kBatch - 1) * kWaves < r1; r += kBatch * kWaves)
+    {
+        float4 x[kBatch];
+#pragma unroll
+        for (unsigned k = 0; k < kBatch; ++k) x[k] = L4[(r + k * kWaves) * N4 + c4];
+#pragma unroll
+        for (unsigned k = 0; k < kBatch; ++k) one(x[k], r + k * kWaves);
     }
+    for (; r < r1; r += kWaves) one(L4[r * N4 + c4], r);
 }
 
 // ── row softmax ─────────────────────────────────────────────────────────────
@@ -519,8 +555,36 @@ extern "C" int nnhip_col_softmax_sparse_forward(const float* logits, const float
     else
         hipLaunchKernelGGL(k_col_stats<false>, dim3(static_cast<unsigned>(p.col_blocks), static_cast<unsigned>(p.chunks)),
                            dim3(kThreads), 0, s, logits, nullptr, pm, ps, C, N, p.rows_per_chunk);
-    hipLaunchKernelGGL(k_ce_combine, dim3(grid_for(N, kThreads, 1u << 30)), dim3(kThreads), 0, s, logits, labels, mask,
-                       pm, ps, cm, cs, loss_vec, p.chunks, C, N, vocab_size);
+    hipLaunchKernelGGL(k_ce_combine_wide, dim3(static_cast<unsigned>((N + 63) / 64)), dim3(kThreads), 0, s, logits,
+                       labels, mask, pm, ps, cm, cs, loss_vec, p.chunks, C, N, vocab_size);
+    if (v4)
+    {
+        const size_t rows_per_block = 64, col_blocks = (N / 4 + 63) / 64;
+        const size_t row_blocks = (C + rows_per_block - 1) / rows_per_block;
+        if (row_blocks > 65535) return -3;
+        hipLaunchKernelGGL(k_ce_grad4, dim3(static_cast<unsigned>(col_blocks), static_cast<unsigned>(row_blocks)),
+                           dim3(kThreads), 0, s, logits, labels, cm, cs, grad, C, N, inv_num_valid, rows_per_block);
+    }
+    else
+        hipLaunchKernelGGL(k_ce_grad, dim3(grid_for(C * N, kThreads, 256 * 64)), dim3(kThreads), 0, s, logits, labels,
+                           cm, cs, grad, C, N, inv_num_valid);
+    return launch_status();
+}
+
+extern "C" int nnhip_col_softmax_sparse_from_stats(const float* logits, const float* labels, const float* mask,
+                                                   const float* stats, size_t tiles, float* grad, float* loss_vec,
+                                                   size_t C, size_t N, size_t vocab_size, float inv_num_valid,
+                                                   void* workspace, void* stream)
+{
+    if (vocab_size > (size_t{1} << 24) || vocab_size > C) return -2;
+    if (N == 0) return 0;
+    if (C == 0 || tiles == 0 || !stats || !workspace) return -1;
+    auto s = static_cast<hipStream_t>(stream);
+    float* cm = static_cast<float*>(workspace);
+    float* cs = cm + N;
+    hipLaunchKernelGGL(k_ce_combine_wide, dim3(static_cast<unsigned>((N + 63) / 64)), dim3(kThreads), 0, s, logits,
+                       labels, mask, stats, stats + tiles * N, cm, cs, loss_vec, tiles, C, N, vocab_size);
+    const bool v4 = cols4_ok(logits, N) && aligned16(labels) && aligned16(workspace) && aligned16(grad);
     if (v4)
     {
         const size_t rows_per_block = 64, col_blocks = (N / 4 + 63) / 64;

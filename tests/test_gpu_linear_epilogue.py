@@ -105,3 +105,38 @@ def test_other_consumers(hip):
     c3 = hip.matmul(a, bm)
     hip.scale_inplace(a, 2.0)                           # an input written before the product ran
     assert nrm_err(c3.numpy(), A.astype(np.float64) @ B.astype(np.float64)) <= 1e-5
+
+
+@pytest.mark.parametrize("M,N,K,masked", [(32000, 2048, 768, True), (4096, 4096, 128, False), (1000, 520, 64, True),
+                                          (300, 200, 64, False)])
+def test_ce_from_product_statistics(hip, cpu, M, N, K, masked):
+    """The lm_head Linear then sparse cross-entropy (compute_layer.hpp Linear::forward, compute_loss.hpp:229-309):
+    matmul(W, x), broadcast_row_inplace(logits, b), col_softmax_sparse_forward(logits, ...). When the CE call
+    reads the still-recorded product, the product's epilogue yields per-tile column statistics and the CE
+    reads the logits once (shapes with >= 512 output tiles of 256 x 128; the others take the plain path).
+    Bars: logits bit-exact against the calls launched one by one; gradient and loss within 1e-5 of the
+    unfused HIP path and of the oracle."""
+    rng = np.random.default_rng(M + N + K)
+    W, X = uniform(rng, (M, K), -0.2, 0.2), uniform(rng, (K, N))
+    b = uniform(rng, (M, 1))
+    labels = rng.integers(0, M, size=N).astype(np.float32)
+    labels[::13] = M + 1                       # invalid: zero column
+    mask = (rng.random(N) > 0.1).astype(np.float32) if masked else None
+    inv = 1.0 / N
+
+    def run(e, settle):
+        w, x, bb = e.tensor(W), e.tensor(X), e.tensor(b)
+        lab = e.tensor(labels.reshape(1, -1))
+        mk = e.tensor(mask.reshape(1, -1)) if masked else None
+        logits = e.matmul(w, x)
+        e.broadcast_row_inplace(logits, bb, "Add")
+        if settle:
+            e.settle()
+        g, lv = e.col_softmax_sparse_forward(logits, lab, mk, M, inv)
+        return logits.numpy(), g.numpy(), lv.numpy()
+
+    fused, calls, ref = run(hip, False), run(hip, True), run(cpu, False)
+    assert np.array_equal(bits(fused[0]), bits(calls[0]))
+    for a, c, r in zip(fused[1:], calls[1:], ref[1:]):
+        assert nrm_err(a, c) <= 1e-5
+        assert nrm_err(a, r) <= 1e-5
