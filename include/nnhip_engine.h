@@ -73,6 +73,12 @@ const char* nnhip_last_error(void);
 
 /* Engine on the current HIP device (its own stream, its own caching pool). */
 int nnhip_engine_create(nnhip_engine** out);
+/* Engine selection as the reference's cli::create_engine (include/neuralnet.cpp/cli/engine_factory.hpp:45-88)
+ * with a use_hip flag first in priority (HIP > CUDA > Vulkan > CPU): the requested backend, or an error
+ * and *out = NULL, never a fallback to another engine. This library holds the HIP engine only, so a CUDA or
+ * Vulkan request, or none (the reference's CpuEngine), is an error naming the engine to use. verbose: one
+ * line on stderr naming the engine. */
+int nnhip_engine_select(int use_hip, int use_cuda, int use_gpu, int verbose, nnhip_engine** out);
 void nnhip_engine_destroy(nnhip_engine* e);
 int nnhip_engine_sync(nnhip_engine* e);   /* end_batch: waits for all queued work */
 

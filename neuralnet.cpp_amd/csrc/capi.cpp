@@ -1,5 +1,8 @@
 // capi.cpp — the engine C-ABI (include/nnhip_engine.h) over HipEngine.
+#include <iostream>
+
 #include "nn/engine_capi.hpp"
+#include "nn/engine_factory.hpp"
 #include "nn/hip_engine.hpp"
 
 namespace
@@ -63,4 +66,20 @@ extern "C" NN_CAPI_EXPORT int nnhip_engine_settle(void* e)
     if (!h) return nn::capi::set_error("settle: not a HIP engine");
     auto r = h->settle();
     return r ? 0 : nn::capi::set_error(r.error().message);
+}
+
+// cli::create_engine with the reference's flags (cli/engine_factory.hpp:45-88)
+// plus use_hip: the requested backend or an error, never another engine.
+extern "C" NN_CAPI_EXPORT int nnhip_engine_select(int use_hip, int use_cuda, int use_gpu, int verbose, void** out)
+{
+    if (!out) return nn::capi::set_error("engine_select: null output");
+    *out = nullptr;
+    nn::cli::EngineConfig cfg;
+    cfg.use_hip = use_hip != 0;
+    cfg.use_cuda = use_cuda != 0;
+    cfg.use_gpu = use_gpu != 0;
+    auto r = nn::cli::create_engine(cfg, verbose ? &std::cerr : nullptr);
+    if (!r) return nn::capi::set_error(r.error().message);
+    *out = new nn::capi::EngineHandle{std::move(*r)};
+    return 0;
 }

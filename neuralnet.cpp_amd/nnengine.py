@@ -52,6 +52,20 @@ def hip_library() -> ctypes.CDLL:
     return ctypes.CDLL(HIP_LIB_PATH)
 
 
+def create_engine(use_hip: bool = False, use_cuda: bool = False, use_gpu: bool = False,
+                  verbose: bool = False) -> "Engine":
+    """cli::create_engine with the reference's selection rules (cli/engine_factory.hpp:45-88) plus use_hip:
+    the requested engine or EngineError, never a fallback to another engine."""
+    lib = hip_library()
+    fn = lib.nnhip_engine_select
+    fn.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_void_p)]
+    h = ctypes.c_void_p()
+    if fn(int(use_hip), int(use_cuda), int(use_gpu), int(verbose), ctypes.byref(h)) != 0:
+        lib.nnhip_last_error.restype = ctypes.c_char_p
+        raise EngineError(lib.nnhip_last_error().decode())
+    return Engine(lib, handle=h.value)
+
+
 class _GptConfig(ctypes.Structure):
     _fields_ = [("vocab_size", ctypes.c_size_t), ("d_model", ctypes.c_size_t), ("seq_len", ctypes.c_size_t),
                 ("num_heads", ctypes.c_size_t), ("d_ff", ctypes.c_size_t), ("num_layers", ctypes.c_size_t),
@@ -161,9 +175,12 @@ class Tensor:
 class Engine:
     """Python mirror of nn::ComputeEngine over a library exporting include/nnhip_engine.h."""
 
-    def __init__(self, lib: Optional[ctypes.CDLL] = None, prefix: str = "nnhip_"):
+    def __init__(self, lib: Optional[ctypes.CDLL] = None, prefix: str = "nnhip_", handle: Optional[int] = None):
         self._lib = lib if lib is not None else hip_library()
         self._f = _bind(self._lib, prefix)
+        if handle is not None:   # an engine already created (create_engine)
+            self._e = ctypes.c_void_p(handle)
+            return
         e = ctypes.c_void_p()
         self._check(self._f["engine_create"](ctypes.byref(e)))
         self._e = e

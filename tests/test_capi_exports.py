@@ -45,7 +45,8 @@ def test_product_library_exports_every_declared_symbol(header):
 def test_oracle_mirrors_engine_abi():
     lib = ctypes.CDLL(ORACLE_LIB)
     names = [n for n in _declared(os.path.join(ROOT, "include", "nnhip_engine.h"))
-             if not n.startswith("nnhip_engine_profile") and n not in ("nnhip_engine_stream", "nnhip_engine_settle")]
+             if not n.startswith("nnhip_engine_profile")
+             and n not in ("nnhip_engine_stream", "nnhip_engine_settle", "nnhip_engine_select")]
     missing = [n for n in names if not hasattr(lib, "nnoracle_" + n[len("nnhip_"):])]
     assert not missing, f"oracle lacks the mirror of {missing}"
 
@@ -75,3 +76,20 @@ def test_expr_spec_serialisation_layout():
     assert list(instrs[1][4:6]) == [nnengine.OPND["Const"], 0]
     assert list(kinds) == [nnengine.VIEW["Linear"], 0, nnengine.VIEW["ColBroadcast"], 1]
     assert list(params) == [0, 3] and consts.dtype == np.float32 and consts[0] == 0.5
+
+
+def test_engine_selection_never_falls_back():
+    """cli::create_engine's rules (reference cli/engine_factory.hpp:45-88) with use_hip added: a requested
+    backend that cannot be created is an error, never another engine. This container has no GPU, so a HIP
+    request fails here; CUDA / Vulkan requests and no request name the reference's engines."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present: the HIP request succeeds (tests/test_gpu_engine_select.py)")
+    with pytest.raises(nnengine.EngineError, match="no fallback"):
+        nnengine.create_engine(use_hip=True)
+    with pytest.raises(nnengine.EngineError, match="CUDA.*no fallback"):
+        nnengine.create_engine(use_cuda=True)
+    with pytest.raises(nnengine.EngineError, match="Vulkan.*no fallback"):
+        nnengine.create_engine(use_gpu=True)
+    with pytest.raises(nnengine.EngineError, match="HIP engine only"):
+        nnengine.create_engine()
