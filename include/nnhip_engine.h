@@ -120,11 +120,14 @@ int nnhip_window_batch(const uint64_t* flow, const uint64_t* flow_doc, size_t n_
                        size_t batch, size_t seq, uint64_t pad_id, float* tokens, uint64_t* labels, float* loss_mask,
                        uint64_t* doc_ids, size_t* valid);
 
-/* GPT training session (GPTModel + sparse CE + AdamW; SwiGLU FFN, RMSNorm). */
+/* GPT training session (GPTModel + sparse CE + an optimizer; compute_layer.hpp:2662-3096, domain_gpt.hpp:48-63). */
 typedef struct nnhip_gpt_config {
     size_t vocab_size, d_model, seq_len, num_heads, d_ff, num_layers;
-    uint32_t pos_enc; /* 0 learned, 1 sinusoidal, 2 ALiBi (model_spec.hpp:24-30) */
-    float lr, beta1, beta2, eps, weight_decay;
+    uint32_t pos_enc; /* 0 learned, 1 sinusoidal, 2 ALiBi, 3 RoPE (model_spec.hpp:24-30) */
+    float lr, beta1, beta2, eps, weight_decay;   /* beta1 / beta2 / eps: AdamW only */
+    uint32_t activation;  /* 0 QuickGeLU, 1 SwiGLU (model_spec.hpp:33-37) */
+    uint32_t norm_type;   /* 0 LayerNorm, 1 RMSNorm (model_spec.hpp:40-45) */
+    uint32_t optimizer;   /* 0 adamw, 1 adam, 2 sgd, 3 sgd_momentum, 4 muon (compute_optimizer.hpp:594-615) */
 } nnhip_gpt_config;
 
 int nnhip_gpt_create(nnhip_engine* e, const nnhip_gpt_config* cfg, nnhip_gpt** out);
@@ -143,7 +146,7 @@ int nnhip_gpt_load_batch(nnhip_gpt* g, const float* tokens, size_t seq, size_t b
 int nnhip_gpt_forward_loss(nnhip_gpt* g, float* loss_out);   /* forward + sparse CE on the resident batch */
 int nnhip_gpt_logits(nnhip_gpt* g, float* out);              /* (vocab, batch*seq) of the last forward */
 int nnhip_gpt_backward(nnhip_gpt* g);
-int nnhip_gpt_optimizer_step(nnhip_gpt* g);                  /* AdamW */
+int nnhip_gpt_optimizer_step(nnhip_gpt* g);                  /* the session's optimizer (cfg.optimizer) */
 int nnhip_gpt_zero_grad(nnhip_gpt* g);
 /* forward + CE + backward + AdamW + zero_grad on the resident batch. */
 int nnhip_gpt_train_step(nnhip_gpt* g, float* loss_out);
@@ -164,6 +167,19 @@ int nnhip_gpt_clip_grad_norm(nnhip_gpt* g, float max_norm);
  * backward scaled by 1 / accum_steps (accum_steps >= 1); when do_update != 0 also
  * clip_grad_norm(max_norm) if max_norm > 0, AdamW step and zero_grad. */
 int nnhip_gpt_train_step_ex(nnhip_gpt* g, size_t accum_steps, float max_norm, int do_update, float* loss_out);
+/* Incremental inference with KV caches (GPTModel::forward_step / generate, compute_layer.hpp:2906-3096).
+ * _forward_step runs one token (id `token` at position `pos`) through the model with the session's
+ * per-block K / V caches ((seq_len, d_model) each, created on first use), writing cache row cur_len and
+ * attending over rows [0, cur_len]; logits_out (vocab floats) may be NULL. _reset_cache drops the caches.
+ * _generate fills fresh caches from the prompt (its last seq_len tokens), then samples up to max_new
+ * tokens (temperature 0: argmax; else softmax(logits / temperature) and one uniform draw of
+ * std::mt19937_64(seed) per token; caches refilled with the last seq_len - 1 tokens when full) and stops
+ * early at eos once min_new tokens are out; *n_out = tokens generated, up to out_cap copied to out. The
+ * reference seeds its generator from std::random_device; the seed argument makes runs repeatable. */
+int nnhip_gpt_forward_step(nnhip_gpt* g, uint64_t token, size_t pos, size_t cur_len, float* logits_out);
+int nnhip_gpt_reset_cache(nnhip_gpt* g);
+int nnhip_gpt_generate(nnhip_gpt* g, const uint64_t* prompt, size_t n_prompt, size_t max_new, float temperature,
+                       uint64_t eos, size_t min_new, uint64_t seed, uint64_t* out, size_t out_cap, size_t* n_out);
 
 /* Measurement hooks (no reference counterpart). While enabled, every GEMM launch of the
  * engine is bracketed by HIP events on the engine's stream; _read waits for the stream and

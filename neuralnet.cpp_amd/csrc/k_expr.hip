@@ -25,15 +25,36 @@ namespace
 
 constexpr unsigned kThreads = 256;
 
+// Device-side copy of the program. Every field indexed at run time is a
+// 32-bit word or wider and every record is 8-byte aligned: a byte array
+// indexed by a run-time value lets the compiler form a scalar-load base of
+// kernarg + index (not dword-aligned) and reuse it for the word arrays beside
+// it, and scalar loads drop the low two address bits of such a base.
+struct ViewArg
+{
+    const float* in;
+    const float* vred;      // reduce-view vector
+    unsigned param;         // RotateHalf block / RowMod modulus
+    unsigned kind;
+    unsigned negate;
+    unsigned pad;
+};
 struct ExprArgs
 {
-    nnhip_expr_program p;
-    const float* in[8];
-    const float* vred[8];     // reduce-view vectors
+    unsigned instrs[64][2];   // the 8 instruction bytes as two little-endian words
+    float consts[16];
+    ViewArg view[8];
     const float* rvec[16];    // reduce-instruction vectors, by destination register
-    unsigned char raxis[16];  // 1 = per column, 0 = per row
+    unsigned raxis[16];       // 1 = per column, 0 = per row
+    unsigned n_instrs;
     size_t rows, cols;
 };
+
+// Byte b (0..7) of instruction j.
+__device__ __forceinline__ unsigned ibyte(const ExprArgs& A, unsigned j, unsigned b)
+{
+    return (A.instrs[j][b >> 2] >> (8 * (b & 3))) & 0xffu;
+}
 
 enum : unsigned char { K_REG = 0, K_INPUT = 1, K_CONST = 2, K_FANOUT = 3, K_REDUCE = 4 };
 enum : unsigned char
@@ -47,45 +68,46 @@ enum : unsigned char
     E_GT, E_GE, E_EQ, E_NE, E_SELECT, E_COLSUM, E_COLMAX, E_ROWSUM, E_ROWMAX
 };
 
-__device__ __forceinline__ bool is_reduce(unsigned char op) { return op >= E_COLSUM; }
+__device__ __forceinline__ bool is_reduce(unsigned op) { return op >= E_COLSUM; }
 
 __device__ __forceinline__ float read_input(const ExprArgs& A, unsigned k, size_t r, size_t c)
 {
-    const float* s = A.in[k];
+    const ViewArg& v = A.view[k];
+    const float* s = v.in;
     const size_t cols = A.cols;
-    switch (A.p.view_kind[k])
+    switch (v.kind)
     {
     case V_ROTATE:
     {
-        const size_t blk = A.p.view_param[k], rl = r % blk, h = blk / 2;
+        const size_t blk = v.param, rl = r % blk, h = blk / 2;
         const size_t rr = (r / blk) * blk + (rl < h ? rl + h : rl - h);
-        const float v = s[rr * cols + c];
-        return (A.p.view_negate[k] && rl < h) ? -v : v;
+        const float x = s[rr * cols + c];
+        return (v.negate && rl < h) ? -x : x;
     }
-    case V_ROWMOD: return s[(r % A.p.view_param[k]) * cols + c];
+    case V_ROWMOD: return s[(r % v.param) * cols + c];
     case V_ROWSUM:
-    case V_ROWMAX: return A.vred[k][r];
+    case V_ROWMAX: return v.vred[r];
     case V_COLSUM:
-    case V_COLMAX: return A.vred[k][c];
+    case V_COLMAX: return v.vred[c];
     case V_ROWBC: return s[r];
     case V_COLBC: return s[c];
     default: return s[r * cols + c];
     }
 }
 
-__device__ __forceinline__ float operand(const ExprArgs& A, unsigned char kind, unsigned char idx, size_t r, size_t c,
+__device__ __forceinline__ float operand(const ExprArgs& A, unsigned kind, unsigned idx, size_t r, size_t c,
                                          const float* regs)
 {
     switch (kind)
     {
-    case K_CONST: return A.p.consts[idx];
+    case K_CONST: return A.consts[idx];
     case K_INPUT: return read_input(A, idx, r, c);
     case K_REDUCE: return A.rvec[idx][A.raxis[idx] ? c : r];
     default: return regs[idx];
     }
 }
 
-__device__ __forceinline__ float apply(unsigned char op, float a, float b, float c)
+__device__ __forceinline__ float apply(unsigned op, float a, float b, float c)
 {
     switch (op)
     {
@@ -118,13 +140,12 @@ __device__ __forceinline__ void run_prefix(const ExprArgs& A, unsigned upto, siz
 {
     for (unsigned j = 0; j < upto; ++j)
     {
-        const unsigned char* in = A.p.instrs[j];
-        const unsigned char op = in[0];
+        const unsigned op = ibyte(A, j, 0);
         if (is_reduce(op)) continue;
-        const float a = operand(A, in[2], in[3], r, c, regs);
-        const float b = (op >= E_ADD) ? operand(A, in[4], in[5], r, c, regs) : 0.0f;
-        const float cc = (op == E_SELECT) ? operand(A, in[6], in[7], r, c, regs) : 0.0f;
-        regs[in[1]] = apply(op, a, b, cc);
+        const float a = operand(A, ibyte(A, j, 2), ibyte(A, j, 3), r, c, regs);
+        const float b = (op >= E_ADD) ? operand(A, ibyte(A, j, 4), ibyte(A, j, 5), r, c, regs) : 0.0f;
+        const float cc = (op == E_SELECT) ? operand(A, ibyte(A, j, 6), ibyte(A, j, 7), r, c, regs) : 0.0f;
+        regs[ibyte(A, j, 1)] = apply(op, a, b, cc);
     }
 }
 
@@ -132,8 +153,7 @@ __device__ __forceinline__ float eval_reduce_source(const ExprArgs& A, unsigned 
 {
     float regs[16];
     run_prefix(A, ri, r, c, regs);
-    const unsigned char* in = A.p.instrs[ri];
-    return operand(A, in[2], in[3], r, c, regs);
+    return operand(A, ibyte(A, ri, 2), ibyte(A, ri, 3), r, c, regs);
 }
 
 // Row-axis reduce instruction ri: one wave per row.
@@ -184,8 +204,8 @@ __global__ __launch_bounds__(kThreads) void k_expr_merge_cols(const float* part,
 __global__ __launch_bounds__(kThreads) void k_expr_elementwise(ExprArgs A, float* out)
 {
     const size_t n = A.rows * A.cols;
-    const unsigned last = A.p.n_instrs - 1;
-    const unsigned char lop = A.p.instrs[last][0], ldst = A.p.instrs[last][1];
+    const unsigned last = A.n_instrs - 1;
+    const unsigned lop = ibyte(A, last, 0), ldst = ibyte(A, last, 1);
     const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
     for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
     {
@@ -196,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void k_expr_elementwise(ExprArgs A, float
             continue;
         }
         float regs[16];
-        run_prefix(A, A.p.n_instrs, r, c, regs);
+        run_prefix(A, A.n_instrs, r, c, regs);
         out[i] = regs[ldst];
     }
 }
@@ -206,8 +226,8 @@ __global__ __launch_bounds__(kThreads) void k_expr_vector(ExprArgs A, float* out
 {
     const size_t k = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
     if (k >= len) return;
-    const unsigned last = A.p.n_instrs - 1;
-    const unsigned char lop = A.p.instrs[last][0], ldst = A.p.instrs[last][1];
+    const unsigned last = A.n_instrs - 1;
+    const unsigned lop = ibyte(A, last, 0), ldst = ibyte(A, last, 1);
     if (is_reduce(lop))
     {
         out[k] = A.rvec[ldst][k];
@@ -215,7 +235,7 @@ __global__ __launch_bounds__(kThreads) void k_expr_vector(ExprArgs A, float* out
     }
     float regs[16];
     const size_t r = row_axis ? k : 0, c = row_axis ? 0 : k;
-    run_prefix(A, A.p.n_instrs, r, c, regs);
+    run_prefix(A, A.n_instrs, r, c, regs);
     out[k] = regs[ldst];
 }
 
@@ -311,10 +331,19 @@ extern "C" int nnhip_eval_expr(const nnhip_expr_program* prog, const float* cons
     float* ws = static_cast<float*>(workspace);
     ExprArgs A;
     std::memset(&A, 0, sizeof(A));
-    A.p = p;
+    for (unsigned j = 0; j < p.n_instrs; ++j)
+        for (unsigned b = 0; b < 8; ++b) A.instrs[j][b >> 2] |= static_cast<unsigned>(p.instrs[j][b]) << (8 * (b & 3));
+    for (unsigned q = 0; q < p.n_consts; ++q) A.consts[q] = p.consts[q];
+    A.n_instrs = p.n_instrs;
     A.rows = rows;
     A.cols = cols;
-    for (unsigned k = 0; k < p.n_views; ++k) A.in[k] = inputs[k];
+    for (unsigned k = 0; k < p.n_views; ++k)
+    {
+        A.view[k].in = inputs[k];
+        A.view[k].param = p.view_param[k];
+        A.view[k].kind = p.view_kind[k];
+        A.view[k].negate = p.view_negate[k];
+    }
 
     // 1. reduce views (an input that appears twice with the same view is reduced once).
     for (unsigned k = 0; k < p.n_views; ++k)
@@ -322,12 +351,12 @@ extern "C" int nnhip_eval_expr(const nnhip_expr_program* prog, const float* cons
         const unsigned char v = p.view_kind[k];
         if (v < V_COLSUM || v > V_ROWMAX) continue;
         float* dst = ws + L.view_off[k];
-        A.vred[k] = dst;
+        A.view[k].vred = dst;
         bool reused = false;
         for (unsigned q = 0; q < k; ++q)
             if (p.view_kind[q] == v && inputs[q] == inputs[k])
             {
-                A.vred[k] = A.vred[q];
+                A.view[k].vred = A.view[q].vred;
                 reused = true;
                 break;
             }

@@ -9,9 +9,11 @@
 //   * Linear: out = W (out,in) x X (in,N) + b (out,1);
 //   * attention heads: rearrange_3d(Q (H*dk, B*T), H*dk, B, T) -> (B*H*dk, T),
 //     so the batch index of every batched primitive is b*H + h.
-// Covered subset: Linear, SwiGLU, RMSNorm, Softmax, attention (two-pass fused
-// path for a pure causal mask, materialised path for ALiBi / document masks),
-// FeedForward, GPTBlock, learned / sinusoidal / no position encoders, GPTModel.
+// Covered: Linear, SwiGLU, QuickGeLU, RMSNorm, LayerNorm, Softmax, attention
+// (two-pass fused path for a pure causal mask, materialised path for ALiBi /
+// document masks, RoPE on Q / K), FeedForward, GPTBlock, learned / sinusoidal /
+// no position encoders, GPTModel, and incremental inference (forward_step with
+// per-layer KV caches, generate).
 #pragma once
 
 #include <cmath>
@@ -230,6 +232,120 @@ private:
     Tensor gamma_, grad_gamma_, normed_cache_, rms_inv_cache_;
 };
 
+// ── QuickGeLU (reference compute_layer.hpp:256-336), beta = 1.702 ─────────
+//   fwd: t1 = x*beta; t2 = -t1; t3 = exp(t2); t4 = t3 + 1; s = 1 / t4; out = x*s
+//   bwd: 1 - s; beta*x; (beta*x)*(1-s); + 1; s*(.); grad*(.)
+class GeLU final : public Layer
+{
+public:
+    static constexpr Scalar kBeta = 1.702f;
+    Result<Tensor> forward(ComputeEngine& engine, const Tensor& input) override
+    {
+        input_cache_ = input;
+        NN_TRY(t1, engine.elementwise_binary_scalar(BinaryOp::Mul, input, kBeta));
+        NN_TRY(t2, engine.elementwise_unary(UnaryOp::Neg, t1));
+        NN_TRY(t3, engine.elementwise_unary(UnaryOp::Exp, t2));
+        NN_TRY(t4, engine.elementwise_binary_scalar(BinaryOp::Add, t3, Scalar{1}));
+        NN_TRY(sg, engine.elementwise_binary_scalar(BinaryOp::Div, t4, Scalar{1}, true));
+        sigmoid_cache_ = sg;
+        return engine.elementwise_binary(BinaryOp::Mul, input, sigmoid_cache_);
+    }
+    Result<Tensor> backward(ComputeEngine& engine, const Tensor& grad_output) override
+    {
+        if (input_cache_.rows() != grad_output.rows() || input_cache_.cols() != grad_output.cols())
+            return fail("gelu backward: shape mismatch");
+        NN_TRY(one_minus_s, engine.elementwise_binary_scalar(BinaryOp::Sub, sigmoid_cache_, Scalar{1}, true));
+        NN_TRY(bx, engine.elementwise_binary_scalar(BinaryOp::Mul, input_cache_, kBeta));
+        NN_TRY(inner, engine.elementwise_binary(BinaryOp::Mul, bx, one_minus_s));
+        NN_TRY(paren, engine.elementwise_binary_scalar(BinaryOp::Add, inner, Scalar{1}));
+        NN_TRY(factor, engine.elementwise_binary(BinaryOp::Mul, sigmoid_cache_, paren));
+        return engine.elementwise_binary(BinaryOp::Mul, grad_output, factor);
+    }
+
+private:
+    Tensor input_cache_, sigmoid_cache_;
+};
+
+// ── LayerNorm (reference compute_layer.hpp:479-662), eps = 1e-5 ───────────
+//   fwd: mean = ColSum(x)*(1/F); diff = x - colbcast(mean); var = ColSum(diff^2)*(1/F);
+//        std_inv = rsqrt(var + eps); normed = diff*colbcast(std_inv);
+//        out = normed*rowbcast(gamma) + rowbcast(beta)
+//   bwd: mean_g = ColSum(g*gamma)/F; mean_gn = ColSum(g*gamma*normed)/F;
+//        dx = (g*gamma - mean_g - normed*mean_gn)*std_inv;
+//        dgamma += RowSum(g*gamma*normed) (gamma times the true gradient, as the
+//        reference accumulates it); dbeta += RowSum(g)
+class LayerNorm final : public Layer
+{
+public:
+    explicit LayerNorm(ComputeEngine& engine, std::size_t features, Scalar epsilon = Scalar{1e-5f})
+        : features_(features), epsilon_(epsilon)
+    {
+        gamma_ = layer_take_(engine.from_matrix(Matrix(features, 1, Scalar{1})));
+        beta_ = layer_take_(engine.from_matrix(Matrix(features, 1, Scalar{0})));
+        grad_gamma_ = engine.create_tensor(features, 1);
+        grad_beta_ = engine.create_tensor(features, 1);
+        layer_take_(engine.zero(grad_gamma_));
+        layer_take_(engine.zero(grad_beta_));
+    }
+
+    std::vector<TensorRef> parameters() override { return {gamma_, beta_}; }
+    std::vector<TensorRef> param_gradients() override { return {grad_gamma_, grad_beta_}; }
+
+    Result<Tensor> forward(ComputeEngine& engine, const Tensor& input) override
+    {
+        if (input.rows() != features_)
+            return fail("layernorm forward: input shape mismatch");
+        const Scalar inv_f = Scalar{1} / static_cast<Scalar>(features_);
+        const std::size_t F = features_, N = input.cols();
+        NN_TRY(mean_raw, dsl::compute_reduce(engine, layer_exprs::ln_col_sum(input), F, N));
+        NN_TRY(mean, engine.elementwise_binary_scalar(BinaryOp::Mul, mean_raw, inv_f));
+        NN_TRY(diff, dsl::compute(engine, layer_exprs::ln_center(input, mean), F, N));
+        NN_TRY(var_raw, dsl::compute_reduce(engine, layer_exprs::ln_sum_sq(diff), F, N));
+        NN_TRY(var, engine.elementwise_binary_scalar(BinaryOp::Mul, var_raw, inv_f));
+        NN_TRY(var_eps, engine.elementwise_binary_scalar(BinaryOp::Add, var, epsilon_));
+        NN_TRY(std_inv, engine.elementwise_unary(UnaryOp::Rsqrt, var_eps));
+        std_cache_ = std_inv;
+        NN_TRY(normed, dsl::compute(engine, layer_exprs::ln_normalize(diff, std_cache_), F, N));
+        normed_cache_ = normed;
+        return dsl::compute(engine, layer_exprs::ln_affine(normed_cache_, gamma_, beta_), F, N);
+    }
+
+    Result<Tensor> backward(ComputeEngine& engine, const Tensor& grad_output) override
+    {
+        const Scalar inv_f = Scalar{1} / static_cast<Scalar>(features_);
+        const std::size_t F = features_, N = grad_output.cols();
+        NN_TRY(mg_raw, dsl::compute_reduce(engine, layer_exprs::ln_bwd_colsum_g(grad_output, gamma_), F, N));
+        NN_TRY(mean_g, engine.elementwise_binary_scalar(BinaryOp::Mul, mg_raw, inv_f));
+        NN_TRY(mgn_raw, dsl::compute_reduce(engine, layer_exprs::ln_bwd_colsum_gn(grad_output, gamma_, normed_cache_),
+                                            F, N));
+        NN_TRY(mean_gn, engine.elementwise_binary_scalar(BinaryOp::Mul, mgn_raw, inv_f));
+        NN_TRY(grad_x, dsl::compute(engine,
+                                    layer_exprs::ln_bwd_dx(grad_output, gamma_, mean_g, normed_cache_, mean_gn,
+                                                           std_cache_),
+                                    F, N));
+        NN_TRY(gg, dsl::compute_reduce(engine, layer_exprs::ln_bwd_rowsum_gn(grad_output, gamma_, normed_cache_), F,
+                                       N));
+        NN_CHECK(engine.add_inplace(grad_gamma_, gg));
+        NN_TRY(gb, dsl::compute_reduce(engine, layer_exprs::ln_bwd_rowsum(grad_output), F, N));
+        NN_CHECK(engine.add_inplace(grad_beta_, gb));
+        return grad_x;
+    }
+
+private:
+    std::size_t features_;
+    Scalar epsilon_;
+    Tensor gamma_, beta_, grad_gamma_, grad_beta_, normed_cache_, std_cache_;
+};
+
+// Reference compute_layer.hpp:804-810.
+[[nodiscard]] inline std::unique_ptr<Layer> make_norm_layer(ComputeEngine& engine, std::size_t d_model,
+                                                            NormType norm_type)
+{
+    if (norm_type == NormType::RMSNorm)
+        return std::make_unique<RMSNorm>(engine, d_model);
+    return std::make_unique<LayerNorm>(engine, d_model);
+}
+
 // ── Softmax over rows (reference compute_layer.hpp:824-863) ───────────────
 //   fwd: exp(x - rowmax(x)) / RowSum(exp(x - rowmax(x)))
 //   bwd: out * (g - RowSum(out * g))
@@ -252,15 +368,85 @@ private:
     Tensor output_cache_;
 };
 
+// ── RotaryEmbedding (reference compute_layer.hpp:884-984) ─────────────────
+// Half-swap convention: q_rot = q*cos + rotate_half(q)*sin, rotate_half(x) =
+// [-x_second_half, x_first_half] per d_k block; cos[j] = cos[j + d_k/2] =
+// cos(pos * theta_j), theta_j = 10000^(-2j/d_k). The tables are (d_k, seq) and
+// read with RowMod(d_k) by the (B*H*d_k, seq) heads; backward rotates by the
+// opposite angle (the rotation is orthogonal).
+class RotaryEmbedding
+{
+public:
+    RotaryEmbedding() = default;
+    explicit RotaryEmbedding(std::size_t d_k) : d_k_(d_k) {}
+
+    Result<Tensor> apply(ComputeEngine& engine, const Tensor& q, std::size_t seq, bool backward)
+    {
+        if (d_k_ == 0 || d_k_ % 2 != 0)
+            return fail("RotaryEmbedding::apply: d_k must be positive and even");
+        if (seq != seq_cached_)
+        {
+            Matrix c(d_k_, seq), sn(d_k_, seq);
+            for (std::size_t pos = 0; pos < seq; ++pos)
+                fill_column_(c, sn, pos, pos);
+            NN_TRY(ct, engine.from_matrix(c));
+            NN_TRY(st, engine.from_matrix(sn));
+            cos_ = ct;
+            sin_ = st;
+            seq_cached_ = seq;
+        }
+        return rotate_(engine, q, cos_, sin_, backward);
+    }
+
+    // One position (incremental inference): q is (H*d_k, 1).
+    Result<Tensor> apply_step(ComputeEngine& engine, const Tensor& q, std::size_t pos, bool backward)
+    {
+        if (d_k_ == 0 || d_k_ % 2 != 0)
+            return fail("RotaryEmbedding::apply_step: d_k must be positive and even");
+        Matrix c(d_k_, 1), sn(d_k_, 1);
+        fill_column_(c, sn, pos, 0);
+        NN_TRY(ct, engine.from_matrix(c));
+        NN_TRY(st, engine.from_matrix(sn));
+        return rotate_(engine, q, ct, st, backward);
+    }
+
+private:
+    void fill_column_(Matrix& c, Matrix& sn, std::size_t pos, std::size_t col) const
+    {
+        const std::size_t half = d_k_ / 2;
+        for (std::size_t j = 0; j < half; ++j)
+        {
+            const Scalar theta = static_cast<Scalar>(pos) /
+                                 std::pow(Scalar{10000}, static_cast<Scalar>(2 * j) / static_cast<Scalar>(d_k_));
+            const Scalar cv = std::cos(theta), sv = std::sin(theta);
+            c.set_value_unchecked(j, col, cv);
+            c.set_value_unchecked(half + j, col, cv);
+            sn.set_value_unchecked(j, col, sv);
+            sn.set_value_unchecked(half + j, col, sv);
+        }
+    }
+    Result<Tensor> rotate_(ComputeEngine& engine, const Tensor& q, const Tensor& c, const Tensor& sn, bool backward)
+    {
+        const auto dk = static_cast<std::uint32_t>(d_k_);
+        if (backward)
+            return dsl::compute(engine, layer_exprs::rope_backward(q, c, sn, dk), q.rows(), q.cols());
+        return dsl::compute(engine, layer_exprs::rope_forward(q, c, sn, dk), q.rows(), q.cols());
+    }
+
+    std::size_t d_k_ = 0, seq_cached_ = 0;
+    Tensor cos_, sin_;
+};
+
 // ── multi-head attention core (reference compute_layer.hpp:1016-1412) ─────
 class AttentionBase : public Layer
 {
 public:
-    AttentionBase(ComputeEngine& engine, std::size_t d_model, std::size_t num_heads, std::size_t seq_len)
+    AttentionBase(ComputeEngine& engine, std::size_t d_model, std::size_t num_heads, std::size_t seq_len,
+                  PosEncodingType pos_enc = PosEncodingType::Learned)
         : d_model_(d_model), num_heads_(num_heads), d_k_(d_model / num_heads), seq_len_(seq_len),
           scale_(Scalar{1} / std::sqrt(static_cast<Scalar>(d_model / num_heads))),
           w_q_(engine, d_model, d_model), w_k_(engine, d_model, d_model), w_v_(engine, d_model, d_model),
-          w_o_(engine, d_model, d_model)
+          w_o_(engine, d_model, d_model), use_rope_(pos_enc == PosEncodingType::RoPE), rope_(d_model / num_heads)
     {
     }
 
@@ -306,6 +492,13 @@ public:
             Q_ = q;
             K_ = k;
             V_ = v;
+        }
+        if (use_rope_)   // reference :1176-1186, on the (B*H*d_k, seq) heads
+        {
+            NN_TRY(qr2, rope_.apply(engine, Q_, seq, false));
+            Q_ = qr2;
+            NN_TRY(kr2, rope_.apply(engine, K_, seq, false));
+            K_ = kr2;
         }
 
         NN_TRY(tpm, two_pass_mask_(engine, batch, seq));
@@ -390,6 +583,13 @@ public:
             gQ = gq;
             gK = gk;
         }
+        if (use_rope_)   // reference :1363-1372: the inverse rotation of the Q / K gradients
+        {
+            NN_TRY(gq2, rope_.apply(engine, gQ, seq, true));
+            gQ = gq2;
+            NN_TRY(gk2, rope_.apply(engine, gK, seq, true));
+            gK = gk2;
+        }
 
         if (batch > 1)
         {
@@ -409,12 +609,50 @@ public:
         return dx;
     }
 
+    // Incremental inference, one token (reference compute_layer.hpp:1426-1511):
+    // x_new (d_model, 1); the caches are (seq_len, d_model) with rows [0, cur_len)
+    // holding the earlier tokens' K / V. Writes row cur_len, attends over rows
+    // [0, cur_len] (no causal mask needed: the cache holds only earlier tokens).
+    Result<Tensor> forward_step(ComputeEngine& engine, const Tensor& x_new, Tensor& k_cache, Tensor& v_cache,
+                                std::size_t cur_len)
+    {
+        if (x_new.rows() != d_model_ || x_new.cols() != 1)
+            return fail("AttentionBase forward_step: x_new must be (d_model, 1)");
+        NN_TRY(q0, w_q_.forward(engine, x_new));
+        NN_TRY(k0, w_k_.forward(engine, x_new));
+        NN_TRY(v_new, w_v_.forward(engine, x_new));
+        Tensor q = q0, k_new = k0;
+        if (use_rope_)
+        {
+            NN_TRY(qr, rope_.apply_step(engine, q, cur_len, false));
+            q = qr;
+            NN_TRY(kr, rope_.apply_step(engine, k_new, cur_len, false));
+            k_new = kr;
+        }
+        NN_TRY(k_new_T, engine.transpose(k_new));   // (1, H*d_k), the cache's row layout
+        NN_TRY(v_new_T, engine.transpose(v_new));
+        NN_CHECK(engine.insert_rows(k_cache, cur_len, k_new_T));
+        NN_CHECK(engine.insert_rows(v_cache, cur_len, v_new_T));
+        const std::size_t new_len = cur_len + 1;
+        NN_TRY(k_valid, engine.slice_rows(k_cache, 0, new_len));
+        NN_TRY(v_valid, engine.slice_rows(v_cache, 0, new_len));
+        NN_TRY(K_T, engine.transpose(k_valid));     // (H*d_k, new_len)
+        NN_TRY(V_T, engine.transpose(v_valid));
+        NN_TRY(scores, engine.batched_matmul(q, K_T, num_heads_, true, false, scale_));   // (H, new_len)
+        NN_TRY(masked, apply_mask_step_(engine, std::move(scores), cur_len));
+        NN_TRY(attn, softmax_.forward(engine, masked));
+        NN_TRY(attn_out, engine.batched_matmul(V_T, attn, num_heads_, false, true));   // (H*d_k, 1)
+        return w_o_.forward(engine, attn_out);
+    }
+
 protected:
     struct TwoPassMask
     {
         bool use_two_pass = true;
         Tensor mask;
     };
+    // Incremental-inference mask hook (reference :1076-1081): none by default.
+    virtual Result<Tensor> apply_mask_step_(ComputeEngine&, Tensor&& scores, std::size_t) { return std::move(scores); }
     virtual Result<TwoPassMask> two_pass_mask_(ComputeEngine&, std::size_t, std::size_t)
     {
         return TwoPassMask{true, {}};
@@ -432,6 +670,8 @@ protected:
     Tensor attn_;                // (BH*seq, seq), materialised path
     Tensor m_, l_, shared_mask_; // two-pass path
     bool two_pass_ = false;
+    bool use_rope_ = false;
+    RotaryEmbedding rope_;
 };
 
 // ── build_attention_mask (reference compute_layer.hpp:2081-2128) ──────────
@@ -481,7 +721,7 @@ class CausalSelfAttention final : public AttentionBase
 public:
     CausalSelfAttention(ComputeEngine& engine, std::size_t d_model, std::size_t num_heads, std::size_t seq_len,
                         PosEncodingType pos_enc)
-        : AttentionBase(engine, d_model, num_heads, seq_len), use_alibi_(pos_enc == PosEncodingType::ALiBi)
+        : AttentionBase(engine, d_model, num_heads, seq_len, pos_enc), use_alibi_(pos_enc == PosEncodingType::ALiBi)
     {
         if (use_alibi_)
             slopes_ = alibi_slopes(num_heads);
@@ -506,6 +746,20 @@ protected:
             mask_seq_ = seq;
         }
         return engine.elementwise_binary(BinaryOp::Add, scores, mask_);
+    }
+
+    // ALiBi at inference (reference :2267-2290): scores (H, cur_len + 1) +=
+    // -slope_h * (cur_len - j), the query at position cur_len.
+    Result<Tensor> apply_mask_step_(ComputeEngine& engine, Tensor&& scores, std::size_t cur_len) override
+    {
+        if (!use_alibi_) return std::move(scores);
+        const std::size_t new_len = cur_len + 1;
+        Matrix bias(num_heads_, new_len);
+        for (std::size_t h = 0; h < num_heads_; ++h)
+            for (std::size_t j = 0; j < new_len; ++j)
+                bias.set_value_unchecked(h, j, -slopes_[h] * static_cast<Scalar>(cur_len - j));
+        NN_TRY(bt, engine.from_matrix(bias));
+        return engine.elementwise_binary(BinaryOp::Add, scores, bt);
     }
 
     Result<TwoPassMask> two_pass_mask_(ComputeEngine& engine, std::size_t, std::size_t seq) override
@@ -536,11 +790,14 @@ private:
 };
 
 // ── FeedForward with SwiGLU (reference compute_layer.hpp:1623-1689) ───────
+// QuickGeLU FFN: fc1 d_model -> d_ff; SwiGLU FFN: fc1 d_model -> 2*d_ff.
 class FeedForward final : public Layer
 {
 public:
-    FeedForward(ComputeEngine& engine, std::size_t d_model, std::size_t d_ff)
-        : fc1_(engine, d_model, 2 * d_ff), fc2_(engine, d_ff, d_model), act_(d_ff)
+    FeedForward(ComputeEngine& engine, std::size_t d_model, std::size_t d_ff,
+                ActivationType activation = ActivationType::SwiGLU)
+        : fc1_(engine, d_model, activation == ActivationType::SwiGLU ? 2 * d_ff : d_ff), fc2_(engine, d_ff, d_model),
+          act_(d_ff), use_swiglu_(activation == ActivationType::SwiGLU)
     {
     }
     std::vector<TensorRef> parameters() override
@@ -558,19 +815,41 @@ public:
     Result<Tensor> forward(ComputeEngine& engine, const Tensor& input) override
     {
         NN_TRY(h1, fc1_.forward(engine, input));
-        NN_TRY(h2, act_.forward(engine, h1));
+        Tensor h2;
+        if (use_swiglu_)
+        {
+            NN_TRY(a, act_.forward(engine, h1));
+            h2 = a;
+        }
+        else
+        {
+            NN_TRY(a, gelu_.forward(engine, h1));
+            h2 = a;
+        }
         return fc2_.forward(engine, h2);
     }
     Result<Tensor> backward(ComputeEngine& engine, const Tensor& grad_output) override
     {
         NN_TRY(b2, fc2_.backward(engine, grad_output));
-        NN_TRY(bg, act_.backward(engine, b2));
+        Tensor bg;
+        if (use_swiglu_)
+        {
+            NN_TRY(g, act_.backward(engine, b2));
+            bg = g;
+        }
+        else
+        {
+            NN_TRY(g, gelu_.backward(engine, b2));
+            bg = g;
+        }
         return fc1_.backward(engine, bg);
     }
 
 private:
     Linear fc1_, fc2_;
     SwiGLU act_;
+    GeLU gelu_;
+    bool use_swiglu_;
 };
 
 // ── GPTBlock, pre-norm (reference compute_layer.hpp:2313-2405) ────────────
@@ -579,51 +858,64 @@ class GPTBlock final : public Layer
 {
 public:
     GPTBlock(ComputeEngine& engine, std::size_t d_model, std::size_t heads, std::size_t d_ff, std::size_t seq_len,
-             PosEncodingType pos_enc)
-        : attn_(engine, d_model, heads, seq_len, pos_enc), norm1_(engine, d_model), ff_(engine, d_model, d_ff),
-          norm2_(engine, d_model)
+             PosEncodingType pos_enc, ActivationType activation = ActivationType::SwiGLU,
+             NormType norm_type = NormType::RMSNorm)
+        : attn_(engine, d_model, heads, seq_len, pos_enc), norm1_(make_norm_layer(engine, d_model, norm_type)),
+          ff_(engine, d_model, d_ff, activation), norm2_(make_norm_layer(engine, d_model, norm_type))
     {
     }
     std::vector<TensorRef> parameters() override
     {
         std::vector<TensorRef> p;
-        append_refs_(p, attn_.parameters(), norm1_.parameters(), ff_.parameters(), norm2_.parameters());
+        append_refs_(p, attn_.parameters(), norm1_->parameters(), ff_.parameters(), norm2_->parameters());
         return p;
     }
     std::vector<TensorRef> param_gradients() override
     {
         std::vector<TensorRef> g;
-        append_refs_(g, attn_.param_gradients(), norm1_.param_gradients(), ff_.param_gradients(),
-                     norm2_.param_gradients());
+        append_refs_(g, attn_.param_gradients(), norm1_->param_gradients(), ff_.param_gradients(),
+                     norm2_->param_gradients());
         return g;
     }
     void set_doc_ids(std::span<const std::size_t> ids) override { attn_.set_doc_ids(ids); }
 
     Result<Tensor> forward(ComputeEngine& engine, const Tensor& input) override
     {
-        NN_TRY(n1, norm1_.forward(engine, input));
+        NN_TRY(n1, norm1_->forward(engine, input));
         NN_TRY(a, attn_.forward(engine, n1));
         NN_TRY(r2, engine.elementwise_binary(BinaryOp::Add, input, a));
         residual_ = r2;
-        NN_TRY(n2, norm2_.forward(engine, residual_));
+        NN_TRY(n2, norm2_->forward(engine, residual_));
         NN_TRY(f, ff_.forward(engine, n2));
         return engine.elementwise_binary(BinaryOp::Add, residual_, f);
     }
     Result<Tensor> backward(ComputeEngine& engine, const Tensor& grad_output) override
     {
         NN_TRY(gff, ff_.backward(engine, grad_output));
-        NN_TRY(gn2, norm2_.backward(engine, gff));
+        NN_TRY(gn2, norm2_->backward(engine, gff));
         NN_TRY(gr1, engine.elementwise_binary(BinaryOp::Add, grad_output, gn2));
         NN_TRY(gsa, attn_.backward(engine, gr1));
-        NN_TRY(gn1, norm1_.backward(engine, gsa));
+        NN_TRY(gn1, norm1_->backward(engine, gsa));
         return engine.elementwise_binary(BinaryOp::Add, gr1, gn1);
+    }
+
+    // One token through the block with the layer's KV cache (reference :2413-2437).
+    Result<Tensor> forward_step(ComputeEngine& engine, const Tensor& x_new, Tensor& k_cache, Tensor& v_cache,
+                                std::size_t cur_len)
+    {
+        NN_TRY(n1, norm1_->forward(engine, x_new));
+        NN_TRY(a, attn_.forward_step(engine, n1, k_cache, v_cache, cur_len));
+        NN_TRY(r2, engine.elementwise_binary(BinaryOp::Add, x_new, a));
+        NN_TRY(n2, norm2_->forward(engine, r2));
+        NN_TRY(f, ff_.forward(engine, n2));
+        return engine.elementwise_binary(BinaryOp::Add, r2, f);
     }
 
 private:
     CausalSelfAttention attn_;
-    RMSNorm norm1_;
+    std::unique_ptr<Layer> norm1_;
     FeedForward ff_;
-    RMSNorm norm2_;
+    std::unique_ptr<Layer> norm2_;
     Tensor residual_;
 };
 
@@ -633,6 +925,8 @@ class PositionEncoder
 public:
     virtual ~PositionEncoder() = default;
     virtual Result<Tensor> apply(ComputeEngine& engine, const Tensor& emb_T, std::size_t batch, std::size_t seq) = 0;
+    // One position at inference (reference :2467-2468): x (d_model, 1).
+    virtual Result<Tensor> apply_step(ComputeEngine& engine, const Tensor& x, std::size_t pos) = 0;
     virtual Result<void> backward(ComputeEngine& engine, const Tensor& grad_T) = 0;
     virtual std::vector<TensorRef> parameters() { return {}; }
     virtual std::vector<TensorRef> param_gradients() { return {}; }
@@ -670,6 +964,14 @@ public:
         NN_TRY(gT, engine.transpose(g));
         return engine.elementwise_binary(BinaryOp::Add, emb_T, gT);
     }
+    // Reference :2550-2565: x + transpose(gather_rows(table, [pos])).
+    Result<Tensor> apply_step(ComputeEngine& engine, const Tensor& x, std::size_t pos) override
+    {
+        NN_TRY(pt, engine.from_matrix(Matrix(1, 1, static_cast<Scalar>(pos))));
+        NN_TRY(g, engine.gather_rows(table_, pt));
+        NN_TRY(gT, engine.transpose(g));
+        return engine.elementwise_binary(BinaryOp::Add, x, gT);
+    }
     Result<void> backward(ComputeEngine& engine, const Tensor& grad_T) override
     {
         if (!learnable_)
@@ -697,6 +999,7 @@ class NoPositionEncoder final : public PositionEncoder
 {
 public:
     Result<Tensor> apply(ComputeEngine&, const Tensor& emb_T, std::size_t, std::size_t) override { return emb_T; }
+    Result<Tensor> apply_step(ComputeEngine&, const Tensor& x, std::size_t) override { return x; }
     Result<void> backward(ComputeEngine&, const Tensor&) override { return {}; }
 };
 
@@ -722,8 +1025,9 @@ class GPTModel final : public Layer
 {
 public:
     GPTModel(ComputeEngine& engine, std::size_t vocab, std::size_t d_model, std::size_t seq_len, std::size_t heads,
-             std::size_t d_ff, std::size_t layers, PosEncodingType pos_enc)
-        : vocab_(vocab), seq_len_(seq_len), ln_f_(engine, d_model),
+             std::size_t d_ff, std::size_t layers, PosEncodingType pos_enc,
+             ActivationType activation = ActivationType::SwiGLU, NormType norm_type = NormType::RMSNorm)
+        : vocab_(vocab), d_model_(d_model), seq_len_(seq_len), ln_f_(make_norm_layer(engine, d_model, norm_type)),
           lm_head_(engine, d_model, vocab)
     {
         // Embeddings ~ N(0, 0.02) from mt19937_64{42}, as the reference; the
@@ -749,7 +1053,8 @@ public:
             pos_ = std::make_unique<NoPositionEncoder>();
         blocks_.reserve(layers);
         for (std::size_t i = 0; i < layers; ++i)
-            blocks_.push_back(std::make_unique<GPTBlock>(engine, d_model, heads, d_ff, seq_len, pos_enc));
+            blocks_.push_back(
+                std::make_unique<GPTBlock>(engine, d_model, heads, d_ff, seq_len, pos_enc, activation, norm_type));
     }
 
     std::vector<TensorRef> parameters() override
@@ -758,7 +1063,7 @@ public:
         append_refs_(p, pos_->parameters());
         for (auto& b : blocks_)
             append_refs_(p, b->parameters());
-        append_refs_(p, ln_f_.parameters(), lm_head_.parameters());
+        append_refs_(p, ln_f_->parameters(), lm_head_.parameters());
         return p;
     }
     std::vector<TensorRef> param_gradients() override
@@ -767,7 +1072,7 @@ public:
         append_refs_(g, pos_->param_gradients());
         for (auto& b : blocks_)
             append_refs_(g, b->param_gradients());
-        append_refs_(g, ln_f_.param_gradients(), lm_head_.param_gradients());
+        append_refs_(g, ln_f_->param_gradients(), lm_head_.param_gradients());
         return g;
     }
     void set_doc_ids(std::span<const std::size_t> ids) override { doc_ids_.assign(ids.begin(), ids.end()); }
@@ -792,14 +1097,14 @@ public:
             if (flush_interval_ > 0 && (bi + 1) % flush_interval_ == 0 && bi + 1 < blocks_.size())
                 NN_CHECK(engine.flush_batch());
         }
-        NN_TRY(xn, ln_f_.forward(engine, x));
+        NN_TRY(xn, ln_f_->forward(engine, x));
         return lm_head_.forward(engine, xn);
     }
 
     Result<Tensor> backward(ComputeEngine& engine, const Tensor& grad_output) override
     {
         NN_TRY(g0, lm_head_.backward(engine, grad_output));
-        NN_TRY(g1, ln_f_.backward(engine, g0));
+        NN_TRY(g1, ln_f_->backward(engine, g0));
         Tensor g = g1;
         const std::size_t n = blocks_.size();
         for (std::size_t bi = 0; bi < n; ++bi)
@@ -816,13 +1121,141 @@ public:
     }
 
     [[nodiscard]] std::size_t vocab_size() const noexcept { return vocab_; }
+    [[nodiscard]] std::size_t num_blocks() const noexcept { return blocks_.size(); }
+    [[nodiscard]] std::size_t seq_len() const noexcept { return seq_len_; }
+    [[nodiscard]] std::size_t d_model() const noexcept { return d_model_; }
+
+    // One token with per-layer KV caches (reference compute_layer.hpp:2906-2950):
+    // token_emb[token] (gather + transpose), the position at `pos`, every block's
+    // forward_step, the final norm and the LM head. Returns logits (vocab, 1).
+    Result<Tensor> forward_step(ComputeEngine& engine, std::size_t token_id, std::size_t pos,
+                                std::vector<Tensor>& k_caches, std::vector<Tensor>& v_caches, std::size_t cur_len)
+    {
+        if (k_caches.size() != blocks_.size() || v_caches.size() != blocks_.size())
+            return fail("GPTModel forward_step: one K and one V cache per block required");
+        if (cur_len >= seq_len_)
+            return fail("GPTModel forward_step: cur_len must be below seq_len (the caches' rows)");
+        NN_TRY(id_t, engine.from_matrix(Matrix(1, 1, static_cast<Scalar>(token_id))));
+        NN_TRY(emb, engine.gather_rows(token_emb_, id_t));
+        NN_TRY(x0, engine.transpose(emb));
+        NN_TRY(xp, pos_->apply_step(engine, x0, pos));
+        Tensor x = xp;
+        for (std::size_t i = 0; i < blocks_.size(); ++i)
+        {
+            NN_TRY(y, blocks_[i]->forward_step(engine, x, k_caches[i], v_caches[i], cur_len));
+            x = y;
+            if (flush_interval_ > 0 && (i + 1) % flush_interval_ == 0 && i + 1 < blocks_.size())
+                NN_CHECK(engine.flush_batch());
+        }
+        NN_TRY(ln, ln_f_->forward(engine, x));
+        return lm_head_.forward(engine, ln);
+    }
+
+    // Sampling with KV caches (reference compute_layer.hpp:2963-3096): the
+    // caches are (seq_len, d_model) per block; the prompt (its last seq_len
+    // tokens) fills them token by token; each new token is drawn from the last
+    // logits (temperature scaling, softmax, inverse-CDF draw from one uniform;
+    // temperature 0 = argmax) and fed back; when the caches are full they are
+    // zeroed and refilled with the last seq_len - 1 tokens (sliding window).
+    // Generation stops after max_new_tokens, or at eos once min_new_tokens are
+    // out (eos itself is not returned). The reference seeds its generator from
+    // std::random_device; here the caller passes the seed of the same
+    // std::mt19937_64 / uniform_real_distribution draw.
+    Result<std::vector<std::size_t>> generate(ComputeEngine& engine, const std::vector<std::size_t>& prompt,
+                                              std::size_t max_new_tokens, Scalar temperature,
+                                              std::size_t eos_token_id, std::size_t min_new_tokens,
+                                              std::uint64_t seed)
+    {
+        if (prompt.empty()) return fail("GPTModel generate: empty prompt");
+        std::vector<std::size_t> context(prompt), generated;
+        std::mt19937_64 rng{seed};
+        std::uniform_real_distribution<Scalar> dist(Scalar{0}, Scalar{1});
+        std::vector<Tensor> kc, vc;
+        for (std::size_t i = 0; i < blocks_.size(); ++i)
+        {
+            kc.push_back(engine.create_tensor(seq_len_, d_model_));
+            vc.push_back(engine.create_tensor(seq_len_, d_model_));
+        }
+        std::size_t cur_len = 0;
+        Tensor last;
+        auto fill = [&](std::size_t start) -> Result<void> {
+            for (std::size_t i = start; i < context.size(); ++i)
+            {
+                NN_TRY(r, forward_step(engine, context[i], cur_len, kc, vc, cur_len));
+                last = r;
+                ++cur_len;
+            }
+            return {};
+        };
+        NN_CHECK(fill(context.size() > seq_len_ ? context.size() - seq_len_ : 0));
+        for (std::size_t step = 0; step < max_new_tokens; ++step)
+        {
+            if (cur_len >= seq_len_)
+            {
+                for (auto& t : kc) NN_CHECK(engine.zero(t));
+                for (auto& t : vc) NN_CHECK(engine.zero(t));
+                cur_len = 0;
+                const std::size_t keep = seq_len_ - 1;
+                NN_CHECK(fill(context.size() > keep ? context.size() - keep : 0));
+            }
+            NN_TRY(lm, engine.to_matrix(last));
+            std::vector<Scalar> p(vocab_);
+            for (std::size_t v = 0; v < vocab_; ++v) p[v] = lm.at(v, 0);
+            if (temperature > 0 && temperature != Scalar{1})
+                for (auto& v : p) v /= temperature;
+            Scalar mx = p[0];
+            for (std::size_t v = 1; v < vocab_; ++v) mx = std::max(mx, p[v]);
+            Scalar sum = 0;
+            for (auto& v : p)
+            {
+                v = std::exp(v - mx);
+                sum += v;
+            }
+            for (auto& v : p) v /= sum;
+            std::size_t next = 0;
+            if (temperature > 0)
+            {
+                const Scalar r = dist(rng);
+                Scalar cum = 0;
+                next = vocab_ - 1;
+                for (std::size_t v = 0; v < vocab_; ++v)
+                {
+                    cum += p[v];
+                    if (r <= cum)
+                    {
+                        next = v;
+                        break;
+                    }
+                }
+            }
+            else
+            {
+                Scalar best = p[0];
+                for (std::size_t v = 1; v < vocab_; ++v)
+                    if (p[v] > best)
+                    {
+                        best = p[v];
+                        next = v;
+                    }
+            }
+            context.push_back(next);
+            if (step >= min_new_tokens && next == eos_token_id) break;
+            generated.push_back(next);
+            NN_CHECK(engine.begin_batch());
+            NN_TRY(r, forward_step(engine, next, cur_len, kc, vc, cur_len));
+            NN_CHECK(engine.end_batch());
+            last = r;
+            ++cur_len;
+        }
+        return generated;
+    }
 
 private:
-    std::size_t vocab_, seq_len_;
+    std::size_t vocab_, d_model_, seq_len_;
     Tensor token_emb_, grad_token_emb_, tokens_;
     std::unique_ptr<PositionEncoder> pos_;
     std::vector<std::unique_ptr<GPTBlock>> blocks_;
-    RMSNorm ln_f_;
+    std::unique_ptr<Layer> ln_f_;
     Linear lm_head_;
     std::size_t batch_ = 0;
     std::vector<std::size_t> doc_ids_;

@@ -4,6 +4,7 @@
 #pragma once
 
 #include <cstring>
+#include <iterator>
 #include <memory>
 #include <string>
 #include <vector>
@@ -229,7 +230,12 @@ struct GptConfigC
     std::size_t vocab_size, d_model, seq_len, num_heads, d_ff, num_layers;
     std::uint32_t pos_enc;
     float lr, beta1, beta2, eps, weight_decay;
+    std::uint32_t activation, norm_type, optimizer;
 };
+
+// Optimizer codes of GptConfigC::optimizer, the names create_optimizer takes
+// (reference compute_optimizer.hpp:594-615).
+constexpr const char* kOptimizerNames[] = {"adamw", "adam", "sgd", "sgd_momentum", "muon"};
 
 // One training session: GPTModel + CrossEntropyLoss + AdamW on one engine,
 // issuing the reference train-step sequence (src/text_train.cpp:1181-1330):
@@ -240,13 +246,30 @@ struct GptSession
     ComputeEngine* eng = nullptr;
     Model model;
     std::vector<TensorRef> params, grads;
-    std::unique_ptr<AdamW> opt;
+    std::unique_ptr<Optimizer> opt;
+    std::vector<Tensor> k_cache, v_cache;   // incremental inference, one pair per block
     CrossEntropyLoss ce;
     std::size_t vocab = 0, seq = 0, batch = 0, num_valid = 0;
     Tensor tokens, labels, mask, logits;
     bool has_batch = false, has_mask = false;
     GptConfigC cfg{};
 };
+
+// The session's optimizer over its parameters: AdamW with the session's
+// betas / eps / weight decay, else create_optimizer by name with lr (and the
+// weight decay), as text_train creates it (text_train.cpp:966-969).
+inline Result<std::unique_ptr<Optimizer>> make_optimizer(ComputeEngine& eng, const GptConfigC& c,
+                                                         std::vector<TensorRef> params, std::vector<TensorRef> grads)
+{
+    if (c.optimizer == 0)
+        return std::unique_ptr<Optimizer>(std::make_unique<AdamW>(eng, std::move(params), std::move(grads), c.lr,
+                                                                  c.beta1, c.beta2, c.eps, c.weight_decay));
+    if (c.optimizer >= std::size(kOptimizerNames)) return fail("gpt: unknown optimizer code");
+    auto o = create_optimizer(kOptimizerNames[c.optimizer], eng, std::move(params), std::move(grads), c.lr,
+                              c.weight_decay);
+    if (!o) return fail("gpt: unknown optimizer");
+    return o;
+}
 
 inline int gpt_create(EngineHandle* e, const GptConfigC* c, GptSession** out)
 {
@@ -258,6 +281,8 @@ inline int gpt_create(EngineHandle* e, const GptConfigC* c, GptSession** out)
     cfg.d_ff = c->d_ff;
     cfg.num_layers = c->num_layers;
     cfg.pos_enc = static_cast<PosEncodingType>(c->pos_enc);
+    cfg.activation = static_cast<ActivationType>(c->activation);
+    cfg.norm_type = static_cast<NormType>(c->norm_type);
     auto m = build_gpt_model(*e->eng, cfg);
     if (!m) return set_error(m.error().message);
     auto s = std::make_unique<GptSession>();
@@ -265,7 +290,9 @@ inline int gpt_create(EngineHandle* e, const GptConfigC* c, GptSession** out)
     s->model = std::move(*m);
     s->params = s->model.parameters();
     s->grads = s->model.param_gradients();
-    s->opt = std::make_unique<AdamW>(*s->eng, s->params, s->grads, c->lr, c->beta1, c->beta2, c->eps, c->weight_decay);
+    auto o = make_optimizer(*s->eng, *c, s->params, s->grads);
+    if (!o) return set_error(o.error().message);
+    s->opt = std::move(*o);
     s->vocab = c->vocab_size;
     s->cfg = *c;
     if (auto r = s->eng->end_batch(); !r) return set_error(r.error().message);
@@ -420,8 +447,8 @@ inline model_file::GptSpec session_spec(const GptSession& g)
     s.vocab_size = g.cfg.vocab_size;
     s.seq_len = g.cfg.seq_len;
     s.pos_encoding = g.cfg.pos_enc;
-    s.activation = model_file::kActivationSwiGLU;
-    s.norm_type = model_file::kNormRMSNorm;
+    s.activation = g.cfg.activation;
+    s.norm_type = g.cfg.norm_type;
     return s;
 }
 
@@ -474,11 +501,74 @@ inline int gpt_load(GptSession* g, const char* path, char* tok_out, std::size_t 
                              ", this session's model has " + std::to_string(v.second));
     for (std::size_t i = 0; i < ms.size(); ++i)
         if (auto r = g->eng->copy_from(g->params[i].get(), ms[i]); !r) return set_error(r.error().message);
-    g->opt = std::make_unique<AdamW>(*g->eng, g->params, g->grads, g->cfg.lr, g->cfg.beta1, g->cfg.beta2,
-                                     g->cfg.eps, g->cfg.weight_decay);
+    auto o = make_optimizer(*g->eng, g->cfg, g->params, g->grads);
+    if (!o) return set_error(o.error().message);
+    g->opt = std::move(*o);
     if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
     if (tok_len) *tok_len = tok.size();
     if (tok_out && tok_cap) std::memcpy(tok_out, tok.data(), std::min(tok_cap, tok.size()));
+    return 0;
+}
+
+// ── incremental inference (reference compute_layer.hpp:2906-3096) ─────────
+inline GPTModel* gpt_model(GptSession* g) { return dynamic_cast<GPTModel*>(&g->model.layer_at(0)); }
+
+// One token through the model with the session's per-block KV caches
+// ((seq_len, d_model) each, created on first use): GPTModel::forward_step.
+// logits_out: vocab floats.
+inline int gpt_forward_step(GptSession* g, std::uint64_t token, std::size_t pos, std::size_t cur_len,
+                            float* logits_out)
+{
+    GPTModel* m = gpt_model(g);
+    if (!m) return set_error("gpt_forward_step: the session holds no GPT model");
+    if (token >= m->vocab_size()) return set_error("gpt_forward_step: token id out of range");
+    if (pos >= m->seq_len()) return set_error("gpt_forward_step: position out of range");
+    if (g->k_cache.size() != m->num_blocks())
+    {
+        g->k_cache.clear();
+        g->v_cache.clear();
+        for (std::size_t i = 0; i < m->num_blocks(); ++i)
+        {
+            g->k_cache.push_back(g->eng->create_tensor(m->seq_len(), m->d_model()));
+            g->v_cache.push_back(g->eng->create_tensor(m->seq_len(), m->d_model()));
+            if (auto r = g->eng->zero(g->k_cache.back()); !r) return set_error(r.error().message);
+            if (auto r = g->eng->zero(g->v_cache.back()); !r) return set_error(r.error().message);
+        }
+    }
+    if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
+    auto y = m->forward_step(*g->eng, static_cast<std::size_t>(token), pos, g->k_cache, g->v_cache, cur_len);
+    if (!y) return set_error(y.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    return logits_out ? gpt_read(g, *y, logits_out) : 0;
+}
+
+inline int gpt_reset_cache(GptSession* g)
+{
+    g->k_cache.clear();
+    g->v_cache.clear();
+    return 0;
+}
+
+// GPTModel::generate with the caller's seed; *n_out tokens (at most out_cap are copied).
+inline int gpt_generate(GptSession* g, const std::uint64_t* prompt, std::size_t n_prompt, std::size_t max_new,
+                        float temperature, std::uint64_t eos, std::size_t min_new, std::uint64_t seed,
+                        std::uint64_t* out, std::size_t out_cap, std::size_t* n_out)
+{
+    GPTModel* m = gpt_model(g);
+    if (!m) return set_error("gpt_generate: the session holds no GPT model");
+    if (!prompt || n_prompt == 0) return set_error("gpt_generate: empty prompt");
+    std::vector<std::size_t> pr(n_prompt);
+    for (std::size_t i = 0; i < n_prompt; ++i)
+    {
+        if (prompt[i] >= m->vocab_size()) return set_error("gpt_generate: prompt token out of range");
+        pr[i] = static_cast<std::size_t>(prompt[i]);
+    }
+    if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
+    auto toks = m->generate(*g->eng, pr, max_new, temperature, static_cast<std::size_t>(eos), min_new, seed);
+    if (!toks) return set_error(toks.error().message);
+    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    if (n_out) *n_out = toks->size();
+    for (std::size_t i = 0; i < toks->size() && i < out_cap && out; ++i) out[i] = (*toks)[i];
     return 0;
 }
 
@@ -712,6 +802,18 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
     {                                                                                                               \
         return nn::capi::gpt_train_step_ex(static_cast<nn::capi::GptSession*>(g), accum_steps, max_norm,            \
                                            do_update, loss);                                                        \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_forward_step)(void* g, uint64_t token, size_t pos, size_t cur_len, float* logits)       \
+    {                                                                                                               \
+        return nn::capi::gpt_forward_step(static_cast<nn::capi::GptSession*>(g), token, pos, cur_len, logits);     \
+    }                                                                                                               \
+    int NN_CAPI_CAT(P, gpt_reset_cache)(void* g) { return nn::capi::gpt_reset_cache(static_cast<nn::capi::GptSession*>(g)); } \
+    int NN_CAPI_CAT(P, gpt_generate)(void* g, const uint64_t* prompt, size_t n_prompt, size_t max_new,             \
+                                     float temperature, uint64_t eos, size_t min_new, uint64_t seed, uint64_t* out,  \
+                                     size_t out_cap, size_t* n_out)                                                 \
+    {                                                                                                               \
+        return nn::capi::gpt_generate(static_cast<nn::capi::GptSession*>(g), prompt, n_prompt, max_new,            \
+                                      temperature, eos, min_new, seed, out, out_cap, n_out);                        \
     }                                                                                                               \
     }                                                                                                               \
     _Pragma("GCC visibility pop")

@@ -11,6 +11,8 @@
 //   RMSNorm forward  compute_layer.hpp:733-754,  backward :772-795
 //   Softmax forward  :840-844,                   backward :855-860
 //   SwiGLU backward  :436-444
+//   LayerNorm        forward :541-592, backward :601-660
+//   RoPE             :884-984
 #pragma once
 
 #include "expr_dsl.hpp"
@@ -63,6 +65,53 @@ inline auto swiglu_grad_gate(const Tensor& g, const Tensor& up, const Tensor& s,
 inline auto swiglu_grad_up(const Tensor& g, const Tensor& gate, const Tensor& s)
 {
     return dsl::leaf(g) * dsl::leaf(gate) * dsl::leaf(s);
+}
+
+// LayerNorm forward (reference compute_layer.hpp:541-592): mean_raw = ColSum(x);
+// diff = x - colbcast(mean); var_raw = ColSum(diff*diff); normed = diff * colbcast(std_inv);
+// out = normed * rowbcast(gamma) + rowbcast(beta).
+inline auto ln_col_sum(const Tensor& x) { return dsl::col_reduce_sum(dsl::leaf(x)); }
+inline auto ln_center(const Tensor& x, const Tensor& mean) { return dsl::leaf(x) - dsl::col_broadcast(mean); }
+inline auto ln_sum_sq(const Tensor& diff) { return dsl::col_reduce_sum(dsl::leaf(diff) * dsl::leaf(diff)); }
+inline auto ln_normalize(const Tensor& diff, const Tensor& std_inv)
+{
+    return dsl::leaf(diff) * dsl::col_broadcast(std_inv);
+}
+inline auto ln_affine(const Tensor& normed, const Tensor& gamma, const Tensor& beta)
+{
+    return dsl::leaf(normed) * dsl::row_broadcast(gamma) + dsl::row_broadcast(beta);
+}
+// LayerNorm backward (reference :601-660).
+inline auto ln_bwd_colsum_g(const Tensor& g, const Tensor& gamma)
+{
+    return dsl::col_reduce_sum(dsl::leaf(g) * dsl::row_broadcast(gamma));
+}
+inline auto ln_bwd_colsum_gn(const Tensor& g, const Tensor& gamma, const Tensor& normed)
+{
+    return dsl::col_reduce_sum(dsl::leaf(g) * dsl::row_broadcast(gamma) * dsl::leaf(normed));
+}
+inline auto ln_bwd_dx(const Tensor& g, const Tensor& gamma, const Tensor& mean_g, const Tensor& normed,
+                      const Tensor& mean_gn, const Tensor& std_inv)
+{
+    return (dsl::leaf(g) * dsl::row_broadcast(gamma) - dsl::col_broadcast(mean_g) -
+            dsl::leaf(normed) * dsl::col_broadcast(mean_gn)) *
+           dsl::col_broadcast(std_inv);
+}
+inline auto ln_bwd_rowsum_gn(const Tensor& g, const Tensor& gamma, const Tensor& normed)
+{
+    return dsl::row_reduce_sum(dsl::leaf(g) * dsl::row_broadcast(gamma) * dsl::leaf(normed));
+}
+inline auto ln_bwd_rowsum(const Tensor& g) { return dsl::row_reduce_sum(dsl::leaf(g)); }
+
+// RoPE (reference :884-984): q*RowMod(cos) + RotateHalf(q)*RowMod(sin), its
+// inverse rotation with Sub; RotateHalf negates the first half of each block.
+inline auto rope_forward(const Tensor& q, const Tensor& cos, const Tensor& sin, std::uint32_t dk)
+{
+    return dsl::leaf(q) * dsl::row_mod(cos, dk) + dsl::rotate_half(q, dk) * dsl::row_mod(sin, dk);
+}
+inline auto rope_backward(const Tensor& q, const Tensor& cos, const Tensor& sin, std::uint32_t dk)
+{
+    return dsl::leaf(q) * dsl::row_mod(cos, dk) - dsl::rotate_half(q, dk) * dsl::row_mod(sin, dk);
 }
 
 } // namespace nn::layer_exprs

@@ -2,9 +2,9 @@
 //
 // Model follows include/neuralnet.cpp/model_container.hpp:31-188 (ordered
 // layers, forward in order, backward in reverse, concatenated parameters);
-// GptConfig / build_gpt_model follow include/neuralnet.cpp/domain_gpt.hpp:32-63.
-// Only the architecture the GPT hot path uses is built: SwiGLU FFN and
-// RMSNorm; GeLU, LayerNorm and RoPE are rejected with an error.
+// GptConfig / build_gpt_model follow include/neuralnet.cpp/domain_gpt.hpp:32-63:
+// GeLU or SwiGLU feed-forward, LayerNorm or RMSNorm, learned / sinusoidal /
+// ALiBi / RoPE positions.
 #pragma once
 
 #include <memory>
@@ -109,15 +109,17 @@ struct GptConfig
         return fail("GPT d_ff and num_layers must be positive");
     if (c.d_model % c.num_heads != 0)
         return fail("GPT d_model must be divisible by num_heads");
-    if (c.activation != ActivationType::SwiGLU)
-        return fail("build_gpt_model: only the SwiGLU feed-forward is built here");
-    if (c.norm_type != NormType::RMSNorm)
-        return fail("build_gpt_model: only RMSNorm is built here");
-    if (c.pos_enc == PosEncodingType::RoPE)
-        return fail("build_gpt_model: RoPE is not built here");
+    if (c.activation != ActivationType::SwiGLU && c.activation != ActivationType::GeLU)
+        return fail("build_gpt_model: activation must be GeLU or SwiGLU");
+    if (c.norm_type != NormType::RMSNorm && c.norm_type != NormType::LayerNorm)
+        return fail("build_gpt_model: norm must be LayerNorm or RMSNorm");
+    if (static_cast<std::uint32_t>(c.pos_enc) > static_cast<std::uint32_t>(PosEncodingType::RoPE))
+        return fail("build_gpt_model: unknown position encoding");
+    if (c.pos_enc == PosEncodingType::RoPE && (c.d_model / c.num_heads) % 2 != 0)
+        return fail("build_gpt_model: RoPE needs an even head dimension");
     Model m(engine);
     m.add_layer(std::make_unique<GPTModel>(engine, c.vocab_size, c.d_model, c.seq_len, c.num_heads, c.d_ff,
-                                           c.num_layers, c.pos_enc));
+                                           c.num_layers, c.pos_enc, c.activation, c.norm_type));
     return m;
 }
 

@@ -1,5 +1,5 @@
 """The ExprSpec programs the GPT layers issue (compute_layer.hpp:733-795 RMSNorm,
-:436-444 SwiGLU backward, :840-860 Softmax), built the way the expression DSL
+:436-444 SwiGLU backward, :840-860 Softmax, :884-984 RoPE), built the way the expression DSL
 folds them (left operand before right; every leaf or view is a new input
 slot; reduce instructions are referenced through Reduce operands). The HIP
 engine recognises exactly these programs and runs a fused kernel for each,
@@ -109,6 +109,25 @@ def softmax_rows_backward():             # y * (g - RowSum(y*g))
     r2 = s.ins("Sub", inp(1), red(r1))
     s.ins("Mul", inp(0), reg(r2))
     return s, ("y", "g", "y", "g")
+
+
+def rope(dk, backward=False):            # q*RowMod(cos) +/- RotateHalf(q)*RowMod(sin)  (compute_layer.hpp:884-984)
+    s = ExprSpec()
+    s.view("Linear"), s.view("RowMod", dk), s.view("RotateHalf", dk, 1), s.view("RowMod", dk)
+    r0 = s.ins("Mul", inp(0), inp(1))
+    r1 = s.ins("Mul", inp(2), inp(3))
+    s.ins("Sub" if backward else "Add", reg(r0), reg(r1))
+    return s, ("q", "cos", "q", "sin")
+
+
+def rope_tables(dk, T):
+    """(dk, T) cos / sin tables: rows j and j + dk/2 hold cos / sin(pos * 10000^(-2j/dk))."""
+    import numpy as np
+    half = dk // 2
+    ang = np.arange(T)[None, :] / (10000.0 ** (2.0 * np.arange(half)[:, None] / dk))
+    c = np.concatenate([np.cos(ang)] * 2).astype(np.float32)
+    sn = np.concatenate([np.sin(ang)] * 2).astype(np.float32)
+    return c, sn
 
 
 # (builder, reduced-vector output, closed form over float64 numpy arrays)

@@ -37,7 +37,7 @@ UNARY = dict(Neg=0, Exp=1, Log=2, Sqrt=3, Rsqrt=4, Abs=5, Tanh=6)
 BINARY = dict(Add=0, Sub=1, Mul=2, Div=3, Max=4, Min=5)
 COMPARE = dict(Lt=0, Le=1, Gt=2, Ge=3, Eq=4, Ne=5)
 REDUCE = dict(Sum=0, Max=1, Min=2)
-POS_ENC = dict(learned=0, sinusoidal=1, alibi=2)
+POS_ENC = dict(learned=0, sinusoidal=1, alibi=2, rope=3)
 
 
 class EngineError(RuntimeError):
@@ -70,7 +70,13 @@ class _GptConfig(ctypes.Structure):
     _fields_ = [("vocab_size", ctypes.c_size_t), ("d_model", ctypes.c_size_t), ("seq_len", ctypes.c_size_t),
                 ("num_heads", ctypes.c_size_t), ("d_ff", ctypes.c_size_t), ("num_layers", ctypes.c_size_t),
                 ("pos_enc", ctypes.c_uint32), ("lr", ctypes.c_float), ("beta1", ctypes.c_float),
-                ("beta2", ctypes.c_float), ("eps", ctypes.c_float), ("weight_decay", ctypes.c_float)]
+                ("beta2", ctypes.c_float), ("eps", ctypes.c_float), ("weight_decay", ctypes.c_float),
+                ("activation", ctypes.c_uint32), ("norm_type", ctypes.c_uint32), ("optimizer", ctypes.c_uint32)]
+
+
+ACTIVATION = dict(gelu=0, swiglu=1)
+NORM = dict(layernorm=0, rmsnorm=1)
+OPTIMIZER = dict(adamw=0, adam=1, sgd=2, sgd_momentum=3, muon=4)
 
 
 def _bind(lib: ctypes.CDLL, prefix: str):
@@ -117,6 +123,10 @@ def _bind(lib: ctypes.CDLL, prefix: str):
                                ctypes.POINTER(ctypes.c_size_t)]),
         "gpt_clip_grad_norm": (i32, [vp, ctypes.c_float]),
         "gpt_train_step_ex": (i32, [vp, ctypes.c_size_t, ctypes.c_float, ctypes.c_int, fp]),
+        "gpt_forward_step": (i32, [vp, ctypes.c_uint64, sz, sz, fp]),
+        "gpt_reset_cache": (i32, [vp]),
+        "gpt_generate": (i32, [vp, u64p, sz, sz, ctypes.c_float, ctypes.c_uint64, sz, ctypes.c_uint64, u64p, sz,
+                               ctypes.POINTER(ctypes.c_size_t)]),
         "build_attention_mask": (i32, [sz, sz, sz, i32, fp, ctypes.POINTER(ctypes.c_uint64), sz, fp]),
     }
     fns = {}
@@ -412,11 +422,12 @@ class GptSession:
     """GPTModel + sparse cross-entropy + AdamW on one engine (include/nnhip_engine.h)."""
 
     def __init__(self, eng: Engine, vocab_size, d_model, seq_len, num_heads, d_ff, num_layers, pos_enc="learned",
-                 lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01):
+                 lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, activation="swiglu", norm="rmsnorm",
+                 optimizer="adamw"):
         self._eng = eng
         self._f = eng._f
         cfg = _GptConfig(vocab_size, d_model, seq_len, num_heads, d_ff, num_layers, POS_ENC[pos_enc], lr, beta1,
-                         beta2, eps, weight_decay)
+                         beta2, eps, weight_decay, ACTIVATION[activation], NORM[norm], OPTIMIZER[optimizer])
         g = ctypes.c_void_p()
         eng._check(self._f["gpt_create"](eng._e, ctypes.byref(cfg), ctypes.byref(g)))
         self._g = g
@@ -500,6 +511,27 @@ class GptSession:
         buf = ctypes.create_string_buffer(max(1, os.path.getsize(path)))
         self._eng._check(self._f["gpt_load"](self._g, path.encode(), buf, len(buf), ctypes.byref(n)))
         return buf.raw[:n.value]
+
+    def forward_step(self, token: int, pos: int, cur_len: int) -> np.ndarray:
+        """GPTModel::forward_step with the session's KV caches: logits (vocab,) of one token."""
+        out = np.empty(self.vocab_size, dtype=np.float32)
+        self._eng._check(self._f["gpt_forward_step"](self._g, int(token), int(pos), int(cur_len), _fptr(out)))
+        return out
+
+    def reset_cache(self) -> None:
+        self._eng._check(self._f["gpt_reset_cache"](self._g))
+
+    def generate(self, prompt, max_new: int, temperature: float = 0.0, eos: int = 2 ** 64 - 1, min_new: int = 0,
+                 seed: int = 0):
+        """GPTModel::generate (sampling with KV caches); the generated token ids."""
+        pr = np.ascontiguousarray(np.asarray(prompt, dtype=np.uint64))
+        out = np.zeros(max(1, max_new), dtype=np.uint64)
+        n = ctypes.c_size_t()
+        u64p = ctypes.POINTER(ctypes.c_uint64)
+        self._eng._check(self._f["gpt_generate"](self._g, pr.ctypes.data_as(u64p), pr.size, int(max_new),
+                                                 float(temperature), int(eos), int(min_new), int(seed),
+                                                 out.ctypes.data_as(u64p), out.size, ctypes.byref(n)))
+        return out[:n.value].astype(np.int64).tolist()
 
     def backward_scaled(self, grad_scale: float) -> None:
         """Backward of one accumulated micro-batch: loss gradient scaled by grad_scale first."""

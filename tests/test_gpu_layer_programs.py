@@ -94,3 +94,60 @@ def test_same_program_distinct_tensors_uses_general_path(hip, cpu):
     a, b = normal(rng, (64, 128)), normal(rng, (64, 128))
     h = hip.eval_expr_reduce(spec, [hip.tensor(a), hip.tensor(b)], 64, 128).numpy()
     assert nrm_err(h, (a.astype(np.float64) * b).sum(0, keepdims=True)) <= 1e-5
+
+
+@pytest.mark.parametrize("dk,heads,T", [(16, 4, 32), (64, 96, 1024), (8, 3, 7), (64, 12, 1)])
+@pytest.mark.parametrize("backward", [False, True])
+def test_rope_program(hip, cpu, dk, heads, T, backward):
+    """RoPE (compute_layer.hpp:884-984) on the generic interpreter: RotateHalf (first half negated) and
+    RowMod views, on (heads*dk, T) heads with (dk, T) tables; bit-exact against the oracle (each
+    output is one multiply per term and one add, the same roundings)."""
+    spec, slots = lp.rope(dk, backward)
+    print(f"[rope] dk {dk} heads {heads} T {T} backward {backward}", flush=True)
+    rng = np.random.default_rng(dk * 1000 + T + backward)
+    q = normal(rng, (heads * dk, T))
+    c, s = lp.rope_tables(dk, T)
+    args = dict(q=q, cos=c, sin=s)
+    h = _run(hip, spec, slots, args, heads * dk, T, False)
+    o = _run(cpu, spec, slots, args, heads * dk, T, False)
+    assert nrm_err(h, o) <= 1e-6
+    half = dk // 2
+    qb = q.reshape(heads, dk, T).astype(np.float64)
+    rot = np.concatenate([-qb[:, half:], qb[:, :half]], axis=1) * (-1 if backward else 1)
+    ref = (qb * c.astype(np.float64) + rot * s.astype(np.float64)).reshape(heads * dk, T)
+    assert nrm_err(h, ref) <= 1e-6
+
+
+@pytest.mark.parametrize("slot", [0, 3])
+@pytest.mark.parametrize("view", ["RowReduceSum", "RowReduceMax", "ColReduceSum", "ColReduceMax"])
+@pytest.mark.parametrize("R,C", [(37, 129), (768, 1024)])
+def test_reduce_views_and_select(hip, cpu, view, R, C, slot):
+    """The reduce views and Select on the GPU interpreter against the oracle: out = Select(x > 0,
+    view(x) - 2y, y), with the reduce view at input slot 0 or 3 (each view's record is read at its own
+    slot)."""
+    from nnengine import ExprSpec, cst, inp, reg
+    print(f"[expr] {view} slot {slot} {R}x{C}", flush=True)
+    rng = np.random.default_rng(R + C)
+    x, y = normal(rng, (R, C)), normal(rng, (R, C))
+    s = ExprSpec()
+    kinds = ["Linear"] * 4
+    kinds[slot] = view
+    for k in kinds:
+        s.view(k)
+    xr, y1, x2, y3 = (slot, 1, 2, 0) if slot == 3 else (0, 1, 2, 3)   # slots reading x (reduced), y, x, y
+    c2, c0 = s.const(2.0), s.const(0.0)
+    r0 = s.ins("Mul", inp(y1), cst(c2))
+    r1 = s.ins("Sub", inp(xr), reg(r0))
+    r2 = s.ins("Gt", inp(x2), cst(c0))
+    s.ins("Select", reg(r2), reg(r1), inp(y3))
+
+    def run(e):
+        ts = [None] * 4
+        ts[xr], ts[y1], ts[x2], ts[y3] = e.tensor(x), e.tensor(y), e.tensor(x), e.tensor(y)
+        return e.eval_expr(s, ts, R, C).numpy()
+    h, c = run(hip), run(cpu)
+    assert nrm_err(h, c) <= 1e-5
+    red = {"RowReduceSum": x.astype(np.float64).sum(1, keepdims=True), "RowReduceMax": x.max(1, keepdims=True),
+           "ColReduceSum": x.astype(np.float64).sum(0, keepdims=True), "ColReduceMax": x.max(0, keepdims=True)}[view]
+    ref = np.where(x > 0, red - 2.0 * y.astype(np.float64), y)
+    assert nrm_err(h, ref) <= 1e-5

@@ -659,3 +659,160 @@ def test_build_attention_mask_rejects_missing_slopes(cpu):
     out = np.empty((8, 4), np.float32)
     assert cpu._f["build_attention_mask"](1, 4, 2, 1, None, None, 0, out.ctypes.data_as(
         ctypes.POINTER(ctypes.c_float))) != 0
+
+
+# ── GPT variants: QuickGeLU, LayerNorm, RoPE (reference compute_layer.hpp:256, 479, 884) ──
+@pytest.mark.parametrize("variant", [dict(pos_enc="learned", activation="gelu", norm="layernorm"),
+                                     dict(pos_enc="rope", activation="swiglu", norm="rmsnorm"),
+                                     dict(pos_enc="rope", activation="gelu", norm="layernorm"),
+                                     dict(pos_enc="alibi", activation="gelu", norm="rmsnorm")],
+                         ids=lambda v: "-".join(v.values()))
+@pytest.mark.parametrize("with_doc", [False, True])
+def test_gpt_variants_vs_torch_float64(cpu, variant, with_doc):
+    """The other GPT variants against the independent float64 model (LayerNorm with biased variance,
+    QuickGeLU x*sigmoid(1.702x), RoPE as a complex rotation of dimension pairs (j, j + d_k/2))."""
+    cfg = dict(vocab_size=40, d_model=16, seq_len=8, num_heads=2, d_ff=24, num_layers=2, **variant)
+    rng = np.random.default_rng(321)
+    B = 3
+    shapes = torch_gpt.param_shapes(cfg)
+    params = [rng.normal(0, 0.2, s).astype(np.float32) for s in shapes]
+    toks = rng.integers(0, 40, size=(9, B))
+    doc = np.repeat(np.arange(6), 4).astype(np.uint64) if with_doc else None
+    g = cpu.gpt(**cfg)
+    assert g.param_shapes() == shapes
+    g.set_params(params)
+    if doc is not None:
+        g.set_doc_ids(doc)
+    g.load_batch(toks[:8].astype(np.float32), toks[1:].T.reshape(-1))
+    loss = g.forward_loss()
+    logits = g.logits()
+    g.backward()
+    grads = g.grads()
+    rloss, rlogits, rgrads = torch_gpt.loss_and_grads(params, toks[:8], toks[1:].T.reshape(-1), cfg, doc_ids=doc)
+    assert abs(loss - rloss) <= 1e-5 * abs(rloss)
+    assert nrm_err(logits, rlogits) <= 1e-5
+    errs = grad_errs(grads, torch_gpt.reference_gamma_grads(params, rgrads, cfg))
+    assert max(errs) <= 1e-4, errs
+
+
+def test_rope_rotation_properties(cpu):
+    """RoPE's scores depend on relative position only (q_i . k_j after rotation = f(i - j)), and the
+    backward rotation is the forward's inverse."""
+    import layer_programs as lp
+    dk, T = 8, 6
+    rng = np.random.default_rng(2)
+    q = normal(rng, (dk, 1)).repeat(T, axis=1)      # the same vector at every position
+    k = normal(rng, (dk, 1)).repeat(T, axis=1)
+    c, s = lp.rope_tables(dk, T)
+    fwd, bwd = lp.rope(dk, False)[0], lp.rope(dk, True)[0]
+    ct, st = cpu.tensor(c), cpu.tensor(s)
+    qr = cpu.eval_expr(fwd, [cpu.tensor(q), ct, cpu.tensor(q), st], dk, T)
+    kr = cpu.eval_expr(fwd, [cpu.tensor(k), ct, cpu.tensor(k), st], dk, T)
+    S = qr.numpy().T.astype(np.float64) @ kr.numpy().astype(np.float64)     # (T, T)
+    for d in range(-T + 1, T):
+        diag = np.diagonal(S, offset=d)
+        assert np.abs(diag - diag[0]).max() <= 1e-5 * max(1.0, np.abs(S).max())
+    back = cpu.eval_expr(bwd, [qr, ct, qr, st], dk, T).numpy()
+    assert nrm_err(back, q) <= 1e-6
+
+
+# ── incremental inference (reference compute_layer.hpp:1426-1511, 2413-2437, 2906-3096) ──
+def _session_with(cpu_or_hip, cfg, params):
+    g = cpu_or_hip.gpt(**cfg)
+    g.set_params(params)
+    return g
+
+
+@pytest.mark.parametrize("pos", ["learned", "sinusoidal", "alibi", "rope"])
+def test_forward_step_equals_full_forward(cpu, pos):
+    """The reference's attn_consistency_test method (src/attn_consistency_test.cpp): logits of token t
+    from forward_step with KV caches (positions 0..t) equal column t of the full forward over the
+    sequence (causal, so later tokens do not matter)."""
+    cfg = dict(vocab_size=48, d_model=16, seq_len=10, num_heads=2, d_ff=24, num_layers=2, pos_enc=pos)
+    rng = np.random.default_rng(5)
+    params = [rng.normal(0, 0.2, s).astype(np.float32) for s in torch_gpt.param_shapes(cfg)]
+    toks = rng.integers(0, 48, size=10)
+    g = _session_with(cpu, cfg, params)
+    g.load_batch(toks.reshape(10, 1).astype(np.float32), np.zeros(10, np.uint64))
+    g.forward_loss()
+    full = g.logits()                               # (V, 10)
+    for t in range(10):
+        step = g.forward_step(int(toks[t]), t, t)
+        assert nrm_err(step, full[:, t]) <= 1e-5, t
+    g.reset_cache()
+    assert nrm_err(g.forward_step(int(toks[0]), 0, 0), full[:, 0]) <= 1e-5
+
+
+def test_generate_greedy_is_argmax_of_full_forward(cpu):
+    """generate at temperature 0 appends argmax of the last logits; checked by recomputing each step's
+    logits with a full forward of the context (no caches), including a sliding-window refill once the
+    caches are full (context longer than seq_len), and an eos stop."""
+    cfg = dict(vocab_size=32, d_model=16, seq_len=6, num_heads=2, d_ff=24, num_layers=2, pos_enc="alibi")
+    rng = np.random.default_rng(8)
+    params = [rng.normal(0, 0.5, s).astype(np.float32) for s in torch_gpt.param_shapes(cfg)]
+    g = _session_with(cpu, cfg, params)
+    prompt = [3, 17, 5]
+    out = g.generate(prompt, 7, temperature=0.0)
+    assert len(out) == 7
+    ctx = list(prompt)
+    for tok in out:
+        window = ctx if len(ctx) < 6 else ctx[-5:]   # full caches are refilled with the last seq_len - 1 tokens
+        T = len(window)
+        c2 = dict(cfg, seq_len=T)
+        full = _session_with(cpu, c2, params[:])
+        full.load_batch(np.asarray(window, np.float32).reshape(T, 1), np.zeros(T, np.uint64))
+        full.forward_loss()
+        assert tok == int(np.argmax(full.logits()[:, -1])), (ctx, tok)
+        ctx.append(tok)
+    eos = out[2]
+    stopped = g.generate(prompt, 7, temperature=0.0, eos=eos, min_new=0)
+    assert stopped == out[:out.index(eos)]
+    sampled = g.generate(prompt, 5, temperature=0.8, seed=11)
+    assert sampled == g.generate(prompt, 5, temperature=0.8, seed=11) and all(0 <= t < 32 for t in sampled)
+
+
+# ── optimizers by name (reference compute_optimizer.hpp:153-216, 415-615) ──
+def _ns_closed_form(G, steps=5):
+    """Newton-Schulz on G as its action on the singular values: the iteration X <- aX + (bA + cA^2)X with
+    A = XX^T keeps G's singular vectors and maps each normalised singular value x to a x + b x^3 + c x^5."""
+    a, b, c = 3.4445, -4.7750, 2.0315
+    G = np64(G)
+    U, sv, Vt = np.linalg.svd(G, full_matrices=False)
+    x = sv / np.sqrt((G ** 2).sum() + 1e-14)
+    for _ in range(steps):
+        x = a * x + b * x ** 3 + c * x ** 5
+    return (U * x) @ Vt
+
+
+@pytest.mark.parametrize("name", ["sgd", "sgd_momentum", "adam", "muon"])
+def test_optimizer_first_step_closed_form(cpu, name):
+    """One step of each optimizer the session can use, from zero state, against its closed form: SGD
+    p - lr g; momentum p - lr (1 - beta) g; Adam p - lr g / (|g| + eps); Muon (momentum 0.95, Nesterov)
+    p - lr NS(1.95 g) for matrices (NS through the SVD, above) and p - lr 1.95 g for vectors."""
+    cfg = dict(vocab_size=24, d_model=16, seq_len=6, num_heads=2, d_ff=12, num_layers=1, pos_enc="learned")
+    rng = np.random.default_rng(13)
+    params = [rng.normal(0, 0.2, s).astype(np.float32) for s in torch_gpt.param_shapes(cfg)]
+    toks = rng.integers(0, 24, size=(7, 2))
+    lr = 0.05
+    g = cpu.gpt(**cfg, optimizer=name, lr=lr, weight_decay=0.0)
+    g.set_params(params)
+    g.load_batch(toks[:6].astype(np.float32), toks[1:].T.reshape(-1))
+    g.forward_loss()
+    g.backward()
+    grads = [np64(x) for x in g.grads()]
+    g.optimizer_step()
+    new = g.params()
+    for p, gr, q in zip(params, grads, new):
+        if name == "sgd":
+            ref = np64(p) - lr * gr
+        elif name == "sgd_momentum":
+            ref = np64(p) - lr * 0.1 * gr
+        elif name == "adam":
+            ref = np64(p) - lr * gr / (np.abs(gr) + 1e-8)
+        else:
+            upd = 1.95 * gr
+            ref = np64(p) - lr * (_ns_closed_form(upd) if p.shape[0] > 1 and p.shape[1] > 1 else upd)
+        tol = 2e-6 if name != "muon" else 2e-5
+        assert np.abs(q - ref).max() <= tol * max(1.0, np.abs(ref).max()), (name, p.shape)
+    with pytest.raises(KeyError):
+        cpu.gpt(**cfg, optimizer="lion")

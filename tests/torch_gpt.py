@@ -14,31 +14,44 @@ import numpy as np
 import torch
 
 
-def param_shapes(cfg):
+def _norm(cfg):
+    return cfg.get("norm", "rmsnorm")
+
+
+def _act(cfg):
+    return cfg.get("activation", "swiglu")
+
+
+def _layout(cfg):
+    """(shape, role) per parameter in parameters() order; roles: 'gain' (RMSNorm / LayerNorm gamma),
+    'shift' (LayerNorm beta), 'other'."""
     V, D, T, H, F, L = (cfg[k] for k in ("vocab_size", "d_model", "seq_len", "num_heads", "d_ff", "num_layers"))
-    shapes = [(V, D)]
+    norm = [((D, 1), "gain")] + ([((D, 1), "shift")] if _norm(cfg) == "layernorm" else [])
+    f1 = 2 * F if _act(cfg) == "swiglu" else F
+    out = [((V, D), "other")]
     if cfg["pos_enc"] == "learned":
-        shapes.append((T, D))
+        out.append(((T, D), "other"))
     for _ in range(L):
-        shapes += [(D, D), (D, 1)] * 4 + [(D, 1), (2 * F, D), (2 * F, 1), (D, F), (D, 1), (D, 1)]
-    shapes += [(D, 1), (V, D), (V, 1)]
-    return shapes
+        out += [((D, D), "other"), ((D, 1), "other")] * 4 + norm
+        out += [((f1, D), "other"), ((f1, 1), "other"), ((D, F), "other"), ((D, 1), "other")] + norm
+    out += norm + [((V, D), "other"), ((V, 1), "other")]
+    return out
+
+
+def param_shapes(cfg):
+    return [s for s, _ in _layout(cfg)]
 
 
 def gamma_indices(cfg):
-    """Positions of the RMSNorm gains in parameters() order."""
-    base = 2 if cfg["pos_enc"] == "learned" else 1
-    idx = []
-    for l in range(cfg["num_layers"]):
-        idx += [base + 14 * l + 8, base + 14 * l + 13]
-    idx.append(base + 14 * cfg["num_layers"])
-    return idx
+    """Positions of the norm gains (RMSNorm / LayerNorm gamma) in parameters() order."""
+    return [i for i, (_, r) in enumerate(_layout(cfg)) if r == "gain"]
 
 
 def reference_gamma_grads(params_np, grads, cfg):
     """The reference accumulates grad_gamma += row_reduce_sum(g * gamma * normed)
-    (compute_layer.hpp:788-795), i.e. gamma times the true gradient sum(g * normed);
-    the two agree at gamma = 1. Returns grads with that convention applied."""
+    (RMSNorm compute_layer.hpp:788-795, LayerNorm :636-644), i.e. gamma times the
+    true gradient sum(g * normed); the two agree at gamma = 1. Returns grads with
+    that convention applied."""
     out = list(grads)
     for i in gamma_indices(cfg):
         out[i] = np.asarray(params_np[i], dtype=np.float64) * grads[i]
@@ -48,6 +61,26 @@ def reference_gamma_grads(params_np, grads, cfg):
 def _rmsnorm(x, g):
     rms_inv = 1.0 / torch.sqrt((x * x).mean(dim=0, keepdim=True) + 1e-5)
     return x * rms_inv * g
+
+
+def _layernorm(x, g, b):
+    """LayerNorm over features (compute_layer.hpp:479-662): biased variance, eps 1e-5."""
+    mu = x.mean(dim=0, keepdim=True)
+    var = ((x - mu) ** 2).mean(dim=0, keepdim=True)
+    return (x - mu) / torch.sqrt(var + 1e-5) * g + b
+
+
+def _rope(x, T, dk):
+    """Rotary positions as complex rotation: per head block of dk rows, the pair (j, j + dk/2) is the
+    complex number x_j + i x_{j+dk/2} turned by pos * 10000^(-2j/dk) (compute_layer.hpp:884-984)."""
+    half = dk // 2
+    j = torch.arange(half, dtype=torch.float64)
+    theta = 10000.0 ** (-2.0 * j / dk)
+    ang = torch.arange(T, dtype=torch.float64)[None, :] * theta[:, None]        # (half, T)
+    rot = torch.polar(torch.ones_like(ang), ang)
+    blocks = x.reshape(-1, dk, T)
+    z = torch.complex(blocks[:, :half], blocks[:, half:]) * rot
+    return torch.cat([z.real, z.imag], dim=1).reshape(x.shape)
 
 
 def _sinusoidal(T, D):
@@ -90,9 +123,15 @@ def forward(params, tokens, cfg, doc_ids=None):
         x = x + _sinusoidal(T, D)[tpos]
     x = x.T                                         # (D, N)
     docs = None if doc_ids is None else torch.as_tensor(np.asarray(doc_ids, dtype=np.int64)).reshape(B, T)
+    def norm(x):
+        if _norm(cfg) == "layernorm":
+            g, b = next(it), next(it)
+            return _layernorm(x, g, b)
+        return _rmsnorm(x, next(it))
+
     for _ in range(L):
-        Wq, bq, Wk, bk, Wv, bv, Wo, bo, g1, W1, b1, W2, b2, g2 = (next(it) for _ in range(14))
-        h = _rmsnorm(x, g1)
+        Wq, bq, Wk, bk, Wv, bv, Wo, bo = (next(it) for _ in range(8))
+        h = norm(x)
         q, k, v = Wq @ h + bq, Wk @ h + bk, Wv @ h + bv
         out = torch.zeros_like(q)
         for b in range(B):
@@ -100,17 +139,25 @@ def forward(params, tokens, cfg, doc_ids=None):
             for hh in range(H):
                 rows = slice(hh * dk, (hh + 1) * dk)
                 Q, K_, Vv = q[rows, cols], k[rows, cols], v[rows, cols]          # (dk, T)
+                if pos == "rope":
+                    Q, K_ = _rope(Q, T, dk), _rope(K_, T, dk)
                 S = (Q.T @ K_) / math.sqrt(dk) + _mask(T, hh, H, pos == "alibi",
                                                        None if docs is None else docs[b])
                 A = torch.softmax(S, dim=1)
                 out[rows, cols] = Vv @ A.T
         x = x + (Wo @ out + bo)
-        h2 = _rmsnorm(x, g2)
+        W1, b1, W2, b2 = (next(it) for _ in range(4))
+        h2 = norm(x)
         u = W1 @ h2 + b1
-        gate, up = u[:F], u[F:]
-        x = x + (W2 @ (gate * torch.sigmoid(gate) * up) + b2)
-    gf, Wl, bl = next(it), next(it), next(it)
-    return Wl @ _rmsnorm(x, gf) + bl
+        if _act(cfg) == "swiglu":
+            gate, up = u[:F], u[F:]
+            act = gate * torch.sigmoid(gate) * up
+        else:
+            act = u * torch.sigmoid(1.702 * u)   # QuickGeLU (compute_layer.hpp:256-336)
+        x = x + (W2 @ act + b2)
+    xf = norm(x)
+    Wl, bl = next(it), next(it)
+    return Wl @ xf + bl
 
 
 def loss_and_grads(params_np, tokens, labels, cfg, doc_ids=None, loss_mask=None):
