@@ -233,6 +233,29 @@ int nnhip_flash_backward_ds(const float* Q, const float* Kt, const float* dO, co
                             const float* mask, const void* cells, const float* m, const float* l, float* dQ, float* dK,
                             float* dV, size_t batch, size_t M, size_t N, size_t K, float alpha, float alpha2,
                             size_t mask_batch_stride, void* workspace, void* stream);
+/* Work order of the calls above with a mask (no CUDA counterpart). The kernels' time is set by the most
+ * loaded CU; an order table (built from a cell table for one (batch, M, N): kind 0 the forward, 1 the
+ * backward, 2 the backward from the forward output) sorts the line groups by the cells they visit and
+ * spreads heavy and light ones over the CUs. Build it once per cell table and shape and pass it to the
+ * _ordered variants, which are the calls above plus `order` (NULL: the calls above). Results do not
+ * depend on the order. */
+size_t nnhip_flash_order_bytes(size_t batch, size_t M, size_t N, int kind);
+int nnhip_flash_build_order(const void* cells, size_t batch, size_t M, size_t N, size_t mask_batch_stride, int kind,
+                            void* order, void* stream);
+int nnhip_flash_forward_ordered(const float* Q, const float* Kt, const float* V, const float* mask, const void* cells,
+                                float* m, float* l, float* O, size_t batch, size_t M, size_t N, size_t K, size_t D,
+                                float alpha, size_t mask_batch_stride, int v_dim_major, int o_dim_major,
+                                const void* order, void* workspace, void* stream);
+int nnhip_flash_backward_ordered(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* G,
+                                 size_t ldg, const float* mask, const void* cells, const float* m, const float* l,
+                                 float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K,
+                                 size_t Kd, float alpha, float alpha2, size_t mask_batch_stride, int g_is_do,
+                                 const void* order, void* workspace, void* stream);
+int nnhip_flash_backward_ds_ordered(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* O,
+                                    const float* mask, const void* cells, const float* m, const float* l, float* dQ,
+                                    float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K, float alpha,
+                                    float alpha2, size_t mask_batch_stride, const void* order, void* workspace,
+                                    void* stream);
 
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */

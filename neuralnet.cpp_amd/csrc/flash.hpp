@@ -19,6 +19,7 @@ struct FlashGeo
     const unsigned char* cls;   // RT x CT mask cell classes, or nullptr without a mask
     long cls_bs;     // bytes between batch entries' cell tables (0: one table shared)
     float* part;     // partials of lines cut into several ranges
+    const int* order;   // workgroup -> work item (a permutation of the grid), or nullptr
 };
 
 // Forward: m, l (batch*M) and, when O is not null, O (batch*M, D).

@@ -666,8 +666,31 @@ Result<const void*> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, st
                      "attention mask cells"));
     constexpr std::size_t kKeep = 32;   // one per layer's mask in a 12-32 layer model
     if (cells_.size() == kKeep) cells_.erase(cells_.begin());
-    cells_.push_back({*mask, buf, M});
+    cells_.push_back({*mask, buf, M, {}});
     return static_cast<const void*>(buf->data());
+}
+
+// Work order of a one-pass attention launch over a cached cell table (kind 0
+// forward, 1 backward, 2 backward from the forward output), built once per
+// table and shape and kept with the table.
+Result<const void*> HipEngine::flash_order_(const void* cells, std::size_t batch, std::size_t M, std::size_t N,
+                                            std::size_t mask_bs, int kind)
+{
+    if (!cells) return static_cast<const void*>(nullptr);
+    for (CellTable& t : cells_)
+    {
+        if (t.cells->data() != cells) continue;
+        const bool pb = mask_bs != 0;
+        for (const OrderTable& o : t.orders)
+            if (o.batch == batch && o.N == N && o.kind == kind && o.per_batch == pb)
+                return static_cast<const void*>(o.buf->data());
+        NN_TRY(buf, scratch_(nnhip_flash_order_bytes(batch, M, N, kind)));
+        NN_CHECK(kernel_(nnhip_flash_build_order(cells, batch, M, N, mask_bs, kind, buf->data(), stream_),
+                         "attention work order"));
+        t.orders.push_back({batch, N, kind, pb, buf});
+        return static_cast<const void*>(buf->data());
+    }
+    return static_cast<const void*>(nullptr);
 }
 
 Result<void> HipEngine::settle_write_(const Tensor& t)
@@ -742,9 +765,11 @@ Result<void> HipEngine::settle_fwd_()
         l = t;
     }
     NN_TRY(cells, mask_cells_(f->mask ? &*f->mask : nullptr, f->M, f->N));
+    NN_TRY(order, flash_order_(cells, f->batch, f->M, f->N, 0, 0));
     NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(f->batch, f->M, f->N, f->Kd, 4, 0)));
-    return kernel_(nnhip_flash_forward(D(f->Q), D(f->K), nullptr, f->mask ? D(*f->mask) : nullptr, cells, W(f->m),
-                                       W(l), nullptr, f->batch, f->M, f->N, f->Kd, 4, f->alpha, ws->data(), stream_),
+    return kernel_(nnhip_flash_forward_ordered(D(f->Q), D(f->K), nullptr, f->mask ? D(*f->mask) : nullptr, cells,
+                                               W(f->m), W(l), nullptr, f->batch, f->M, f->N, f->Kd, 4, f->alpha, 0, 0,
+                                               0, order, ws->data(), stream_),
                    "batched_matmul_reduce");
 }
 
@@ -875,10 +900,11 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
         NN_TRY(l, alloc_(batch * p->M, 1));
         NN_TRY(cells, mask_cells_(&p->mask, p->M, p->N));
         const std::size_t bs = p->mask.rows() == p->M ? 0 : p->M * p->N;
+        NN_TRY(order, flash_order_(cells, batch, p->M, p->N, bs, 0));
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, p->M, p->N, p->Kd, Dv, 0)));
-        NN_CHECK(kernel_(nnhip_flash_forward_layout(D(p->Q), D(p->K), D(A), D(p->mask), cells, W(m), W(l), W(out),
-                                                    batch, p->M, p->N, p->Kd, Dv, p->alpha, bs, 1, 1, ws->data(),
-                                                    stream_),
+        NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(p->Q), D(p->K), D(A), D(p->mask), cells, W(m), W(l), W(out),
+                                                     batch, p->M, p->N, p->Kd, Dv, p->alpha, bs, 1, 1, order,
+                                                     ws->data(), stream_),
                          "attention forward"));
         p->m = m;
         p->l = l;
@@ -919,20 +945,23 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
         if (q.O.dev_ptr() && same_t(pds_->Vp, q.V) && q.V.rows() == batch * q.Kd)
         {
             // R from the forward output (same V): one key-line pass plus dQ from the stored dS.
+            NN_TRY(order, flash_order_(cells, batch, q.M, q.N, bs, 2));
             NN_TRY(ws, scratch_(nnhip_flash_ds_workspace_bytes(batch, q.M, q.N, q.Kd)));
-            NN_CHECK(kernel_(nnhip_flash_backward_ds(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), D(q.O), D(q.mask),
-                                                     cells, D(q.m), D(q.l), W(dQ), W(dK), W(dV), batch, q.M, q.N,
-                                                     q.Kd, q.alpha, pds_->alpha2, bs, ws->data(), stream_),
+            NN_CHECK(kernel_(nnhip_flash_backward_ds_ordered(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), D(q.O),
+                                                             D(q.mask), cells, D(q.m), D(q.l), W(dQ), W(dK), W(dV),
+                                                             batch, q.M, q.N, q.Kd, q.alpha, pds_->alpha2, bs, order,
+                                                             ws->data(), stream_),
                              "attention backward"));
         }
         else
         {
             NN_TRY(Rr, alloc_(batch * q.M, 1));
+            NN_TRY(order, flash_order_(cells, batch, q.M, q.N, bs, 1));
             NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, q.M, q.N, q.Kd, 4, 1)));
-            NN_CHECK(kernel_(nnhip_flash_backward_layout(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), nullptr, 0,
-                                                         D(q.mask), cells, D(q.m), D(q.l), W(Rr), W(dQ), W(dK), W(dV),
-                                                         batch, q.M, q.N, q.Kd, pds_->Kd2, q.alpha, pds_->alpha2, bs,
-                                                         1, ws->data(), stream_),
+            NN_CHECK(kernel_(nnhip_flash_backward_ordered(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), nullptr, 0,
+                                                          D(q.mask), cells, D(q.m), D(q.l), W(Rr), W(dQ), W(dK),
+                                                          W(dV), batch, q.M, q.N, q.Kd, pds_->Kd2, q.alpha,
+                                                          pds_->alpha2, bs, 1, order, ws->data(), stream_),
                              "attention backward"));
         }
         if (dv_here) pdv_.reset();
@@ -1578,9 +1607,11 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
         std::unique_ptr<PendingFwd> f = std::move(pfwd_);
         NN_TRY(o, alloc_(batch * d.M, V.cols()));
         NN_TRY(cells, mask_cells_(mask, d.M, d.N));
+        NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 0));
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, d.K, V.cols(), 0)));
-        NN_CHECK(kernel_(nnhip_flash_forward(D(A), D(B), D(V), mask ? D(*mask) : nullptr, cells, W(f->m), W(*f->l),
-                                             W(o), batch, d.M, d.N, d.K, V.cols(), alpha, ws->data(), stream_),
+        NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(A), D(B), D(V), mask ? D(*mask) : nullptr, cells, W(f->m),
+                                                     W(*f->l), W(o), batch, d.M, d.N, d.K, V.cols(), alpha, 0, 0, 0,
+                                                     order, ws->data(), stream_),
                          "batched_matmul_softmax_apply"));
         return o;
     }
@@ -1657,10 +1688,12 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
         std::unique_ptr<PendingBwd> q = std::move(pbwd_);
         const PendingGemm& g = *pgemm_;
         NN_TRY(cells, mask_cells_(mask, d.M, d.N));
+        NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 1));
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, std::max(d.K, g.K), 4, 1)));
-        NN_CHECK(kernel_(nnhip_flash_backward(D(A), D(B), D(g.A), D(g.B), D(G), G.cols(), mask ? D(*mask) : nullptr,
-                                              cells, D(row_max), D(denom), W(q->R), W(q->dQ), W(dk), W(dv), batch,
-                                              d.M, d.N, d.K, g.K, alpha, g.alpha, ws->data(), stream_),
+        NN_CHECK(kernel_(nnhip_flash_backward_ordered(D(A), D(B), D(g.A), D(g.B), D(G), G.cols(),
+                                                      mask ? D(*mask) : nullptr, cells, D(row_max), D(denom),
+                                                      W(q->R), W(q->dQ), W(dk), W(dv), batch, d.M, d.N, d.K, g.K,
+                                                      alpha, g.alpha, 0, 0, order, ws->data(), stream_),
                          "batched_matmul_softmax_backward_kv"));
         grad_v_out = dv;
         return dk;

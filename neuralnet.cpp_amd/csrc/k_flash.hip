@@ -128,12 +128,21 @@ struct Item
 {
     int b, grp, rg;
 };
-// Batch entry, line group and range of this workgroup. Groups run heaviest
-// first (with causal masks later groups have more cells), so the dispatcher
-// backfills CUs that finish light groups.
+// Batch entry, line group and range of this workgroup. With an order table
+// (k_flash_order: items by cell count, laid out so that each CU's resident
+// workgroups add up to about the same work) the workgroup takes the item the
+// table names; an entry outside the grid is never used (identity instead).
+// Without one, groups run heaviest first within each batch entry (with causal
+// masks later groups have more cells).
 __device__ __forceinline__ Item item_of(const FlashGeo& g)
 {
-    const int it = xcd_item(blockIdx.x, gridDim.x), per = g.G * g.NR;
+    int it = xcd_item(blockIdx.x, gridDim.x);
+    if (g.order)
+    {
+        const int o = g.order[blockIdx.x];
+        it = (o >= 0 && o < static_cast<int>(gridDim.x)) ? o : static_cast<int>(blockIdx.x);
+    }
+    const int per = g.G * g.NR;
     Item r;
     r.b = it / per;
     const int rem = it % per;
@@ -1099,6 +1108,99 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a,
     rows_store<KP>(a, g, lw, b, line, rg, 0.0f, x, y);
 }
 
+// Work order of a flash launch (one workgroup of 1024 threads). The weight of
+// an item (batch entry, line group, range) is the number of cells of its range
+// that at least one of its 4 lines has to visit (mask cell class != 0); the
+// kernel time is set by the most loaded CU, so items are sorted heaviest first
+// (counting sort, weights 0..R) and sorted position p is given to workgroup
+//   p < resident:  ncu r + (r even ? q : n_r - 1 - q),  r = p / ncu, q = p % ncu
+//   p >= resident: p
+// (n_r: items in round r, ncu unless it is the last, partial round)
+// (ncu = CUs; resident = workgroups per CU x ncu). Workgroups are dispatched
+// round-robin over the CUs, so round r of resident workgroups runs together and
+// the serpentine gives every CU one heavy and one light item per pair of
+// rounds; later workgroups backfill CUs as they free up, heaviest first. Items
+// of equal weight may be placed in any order (only the timing depends on it).
+constexpr int kOrderThreads = 1024;
+__global__ __launch_bounds__(kOrderThreads) void k_flash_order(FlashGeo g, int rows, int nitems, int ncu,
+                                                               int resident, int* __restrict__ order,
+                                                               unsigned char* __restrict__ weight)
+{
+    __shared__ int count[65], cursor[65];
+    const int t = threadIdx.x, lines = rows ? g.RT : g.CT, cells = rows ? g.CT : g.RT, per = g.G * g.NR;
+    if (t < 65) count[t] = 0;
+    __syncthreads();
+    for (int it = t; it < nitems; it += kOrderThreads)
+    {
+        const int b = it / per, rem = it % per, grp = g.G - 1 - rem / g.NR, rg = rem % g.NR;
+        const unsigned char* cls = g.cls + (long)b * g.cls_bs;
+        const int x0 = rg * g.R, x1 = min(x0 + g.R, cells), l0 = grp * kWaves;
+        int w = 0;
+        if ((g.CT & 3) == 0)
+        {
+            // 32-bit reads (the table and every row start at multiples of 4 bytes): rows: 4 cells of
+            // one line per word, OR over the 4 lines; columns: the 4 lines of one cell per word.
+            if (rows)
+            {
+                for (int x = x0; x < x1; x += 4)
+                {
+                    unsigned u = 0;
+#pragma unroll
+                    for (int k = 0; k < kWaves; ++k)
+                        if (l0 + k < lines) u |= *reinterpret_cast<const unsigned*>(cls + (long)(l0 + k) * g.CT + x);
+                    w += ((u & 0xffu) != 0) + ((u & 0xff00u) != 0) + ((u & 0xff0000u) != 0) + ((u >> 24) != 0);
+                }
+            }
+            else
+            {
+                const int valid = min(kWaves, lines - l0);
+                const unsigned keep = valid >= 4 ? ~0u : (1u << (8 * valid)) - 1u;
+                for (int x = x0; x < x1; ++x)
+                    w += (*reinterpret_cast<const unsigned*>(cls + (long)x * g.CT + l0) & keep) != 0;
+            }
+        }
+        else
+        {
+            for (int x = x0; x < x1; ++x)
+            {
+                bool any = false;
+                for (int k = 0; k < kWaves; ++k)
+                {
+                    const int line = l0 + k;
+                    if (line < lines)
+                        any = any || (rows ? cls[(long)line * g.CT + x] : cls[(long)x * g.CT + line]) != 0;
+                }
+                w += any ? 1 : 0;
+            }
+        }
+        weight[it] = static_cast<unsigned char>(w);
+        atomicAdd(&count[w], 1);
+    }
+    __syncthreads();
+    if (t == 0)
+    {
+        int acc = 0;
+        for (int w = 64; w >= 0; --w)
+        {
+            cursor[w] = acc;
+            acc += count[w];
+        }
+    }
+    __syncthreads();
+    for (int it = t; it < nitems; it += kOrderThreads)
+    {
+        const int p = atomicAdd(&cursor[weight[it]], 1);
+        int bid = p;
+        if (p < resident)
+        {
+            // a last, partial round is reversed within its own n items: bid stays below nitems
+            const int r = p / ncu, q = p % ncu, n = min(ncu, nitems - r * ncu);
+            bid = r * ncu + ((r & 1) ? n - 1 - q : q);
+        }
+        order[bid] = it;
+    }
+}
+
 // R_i = alpha2 sum_d dO(d, i) O(d, i): per batch (Kd, M) dim-major operands.
 __global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ dO, const float* __restrict__ O,
                                                       float* __restrict__ R, int M, int Kd, long total, float alpha2)
@@ -1179,6 +1281,7 @@ FlashGeo geo(size_t batch, size_t M, size_t N, bool rows, int pw, const unsigned
     g.cls = cls;
     g.cls_bs = per_batch_cls ? static_cast<long>(g.RT) * g.CT : 0;
     g.part = static_cast<float*>(ws);
+    g.order = nullptr;
     return g;
 }
 
@@ -1193,20 +1296,58 @@ unsigned grid_of(const FlashGeo& g, size_t batch)
     return static_cast<unsigned>(batch * static_cast<size_t>(g.G) * g.NR);
 }
 
+// One order table: the workgroup -> item map, then the item weights.
+size_t order_table_bytes(const FlashGeo& g, size_t batch)
+{
+    const size_t n = grid_of(g, batch);
+    return align256(n * sizeof(int)) + align256(n);
+}
+
+// CUs of the current device (cached per device).
+int device_cus()
+{
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0)
+    {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Builds g's order table at `at` (order_table_bytes(g, batch) bytes); `resident`:
+// workgroups of the kernel per CU.
+int build_order(const FlashGeo& g, size_t batch, bool rows, int resident, char* at, hipStream_t s)
+{
+    const size_t n = grid_of(g, batch);
+    if (n == 0) return 0;
+    int* order = reinterpret_cast<int*>(at);
+    unsigned char* weight = reinterpret_cast<unsigned char*>(at + align256(n * sizeof(int)));
+    const int ncu = device_cus();
+    hipLaunchKernelGGL(k_flash_order, dim3(1), dim3(kOrderThreads), 0, s, g, rows ? 1 : 0, static_cast<int>(n), ncu,
+                       resident * ncu, order, weight);
+    return launch_status();
+}
+
 int fwd_pw(int DP) { return 64 + 32 * DP; }
 int rows_pw(int KP) { return 32 + 64 * KP; }
 int cols_pw(int KP) { return 64 * KP; }
 
 template <int KP, int DP, bool WITH_O>
-int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g, size_t batch, hipStream_t s)
+int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g0, size_t batch, const int* order, hipStream_t s)
 {
     // Cells per step: one cell (3 workgroups per CU: 35 KB of LDS, <= 168
     // VGPRs) when a line range holds >= 32 cells, two (2 per CU) for shorter
     // ranges, where fewer barriers per cell pay more. Measured: causal
     // (96 x 1024)^2 58 -> 71 TFLOP/s with one; causal (128 x 512)^2 and the
     // document-masked rows 3-4 % faster with two.
-    const dim3 grid(grid_of(g, batch)), block(64 * kWaves);
-    const bool one = std::min(g.R, g.CT) >= 32;
+    const dim3 grid(grid_of(g0, batch)), block(64 * kWaves);
+    const bool one = std::min(g0.R, g0.CT) >= 32;
+    FlashGeo g = g0;
+    g.order = order;
     if (WITH_O && a.v_dm)
     {
         if (one) hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true, 1>), grid, block, 0, s, a, g);
@@ -1225,8 +1366,12 @@ int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g, size_t batch, hipStream
 }
 
 template <int KP>
-int launch_bwd(const FlashBwdArgs& a, const FlashGeo& gr, const FlashGeo& gc, size_t batch, hipStream_t s)
+int launch_bwd(const FlashBwdArgs& a, const FlashGeo& gr0, const FlashGeo& gc0, size_t batch,
+               const int* order_rows, const int* order_cols, hipStream_t s)
 {
+    FlashGeo gr = gr0, gc = gc0;
+    gr.order = order_rows;
+    gc.order = order_cols;
     hipLaunchKernelGGL((k_flash_bwd_rows<KP>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, a, gr);
     if (int rc = launch_status()) return rc;
     if (gr.NR > 1)
@@ -1282,18 +1427,51 @@ size_t flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t 
                     part_bytes(geo(batch, M, N, false, cols_pw(KP), nullptr, nullptr), batch, false));
 }
 
-int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batch, void* ws, hipStream_t s)
+// Order tables (k_flash_order) for a call with a mask cell table: kind 0 the
+// forward (one table), 1 the backward (query lines, then key lines), 2 the
+// backward from the forward output (key lines, then the dQ pass). They depend
+// on the cell table and (batch, M, N) only.
+size_t flash_order_bytes(size_t batch, size_t M, size_t N, int kind)
+{
+    const FlashGeo gr = geo(batch, M, N, true, 0, nullptr, nullptr);
+    if (kind == 0) return order_table_bytes(gr, batch);
+    const FlashGeo gc = geo(batch, M, N, false, 0, nullptr, nullptr);
+    return order_table_bytes(gr, batch) + order_table_bytes(gc, batch);
+}
+
+int flash_build_order(const unsigned char* cells, size_t batch, size_t M, size_t N, bool per_batch_cls, int kind,
+                      void* out, hipStream_t s)
+{
+    char* at = static_cast<char*>(out);
+    const FlashGeo gr = geo(batch, M, N, true, 0, cells, nullptr, per_batch_cls);
+    const FlashGeo gc = geo(batch, M, N, false, 0, cells, nullptr, per_batch_cls);
+    if (kind == 0) return build_order(gr, batch, true, std::min(gr.R, gr.CT) >= 32 ? 3 : 2, at, s);
+    if (kind == 1)
+    {
+        if (int rc = build_order(gr, batch, true, 2, at, s)) return rc;
+        return build_order(gc, batch, false, 2, at + order_table_bytes(gr, batch), s);
+    }
+    if (int rc = build_order(gc, batch, false, 2, at, s)) return rc;
+    return build_order(gr, batch, true, 3, at + order_table_bytes(gc, batch), s);
+}
+
+int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batch, void* ws, const int* order,
+                  hipStream_t s)
 {
     const int KP = pad32(static_cast<size_t>(a.K)), DP = a.O ? pad32(static_cast<size_t>(a.D)) : 32;
     const FlashGeo g = geo(batch, static_cast<size_t>(a.M), static_cast<size_t>(a.N), true, fwd_pw(DP),
                            a.mask ? cells : nullptr, ws, a.mask && a.mask_bs != 0);
     if (g.NR > 1 && !ws) return -1;
-    if (!a.O) return KP == 32 ? launch_fwd<32, 32, false>(a, g, batch, s) : launch_fwd<64, 32, false>(a, g, batch, s);
-    if (KP == 32) return DP == 32 ? launch_fwd<32, 32, true>(a, g, batch, s) : launch_fwd<32, 64, true>(a, g, batch, s);
-    return DP == 32 ? launch_fwd<64, 32, true>(a, g, batch, s) : launch_fwd<64, 64, true>(a, g, batch, s);
+    const int* ow = a.mask ? order : nullptr;
+    if (!a.O)
+        return KP == 32 ? launch_fwd<32, 32, false>(a, g, batch, ow, s) : launch_fwd<64, 32, false>(a, g, batch, ow, s);
+    if (KP == 32)
+        return DP == 32 ? launch_fwd<32, 32, true>(a, g, batch, ow, s) : launch_fwd<32, 64, true>(a, g, batch, ow, s);
+    return DP == 32 ? launch_fwd<64, 32, true>(a, g, batch, ow, s) : launch_fwd<64, 64, true>(a, g, batch, ow, s);
 }
 
-int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t batch, void* ws, hipStream_t s)
+int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t batch, void* ws, const int* order,
+                   hipStream_t s)
 {
     const int KP = pad32(static_cast<size_t>(std::max(a.K, a.Kd)));
     const unsigned char* cl = a.mask ? cells : nullptr;
@@ -1303,7 +1481,11 @@ int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t bat
     const FlashGeo gc =
         geo(batch, static_cast<size_t>(a.M), static_cast<size_t>(a.N), false, cols_pw(KP), cl, ws, pb);
     if ((gr.NR > 1 || gc.NR > 1) && !ws) return -1;
-    return KP == 32 ? launch_bwd<32>(a, gr, gc, batch, s) : launch_bwd<64>(a, gr, gc, batch, s);
+    const int* orr = a.mask ? order : nullptr;
+    const int* occ = orr ? reinterpret_cast<const int*>(reinterpret_cast<const char*>(orr) +
+                                                         order_table_bytes(gr, batch))
+                         : nullptr;
+    return KP == 32 ? launch_bwd<32>(a, gr, gc, batch, orr, occ, s) : launch_bwd<64>(a, gr, gc, batch, orr, occ, s);
 }
 
 size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K)
@@ -1315,7 +1497,7 @@ size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K)
 }
 
 int flash_backward_ds(const FlashBwdArgs& a0, const float* O, const unsigned char* cells, size_t batch, void* ws,
-                      hipStream_t s)
+                      const int* order, hipStream_t s)
 {
     if (!ws || a0.K != a0.Kd) return -1;
     FlashBwdArgs a = a0;
@@ -1329,8 +1511,13 @@ int flash_backward_ds(const FlashBwdArgs& a0, const float* O, const unsigned cha
     const int KP = pad32(static_cast<size_t>(a.K));
     const unsigned char* cl = a.mask ? cells : nullptr;
     const bool pb = a.mask && a.mask_bs != 0;
-    const FlashGeo gr = geo(batch, M, N, true, rows_pw(KP), cl, w, pb);
-    const FlashGeo gc = geo(batch, M, N, false, cols_pw(KP), cl, w, pb);
+    FlashGeo gr = geo(batch, M, N, true, rows_pw(KP), cl, w, pb);
+    FlashGeo gc = geo(batch, M, N, false, cols_pw(KP), cl, w, pb);
+    if (a.mask && order)
+    {
+        gc.order = order;
+        gr.order = reinterpret_cast<const int*>(reinterpret_cast<const char*>(order) + order_table_bytes(gc, batch));
+    }
     const long total = static_cast<long>(batch * M);
     hipLaunchKernelGGL(k_flash_rowdot, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, a.dO, O,
                        a.R, a.M, a.Kd, total, a.alpha2);
@@ -1373,6 +1560,17 @@ extern "C" int nnhip_flash_backward_ds(const float* Q, const float* Kt, const fl
                                        size_t N, size_t K, float alpha, float alpha2, size_t mask_batch_stride,
                                        void* workspace, void* stream)
 {
+    return nnhip_flash_backward_ds_ordered(Q, Kt, dO, Vp, O, mask, cells, m, l, dQ, dK, dV, batch, M, N, K, alpha,
+                                           alpha2, mask_batch_stride, nullptr, workspace, stream);
+}
+
+extern "C" int nnhip_flash_backward_ds_ordered(const float* Q, const float* Kt, const float* dO, const float* Vp,
+                                               const float* O, const float* mask, const void* cells, const float* m,
+                                               const float* l, float* dQ, float* dK, float* dV, size_t batch,
+                                               size_t M, size_t N, size_t K, float alpha, float alpha2,
+                                               size_t mask_batch_stride, const void* order, void* workspace,
+                                               void* stream)
+{
     if (!Q || !Kt || !dO || !Vp || !O || !m || !l || !dQ || !dK || !dV || !workspace || (mask && !cells)) return -1;
     if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
     if (!nnhip::flash_supported(batch, M, N, K, 4) || K % 4 != 0) return -3;
@@ -1381,7 +1579,7 @@ extern "C" int nnhip_flash_backward_ds(const float* Q, const float* Kt, const fl
                           alpha2};
     a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
     return nnhip::flash_backward_ds(a, O, static_cast<const unsigned char*>(cells), batch, workspace,
-                                    static_cast<hipStream_t>(stream));
+                                    static_cast<const int*>(order), static_cast<hipStream_t>(stream));
 }
 
 extern "C" int nnhip_flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D)
@@ -1424,6 +1622,16 @@ extern "C" int nnhip_flash_forward_layout(const float* Q, const float* Kt, const
                                           size_t N, size_t K, size_t D, float alpha, size_t mask_batch_stride,
                                           int v_dim_major, int o_dim_major, void* workspace, void* stream)
 {
+    return nnhip_flash_forward_ordered(Q, Kt, V, mask, cells, m, l, O, batch, M, N, K, D, alpha, mask_batch_stride,
+                                       v_dim_major, o_dim_major, nullptr, workspace, stream);
+}
+
+extern "C" int nnhip_flash_forward_ordered(const float* Q, const float* Kt, const float* V, const float* mask,
+                                           const void* cells, float* m, float* l, float* O, size_t batch, size_t M,
+                                           size_t N, size_t K, size_t D, float alpha, size_t mask_batch_stride,
+                                           int v_dim_major, int o_dim_major, const void* order, void* workspace,
+                                           void* stream)
+{
     if (!Q || !Kt || !m || !l || (O && !V) || (mask && !cells)) return -1;
     if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
     if (!nnhip::flash_supported(batch, M, N, K, O ? D : 4)) return -3;
@@ -1433,7 +1641,7 @@ extern "C" int nnhip_flash_forward_layout(const float* Q, const float* Kt, const
     a.v_dm = v_dim_major ? 1 : 0;
     a.o_dm = o_dim_major ? 1 : 0;
     return nnhip::flash_forward(a, static_cast<const unsigned char*>(cells), batch, workspace,
-                                static_cast<hipStream_t>(stream));
+                                static_cast<const int*>(order), static_cast<hipStream_t>(stream));
 }
 
 extern "C" int nnhip_flash_backward(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* G,
@@ -1453,6 +1661,17 @@ extern "C" int nnhip_flash_backward_layout(const float* Q, const float* Kt, cons
                                            float alpha2, size_t mask_batch_stride, int g_is_do, void* workspace,
                                            void* stream)
 {
+    return nnhip_flash_backward_ordered(Q, Kt, dO, Vp, G, ldg, mask, cells, m, l, R, dQ, dK, dV, batch, M, N, K, Kd,
+                                        alpha, alpha2, mask_batch_stride, g_is_do, nullptr, workspace, stream);
+}
+
+extern "C" int nnhip_flash_backward_ordered(const float* Q, const float* Kt, const float* dO, const float* Vp,
+                                            const float* G, size_t ldg, const float* mask, const void* cells,
+                                            const float* m, const float* l, float* R, float* dQ, float* dK,
+                                            float* dV, size_t batch, size_t M, size_t N, size_t K, size_t Kd,
+                                            float alpha, float alpha2, size_t mask_batch_stride, int g_is_do,
+                                            const void* order, void* workspace, void* stream)
+{
     if (!Q || !Kt || !dO || !Vp || (!G && !g_is_do) || !m || !l || !R || !dQ || !dK || !dV || (mask && !cells))
         return -1;
     if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
@@ -1466,5 +1685,20 @@ extern "C" int nnhip_flash_backward_layout(const float* Q, const float* Kt, cons
     a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
     a.g_do = g_is_do ? 1 : 0;
     return nnhip::flash_backward(a, static_cast<const unsigned char*>(cells), batch, workspace,
-                                 static_cast<hipStream_t>(stream));
+                                 static_cast<const int*>(order), static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t nnhip_flash_order_bytes(size_t batch, size_t M, size_t N, int kind)
+{
+    if (kind < 0 || kind > 2 || batch == 0 || M == 0 || N == 0) return 0;
+    return nnhip::flash_order_bytes(batch, M, N, kind);
+}
+
+extern "C" int nnhip_flash_build_order(const void* cells, size_t batch, size_t M, size_t N, size_t mask_batch_stride,
+                                       int kind, void* order, void* stream)
+{
+    if (!cells || !order || kind < 0 || kind > 2) return -1;
+    if (!nnhip::flash_supported(batch, M, N, 1, 4)) return -3;
+    return nnhip::flash_build_order(static_cast<const unsigned char*>(cells), batch, M, N, mask_batch_stride != 0,
+                                    kind, order, static_cast<hipStream_t>(stream));
 }

@@ -167,15 +167,25 @@ private:
 
     // Mask cell tables of the one-pass attention kernels, kept per mask tensor
     // (most recent last) until the mask is written in place or evicted.
+    struct OrderTable
+    {
+        std::size_t batch, N;
+        int kind;
+        bool per_batch;
+        std::shared_ptr<DeviceBuffer> buf;
+    };
     struct CellTable
     {
         Tensor mask;
         std::shared_ptr<DeviceBuffer> cells;
         std::size_t M;   // rows of one mask (the tensor holds rows / M of them)
+        std::vector<OrderTable> orders;   // work orders of the launches over this table
     };
     std::vector<CellTable> cells_;
     std::vector<std::weak_ptr<DeviceBuffer>> views_;   // live row-slice views (HipView)
     Result<const void*> mask_cells_(const Tensor* mask, std::size_t M, std::size_t N);
+    Result<const void*> flash_order_(const void* cells, std::size_t batch, std::size_t M, std::size_t N,
+                                     std::size_t mask_bs, int kind);
 
     struct PendingFwd;
     struct PendingGemm;
