@@ -59,9 +59,9 @@ int nnhip_gemm_epilogue(const float* A, const float* B, float* C, size_t A_rows,
  * batch) bytes of workspace, so the results are identical. Returns -6, launching nothing, when that
  * workspace size exceeds NNHIP_GEMM_NOALLOC_SCRATCH_BYTES: products whose output grid fills the GPU need
  * none; among the config-4 step's, the long-K ones into small outputs (768 x 8192 from K = 6144 or
- * 32000, the 6144 x 768 weight gradient) need 96-108 MiB and are rejected. All calls on one GPU share its
- * scratch: calls that may overlap in time on one GPU (other streams, other threads) race and must be
- * ordered by the caller. */
+ * 32000, the 6144 x 768 and 768 x 3072 weight gradients) need 72-144 MiB and are rejected. All calls on
+ * one GPU share its scratch: calls that may overlap in time on one GPU (other streams, other threads) race
+ * and must be ordered by the caller. */
 #define NNHIP_GEMM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int nnhip_gemm_noalloc(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
                        size_t B_cols, size_t batch, int transA, int transB, float alpha, void* stream);

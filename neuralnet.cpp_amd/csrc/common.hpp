@@ -98,6 +98,21 @@ inline unsigned grid_for(size_t work, unsigned per_block, unsigned cap = 1u << 2
 }
 
 // Launch status of the last kernel on this thread, as a C-ABI return code.
+// CUs of the current device (cached per device; 256 when the query fails).
+inline int device_cus()
+{
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0)
+    {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 inline int launch_status()
 {
     const hipError_t e = hipGetLastError();

@@ -1303,21 +1303,6 @@ size_t order_table_bytes(const FlashGeo& g, size_t batch)
     return align256(n * sizeof(int)) + align256(n);
 }
 
-// CUs of the current device (cached per device).
-int device_cus()
-{
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0)
-    {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
 // Builds g's order table at `at` (order_table_bytes(g, batch) bytes); `resident`:
 // workgroups of the kernel per CU.
 int build_order(const FlashGeo& g, size_t batch, bool rows, int resident, char* at, hipStream_t s)

@@ -480,6 +480,33 @@ Plan plan_gemm(size_t M, size_t N, size_t K, size_t batch, bool allow_split)
             p.splits = static_cast<int>((K + ks - 1) / ks);
         }
     };
+    // Mid-sized outputs with K >= 2048: split K so that the workgroups make whole
+    // rounds of 3 per CU (768 on MI355X); the first of 256x128, 128x128, 128x64
+    // whose split leaves >= 1024 of K per slice (measured on the config-3/4
+    // shapes: 6144x768 K8192 NT 110 -> 123, 768x3072 K8192 NT 105 -> 115,
+    // 768x8192 K3072 NN 121 -> 124 TFLOP/s; round counts that are not whole lose
+    // the fraction).
+    if (M > 64 && N > 64 && allow_split && K >= 2048 && tiles(256, 128) < 512)
+    {
+        const size_t round = 3 * static_cast<size_t>(device_cus());
+        const Cfg cs[3] = {kTall, kSquare, kThinWaves};
+        const int bms[3] = {256, 128, 128}, bns[3] = {128, 128, 64};
+        for (int i = 0; i < 3; ++i)
+        {
+            const size_t t = tiles(bms[i], bns[i]);
+            size_t s = 1;
+            while (s <= 64 && (t * s) % round != 0) ++s;
+            if (s > 64) continue;
+            const size_t ks = ((K + s - 1) / s + 31) / 32 * 32;
+            if (ks < 1024) continue;
+            p.cfg = cs[i];
+            p.bm = bms[i];
+            p.bn = bns[i];
+            p.k_split = static_cast<int>(ks);
+            p.splits = static_cast<int>((K + ks - 1) / ks);
+            return p;
+        }
+    }
     if (M <= 64) { p.cfg = kThinWavesM64; p.bm = 64; p.bn = 128; }
     else if (N <= 64) { p.cfg = kSkinnyN; p.bm = 256; p.bn = 64; }
     else if (tiles(256, 128) >= 512) { p.cfg = kTall; p.bm = 256; p.bn = 128; }

@@ -51,7 +51,7 @@ def _pair(hip, lib, M, N, K, batch, tA, tB, alpha, seed):
 
 
 @pytest.mark.parametrize("first,second", [
-    ((768, 3072, 8192, 1, False, True), (256, 384, 2048, 1, False, True)),    # split-K twice, smaller second
+    ((768, 2048, 8192, 1, False, True), (256, 384, 2048, 1, False, True)),    # split-K twice, smaller second
     ((768, 768, 8192, 1, False, True), (100, 70, 3001, 1, True, False)),      # weight-gradient shape, ragged
     ((1024, 64, 1024, 12, False, True), (300, 200, 1500, 1, False, False)),   # batched split-K, ragged
     ((512, 1024, 256, 2, True, False), (37, 53, 29, 1, True, True)),          # no split at all
@@ -67,7 +67,7 @@ def test_noalloc_matches_gemm_twice(hip, first, second):
 
 
 def test_noalloc_rejects_beyond_scratch(hip):
-    """The 6144 x 768 weight gradient over 8192 tokens splits K into partials of 108 MiB: rejected with
+    """The 6144 x 768 weight gradient over 8192 tokens splits K into partials of 144 MiB: rejected with
     -6 on the host, nothing launched (the output keeps its contents)."""
     lib = _lib()
     M, N, K = 6144, 768, 8192
