@@ -320,28 +320,36 @@ __global__ __launch_bounds__(kThreads) void k_adam_list(AdamList L)
                        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(g)) & 15u) == 0;
     if (vec && base + kAdamBlockFloats <= n)
     {
-        // A whole block of float4s: every load issued before any update.
-        float4 pp[4], mm[4], vv[4], gg[4];
+        // A whole block of float4s: every load issued before any update. Each
+        // value is read and written once per step, so the accesses are
+        // non-temporal (streamed past the caches).
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        f4 pp[4], mm[4], vv[4], gg[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k)
         {
             const size_t i = base + (static_cast<size_t>(k) * kThreads + threadIdx.x) * 4;
-            pp[k] = *reinterpret_cast<const float4*>(p + i);
-            mm[k] = *reinterpret_cast<const float4*>(m + i);
-            vv[k] = *reinterpret_cast<const float4*>(v + i);
-            gg[k] = *reinterpret_cast<const float4*>(g + i);
+            pp[k] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p + i));
+            mm[k] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(m + i));
+            vv[k] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(v + i));
+            gg[k] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(g + i));
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k)
         {
             const size_t i = base + (static_cast<size_t>(k) * kThreads + threadIdx.x) * 4;
-            adam_elem(pp[k].x, mm[k].x, vv[k].x, gg[k].x, L.a);
-            adam_elem(pp[k].y, mm[k].y, vv[k].y, gg[k].y, L.a);
-            adam_elem(pp[k].z, mm[k].z, vv[k].z, gg[k].z, L.a);
-            adam_elem(pp[k].w, mm[k].w, vv[k].w, gg[k].w, L.a);
-            *reinterpret_cast<float4*>(p + i) = pp[k];
-            *reinterpret_cast<float4*>(m + i) = mm[k];
-            *reinterpret_cast<float4*>(v + i) = vv[k];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                float pe = pp[k][e], me = mm[k][e], ve = vv[k][e];
+                adam_elem(pe, me, ve, gg[k][e], L.a);
+                pp[k][e] = pe;
+                mm[k][e] = me;
+                vv[k][e] = ve;
+            }
+            __builtin_nontemporal_store(pp[k], reinterpret_cast<f4*>(p + i));
+            __builtin_nontemporal_store(mm[k], reinterpret_cast<f4*>(m + i));
+            __builtin_nontemporal_store(vv[k], reinterpret_cast<f4*>(v + i));
         }
         return;
     }

@@ -147,25 +147,44 @@ __global__ __launch_bounds__(kThreads) void k_ce_combine(const float* L, const f
 }
 
 // The same over many chunks (one per 256-row block of a product's statistics):
-// a workgroup owns 64 columns, its 4 waves merge a quarter of the chunks each
-// (in chunk order), then wave 0 merges the 4 results in wave order.
-__global__ __launch_bounds__(kThreads) void k_ce_combine_wide(const float* L, const float* labels, const float* mask,
-                                                              const float* part_m, const float* part_s, float* col_m,
-                                                              float* col_s, float* loss_vec, size_t chunks, size_t C,
-                                                              size_t N, size_t vocab)
+// a workgroup owns 64 columns, its 16 waves merge a sixteenth of the chunks
+// each (loads first, then in chunk order), then wave 0 merges the 16 results
+// in wave order.
+constexpr unsigned kWideWaves = 16, kWideBatch = 8;
+__global__ __launch_bounds__(64 * kWideWaves) void k_ce_combine_wide(const float* L, const float* labels,
+                                                                     const float* mask, const float* part_m,
+                                                                     const float* part_s, float* col_m, float* col_s,
+                                                                     float* loss_vec, size_t chunks, size_t C,
+                                                                     size_t N, size_t vocab)
 {
-    __shared__ float sm[kWaves][64], ss[kWaves][64];
+    __shared__ float sm[kWideWaves][64], ss[kWideWaves][64];
     const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const size_t c = static_cast<size_t>(blockIdx.x) * 64 + lane;
-    const size_t per = (chunks + kWaves - 1) / kWaves, k0 = wave * per, k1 = k0 + per < chunks ? k0 + per : chunks;
+    const size_t per = (chunks + kWideWaves - 1) / kWideWaves, k0 = wave * per,
+                 k1 = k0 + per < chunks ? k0 + per : chunks;
     float m = -__builtin_huge_valf(), s = 0.0f;
     if (c < N)
-        for (size_t k = k0; k < k1; ++k) merge(m, s, part_m[k * N + c], part_s[k * N + c]);
+    {
+        size_t k = k0;
+        for (; k + kWideBatch <= k1; k += kWideBatch)
+        {
+            float pm[kWideBatch], ps[kWideBatch];
+#pragma unroll
+            for (unsigned j = 0; j < kWideBatch; ++j)
+            {
+                pm[j] = part_m[(k + j) * N + c];
+                ps[j] = part_s[(k + j) * N + c];
+            }
+#pragma unroll
+            for (unsigned j = 0; j < kWideBatch; ++j) merge(m, s, pm[j], ps[j]);
+        }
+        for (; k < k1; ++k) merge(m, s, part_m[k * N + c], part_s[k * N + c]);
+    }
     sm[wave][lane] = m;
     ss[wave][lane] = s;
     __syncthreads();
     if (wave != 0 || c >= N) return;
-    for (unsigned w = 1; w < kWaves; ++w) merge(m, s, sm[w][lane], ss[w][lane]);
+    for (unsigned w = 1; w < kWideWaves; ++w) merge(m, s, sm[w][lane], ss[w][lane]);
     const size_t lbl = label_of(labels[c]);
     const bool valid = (!mask || mask[c] >= 0.5f) && lbl < vocab;
     col_m[c] = m;
@@ -299,30 +318,33 @@ __global__ __launch_bounds__(kThreads) void k_ce_grad4(const float* L, const flo
         at(f, e) = at(sv, e) != 0.0f ? inv / at(sv, e) : 0.0f;
         lbl[e] = at(sv, e) != 0.0f ? label_of(at(lb, e)) : ~size_t{0};
     }
-    const float4* __restrict__ L4 = reinterpret_cast<const float4*>(L);
-    float4* __restrict__ G4 = reinterpret_cast<float4*>(grad);
-    auto one = [&](const float4& x, size_t r) {
-        float4 gv;
+    // The logits are read once and the gradient written once (each 4 bytes x C x N, far more than the
+    // caches hold): non-temporal accesses.
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4* __restrict__ L4 = reinterpret_cast<const f4*>(L);
+    f4* __restrict__ G4 = reinterpret_cast<f4*>(grad);
+    auto one = [&](const f4& x, size_t r) {
+        f4 gv;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
         {
-            float gg = at(f, e) * __expf(at(x, e) - at(m, e));
+            float gg = at(f, e) * __expf(x[e] - at(m, e));
             if (lbl[e] == r) gg -= inv;
-            at(gv, e) = gg;
+            gv[e] = gg;
         }
-        G4[r * N4 + c4] = gv;
+        __builtin_nontemporal_store(gv, G4 + r * N4 + c4);
     };
     constexpr unsigned kBatch = 4;   // rows whose loads are in flight together
     size_t r = r0 + wave;
     for (; r + (kBatch - 1) * kWaves < r1; r += kBatch * kWaves)
     {
-        float4 x[kBatch];
+        f4 x[kBatch];
 #pragma unroll
-        for (unsigned k = 0; k < kBatch; ++k) x[k] = L4[(r + k * kWaves) * N4 + c4];
+        for (unsigned k = 0; k < kBatch; ++k) x[k] = __builtin_nontemporal_load(L4 + (r + k * kWaves) * N4 + c4);
 #pragma unroll
         for (unsigned k = 0; k < kBatch; ++k) one(x[k], r + k * kWaves);
     }
-    for (; r < r1; r += kWaves) one(L4[r * N4 + c4], r);
+    for (; r < r1; r += kWaves) one(__builtin_nontemporal_load(L4 + r * N4 + c4), r);
 }
 
 // ── row softmax ─────────────────────────────────────────────────────────────
@@ -555,7 +577,7 @@ extern "C" int nnhip_col_softmax_sparse_forward(const float* logits, const float
     else
         hipLaunchKernelGGL(k_col_stats<false>, dim3(static_cast<unsigned>(p.col_blocks), static_cast<unsigned>(p.chunks)),
                            dim3(kThreads), 0, s, logits, nullptr, pm, ps, C, N, p.rows_per_chunk);
-    hipLaunchKernelGGL(k_ce_combine_wide, dim3(static_cast<unsigned>((N + 63) / 64)), dim3(kThreads), 0, s, logits,
+    hipLaunchKernelGGL(k_ce_combine_wide, dim3(static_cast<unsigned>((N + 63) / 64)), dim3(64 * kWideWaves), 0, s, logits,
                        labels, mask, pm, ps, cm, cs, loss_vec, p.chunks, C, N, vocab_size);
     if (v4)
     {
@@ -582,7 +604,7 @@ extern "C" int nnhip_col_softmax_sparse_from_stats(const float* logits, const fl
     auto s = static_cast<hipStream_t>(stream);
     float* cm = static_cast<float*>(workspace);
     float* cs = cm + N;
-    hipLaunchKernelGGL(k_ce_combine_wide, dim3(static_cast<unsigned>((N + 63) / 64)), dim3(kThreads), 0, s, logits,
+    hipLaunchKernelGGL(k_ce_combine_wide, dim3(static_cast<unsigned>((N + 63) / 64)), dim3(64 * kWideWaves), 0, s, logits,
                        labels, mask, stats, stats + tiles * N, cm, cs, loss_vec, tiles, C, N, vocab_size);
     const bool v4 = cols4_ok(logits, N) && aligned16(labels) && aligned16(workspace) && aligned16(grad);
     if (v4)
