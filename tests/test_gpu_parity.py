@@ -183,7 +183,7 @@ def test_transpose(hip, cpu, shape):
     assert np.array_equal(h, c) and np.array_equal(h, A.T)
 
 
-@pytest.mark.parametrize("M,B,N", [(768, 8, 64), (5, 3, 7), (64, 12, 1024)])
+@pytest.mark.parametrize("M,B,N", [(768, 8, 64), (5, 3, 7), (64, 12, 1024), (7, 3, 260), (768, 8, 1024)])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_rearrange_3d(hip, cpu, M, B, N, inverse):
     X = uniform(np.random.default_rng(2), (B * M, N) if inverse else (M, B * N))
