@@ -585,6 +585,148 @@ void launch_trans(const Plan& p, const float* A, const float* B, float* C, int M
     }
 }
 
+// ── matrix-vector products (N == 1 or M == 1) ───────────────────────────────
+// Memory-bound: each matrix element is read once, so these bypass the MFMA
+// tiles (a 64-wide tile would waste 63/64 of its work). The epilogue rounds as
+// the split-K reduction does: v = alpha * sum, v += bias, v = C_old + v.
+__device__ __forceinline__ float gemv_epilogue(float acc, float alpha, const float* bias, long brow, const float* y,
+                                               int accum)
+{
+#pragma clang fp contract(off)
+    float v = alpha * acc;
+    if (bias) v = v + bias[brow];
+    if (accum) v = *y + v;
+    return v;
+}
+
+// y[i] = alpha * sum_k R[i][k] x[k] over rows of R (row stride ldr): one wave per output.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_gemv_rows(const float* __restrict__ R, long ldr, long sR,
+                                                   const float* __restrict__ x, long sx, float* y, long sy, int rows,
+                                                   int K, float alpha, const float* bias, int bias_each, int accum)
+{
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int i = blockIdx.x * 4 + static_cast<int>(wave);
+    if (i >= rows) return;
+    const long b = blockIdx.y;
+    const float* r = R + b * sR + (long)i * ldr;
+    const float* xv = x + b * sx;
+    float acc = 0.0f;
+    int k = 0;
+    if constexpr (VEC)
+    {
+        const float4* r4 = reinterpret_cast<const float4*>(r);
+        const float4* x4 = reinterpret_cast<const float4*>(xv);
+        const int K4 = K / 4;
+        for (int q = static_cast<int>(lane); q < K4; q += 64)
+        {
+            const float4 a = r4[q], v = x4[q];
+            acc = __builtin_fmaf(a.x, v.x, acc);
+            acc = __builtin_fmaf(a.y, v.y, acc);
+            acc = __builtin_fmaf(a.z, v.z, acc);
+            acc = __builtin_fmaf(a.w, v.w, acc);
+        }
+        k = 4 * K4;
+    }
+    for (int kk = k + static_cast<int>(lane); kk < K; kk += 64) acc = __builtin_fmaf(r[kk], xv[kk], acc);
+    acc = wave_sum(acc);
+    if (lane == 0)
+    {
+        float* out = y + b * sy + i;
+        *out = gemv_epilogue(acc, alpha, bias, bias_each ? i : 0, out, accum);
+    }
+}
+
+// y[j] = alpha * sum_k x[k] Q[k][j] over rows of Q (row stride ldq), read along j: one thread per output,
+// k in order.
+__global__ __launch_bounds__(256) void k_gemv_cols(const float* __restrict__ Q, long ldq, long sQ,
+                                                   const float* __restrict__ x, long sx, float* y, long sy, int cols,
+                                                   int K, float alpha, const float* bias, int bias_each, int accum)
+{
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= cols) return;
+    const long b = blockIdx.y;
+    const float* q = Q + b * sQ + j;
+    const float* xv = x + b * sx;
+    float acc = 0.0f;
+    int k = 0;
+    for (; k + 4 <= K; k += 4)
+    {
+        const float a0 = q[(long)k * ldq], a1 = q[(long)(k + 1) * ldq], a2 = q[(long)(k + 2) * ldq],
+                    a3 = q[(long)(k + 3) * ldq];
+        acc = __builtin_fmaf(a0, xv[k], acc);
+        acc = __builtin_fmaf(a1, xv[k + 1], acc);
+        acc = __builtin_fmaf(a2, xv[k + 2], acc);
+        acc = __builtin_fmaf(a3, xv[k + 3], acc);
+    }
+    for (; k < K; ++k) acc = __builtin_fmaf(q[(long)k * ldq], xv[k], acc);
+    float* out = y + b * sy + j;
+    *out = gemv_epilogue(acc, alpha, bias, bias_each ? j : 0, out, accum);
+}
+
+// Runs C = alpha op(A) op(B) (+ epilogue) as matrix-vector products when N == 1 or M == 1 and the
+// layout allows it; returns 1 when launched (0 / error from launch_status via rc), 0 when not handled.
+int try_gemv(const float* A, const float* B, float* C, size_t M, size_t N, size_t K, size_t lda, size_t ldb,
+             size_t sA, size_t sB, size_t sC, bool tA, bool tB, float alpha, size_t batch, hipStream_t s, Epi e,
+             int& rc)
+{
+    if (K == 0 || K > 0x7fffffff) return 0;
+    const float* R = nullptr;   // matrix whose rows the outputs dot with, or whose rows the outputs run along
+    const float* x = nullptr;
+    long ld = 0, sR = 0, sx = 0;
+    size_t outs = 0;
+    bool rows = false;
+    int bias_each = 0;
+    if (N == 1 && M > 1)
+    {
+        // the vector is B's only column (tB = 0: stride ldb = 1) or row (tB = 1)
+        if (!tB && ldb != 1) return 0;
+        x = B;
+        sx = static_cast<long>(sB);
+        R = A;
+        ld = static_cast<long>(lda);
+        sR = static_cast<long>(sA);
+        outs = M;
+        rows = !tA;
+        bias_each = 1;
+    }
+    else if (M == 1)
+    {
+        if (tA && lda != 1) return 0;
+        x = A;
+        sx = static_cast<long>(sA);
+        R = B;
+        ld = static_cast<long>(ldb);
+        sR = static_cast<long>(sB);
+        outs = N;
+        rows = tB;
+        bias_each = 0;
+    }
+    else
+        return 0;
+    if (!rows && K > 4096) return 0;   // the column form runs k serially per output
+    if (outs > 0x7fffffff) return 0;
+    if (rows)
+    {
+        const bool vec = ld % 4 == 0 && sR % 4 == 0 && sx % 4 == 0 && aligned16(R) && aligned16(x);
+        const dim3 grid(static_cast<unsigned>((outs + 3) / 4), static_cast<unsigned>(batch));
+        if (vec)
+            hipLaunchKernelGGL(k_gemv_rows<true>, grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC, (int)outs,
+                               (int)K, alpha, e.bias, bias_each, e.accum);
+        else
+            hipLaunchKernelGGL(k_gemv_rows<false>, grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC, (int)outs,
+                               (int)K, alpha, e.bias, bias_each, e.accum);
+    }
+    else
+    {
+        const dim3 grid(static_cast<unsigned>((outs + 255) / 256), static_cast<unsigned>(batch));
+        hipLaunchKernelGGL(k_gemv_cols, grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC, (int)outs, (int)K,
+                           alpha, e.bias, bias_each, e.accum);
+    }
+    rc = launch_status();
+    return 1;
+}
+
 int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, size_t K, size_t lda, size_t ldb,
                   size_t sA, size_t sB, size_t sC, bool tA, bool tB, float alpha, size_t batch, void* workspace,
                   size_t ws_bytes, void* stream, Epi e = {nullptr, 0})
@@ -592,6 +734,7 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
     if (M == 0 || N == 0 || batch == 0) return 0;
     if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || batch > 65535) return -1;
     auto s = static_cast<hipStream_t>(stream);
+    if (int rc = 0; try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc)) return rc;
     Plan p = plan_gemm(M, N, K, batch, workspace != nullptr);
     if (p.splits > 1 && static_cast<size_t>(p.splits) * batch * M * N * sizeof(float) > ws_bytes)
         p = plan_gemm(M, N, K, batch, false);

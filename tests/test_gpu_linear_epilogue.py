@@ -21,7 +21,7 @@ def bits(a):
     return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
 
 
-SHAPES = [(64, 48, 40), (768, 8192, 768), (6144, 768, 8192), (37, 29, 1500), (3, 5, 7)]
+SHAPES = [(64, 48, 40), (768, 8192, 768), (6144, 768, 8192), (37, 29, 1500), (3, 5, 7), (768, 1, 768), (5, 1, 13)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)

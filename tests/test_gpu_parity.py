@@ -73,6 +73,29 @@ def test_matmul_split_k(hip, cpu, M, N, K, batch, tA, tB):
     assert np.all(np.abs(h - ref) <= 2 * K * 2.0 ** -24 * absprod + 1e-30)
 
 
+@pytest.mark.parametrize("tA", [False, True])
+@pytest.mark.parametrize("tB", [False, True])
+@pytest.mark.parametrize("M,N,K,batch", [(768, 1, 768, 1), (32000, 1, 768, 1), (3, 1, 5, 1), (700, 1, 3001, 2),
+                                         (1, 1024, 64, 12), (1, 700, 13, 1), (1, 33, 4096, 1), (64, 1, 517, 12),
+                                         (1, 1, 9, 3)])
+def test_matrix_vector(hip, cpu, M, N, K, batch, tA, tB):
+    """Products with N == 1 or M == 1 (one token's Linear layers, a head's scores against the key
+    cache and its value sum in incremental inference) take the matrix-vector kernels: against the
+    oracle and float64, with the a-priori bound, every transpose, batched, K not a multiple of 4."""
+    rng = np.random.default_rng(M + 3 * N + 7 * K + batch)
+    A = uniform(rng, (batch * (K if tA else M), M if tA else K))
+    B = uniform(rng, (batch * (N if tB else K), K if tB else N))
+    h, c = both(hip, cpu, lambda e: e.batched_matmul(e.tensor(A), e.tensor(B), batch, tA, tB, 0.75))
+    assert h.shape == (batch * M, N)
+    assert nrm_err(h, c) <= 1e-5
+    Ae = A.reshape(batch, -1, A.shape[1]).astype(np.float64)
+    Be = B.reshape(batch, -1, B.shape[1]).astype(np.float64)
+    ref = 0.75 * np.concatenate([(Ae[b].T if tA else Ae[b]) @ (Be[b].T if tB else Be[b]) for b in range(batch)])
+    absprod = 0.75 * np.concatenate([np.abs(Ae[b].T if tA else Ae[b]) @ np.abs(Be[b].T if tB else Be[b])
+                                     for b in range(batch)])
+    assert np.all(np.abs(h - ref) <= 2 * K * 2.0 ** -24 * absprod + 1e-30)
+
+
 @pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
 def test_batched_matmul_alpha(hip, cpu, tA, tB):
     rng = np.random.default_rng(7)
