@@ -75,6 +75,25 @@ def _gain_indices(cfg):
     return idx + [base + 14 * cfg["num_layers"]]
 
 
+def inference_leg(g, seed, tokens=64, warmup=8):
+    """Incremental inference on the trained config-4 model (GPTModel::forward_step with KV caches,
+    reference compute_layer.hpp:2906-2960): one token per call at positions 0..tokens-1, logits
+    (32000 floats) copied to the host after each, so a call is one token's full latency."""
+    rng = np.random.default_rng(seed + 17)
+    ids = rng.integers(0, CFG["vocab_size"], size=warmup + tokens)
+    g.reset_cache()
+    for p in range(warmup):
+        g.forward_step(int(ids[p]), p, p)
+    t0 = time.perf_counter()
+    for p in range(warmup, warmup + tokens):
+        g.forward_step(int(ids[p]), p, p)
+    el = time.perf_counter() - t0
+    g.reset_cache()
+    return {"tokens": tokens, "positions": [warmup, warmup + tokens - 1], "ms_per_token": 1000.0 * el / tokens,
+            "tokens_per_s": tokens / el,
+            "workload": "config-4 model, batch 1, one token per forward_step (KV caches), logits read back"}
+
+
 def gpu_leg(steps, warmup, seed):
     import nnengine
     lib = nnengine.hip_library()
@@ -122,10 +141,12 @@ def gpu_leg(steps, warmup, seed):
     ms = ctypes.c_double(float(rec[:, 6].sum()))
     print(f"[bench] timed {steps} steps in {elapsed:.3f}s, losses {[round(x, 4) for x in losses]}",
           file=sys.stderr, flush=True)
+    infer = inference_leg(g, seed)
     for x in losses:
         if not math.isfinite(x):
             raise RuntimeError(f"non-finite loss {x}")
-    return dict(elapsed=elapsed, gemm_launches=launches.value, gemm_flops=flops.value, gemm_ms=ms.value,
+    return dict(elapsed=elapsed, inference=infer, gemm_launches=launches.value, gemm_flops=flops.value,
+                gemm_ms=ms.value,
                 losses=losses, gemm_shapes=shapes)
 
 
@@ -620,6 +641,7 @@ def main():
                      "share_of_step": gpu["gemm_ms"] / (gpu["elapsed"] * 1000.0),
                      "by_shape": gpu["gemm_shapes"]},
     }
+    out["inference"] = gpu["inference"]
     if attn is not None:
         out["attention"] = attn
     if sweep is not None:
