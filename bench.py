@@ -194,15 +194,16 @@ class Busy:
             del c
 
 
-def timed_ms(timer, busy, fn, reps):
-    """Average milliseconds per call of fn over reps back-to-back calls. The
-    engine records some calls instead of launching them and skips results that
-    nobody references, so each call's outputs are held until settle() has
-    launched what the call recorded, then dropped (the pool hands the same
-    block to the next call)."""
-    keep = fn()
-    busy.eng.settle()
-    del keep
+def timed_ms(timer, busy, fn, reps, warmup=3):
+    """Average milliseconds per call of fn over reps back-to-back calls, after
+    `warmup` untimed calls. The engine records some calls instead of launching
+    them and skips results that nobody references, so each call's outputs are
+    held until settle() has launched what the call recorded, then dropped (the
+    pool hands the same block to the next call)."""
+    for _ in range(warmup):
+        keep = fn()
+        busy.eng.settle()
+        del keep
     busy()
     timer.start()
     for _ in range(reps):

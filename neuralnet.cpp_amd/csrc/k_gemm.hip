@@ -19,6 +19,7 @@
 // MFMA 32x32x2 f32 operand layout (per lane l, k-step of 2):
 //   A: A[i = l%32][k = l/32],  B: B[k = l/32][j = l%32],
 //   D: 16 values, value r at row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#include <cmath>
 #include <mutex>
 
 #include "common.hpp"
@@ -509,7 +510,29 @@ Plan plan_gemm(size_t M, size_t N, size_t K, size_t batch, bool allow_split)
     }
     if (M <= 64) { p.cfg = kThinWavesM64; p.bm = 64; p.bn = 128; }
     else if (N <= 64) { p.cfg = kSkinnyN; p.bm = 256; p.bn = 64; }
-    else if (tiles(256, 128) >= 512) { p.cfg = kTall; p.bm = 256; p.bn = 128; }
+    else if (tiles(256, 128) >= 512)
+    {
+        p.cfg = kTall;
+        p.bm = 256;
+        p.bn = 128;
+        // Under 4 resident rounds of 256x128 tiles the last, partial round
+        // costs a whole round: take smaller tiles when their whole rounds win
+        // clearly (per-tile efficiency 1 : 0.985 : 0.94 measured on the config-3/4
+        // shapes; 8192x2304 K768: 576 tiles of 256x128, 94 -> 120 TFLOP/s as
+        // 2304 of 128x64). Grids of >= 4 rounds (the lm_head product) keep 256x128.
+        const double round = 3.0 * device_cus();
+        if (static_cast<double>(tiles(256, 128)) < 4.0 * round)
+        {
+            auto est = [&](size_t t, double eff) {
+                const double r = static_cast<double>(t) / round;
+                return r / std::ceil(r) * eff;
+            };
+            const double eT = est(tiles(256, 128), 1.0), eS = est(tiles(128, 128), 0.985),
+                         eN = est(tiles(128, 64), 0.94);
+            if (eN > eT + 0.05 && eN >= eS) { p.cfg = kThinWaves; p.bm = 128; p.bn = 64; }
+            else if (eS > eT + 0.05) { p.cfg = kSquare; p.bm = 128; p.bn = 128; }
+        }
+    }
     else if (allow_split && K >= 4096)
     {
         p.cfg = kTall;
