@@ -127,6 +127,11 @@ int nnhip_broadcast_col(const float* A, const float* vec, float* out, size_t row
 
 /* ── layout (cuda_kernels.h:131-143) ──────────────────────────────────────── */
 int nnhip_transpose(const float* A, float* out, size_t R, size_t C, void* stream);
+/* Per batch b: out rows [b*C, (b+1)*C) = (A rows [b*R, (b+1)*R))^T, i.e. rearrange_3d(transpose(A), C,
+ * batch, R) (cpu_engine.hpp:226-287) in one pass; the reference's two-pass attention makes V and dO
+ * (per batch (d_k, seq)) query-major that way (compute_layer.hpp:1211-1214, :1309-1313). No CUDA
+ * counterpart. */
+int nnhip_transpose_batched(const float* A, float* out, size_t batch, size_t R, size_t C, void* stream);
 int nnhip_rearrange_3d(const float* A, float* out, size_t M, size_t B, size_t N, unsigned inverse, void* stream);
 
 /* ── gather / scatter (cuda_kernels.h:151-163) ───────────────────────────
@@ -251,11 +256,13 @@ int nnhip_flash_backward_ordered(const float* Q, const float* Kt, const float* d
                                  float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K,
                                  size_t Kd, float alpha, float alpha2, size_t mask_batch_stride, int g_is_do,
                                  const void* order, void* workspace, void* stream);
+/* nnhip_flash_backward_ds_ordered also takes O per batch (M, K) query-major when o_query_major (the
+ * two-pass chain's softmax_apply output) and writes R (batch*M) when R is not NULL. */
 int nnhip_flash_backward_ds_ordered(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* O,
-                                    const float* mask, const void* cells, const float* m, const float* l, float* dQ,
-                                    float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K, float alpha,
-                                    float alpha2, size_t mask_batch_stride, const void* order, void* workspace,
-                                    void* stream);
+                                    int o_query_major, const float* mask, const void* cells, const float* m,
+                                    const float* l, float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M,
+                                    size_t N, size_t K, float alpha, float alpha2, size_t mask_batch_stride,
+                                    const void* order, void* workspace, void* stream);
 
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */

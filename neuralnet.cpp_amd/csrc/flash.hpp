@@ -70,12 +70,20 @@ bool flash_supported(size_t batch, size_t M, size_t N, size_t K, size_t D);
 size_t flash_cells_bytes(size_t M, size_t N);
 int flash_classify(const float* mask, size_t masks, long mask_bs, size_t M, size_t N, void* cells, hipStream_t s);
 size_t flash_workspace_bytes(size_t batch, size_t M, size_t N, size_t K, size_t D, bool backward);
-int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, hipStream_t s);
-int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, hipStream_t s);
-// Backward when the forward output O (per batch (Kd, M), dim-major, from the same V as V') is at hand:
-// R_i = alpha2 dO_i . O_i directly, one key-line pass for dK, dV and dS, then dQ = alpha dS K.
+// Work order tables (workgroup -> item) for kind 0 forward, 1 backward, 2 the dS backward.
+size_t flash_order_bytes(size_t batch, size_t M, size_t N, int kind);
+int flash_build_order(const unsigned char* cells, size_t batch, size_t M, size_t N, bool per_batch_cls, int kind,
+                      void* order, hipStream_t s);
+// order: a table from flash_build_order for the same cells and shape, or nullptr (grid order).
+int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, const int* order,
+                  hipStream_t s);
+int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t batch, void* workspace, const int* order,
+                   hipStream_t s);
+// Backward when the forward output O (from the same V as V') is at hand: R_i = alpha2 dO_i . O_i
+// directly (O per batch (Kd, M) dim-major, or (M, Kd) query-major when o_qm; R kept when a.R is set),
+// one key-line pass for dK, dV and dS, then dQ = alpha dS K.
 size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K);
-int flash_backward_ds(const FlashBwdArgs& a, const float* O, const unsigned char* cells, size_t batch,
-                      void* workspace, hipStream_t s);
+int flash_backward_ds(const FlashBwdArgs& a, const float* O, int o_qm, const unsigned char* cells, size_t batch,
+                      void* workspace, const int* order, hipStream_t s);
 
 } // namespace nnhip

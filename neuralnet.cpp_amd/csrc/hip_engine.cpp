@@ -443,6 +443,37 @@ struct HipEngine::AttnGrads
     bool q_taken = false, k_taken = false;
 };
 
+// transpose(S) not launched yet, or the per-batch transpose that
+// rearrange_3d(transpose(S), M, B, N) makes of it: out rows [b*M, (b+1)*M)
+// are the transpose of S rows [b*N, (b+1)*N). The two-pass attention turns V
+// and dO from per batch (d_k, seq) into (seq, d_k) this way
+// (compute_layer.hpp:1211-1214, :1309-1313); its kernels read S in place
+// instead, and anything else that reads out gets the copy.
+struct HipEngine::PendingLayout
+{
+    Tensor S, out;
+    bool per_batch;
+    std::size_t M, B, N;   // per_batch: out (B*M, N) from S (B*N, M)
+    bool uses(const float* p) const { return has_buf(S, p) || has_buf(out, p); }
+};
+
+// The two-pass chain's softmax_apply output O (per batch (M, D), query-major)
+// with what it came from; V was read from Vs (per batch (D, N)). The backward
+// takes R_i = alpha2 dO_i . O_i from it instead of a second score pass.
+struct HipEngine::TwoPassOut
+{
+    Tensor Q, K;
+    std::optional<Tensor> mask;
+    Tensor m, l, Vs, O;
+    std::size_t batch;
+    float alpha;
+    bool uses(const float* p) const
+    {
+        return has_buf(Q, p) || has_buf(K, p) || (mask && has_buf(*mask, p)) || has_buf(m, p) || has_buf(l, p) ||
+               has_buf(Vs, p) || has_buf(O, p);
+    }
+};
+
 namespace
 {
 
@@ -636,6 +667,14 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
                 break;
             }
         if (pmadd_ && has_buf(pmadd_->out, p)) NN_CHECK(settle_madd_());
+        for (std::size_t i = 0; i < playout_.size(); ++i)
+            if (has_buf(playout_[i].out, p))
+            {
+                const PendingLayout r = std::move(playout_[i]);
+                playout_.erase(playout_.begin() + static_cast<std::ptrdiff_t>(i));
+                NN_CHECK(materialise_layout_(r));
+                break;
+            }
         if (pdv_ && has_buf(pdv_->out, p)) NN_CHECK(settle_dv_());
         if (pds_ && has_buf(pds_->out, p)) NN_CHECK(settle_ds_());
         for (auto& a : pattn_)
@@ -713,6 +752,14 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb)
             break;
         }
     if (pmadd_ && pmadd_->uses(p)) NN_CHECK(settle_madd_());
+    for (std::size_t i = playout_.size(); i-- > 0;)
+        if (playout_[i].uses(p))
+        {
+            const PendingLayout r = std::move(playout_[i]);
+            playout_.erase(playout_.begin() + static_cast<std::ptrdiff_t>(i));
+            if (live(r.out)) NN_CHECK(materialise_layout_(r));
+        }
+    std::erase_if(ptwo_, [p](const TwoPassOut& r) { return r.uses(p); });
     if (pdv_ && pdv_->uses(p)) NN_CHECK(settle_dv_());
     if (pds_ && pds_->uses(p)) NN_CHECK(settle_ds_());
     if (pgrads_ && (has_buf(pgrads_->dQ, p) || has_buf(pgrads_->dK, p))) pgrads_.reset();
@@ -741,10 +788,12 @@ Result<void> HipEngine::settle()
     NN_CHECK(settle_mm_());
     NN_CHECK(settle_swb_());
     NN_CHECK(settle_madd_());
+    NN_CHECK(settle_layout_());
     NN_CHECK(settle_dv_());
     NN_CHECK(settle_ds_());
     if (pgrads_ && !live(pgrads_->dQ) && !live(pgrads_->dK)) pgrads_.reset();
     forget_dead_attn_();
+    forget_dead_two_();
     NN_CHECK(settle_bwd_());
     NN_CHECK(settle_gemm_());
     return settle_fwd_();
@@ -802,6 +851,50 @@ void HipEngine::forget_dead_attn_()
 {
     for (std::size_t i = pattn_.size(); i-- > 0;)
         if (!live(pattn_[i]->A) && pattn_[i].use_count() == 1) pattn_.erase(pattn_.begin() + static_cast<std::ptrdiff_t>(i));
+}
+
+void HipEngine::forget_dead_two_()
+{
+    std::erase_if(ptwo_, [](const TwoPassOut& r) { return !live(r.m) || !live(r.l); });
+}
+
+// ── recorded transposes ─────────────────────────────────────────────────────
+Result<void> HipEngine::push_layout_(PendingLayout r)
+{
+    std::erase_if(playout_, [](const PendingLayout& q) { return !live(q.out); });
+    constexpr std::size_t kKeep = 16;
+    if (playout_.size() >= kKeep)
+    {
+        const PendingLayout o = std::move(playout_.front());
+        playout_.erase(playout_.begin());
+        NN_CHECK(materialise_layout_(o));
+    }
+    playout_.push_back(std::move(r));
+    return {};
+}
+
+Result<void> HipEngine::materialise_layout_(const PendingLayout& r)
+{
+    if (!r.per_batch)
+        return kernel_(nnhip_transpose(D(r.S), W(r.out), r.S.rows(), r.S.cols(), stream_), "transpose");
+    return kernel_(nnhip_transpose_batched(D(r.S), W(r.out), r.B, r.N, r.M, stream_), "rearrange_3d");
+}
+
+// Copies still referenced are made; the others are dropped.
+Result<void> HipEngine::settle_layout_()
+{
+    std::vector<PendingLayout> rs = std::move(playout_);
+    playout_.clear();
+    for (const PendingLayout& r : rs)
+        if (live(r.out)) NN_CHECK(materialise_layout_(r));
+    return {};
+}
+
+const HipEngine::PendingLayout* HipEngine::layout_of_(const Tensor& t) const
+{
+    for (const PendingLayout& r : playout_)
+        if (same_t(r.out, t)) return &r;
+    return nullptr;
 }
 
 std::shared_ptr<HipEngine::PendingAttn> HipEngine::attn_of_(const Tensor& A) const
@@ -947,10 +1040,10 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
             // R from the forward output (same V): one key-line pass plus dQ from the stored dS.
             NN_TRY(order, flash_order_(cells, batch, q.M, q.N, bs, 2));
             NN_TRY(ws, scratch_(nnhip_flash_ds_workspace_bytes(batch, q.M, q.N, q.Kd)));
-            NN_CHECK(kernel_(nnhip_flash_backward_ds_ordered(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), D(q.O),
-                                                             D(q.mask), cells, D(q.m), D(q.l), W(dQ), W(dK), W(dV),
-                                                             batch, q.M, q.N, q.Kd, q.alpha, pds_->alpha2, bs, order,
-                                                             ws->data(), stream_),
+            NN_CHECK(kernel_(nnhip_flash_backward_ds_ordered(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), D(q.O), 0,
+                                                             D(q.mask), cells, D(q.m), D(q.l), nullptr, W(dQ), W(dK),
+                                                             W(dV), batch, q.M, q.N, q.Kd, q.alpha, pds_->alpha2, bs,
+                                                             order, ws->data(), stream_),
                              "attention backward"));
         }
         else
@@ -1431,18 +1524,31 @@ Result<void> HipEngine::scatter_add_rows(Tensor& dst, const Tensor& indices, con
 // ── layout (cpu_engine.hpp:226-287) ─────────────────────────────────────────
 Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size_t B, std::size_t N, bool inverse)
 {
-    NN_CHECK(need_gpu_({&x}, "rearrange_3d"));
+    NN_CHECK(check_gpu_({&x}, "rearrange_3d"));
     if (x.size() != M * B * N) return fail("rearrange_3d: element count mismatch");
+    // Of a recorded transpose of S (B*N, M): the per-batch transpose of S, recorded too.
+    const PendingLayout* t = inverse ? nullptr : layout_of_(x);
+    if (t && !t->per_batch && x.rows() == M && x.size() > 0)
+    {
+        const Tensor S = t->S;
+        NN_TRY(out, alloc_(B * M, N));
+        NN_CHECK(push_layout_(PendingLayout{S, out, true, M, B, N}));
+        return out;
+    }
+    NN_CHECK(settle_reads_({&x}));
     NN_TRY(out, alloc_(inverse ? M : B * M, inverse ? B * N : N));
     NN_CHECK(kernel_(nnhip_rearrange_3d(D(x), W(out), M, B, N, inverse ? 1u : 0u, stream_), "rearrange_3d"));
     return out;
 }
 
+// Recorded: the two-pass attention reads the source in place; any other read
+// of the result launches the copy.
 Result<Tensor> HipEngine::transpose(const Tensor& A)
 {
     NN_CHECK(need_gpu_({&A}, "transpose"));
     NN_TRY(out, alloc_(A.cols(), A.rows()));
-    NN_CHECK(kernel_(nnhip_transpose(D(A), W(out), A.rows(), A.cols(), stream_), "transpose"));
+    if (out.size() == 0) return out;
+    NN_CHECK(push_layout_(PendingLayout{A, out, false, 0, 0, 0}));
     return out;
 }
 
@@ -1598,9 +1704,14 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
     NN_CHECK(vec_ok(row_max, batch * d.M, "batched_matmul_softmax_apply", "row_max"));
     NN_CHECK(vec_ok(denom, batch * d.M, "batched_matmul_softmax_apply", "denom"));
     NN_CHECK(mask_ok(mask, d.M, d.N, "batched_matmul_softmax_apply"));
-    // Last call of the forward chain: m, l and O in one pass.
+    // Last call of the forward chain: m, l and O in one pass. V made from Vs
+    // (per batch (D, N)) by a recorded rearrange_3d(transpose(Vs), N, batch, D)
+    // is read from Vs.
     const bool v_from_chain = pfwd_ && pfwd_->yields(V.dev_ptr());
-    if (!v_from_chain) NN_CHECK(settle_reads_({&V}));
+    const PendingLayout* vl = layout_of_(V);
+    const bool v_src = vl && vl->per_batch && vl->B == batch && vl->M == d.N && vl->N == V.cols();
+    const Tensor Vs = v_src ? vl->S : V;
+    if (!v_from_chain && !v_src) NN_CHECK(settle_reads_({&V}));
     if (!v_from_chain && pfwd_ && pfwd_->l && same_t(row_max, pfwd_->m) && same_t(denom, *pfwd_->l) &&
         pfwd_->matches(A, B, batch, tA, tB, alpha, mask) && nnhip_flash_supported(batch, d.M, d.N, d.K, V.cols()))
     {
@@ -1609,10 +1720,18 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
         NN_TRY(cells, mask_cells_(mask, d.M, d.N));
         NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 0));
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, d.K, V.cols(), 0)));
-        NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(A), D(B), D(V), mask ? D(*mask) : nullptr, cells, W(f->m),
-                                                     W(*f->l), W(o), batch, d.M, d.N, d.K, V.cols(), alpha, 0, 0, 0,
-                                                     order, ws->data(), stream_),
+        NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(A), D(B), D(Vs), mask ? D(*mask) : nullptr, cells, W(f->m),
+                                                     W(*f->l), W(o), batch, d.M, d.N, d.K, V.cols(), alpha, 0,
+                                                     v_src ? 1 : 0, 0, order, ws->data(), stream_),
                          "batched_matmul_softmax_apply"));
+        if (v_src)
+        {
+            forget_dead_two_();
+            constexpr std::size_t kKeep = 64;   // one per layer
+            if (ptwo_.size() >= kKeep) ptwo_.erase(ptwo_.begin());
+            ptwo_.push_back(TwoPassOut{A, B, mask ? std::optional<Tensor>(*mask) : std::nullopt, f->m, *f->l, Vs, o,
+                                       batch, alpha});
+        }
         return o;
     }
     NN_CHECK(settle_reads_({&A, &B, &V, &row_max, &denom, mask}));
@@ -1677,9 +1796,14 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
     if (G.cols() < d.K) return fail("batched_matmul_softmax_backward_kv: G cols < K");
     NN_TRY(dk, alloc_(batch * d.K, d.N));
     NN_TRY(dv, alloc_(batch * d.K, d.N));
-    // Last call of the backward chain: R, dQ, dK, dV with dP recomputed, never stored.
+    // Last call of the backward chain: R, dQ, dK, dV with dP recomputed, never
+    // stored. G made from dO (the dP product's left operand) by a recorded
+    // rearrange_3d(transpose(dO), M, batch, Kd) is read from dO's columns.
     const bool g_from_chain = (pbwd_ && pbwd_->yields(G.dev_ptr())) || (pgemm_ && pgemm_->yields(G.dev_ptr()));
-    if (!g_from_chain) NN_CHECK(settle_reads_({&G}));
+    const PendingLayout* gl = layout_of_(G);
+    const bool g_do = gl && gl->per_batch && pgemm_ && same_t(gl->S, pgemm_->A) && gl->B == batch &&
+                      gl->M == d.M && gl->N == pgemm_->K && pgemm_->K == d.K;
+    if (!g_from_chain && !g_do) NN_CHECK(settle_reads_({&G}));
     if (!g_from_chain && pbwd_ && pgemm_ && same_t(P, pbwd_->P) && same_t(P, pgemm_->C) && same_t(R, pbwd_->R) &&
         same_t(A, pbwd_->Q) && same_t(B, pbwd_->K) && same_t(row_max, pbwd_->m) && same_t(denom, pbwd_->l) &&
         same_mask(mask, pbwd_->mask) && batch == pbwd_->batch && tA && !tB && alpha == pbwd_->alpha &&
@@ -1688,13 +1812,40 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
         std::unique_ptr<PendingBwd> q = std::move(pbwd_);
         const PendingGemm& g = *pgemm_;
         NN_TRY(cells, mask_cells_(mask, d.M, d.N));
-        NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 1));
-        NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, std::max(d.K, g.K), 4, 1)));
-        NN_CHECK(kernel_(nnhip_flash_backward_ordered(D(A), D(B), D(g.A), D(g.B), D(G), G.cols(),
-                                                      mask ? D(*mask) : nullptr, cells, D(row_max), D(denom),
-                                                      W(q->R), W(q->dQ), W(dk), W(dv), batch, d.M, d.N, d.K, g.K,
-                                                      alpha, g.alpha, 0, 0, order, ws->data(), stream_),
-                         "batched_matmul_softmax_backward_kv"));
+        // The forward's output from the same inputs (V from g.B): R from it,
+        // then one score pass storing dS and dQ from dS.
+        std::ptrdiff_t fo = -1;
+        for (std::size_t i = 0; g_do && i < ptwo_.size(); ++i)
+        {
+            const TwoPassOut& r = ptwo_[i];
+            if (same_t(r.Q, A) && same_t(r.K, B) && same_t(r.m, row_max) && same_t(r.l, denom) &&
+                same_mask(mask, r.mask) && r.batch == batch && r.alpha == alpha && same_t(r.Vs, g.B) &&
+                r.O.cols() == d.K)
+                fo = static_cast<std::ptrdiff_t>(i);
+        }
+        if (fo >= 0)
+        {
+            const TwoPassOut r = std::move(ptwo_[static_cast<std::size_t>(fo)]);
+            ptwo_.erase(ptwo_.begin() + fo);
+            NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 2));
+            NN_TRY(ws, scratch_(nnhip_flash_ds_workspace_bytes(batch, d.M, d.N, d.K)));
+            NN_CHECK(kernel_(nnhip_flash_backward_ds_ordered(D(A), D(B), D(g.A), D(g.B), D(r.O), 1,
+                                                             mask ? D(*mask) : nullptr, cells, D(row_max), D(denom),
+                                                             W(q->R), W(q->dQ), W(dk), W(dv), batch, d.M, d.N, d.K,
+                                                             alpha, g.alpha, 0, order, ws->data(), stream_),
+                             "batched_matmul_softmax_backward_kv"));
+        }
+        else
+        {
+            NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 1));
+            NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, std::max(d.K, g.K), 4, 1)));
+            NN_CHECK(kernel_(nnhip_flash_backward_ordered(D(A), D(B), D(g.A), D(g.B), g_do ? nullptr : D(G),
+                                                          g_do ? d.K : G.cols(), mask ? D(*mask) : nullptr, cells,
+                                                          D(row_max), D(denom), W(q->R), W(q->dQ), W(dk), W(dv),
+                                                          batch, d.M, d.N, d.K, g.K, alpha, g.alpha, 0, g_do ? 1 : 0,
+                                                          order, ws->data(), stream_),
+                             "batched_matmul_softmax_backward_kv"));
+        }
         grad_v_out = dv;
         return dk;
     }

@@ -96,7 +96,7 @@ __device__ __forceinline__ Rsrc rsrc(const float* base, long floats)
 // branch around the load, with a wait for every load in flight inside it.
 __device__ __forceinline__ unsigned oob_if_neg(unsigned off, int sgn)
 {
-    return off | (static_cast<unsigned>(sgn) & 0x80000000u);
+    return off | (static_cast<unsigned>(sgn) & kOob);
 }
 __device__ __forceinline__ float bload(Rsrc r, unsigned off)
 {
@@ -1201,23 +1201,26 @@ __global__ __launch_bounds__(kOrderThreads) void k_flash_order(FlashGeo g, int r
     }
 }
 
-// R_i = alpha2 sum_d dO(d, i) O(d, i): per batch (Kd, M) dim-major operands.
+// R_i = alpha2 sum_d dO(d, i) O(d, i): dO per batch (Kd, M) dim-major; O the
+// same, or (M, Kd) query-major when o_qm.
 __global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ dO, const float* __restrict__ O,
-                                                      float* __restrict__ R, int M, int Kd, long total, float alpha2)
+                                                      float* __restrict__ R, int M, int Kd, long total, float alpha2,
+                                                      int o_qm)
 {
     const long t = (long)blockIdx.x * 256 + threadIdx.x;
     if (t >= total) return;
     const long b = t / M, i = t % M;
     const float* p = dO + b * Kd * M + i;
-    const float* q = O + b * Kd * M + i;
+    const float* q = o_qm ? O + t * Kd : O + b * Kd * M + i;
+    const long qs = o_qm ? 1 : M;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // four independent chains keep loads in flight
     int d = 0;
     for (; d + 4 <= Kd; d += 4)
     {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(p[(long)(d + e) * M], q[(long)(d + e) * M], acc[e]);
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(p[(long)(d + e) * M], q[(d + e) * qs], acc[e]);
     }
-    for (; d < Kd; ++d) acc[0] = __builtin_fmaf(p[(long)d * M], q[(long)d * M], acc[0]);
+    for (; d < Kd; ++d) acc[0] = __builtin_fmaf(p[(long)d * M], q[d * qs], acc[0]);
     R[t] = alpha2 * ((acc[0] + acc[1]) + (acc[2] + acc[3]));
 }
 
@@ -1481,8 +1484,8 @@ size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K)
     return align256(batch * M * N * sizeof(float)) + align256(batch * M * sizeof(float)) + part;
 }
 
-int flash_backward_ds(const FlashBwdArgs& a0, const float* O, const unsigned char* cells, size_t batch, void* ws,
-                      const int* order, hipStream_t s)
+int flash_backward_ds(const FlashBwdArgs& a0, const float* O, int o_qm, const unsigned char* cells, size_t batch,
+                      void* ws, const int* order, hipStream_t s)
 {
     if (!ws || a0.K != a0.Kd) return -1;
     FlashBwdArgs a = a0;
@@ -1490,9 +1493,14 @@ int flash_backward_ds(const FlashBwdArgs& a0, const float* O, const unsigned cha
     const size_t M = static_cast<size_t>(a.M), N = static_cast<size_t>(a.N);
     a.dS = reinterpret_cast<float*>(w);
     w += align256(batch * M * N * sizeof(float));
-    a.R = reinterpret_cast<float*>(w);
+    // R in the workspace unless the caller wants it; the dQ pass ends in the
+    // query-line store, which also writes R (as 0): it is pointed there.
+    float* r_ws = reinterpret_cast<float*>(w);
+    if (!a.R) a.R = r_ws;
     w += align256(batch * M * sizeof(float));
     a.g_do = 1;
+    FlashBwdArgs adq = a;
+    adq.R = r_ws;
     const int KP = pad32(static_cast<size_t>(a.K));
     const unsigned char* cl = a.mask ? cells : nullptr;
     const bool pb = a.mask && a.mask_bs != 0;
@@ -1505,7 +1513,7 @@ int flash_backward_ds(const FlashBwdArgs& a0, const float* O, const unsigned cha
     }
     const long total = static_cast<long>(batch * M);
     hipLaunchKernelGGL(k_flash_rowdot, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, a.dO, O,
-                       a.R, a.M, a.Kd, total, a.alpha2);
+                       a.R, a.M, a.Kd, total, a.alpha2, o_qm ? 1 : 0);
     if (int rc = launch_status()) return rc;
     auto run = [&](auto kp) -> int {
         constexpr int P = decltype(kp)::value;
@@ -1518,12 +1526,12 @@ int flash_backward_ds(const FlashBwdArgs& a0, const float* O, const unsigned cha
                                0, s, a, gc);
             if (int rc = launch_status()) return rc;
         }
-        hipLaunchKernelGGL((k_flash_bwd_dq<P>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, a, gr);
+        hipLaunchKernelGGL((k_flash_bwd_dq<P>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, adq, gr);
         if (int rc = launch_status()) return rc;
         if (gr.NR > 1)
         {
             hipLaunchKernelGGL((k_flash_bwd_rows_combine<P>), dim3(static_cast<unsigned>(batch * gr.RT)), dim3(64),
-                               0, s, a, gr);
+                               0, s, adq, gr);
             if (int rc = launch_status()) return rc;
         }
         return 0;
@@ -1545,25 +1553,25 @@ extern "C" int nnhip_flash_backward_ds(const float* Q, const float* Kt, const fl
                                        size_t N, size_t K, float alpha, float alpha2, size_t mask_batch_stride,
                                        void* workspace, void* stream)
 {
-    return nnhip_flash_backward_ds_ordered(Q, Kt, dO, Vp, O, mask, cells, m, l, dQ, dK, dV, batch, M, N, K, alpha,
-                                           alpha2, mask_batch_stride, nullptr, workspace, stream);
+    return nnhip_flash_backward_ds_ordered(Q, Kt, dO, Vp, O, 0, mask, cells, m, l, nullptr, dQ, dK, dV, batch, M, N,
+                                           K, alpha, alpha2, mask_batch_stride, nullptr, workspace, stream);
 }
 
 extern "C" int nnhip_flash_backward_ds_ordered(const float* Q, const float* Kt, const float* dO, const float* Vp,
-                                               const float* O, const float* mask, const void* cells, const float* m,
-                                               const float* l, float* dQ, float* dK, float* dV, size_t batch,
-                                               size_t M, size_t N, size_t K, float alpha, float alpha2,
-                                               size_t mask_batch_stride, const void* order, void* workspace,
-                                               void* stream)
+                                               const float* O, int o_query_major, const float* mask,
+                                               const void* cells, const float* m, const float* l, float* R, float* dQ,
+                                               float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K,
+                                               float alpha, float alpha2, size_t mask_batch_stride, const void* order,
+                                               void* workspace, void* stream)
 {
     if (!Q || !Kt || !dO || !Vp || !O || !m || !l || !dQ || !dK || !dV || !workspace || (mask && !cells)) return -1;
     if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
     if (!nnhip::flash_supported(batch, M, N, K, 4) || K % 4 != 0) return -3;
-    nnhip::FlashBwdArgs a{Q, Kt, dO, Vp, nullptr, mask, m, l, nullptr, dQ, dK, dV, static_cast<int>(M),
+    nnhip::FlashBwdArgs a{Q, Kt, dO, Vp, nullptr, mask, m, l, R, dQ, dK, dV, static_cast<int>(M),
                           static_cast<int>(N), static_cast<int>(K), static_cast<int>(K), static_cast<int>(K), alpha,
                           alpha2};
     a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
-    return nnhip::flash_backward_ds(a, O, static_cast<const unsigned char*>(cells), batch, workspace,
+    return nnhip::flash_backward_ds(a, O, o_query_major, static_cast<const unsigned char*>(cells), batch, workspace,
                                     static_cast<const int*>(order), static_cast<hipStream_t>(stream));
 }
 

@@ -20,9 +20,12 @@ namespace
 constexpr unsigned kThreads = 256;
 
 // ── transpose: 64x64 tiles through LDS (+1 column of padding) ──────────────
+// blockIdx.z picks one of a batch of (R, C) matrices stored back to back.
 __global__ __launch_bounds__(256) void k_transpose(const float* A, float* out, size_t R, size_t C)
 {
     __shared__ float tile[64][65];
+    A += static_cast<size_t>(blockIdx.z) * R * C;
+    out += static_cast<size_t>(blockIdx.z) * R * C;
     const size_t r0 = static_cast<size_t>(blockIdx.y) * 64, c0 = static_cast<size_t>(blockIdx.x) * 64;
     const unsigned tx = threadIdx.x % 64, ty = threadIdx.x / 64;   // 64 x 4
     for (unsigned k = ty; k < 64; k += 4)
@@ -44,6 +47,8 @@ __global__ __launch_bounds__(256) void k_transpose(const float* A, float* out, s
 __global__ __launch_bounds__(256) void k_transpose4(const float* A, float* out, size_t R, size_t C)
 {
     __shared__ float tile[64][65];
+    A += static_cast<size_t>(blockIdx.z) * R * C;
+    out += static_cast<size_t>(blockIdx.z) * R * C;
     const size_t r0 = static_cast<size_t>(blockIdx.y) * 64, c0 = static_cast<size_t>(blockIdx.x) * 64;
     const unsigned tx = threadIdx.x % 16, ty = threadIdx.x / 16;   // 16 x 16
 #pragma unroll
@@ -249,9 +254,15 @@ using namespace nnhip;
 
 extern "C" int nnhip_transpose(const float* A, float* out, size_t R, size_t C, void* stream)
 {
-    if (R == 0 || C == 0) return 0;
-    if ((C + 63) / 64 > 0x7fffffff || (R + 63) / 64 > 65535) return -1;
-    const dim3 grid(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>((R + 63) / 64));
+    return nnhip_transpose_batched(A, out, 1, R, C, stream);
+}
+
+extern "C" int nnhip_transpose_batched(const float* A, float* out, size_t batch, size_t R, size_t C, void* stream)
+{
+    if (batch == 0 || R == 0 || C == 0) return 0;
+    if ((C + 63) / 64 > 0x7fffffff || (R + 63) / 64 > 65535 || batch > 65535) return -1;
+    const dim3 grid(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>((R + 63) / 64),
+                    static_cast<unsigned>(batch));
     if (R % 4 == 0 && C % 4 == 0 && aligned16(A) && aligned16(out))
         hipLaunchKernelGGL(k_transpose4, grid, dim3(256), 0, static_cast<hipStream_t>(stream), A, out, R, C);
     else

@@ -129,25 +129,9 @@ __device__ __forceinline__ size_t label_of(float f)
     return 0;
 }
 
-// Merge chunk statistics; emit per-column max, denominator, validity and loss.
-__global__ __launch_bounds__(kThreads) void k_ce_combine(const float* L, const float* labels, const float* mask,
-                                                         const float* part_m, const float* part_s, float* col_m,
-                                                         float* col_s, float* loss_vec, size_t chunks, size_t C,
-                                                         size_t N, size_t vocab)
-{
-    const size_t c = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (c >= N) return;
-    const size_t lbl = label_of(labels[c]);
-    const bool valid = (!mask || mask[c] >= 0.5f) && lbl < vocab;
-    float m = part_m[c], s = part_s[c];
-    for (size_t k = 1; k < chunks; ++k) merge(m, s, part_m[k * N + c], part_s[k * N + c]);
-    col_m[c] = m;
-    col_s[c] = valid ? s : 0.0f;   // 0 marks an invalid column for the gradient pass
-    loss_vec[c] = valid ? L[lbl * N + c] - m - logf(s) : 0.0f;
-}
-
-// The same over many chunks (one per 256-row block of a product's statistics):
-// a workgroup owns 64 columns, its 16 waves merge a sixteenth of the chunks
+// Merge chunk statistics (one chunk per 256-row block of the logits or of a
+// product's statistics); emit per-column max, denominator, validity and loss.
+// A workgroup owns 64 columns, its 16 waves merge a sixteenth of the chunks
 // each (loads first, then in chunk order), then wave 0 merges the 16 results
 // in wave order.
 constexpr unsigned kWideWaves = 16, kWideBatch = 8;

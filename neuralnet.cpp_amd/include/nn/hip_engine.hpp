@@ -220,6 +220,17 @@ private:
                                             Scalar alpha);
     Result<std::optional<Tensor>> attn_softmax_(const ExprSpec& spec, std::span<const Tensor> inputs,
                                                 std::size_t rows, std::size_t cols);
+    // transpose calls (and rearrange_3d of them) not launched yet, most recent last.
+    struct PendingLayout;
+    std::vector<PendingLayout> playout_;
+    Result<void> push_layout_(PendingLayout r);
+    Result<void> materialise_layout_(const PendingLayout& r);
+    Result<void> settle_layout_();
+    const PendingLayout* layout_of_(const Tensor& t) const;
+    // Outputs of the two-pass chain's forward kept for the backward, one per layer.
+    struct TwoPassOut;
+    std::vector<TwoPassOut> ptwo_;
+    void forget_dead_two_();
     std::unique_ptr<PendingFwd> pfwd_;
     std::unique_ptr<PendingGemm> pgemm_;
     std::unique_ptr<PendingBwd> pbwd_;

@@ -142,6 +142,9 @@ def test_doc_masked_attention_config5_row(hip):
     dk, dv = e.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, l, H, True, False, 0.125, mk)
     ref = _torch_attention(Q, K, V, mask, 0.125, H, d, dO)
     assert nrm_err(o.numpy(), ref["O"].reshape(H * T, d)) <= 1e-4
+    # R_i = sum_j W_ij P_ij = dO_i . O_i
+    R_ref = (dO.astype(np.float64).reshape(H, d, T).transpose(0, 2, 1) * ref["O"]).sum(-1)
+    assert nrm_err(r.numpy()[:, 0], R_ref.reshape(-1)) <= 1e-4
     for name, t in (("dQ", dq), ("dK", dk), ("dV", dv)):
         assert nrm_err(t.numpy(), ref[name].reshape(H * d, T)) <= 1e-3, name
 
