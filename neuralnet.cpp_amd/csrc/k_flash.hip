@@ -605,24 +605,37 @@ __global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(Fla
     fwd_store<DP, WITH_O>(a, g, lw, it.b, line, it.rg, mrun, lrun, o);
 }
 
-// Merges the range partials of lines with several non-empty ranges, in range order.
+// Merges of lines cut into several ranges (the k_flash_*_combine kernels):
+// one workgroup per line. Wave w takes rows r = w, w+4, w+8, w+12 of the
+// f32x16 lane layout (every u), so each partial is read by all four waves at
+// once in 256-byte rows; every element is still merged in range order.
 template <int DP, bool WITH_O>
-__global__ __launch_bounds__(64) void k_flash_fwd_combine(FlashFwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(256) void k_flash_fwd_combine(FlashFwdArgs a, FlashGeo g)
 {
     constexpr int DU = DP / 32;
-    const int lane = threadIdx.x, c = lane & 31;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
     const LineWork lw = line_work(g, true, b, line, 0);
     if (lw.nne <= 1) return;
     float m = kLowest, l = 0.0f;
-    f32x16 o[DU];
+    float o[DU][4];
 #pragma unroll
-    for (int u = 0; u < DU; ++u) o[u] = zero16();
+    for (int u = 0; u < DU; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[u][k] = 0.0f;
     for (unsigned long long rs = lw.ranges; rs; rs &= rs - 1)
     {
         const float* pp = g.part + (lidx * g.NR + __builtin_ctzll(rs)) * g.pw;
         const float mr = pp[c], lr = pp[32 + c];
+        float t[DU][4];
+        if constexpr (WITH_O)
+        {
+#pragma unroll
+            for (int u = 0; u < DU; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) t[u][k] = pp[64 + (u * 16 + wave + 4 * k) * 64 + lane];
+        }
         const float mn = fmax_f(m, mr);
         const float sa = exp_neg(m - mn), sb = exp_neg(mr - mn);
         l = l * sa + lr * sb;
@@ -632,11 +645,37 @@ __global__ __launch_bounds__(64) void k_flash_fwd_combine(FlashFwdArgs a, FlashG
 #pragma unroll
             for (int u = 0; u < DU; ++u)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o[u][r] = o[u][r] * sa + pp[64 + (u * 16 + r) * 64 + lane] * sb;
+                for (int k = 0; k < 4; ++k) o[u][k] = o[u][k] * sa + t[u][k] * sb;
         }
     }
-    const LineWork one{1ull, 0ull, 1ull, 1};
-    fwd_store<DP, WITH_O>(a, g, one, b, line, 0, m, l, o);
+    const int qi = line * 32 + c;
+    if (qi >= g.M) return;
+    const long row = (long)b * g.M + qi;
+    if (wave == 0 && h == 0)
+    {
+        a.m[row] = m;
+        a.l[row] = l;
+    }
+    if constexpr (WITH_O)
+    {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const int d0 = DU * drow(wave + 4 * k, h);
+            if (d0 >= a.D) continue;
+            if (a.o_dm)
+            {
+                float* ocol = a.O + (long)b * a.D * g.M + qi;   // O per batch (D, M)
+#pragma unroll
+                for (int u = 0; u < DU; ++u) ocol[(long)(d0 + u) * g.M] = o[u][k] * inv;
+            }
+            else if constexpr (DU == 2)
+                *reinterpret_cast<float2*>(a.O + row * a.D + d0) = make_float2(o[0][k] * inv, o[1][k] * inv);
+            else
+                a.O[row * a.D + d0] = o[0][k] * inv;
+        }
+    }
 }
 
 // ── backward over query lines: R and dQ ────────────────────────────────────
@@ -777,37 +816,55 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_rows(FlashBwdArgs 
 }
 
 template <int KP>
-__global__ __launch_bounds__(64) void k_flash_bwd_rows_combine(FlashBwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(256) void k_flash_bwd_rows_combine(FlashBwdArgs a, FlashGeo g)
 {
     constexpr int DU = KP / 32;
-    const int lane = threadIdx.x, c = lane & 31;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
     const LineWork lw = line_work(g, true, b, line, 0);
     if (lw.nne <= 1) return;
     float racc = 0.0f;
-    f32x16 x[DU], y[DU];
+    float x[DU][4], y[DU][4];
 #pragma unroll
     for (int u = 0; u < DU; ++u)
-    {
-        x[u] = zero16();
-        y[u] = zero16();
-    }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[u][k] = y[u][k] = 0.0f;
     for (unsigned long long rs = lw.ranges; rs; rs &= rs - 1)
     {
         const float* pp = g.part + (lidx * g.NR + __builtin_ctzll(rs)) * g.pw;
-        racc += pp[c];
+        float tx[DU][4], ty[DU][4];
+        const float rr = pp[c];
 #pragma unroll
         for (int u = 0; u < DU; ++u)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
+            for (int k = 0; k < 4; ++k)
             {
-                x[u][r] += pp[32 + (u * 16 + r) * 64 + lane];
-                y[u][r] += pp[32 + ((DU + u) * 16 + r) * 64 + lane];
+                tx[u][k] = pp[32 + (u * 16 + wave + 4 * k) * 64 + lane];
+                ty[u][k] = pp[32 + ((DU + u) * 16 + wave + 4 * k) * 64 + lane];
+            }
+        racc += rr;
+#pragma unroll
+        for (int u = 0; u < DU; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                x[u][k] += tx[u][k];
+                y[u][k] += ty[u][k];
             }
     }
-    const LineWork one{1ull, 0ull, 1ull, 1};
-    rows_store<KP>(a, g, one, b, line, 0, racc, x, y);
+    const int qi = line * 32 + c;
+    if (qi >= g.M) return;
+    if (wave == 0 && h == 0) a.R[(long)b * g.M + qi] = racc;
+    float* dq = a.dQ + (long)b * a.K * g.M + qi;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int u = 0; u < DU; ++u)
+        {
+            const int d = DU * drow(wave + 4 * k, h) + u;
+            if (d < a.K) dq[(long)d * g.M] = a.alpha * (x[u][k] - racc * y[u][k]);
+        }
 }
 
 // Loads the query-side tiles of one cell of the key-line kernel into registers:
@@ -1016,44 +1073,131 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdArgs 
 }
 
 template <int KP>
-__global__ __launch_bounds__(64) void k_flash_bwd_cols_combine(FlashBwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(256) void k_flash_bwd_cols_combine(FlashBwdArgs a, FlashGeo g)
 {
     constexpr int DU = KP / 32;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.CT), line = static_cast<int>(lidx % g.CT);
     const LineWork lw = line_work(g, false, b, line, 0);
     if (lw.nne <= 1) return;
-    f32x16 dk[DU], dv[DU];
+    float dk[DU][4], dv[DU][4];
 #pragma unroll
     for (int u = 0; u < DU; ++u)
-    {
-        dk[u] = zero16();
-        dv[u] = zero16();
-    }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dk[u][k] = dv[u][k] = 0.0f;
     for (unsigned long long rs = lw.ranges; rs; rs &= rs - 1)
     {
         const float* pp = g.part + (lidx * g.NR + __builtin_ctzll(rs)) * g.pw;
-        // All of a partial's loads first, then the sums: keeps them in flight together.
-        float t[2 * DU * 16];
+        float tk[DU][4], tv[DU][4];
 #pragma unroll
-        for (int q = 0; q < 2 * DU * 16; ++q) t[q] = pp[q * 64 + lane];
+        for (int u = 0; u < DU; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                tk[u][k] = pp[(u * 16 + wave + 4 * k) * 64 + lane];
+                tv[u][k] = pp[((DU + u) * 16 + wave + 4 * k) * 64 + lane];
+            }
+#pragma unroll
+        for (int u = 0; u < DU; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                dk[u][k] += tk[u][k];
+                dv[u][k] += tv[u][k];
+            }
+    }
+    const int kj = line * 32 + c;
+    if (kj >= g.N) return;
+    float* dkb = a.dK + (long)b * a.K * g.N + kj;
+    float* dvb = a.dV + (long)b * a.K * g.N + kj;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int u = 0; u < DU; ++u)
+        {
+            const int d = DU * drow(wave + 4 * k, h) + u;
+            if (d < a.K)
+            {
+                dkb[(long)d * g.N] = a.alpha * dk[u][k];
+                dvb[(long)d * g.N] = dv[u][k];
+            }
+        }
+}
+
+// dQ of one query line from the dq pass, dQ = alpha x: written directly, or
+// x as the range's partial (pw = 32 KP floats) for k_flash_bwd_dq_combine.
+template <int KP>
+__device__ __forceinline__ void dq_store(const FlashBwdArgs& a, const FlashGeo& g, const LineWork& lw, int b,
+                                         int line, int rg, const f32x16* x)
+{
+    constexpr int DU = KP / 32;
+    const int lane = threadIdx.x & 63, h = lane >> 5, c = lane & 31, qi = line * 32 + c;
+    if (line >= g.RT) return;
+    if (direct_writer(lw, rg))
+    {
+        if (qi >= g.M) return;
+        float* dq = a.dQ + (long)b * a.K * g.M + qi;
 #pragma unroll
         for (int u = 0; u < DU; ++u)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
-                dk[u][r] += t[u * 16 + r];
-                dv[u][r] += t[(DU + u) * 16 + r];
+                const int d = DU * drow(r, h) + u;
+                if (d < a.K) dq[(long)d * g.M] = a.alpha * x[u][r];
             }
+        return;
     }
-    const LineWork one{1ull, 0ull, 1ull, 1};
-    cols_store<KP>(a, g, one, b, line, 0, dk, dv);
+    if (lw.nne <= 1 || !lw.nz) return;
+    float* pp = g.part + (((long)b * g.RT + line) * g.NR + rg) * g.pw;
+#pragma unroll
+    for (int u = 0; u < DU; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pp[(u * 16 + r) * 64 + lane] = x[u][r];
+}
+
+template <int KP>
+__global__ __launch_bounds__(256) void k_flash_bwd_dq_combine(FlashBwdArgs a, FlashGeo g)
+{
+    constexpr int DU = KP / 32;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
+    const long lidx = blockIdx.x;
+    const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
+    const LineWork lw = line_work(g, true, b, line, 0);
+    if (lw.nne <= 1) return;
+    float x[DU][4];
+#pragma unroll
+    for (int u = 0; u < DU; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[u][k] = 0.0f;
+    for (unsigned long long rs = lw.ranges; rs; rs &= rs - 1)
+    {
+        const float* pp = g.part + (lidx * g.NR + __builtin_ctzll(rs)) * g.pw;
+        float t[DU][4];
+#pragma unroll
+        for (int u = 0; u < DU; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t[u][k] = pp[(u * 16 + wave + 4 * k) * 64 + lane];
+#pragma unroll
+        for (int u = 0; u < DU; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) x[u][k] += t[u][k];
+    }
+    const int qi = line * 32 + c;
+    if (qi >= g.M) return;
+    float* dq = a.dQ + (long)b * a.K * g.M + qi;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int u = 0; u < DU; ++u)
+        {
+            const int d = DU * drow(wave + 4 * k, h) + u;
+            if (d < a.K) dq[(long)d * g.M] = a.alpha * x[u][k];
+        }
 }
 
 // dQ from the stored dS: dQ_i = alpha sum_j dS_ij k_j over the non-empty cells
-// of the line's range, with the rows kernel's lines, ranges, partials and
-// combine (R and Y of the partials are zero).
+// of the line's range, with the rows kernel's lines and ranges.
 template <int KP>
 __global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a, FlashGeo g)
 {
@@ -1068,13 +1212,9 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a,
     if (lane == 0) nz_s[wave] = lw.nz;
     __syncthreads();
     const unsigned long long any = nz_s[0] | nz_s[1] | nz_s[2] | nz_s[3];
-    f32x16 x[DU], y[DU];
+    f32x16 x[DU];
 #pragma unroll
-    for (int u = 0; u < DU; ++u)
-    {
-        x[u] = zero16();
-        y[u] = zero16();
-    }
+    for (int u = 0; u < DU; ++u) x[u] = zero16();
     if (any)
     {
         const int cell0 = rg * g.R;
@@ -1105,7 +1245,7 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a,
             rest &= rest - 1;
         }
     }
-    rows_store<KP>(a, g, lw, b, line, rg, 0.0f, x, y);
+    dq_store<KP>(a, g, lw, b, line, rg, x);
 }
 
 // Work order of a flash launch (one workgroup of 1024 threads). The weight of
@@ -1202,26 +1342,58 @@ __global__ __launch_bounds__(kOrderThreads) void k_flash_order(FlashGeo g, int r
 }
 
 // R_i = alpha2 sum_d dO(d, i) O(d, i): dO per batch (Kd, M) dim-major; O the
-// same, or (M, Kd) query-major when o_qm.
+// same, or (M, Kd) query-major when o_qm. A workgroup takes 64 rows (one per
+// lane); wave w sums dims [w Kd/4, (w+1) Kd/4) (Kd % 4 == 0, Kd <= 64) in two
+// chains, and wave 0 adds the four partials in wave order. Query-major O rows
+// are contiguous: the workgroup's 64 Kd floats are staged through LDS.
 __global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ dO, const float* __restrict__ O,
                                                       float* __restrict__ R, int M, int Kd, long total, float alpha2,
                                                       int o_qm)
 {
-    const long t = (long)blockIdx.x * 256 + threadIdx.x;
-    if (t >= total) return;
-    const long b = t / M, i = t % M;
-    const float* p = dO + b * Kd * M + i;
-    const float* q = o_qm ? O + t * Kd : O + b * Kd * M + i;
-    const long qs = o_qm ? 1 : M;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // four independent chains keep loads in flight
-    int d = 0;
-    for (; d + 4 <= Kd; d += 4)
+    __shared__ float part[4][64];
+    __shared__ float Ot[64][65];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long t0 = (long)blockIdx.x * 64, t = t0 + lane;
+    const int q = Kd / 4, d0 = wave * q;
+    if (o_qm)
     {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(p[(long)(d + e) * M], q[(d + e) * qs], acc[e]);
+        const long n = min(64L, total - t0) * Kd;
+        const float* ob = O + t0 * Kd;
+        for (int e = threadIdx.x; e < 64 * Kd; e += 256)
+            if (e < n) Ot[e / Kd][e % Kd] = ob[e];
+        __syncthreads();
     }
-    for (; d < Kd; ++d) acc[0] = __builtin_fmaf(p[(long)d * M], q[d * qs], acc[0]);
-    R[t] = alpha2 * ((acc[0] + acc[1]) + (acc[2] + acc[3]));
+    float acc[2] = {0.0f, 0.0f};
+    if (t < total)
+    {
+        const long b = t / M, i = t % M;
+        const float* p = dO + (b * Kd + d0) * M + i;
+        if (o_qm)
+        {
+            const float* o = &Ot[lane][d0];
+            int d = 0;
+            for (; d + 2 <= q; d += 2)
+            {
+                acc[0] = __builtin_fmaf(p[(long)d * M], o[d], acc[0]);
+                acc[1] = __builtin_fmaf(p[(long)(d + 1) * M], o[d + 1], acc[1]);
+            }
+            if (d < q) acc[0] = __builtin_fmaf(p[(long)d * M], o[d], acc[0]);
+        }
+        else
+        {
+            const float* o = O + (b * Kd + d0) * M + i;
+            int d = 0;
+            for (; d + 2 <= q; d += 2)
+            {
+                acc[0] = __builtin_fmaf(p[(long)d * M], o[(long)d * M], acc[0]);
+                acc[1] = __builtin_fmaf(p[(long)(d + 1) * M], o[(long)(d + 1) * M], acc[1]);
+            }
+            if (d < q) acc[0] = __builtin_fmaf(p[(long)d * M], o[(long)d * M], acc[0]);
+        }
+    }
+    part[wave][lane] = acc[0] + acc[1];
+    __syncthreads();
+    if (wave == 0 && t < total) R[t] = alpha2 * (((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]);
 }
 
 // Mask cell classes: 0 all -inf, 1 all zero, 2 general. blockIdx.z: which mask.
@@ -1323,6 +1495,7 @@ int build_order(const FlashGeo& g, size_t batch, bool rows, int resident, char* 
 int fwd_pw(int DP) { return 64 + 32 * DP; }
 int rows_pw(int KP) { return 32 + 64 * KP; }
 int cols_pw(int KP) { return 64 * KP; }
+int dq_pw(int KP) { return 32 * KP; }
 
 template <int KP, int DP, bool WITH_O>
 int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g0, size_t batch, const int* order, hipStream_t s)
@@ -1348,7 +1521,7 @@ int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g0, size_t batch, const in
     }
     if (int rc = launch_status()) return rc;
     if (g.NR == 1) return 0;
-    hipLaunchKernelGGL((k_flash_fwd_combine<DP, WITH_O>), dim3(static_cast<unsigned>(batch * g.RT)), dim3(64), 0, s,
+    hipLaunchKernelGGL((k_flash_fwd_combine<DP, WITH_O>), dim3(static_cast<unsigned>(batch * g.RT)), dim3(256), 0, s,
                        a, g);
     return launch_status();
 }
@@ -1364,7 +1537,7 @@ int launch_bwd(const FlashBwdArgs& a, const FlashGeo& gr0, const FlashGeo& gc0, 
     if (int rc = launch_status()) return rc;
     if (gr.NR > 1)
     {
-        hipLaunchKernelGGL((k_flash_bwd_rows_combine<KP>), dim3(static_cast<unsigned>(batch * gr.RT)), dim3(64), 0,
+        hipLaunchKernelGGL((k_flash_bwd_rows_combine<KP>), dim3(static_cast<unsigned>(batch * gr.RT)), dim3(256), 0,
                            s, a, gr);
         if (int rc = launch_status()) return rc;
     }
@@ -1376,7 +1549,7 @@ int launch_bwd(const FlashBwdArgs& a, const FlashGeo& gr0, const FlashGeo& gc0, 
                            gc);
     if (int rc = launch_status()) return rc;
     if (gc.NR == 1) return 0;
-    hipLaunchKernelGGL((k_flash_bwd_cols_combine<KP>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(64), 0, s, a,
+    hipLaunchKernelGGL((k_flash_bwd_cols_combine<KP>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(256), 0, s, a,
                        gc);
     return launch_status();
 }
@@ -1479,7 +1652,7 @@ int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t bat
 size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K)
 {
     const int KP = pad32(K);
-    const size_t part = std::max(part_bytes(geo(batch, M, N, true, rows_pw(KP), nullptr, nullptr), batch, true),
+    const size_t part = std::max(part_bytes(geo(batch, M, N, true, dq_pw(KP), nullptr, nullptr), batch, true),
                                  part_bytes(geo(batch, M, N, false, cols_pw(KP), nullptr, nullptr), batch, false));
     return align256(batch * M * N * sizeof(float)) + align256(batch * M * sizeof(float)) + part;
 }
@@ -1493,18 +1666,13 @@ int flash_backward_ds(const FlashBwdArgs& a0, const float* O, int o_qm, const un
     const size_t M = static_cast<size_t>(a.M), N = static_cast<size_t>(a.N);
     a.dS = reinterpret_cast<float*>(w);
     w += align256(batch * M * N * sizeof(float));
-    // R in the workspace unless the caller wants it; the dQ pass ends in the
-    // query-line store, which also writes R (as 0): it is pointed there.
-    float* r_ws = reinterpret_cast<float*>(w);
-    if (!a.R) a.R = r_ws;
+    if (!a.R) a.R = reinterpret_cast<float*>(w);   // R kept in the workspace unless the caller wants it
     w += align256(batch * M * sizeof(float));
     a.g_do = 1;
-    FlashBwdArgs adq = a;
-    adq.R = r_ws;
     const int KP = pad32(static_cast<size_t>(a.K));
     const unsigned char* cl = a.mask ? cells : nullptr;
     const bool pb = a.mask && a.mask_bs != 0;
-    FlashGeo gr = geo(batch, M, N, true, rows_pw(KP), cl, w, pb);
+    FlashGeo gr = geo(batch, M, N, true, dq_pw(KP), cl, w, pb);
     FlashGeo gc = geo(batch, M, N, false, cols_pw(KP), cl, w, pb);
     if (a.mask && order)
     {
@@ -1512,7 +1680,7 @@ int flash_backward_ds(const FlashBwdArgs& a0, const float* O, int o_qm, const un
         gr.order = reinterpret_cast<const int*>(reinterpret_cast<const char*>(order) + order_table_bytes(gc, batch));
     }
     const long total = static_cast<long>(batch * M);
-    hipLaunchKernelGGL(k_flash_rowdot, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, a.dO, O,
+    hipLaunchKernelGGL(k_flash_rowdot, dim3(static_cast<unsigned>((total + 63) / 64)), dim3(256), 0, s, a.dO, O,
                        a.R, a.M, a.Kd, total, a.alpha2, o_qm ? 1 : 0);
     if (int rc = launch_status()) return rc;
     auto run = [&](auto kp) -> int {
@@ -1522,16 +1690,16 @@ int flash_backward_ds(const FlashBwdArgs& a0, const float* O, int o_qm, const un
         if (int rc = launch_status()) return rc;
         if (gc.NR > 1)
         {
-            hipLaunchKernelGGL((k_flash_bwd_cols_combine<P>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(64),
+            hipLaunchKernelGGL((k_flash_bwd_cols_combine<P>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(256),
                                0, s, a, gc);
             if (int rc = launch_status()) return rc;
         }
-        hipLaunchKernelGGL((k_flash_bwd_dq<P>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, adq, gr);
+        hipLaunchKernelGGL((k_flash_bwd_dq<P>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, a, gr);
         if (int rc = launch_status()) return rc;
         if (gr.NR > 1)
         {
-            hipLaunchKernelGGL((k_flash_bwd_rows_combine<P>), dim3(static_cast<unsigned>(batch * gr.RT)), dim3(64),
-                               0, s, adq, gr);
+            hipLaunchKernelGGL((k_flash_bwd_dq_combine<P>), dim3(static_cast<unsigned>(batch * gr.RT)), dim3(256),
+                               0, s, a, gr);
             if (int rc = launch_status()) return rc;
         }
         return 0;
