@@ -297,39 +297,62 @@ __device__ __forceinline__ void mask_row16(const MRow& x, int N, int jbase, int 
 }
 
 // Score chain: D[token drow(r,h)][line token c] = sum_k tile[c][k] * reg[k] over KP dims.
-template <int KP>
+// Scheduling fence after a chain's LDS reads when PRE: only VALU, SALU and
+// transcendental instructions may move across it, so the reads are all issued
+// before the first MFMA and the chain runs without waiting on LDS (costs the
+// registers of the whole A operand).
+template <bool PRE>
+__device__ __forceinline__ void operands_first()
+{
+    if constexpr (PRE) __builtin_amdgcn_sched_barrier(0x0406);
+}
+
+template <int KP, bool PRE = false>
 __device__ __forceinline__ f32x16 score_chain(const float (*tile)[KP + 4], const float* reg, int h, int c)
 {
     constexpr int KH = KP / 2;
+    float4 a[KH / 4];
+#pragma unroll
+    for (int q4 = 0; q4 < KH / 4; ++q4) a[q4] = *reinterpret_cast<const float4*>(&tile[c][KH * h + 4 * q4]);
+    operands_first<PRE>();
     f32x16 s = zero16();
 #pragma unroll
     for (int q4 = 0; q4 < KH / 4; ++q4)
     {
-        const float4 a = *reinterpret_cast<const float4*>(&tile[c][KH * h + 4 * q4]);
-        s = mfma(a.x, reg[4 * q4 + 0], s);
-        s = mfma(a.y, reg[4 * q4 + 1], s);
-        s = mfma(a.z, reg[4 * q4 + 2], s);
-        s = mfma(a.w, reg[4 * q4 + 3], s);
+        s = mfma(a[q4].x, reg[4 * q4 + 0], s);
+        s = mfma(a[q4].y, reg[4 * q4 + 1], s);
+        s = mfma(a[q4].z, reg[4 * q4 + 2], s);
+        s = mfma(a[q4].w, reg[4 * q4 + 3], s);
     }
     return s;
 }
 
 // acc[u] += tile^T (dims DU*c + u, tokens drow(r,h)) x w (tokens drow(r,h), line token c).
-template <int DP>
+template <int DP, bool PRE = false>
 __device__ __forceinline__ void value_chain(const float (*tile)[DP + 4], const float* w, int h, int c, f32x16* acc)
 {
     constexpr int DU = DP / 32;
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
+    if constexpr (DU == 2)
     {
-        if constexpr (DU == 2)
+        float2 a[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a[r] = *reinterpret_cast<const float2*>(&tile[drow(r, h)][2 * c]);
+        operands_first<PRE>();
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
         {
-            const float2 a = *reinterpret_cast<const float2*>(&tile[drow(r, h)][2 * c]);
-            acc[0] = mfma(a.x, w[r], acc[0]);
-            acc[1] = mfma(a.y, w[r], acc[1]);
+            acc[0] = mfma(a[r].x, w[r], acc[0]);
+            acc[1] = mfma(a[r].y, w[r], acc[1]);
         }
-        else
-            acc[0] = mfma(tile[drow(r, h)][c], w[r], acc[0]);
+    }
+    else
+    {
+        float a[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a[r] = tile[drow(r, h)][c];
+        operands_first<PRE>();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0] = mfma(a[r], w[r], acc[0]);
     }
 }
 
@@ -541,6 +564,12 @@ __global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(Fla
             if (act0 || act1)
             {
                 float x[CPS][16], cmax = kLowest;
+                // Every active cell's score chain first: the matrix core works
+                // on the second while the first one's scores are processed.
+                f32x16 scs[CPS];
+#pragma unroll
+                for (int t = 0; t < CPS; ++t)
+                    if (t ? act1 : act0) scs[t] = score_chain<KP, CPS == 2>(Ks[buf][t], qf, h, c);
 #pragma unroll
                 for (int t = 0; t < CPS; ++t)
                 {
@@ -552,7 +581,7 @@ __global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(Fla
                         continue;
                     }
                     const int jbase = 32 * (cell0 + cell);
-                    const f32x16 sc = score_chain<KP>(Ks[buf][t], qf, h, c);
+                    const f32x16& sc = scs[t];
                     const bool gen = (lw.gen >> cell) & 1ull, full = jbase + 32 <= g.N;
                     float cm;
                     if (full && !gen)
@@ -590,7 +619,7 @@ __global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(Fla
                         x[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[t][r], kLog2e, -mb));
                         lrun += x[t][r];
                     }
-                    if constexpr (WITH_O) value_chain<DP>(Vs[buf][t], x[t], h, c, o);
+                    if constexpr (WITH_O) value_chain<DP, CPS == 2>(Vs[buf][t], x[t], h, c, o);
                 }
             }
             if (n0 < 0) break;
@@ -1343,9 +1372,11 @@ __global__ __launch_bounds__(kOrderThreads) void k_flash_order(FlashGeo g, int r
 
 // R_i = alpha2 sum_d dO(d, i) O(d, i): dO per batch (Kd, M) dim-major; O the
 // same, or (M, Kd) query-major when o_qm. A workgroup takes 64 rows (one per
-// lane); wave w sums dims [w Kd/4, (w+1) Kd/4) (Kd % 4 == 0, Kd <= 64) in two
-// chains, and wave 0 adds the four partials in wave order. Query-major O rows
-// are contiguous: the workgroup's 64 Kd floats are staged through LDS.
+// lane); wave w sums dims [w q, (w+1) q), q = Kd / 4 <= 16, in two chains
+// (even and odd dims), and wave 0 adds the four partials in wave order.
+// Query-major O rows are contiguous: the workgroup's 64 Kd floats are staged
+// through LDS. Loops run a fixed 16 steps over clamped addresses, so every
+// load is in flight at once.
 __global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ dO, const float* __restrict__ O,
                                                       float* __restrict__ R, int M, int Kd, long total, float alpha2,
                                                       int o_qm)
@@ -1357,10 +1388,19 @@ __global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ 
     const int q = Kd / 4, d0 = wave * q;
     if (o_qm)
     {
+        // 64 rows x Kd floats, Kd / 4 per thread; past the last row reads 0.
         const long n = min(64L, total - t0) * Kd;
-        const float* ob = O + t0 * Kd;
-        for (int e = threadIdx.x; e < 64 * Kd; e += 256)
-            if (e < n) Ot[e / Kd][e % Kd] = ob[e];
+        const Rsrc rs = rsrc(O + t0 * Kd, n);
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = bload(rs, 4u * static_cast<unsigned>(threadIdx.x + 256 * k));
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (k < q)
+            {
+                const unsigned e = threadIdx.x + 256u * k;
+                Ot[e / static_cast<unsigned>(Kd)][e % static_cast<unsigned>(Kd)] = v[k];
+            }
         __syncthreads();
     }
     float acc[2] = {0.0f, 0.0f};
@@ -1368,28 +1408,18 @@ __global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ 
     {
         const long b = t / M, i = t % M;
         const float* p = dO + (b * Kd + d0) * M + i;
-        if (o_qm)
+        const float* od = O + (b * Kd + d0) * M + i;
+        float pv[16], ov[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
         {
-            const float* o = &Ot[lane][d0];
-            int d = 0;
-            for (; d + 2 <= q; d += 2)
-            {
-                acc[0] = __builtin_fmaf(p[(long)d * M], o[d], acc[0]);
-                acc[1] = __builtin_fmaf(p[(long)(d + 1) * M], o[d + 1], acc[1]);
-            }
-            if (d < q) acc[0] = __builtin_fmaf(p[(long)d * M], o[d], acc[0]);
+            const int kc = min(k, q - 1);
+            pv[k] = p[(long)kc * M];
+            ov[k] = o_qm ? Ot[lane][d0 + kc] : od[(long)kc * M];
         }
-        else
-        {
-            const float* o = O + (b * Kd + d0) * M + i;
-            int d = 0;
-            for (; d + 2 <= q; d += 2)
-            {
-                acc[0] = __builtin_fmaf(p[(long)d * M], o[(long)d * M], acc[0]);
-                acc[1] = __builtin_fmaf(p[(long)(d + 1) * M], o[(long)(d + 1) * M], acc[1]);
-            }
-            if (d < q) acc[0] = __builtin_fmaf(p[(long)d * M], o[(long)d * M], acc[0]);
-        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (k < q) acc[k & 1] = __builtin_fmaf(pv[k], ov[k], acc[k & 1]);
     }
     part[wave][lane] = acc[0] + acc[1];
     __syncthreads();
