@@ -13,7 +13,8 @@ part: the fused causal-attention primitives on BASELINE config 2 (forward:
 bmm_reduce Max -> softmax_denom -> softmax_apply) and config 5 (document-masked
 forward + backward over the 8 packed rows), as algorithmic TFLOP/s (4*d*P
 forward, 8*d*P backward over the P allowed (query, key) pairs) and as a
-fraction of the fp32 MFMA peak, timed with HIP events on the engine's stream.
+fraction of the fp32 MFMA peak, timed with HIP events on the engine's stream
+at a steady clock (0.25 s of untimed calls first, then at least 20 ms timed).
 `cpu_baseline` runs the CPU restatement of the reference CpuEngine (oracle/,
 loaded only for this leg) on a bounded sample of the same workload: the
 config-4 model at batch 1 of 8, one warmup and three timed training steps.
@@ -178,33 +179,82 @@ class StreamTimer:
 
 
 class Busy:
-    """Keeps the GPU busy while the host queues short kernels: two 4096^3 GEMMs
-    (~3 ms) are enqueued before the start event, so the launches that follow run
-    back to back and the event interval measures kernel time, not host
-    submission rate."""
+    """Keeps the GPU busy while the host queues short kernels: 4096^3 GEMMs
+    covering `ms` milliseconds are enqueued before the start event, so the
+    launches that follow run back to back and the event interval measures
+    kernel time, not host submission rate."""
 
     def __init__(self, eng, rng):
         self.eng = eng
         self.a = eng.tensor(rng.uniform(-1, 1, (4096, 4096)).astype(np.float32))
+        self.gemm_ms = None
 
-    def __call__(self):
-        for _ in range(2):
-            c = self.eng.matmul(self.a, self.a)
-            self.eng.settle()   # matmul is recorded until its result is used: launch it now
-            del c
+    def _gemm(self):
+        c = self.eng.matmul(self.a, self.a)
+        self.eng.settle()   # matmul is recorded until its result is used: launch it now
+        del c
+
+    def __call__(self, ms=3.0):
+        if self.gemm_ms is None:
+            self._gemm()
+            self.eng.sync()
+            t0 = time.perf_counter()
+            for _ in range(4):
+                self._gemm()
+            self.eng.sync()
+            self.gemm_ms = (time.perf_counter() - t0) * 1e3 / 4
+        for _ in range(max(2, math.ceil(ms / self.gemm_ms))):
+            self._gemm()
 
 
-def timed_ms(timer, busy, fn, reps, warmup=3):
-    """Average milliseconds per call of fn over reps back-to-back calls, after
-    `warmup` untimed calls. The engine records some calls instead of launching
-    them and skips results that nobody references, so each call's outputs are
-    held until settle() has launched what the call recorded, then dropped (the
-    pool hands the same block to the next call)."""
-    for _ in range(warmup):
+def timed_ms(timer, busy, fn, reps, warmup=3, steady=True, warm_s=0.25, min_ms=20.0):
+    """Average milliseconds per call of fn over back-to-back calls. steady
+    (compute-bound calls): after untimed calls for at least `warmup` calls and
+    warm_s seconds, over at least `reps` calls and min_ms of work, since the
+    GPU raises its clock only after a while under load (a config-2 forward
+    measured 63 TFLOP/s cold and 79 after a second of work) and short timed
+    regions would report the ramp. Otherwise (the short memory-bound kernels):
+    `warmup` untimed calls, then `reps` timed calls behind ~3 ms of GEMMs. The
+    engine records some calls instead of launching them and skips results that
+    nobody references, so each call's outputs are held until settle() has
+    launched what the call recorded, then dropped (the pool hands the same
+    block to the next call)."""
+    def call():
         keep = fn()
         busy.eng.settle()
         del keep
-    busy()
+
+    if not steady:
+        for _ in range(warmup):
+            call()
+        busy()
+        timer.start()
+        for _ in range(reps):
+            call()
+        return timer.stop_ms() / reps
+
+    t0, n = time.perf_counter(), 0
+    while n < warmup or time.perf_counter() - t0 < warm_s:
+        call()
+        n += 1
+        if n % 8 == 0:
+            busy.eng.sync()   # keep the host within a few calls of the GPU
+    busy.eng.sync()
+    # Host cost of queueing one call (measured behind GEMMs that keep the GPU
+    # busy) and an upper bound of its GPU time (host and GPU serialised).
+    busy(6.0)
+    t1 = time.perf_counter()
+    for _ in range(4):
+        call()
+    host_ms = (time.perf_counter() - t1) * 1e3 / 4
+    busy.eng.sync()
+    t2 = time.perf_counter()
+    for _ in range(4):
+        call()
+    busy.eng.sync()
+    gpu_ms = (time.perf_counter() - t2) * 1e3 / 4
+    reps = max(reps, min(2000, math.ceil(min_ms / max(gpu_ms, 1e-3))))
+    busy(1.25 * reps * host_ms + 2.0)
     timer.start()
     for _ in range(reps):
         keep = fn()
@@ -405,7 +455,7 @@ def hbm_leg(seed):
             it[0] += 1
             return call(t)
         reps = max(20, copies)
-        ms = timed_ms(timer, busy, fn_call, reps)
+        ms = timed_ms(timer, busy, fn_call, reps, steady=False)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out.append({"kernel": name, "bytes": nbytes, "ms": ms, "GB_s": gbs, "frac_of_hbm_peak": gbs / PEAK_HBM_GBS,
                     "input_copies": copies})
