@@ -95,7 +95,7 @@ def inference_leg(g, seed, tokens=64, warmup=8):
             "workload": "config-4 model, batch 1, one token per forward_step (KV caches), logits read back"}
 
 
-def gpu_leg(steps, warmup, seed):
+def gpu_leg(steps, warmup, seed, inference=True):
     import nnengine
     lib = nnengine.hip_library()
     eng = nnengine.Engine(lib)
@@ -142,7 +142,7 @@ def gpu_leg(steps, warmup, seed):
     ms = ctypes.c_double(float(rec[:, 6].sum()))
     print(f"[bench] timed {steps} steps in {elapsed:.3f}s, losses {[round(x, 4) for x in losses]}",
           file=sys.stderr, flush=True)
-    infer = inference_leg(g, seed)
+    infer = inference_leg(g, seed) if inference else None
     for x in losses:
         if not math.isfinite(x):
             raise RuntimeError(f"non-finite loss {x}")
@@ -628,6 +628,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--skip-cpu-baseline", action="store_true")
     ap.add_argument("--skip-attention", action="store_true")
+    ap.add_argument("--skip-inference", action="store_true",
+                    help="no incremental-inference leg (kernel traces of the training step alone)")
     ap.add_argument("--skip-gemm-sweep", action="store_true")
     ap.add_argument("--skip-hbm", action="store_true")
     ap.add_argument("--pmc-sample", action="store_true",
@@ -656,7 +658,7 @@ def main():
     if args.hbm_only:
         print(json.dumps({"hbm_kernels": hbm_leg(args.seed)}), flush=True)
         return
-    gpu = gpu_leg(args.steps, args.warmup, args.seed)
+    gpu = gpu_leg(args.steps, args.warmup, args.seed, inference=not args.skip_inference)
     attn = None if args.skip_attention else attention_leg(args.seed)
     sweep = None if args.skip_gemm_sweep else gemm_leg(args.seed)
     hbm = None if args.skip_hbm else hbm_leg(args.seed)
