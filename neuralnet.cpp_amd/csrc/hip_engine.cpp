@@ -1385,6 +1385,18 @@ Result<Tensor> HipEngine::slice_rows(const Tensor& src, std::size_t start, std::
     auto view = std::make_shared<HipView>(std::move(root), off, n);
     std::erase_if(views_, [](const std::weak_ptr<DeviceBuffer>& w) { return w.expired(); });
     views_.push_back(view);
+    if (view_keys_.size() > 4 * views_.size() + 64)   // drop keys of views gone since the last rebuild
+    {
+        view_keys_.clear();
+        for (const auto& w : views_)
+            if (auto sp = w.lock())
+            {
+                view_keys_.insert(sp.get());
+                view_keys_.insert(static_cast<HipView*>(sp.get())->root());
+            }
+    }
+    view_keys_.insert(view.get());
+    view_keys_.insert(view->root());
     return Tensor(std::static_pointer_cast<DeviceBuffer>(view), count, src.cols());
 }
 
@@ -1396,7 +1408,7 @@ Result<void> HipEngine::unshare_(const Tensor& t)
 {
     if (views_.empty()) return {};
     const DeviceBuffer* b = t.device_buffer().get();
-    if (!b) return {};
+    if (!b || !view_keys_.count(b)) return {};   // neither a view nor the memory of one
     auto take_copy = [&](HipView& v) -> Result<void> {
         const std::size_t n = v.capacity();
         NN_TRY(own, alloc_(1, n));
@@ -1414,6 +1426,13 @@ Result<void> HipEngine::unshare_(const Tensor& t)
         auto sp = w.lock();
         return !sp || !static_cast<HipView*>(sp.get())->aliased();
     });
+    view_keys_.clear();
+    for (const auto& w : views_)
+        if (auto sp = w.lock())
+        {
+            view_keys_.insert(sp.get());
+            view_keys_.insert(static_cast<HipView*>(sp.get())->root());
+        }
     return {};
 }
 

@@ -37,6 +37,7 @@
 #include <memory>
 #include <optional>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "compute_engine.hpp"
@@ -183,6 +184,9 @@ private:
     };
     std::vector<CellTable> cells_;
     std::vector<std::weak_ptr<DeviceBuffer>> views_;   // live row-slice views (HipView)
+    // Every live aliased view and its root (may also hold buffers no longer
+    // in that role): a write to any other buffer needs no unsharing.
+    std::unordered_set<const DeviceBuffer*> view_keys_;
     Result<const void*> mask_cells_(const Tensor* mask, std::size_t M, std::size_t N);
     Result<const void*> flash_order_(const void* cells, std::size_t batch, std::size_t M, std::size_t N,
                                      std::size_t mask_bs, int kind);
