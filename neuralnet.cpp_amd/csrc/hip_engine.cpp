@@ -554,7 +554,24 @@ HipEngine::~HipEngine()
 }
 
 // ── GEMM event profile ──────────────────────────────────────────────────────
-void HipEngine::set_gemm_profile(bool on) { profile_ = on; }
+// Turning the profile on creates the events of the launches to come first
+// (two per GEMM; 8192 cover a default bench run of 10 config-4 steps), so the
+// profiled region records events without creating them.
+void HipEngine::set_gemm_profile(bool on)
+{
+    profile_ = on;
+    constexpr std::size_t kReserve = 8192;
+    while (on && event_pool_.size() < kReserve)
+    {
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess)
+        {
+            (void)hipGetLastError();
+            break;
+        }
+        event_pool_.push_back(e);
+    }
+}
 
 void HipEngine::prof_begin_()
 {
