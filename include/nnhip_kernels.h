@@ -247,10 +247,14 @@ int nnhip_flash_backward_ds(const float* Q, const float* Kt, const float* dO, co
 size_t nnhip_flash_order_bytes(size_t batch, size_t M, size_t N, int kind);
 int nnhip_flash_build_order(const void* cells, size_t batch, size_t M, size_t N, size_t mask_batch_stride, int kind,
                             void* order, void* stream);
+/* scores (forward, may be NULL): each visited 32 x 32 cell's alpha q.k + mask, -inf past N, stored as
+ * a block of 1024 floats at ((b*RT + query tile)*CT + key tile)*1024 (RT, CT = M, N in 32-tiles), score
+ * (query q, key k) at r*64 + h*32 + q where k = 8*(r/4) + 4*h + r%4; batch*RT*CT*1024 floats. The
+ * dS backward reads them back (scores, same cells and shape) instead of computing them again. */
 int nnhip_flash_forward_ordered(const float* Q, const float* Kt, const float* V, const float* mask, const void* cells,
                                 float* m, float* l, float* O, size_t batch, size_t M, size_t N, size_t K, size_t D,
                                 float alpha, size_t mask_batch_stride, int v_dim_major, int o_dim_major,
-                                const void* order, void* workspace, void* stream);
+                                float* scores, const void* order, void* workspace, void* stream);
 int nnhip_flash_backward_ordered(const float* Q, const float* Kt, const float* dO, const float* Vp, const float* G,
                                  size_t ldg, const float* mask, const void* cells, const float* m, const float* l,
                                  float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K,
@@ -262,7 +266,7 @@ int nnhip_flash_backward_ds_ordered(const float* Q, const float* Kt, const float
                                     int o_query_major, const float* mask, const void* cells, const float* m,
                                     const float* l, float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M,
                                     size_t N, size_t K, float alpha, float alpha2, size_t mask_batch_stride,
-                                    const void* order, void* workspace, void* stream);
+                                    const float* scores, const void* order, void* workspace, void* stream);
 
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */

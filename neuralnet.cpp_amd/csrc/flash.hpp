@@ -37,6 +37,7 @@ struct FlashFwdArgs
     long mask_bs;        // floats between batch entries' masks (0: one mask shared)
     int v_dm;            // V per batch is (D, N) [dim][key] instead of (N, D)
     int o_dm;            // O per batch is written (D, M) [dim][query] instead of (M, D)
+    float* S;            // when set: each visited cell's scores (alpha q.k + mask) as a score block
 };
 
 // Backward: R (batch*M), dQ (batch*K, M), dK and dV (batch*K, N) from
@@ -60,7 +61,16 @@ struct FlashBwdArgs
     long mask_bs;        // floats between batch entries' masks (0: one mask shared)
     int g_do;            // G_i is dO's column i (dV_j = sum_i W dO_i; needs Kd == K)
     float* dS;           // the key-line pass also stores dS_ij = W (P - R_i) here, (batch*M, N)
+    const float* S;      // when set: the forward's score blocks; the key-line pass reads them instead of
+                         // recomputing alpha q.k + mask
 };
+// Score blocks: one per 32 x 32 cell, block (b, query tile, key tile) at
+// ((b RT + qt) CT + kt) 1024 floats; inside, score (query q, key k) at
+// r 64 + h 32 + q with drow(r, h) = k (the forward's lane order).
+inline size_t score_blocks_floats(size_t batch, size_t M, size_t N)
+{
+    return batch * ((M + 31) / 32) * ((N + 31) / 32) * 1024;
+}
 
 // Shapes the one-pass kernels take: head dims K (and Kd) <= 64, value width
 // D <= 64 with D % 4 == 0. The backward also needs K % 4 == 0 and ldg % 4 == 0.

@@ -412,6 +412,7 @@ struct HipEngine::PendingAttn
     Tensor m, l;              // row max and sum, once the fused forward has run
     Tensor V, O;              // the fused forward's values and output (R_i = dO_i . O_i in the backward)
     bool stats = false, materialised = false;
+    bool scores = false;      // A's memory holds the fused forward's score blocks (until materialised)
     bool uses(const float* p) const
     {
         return has_buf(Q, p) || has_buf(K, p) || has_buf(mask, p) || has_buf(A, p) || has_buf(V, p) ||
@@ -835,7 +836,7 @@ Result<void> HipEngine::settle_fwd_()
     NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(f->batch, f->M, f->N, f->Kd, 4, 0)));
     return kernel_(nnhip_flash_forward_ordered(D(f->Q), D(f->K), nullptr, f->mask ? D(*f->mask) : nullptr, cells,
                                                W(f->m), W(l), nullptr, f->batch, f->M, f->N, f->Kd, 4, f->alpha, 0, 0,
-                                               0, order, ws->data(), stream_),
+                                               0, nullptr, order, ws->data(), stream_),
                    "batched_matmul_reduce");
 }
 
@@ -1012,15 +1013,19 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
         const std::size_t bs = p->mask.rows() == p->M ? 0 : p->M * p->N;
         NN_TRY(order, flash_order_(cells, batch, p->M, p->N, bs, 0));
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, p->M, p->N, p->Kd, Dv, 0)));
+        // The scores go to A's memory (the probabilities, written only if read through the engine),
+        // one 32 x 32 block per cell, when M and N are whole tiles (then the blocks fill it exactly).
+        const bool keep_scores = !p->materialised && p->M % 32 == 0 && p->N % 32 == 0;
         NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(p->Q), D(p->K), D(A), D(p->mask), cells, W(m), W(l), W(out),
-                                                     batch, p->M, p->N, p->Kd, Dv, p->alpha, bs, 1, 1, order,
-                                                     ws->data(), stream_),
+                                                     batch, p->M, p->N, p->Kd, Dv, p->alpha, bs, 1, 1,
+                                                     keep_scores ? W(p->A) : nullptr, order, ws->data(), stream_),
                          "attention forward"));
         p->m = m;
         p->l = l;
         p->V = A;
         p->O = out;
         p->stats = true;
+        p->scores = keep_scores;
         return R(out);
     }
     // dV = dO A per batch: recorded for the fused backward.
@@ -1060,7 +1065,8 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
             NN_CHECK(kernel_(nnhip_flash_backward_ds_ordered(D(q.Q), D(q.K), D(pds_->dO), D(pds_->Vp), D(q.O), 0,
                                                              D(q.mask), cells, D(q.m), D(q.l), nullptr, W(dQ), W(dK),
                                                              W(dV), batch, q.M, q.N, q.Kd, q.alpha, pds_->alpha2, bs,
-                                                             order, ws->data(), stream_),
+                                                             q.scores && !q.materialised ? D(q.A) : nullptr, order,
+                                                             ws->data(), stream_),
                              "attention backward"));
         }
         else
@@ -1763,7 +1769,7 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, d.K, V.cols(), 0)));
         NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(A), D(B), D(Vs), mask ? D(*mask) : nullptr, cells, W(f->m),
                                                      W(*f->l), W(o), batch, d.M, d.N, d.K, V.cols(), alpha, 0,
-                                                     v_src ? 1 : 0, 0, order, ws->data(), stream_),
+                                                     v_src ? 1 : 0, 0, nullptr, order, ws->data(), stream_),
                          "batched_matmul_softmax_apply"));
         if (v_src)
         {
@@ -1873,7 +1879,7 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
             NN_CHECK(kernel_(nnhip_flash_backward_ds_ordered(D(A), D(B), D(g.A), D(g.B), D(r.O), 1,
                                                              mask ? D(*mask) : nullptr, cells, D(row_max), D(denom),
                                                              W(q->R), W(q->dQ), W(dk), W(dv), batch, d.M, d.N, d.K,
-                                                             alpha, g.alpha, 0, order, ws->data(), stream_),
+                                                             alpha, g.alpha, 0, nullptr, order, ws->data(), stream_),
                              "batched_matmul_softmax_backward_kv"));
         }
         else

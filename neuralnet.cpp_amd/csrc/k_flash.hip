@@ -593,6 +593,13 @@ __global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(Fla
                     else
                         cm = cell_scores<false, true>(sc, a.alpha, mrow, g.N, jbase, h, x[t]);
                     cmax = fmax_f(cmax, cm);
+                    if (a.S)
+                    {
+                        // The cell's scores for the key-line pass, in this lane order.
+                        float* blk = a.S + (((long)it.b * g.RT + line) * g.CT + (cell0 + cell)) * 1024 + lane;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) blk[r * 64] = x[t][r];
+                    }
                 }
                 cmax = fmax_f(cmax, __shfl_xor(cmax, 32));
                 const float mnew = fmax_f(mrun, cmax);
@@ -983,7 +990,7 @@ __device__ __forceinline__ void cols_store(const FlashBwdArgs& a, const FlashGeo
         }
 }
 
-template <int KP, bool GDO, bool WDS>
+template <int KP, bool GDO, bool WDS, bool SST>
 __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo& g, int b, int grp, int rg,
                                            float (*Qs)[32][KP + 4], float (*Os)[32][KP + 4],
                                            float (*Gs)[32][KP + 4], float (*St)[3][32], unsigned long long* nz_s)
@@ -1020,9 +1027,13 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
         int cur = __builtin_ctzll(any);
         unsigned long long rest = any & (any - 1);
         stage_cols<KP, GDO>(qt, ot, gt, st, Qb, Ob, Gb, mb, lb, Rb, a, g.M, 32 * (cell0 + cur));
-        float kf[KP / 2], vf[KP / 2];
-        line_operand<KP>(Kb, a.K, g.N, kj, h, kf);
+        float kf[SST ? 1 : KP / 2], vf[KP / 2];
+        if constexpr (!SST) line_operand<KP>(Kb, a.K, g.N, kj, h, kf);
         line_operand<KP>(Vb, a.Kd, g.N, kj, h, vf);
+        // SST: this lane's key c in the forward's score blocks (r 64 + h 32 + q with drow(r, h) = c).
+        const float* sl = SST ? a.S + ((long)b * g.RT * g.CT + line) * 1024 + (4 * (c >> 3) + (c & 3)) * 64 +
+                                    ((c >> 2) & 1) * 32 + 4 * h
+                              : nullptr;
         const int jc = min(kj, g.N - 1);
         const float* mk = a.mask ? a.mask + b * a.mask_bs : nullptr;
         qt.store(Qs[0], threadIdx.x);
@@ -1038,18 +1049,41 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
             if ((lw.nz >> cur) & 1ull)
             {
                 const int ibase = 32 * (cell0 + cur);
-                const f32x16 s = score_chain<KP>(Qs[buf], kf, h, c);
-                const f32x16 p = score_chain<KP>(Os[buf], vf, h, c);
                 float w[16], ds[16];
                 const bool gen = (lw.gen >> cur) & 1ull, full = ibase + 32 <= g.M && (line + 1) * 32 <= g.N;
-                if (full && !gen)
-                    col_scores<true, false>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
-                else if (full)
-                    col_scores<true, true>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
-                else if (!gen)
-                    col_scores<false, false>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
-                else
-                    col_scores<false, true>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
+                if constexpr (SST)
+                {
+                    // Block (query tile cell0 + cur, key tile line): queries drow(r, h), 4 at a time.
+                    const float* blk = sl + (long)(cell0 + cur) * g.CT * 1024;
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4)
+                    {
+                        const float4 v = *reinterpret_cast<const float4*>(blk + 8 * g4);
+                        w[4 * g4 + 0] = v.x;
+                        w[4 * g4 + 1] = v.y;
+                        w[4 * g4 + 2] = v.z;
+                        w[4 * g4 + 3] = v.w;
+                    }
+                    if (!full)
+                    {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            w[r] = (ibase + drow(r, h) < g.M && kj < g.N) ? w[r] : kNegInf;
+                    }
+                }
+                const f32x16 p = score_chain<KP>(Os[buf], vf, h, c);
+                if constexpr (!SST)
+                {
+                    const f32x16 s = score_chain<KP>(Qs[buf], kf, h, c);
+                    if (full && !gen)
+                        col_scores<true, false>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
+                    else if (full)
+                        col_scores<true, true>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
+                    else if (!gen)
+                        col_scores<false, false>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
+                    else
+                        col_scores<false, true>(s, a, mk, ibase, jc, kj, h, g.M, g.N, w);
+                }
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                 {
@@ -1089,7 +1123,7 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
     cols_store<KP>(a, g, lw, b, line, rg, dk, dv);
 }
 
-template <int KP, bool GDO, bool WDS>
+template <int KP, bool GDO, bool WDS, bool SST = false>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdArgs a, FlashGeo g)
 {
     __shared__ __align__(16) float Qs[2][32][KP + 4];   // query tile [query][dim]
@@ -1098,7 +1132,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdArgs 
     __shared__ float St[2][3][32];                      // m, 1/l, R of the tile's queries
     __shared__ unsigned long long nz_s[kWaves];
     const Item it = item_of(g);
-    cols_group<KP, GDO, WDS>(a, g, it.b, it.grp, it.rg, Qs, Os, Gs, St, nz_s);
+    cols_group<KP, GDO, WDS, SST>(a, g, it.b, it.grp, it.rg, Qs, Os, Gs, St, nz_s);
 }
 
 template <int KP>
@@ -1715,8 +1749,12 @@ int flash_backward_ds(const FlashBwdArgs& a0, const float* O, int o_qm, const un
     if (int rc = launch_status()) return rc;
     auto run = [&](auto kp) -> int {
         constexpr int P = decltype(kp)::value;
-        hipLaunchKernelGGL((k_flash_bwd_cols<P, true, true>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a,
-                           gc);
+        if (a.S)
+            hipLaunchKernelGGL((k_flash_bwd_cols<P, true, true, true>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0,
+                               s, a, gc);
+        else
+            hipLaunchKernelGGL((k_flash_bwd_cols<P, true, true>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s,
+                               a, gc);
         if (int rc = launch_status()) return rc;
         if (gc.NR > 1)
         {
@@ -1752,15 +1790,15 @@ extern "C" int nnhip_flash_backward_ds(const float* Q, const float* Kt, const fl
                                        void* workspace, void* stream)
 {
     return nnhip_flash_backward_ds_ordered(Q, Kt, dO, Vp, O, 0, mask, cells, m, l, nullptr, dQ, dK, dV, batch, M, N,
-                                           K, alpha, alpha2, mask_batch_stride, nullptr, workspace, stream);
+                                           K, alpha, alpha2, mask_batch_stride, nullptr, nullptr, workspace, stream);
 }
 
 extern "C" int nnhip_flash_backward_ds_ordered(const float* Q, const float* Kt, const float* dO, const float* Vp,
                                                const float* O, int o_query_major, const float* mask,
                                                const void* cells, const float* m, const float* l, float* R, float* dQ,
                                                float* dK, float* dV, size_t batch, size_t M, size_t N, size_t K,
-                                               float alpha, float alpha2, size_t mask_batch_stride, const void* order,
-                                               void* workspace, void* stream)
+                                               float alpha, float alpha2, size_t mask_batch_stride,
+                                               const float* scores, const void* order, void* workspace, void* stream)
 {
     if (!Q || !Kt || !dO || !Vp || !O || !m || !l || !dQ || !dK || !dV || !workspace || (mask && !cells)) return -1;
     if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
@@ -1769,6 +1807,7 @@ extern "C" int nnhip_flash_backward_ds_ordered(const float* Q, const float* Kt, 
                           static_cast<int>(N), static_cast<int>(K), static_cast<int>(K), static_cast<int>(K), alpha,
                           alpha2};
     a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
+    a.S = scores;
     return nnhip::flash_backward_ds(a, O, o_query_major, static_cast<const unsigned char*>(cells), batch, workspace,
                                     static_cast<const int*>(order), static_cast<hipStream_t>(stream));
 }
@@ -1814,14 +1853,14 @@ extern "C" int nnhip_flash_forward_layout(const float* Q, const float* Kt, const
                                           int v_dim_major, int o_dim_major, void* workspace, void* stream)
 {
     return nnhip_flash_forward_ordered(Q, Kt, V, mask, cells, m, l, O, batch, M, N, K, D, alpha, mask_batch_stride,
-                                       v_dim_major, o_dim_major, nullptr, workspace, stream);
+                                       v_dim_major, o_dim_major, nullptr, nullptr, workspace, stream);
 }
 
 extern "C" int nnhip_flash_forward_ordered(const float* Q, const float* Kt, const float* V, const float* mask,
                                            const void* cells, float* m, float* l, float* O, size_t batch, size_t M,
                                            size_t N, size_t K, size_t D, float alpha, size_t mask_batch_stride,
-                                           int v_dim_major, int o_dim_major, const void* order, void* workspace,
-                                           void* stream)
+                                           int v_dim_major, int o_dim_major, float* scores, const void* order,
+                                           void* workspace, void* stream)
 {
     if (!Q || !Kt || !m || !l || (O && !V) || (mask && !cells)) return -1;
     if (mask && mask_batch_stride != 0 && mask_batch_stride < M * N) return -1;
@@ -1831,6 +1870,7 @@ extern "C" int nnhip_flash_forward_ordered(const float* Q, const float* Kt, cons
     a.mask_bs = mask ? static_cast<long>(mask_batch_stride) : 0;
     a.v_dm = v_dim_major ? 1 : 0;
     a.o_dm = o_dim_major ? 1 : 0;
+    a.S = scores;
     return nnhip::flash_forward(a, static_cast<const unsigned char*>(cells), batch, workspace,
                                 static_cast<const int*>(order), static_cast<hipStream_t>(stream));
 }

@@ -121,6 +121,23 @@ def test_chain_reads_and_orders(hip, cpu, read_A, read_gS, order, with_dv):
     check(run(hip, arrs, mask, B * H, T, 0.125, **kw), run(cpu, arrs, mask, B * H, T, 0.125, **kw))
 
 
+def test_probabilities_read_after_backward(hip, cpu):
+    """With whole 32 x 32 tiles the fused forward keeps its scores in A's memory for the backward;
+    A read after the backward still holds the probabilities."""
+    B, H, T, dk = 2, 2, 128, 64
+    BH = B * H
+    mask = attn_mask(B, H, T)
+    arrs = inputs(5, BH, T, dk)
+
+    def go(e):
+        q, k, v, g = (e.tensor(a) for a in arrs)
+        A, O = fwd(e, q, k, v, e.tensor(mask), BH, T, 0.125)
+        gS, gq, gk, gv = bwd(e, q, k, v, A, g, BH, T, 0.125)
+        return {"O": O.numpy(), "dQ": gq.numpy(), "dK": gk.numpy(), "dV": gv.numpy(), "A": A.numpy()}
+
+    check(go(hip), go(cpu))
+
+
 def test_two_layers_back_to_back(hip, cpu):
     """Two recorded layers between forward and backward (backward in reverse order), as in a model."""
     B, H, T, dk = 1, 3, 128, 64
