@@ -468,6 +468,7 @@ struct HipEngine::TwoPassOut
     Tensor m, l, Vs, O;
     std::size_t batch;
     float alpha;
+    Tensor S;   // the forward's score blocks for the backward, or empty
     bool uses(const float* p) const
     {
         return has_buf(Q, p) || has_buf(K, p) || (mask && has_buf(*mask, p)) || has_buf(m, p) || has_buf(l, p) ||
@@ -1767,18 +1768,32 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
         NN_TRY(cells, mask_cells_(mask, d.M, d.N));
         NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 0));
         NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, d.K, V.cols(), 0)));
-        NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(A), D(B), D(Vs), mask ? D(*mask) : nullptr, cells, W(f->m),
-                                                     W(*f->l), W(o), batch, d.M, d.N, d.K, V.cols(), alpha, 0,
-                                                     v_src ? 1 : 0, 0, nullptr, order, ws->data(), stream_),
-                         "batched_matmul_softmax_apply"));
+        // A recorded output also keeps the forward's scores for the backward
+        // (one 32 x 32 block per cell, so M and N whole tiles), while all
+        // records together hold at most kScoreBytes of them.
+        Tensor S;
         if (v_src)
         {
             forget_dead_two_();
             constexpr std::size_t kKeep = 64;   // one per layer
             if (ptwo_.size() >= kKeep) ptwo_.erase(ptwo_.begin());
-            ptwo_.push_back(TwoPassOut{A, B, mask ? std::optional<Tensor>(*mask) : std::nullopt, f->m, *f->l, Vs, o,
-                                       batch, alpha});
+            constexpr std::size_t kScoreBytes = std::size_t(8) << 30;
+            std::size_t held = 0;
+            for (const TwoPassOut& r : ptwo_) held += r.S.size() * sizeof(float);
+            if (d.M % 32 == 0 && d.N % 32 == 0 && held + batch * d.M * d.N * sizeof(float) <= kScoreBytes)
+            {
+                NN_TRY(t, alloc_(batch * d.M, d.N));
+                S = t;
+            }
         }
+        NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(A), D(B), D(Vs), mask ? D(*mask) : nullptr, cells, W(f->m),
+                                                     W(*f->l), W(o), batch, d.M, d.N, d.K, V.cols(), alpha, 0,
+                                                     v_src ? 1 : 0, 0, S.size() ? W(S) : nullptr, order, ws->data(),
+                                                     stream_),
+                         "batched_matmul_softmax_apply"));
+        if (v_src)
+            ptwo_.push_back(TwoPassOut{A, B, mask ? std::optional<Tensor>(*mask) : std::nullopt, f->m, *f->l, Vs, o,
+                                       batch, alpha, S});
         return o;
     }
     NN_CHECK(settle_reads_({&A, &B, &V, &row_max, &denom, mask}));
@@ -1879,7 +1894,8 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
             NN_CHECK(kernel_(nnhip_flash_backward_ds_ordered(D(A), D(B), D(g.A), D(g.B), D(r.O), 1,
                                                              mask ? D(*mask) : nullptr, cells, D(row_max), D(denom),
                                                              W(q->R), W(q->dQ), W(dk), W(dv), batch, d.M, d.N, d.K,
-                                                             alpha, g.alpha, 0, nullptr, order, ws->data(), stream_),
+                                                             alpha, g.alpha, 0, r.S.size() ? D(r.S) : nullptr, order,
+                                                             ws->data(), stream_),
                              "batched_matmul_softmax_backward_kv"));
         }
         else

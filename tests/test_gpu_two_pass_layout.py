@@ -5,7 +5,9 @@ with transpose + rearrange_3d (reference compute_layer.hpp:1211-1214,
 :1309-1313). The HIP engine records both calls: softmax_apply reads V from its
 source, backward_kv reads G from dO, and any other reader of a recorded result
 gets the copy. When the forward's output O is still referenced, backward_kv
-takes R_i = dO_i . O_i from it and makes one score pass instead of two.
+takes R_i = dO_i . O_i from it and makes one score pass instead of two; with
+whole 32 x 32 tiles (T 256, 512 here) that pass reads the scores the forward
+kept instead of forming them again.
 
 Bars: the recorded layouts bit-exact against numpy, including after in-place
 writes to their source or result; every backward variant within 1e-4 (O, R)
@@ -103,7 +105,8 @@ def _row(e, Q, K, V, dO, mask, H, variant):
     return out
 
 
-@pytest.mark.parametrize("H,T,d,masked", [(4, 300, 64, True), (3, 256, 32, False), (2, 520, 64, True)])
+@pytest.mark.parametrize("H,T,d,masked", [(4, 300, 64, True), (3, 256, 32, False), (2, 520, 64, True),
+                                            (2, 512, 64, True)])
 def test_two_pass_backward_variants(hip, cpu, H, T, d, masked):
     rng = np.random.default_rng(H * T + d)
     mask = doc_mask(doc_ids_from_lengths(doc_lengths(rng, T, 20, 200))) if masked else None
