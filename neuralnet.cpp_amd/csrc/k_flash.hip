@@ -1036,6 +1036,23 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
                               : nullptr;
         const int jc = min(kj, g.N - 1);
         const float* mk = a.mask ? a.mask + b * a.mask_bs : nullptr;
+        // SST: block (query tile cell0 + x, key tile line), queries drow(r, h), 4 at a time;
+        // a cell's block is loaded one cell ahead of its chains.
+        auto score_block = [&](int x, float* w) {
+            const float* blk = sl + (long)(cell0 + x) * g.CT * 1024;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4)
+            {
+                const float4 v = *reinterpret_cast<const float4*>(blk + 8 * g4);
+                w[4 * g4 + 0] = v.x;
+                w[4 * g4 + 1] = v.y;
+                w[4 * g4 + 2] = v.z;
+                w[4 * g4 + 3] = v.w;
+            }
+        };
+        float sw[SST ? 16 : 1];
+        if constexpr (SST)
+            if ((lw.nz >> cur) & 1ull) score_block(cur, sw);
         qt.store(Qs[0], threadIdx.x);
         ot.store(Os[0], threadIdx.x);
         if constexpr (!GDO) gt.store(Gs[0], threadIdx.x);
@@ -1046,6 +1063,9 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
         {
             const int nxt = rest ? __builtin_ctzll(rest) : -1;
             if (nxt >= 0) stage_cols<KP, GDO>(qt, ot, gt, st, Qb, Ob, Gb, mb, lb, Rb, a, g.M, 32 * (cell0 + nxt));
+            float swn[SST ? 16 : 1];
+            if constexpr (SST)
+                if (nxt >= 0 && ((lw.nz >> nxt) & 1ull)) score_block(nxt, swn);
             if ((lw.nz >> cur) & 1ull)
             {
                 const int ibase = 32 * (cell0 + cur);
@@ -1053,17 +1073,8 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
                 const bool gen = (lw.gen >> cur) & 1ull, full = ibase + 32 <= g.M && (line + 1) * 32 <= g.N;
                 if constexpr (SST)
                 {
-                    // Block (query tile cell0 + cur, key tile line): queries drow(r, h), 4 at a time.
-                    const float* blk = sl + (long)(cell0 + cur) * g.CT * 1024;
 #pragma unroll
-                    for (int g4 = 0; g4 < 4; ++g4)
-                    {
-                        const float4 v = *reinterpret_cast<const float4*>(blk + 8 * g4);
-                        w[4 * g4 + 0] = v.x;
-                        w[4 * g4 + 1] = v.y;
-                        w[4 * g4 + 2] = v.z;
-                        w[4 * g4 + 3] = v.w;
-                    }
+                    for (int r = 0; r < 16; ++r) w[r] = sw[r];
                     if (!full)
                     {
 #pragma unroll
@@ -1110,6 +1121,11 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
                 }
             }
             if (nxt < 0) break;
+            if constexpr (SST)
+            {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sw[r] = swn[r];
+            }
             qt.store(Qs[buf ^ 1], threadIdx.x);
             ot.store(Os[buf ^ 1], threadIdx.x);
             if constexpr (!GDO) gt.store(Gs[buf ^ 1], threadIdx.x);
@@ -1287,20 +1303,25 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a,
         int cur = __builtin_ctzll(any);
         unsigned long long rest = any & (any - 1);
         kt.load(Kb, a.K, g.N, 32 * (cell0 + cur), threadIdx.x);
+        // This line's dS of a cell is loaded one cell ahead of its chain.
+        float w[16];
+        if ((lw.nz >> cur) & 1ull) mask_row16(dsrow, g.N, 32 * (cell0 + cur), h, w);
         kt.store(Ks[0], threadIdx.x);
         __syncthreads();
         int buf = 0;
         while (true)
         {
             const int nxt = rest ? __builtin_ctzll(rest) : -1;
-            if (nxt >= 0) kt.load(Kb, a.K, g.N, 32 * (cell0 + nxt), threadIdx.x);
-            if ((lw.nz >> cur) & 1ull)
+            float wn[16];
+            if (nxt >= 0)
             {
-                float w[16];
-                mask_row16(dsrow, g.N, 32 * (cell0 + cur), h, w);
-                value_chain<KP>(Ks[buf], w, h, c, x);
+                kt.load(Kb, a.K, g.N, 32 * (cell0 + nxt), threadIdx.x);
+                if ((lw.nz >> nxt) & 1ull) mask_row16(dsrow, g.N, 32 * (cell0 + nxt), h, wn);
             }
+            if ((lw.nz >> cur) & 1ull) value_chain<KP>(Ks[buf], w, h, c, x);
             if (nxt < 0) break;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) w[r] = wn[r];
             kt.store(Ks[buf ^ 1], threadIdx.x);
             __syncthreads();
             buf ^= 1;
