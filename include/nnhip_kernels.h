@@ -312,6 +312,12 @@ int nnhip_row_softmax_backward(const float* Y, const float* G, float* out, size_
 int nnhip_rmsnorm_sumsq(const float* X, float* out, size_t F, size_t N, void* stream);
 int nnhip_colbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream);
 int nnhip_rowbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream);
+/* RMSNorm::forward's six calls in one pass (compute_layer.hpp:733-754; no CUDA counterpart): s = sumsq(X),
+ * scaled = s * inv_f, var_eps = scaled + eps, rinv = 1 / sqrt(var_eps), normed = X * rinv[c],
+ * out = normed * gamma[r], equal bit for bit to the separate calls; s_raw, scaled and var_eps (N) may be
+ * NULL (not written). 1 <= F <= 1024. */
+int nnhip_rmsnorm_forward(const float* X, const float* gamma, float inv_f, float eps, float* s_raw, float* scaled,
+                          float* var_eps, float* rinv, float* normed, float* out, size_t F, size_t N, void* stream);
 int nnhip_rmsnorm_bwd_colsum(const float* G, const float* gamma, const float* Nrm, float* out, size_t F, size_t N,
                              void* stream);
 int nnhip_rmsnorm_bwd_dx(const float* G, const float* gamma, const float* m, const float* Nrm, const float* rinv,

@@ -458,6 +458,27 @@ struct HipEngine::PendingLayout
     bool uses(const float* p) const { return has_buf(S, p) || has_buf(out, p); }
 };
 
+// RMSNorm::forward (compute_layer.hpp RMSNorm) as the layer issues it:
+//   s       = eval_expr_reduce(sum of squares, x)       stage 1
+//   scaled  = s * inv_f                                 stage 2
+//   var_eps = scaled + eps                              stage 3
+//   rinv    = rsqrt(var_eps)                            stage 4
+//   normed  = eval_expr(normalize, x, rinv)             stage 5
+//   out     = eval_expr(scale, normed, gamma)           one nnhip_rmsnorm_forward pass
+// Each call returns its tensor unlaunched; any other use of one of them (or a
+// write to x) runs the calls so far with their separate kernels.
+struct HipEngine::PendingRms
+{
+    Tensor x, s, scaled, var_eps, rinv, normed;
+    float inv_f = 0.0f, eps = 0.0f;
+    int stage = 1;
+    bool yields(const float* p) const
+    {
+        return has_buf(s, p) || has_buf(scaled, p) || has_buf(var_eps, p) || has_buf(rinv, p) || has_buf(normed, p);
+    }
+    bool uses(const float* p) const { return has_buf(x, p) || yields(p); }
+};
+
 // The two-pass chain's softmax_apply output O (per batch (M, D), query-major)
 // with what it came from; V was read from Vs (per batch (D, N)). The backward
 // takes R_i = alpha2 dO_i . O_i from it instead of a second score pass.
@@ -686,6 +707,7 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
                 break;
             }
         if (pmadd_ && has_buf(pmadd_->out, p)) NN_CHECK(settle_madd_());
+        if (prms_ && prms_->yields(p)) NN_CHECK(settle_rms_());
         for (std::size_t i = 0; i < playout_.size(); ++i)
             if (has_buf(playout_[i].out, p))
             {
@@ -771,6 +793,7 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb)
             break;
         }
     if (pmadd_ && pmadd_->uses(p)) NN_CHECK(settle_madd_());
+    if (prms_ && prms_->uses(p)) NN_CHECK(settle_rms_());
     for (std::size_t i = playout_.size(); i-- > 0;)
         if (playout_[i].uses(p))
         {
@@ -807,6 +830,7 @@ Result<void> HipEngine::settle()
     NN_CHECK(settle_mm_());
     NN_CHECK(settle_swb_());
     NN_CHECK(settle_madd_());
+    NN_CHECK(settle_rms_());
     NN_CHECK(settle_layout_());
     NN_CHECK(settle_dv_());
     NN_CHECK(settle_ds_());
@@ -2153,6 +2177,13 @@ Result<Tensor> HipEngine::elementwise_unary(UnaryOp op, const Tensor& A)
 {
     NN_CHECK(check_gpu_({&A}, "elementwise_unary"));
     if (static_cast<unsigned>(op) > static_cast<unsigned>(UnaryOp::Tanh)) return fail("elementwise_unary: bad op");
+    if (op == UnaryOp::Rsqrt && prms_ && prms_->stage == 3 && same_t(A, prms_->var_eps))
+    {
+        NN_TRY(o, alloc_(A.rows(), A.cols()));
+        prms_->rinv = o;
+        prms_->stage = 4;
+        return o;
+    }
     NN_CHECK(settle_chain_reads_({&A}));
     NN_TRY(o, alloc_(A.rows(), A.cols()));
     if (A.size()) NN_CHECK(ew_push_(kUnary, static_cast<unsigned>(op), false, o, A, nullptr, 0.0f));
@@ -2187,6 +2218,23 @@ Result<Tensor> HipEngine::elementwise_binary_scalar(BinaryOp op, const Tensor& A
     NN_CHECK(check_gpu_({&A}, "elementwise_binary_scalar"));
     if (static_cast<unsigned>(op) > static_cast<unsigned>(BinaryOp::Min))
         return fail("elementwise_binary_scalar: bad op");
+    if (prms_ && !first && ((op == BinaryOp::Mul && prms_->stage == 1 && same_t(A, prms_->s)) ||
+                            (op == BinaryOp::Add && prms_->stage == 2 && same_t(A, prms_->scaled))))
+    {
+        NN_TRY(o, alloc_(A.rows(), A.cols()));
+        if (prms_->stage == 1)
+        {
+            prms_->scaled = o;
+            prms_->inv_f = s;
+        }
+        else
+        {
+            prms_->var_eps = o;
+            prms_->eps = s;
+        }
+        ++prms_->stage;
+        return o;
+    }
     NN_CHECK(settle_chain_reads_({&A}));
     NN_TRY(o, alloc_(A.rows(), A.cols()));
     if (A.size()) NN_CHECK(ew_push_(kScalar, static_cast<unsigned>(op), first, o, A, nullptr, s));
@@ -2225,6 +2273,10 @@ Result<Tensor> HipEngine::eval_impl_(const ExprSpec& spec, std::span<const Tenso
     {
         NN_TRY(chained, attn_softmax_(spec, inputs, rows, cols));
         if (chained) return std::move(*chained);
+    }
+    {
+        NN_TRY(rms, rms_program_(spec, inputs, rows, cols, vector_out));
+        if (rms) return std::move(*rms);
     }
     for (const Tensor& t : inputs)
     {
@@ -2296,6 +2348,83 @@ Result<Tensor> HipEngine::eval_impl_(const ExprSpec& spec, std::span<const Tenso
                     "the reduced axis");
     NN_CHECK(kernel_(rc, "eval_expr"));
     return o;
+}
+
+// RMSNorm::forward's programs: the sum of squares starts a PendingRms, the
+// normalize continues it and the scale runs the whole forward in one pass.
+Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std::span<const Tensor> inputs,
+                                                      std::size_t rows, std::size_t cols, bool vector_out)
+{
+    using R = std::optional<Tensor>;
+    const float* a[5] = {};
+    if (vector_out)
+    {
+        if (inputs.size() < 1 || !bind(canon(LayerProg::RmsSumSq), spec, inputs, a)) return R();
+        const Tensor& x = inputs[0];
+        if (!x.is_gpu() || a[0] != x.dev_ptr() || x.rows() != rows || x.cols() != cols || rows == 0 ||
+            rows > 1024 || cols == 0 || cols % 4 != 0 || !aligned16(a[0]))
+            return R();
+        NN_CHECK(settle_rms_());
+        NN_CHECK(settle_reads_({&x}));
+        NN_TRY(o, alloc_(1, cols));
+        prms_ = std::make_unique<PendingRms>();
+        prms_->x = x;
+        prms_->s = o;
+        return R(o);
+    }
+    if (!prms_ || inputs.size() < 2) return R();
+    PendingRms& r = *prms_;
+    if (r.x.rows() != rows || r.x.cols() != cols) return R();
+    if (r.stage == 4 && bind(canon(LayerProg::RmsNormalize), spec, inputs, a) && a[0] == r.x.dev_ptr() &&
+        a[1] == r.rinv.dev_ptr())
+    {
+        NN_TRY(o, alloc_(rows, cols));
+        r.normed = o;
+        r.stage = 5;
+        return R(o);
+    }
+    if (r.stage == 5 && bind(canon(LayerProg::RmsScale), spec, inputs, a) && a[0] == r.normed.dev_ptr() &&
+        aligned16(a[1]))
+    {
+        const Tensor* gamma = nullptr;
+        for (const Tensor& t : inputs)
+            if (t.dev_ptr() == a[1]) gamma = &t;
+        if (!gamma || gamma->rows() != rows || gamma->cols() != 1 || prms_->uses(a[1])) return R();
+        NN_CHECK(settle_reads_({gamma}));
+        if (!prms_ || prms_->stage != 5) return R();
+        std::unique_ptr<PendingRms> q = std::move(prms_);
+        NN_TRY(o, alloc_(rows, cols));
+        NN_CHECK(kernel_(nnhip_rmsnorm_forward(D(q->x), D(*gamma), q->inv_f, q->eps, W(q->s), W(q->scaled),
+                                               W(q->var_eps), W(q->rinv), W(q->normed), W(o), rows, cols, stream_),
+                         "rmsnorm forward"));
+        return R(o);
+    }
+    return R();
+}
+
+// The recorded RMSNorm calls so far, with their separate kernels.
+Result<void> HipEngine::settle_rms_()
+{
+    if (!prms_) return {};
+    std::unique_ptr<PendingRms> r = std::move(prms_);
+    const std::size_t F = r->x.rows(), N = r->x.cols();
+    NN_CHECK(kernel_(nnhip_rmsnorm_sumsq(D(r->x), W(r->s), F, N, stream_), "eval_expr_reduce(rmsnorm sum of squares)"));
+    if (r->stage >= 2)
+        NN_CHECK(kernel_(nnhip_elementwise_binary_scalar(D(r->s), W(r->scaled), N, static_cast<unsigned>(BinaryOp::Mul),
+                                                         r->inv_f, 0, stream_),
+                         "elementwise_binary_scalar"));
+    if (r->stage >= 3)
+        NN_CHECK(kernel_(nnhip_elementwise_binary_scalar(D(r->scaled), W(r->var_eps), N,
+                                                         static_cast<unsigned>(BinaryOp::Add), r->eps, 0, stream_),
+                         "elementwise_binary_scalar"));
+    if (r->stage >= 4)
+        NN_CHECK(kernel_(nnhip_elementwise_unary(D(r->var_eps), W(r->rinv), N, static_cast<unsigned>(UnaryOp::Rsqrt),
+                                                 stream_),
+                         "elementwise_unary"));
+    if (r->stage >= 5)
+        NN_CHECK(kernel_(nnhip_colbcast_mul(D(r->x), D(r->rinv), W(r->normed), F, N, stream_),
+                         "eval_expr(rmsnorm normalize)"));
+    return {};
 }
 
 // Softmax rows of a recorded scores + mask (the attention probabilities), and

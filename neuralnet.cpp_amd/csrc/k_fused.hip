@@ -235,6 +235,107 @@ __global__ __launch_bounds__(kColT) void k_fused_colsum(F f, float* out, unsigne
     }
 }
 
+// ── RMSNorm forward in one pass (compute_layer.hpp RMSNorm::forward) ──────────
+// The layer's six calls over x (F, N): s = column sums of x^2 (the SumSq
+// program), scaled = s * inv_f, var_eps = scaled + eps, rinv = 1 / sqrt(var_eps),
+// normed = x * rinv (per column), out = normed * gamma (per row). The sums take
+// k_fused_colsum's geometry and order (thread rows rg, rg + 128, ... added in
+// turn, the same lane and wave merges; x^2 + acc as one fma, as the compiler
+// contracts it there) and every other value the same expression as its
+// separate kernel, so the results equal the six calls' bit for bit. A thread
+// keeps its KM rows of x in registers between the sums and the products:
+// x is read once. s, scaled and var_eps are written when their pointer is set.
+template <unsigned KM>
+__global__ __launch_bounds__(kColT) void k_rms_fwd(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                   float inv_f, float eps, float* s_raw, float* scaled,
+                                                   float* var_eps, float* __restrict__ rinv,
+                                                   float* __restrict__ normed, float* __restrict__ out,
+                                                   unsigned rows, unsigned cols4, size_t cols)
+{
+    __shared__ float4 part[kColWaves][kColQuads];
+    __shared__ float4 rq[kColQuads];
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const unsigned qi = lane % kColQuads, rg = threadIdx.x / kColQuads;
+    const unsigned q = blockIdx.x * kColQuads + qi;
+    float4 xv[KM];
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < cols4)
+    {
+#pragma unroll
+        for (unsigned k = 0; k < KM; ++k)
+        {
+            const unsigned r = rg + k * kRowGroups;
+            if (r < rows) xv[k] = ld4(x + size_t(r) * cols + 4u * q);
+        }
+#pragma unroll
+        for (unsigned k = 0; k < KM; ++k)
+            if (rg + k * kRowGroups < rows)
+            {
+                acc.x = __builtin_fmaf(xv[k].x, xv[k].x, acc.x);
+                acc.y = __builtin_fmaf(xv[k].y, xv[k].y, acc.y);
+                acc.z = __builtin_fmaf(xv[k].z, xv[k].z, acc.z);
+                acc.w = __builtin_fmaf(xv[k].w, xv[k].w, acc.w);
+            }
+    }
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1)
+    {
+        acc.x += __shfl_xor(acc.x, o, 64);
+        acc.y += __shfl_xor(acc.y, o, 64);
+        acc.z += __shfl_xor(acc.z, o, 64);
+        acc.w += __shfl_xor(acc.w, o, 64);
+    }
+    if (lane < kColQuads) part[wave][lane] = acc;
+    __syncthreads();
+    if (threadIdx.x < kColQuads)
+    {
+        const unsigned qo = blockIdx.x * kColQuads + threadIdx.x;
+        float4 s = part[0][threadIdx.x];
+        for (unsigned k = 1; k < kColWaves; ++k)
+        {
+            const float4 v = part[k][threadIdx.x];
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+        {
+#pragma clang fp contract(off)
+            const float4 sc = make_float4(s.x * inv_f, s.y * inv_f, s.z * inv_f, s.w * inv_f);
+            const float4 ve = make_float4(sc.x + eps, sc.y + eps, sc.z + eps, sc.w + eps);
+            const float4 ri =
+                make_float4(1.0f / sqrtf(ve.x), 1.0f / sqrtf(ve.y), 1.0f / sqrtf(ve.z), 1.0f / sqrtf(ve.w));
+            if (qo < cols4)
+            {
+                if (s_raw) st4(s_raw + 4u * qo, s);
+                if (scaled) st4(scaled + 4u * qo, sc);
+                if (var_eps) st4(var_eps + 4u * qo, ve);
+                st4(rinv + 4u * qo, ri);
+            }
+            rq[threadIdx.x] = ri;
+        }
+    }
+    __syncthreads();
+    if (q < cols4)
+    {
+        const float4 ri = rq[qi];
+#pragma unroll
+        for (unsigned k = 0; k < KM; ++k)
+        {
+            const unsigned r = rg + k * kRowGroups;
+            if (r < rows)
+            {
+#pragma clang fp contract(off)
+                const size_t i = size_t(r) * cols + 4u * q;
+                const float4 n = make_float4(xv[k].x * ri.x, xv[k].y * ri.y, xv[k].z * ri.z, xv[k].w * ri.w);
+                st4(normed + i, n);
+                const float g = gamma[r];
+                st4(out + i, make_float4(n.x * g, n.y * g, n.z * g, n.w * g));
+            }
+        }
+    }
+}
+
 // ── row sums: out[r] = sum_c g[r,c] * gamma[r] * normed[r,c], one workgroup per row ──
 __global__ __launch_bounds__(kT) void k_fused_rowsum_ggn(const float* g, const float* gamma, const float* n,
                                                          float* out, unsigned cols4, size_t cols)
@@ -312,6 +413,28 @@ extern "C" int nnhip_rmsnorm_sumsq(const float* X, float* out, size_t F, size_t 
 {
     if (!shape_ok(F, N, {X, out})) return kBadShape;
     return launch_colsum(SumSq{X, N}, out, F, N, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_rmsnorm_forward(const float* X, const float* gamma, float inv_f, float eps, float* s_raw,
+                                     float* scaled, float* var_eps, float* rinv, float* normed, float* out, size_t F,
+                                     size_t N, void* stream)
+{
+    if (!X || !gamma || !rinv || !normed || !out || F == 0 || F > 8 * kRowGroups) return kBadShape;
+    if (!shape_ok(F, N, {X, rinv, normed, out, s_raw, scaled, var_eps})) return kBadShape;
+    if (N == 0) return 0;
+    const unsigned cols4 = unsigned(N / 4);
+    const dim3 grid((cols4 + kColQuads - 1) / kColQuads), block(kColT);
+    const auto s = static_cast<hipStream_t>(stream);
+    if (F <= 2 * kRowGroups)
+        hipLaunchKernelGGL(k_rms_fwd<2>, grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
+                           normed, out, unsigned(F), cols4, N);
+    else if (F <= 6 * kRowGroups)
+        hipLaunchKernelGGL(k_rms_fwd<6>, grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
+                           normed, out, unsigned(F), cols4, N);
+    else
+        hipLaunchKernelGGL(k_rms_fwd<8>, grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
+                           normed, out, unsigned(F), cols4, N);
+    return launch_status();
 }
 
 extern "C" int nnhip_colbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream)

@@ -231,6 +231,12 @@ private:
     Result<void> materialise_layout_(const PendingLayout& r);
     Result<void> settle_layout_();
     const PendingLayout* layout_of_(const Tensor& t) const;
+    // RMSNorm::forward's calls from the sum of squares on, not launched yet.
+    struct PendingRms;
+    std::unique_ptr<PendingRms> prms_;
+    Result<void> settle_rms_();
+    Result<std::optional<Tensor>> rms_program_(const ExprSpec& spec, std::span<const Tensor> inputs,
+                                               std::size_t rows, std::size_t cols, bool vector_out);
     // Outputs of the two-pass chain's forward kept for the backward, one per layer.
     struct TwoPassOut;
     std::vector<TwoPassOut> ptwo_;

@@ -1,0 +1,91 @@
+"""RMSNorm::forward through the engine as the layer issues it (compute_layer.hpp RMSNorm):
+s = sum of squares of x's columns, s * 1/F, + eps, rsqrt, normalize, scale by gamma.
+
+The HIP engine records these calls and, when the scale arrives, runs all six as
+one pass (nnhip_rmsnorm_forward, x read once); any other use of an intermediate,
+or a write to x, runs the calls so far with their separate kernels. Bars: every
+output of the one-pass run bit-identical to the separate kernels' (the chain cut
+right after its first call), every cut variant equal to it too, and all of them
+within 1e-5 (normwise) of the oracle running the same calls.
+"""
+import numpy as np
+import pytest
+
+import layer_programs as lp
+from helpers import normal, nrm_err, uniform
+
+pytestmark = pytest.mark.gpu
+
+SQ, _ = lp.rms_sum_sq()
+NORM, _ = lp.rms_normalize()
+SCALE, _ = lp.rms_scale()
+NAMES = ("s", "scaled", "var_eps", "rinv", "normed", "out")
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def chain(e, X, G, eps, cut=None):
+    """The layer's calls; `cut` names the interruption: "s" reads s after the first call,
+    "rinv" reads rinv before the normalize, "write_x" scales x in place before the scale call."""
+    F, N = X.shape
+    x, g = e.tensor(X), e.tensor(G)
+    s = e.eval_expr_reduce(SQ, [x, x], F, N)
+    if cut == "s":
+        s.numpy()
+    sc = e.elementwise_binary_scalar("Mul", s, 1.0 / F)
+    ve = e.elementwise_binary_scalar("Add", sc, eps)
+    ri = e.elementwise_unary("Rsqrt", ve)
+    if cut == "rinv":
+        ri.numpy()
+    nm = e.eval_expr(NORM, [x, ri], F, N)
+    if cut == "write_x":
+        e.scale_inplace(x, 2.0)
+    out = e.eval_expr(SCALE, [nm, g], F, N)
+    res = dict(zip(NAMES, (t.numpy() for t in (s, sc, ve, ri, nm, out))))
+    res["x"] = x.numpy()
+    return res
+
+
+@pytest.mark.parametrize("F,N", [(768, 8192), (128, 36), (1024, 64), (1100, 40), (24, 10), (5, 4), (300, 100)])
+def test_rmsnorm_forward_chain(hip, cpu, F, N):
+    rng = np.random.default_rng(F * 131 + N)
+    X, G = normal(rng, (F, N)), uniform(rng, (F, 1), 0.5, 1.5)
+    eps = 1e-5
+    fused = chain(hip, X, G, eps)
+    ref = chain(cpu, X, G, eps)
+    for cut in ("s", "rinv", "write_x"):
+        other = chain(hip, X, G, eps, cut)
+        print(f"[rmsnorm] F{F} N{N} cut={cut}", flush=True)
+        for n in NAMES:
+            assert np.array_equal(bits(fused[n]), bits(other[n])), (cut, n)
+        assert np.array_equal(bits(other["x"]), bits(X * (2.0 if cut == "write_x" else 1.0))), cut
+    for n in NAMES:
+        assert fused[n].shape == ref[n].shape, n
+        assert nrm_err(fused[n], ref[n]) <= 1e-5, n
+    # closed form in float64
+    x64 = X.astype(np.float64)
+    r = 1.0 / np.sqrt((x64 * x64).sum(0, keepdims=True) / F + eps)
+    assert nrm_err(fused["out"], x64 * r * G.astype(np.float64)) <= 1e-5
+
+
+def test_rmsnorm_chain_two_layers_interleaved(hip, cpu):
+    """A second chain starting before the first is complete runs the first one's calls separately."""
+    rng = np.random.default_rng(11)
+    F, N = 256, 512
+    X1, X2 = normal(rng, (F, N)), normal(rng, (F, N))
+    G = uniform(rng, (F, 1), 0.5, 1.5)
+
+    def go(e):
+        x1, x2, g = e.tensor(X1), e.tensor(X2), e.tensor(G)
+        s1 = e.eval_expr_reduce(SQ, [x1, x1], F, N)
+        s2 = e.eval_expr_reduce(SQ, [x2, x2], F, N)
+        r1 = e.elementwise_unary("Rsqrt", e.elementwise_binary_scalar("Add", e.elementwise_binary_scalar("Mul", s1, 1.0 / F), 1e-5))
+        r2 = e.elementwise_unary("Rsqrt", e.elementwise_binary_scalar("Add", e.elementwise_binary_scalar("Mul", s2, 1.0 / F), 1e-5))
+        o1 = e.eval_expr(SCALE, [e.eval_expr(NORM, [x1, r1], F, N), g], F, N)
+        o2 = e.eval_expr(SCALE, [e.eval_expr(NORM, [x2, r2], F, N), g], F, N)
+        return [t.numpy() for t in (s1, s2, r1, r2, o1, o2)]
+
+    for a, b in zip(go(hip), go(cpu)):
+        assert nrm_err(a, b) <= 1e-5
