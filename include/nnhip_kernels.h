@@ -318,6 +318,11 @@ int nnhip_rowbcast_mul(const float* X, const float* v, float* out, size_t F, siz
  * NULL (not written). 1 <= F <= 1024. */
 int nnhip_rmsnorm_forward(const float* X, const float* gamma, float inv_f, float eps, float* s_raw, float* scaled,
                           float* var_eps, float* rinv, float* normed, float* out, size_t F, size_t N, void* stream);
+/* RMSNorm::backward's column sum, its scaling and dx in one pass (compute_layer.hpp:772-791; no CUDA
+ * counterpart): m_raw = bwd_colsum(G, gamma, Nrm), m = m_raw * inv_f, dx = bwd_dx(G, gamma, m, Nrm, rinv),
+ * equal bit for bit to the separate calls; m_raw may be NULL. 1 <= F <= 1024. */
+int nnhip_rmsnorm_backward(const float* G, const float* gamma, const float* Nrm, const float* rinv, float inv_f,
+                           float* m_raw, float* m, float* dx, size_t F, size_t N, void* stream);
 int nnhip_rmsnorm_bwd_colsum(const float* G, const float* gamma, const float* Nrm, float* out, size_t F, size_t N,
                              void* stream);
 int nnhip_rmsnorm_bwd_dx(const float* G, const float* gamma, const float* m, const float* Nrm, const float* rinv,

@@ -465,18 +465,28 @@ struct HipEngine::PendingLayout
 //   rinv    = rsqrt(var_eps)                            stage 4
 //   normed  = eval_expr(normalize, x, rinv)             stage 5
 //   out     = eval_expr(scale, normed, gamma)           one nnhip_rmsnorm_forward pass
+// and RMSNorm::backward's first three calls (bwd):
+//   m_raw   = eval_expr_reduce(g gamma normed, column sums)   stage 1 (x = g, s = m_raw)
+//   m       = m_raw * inv_f                                    stage 2 (scaled = m)
+//   dx      = eval_expr(dx program, g, gamma, m, normed, rinv) one nnhip_rmsnorm_backward pass
 // Each call returns its tensor unlaunched; any other use of one of them (or a
-// write to x) runs the calls so far with their separate kernels.
+// write to an input) runs the calls so far with their separate kernels.
 struct HipEngine::PendingRms
 {
+    bool bwd = false;
     Tensor x, s, scaled, var_eps, rinv, normed;
+    Tensor gamma;   // bwd: with x = g and normed, an input
     float inv_f = 0.0f, eps = 0.0f;
     int stage = 1;
     bool yields(const float* p) const
     {
+        if (bwd) return has_buf(s, p) || has_buf(scaled, p);
         return has_buf(s, p) || has_buf(scaled, p) || has_buf(var_eps, p) || has_buf(rinv, p) || has_buf(normed, p);
     }
-    bool uses(const float* p) const { return has_buf(x, p) || yields(p); }
+    bool uses(const float* p) const
+    {
+        return has_buf(x, p) || yields(p) || (bwd && (has_buf(gamma, p) || has_buf(normed, p)));
+    }
 };
 
 // The two-pass chain's softmax_apply output O (per batch (M, D), query-major)
@@ -2177,7 +2187,7 @@ Result<Tensor> HipEngine::elementwise_unary(UnaryOp op, const Tensor& A)
 {
     NN_CHECK(check_gpu_({&A}, "elementwise_unary"));
     if (static_cast<unsigned>(op) > static_cast<unsigned>(UnaryOp::Tanh)) return fail("elementwise_unary: bad op");
-    if (op == UnaryOp::Rsqrt && prms_ && prms_->stage == 3 && same_t(A, prms_->var_eps))
+    if (op == UnaryOp::Rsqrt && prms_ && !prms_->bwd && prms_->stage == 3 && same_t(A, prms_->var_eps))
     {
         NN_TRY(o, alloc_(A.rows(), A.cols()));
         prms_->rinv = o;
@@ -2218,8 +2228,9 @@ Result<Tensor> HipEngine::elementwise_binary_scalar(BinaryOp op, const Tensor& A
     NN_CHECK(check_gpu_({&A}, "elementwise_binary_scalar"));
     if (static_cast<unsigned>(op) > static_cast<unsigned>(BinaryOp::Min))
         return fail("elementwise_binary_scalar: bad op");
-    if (prms_ && !first && ((op == BinaryOp::Mul && prms_->stage == 1 && same_t(A, prms_->s)) ||
-                            (op == BinaryOp::Add && prms_->stage == 2 && same_t(A, prms_->scaled))))
+    if (prms_ && !first &&
+        ((op == BinaryOp::Mul && prms_->stage == 1 && same_t(A, prms_->s)) ||
+         (op == BinaryOp::Add && !prms_->bwd && prms_->stage == 2 && same_t(A, prms_->scaled))))
     {
         NN_TRY(o, alloc_(A.rows(), A.cols()));
         if (prms_->stage == 1)
@@ -2357,6 +2368,47 @@ Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std:
 {
     using R = std::optional<Tensor>;
     const float* a[5] = {};
+    auto input = [&](const float* p) -> const Tensor* {
+        for (const Tensor& t : inputs)
+            if (t.dev_ptr() == p) return &t;
+        return nullptr;
+    };
+    if (vector_out && inputs.size() >= 3 && bind(canon(LayerProg::RmsBwdColSum), spec, inputs, a))
+    {
+        const Tensor *g = input(a[0]), *gamma = input(a[1]), *nrm = input(a[2]);
+        if (!g || !gamma || !nrm || !g->is_gpu() || g->rows() != rows || g->cols() != cols ||
+            nrm->rows() != rows || nrm->cols() != cols || gamma->rows() != rows || gamma->cols() != 1 ||
+            rows == 0 || rows > 1024 || cols == 0 || cols % 4 != 0 || !aligned16(a[0]) || !aligned16(a[2]))
+            return R();
+        NN_CHECK(settle_rms_());
+        NN_CHECK(settle_reads_({g, gamma, nrm}));
+        NN_TRY(o, alloc_(1, cols));
+        prms_ = std::make_unique<PendingRms>();
+        prms_->bwd = true;
+        prms_->x = *g;
+        prms_->gamma = *gamma;
+        prms_->normed = *nrm;
+        prms_->s = o;
+        return R(o);
+    }
+    if (!vector_out && prms_ && prms_->bwd && prms_->stage == 2 && inputs.size() >= 5 &&
+        bind(canon(LayerProg::RmsBwdDx), spec, inputs, a))
+    {
+        PendingRms& r = *prms_;
+        const Tensor* rinv = input(a[4]);
+        if (a[0] != r.x.dev_ptr() || a[1] != r.gamma.dev_ptr() || a[2] != r.scaled.dev_ptr() ||
+            a[3] != r.normed.dev_ptr() || !rinv || rinv->rows() != 1 || rinv->cols() != cols ||
+            r.x.rows() != rows || r.x.cols() != cols || !aligned16(a[4]) || r.uses(a[4]))
+            return R();
+        NN_CHECK(settle_reads_({rinv}));
+        if (!prms_ || !prms_->bwd || prms_->stage != 2) return R();
+        std::unique_ptr<PendingRms> q = std::move(prms_);
+        NN_TRY(o, alloc_(rows, cols));
+        NN_CHECK(kernel_(nnhip_rmsnorm_backward(D(q->x), D(q->gamma), D(q->normed), D(*rinv), q->inv_f, W(q->s),
+                                                W(q->scaled), W(o), rows, cols, stream_),
+                         "rmsnorm backward"));
+        return R(o);
+    }
     if (vector_out)
     {
         if (inputs.size() < 1 || !bind(canon(LayerProg::RmsSumSq), spec, inputs, a)) return R();
@@ -2372,7 +2424,7 @@ Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std:
         prms_->s = o;
         return R(o);
     }
-    if (!prms_ || inputs.size() < 2) return R();
+    if (!prms_ || prms_->bwd || inputs.size() < 2) return R();
     PendingRms& r = *prms_;
     if (r.x.rows() != rows || r.x.cols() != cols) return R();
     if (r.stage == 4 && bind(canon(LayerProg::RmsNormalize), spec, inputs, a) && a[0] == r.x.dev_ptr() &&
@@ -2408,6 +2460,16 @@ Result<void> HipEngine::settle_rms_()
     if (!prms_) return {};
     std::unique_ptr<PendingRms> r = std::move(prms_);
     const std::size_t F = r->x.rows(), N = r->x.cols();
+    if (r->bwd)
+    {
+        NN_CHECK(kernel_(nnhip_rmsnorm_bwd_colsum(D(r->x), D(r->gamma), D(r->normed), W(r->s), F, N, stream_),
+                         "eval_expr_reduce(rmsnorm backward column sum)"));
+        if (r->stage >= 2)
+            NN_CHECK(kernel_(nnhip_elementwise_binary_scalar(D(r->s), W(r->scaled), N,
+                                                             static_cast<unsigned>(BinaryOp::Mul), r->inv_f, 0, stream_),
+                             "elementwise_binary_scalar"));
+        return {};
+    }
     NN_CHECK(kernel_(nnhip_rmsnorm_sumsq(D(r->x), W(r->s), F, N, stream_), "eval_expr_reduce(rmsnorm sum of squares)"));
     if (r->stage >= 2)
         NN_CHECK(kernel_(nnhip_elementwise_binary_scalar(D(r->s), W(r->scaled), N, static_cast<unsigned>(BinaryOp::Mul),

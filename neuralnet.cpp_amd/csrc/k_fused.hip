@@ -336,6 +336,104 @@ __global__ __launch_bounds__(kColT) void k_rms_fwd(const float* __restrict__ x, 
     }
 }
 
+// ── RMSNorm backward's column sum, scale and dx in one pass ───────────────────
+// The layer's calls (compute_layer.hpp RMSNorm::backward): m_raw = column sums
+// of g * gamma[r] * normed (the GGammaN program), m = m_raw * inv_f, dx =
+// (g * gamma[r] - m * normed) * rinv, each with its separate kernel's
+// expression and k_fused_colsum's summation order, so equal bit for bit; g and
+// normed are read once.
+template <unsigned KM>
+__global__ __launch_bounds__(kColT) void k_rms_bwd(const float* __restrict__ g, const float* __restrict__ gamma,
+                                                   const float* __restrict__ nrm, const float* __restrict__ rinv,
+                                                   float inv_f, float* m_raw, float* __restrict__ m,
+                                                   float* __restrict__ dx, unsigned rows, unsigned cols4, size_t cols)
+{
+    __shared__ float4 part[kColWaves][kColQuads];
+    __shared__ float4 mq[kColQuads];
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const unsigned qi = lane % kColQuads, rg = threadIdx.x / kColQuads;
+    const unsigned q = blockIdx.x * kColQuads + qi;
+    float4 gv[KM], nv[KM];
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < cols4)
+    {
+#pragma unroll
+        for (unsigned k = 0; k < KM; ++k)
+        {
+            const unsigned r = rg + k * kRowGroups;
+            if (r < rows)
+            {
+                const size_t i = size_t(r) * cols + 4u * q;
+                gv[k] = ld4(g + i);
+                nv[k] = ld4(nrm + i);
+            }
+        }
+#pragma unroll
+        for (unsigned k = 0; k < KM; ++k)
+        {
+            const unsigned r = rg + k * kRowGroups;
+            if (r < rows)
+            {
+                const float gr = gamma[r];
+                const float4 a = gv[k], c = nv[k];
+                const float4 v = make_float4((a.x * gr) * c.x, (a.y * gr) * c.y, (a.z * gr) * c.z, (a.w * gr) * c.w);
+                acc.x += v.x;
+                acc.y += v.y;
+                acc.z += v.z;
+                acc.w += v.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1)
+    {
+        acc.x += __shfl_xor(acc.x, o, 64);
+        acc.y += __shfl_xor(acc.y, o, 64);
+        acc.z += __shfl_xor(acc.z, o, 64);
+        acc.w += __shfl_xor(acc.w, o, 64);
+    }
+    if (lane < kColQuads) part[wave][lane] = acc;
+    __syncthreads();
+    if (threadIdx.x < kColQuads)
+    {
+        const unsigned qo = blockIdx.x * kColQuads + threadIdx.x;
+        float4 s = part[0][threadIdx.x];
+        for (unsigned k = 1; k < kColWaves; ++k)
+        {
+            const float4 v = part[k][threadIdx.x];
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+        const float4 mm = make_float4(s.x * inv_f, s.y * inv_f, s.z * inv_f, s.w * inv_f);
+        if (qo < cols4)
+        {
+            if (m_raw) st4(m_raw + 4u * qo, s);
+            st4(m + 4u * qo, mm);
+        }
+        mq[threadIdx.x] = mm;
+    }
+    __syncthreads();
+    if (q < cols4)
+    {
+        const float4 b = mq[qi], d = ld4(rinv + 4u * q);
+#pragma unroll
+        for (unsigned k = 0; k < KM; ++k)
+        {
+            const unsigned r = rg + k * kRowGroups;
+            if (r < rows)
+            {
+                const float gr = gamma[r];
+                const float4 a = gv[k], c = nv[k];
+                st4(dx + size_t(r) * cols + 4u * q,
+                    make_float4(RmsDx::one(a.x, gr, b.x, c.x, d.x), RmsDx::one(a.y, gr, b.y, c.y, d.y),
+                                RmsDx::one(a.z, gr, b.z, c.z, d.z), RmsDx::one(a.w, gr, b.w, c.w, d.w)));
+            }
+        }
+    }
+}
+
 // ── row sums: out[r] = sum_c g[r,c] * gamma[r] * normed[r,c], one workgroup per row ──
 __global__ __launch_bounds__(kT) void k_fused_rowsum_ggn(const float* g, const float* gamma, const float* n,
                                                          float* out, unsigned cols4, size_t cols)
@@ -434,6 +532,28 @@ extern "C" int nnhip_rmsnorm_forward(const float* X, const float* gamma, float i
     else
         hipLaunchKernelGGL(k_rms_fwd<8>, grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
                            normed, out, unsigned(F), cols4, N);
+    return launch_status();
+}
+
+extern "C" int nnhip_rmsnorm_backward(const float* G, const float* gamma, const float* Nrm, const float* rinv,
+                                      float inv_f, float* m_raw, float* m, float* dx, size_t F, size_t N,
+                                      void* stream)
+{
+    if (!G || !gamma || !Nrm || !rinv || !m || !dx || F == 0 || F > 8 * kRowGroups) return kBadShape;
+    if (!shape_ok(F, N, {G, Nrm, rinv, m, dx, m_raw})) return kBadShape;
+    if (N == 0) return 0;
+    const unsigned cols4 = unsigned(N / 4);
+    const dim3 grid((cols4 + kColQuads - 1) / kColQuads), block(kColT);
+    const auto s = static_cast<hipStream_t>(stream);
+    if (F <= 2 * kRowGroups)
+        hipLaunchKernelGGL(k_rms_bwd<2>, grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx, unsigned(F),
+                           cols4, N);
+    else if (F <= 6 * kRowGroups)
+        hipLaunchKernelGGL(k_rms_bwd<6>, grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx, unsigned(F),
+                           cols4, N);
+    else
+        hipLaunchKernelGGL(k_rms_bwd<8>, grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx, unsigned(F),
+                           cols4, N);
     return launch_status();
 }
 

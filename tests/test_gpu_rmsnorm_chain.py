@@ -1,12 +1,15 @@
-"""RMSNorm::forward through the engine as the layer issues it (compute_layer.hpp RMSNorm):
-s = sum of squares of x's columns, s * 1/F, + eps, rsqrt, normalize, scale by gamma.
+"""RMSNorm through the engine as the layer issues it (compute_layer.hpp RMSNorm):
+forward s = sum of squares of x's columns, s * 1/F, + eps, rsqrt, normalize,
+scale by gamma; backward m_raw = column sums of g * gamma * normed, m = m_raw / F,
+dx = (g * gamma - m * normed) * rinv.
 
-The HIP engine records these calls and, when the scale arrives, runs all six as
-one pass (nnhip_rmsnorm_forward, x read once); any other use of an intermediate,
-or a write to x, runs the calls so far with their separate kernels. Bars: every
-output of the one-pass run bit-identical to the separate kernels' (the chain cut
-right after its first call), every cut variant equal to it too, and all of them
-within 1e-5 (normwise) of the oracle running the same calls.
+The HIP engine records these calls and, when the chain's last one arrives, runs
+them as one pass (nnhip_rmsnorm_forward / nnhip_rmsnorm_backward, the big inputs
+read once); any other use of an intermediate, or a write to an input, runs the
+calls so far with their separate kernels. Bars: every output of the one-pass run
+bit-identical to the separate kernels' (the chain cut right after its first
+call), every cut variant equal to it too, and all of them within 1e-5
+(normwise) of the oracle running the same calls.
 """
 import numpy as np
 import pytest
@@ -20,6 +23,10 @@ SQ, _ = lp.rms_sum_sq()
 NORM, _ = lp.rms_normalize()
 SCALE, _ = lp.rms_scale()
 NAMES = ("s", "scaled", "var_eps", "rinv", "normed", "out")
+BCOL, _ = lp.rms_bwd_colsum()
+BDX, _ = lp.rms_bwd_dx()
+BROW, _ = lp.rms_bwd_rowsum()
+BNAMES = ("m_raw", "m", "dx", "gg")
 
 
 def bits(a):
@@ -89,3 +96,44 @@ def test_rmsnorm_chain_two_layers_interleaved(hip, cpu):
 
     for a, b in zip(go(hip), go(cpu)):
         assert nrm_err(a, b) <= 1e-5
+
+
+def bwd_chain(e, Gr, Ga, Nm, Ri, cut=None):
+    """The backward's calls; `cut`: "m_raw" reads m_raw after the first call, "write_g" scales g
+    in place before the dx call, "write_gamma" scales gamma in place there."""
+    F, N = Gr.shape
+    g, ga, nm, ri = e.tensor(Gr), e.tensor(Ga), e.tensor(Nm), e.tensor(Ri)
+    m_raw = e.eval_expr_reduce(BCOL, [g, ga, nm], F, N)
+    if cut == "m_raw":
+        m_raw.numpy()
+    m = e.elementwise_binary_scalar("Mul", m_raw, 1.0 / F)
+    if cut == "write_g":
+        e.scale_inplace(g, 2.0)
+    if cut == "write_gamma":
+        e.scale_inplace(ga, 2.0)
+    dx = e.eval_expr(BDX, [g, ga, m, nm, ri], F, N)
+    gg = e.eval_expr_reduce(BROW, [g, ga, nm], F, N)
+    return dict(zip(BNAMES, (t.numpy() for t in (m_raw, m, dx, gg))))
+
+
+@pytest.mark.parametrize("F,N", [(768, 8192), (128, 36), (1024, 64), (1100, 40), (24, 10), (300, 100)])
+def test_rmsnorm_backward_chain(hip, cpu, F, N):
+    rng = np.random.default_rng(F * 7 + N)
+    Gr, Nm = normal(rng, (F, N)), normal(rng, (F, N))
+    Ga, Ri = uniform(rng, (F, 1), 0.5, 1.5), uniform(rng, (1, N), 0.5, 2.0)
+    fused = bwd_chain(hip, Gr, Ga, Nm, Ri)
+    ref = bwd_chain(cpu, Gr, Ga, Nm, Ri)
+    cut = bwd_chain(hip, Gr, Ga, Nm, Ri, "m_raw")
+    for n in BNAMES:
+        assert np.array_equal(bits(fused[n]), bits(cut[n])), n
+        assert nrm_err(fused[n], ref[n]) <= 1e-5, n
+    # writes between the column sum and dx: the column sums see the old values, dx the new ones
+    for w in ("write_g", "write_gamma"):
+        print(f"[rmsnorm bwd] F{F} N{N} {w}", flush=True)
+        h, c = bwd_chain(hip, Gr, Ga, Nm, Ri, w), bwd_chain(cpu, Gr, Ga, Nm, Ri, w)
+        for n in BNAMES:
+            assert nrm_err(h[n], c[n]) <= 1e-5, (w, n)
+        assert np.array_equal(bits(h["m_raw"]), bits(fused["m_raw"])), w
+    g64, n64, a64 = Gr.astype(np.float64), Nm.astype(np.float64), Ga.astype(np.float64)
+    m = (g64 * a64 * n64).sum(0, keepdims=True) / F
+    assert nrm_err(fused["dx"], (g64 * a64 - m * n64) * Ri.astype(np.float64)) <= 1e-5
