@@ -114,6 +114,9 @@ int nnhip_fill(float* out, size_t count, float value, void* stream);
 
 /* ── reductions (cuda_kernels.h:98-109); mode 0 = sum, 1 = max (init lowest()) ── */
 int nnhip_reduce_row(const float* A, float* out, size_t rows, size_t cols, unsigned mode, void* stream);
+/* out[r] = out[r] + (row sum of A)[r]: the sums added into out as a following add_inplace(out, sums) would
+ * add them (a Linear bias gradient, compute_layer.hpp Linear::backward; no CUDA counterpart). */
+int nnhip_reduce_row_sum_add(const float* A, float* out, size_t rows, size_t cols, void* stream);
 /* Column reduction over row chunks combined in chunk order; workspace from nnhip_reduce_col_workspace_bytes. */
 size_t nnhip_reduce_col_workspace_bytes(size_t rows, size_t cols);
 int nnhip_reduce_col(const float* A, float* out, size_t rows, size_t cols, unsigned mode, void* workspace,
@@ -329,6 +332,10 @@ int nnhip_rmsnorm_bwd_dx(const float* G, const float* gamma, const float* m, con
                          float* out, size_t F, size_t N, void* stream);
 int nnhip_rmsnorm_bwd_rowsum(const float* G, const float* gamma, const float* Nrm, float* out, size_t F, size_t N,
                              void* stream);
+/* out[r] = out[r] + bwd_rowsum(...)[r]: the row sums added into out as a following add_inplace(out, sums)
+ * would add them (RMSNorm::backward's grad_gamma += gg; no CUDA counterpart). */
+int nnhip_rmsnorm_bwd_rowsum_add(const float* G, const float* gamma, const float* Nrm, float* out, size_t F,
+                                 size_t N, void* stream);
 int nnhip_swiglu_grad_gate(const float* G, const float* up, const float* s, const float* gate, float* out,
                            size_t count, void* stream);
 int nnhip_swiglu_grad_up(const float* G, const float* gate, const float* s, float* out, size_t count, void* stream);

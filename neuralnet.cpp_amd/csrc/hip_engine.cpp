@@ -458,6 +458,22 @@ struct HipEngine::PendingLayout
     bool uses(const float* p) const { return has_buf(S, p) || has_buf(out, p); }
 };
 
+// row_reduce_sum(src), or RMSNorm::backward's row sums of src * gamma[r] *
+// normed (kind 1), not launched yet: the layer's next call adds them into its
+// gradient (Linear::backward's grad_b += row_reduce_sum(G), RMSNorm's
+// grad_gamma += gg), which the row-sum kernel then does itself; `out` is
+// computed only if it is read later (`folded`: the sums were already added).
+struct HipEngine::PendingRowSum
+{
+    Tensor src, out, gamma, normed;
+    int kind = 0;
+    bool folded = false;
+    bool uses(const float* p) const
+    {
+        return has_buf(src, p) || has_buf(out, p) || has_buf(gamma, p) || has_buf(normed, p);
+    }
+};
+
 // RMSNorm::forward (compute_layer.hpp RMSNorm) as the layer issues it:
 //   s       = eval_expr_reduce(sum of squares, x)       stage 1
 //   scaled  = s * inv_f                                 stage 2
@@ -718,6 +734,7 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
             }
         if (pmadd_ && has_buf(pmadd_->out, p)) NN_CHECK(settle_madd_());
         if (prms_ && prms_->yields(p)) NN_CHECK(settle_rms_());
+        if (prsum_ && has_buf(prsum_->out, p)) NN_CHECK(settle_rsum_());
         for (std::size_t i = 0; i < playout_.size(); ++i)
             if (has_buf(playout_[i].out, p))
             {
@@ -804,6 +821,7 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb)
         }
     if (pmadd_ && pmadd_->uses(p)) NN_CHECK(settle_madd_());
     if (prms_ && prms_->uses(p)) NN_CHECK(settle_rms_());
+    if (prsum_ && prsum_->uses(p)) NN_CHECK(settle_rsum_());
     for (std::size_t i = playout_.size(); i-- > 0;)
         if (playout_[i].uses(p))
         {
@@ -841,6 +859,7 @@ Result<void> HipEngine::settle()
     NN_CHECK(settle_swb_());
     NN_CHECK(settle_madd_());
     NN_CHECK(settle_rms_());
+    NN_CHECK(settle_rsum_());
     NN_CHECK(settle_layout_());
     NN_CHECK(settle_dv_());
     NN_CHECK(settle_ds_());
@@ -2044,6 +2063,18 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
             return {};
         }
     }
+    if (prsum_ && !prsum_->folded && same_t(B, prsum_->out) && !prsum_->uses(A.dev_ptr()))
+    {
+        // A bias / gamma gradient: the row-sum kernel adds its sums into A; B
+        // stays recorded.
+        NN_CHECK(settle_write_(A));
+        if (prsum_ && same_t(B, prsum_->out))
+        {
+            NN_CHECK(launch_rsum_(*prsum_, W(A), true));
+            prsum_->folded = true;
+            return {};
+        }
+    }
     NN_CHECK(settle_chain_reads_({&B}));
     NN_CHECK(settle_chain_write_(A));
     return ew_push_(kBin, static_cast<unsigned>(BinaryOp::Add), false, A, A, &B, 0.0f);
@@ -2123,8 +2154,32 @@ Result<Tensor> HipEngine::row_reduce_sum(const Tensor& A)
 {
     NN_CHECK(need_gpu_({&A}, "row_reduce_sum"));
     NN_TRY(o, alloc_(A.rows(), 1));
-    NN_CHECK(kernel_(nnhip_reduce_row(D(A), W(o), A.rows(), A.cols(), 0u, stream_), "row_reduce_sum"));
+    if (!A.rows()) return o;
+    NN_CHECK(settle_rsum_());
+    prsum_ = std::make_unique<PendingRowSum>();
+    prsum_->src = A;
+    prsum_->out = o;
     return o;
+}
+
+Result<void> HipEngine::launch_rsum_(const PendingRowSum& r, float* out, bool add)
+{
+    const std::size_t R = r.src.rows(), C = r.src.cols();
+    if (r.kind == 1)
+        return kernel_(add ? nnhip_rmsnorm_bwd_rowsum_add(D(r.src), D(r.gamma), D(r.normed), out, R, C, stream_)
+                           : nnhip_rmsnorm_bwd_rowsum(D(r.src), D(r.gamma), D(r.normed), out, R, C, stream_),
+                       "eval_expr_reduce(rmsnorm backward row sum)");
+    return kernel_(add ? nnhip_reduce_row_sum_add(D(r.src), out, R, C, stream_)
+                       : nnhip_reduce_row(D(r.src), out, R, C, 0u, stream_),
+                   "row_reduce_sum");
+}
+
+Result<void> HipEngine::settle_rsum_()
+{
+    if (!prsum_) return {};
+    std::unique_ptr<PendingRowSum> r = std::move(prsum_);
+    if (!live(r->out)) return {};
+    return launch_rsum_(*r, W(r->out), false);
 }
 Result<Tensor> HipEngine::row_reduce_max(const Tensor& A)
 {
@@ -2621,9 +2676,30 @@ std::optional<Result<Tensor>> HipEngine::fused_layer_program_(const ExprSpec& sp
                    [&](float* o) { return nnhip_rmsnorm_bwd_colsum(a[0], a[1], a[2], o, rows, cols, stream_); },
                    "eval_expr_reduce(rmsnorm backward column sum)");
     if (is(LayerProg::RmsBwdRowSum))
+    {
+        const Tensor *g = nullptr, *gm = nullptr, *nm = nullptr;
+        for (const Tensor& t : inputs)
+        {
+            if (t.dev_ptr() == a[0]) g = &t;
+            if (t.dev_ptr() == a[1]) gm = &t;
+            if (t.dev_ptr() == a[2]) nm = &t;
+        }
+        if (g && gm && nm && aligned16(a[0]) && aligned16(a[2]))
+        {
+            NN_CHECK(settle_rsum_());
+            NN_TRY(o, alloc_(rows, 1));
+            prsum_ = std::make_unique<PendingRowSum>();
+            prsum_->src = *g;
+            prsum_->gamma = *gm;
+            prsum_->normed = *nm;
+            prsum_->kind = 1;
+            prsum_->out = o;
+            return Result<Tensor>(o);
+        }
         return run(rows, 1,
                    [&](float* o) { return nnhip_rmsnorm_bwd_rowsum(a[0], a[1], a[2], o, rows, cols, stream_); },
                    "eval_expr_reduce(rmsnorm backward row sum)");
+    }
     return std::nullopt;
 }
 

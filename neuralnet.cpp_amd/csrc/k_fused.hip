@@ -436,7 +436,7 @@ __global__ __launch_bounds__(kColT) void k_rms_bwd(const float* __restrict__ g, 
 
 // ── row sums: out[r] = sum_c g[r,c] * gamma[r] * normed[r,c], one workgroup per row ──
 __global__ __launch_bounds__(kT) void k_fused_rowsum_ggn(const float* g, const float* gamma, const float* n,
-                                                         float* out, unsigned cols4, size_t cols)
+                                                         float* out, unsigned cols4, size_t cols, bool add)
 {
     __shared__ float wsum[kT / 64];
     const unsigned r = blockIdx.x;
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(kT) void k_fused_rowsum_ggn(const float* g, const f
     {
         float s = wsum[0];
         for (unsigned w = 1; w < kT / 64; ++w) s += wsum[w];
-        out[r] = s;
+        out[r] = add ? out[r] + s : s;   // add: add_inplace of the sums, rounded as that call rounds
     }
 }
 
@@ -583,14 +583,29 @@ extern "C" int nnhip_rmsnorm_bwd_dx(const float* G, const float* gamma, const fl
     return launch_ew(RmsDx{G, gamma, m, normed, rinv, out, N}, F, N, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int nnhip_rmsnorm_bwd_rowsum(const float* G, const float* gamma, const float* normed, float* out, size_t F,
-                                        size_t N, void* stream)
+namespace
+{
+int rowsum_ggn(const float* G, const float* gamma, const float* normed, float* out, size_t F, size_t N, bool add,
+               void* stream)
 {
     if (!shape_ok(F, N, {G, normed})) return kBadShape;
     if (F == 0) return 0;
     hipLaunchKernelGGL(k_fused_rowsum_ggn, dim3(unsigned(F)), dim3(kT), 0, static_cast<hipStream_t>(stream), G, gamma,
-                       normed, out, unsigned(N / 4), N);
+                       normed, out, unsigned(N / 4), N, add);
     return launch_status();
+}
+} // namespace
+
+extern "C" int nnhip_rmsnorm_bwd_rowsum(const float* G, const float* gamma, const float* normed, float* out, size_t F,
+                                        size_t N, void* stream)
+{
+    return rowsum_ggn(G, gamma, normed, out, F, N, false, stream);
+}
+
+extern "C" int nnhip_rmsnorm_bwd_rowsum_add(const float* G, const float* gamma, const float* normed, float* out,
+                                            size_t F, size_t N, void* stream)
+{
+    return rowsum_ggn(G, gamma, normed, out, F, N, true, stream);
 }
 
 extern "C" int nnhip_swiglu_grad_gate(const float* G, const float* up, const float* s, const float* gate, float* out,

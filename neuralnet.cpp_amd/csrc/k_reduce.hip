@@ -18,20 +18,24 @@ constexpr unsigned kThreads = 256;
 
 __device__ __forceinline__ float combine(unsigned mode, float a, float b) { return mode ? fmax_std(a, b) : a + b; }
 
+// The row kernels write out[r] = result, or with `add` out[r] = out[r] + sum
+// (add_inplace of the sums, rounded as that separate call rounds).
+__device__ __forceinline__ void put(float* out, size_t r, float v, bool add) { out[r] = add ? out[r] + v : v; }
+
 // cols <= 32: one thread per row, serial along the row.
 __global__ __launch_bounds__(kThreads) void k_row_thread(const float* A, float* out, size_t rows, size_t cols,
-                                                         unsigned mode)
+                                                         unsigned mode, bool add)
 {
     const size_t r = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
     if (r >= rows) return;
     float acc = mode ? kLowest : 0.0f;
     for (size_t c = 0; c < cols; ++c) acc = combine(mode, acc, A[r * cols + c]);
-    out[r] = acc;
+    put(out, r, acc, add);
 }
 
 // cols <= 4096: one wave per row (4 rows per workgroup).
 __global__ __launch_bounds__(kThreads) void k_row_wave(const float* A, float* out, size_t rows, size_t cols,
-                                                       unsigned mode)
+                                                       unsigned mode, bool add)
 {
     const size_t r = static_cast<size_t>(blockIdx.x) * 4 + threadIdx.x / 64;
     if (r >= rows) return;
@@ -40,12 +44,12 @@ __global__ __launch_bounds__(kThreads) void k_row_wave(const float* A, float* ou
     const float* row = A + r * cols;
     for (size_t c = lane; c < cols; c += 64) acc = combine(mode, acc, row[c]);
     acc = mode ? wave_max(acc) : wave_sum(acc);
-    if (lane == 0) out[r] = acc;
+    if (lane == 0) put(out, r, acc, add);
 }
 
 // long rows: one workgroup per row.
 __global__ __launch_bounds__(kThreads) void k_row_block(const float* A, float* out, size_t rows, size_t cols,
-                                                        unsigned mode)
+                                                        unsigned mode, bool add)
 {
     __shared__ float part[kThreads / 64];
     const size_t r = blockIdx.x;
@@ -93,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void k_row_block(const float* A, float* o
     {
         float t = part[0];
         for (unsigned w = 1; w < kThreads / 64; ++w) t = combine(mode, t, part[w]);
-        out[r] = t;
+        put(out, r, t, add);
     }
 }
 
@@ -143,21 +147,34 @@ __global__ __launch_bounds__(kThreads) void k_col_combine(const float* part, flo
 
 using namespace nnhip;
 
-extern "C" int nnhip_reduce_row(const float* A, float* out, size_t rows, size_t cols, unsigned mode, void* stream)
+namespace
+{
+int reduce_row(const float* A, float* out, size_t rows, size_t cols, unsigned mode, bool add, void* stream)
 {
     if (mode > 1) return -1;
     if (rows == 0) return 0;
     auto s = static_cast<hipStream_t>(stream);
     if (cols <= 32)
         hipLaunchKernelGGL(k_row_thread, dim3(grid_for(rows, kThreads, 1u << 30)), dim3(kThreads), 0, s, A, out, rows,
-                           cols, mode);
+                           cols, mode, add);
     else if (cols <= 4096)
         hipLaunchKernelGGL(k_row_wave, dim3(grid_for(rows, 4, 1u << 30)), dim3(kThreads), 0, s, A, out, rows, cols,
-                           mode);
+                           mode, add);
     else
         hipLaunchKernelGGL(k_row_block, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, s, A, out, rows, cols,
-                           mode);
+                           mode, add);
     return launch_status();
+}
+} // namespace
+
+extern "C" int nnhip_reduce_row(const float* A, float* out, size_t rows, size_t cols, unsigned mode, void* stream)
+{
+    return reduce_row(A, out, rows, cols, mode, false, stream);
+}
+
+extern "C" int nnhip_reduce_row_sum_add(const float* A, float* out, size_t rows, size_t cols, void* stream)
+{
+    return reduce_row(A, out, rows, cols, 0u, true, stream);
 }
 
 extern "C" size_t nnhip_reduce_col_workspace_bytes(size_t rows, size_t cols)

@@ -231,6 +231,11 @@ private:
     Result<void> materialise_layout_(const PendingLayout& r);
     Result<void> settle_layout_();
     const PendingLayout* layout_of_(const Tensor& t) const;
+    // A row sum not launched yet (a Linear bias gradient, RMSNorm's gamma gradient).
+    struct PendingRowSum;
+    std::unique_ptr<PendingRowSum> prsum_;
+    Result<void> settle_rsum_();
+    Result<void> launch_rsum_(const PendingRowSum& r, float* out, bool add);
     // RMSNorm::forward's calls from the sum of squares on, not launched yet.
     struct PendingRms;
     std::unique_ptr<PendingRms> prms_;
