@@ -251,7 +251,7 @@ def test_elementwise_and_reductions(cpu):
     assert nrm_err(cpu.col_reduce_sum(cpu.tensor(big)).numpy()[0], np64(big).sum(0)) <= 1e-6
 
 
-# ── eval_expr programs of the GPT path ─────────────────
+# ── eval_expr programs of the GPT path (the layers' ExprSpec programs) ───────────
 def _softmax_fwd_spec():
     s = ExprSpec()
     for v in ("Linear", "RowReduceMax", "Linear", "RowReduceMax"):
