@@ -42,6 +42,14 @@ int nnhip_gemm(const float* A, const float* B, float* C, size_t A_rows, size_t A
                size_t batch, int transA, int transB, float alpha, void* workspace, size_t workspace_bytes,
                void* stream);
 
+/* A Linear output in the attention heads' layout: out (B*M, T) = rearrange_3d(W X (+ row_bias), M, B, T)
+ * (compute_layer.hpp AttentionBase::forward's q / k / v projections and head split), i.e. per batch b
+ * out[b*M + m][t] = sum_k W[m][k] X[k][b*T + t] (+ row_bias[m]); W (M, K), X (K, B*T). The sums are
+ * those of the product then the rearrange when that product is not split over K (K < 1024 for these
+ * shapes). No CUDA counterpart. */
+int nnhip_gemm_heads(const float* W, const float* X, const float* row_bias, float* out, size_t M, size_t K, size_t B,
+                     size_t T, void* stream);
+
 /* One product with the epilogue of the call that follows it in the reference's Linear layer
  * (compute_layer.hpp Linear::forward / backward): C = alpha * op(A) op(B), then C[i][j] += row_bias[i]
  * (broadcast_row_inplace(C, bias, Add)) when row_bias is not null, and C = C_old + result

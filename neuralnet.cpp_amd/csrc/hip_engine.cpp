@@ -726,6 +726,7 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
         const float* p = t->dev_ptr();
         if (!p) continue;
         if (pmm_ && has_buf(pmm_->C, p)) NN_CHECK(settle_mm_());
+        if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, false));
         for (const auto& r : pswb_)
             if (has_buf(r.out, p) || (r.placed && has_buf(r.dst, p)))
             {
@@ -813,6 +814,7 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb)
     const float* p = t.dev_ptr();
     if (!p) return {};
     if (pmm_ && pmm_->uses(p)) NN_CHECK(settle_mm_());
+    if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, true));
     for (const auto& r : pswb_)
         if (!keep_swb && r.uses(p))
         {
@@ -856,6 +858,7 @@ Result<void> HipEngine::settle()
     NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
     NN_CHECK(settle_mm_());
+    NN_CHECK(settle_mm_prev_(nullptr, false));
     NN_CHECK(settle_swb_());
     NN_CHECK(settle_madd_());
     NN_CHECK(settle_rms_());
@@ -1636,6 +1639,27 @@ Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size
         NN_CHECK(push_layout_(PendingLayout{S, out, true, M, B, N}));
         return out;
     }
+    // Of a recorded Linear output (the attention's head split, compute_layer.hpp
+    // AttentionBase::forward): the product writes the heads' layout itself.
+    if (!inverse && B > 1 && x.size() > 0)
+    {
+        PendingMm* r = nullptr;
+        if (pmm_ && same_t(x, pmm_->C)) r = pmm_.get();
+        for (auto& q : pmm_prev_)
+            if (same_t(x, q->C)) r = q.get();
+        if (r && !r->folded && !r->tA && !r->tB && r->M == M && r->N == B * N && x.rows() == M && r->K < 1024)
+        {
+            NN_CHECK(settle_reads_({&r->A, &r->B}));
+            NN_TRY(out, alloc_(B * M, N));
+            prof_begin_();
+            const int rc = nnhip_gemm_heads(D(r->A), D(r->B), r->bias.size() ? D(r->bias) : nullptr, W(out), M,
+                                            r->K, B, N, stream_);
+            prof_end_(M, N, r->K, B, false, false);
+            NN_CHECK(kernel_(rc, "matmul into heads"));
+            r->folded = true;
+            return out;
+        }
+    }
     NN_CHECK(settle_reads_({&x}));
     NN_TRY(out, alloc_(inverse ? M : B * M, inverse ? B * N : N));
     NN_CHECK(kernel_(nnhip_rearrange_3d(D(x), W(out), M, B, N, inverse ? 1u : 0u, stream_), "rearrange_3d"));
@@ -1667,9 +1691,45 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
     // Recorded: the Linear layer's next call adds the bias to C or adds C to
     // the weight gradient (compute_layer.hpp Linear), both folded into the
     // product's epilogue; any other use launches the plain product.
-    NN_CHECK(settle_mm_());
+    // An earlier record that this product does not read stays recorded (its
+    // output may go straight into the heads' layout, see rearrange_3d).
+    std::erase_if(pmm_prev_, [](const std::unique_ptr<PendingMm>& r) { return !live(r->C); });
+    constexpr std::size_t kKeepPrev = 4;
+    if (pmm_ && !has_buf(pmm_->C, A.dev_ptr()) && !has_buf(pmm_->C, B.dev_ptr()))
+    {
+        if (pmm_prev_.size() >= kKeepPrev)
+        {
+            std::unique_ptr<PendingMm> o = std::move(pmm_prev_.front());
+            pmm_prev_.erase(pmm_prev_.begin());
+            if (live(o->C)) NN_CHECK(launch_mm_(*o, o->C, o->bias.size() ? &o->bias : nullptr, false));
+        }
+        pmm_prev_.push_back(std::move(pmm_));
+    }
+    else
+        NN_CHECK(settle_mm_());
     pmm_ = std::make_unique<PendingMm>(PendingMm{A, B, C, tA, tB, M, N, K, false});
     return C;
+}
+
+// Earlier recorded matmuls that read or write p (every one when p is null):
+// launched (when still referenced) and dropped. Folded ones are launched only
+// when their own output is read or an input written.
+Result<void> HipEngine::settle_mm_prev_(const float* p, bool write)
+{
+    for (std::size_t i = 0; i < pmm_prev_.size();)
+    {
+        PendingMm& r = *pmm_prev_[i];
+        const bool hit = !p || (write ? r.uses(p) : has_buf(r.C, p));
+        if (!hit)
+        {
+            ++i;
+            continue;
+        }
+        std::unique_ptr<PendingMm> o = std::move(pmm_prev_[i]);
+        pmm_prev_.erase(pmm_prev_.begin() + static_cast<std::ptrdiff_t>(i));
+        if (live(o->C)) NN_CHECK(launch_mm_(*o, o->C, o->bias.size() ? &o->bias : nullptr, false));
+    }
+    return {};
 }
 
 // The recorded matmul into `out`: out = A B (+ bias per row) or out += A B.

@@ -854,6 +854,16 @@ extern "C" int nnhip_gemm_epilogue(const float* A, const float* B, float* C, siz
                          transB != 0, alpha, 1, workspace, workspace_bytes, stream, Epi{row_bias, accumulate ? 1 : 0});
 }
 
+extern "C" int nnhip_gemm_heads(const float* W, const float* X, const float* row_bias, float* out, size_t M,
+                                size_t K, size_t B, size_t T, void* stream)
+{
+    // Batch b: out_b (M, T) = W (M, K) X[:, b T : (b + 1) T] (+ bias), X read in place (ldb = B T); no
+    // split-K (the per-batch products are whole tiles of work already).
+    if (!W || !X || !out || B == 0 || T == 0 || M == 0 || K == 0) return -1;
+    return gemm_dispatch(W, X, out, M, T, K, K, B * T, 0, T, M * T, false, false, 1.0f, B, nullptr, 0, stream,
+                         Epi{row_bias, 0});
+}
+
 // ── GEMM without allocation ─────────────────────────────────────────────────
 // Split-K partial tiles of nnhip_gemm_noalloc live in this array. One copy
 // per GPU, held from when the library's code object loads on that GPU until

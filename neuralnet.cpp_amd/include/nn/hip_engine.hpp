@@ -200,7 +200,11 @@ private:
     Result<void> settle_swb_();
     struct PendingMm;
     std::unique_ptr<PendingMm> pmm_;
+    // Earlier matmuls still recorded when the next one did not read them
+    // (the attention's q, k, v projections), oldest first.
+    std::vector<std::unique_ptr<PendingMm>> pmm_prev_;
     Result<void> settle_mm_();
+    Result<void> settle_mm_prev_(const float* p, bool write);
     Result<void> launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate);
     struct PendingMaskAdd;
     struct PendingAttn;

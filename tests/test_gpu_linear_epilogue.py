@@ -140,3 +140,38 @@ def test_ce_from_product_statistics(hip, cpu, M, N, K, masked):
     for a, c, r in zip(fused[1:], calls[1:], ref[1:]):
         assert nrm_err(a, c) <= 1e-5
         assert nrm_err(a, r) <= 1e-5
+
+
+def _heads(e, Ws, bs, X, B, T, how):
+    """AttentionBase::forward's projections and head split: q, k, v = W x + b (matmul,
+    broadcast_row_inplace), then rearrange_3d(., H_dk, B, T). "fold": as issued (the products
+    write the heads' layout); "read": the projections read first (the separate calls); the
+    un-split projections are read at the end either way."""
+    x = e.tensor(X)
+    outs = []
+    for W, b in zip(Ws, bs):
+        y = e.matmul(e.tensor(W), x)
+        e.broadcast_row_inplace(y, e.tensor(b), "Add")
+        outs.append(y)
+    if how == "read":
+        for y in outs:
+            y.numpy()
+    heads = [e.rearrange_3d(y, Ws[0].shape[0], B, T, False) for y in outs]
+    return [h.numpy() for h in heads] + [y.numpy() for y in outs]
+
+
+@pytest.mark.parametrize("D,B,T", [(768, 8, 1024), (64, 3, 40), (96, 2, 36)])
+def test_projections_into_heads(hip, cpu, D, B, T):
+    """nnhip_gemm_heads: the q / k / v products written in the heads' layout, bit-identical to
+    the products then rearrange_3d, and the products themselves still correct when read later."""
+    rng = np.random.default_rng(D + B + T)
+    X = uniform(rng, (D, B * T))
+    Ws = [uniform(rng, (D, D)) for _ in range(3)]
+    bs = [uniform(rng, (D, 1)) for _ in range(3)]
+    fold = _heads(hip, Ws, bs, X, B, T, "fold")
+    sep = _heads(hip, Ws, bs, X, B, T, "read")
+    for i, (a, b) in enumerate(zip(fold, sep)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+    ref = _heads(cpu, Ws, bs, X, B, T, "read")
+    for a, b in zip(fold, ref):
+        assert nrm_err(a, b) <= 1e-5
