@@ -50,6 +50,12 @@ int nnhip_gemm(const float* A, const float* B, float* C, size_t A_rows, size_t A
 int nnhip_gemm_heads(const float* W, const float* X, const float* row_bias, float* out, size_t M, size_t K, size_t B,
                      size_t T, void* stream);
 
+/* Up to three such products of one X in one launch (the q, k and v projections): out[i] as
+ * nnhip_gemm_heads(W[i], X, row_bias ? row_bias[i] : NULL, out[i], ...); count in 1..3, row_bias may be NULL
+ * (no bias) or hold NULL entries. No CUDA counterpart. */
+int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* const* row_bias, float* const* out,
+                           size_t count, size_t M, size_t K, size_t B, size_t T, void* stream);
+
 /* One product with the epilogue of the call that follows it in the reference's Linear layer
  * (compute_layer.hpp Linear::forward / backward): C = alpha * op(A) op(B), then C[i][j] += row_bias[i]
  * (broadcast_row_inplace(C, bias, Add)) when row_bias is not null, and C = C_old + result

@@ -349,6 +349,8 @@ struct HipEngine::PendingMm
     std::size_t M, N, K;
     bool folded;
     Tensor bias;   // the Linear bias added by the call that followed (broadcast_row_inplace), if any
+    Tensor heads;  // C already written in the heads' layout (B_h sequences of N_h) by a grouped launch
+    std::size_t heads_B = 0, heads_N = 0;
     bool uses(const float* p) const { return has_buf(A, p) || has_buf(B, p) || has_buf(C, p) || has_buf(bias, p); }
 };
 
@@ -1647,17 +1649,54 @@ Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size
         if (pmm_ && same_t(x, pmm_->C)) r = pmm_.get();
         for (auto& q : pmm_prev_)
             if (same_t(x, q->C)) r = q.get();
-        if (r && !r->folded && !r->tA && !r->tB && r->M == M && r->N == B * N && x.rows() == M && r->K < 1024)
+        if (r && r->folded && r->heads.size() && r->heads_B == B && r->heads_N == N && x.rows() == M)
         {
-            NN_CHECK(settle_reads_({&r->A, &r->B}));
-            NN_TRY(out, alloc_(B * M, N));
-            prof_begin_();
-            const int rc = nnhip_gemm_heads(D(r->A), D(r->B), r->bias.size() ? D(r->bias) : nullptr, W(out), M,
-                                            r->K, B, N, stream_);
-            prof_end_(M, N, r->K, B, false, false);
-            NN_CHECK(kernel_(rc, "matmul into heads"));
-            r->folded = true;
+            Tensor out = r->heads;   // written by the group launch of an earlier head split
+            r->heads = Tensor();
             return out;
+        }
+        auto fits = [&](const PendingMm& q) {
+            return !q.folded && !q.tA && !q.tB && q.M == M && q.N == B * N && q.K < 1024 &&
+                   aligned16(q.A.dev_ptr()) && (!q.bias.size() || aligned16(q.bias.dev_ptr()));
+        };
+        if (r && fits(*r) && x.rows() == M)
+        {
+            // The other recorded products of the same input (k and v after q) join the launch.
+            std::vector<PendingMm*> grp{r};
+            auto join = [&](PendingMm* q) {
+                if (q != r && grp.size() < 3 && fits(*q) && same_t(q->B, r->B) && q->K == r->K && live(q->C))
+                    grp.push_back(q);
+            };
+            for (auto& q : pmm_prev_) join(q.get());
+            if (pmm_) join(pmm_.get());
+            for (PendingMm* q : grp) NN_CHECK(settle_reads_({&q->A, &q->B}));
+            const float* Ws[3] = {};
+            const float* bs[3] = {};
+            float* outs[3] = {};
+            std::vector<Tensor> hs;
+            for (std::size_t i = 0; i < grp.size(); ++i)
+            {
+                NN_TRY(h, alloc_(B * M, N));
+                hs.push_back(h);
+                Ws[i] = D(grp[i]->A);
+                bs[i] = grp[i]->bias.size() ? D(grp[i]->bias) : nullptr;
+                outs[i] = W(h);
+            }
+            prof_begin_();
+            const int rc = nnhip_gemm_heads_group(Ws, D(r->B), bs, outs, grp.size(), M, r->K, B, N, stream_);
+            prof_end_(M, N, r->K, B * grp.size(), false, false);
+            NN_CHECK(kernel_(rc, "matmul into heads"));
+            for (std::size_t i = 0; i < grp.size(); ++i)
+            {
+                grp[i]->folded = true;
+                if (i > 0)
+                {
+                    grp[i]->heads = hs[i];
+                    grp[i]->heads_B = B;
+                    grp[i]->heads_N = N;
+                }
+            }
+            return hs[0];
         }
     }
     NN_CHECK(settle_reads_({&x}));

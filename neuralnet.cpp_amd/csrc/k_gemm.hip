@@ -53,18 +53,28 @@ __device__ __forceinline__ void tile_coords(int bid, int nt, int tiles_m, int ti
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Up to three products sharing B (the attention's q, k, v projections of one
+// input): workgroup batch z takes member z / nb, batch z % nb of that member.
+struct GemmGroup
+{
+    const float* A[3];
+    float* C[3];
+    const float* bias[3];
+    int nb;
+};
+
 // WM x WN waves; each wave owns (32*FM) x (32*FN) of C as FM x FN MFMA 32x32 blocks.
 // STATS: besides C, each workgroup writes the column softmax statistics of its
 // BM rows of C (as stored, bias included): part[tile_m * N + n] = max over the
 // rows, part[(tiles_m + tile_m) * N + n] = sum of exp(c - max) over them. The
 // sparse cross-entropy that follows the product (the GPT's lm_head logits)
 // merges these instead of reading C once more for them. Needs splits == 1.
-template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD, bool STATS = false>
+template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD, bool STATS = false, bool GRP = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K, long lda, long ldb,
                                                        long strideA, long strideB, long strideC, float alpha,
                                                        int tiles_m, int tiles_n, int k_split, float* __restrict__ part,
-                                                       const float* __restrict__ bias, int accum)
+                                                       const float* __restrict__ bias, int accum, GemmGroup grp)
 {
     constexpr int NT = 64 * WM * WN;
     constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
@@ -91,9 +101,21 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
     const long bz = blockIdx.z;
-    A += bz * strideA;
-    B += bz * strideB;
-    C += bz * strideC;
+    if constexpr (GRP)
+    {
+        const int gi = static_cast<int>(bz / grp.nb);
+        const long bb = bz % grp.nb;
+        A = grp.A[gi];
+        B += bb * strideB;
+        C = grp.C[gi] + bb * strideC;
+        bias = grp.bias[gi];
+    }
+    else
+    {
+        A += bz * strideA;
+        B += bz * strideB;
+        C += bz * strideC;
+    }
     // Split-K: workgroup row y covers k in [y*k_split, min(K, (y+1)*k_split)) and,
     // when there are several, writes its partial tile to part[y][batch][M][N].
     const int k_lo = blockIdx.y * k_split;
@@ -555,8 +577,9 @@ Plan plan_gemm(size_t M, size_t N, size_t K, size_t batch, bool allow_split)
 
 struct Epi
 {
-    const float* bias;   // per output row, or null
-    int accum;           // C += result
+    const float* bias;                  // per output row, or null
+    int accum;                          // C += result
+    const GemmGroup* grp = nullptr;     // members of a grouped launch (no split, NN only)
 };
 
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB>
@@ -569,12 +592,25 @@ void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, l
     const bool guard = !vec_ok || (M % BM) || (N % BN) || (K % BK) || (k_split % BK);
     const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits), static_cast<unsigned>(batch));
     const dim3 block(64 * WM * WN);
+    if constexpr (!TA && !TB)
+        if (e.grp)
+        {
+            if (guard)
+                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, true, false, true>), grid, block, 0, s, A, B, C,
+                                   M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum,
+                                   *e.grp);
+            else
+                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, true>), grid, block, 0, s, A, B,
+                                   C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum,
+                                   *e.grp);
+            return;
+        }
     if (guard)
         hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, true>), grid, block, 0, s, A, B, C, M, N, K, lda, ldb,
-                           sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum);
+                           sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum, GemmGroup{});
     else
         hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false>), grid, block, 0, s, A, B, C, M, N, K, lda, ldb,
-                           sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum);
+                           sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum, GemmGroup{});
 }
 
 template <bool TA, bool TB>
@@ -756,8 +792,10 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
 {
     if (M == 0 || N == 0 || batch == 0) return 0;
     if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || batch > 65535) return -1;
+    if (e.grp && (tA || tB || workspace)) return -1;
     auto s = static_cast<hipStream_t>(stream);
-    if (int rc = 0; try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc)) return rc;
+    if (int rc = 0; !e.grp && try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc))
+        return rc;
     Plan p = plan_gemm(M, N, K, batch, workspace != nullptr);
     if (p.splits > 1 && static_cast<size_t>(p.splits) * batch * M * N * sizeof(float) > ws_bytes)
         p = plan_gemm(M, N, K, batch, false);
@@ -816,10 +854,10 @@ extern "C" int nnhip_gemm_colstats(const float* A, const float* B, float* C, siz
     auto s = static_cast<hipStream_t>(stream);
     if (guard)
         hipLaunchKernelGGL((k_gemm<4, 2, 2, 2, 16, false, false, true, true>), grid, block, 0, s, A, B, C, m, n, k,
-                           (long)A_cols, (long)B_cols, 0L, 0L, 0L, 1.0f, tm, tn, k, stats, row_bias, 0);
+                           (long)A_cols, (long)B_cols, 0L, 0L, 0L, 1.0f, tm, tn, k, stats, row_bias, 0, GemmGroup{});
     else
         hipLaunchKernelGGL((k_gemm<4, 2, 2, 2, 16, false, false, false, true>), grid, block, 0, s, A, B, C, m, n, k,
-                           (long)A_cols, (long)B_cols, 0L, 0L, 0L, 1.0f, tm, tn, k, stats, row_bias, 0);
+                           (long)A_cols, (long)B_cols, 0L, 0L, 0L, 1.0f, tm, tn, k, stats, row_bias, 0, GemmGroup{});
     return launch_status();
 }
 
@@ -862,6 +900,25 @@ extern "C" int nnhip_gemm_heads(const float* W, const float* X, const float* row
     if (!W || !X || !out || B == 0 || T == 0 || M == 0 || K == 0) return -1;
     return gemm_dispatch(W, X, out, M, T, K, K, B * T, 0, T, M * T, false, false, 1.0f, B, nullptr, 0, stream,
                          Epi{row_bias, 0});
+}
+
+extern "C" int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* const* row_bias,
+                                      float* const* out, size_t count, size_t M, size_t K, size_t B, size_t T,
+                                      void* stream)
+{
+    if (!W || !X || !out || count == 0 || count > 3 || B == 0 || T == 0 || M == 0 || K == 0 || B > 21845) return -1;
+    GemmGroup g{};
+    g.nb = static_cast<int>(B);
+    for (size_t i = 0; i < count; ++i)
+    {
+        if (!W[i] || !out[i]) return -1;
+        g.A[i] = W[i];
+        g.C[i] = out[i];
+        g.bias[i] = row_bias ? row_bias[i] : nullptr;
+    }
+    // Member pointers come from the group; A and C here only give the shape checks their operands.
+    return gemm_dispatch(W[0], X, out[0], M, T, K, K, B * T, 0, T, M * T, false, false, 1.0f, count * B, nullptr, 0,
+                         stream, Epi{nullptr, 0, &g});
 }
 
 // ── GEMM without allocation ─────────────────────────────────────────────────
