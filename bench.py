@@ -308,7 +308,8 @@ def attention_leg(seed, reps=5):
 
     def row(q, k, v, g, mk):
         # The reference's call sequence for one packed row (compute_layer.hpp:1196-1221, :1304-1327);
-        # its temporaries (the dP product among them) end with the call, as in the layer.
+        # its temporaries (the dP product among them) end with the call, as in the layer. The engine
+        # records each row's fused forward and backward and launches the rows together.
         m = eng.batched_matmul_reduce(q, k, H, "Max", True, False, 0.125, True, mk)
         l = eng.batched_matmul_softmax_denom(q, k, m, H, True, False, 0.125, mk)
         vt = eng.rearrange_3d(eng.transpose(v), T, H, d)
@@ -320,8 +321,8 @@ def attention_leg(seed, reps=5):
         return o, dq, dk, dv
 
     def fwd_bwd():
-        for q, k, v, g, mk in rows:
-            row(q, k, v, g, mk)
+        # every row's outputs stay referenced until the call is settled, as a caller keeps them
+        return [row(q, k, v, g, mk) for q, k, v, g, mk in rows]
     ms = timed_ms(timer, busy, fwd_bwd, reps)
     flop = 12 * d * pairs * H
     out["doc_masked_config5_forward_backward"] = {

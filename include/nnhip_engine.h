@@ -191,6 +191,11 @@ int nnhip_engine_profile_gemm_read(nnhip_engine* e, double* launches, double* fl
  * at most max; returns the number written (-1 on error) and clears the record. */
 long nnhip_engine_profile_gemm_records(nnhip_engine* e, double* out, size_t max);
 void* nnhip_engine_stream(nnhip_engine* e);
+/* Bytes of attention score blocks that the two-pass chain's recorded forward outputs may hold for their
+ * backward (default 1/8 of the device memory free when the engine was created, at most 8 GiB); 0 keeps
+ * none, and every backward forms its scores again. The blocks only save work: results are the same
+ * either way, and an allocation that fails leaves them out. No reference counterpart. */
+int nnhip_engine_set_score_budget(nnhip_engine* e, size_t bytes);
 /* Launches every deferred attention call (HipEngine defers the reference's two-pass attention chains
  * and runs each as one fused launch) whose results are still referenced, without waiting. */
 int nnhip_engine_settle(nnhip_engine* e);

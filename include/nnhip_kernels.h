@@ -284,6 +284,52 @@ int nnhip_flash_backward_ds_ordered(const float* Q, const float* Kt, const float
                                     const float* l, float* R, float* dQ, float* dK, float* dV, size_t batch, size_t M,
                                     size_t N, size_t K, float alpha, float alpha2, size_t mask_batch_stride,
                                     const float* scores, const void* order, void* workspace, void* stream);
+/* Multi-row launches (no CUDA counterpart): nrows (1..NNHIP_FLASH_MAX_ROWS) independent two-pass chains of one shape, hpr
+ * batch entries each, as one launch. The reference issues a document-masked batch as one chain per
+ * packed row, since each row has its own (M, N) mask (the primitives take one mask shared by the batch:
+ * cpu_engine.hpp:426-915); one row alone fills a small part of the GPU. Row r's pointers are those of
+ * its own one-row call (nnhip_flash_forward_ordered with mask_batch_stride 0; the dS backward's R may be
+ * NULL in every row or in none). Workspaces: nnhip_flash_workspace_bytes / nnhip_flash_ds_workspace_bytes
+ * at batch nrows * hpr. order: a table from nnhip_flash_build_rows_order over the rows' cell tables
+ * (nnhip_flash_order_bytes at batch nrows * hpr), or NULL. */
+#define NNHIP_FLASH_MAX_ROWS 8
+typedef struct nnhip_flash_fwd_row
+{
+    const float* Q;
+    const float* Kt;
+    const float* V;
+    const float* mask;
+    const void* cells;
+    float* m;
+    float* l;
+    float* O;
+    float* scores;
+} nnhip_flash_fwd_row;
+typedef struct nnhip_flash_bwd_row
+{
+    const float* Q;
+    const float* Kt;
+    const float* dO;
+    const float* Vp;
+    const float* O;
+    const float* mask;
+    const void* cells;
+    const float* m;
+    const float* l;
+    const float* scores;
+    float* R;
+    float* dQ;
+    float* dK;
+    float* dV;
+} nnhip_flash_bwd_row;
+int nnhip_flash_forward_rows(const nnhip_flash_fwd_row* rows, size_t nrows, size_t hpr, size_t M, size_t N, size_t K,
+                             size_t D, float alpha, int v_dim_major, int o_dim_major, const void* order,
+                             void* workspace, void* stream);
+int nnhip_flash_backward_ds_rows(const nnhip_flash_bwd_row* rows, size_t nrows, size_t hpr, size_t M, size_t N,
+                                 size_t K, float alpha, float alpha2, int o_query_major, const void* order,
+                                 void* workspace, void* stream);
+int nnhip_flash_build_rows_order(const void* const* cells, size_t nrows, size_t hpr, size_t M, size_t N, int kind,
+                                 void* order, void* stream);
 
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */

@@ -68,6 +68,16 @@ extern "C" NN_CAPI_EXPORT int nnhip_engine_settle(void* e)
     return r ? 0 : nn::capi::set_error(r.error().message);
 }
 
+// Bytes of attention score blocks the two-pass chain's recorded forwards may
+// keep for their backward (HipEngine::set_score_budget).
+extern "C" NN_CAPI_EXPORT int nnhip_engine_set_score_budget(void* e, size_t bytes)
+{
+    auto* h = dynamic_cast<nn::HipEngine*>(static_cast<nn::capi::EngineHandle*>(e)->eng.get());
+    if (!h) return nn::capi::set_error("set_score_budget: not a HIP engine");
+    h->set_score_budget(bytes);
+    return 0;
+}
+
 // cli::create_engine with the reference's flags (cli/engine_factory.hpp:45-88)
 // plus use_hip: the requested backend or an error, never another engine.
 extern "C" NN_CAPI_EXPORT int nnhip_engine_select(int use_hip, int use_cuda, int use_gpu, int verbose, void** out)

@@ -5,6 +5,8 @@
 
 #include <cstddef>
 
+#include "nnhip_kernels.h"
+
 namespace nnhip
 {
 
@@ -64,6 +66,24 @@ struct FlashBwdArgs
     const float* S;      // when set: the forward's score blocks; the key-line pass reads them instead of
                          // recomputing alpha q.k + mask
 };
+// One launch over several independent calls ("rows": e.g. the packed rows of a
+// document-masked batch, each with its own (M, N) mask) of the same shape.
+// Batch entry b of the launch belongs to row b / hpr. Each row's arguments
+// hold pointers pre-offset by -(row * hpr) batch entries, so that the kernels
+// index every array with the launch-wide b exactly as in a one-row launch;
+// cls[row] likewise for the row's mask cell tables.
+constexpr int kFlashMaxRows = NNHIP_FLASH_MAX_ROWS;
+template <class Args>
+struct FlashSet
+{
+    Args a[kFlashMaxRows];
+    const unsigned char* cls[kFlashMaxRows];
+    int hpr;   // batch entries per row (>= 1)
+    int rows;
+};
+using FlashFwdSet = FlashSet<FlashFwdArgs>;
+using FlashBwdSet = FlashSet<FlashBwdArgs>;
+
 // Score blocks: one per 32 x 32 cell, block (b, query tile, key tile) at
 // ((b RT + qt) CT + kt) 1024 floats; inside, score (query q, key k) at
 // r 64 + h 32 + q with drow(r, h) = k (the forward's lane order).
@@ -95,5 +115,17 @@ int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t bat
 size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K);
 int flash_backward_ds(const FlashBwdArgs& a, const float* O, int o_qm, const unsigned char* cells, size_t batch,
                       void* workspace, const int* order, hipStream_t s);
+
+// Multi-row forms: `rows` calls of `hpr` batch entries each, row r with its own
+// arguments (unshifted pointers, as for the one-row call) and cells[r]; the
+// workspace and order table cover batch rows * hpr (flash_rows_order_bytes /
+// flash_build_rows_order; flash_workspace_bytes and flash_ds_workspace_bytes
+// at that batch).
+int flash_forward_rows(const FlashFwdArgs* a, const unsigned char* const* cells, int rows, size_t hpr,
+                       void* workspace, const int* order, hipStream_t s);
+int flash_backward_ds_rows(const FlashBwdArgs* a, const float* const* O, int o_qm, const unsigned char* const* cells,
+                           int rows, size_t hpr, void* workspace, const int* order, hipStream_t s);
+int flash_build_rows_order(const unsigned char* const* cells, int rows, size_t hpr, size_t M, size_t N,
+                           bool per_batch_cls, int kind, void* order, hipStream_t s);
 
 } // namespace nnhip

@@ -525,6 +525,40 @@ struct HipEngine::TwoPassOut
     }
 };
 
+// A fused two-pass launch not run yet: the forward of softmax_apply (m, l, O
+// and the score blocks S from Q, K and V read dim-major from Vs) or the
+// backward of backward_kv from that forward's output (R, dQ, dK, dV from Q,
+// K, dO, V' = Vs, O, m, l and S). The cell table is held so that its address
+// stays this mask's while the record waits.
+struct HipEngine::PendingFlash
+{
+    bool bwd = false;
+    Tensor Q, K, Vs, dO, O, m, l, S, R, dQ, dK, dV;
+    std::optional<Tensor> mask;
+    std::shared_ptr<DeviceBuffer> cells;
+    std::size_t batch = 0, M = 0, N = 0, Kd = 0, D = 0;
+    float alpha = 0.0f, alpha2 = 0.0f;
+    bool v_dm = false;   // forward: Vs per batch (D, N) (the recorded layout's source) instead of (N, D)
+    bool yields(const float* p) const
+    {
+        if (bwd) return has_buf(R, p) || has_buf(dQ, p) || has_buf(dK, p) || has_buf(dV, p);
+        return has_buf(O, p) || has_buf(m, p) || has_buf(l, p) || has_buf(S, p);
+    }
+    bool uses(const float* p) const
+    {
+        return yields(p) || has_buf(Q, p) || has_buf(K, p) || has_buf(Vs, p) || has_buf(dO, p) ||
+               (mask && has_buf(*mask, p)) || (bwd && (has_buf(O, p) || has_buf(m, p) || has_buf(l, p) ||
+                                                       has_buf(S, p)));
+    }
+    // Records that run as rows of one launch.
+    bool joins(const PendingFlash& o) const
+    {
+        return bwd == o.bwd && batch == o.batch && M == o.M && N == o.N && Kd == o.Kd && D == o.D &&
+               !mask == !o.mask && !S.size() == !o.S.size() && alpha == o.alpha && alpha2 == o.alpha2 &&
+               v_dm == o.v_dm;
+    }
+};
+
 namespace
 {
 
@@ -586,6 +620,15 @@ HipEngine::HipEngine()
     }
     stream_ = s;
     pool_ = std::make_shared<DevicePool>(device_);
+    // Score blocks kept from forward to backward: at most 1/8 of the memory
+    // free now and at most 8 GiB.
+    std::size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess)
+    {
+        (void)hipGetLastError();
+        free_b = 0;
+    }
+    score_budget_ = std::min(std::size_t(8) << 30, free_b / 8);
     ok_ = true;
 }
 
@@ -720,13 +763,14 @@ Result<void> HipEngine::settle_reads_(std::initializer_list<const Tensor*> ts)
     return settle_chain_reads_(ts);
 }
 
-Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*> ts)
+Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*> ts, bool keep_flash)
 {
     for (const Tensor* t : ts)
     {
         if (!t) continue;
         const float* p = t->dev_ptr();
         if (!p) continue;
+        if (!keep_flash && flash_yields_(p)) NN_CHECK(settle_flash_());
         if (pmm_ && has_buf(pmm_->C, p)) NN_CHECK(settle_mm_());
         if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, false));
         for (const auto& r : pswb_)
@@ -759,16 +803,16 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
 
 // Cell tables of a mask tensor read as rows / M stacked (M, N) masks (one
 // table each), cached per tensor until it is written in place or evicted.
-Result<const void*> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, std::size_t N)
+Result<std::shared_ptr<DeviceBuffer>> HipEngine::mask_cells_buf_(const Tensor* mask, std::size_t M, std::size_t N)
 {
-    if (!mask) return static_cast<const void*>(nullptr);
+    if (!mask) return std::shared_ptr<DeviceBuffer>();
     for (std::size_t i = 0; i < cells_.size(); ++i)
         if (same_t(cells_[i].mask, *mask) && cells_[i].M == M)
         {
             CellTable t = cells_[i];
             cells_.erase(cells_.begin() + static_cast<std::ptrdiff_t>(i));
             cells_.push_back(t);
-            return static_cast<const void*>(t.cells->data());
+            return t.cells;
         }
     const std::size_t masks = mask->rows() / M;
     NN_TRY(buf, scratch_(masks * nnhip_flash_cells_bytes(M, N)));
@@ -777,7 +821,130 @@ Result<const void*> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, st
     constexpr std::size_t kKeep = 32;   // one per layer's mask in a 12-32 layer model
     if (cells_.size() == kKeep) cells_.erase(cells_.begin());
     cells_.push_back({*mask, buf, M, {}});
+    return buf;
+}
+
+Result<const void*> HipEngine::mask_cells_(const Tensor* mask, std::size_t M, std::size_t N)
+{
+    NN_TRY(buf, mask_cells_buf_(mask, M, N));
+    return static_cast<const void*>(buf ? buf->data() : nullptr);
+}
+
+// Work order of a multi-row launch (kind as flash_order_), built once per set
+// of cell tables and shape; the last few are kept.
+Result<const void*> HipEngine::rows_order_(const std::vector<std::shared_ptr<DeviceBuffer>>& cells, std::size_t hpr,
+                                           std::size_t M, std::size_t N, int kind)
+{
+    for (std::size_t i = 0; i < rows_orders_.size(); ++i)
+    {
+        const RowsOrder& o = rows_orders_[i];
+        if (o.cells == cells && o.hpr == hpr && o.M == M && o.N == N && o.kind == kind)
+            return static_cast<const void*>(o.buf->data());
+    }
+    std::vector<const void*> ptrs;
+    for (const auto& c : cells) ptrs.push_back(c->data());
+    NN_TRY(buf, scratch_(nnhip_flash_order_bytes(cells.size() * hpr, M, N, kind)));
+    NN_CHECK(kernel_(nnhip_flash_build_rows_order(ptrs.data(), cells.size(), hpr, M, N, kind, buf->data(), stream_),
+                     "attention work order"));
+    constexpr std::size_t kKeep = 8;
+    if (rows_orders_.size() == kKeep) rows_orders_.erase(rows_orders_.begin());
+    rows_orders_.push_back(RowsOrder{cells, hpr, M, N, kind, buf});
     return static_cast<const void*>(buf->data());
+}
+
+// ── recorded fused attention launches ───────────────────────────────────────
+bool HipEngine::flash_yields_(const float* p) const
+{
+    for (const PendingFlash& r : pflash_)
+        if (r.yields(p)) return true;
+    return false;
+}
+
+bool HipEngine::flash_uses_(const float* p) const
+{
+    for (const PendingFlash& r : pflash_)
+        if (r.uses(p)) return true;
+    return false;
+}
+
+// Every recorded launch: the forwards, then the backwards (a backward reads
+// only forwards' results; records of one kind never read each other's),
+// records that join each other as rows of one launch, at most
+// NNHIP_FLASH_MAX_ROWS per launch, in call order otherwise.
+Result<void> HipEngine::settle_flash_()
+{
+    if (pflash_.empty()) return {};
+    std::vector<PendingFlash> rs = std::move(pflash_);
+    pflash_.clear();
+    for (int kind = 0; kind < 2; ++kind)
+    {
+        std::vector<bool> done(rs.size(), false);
+        for (std::size_t i = 0; i < rs.size(); ++i)
+        {
+            if (done[i] || rs[i].bwd != (kind == 1)) continue;
+            std::vector<const PendingFlash*> rows{&rs[i]};
+            done[i] = true;
+            for (std::size_t j = i + 1; j < rs.size() && rows.size() < NNHIP_FLASH_MAX_ROWS; ++j)
+                if (!done[j] && rs[j].joins(rs[i]))
+                {
+                    rows.push_back(&rs[j]);
+                    done[j] = true;
+                }
+            NN_CHECK(launch_flash_(rows));
+        }
+    }
+    return {};
+}
+
+Result<void> HipEngine::launch_flash_(const std::vector<const PendingFlash*>& rows)
+{
+    const PendingFlash& f = *rows.front();
+    const std::size_t n = rows.size();
+    std::vector<std::shared_ptr<DeviceBuffer>> cells;
+    for (const PendingFlash* r : rows)
+        if (r->cells) cells.push_back(r->cells);
+    const void* order = nullptr;
+    if (f.mask)
+    {
+        // One row: the table cached with its mask; several: one per set of tables.
+        if (n == 1)
+        {
+            NN_TRY(o, flash_order_(f.cells->data(), f.batch, f.M, f.N, 0, f.bwd ? 2 : 0));
+            order = o;
+        }
+        else
+        {
+            NN_TRY(o, rows_order_(cells, f.batch, f.M, f.N, f.bwd ? 2 : 0));
+            order = o;
+        }
+    }
+    if (!f.bwd)
+    {
+        std::vector<nnhip_flash_fwd_row> a(n);
+        for (std::size_t r = 0; r < n; ++r)
+        {
+            const PendingFlash& x = *rows[r];
+            a[r] = nnhip_flash_fwd_row{D(x.Q), D(x.K), D(x.Vs), x.mask ? D(*x.mask) : nullptr,
+                                       x.cells ? x.cells->data() : nullptr, W(x.m), W(x.l), W(x.O),
+                                       x.S.size() ? W(x.S) : nullptr};
+        }
+        NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(n * f.batch, f.M, f.N, f.Kd, f.D, 0)));
+        return kernel_(nnhip_flash_forward_rows(a.data(), n, f.batch, f.M, f.N, f.Kd, f.D, f.alpha, f.v_dm ? 1 : 0,
+                                                0, order, ws->data(), stream_),
+                       "batched_matmul_softmax_apply");
+    }
+    std::vector<nnhip_flash_bwd_row> a(n);
+    for (std::size_t r = 0; r < n; ++r)
+    {
+        const PendingFlash& x = *rows[r];
+        a[r] = nnhip_flash_bwd_row{D(x.Q), D(x.K), D(x.dO), D(x.Vs), D(x.O), x.mask ? D(*x.mask) : nullptr,
+                                   x.cells ? x.cells->data() : nullptr, D(x.m), D(x.l), x.S.size() ? D(x.S) : nullptr,
+                                   W(x.R), W(x.dQ), W(x.dK), W(x.dV)};
+    }
+    NN_TRY(ws, scratch_(nnhip_flash_ds_workspace_bytes(n * f.batch, f.M, f.N, f.Kd)));
+    return kernel_(nnhip_flash_backward_ds_rows(a.data(), n, f.batch, f.M, f.N, f.Kd, f.alpha, f.alpha2, 1, order,
+                                                ws->data(), stream_),
+                   "batched_matmul_softmax_backward_kv");
 }
 
 // Work order of a one-pass attention launch over a cached cell table (kind 0
@@ -815,6 +982,7 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb)
     NN_CHECK(unshare_(t));
     const float* p = t.dev_ptr();
     if (!p) return {};
+    if (flash_uses_(p)) NN_CHECK(settle_flash_());
     if (pmm_ && pmm_->uses(p)) NN_CHECK(settle_mm_());
     if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, true));
     for (const auto& r : pswb_)
@@ -859,6 +1027,7 @@ Result<void> HipEngine::settle()
 {
     NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
+    NN_CHECK(settle_flash_());
     NN_CHECK(settle_mm_());
     NN_CHECK(settle_mm_prev_(nullptr, false));
     NN_CHECK(settle_swb_());
@@ -912,6 +1081,8 @@ Result<void> HipEngine::settle_gemm_()
 // dQ and R of a deferred backward_q with the general kernels (P computed first).
 Result<void> HipEngine::settle_bwd_()
 {
+    if (!pbwd_) return {};
+    NN_CHECK(settle_flash_());   // m and l may come from a recorded forward
     if (!pbwd_) return {};
     std::unique_ptr<PendingBwd> q = std::move(pbwd_);
     if (!live(q->dQ) && !live(q->R)) return {};
@@ -1917,32 +2088,49 @@ Result<Tensor> HipEngine::batched_matmul_softmax_apply(const Tensor& A, const Te
     {
         std::unique_ptr<PendingFwd> f = std::move(pfwd_);
         NN_TRY(o, alloc_(batch * d.M, V.cols()));
-        NN_TRY(cells, mask_cells_(mask, d.M, d.N));
-        NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 0));
-        NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, d.K, V.cols(), 0)));
+        NN_TRY(cells, mask_cells_buf_(mask, d.M, d.N));
         // A recorded output also keeps the forward's scores for the backward
         // (one 32 x 32 block per cell, so M and N whole tiles), while all
-        // records together hold at most kScoreBytes of them.
+        // records together hold at most score_budget_ bytes of them. The
+        // blocks only save work: when they cannot be had, the backward forms
+        // the scores itself.
         Tensor S;
         if (v_src)
         {
             forget_dead_two_();
             constexpr std::size_t kKeep = 64;   // one per layer
             if (ptwo_.size() >= kKeep) ptwo_.erase(ptwo_.begin());
-            constexpr std::size_t kScoreBytes = std::size_t(8) << 30;
             std::size_t held = 0;
             for (const TwoPassOut& r : ptwo_) held += r.S.size() * sizeof(float);
-            if (d.M % 32 == 0 && d.N % 32 == 0 && held + batch * d.M * d.N * sizeof(float) <= kScoreBytes)
+            if (d.M % 32 == 0 && d.N % 32 == 0 && held + batch * d.M * d.N * sizeof(float) <= score_budget_)
             {
-                NN_TRY(t, alloc_(batch * d.M, d.N));
-                S = t;
+                auto t = alloc_(batch * d.M, d.N);
+                if (t) S = *t;
             }
         }
-        NN_CHECK(kernel_(nnhip_flash_forward_ordered(D(A), D(B), D(Vs), mask ? D(*mask) : nullptr, cells, W(f->m),
-                                                     W(*f->l), W(o), batch, d.M, d.N, d.K, V.cols(), alpha, 0,
-                                                     v_src ? 1 : 0, 0, S.size() ? W(S) : nullptr, order, ws->data(),
-                                                     stream_),
-                         "batched_matmul_softmax_apply"));
+        // The launch waits for others of its shape (the next rows of a
+        // document-masked batch) until its results are read.
+        if (flash_yields_(D(A)) || flash_yields_(D(B)) || flash_yields_(D(Vs)) || (mask && flash_yields_(D(*mask))) ||
+            pflash_.size() >= 2 * NNHIP_FLASH_MAX_ROWS)
+            NN_CHECK(settle_flash_());
+        PendingFlash r;
+        r.Q = A;
+        r.K = B;
+        r.Vs = Vs;
+        r.O = o;
+        r.m = f->m;
+        r.l = *f->l;
+        r.S = S;
+        r.mask = mask ? std::optional<Tensor>(*mask) : std::nullopt;
+        r.cells = cells;
+        r.batch = batch;
+        r.M = d.M;
+        r.N = d.N;
+        r.Kd = d.K;
+        r.D = V.cols();
+        r.alpha = alpha;
+        r.v_dm = v_src;
+        pflash_.push_back(std::move(r));
         if (v_src)
             ptwo_.push_back(TwoPassOut{A, B, mask ? std::optional<Tensor>(*mask) : std::nullopt, f->m, *f->l, Vs, o,
                                        batch, alpha, S});
@@ -1975,7 +2163,11 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_q(const Tensor& A, con
     if (pgemm_ && same_t(P, pgemm_->C) && pgemm_->batch == batch && tA && !tB && d.K % 4 == 0 &&
         nnhip_flash_supported(batch, d.M, d.N, std::max(d.K, pgemm_->K), 4))
     {
-        NN_CHECK(settle_reads_({&A, &B, &row_max, &denom, mask}));
+        // m and l may still be results of a recorded forward: the backward
+        // that consumes this record runs after it.
+        NN_CHECK(settle_zero_());
+        NN_CHECK(settle_ew_());
+        NN_CHECK(settle_chain_reads_({&A, &B, &row_max, &denom, mask}, true));
         NN_CHECK(settle_bwd_());
         pbwd_ = std::make_unique<PendingBwd>(PendingBwd{A, B, P, row_max, denom,
                                                         mask ? std::optional<Tensor>(*mask) : std::nullopt, batch,
@@ -2041,17 +2233,42 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_kv(const Tensor& A, co
         {
             const TwoPassOut r = std::move(ptwo_[static_cast<std::size_t>(fo)]);
             ptwo_.erase(ptwo_.begin() + fo);
-            NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 2));
-            NN_TRY(ws, scratch_(nnhip_flash_ds_workspace_bytes(batch, d.M, d.N, d.K)));
-            NN_CHECK(kernel_(nnhip_flash_backward_ds_ordered(D(A), D(B), D(g.A), D(g.B), D(r.O), 1,
-                                                             mask ? D(*mask) : nullptr, cells, D(row_max), D(denom),
-                                                             W(q->R), W(q->dQ), W(dk), W(dv), batch, d.M, d.N, d.K,
-                                                             alpha, g.alpha, 0, r.S.size() ? D(r.S) : nullptr, order,
-                                                             ws->data(), stream_),
-                             "batched_matmul_softmax_backward_kv"));
+            // Recorded like the forward (the backwards of other rows join it);
+            // it reads recorded forwards' results, never a recorded backward's.
+            NN_TRY(cbuf, mask_cells_buf_(mask, d.M, d.N));
+            bool after_bwd = pflash_.size() >= 2 * NNHIP_FLASH_MAX_ROWS;
+            for (const PendingFlash& x : pflash_)
+                for (const Tensor* t : {&A, &B, &g.A, &g.B, &r.O, &row_max, &denom, &r.S, mask})
+                    after_bwd = after_bwd || (t && x.bwd && x.yields(D(*t)));
+            if (after_bwd) NN_CHECK(settle_flash_());
+            PendingFlash b;
+            b.bwd = true;
+            b.Q = A;
+            b.K = B;
+            b.dO = g.A;
+            b.Vs = g.B;
+            b.O = r.O;
+            b.m = row_max;
+            b.l = denom;
+            b.S = r.S;
+            b.R = q->R;
+            b.dQ = q->dQ;
+            b.dK = dk;
+            b.dV = dv;
+            b.mask = mask ? std::optional<Tensor>(*mask) : std::nullopt;
+            b.cells = cbuf;
+            b.batch = batch;
+            b.M = d.M;
+            b.N = d.N;
+            b.Kd = d.K;
+            b.D = d.K;
+            b.alpha = alpha;
+            b.alpha2 = g.alpha;
+            pflash_.push_back(std::move(b));
         }
         else
         {
+            NN_CHECK(settle_flash_());   // m and l may come from a recorded forward
             NN_TRY(order, flash_order_(cells, batch, d.M, d.N, 0, 1));
             NN_TRY(ws, scratch_(nnhip_flash_workspace_bytes(batch, d.M, d.N, std::max(d.K, g.K), 4, 1)));
             NN_CHECK(kernel_(nnhip_flash_backward_ordered(D(A), D(B), D(g.A), D(g.B), g_do ? nullptr : D(G),

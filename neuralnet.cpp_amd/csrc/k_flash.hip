@@ -47,6 +47,7 @@
 #include "flash.hpp"
 
 #include <algorithm>
+#include <cstdint>
 #include <type_traits>
 
 #include "common.hpp"
@@ -149,6 +150,16 @@ __device__ __forceinline__ Item item_of(const FlashGeo& g)
     r.grp = g.G - 1 - rem / g.NR;
     r.rg = rem % g.NR;
     return r;
+}
+
+// Arguments and cell tables of the row that batch entry b (uniform over the
+// workgroup) belongs to: the row's arguments are pre-offset, so b indexes them.
+template <class Args>
+__device__ __forceinline__ Args row_args(const FlashSet<Args>& t, FlashGeo& g, int b)
+{
+    const int row = __builtin_amdgcn_readfirstlane(b / t.hpr);
+    g.cls = t.cls[row];
+    return t.a[row];
 }
 
 // This range's cells of a line (ballots: bit x <-> cell rg*R + x, non-empty /
@@ -493,7 +504,7 @@ __device__ __forceinline__ float cell_scores(const f32x16& s, float alpha, const
 // rescale, skipped when no row maximum moved) and accumulates the weighted
 // values.
 template <int KP, int DP, bool WITH_O, bool VDM, int CPS>
-__global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(FlashFwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(FlashFwdSet t, FlashGeo g)
 {
     constexpr int DU = DP / 32;
     __shared__ __align__(16) float Ks[2][CPS][32][KP + 4];
@@ -501,6 +512,7 @@ __global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(Fla
     __shared__ unsigned long long nz_s[kWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const Item it = item_of(g);
+    const FlashFwdArgs a = row_args(t, g, it.b);
     const int line = it.grp * kWaves + wave, qi = line * 32 + c;
     const LineWork lw = line_work(g, true, it.b, line, it.rg);
     if (lane == 0) nz_s[wave] = lw.nz;
@@ -646,12 +658,13 @@ __global__ __launch_bounds__(64 * kWaves, CPS == 1 ? 3 : 2) void k_flash_fwd(Fla
 // f32x16 lane layout (every u), so each partial is read by all four waves at
 // once in 256-byte rows; every element is still merged in range order.
 template <int DP, bool WITH_O>
-__global__ __launch_bounds__(256) void k_flash_fwd_combine(FlashFwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(256) void k_flash_fwd_combine(FlashFwdSet t, FlashGeo g)
 {
     constexpr int DU = DP / 32;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
+    const FlashFwdArgs a = row_args(t, g, b);
     const LineWork lw = line_work(g, true, b, line, 0);
     if (lw.nne <= 1) return;
     float m = kLowest, l = 0.0f;
@@ -842,22 +855,24 @@ __device__ __forceinline__ void rows_group(const FlashBwdArgs& a, const FlashGeo
 }
 
 template <int KP>
-__global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_rows(FlashBwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_rows(FlashBwdSet t, FlashGeo g)
 {
     __shared__ __align__(16) float Ks[2][32][KP + 4];   // key tile [key][dim]
     __shared__ __align__(16) float Vs[2][32][KP + 4];   // V' tile [key][dim]
     __shared__ unsigned long long nz_s[kWaves];
     const Item it = item_of(g);
+    const FlashBwdArgs a = row_args(t, g, it.b);
     rows_group<KP>(a, g, it.b, it.grp, it.rg, Ks, Vs, nz_s);
 }
 
 template <int KP>
-__global__ __launch_bounds__(256) void k_flash_bwd_rows_combine(FlashBwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(256) void k_flash_bwd_rows_combine(FlashBwdSet t, FlashGeo g)
 {
     constexpr int DU = KP / 32;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
+    const FlashBwdArgs a = row_args(t, g, b);
     const LineWork lw = line_work(g, true, b, line, 0);
     if (lw.nne <= 1) return;
     float racc = 0.0f;
@@ -1140,7 +1155,7 @@ __device__ __forceinline__ void cols_group(const FlashBwdArgs& a, const FlashGeo
 }
 
 template <int KP, bool GDO, bool WDS, bool SST = false>
-__global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdSet t, FlashGeo g)
 {
     __shared__ __align__(16) float Qs[2][32][KP + 4];   // query tile [query][dim]
     __shared__ __align__(16) float Os[2][32][KP + 4];   // dO tile [query][dim]
@@ -1148,16 +1163,18 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_flash_bwd_cols(FlashBwdArgs 
     __shared__ float St[2][3][32];                      // m, 1/l, R of the tile's queries
     __shared__ unsigned long long nz_s[kWaves];
     const Item it = item_of(g);
+    const FlashBwdArgs a = row_args(t, g, it.b);
     cols_group<KP, GDO, WDS, SST>(a, g, it.b, it.grp, it.rg, Qs, Os, Gs, St, nz_s);
 }
 
 template <int KP>
-__global__ __launch_bounds__(256) void k_flash_bwd_cols_combine(FlashBwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(256) void k_flash_bwd_cols_combine(FlashBwdSet t, FlashGeo g)
 {
     constexpr int DU = KP / 32;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.CT), line = static_cast<int>(lidx % g.CT);
+    const FlashBwdArgs a = row_args(t, g, b);
     const LineWork lw = line_work(g, false, b, line, 0);
     if (lw.nne <= 1) return;
     float dk[DU][4], dv[DU][4];
@@ -1236,12 +1253,13 @@ __device__ __forceinline__ void dq_store(const FlashBwdArgs& a, const FlashGeo& 
 }
 
 template <int KP>
-__global__ __launch_bounds__(256) void k_flash_bwd_dq_combine(FlashBwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(256) void k_flash_bwd_dq_combine(FlashBwdSet t, FlashGeo g)
 {
     constexpr int DU = KP / 32;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const long lidx = blockIdx.x;
     const int b = static_cast<int>(lidx / g.RT), line = static_cast<int>(lidx % g.RT);
+    const FlashBwdArgs a = row_args(t, g, b);
     const LineWork lw = line_work(g, true, b, line, 0);
     if (lw.nne <= 1) return;
     float x[DU][4];
@@ -1278,12 +1296,13 @@ __global__ __launch_bounds__(256) void k_flash_bwd_dq_combine(FlashBwdArgs a, Fl
 // dQ from the stored dS: dQ_i = alpha sum_j dS_ij k_j over the non-empty cells
 // of the line's range, with the rows kernel's lines and ranges.
 template <int KP>
-__global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a, FlashGeo g)
+__global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdSet t, FlashGeo g)
 {
     constexpr int DU = KP / 32;
     __shared__ __align__(16) float Ks[2][32][KP + 4];   // key tile [key][dim]
     __shared__ unsigned long long nz_s[kWaves];
     const Item it = item_of(g);
+    const FlashBwdArgs a = row_args(t, g, it.b);
     const int b = it.b, rg = it.rg;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c = lane & 31;
     const int line = it.grp * kWaves + wave, qi = line * 32 + c;
@@ -1346,8 +1365,14 @@ __global__ __launch_bounds__(64 * kWaves, 3) void k_flash_bwd_dq(FlashBwdArgs a,
 // rounds; later workgroups backfill CUs as they free up, heaviest first. Items
 // of equal weight may be placed in any order (only the timing depends on it).
 constexpr int kOrderThreads = 1024;
-__global__ __launch_bounds__(kOrderThreads) void k_flash_order(FlashGeo g, int rows, int nitems, int ncu,
-                                                               int resident, int* __restrict__ order,
+// Cell tables of the rows of a launch (pre-offset like FlashSet::cls).
+struct FlashCls
+{
+    const unsigned char* cls[kFlashMaxRows];
+    int hpr;
+};
+__global__ __launch_bounds__(kOrderThreads) void k_flash_order(FlashGeo g, FlashCls tab, int rows, int nitems,
+                                                               int ncu, int resident, int* __restrict__ order,
                                                                unsigned char* __restrict__ weight)
 {
     __shared__ int count[65], cursor[65];
@@ -1357,7 +1382,7 @@ __global__ __launch_bounds__(kOrderThreads) void k_flash_order(FlashGeo g, int r
     for (int it = t; it < nitems; it += kOrderThreads)
     {
         const int b = it / per, rem = it % per, grp = g.G - 1 - rem / g.NR, rg = rem % g.NR;
-        const unsigned char* cls = g.cls + (long)b * g.cls_bs;
+        const unsigned char* cls = tab.cls[b / tab.hpr] + (long)b * g.cls_bs;
         const int x0 = rg * g.R, x1 = min(x0 + g.R, cells), l0 = grp * kWaves;
         int w = 0;
         if ((g.CT & 3) == 0)
@@ -1431,13 +1456,21 @@ __global__ __launch_bounds__(kOrderThreads) void k_flash_order(FlashGeo g, int r
 // (even and odd dims), and wave 0 adds the four partials in wave order.
 // Query-major O rows are contiguous: the workgroup's 64 Kd floats are staged
 // through LDS. Loops run a fixed 16 steps over clamped addresses, so every
-// load is in flight at once.
-__global__ __launch_bounds__(256) void k_flash_rowdot(const float* __restrict__ dO, const float* __restrict__ O,
-                                                      float* __restrict__ R, int M, int Kd, long total, float alpha2,
-                                                      int o_qm)
+// load is in flight at once. blockIdx.y: the row of a multi-row launch (its
+// own dO, O and R, `total` entries each).
+struct RowdotSet
+{
+    const float* dO[kFlashMaxRows];
+    const float* O[kFlashMaxRows];
+    float* R[kFlashMaxRows];
+};
+__global__ __launch_bounds__(256) void k_flash_rowdot(RowdotSet set, int M, int Kd, long total, float alpha2, int o_qm)
 {
     __shared__ float part[4][64];
     __shared__ float Ot[64][65];
+    const float* __restrict__ dO = set.dO[blockIdx.y];
+    const float* __restrict__ O = set.O[blockIdx.y];
+    float* __restrict__ R = set.R[blockIdx.y];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const long t0 = (long)blockIdx.x * 64, t = t0 + lane;
     const int q = Kd / 4, d0 = wave * q;
@@ -1563,17 +1596,102 @@ size_t order_table_bytes(const FlashGeo& g, size_t batch)
     return align256(n * sizeof(int)) + align256(n);
 }
 
+// Pointer p moved back by `elems` elements (null stays null): row r of a
+// multi-row launch passes its arrays shifted by r * hpr batch entries, so the
+// kernels' launch-wide entry index b addresses them.
+template <class T>
+T* shifted(T* p, size_t elems)
+{
+    return p ? reinterpret_cast<T*>(reinterpret_cast<std::uintptr_t>(p) - elems * sizeof(T)) : nullptr;
+}
+
+size_t blocks_per_entry(size_t M, size_t N) { return ((M + 31) / 32) * ((N + 31) / 32) * 1024; }
+
+// The rows' cell tables (null rows: no mask), shifted by their first entries.
+FlashCls cls_table(const unsigned char* const* cells, int rows, size_t hpr, long cls_bs)
+{
+    FlashCls t{};
+    t.hpr = static_cast<int>(hpr);
+    for (int r = 0; r < rows; ++r) t.cls[r] = shifted(cells[r], static_cast<size_t>(r) * hpr * cls_bs);
+    return t;
+}
+
+FlashFwdSet fwd_set(const FlashFwdArgs* a, const unsigned char* const* cells, int rows, size_t hpr, long cls_bs)
+{
+    FlashFwdSet t{};
+    t.hpr = static_cast<int>(hpr);
+    t.rows = rows;
+    for (int r = 0; r < rows; ++r)
+    {
+        FlashFwdArgs x = a[r];
+        const size_t b0 = static_cast<size_t>(r) * hpr, M = x.M, N = x.N, K = x.K, D = x.D;
+        x.Q = shifted(x.Q, b0 * K * M);
+        x.Kt = shifted(x.Kt, b0 * K * N);
+        x.V = shifted(x.V, b0 * N * D);
+        x.mask = shifted(x.mask, b0 * static_cast<size_t>(x.mask_bs));
+        x.m = shifted(x.m, b0 * M);
+        x.l = shifted(x.l, b0 * M);
+        x.O = shifted(x.O, b0 * M * D);
+        x.S = shifted(x.S, b0 * blocks_per_entry(M, N));
+        t.a[r] = x;
+        t.cls[r] = x.mask ? shifted(cells[r], b0 * cls_bs) : nullptr;
+    }
+    return t;
+}
+
+FlashBwdSet bwd_set(const FlashBwdArgs* a, const unsigned char* const* cells, int rows, size_t hpr, long cls_bs)
+{
+    FlashBwdSet t{};
+    t.hpr = static_cast<int>(hpr);
+    t.rows = rows;
+    for (int r = 0; r < rows; ++r)
+    {
+        FlashBwdArgs x = a[r];
+        const size_t b0 = static_cast<size_t>(r) * hpr, M = x.M, N = x.N, K = x.K, Kd = x.Kd;
+        x.Q = shifted(x.Q, b0 * K * M);
+        x.Kt = shifted(x.Kt, b0 * K * N);
+        x.dO = shifted(x.dO, b0 * Kd * M);
+        x.Vp = shifted(x.Vp, b0 * Kd * N);
+        x.G = shifted(x.G, b0 * M * static_cast<size_t>(x.ldg));
+        x.mask = shifted(x.mask, b0 * static_cast<size_t>(x.mask_bs));
+        x.m = shifted(x.m, b0 * M);
+        x.l = shifted(x.l, b0 * M);
+        x.R = shifted(x.R, b0 * M);
+        x.dQ = shifted(x.dQ, b0 * K * M);
+        x.dK = shifted(x.dK, b0 * K * N);
+        x.dV = shifted(x.dV, b0 * K * N);
+        x.dS = shifted(x.dS, b0 * M * N);
+        x.S = shifted(x.S, b0 * blocks_per_entry(M, N));
+        t.a[r] = x;
+        t.cls[r] = x.mask ? shifted(cells[r], b0 * cls_bs) : nullptr;
+    }
+    return t;
+}
+
+// Rows of one launch agree on every shape and layout the kernels take from row 0.
+bool same_launch(const FlashFwdArgs& x, const FlashFwdArgs& y)
+{
+    return x.M == y.M && x.N == y.N && x.K == y.K && x.D == y.D && !x.mask == !y.mask && x.mask_bs == y.mask_bs &&
+           x.v_dm == y.v_dm && x.o_dm == y.o_dm && !x.O == !y.O && !x.V == !y.V && !x.S == !y.S;
+}
+bool same_launch(const FlashBwdArgs& x, const FlashBwdArgs& y)
+{
+    return x.M == y.M && x.N == y.N && x.K == y.K && x.Kd == y.Kd && x.ldg == y.ldg && !x.mask == !y.mask &&
+           x.mask_bs == y.mask_bs && x.g_do == y.g_do && !x.G == !y.G && !x.S == !y.S && !x.R == !y.R;
+}
+
 // Builds g's order table at `at` (order_table_bytes(g, batch) bytes); `resident`:
 // workgroups of the kernel per CU.
-int build_order(const FlashGeo& g, size_t batch, bool rows, int resident, char* at, hipStream_t s)
+int build_order(const FlashGeo& g, const FlashCls& tab, size_t batch, bool rows, int resident, char* at,
+                hipStream_t s)
 {
     const size_t n = grid_of(g, batch);
     if (n == 0) return 0;
     int* order = reinterpret_cast<int*>(at);
     unsigned char* weight = reinterpret_cast<unsigned char*>(at + align256(n * sizeof(int)));
     const int ncu = device_cus();
-    hipLaunchKernelGGL(k_flash_order, dim3(1), dim3(kOrderThreads), 0, s, g, rows ? 1 : 0, static_cast<int>(n), ncu,
-                       resident * ncu, order, weight);
+    hipLaunchKernelGGL(k_flash_order, dim3(1), dim3(kOrderThreads), 0, s, g, tab, rows ? 1 : 0, static_cast<int>(n),
+                       ncu, resident * ncu, order, weight);
     return launch_status();
 }
 
@@ -1583,7 +1701,7 @@ int cols_pw(int KP) { return 64 * KP; }
 int dq_pw(int KP) { return 32 * KP; }
 
 template <int KP, int DP, bool WITH_O>
-int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g0, size_t batch, const int* order, hipStream_t s)
+int launch_fwd(const FlashFwdSet& t, const FlashGeo& g0, size_t batch, const int* order, hipStream_t s)
 {
     // Cells per step: one cell (3 workgroups per CU: 35 KB of LDS, <= 168
     // VGPRs) when a line range holds >= 32 cells, two (2 per CU) for shorter
@@ -1594,47 +1712,47 @@ int launch_fwd(const FlashFwdArgs& a, const FlashGeo& g0, size_t batch, const in
     const bool one = std::min(g0.R, g0.CT) >= 32;
     FlashGeo g = g0;
     g.order = order;
-    if (WITH_O && a.v_dm)
+    if (WITH_O && t.a[0].v_dm)
     {
-        if (one) hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true, 1>), grid, block, 0, s, a, g);
-        else hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true, 2>), grid, block, 0, s, a, g);
+        if (one) hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true, 1>), grid, block, 0, s, t, g);
+        else hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, true, 2>), grid, block, 0, s, t, g);
     }
     else
     {
-        if (one) hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, false, 1>), grid, block, 0, s, a, g);
-        else hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, false, 2>), grid, block, 0, s, a, g);
+        if (one) hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, false, 1>), grid, block, 0, s, t, g);
+        else hipLaunchKernelGGL((k_flash_fwd<KP, DP, WITH_O, false, 2>), grid, block, 0, s, t, g);
     }
     if (int rc = launch_status()) return rc;
     if (g.NR == 1) return 0;
     hipLaunchKernelGGL((k_flash_fwd_combine<DP, WITH_O>), dim3(static_cast<unsigned>(batch * g.RT)), dim3(256), 0, s,
-                       a, g);
+                       t, g);
     return launch_status();
 }
 
 template <int KP>
-int launch_bwd(const FlashBwdArgs& a, const FlashGeo& gr0, const FlashGeo& gc0, size_t batch,
+int launch_bwd(const FlashBwdSet& t, const FlashGeo& gr0, const FlashGeo& gc0, size_t batch,
                const int* order_rows, const int* order_cols, hipStream_t s)
 {
     FlashGeo gr = gr0, gc = gc0;
     gr.order = order_rows;
     gc.order = order_cols;
-    hipLaunchKernelGGL((k_flash_bwd_rows<KP>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, a, gr);
+    hipLaunchKernelGGL((k_flash_bwd_rows<KP>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, t, gr);
     if (int rc = launch_status()) return rc;
     if (gr.NR > 1)
     {
         hipLaunchKernelGGL((k_flash_bwd_rows_combine<KP>), dim3(static_cast<unsigned>(batch * gr.RT)), dim3(256), 0,
-                           s, a, gr);
+                           s, t, gr);
         if (int rc = launch_status()) return rc;
     }
-    if (a.g_do)
-        hipLaunchKernelGGL((k_flash_bwd_cols<KP, true, false>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a,
+    if (t.a[0].g_do)
+        hipLaunchKernelGGL((k_flash_bwd_cols<KP, true, false>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, t,
                            gc);
     else
-        hipLaunchKernelGGL((k_flash_bwd_cols<KP, false, false>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, a,
+        hipLaunchKernelGGL((k_flash_bwd_cols<KP, false, false>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s, t,
                            gc);
     if (int rc = launch_status()) return rc;
     if (gc.NR == 1) return 0;
-    hipLaunchKernelGGL((k_flash_bwd_cols_combine<KP>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(256), 0, s, a,
+    hipLaunchKernelGGL((k_flash_bwd_cols_combine<KP>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(256), 0, s, t,
                        gc);
     return launch_status();
 }
@@ -1685,35 +1803,58 @@ size_t flash_order_bytes(size_t batch, size_t M, size_t N, int kind)
     return order_table_bytes(gr, batch) + order_table_bytes(gc, batch);
 }
 
+int flash_build_rows_order(const unsigned char* const* cells, int rows, size_t hpr, size_t M, size_t N,
+                           bool per_batch_cls, int kind, void* out, hipStream_t s)
+{
+    if (rows < 1 || rows > kFlashMaxRows || hpr == 0) return -1;
+    for (int r = 0; r < rows; ++r)
+        if (!cells[r]) return -1;
+    const size_t batch = static_cast<size_t>(rows) * hpr;
+    char* at = static_cast<char*>(out);
+    const FlashGeo gr = geo(batch, M, N, true, 0, cells[0], nullptr, per_batch_cls);
+    const FlashGeo gc = geo(batch, M, N, false, 0, cells[0], nullptr, per_batch_cls);
+    const FlashCls tab = cls_table(cells, rows, hpr, gr.cls_bs);
+    if (kind == 0) return build_order(gr, tab, batch, true, std::min(gr.R, gr.CT) >= 32 ? 3 : 2, at, s);
+    if (kind == 1)
+    {
+        if (int rc = build_order(gr, tab, batch, true, 2, at, s)) return rc;
+        return build_order(gc, tab, batch, false, 2, at + order_table_bytes(gr, batch), s);
+    }
+    if (int rc = build_order(gc, tab, batch, false, 2, at, s)) return rc;
+    return build_order(gr, tab, batch, true, 3, at + order_table_bytes(gc, batch), s);
+}
+
 int flash_build_order(const unsigned char* cells, size_t batch, size_t M, size_t N, bool per_batch_cls, int kind,
                       void* out, hipStream_t s)
 {
-    char* at = static_cast<char*>(out);
-    const FlashGeo gr = geo(batch, M, N, true, 0, cells, nullptr, per_batch_cls);
-    const FlashGeo gc = geo(batch, M, N, false, 0, cells, nullptr, per_batch_cls);
-    if (kind == 0) return build_order(gr, batch, true, std::min(gr.R, gr.CT) >= 32 ? 3 : 2, at, s);
-    if (kind == 1)
-    {
-        if (int rc = build_order(gr, batch, true, 2, at, s)) return rc;
-        return build_order(gc, batch, false, 2, at + order_table_bytes(gr, batch), s);
-    }
-    if (int rc = build_order(gc, batch, false, 2, at, s)) return rc;
-    return build_order(gr, batch, true, 3, at + order_table_bytes(gc, batch), s);
+    return flash_build_rows_order(&cells, 1, batch, M, N, per_batch_cls, kind, out, s);
+}
+
+int flash_forward_rows(const FlashFwdArgs* a, const unsigned char* const* cells, int rows, size_t hpr, void* ws,
+                       const int* order, hipStream_t s)
+{
+    if (rows < 1 || rows > kFlashMaxRows || hpr == 0) return -1;
+    const FlashFwdArgs& a0 = a[0];
+    for (int r = 0; r < rows; ++r)
+        if (!same_launch(a0, a[r]) || (a[r].mask && !cells[r])) return -1;
+    const size_t batch = static_cast<size_t>(rows) * hpr;
+    const int KP = pad32(static_cast<size_t>(a0.K)), DP = a0.O ? pad32(static_cast<size_t>(a0.D)) : 32;
+    const FlashGeo g = geo(batch, static_cast<size_t>(a0.M), static_cast<size_t>(a0.N), true, fwd_pw(DP),
+                           a0.mask ? cells[0] : nullptr, ws, a0.mask && a0.mask_bs != 0);
+    if (g.NR > 1 && !ws) return -1;
+    const FlashFwdSet t = fwd_set(a, cells, rows, hpr, g.cls_bs);
+    const int* ow = a0.mask ? order : nullptr;
+    if (!a0.O)
+        return KP == 32 ? launch_fwd<32, 32, false>(t, g, batch, ow, s) : launch_fwd<64, 32, false>(t, g, batch, ow, s);
+    if (KP == 32)
+        return DP == 32 ? launch_fwd<32, 32, true>(t, g, batch, ow, s) : launch_fwd<32, 64, true>(t, g, batch, ow, s);
+    return DP == 32 ? launch_fwd<64, 32, true>(t, g, batch, ow, s) : launch_fwd<64, 64, true>(t, g, batch, ow, s);
 }
 
 int flash_forward(const FlashFwdArgs& a, const unsigned char* cells, size_t batch, void* ws, const int* order,
                   hipStream_t s)
 {
-    const int KP = pad32(static_cast<size_t>(a.K)), DP = a.O ? pad32(static_cast<size_t>(a.D)) : 32;
-    const FlashGeo g = geo(batch, static_cast<size_t>(a.M), static_cast<size_t>(a.N), true, fwd_pw(DP),
-                           a.mask ? cells : nullptr, ws, a.mask && a.mask_bs != 0);
-    if (g.NR > 1 && !ws) return -1;
-    const int* ow = a.mask ? order : nullptr;
-    if (!a.O)
-        return KP == 32 ? launch_fwd<32, 32, false>(a, g, batch, ow, s) : launch_fwd<64, 32, false>(a, g, batch, ow, s);
-    if (KP == 32)
-        return DP == 32 ? launch_fwd<32, 32, true>(a, g, batch, ow, s) : launch_fwd<32, 64, true>(a, g, batch, ow, s);
-    return DP == 32 ? launch_fwd<64, 32, true>(a, g, batch, ow, s) : launch_fwd<64, 64, true>(a, g, batch, ow, s);
+    return flash_forward_rows(&a, &cells, 1, batch, ws, order, s);
 }
 
 int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t batch, void* ws, const int* order,
@@ -1731,7 +1872,8 @@ int flash_backward(const FlashBwdArgs& a, const unsigned char* cells, size_t bat
     const int* occ = orr ? reinterpret_cast<const int*>(reinterpret_cast<const char*>(orr) +
                                                          order_table_bytes(gr, batch))
                          : nullptr;
-    return KP == 32 ? launch_bwd<32>(a, gr, gc, batch, orr, occ, s) : launch_bwd<64>(a, gr, gc, batch, orr, occ, s);
+    const FlashBwdSet t = bwd_set(&a, &cl, 1, batch, gr.cls_bs);
+    return KP == 32 ? launch_bwd<32>(t, gr, gc, batch, orr, occ, s) : launch_bwd<64>(t, gr, gc, batch, orr, occ, s);
 }
 
 size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K)
@@ -1742,58 +1884,80 @@ size_t flash_ds_workspace_bytes(size_t batch, size_t M, size_t N, size_t K)
     return align256(batch * M * N * sizeof(float)) + align256(batch * M * sizeof(float)) + part;
 }
 
-int flash_backward_ds(const FlashBwdArgs& a0, const float* O, int o_qm, const unsigned char* cells, size_t batch,
-                      void* ws, const int* order, hipStream_t s)
+int flash_backward_ds_rows(const FlashBwdArgs* a, const float* const* O, int o_qm, const unsigned char* const* cells,
+                           int rows, size_t hpr, void* ws, const int* order, hipStream_t s)
 {
-    if (!ws || a0.K != a0.Kd) return -1;
-    FlashBwdArgs a = a0;
+    if (!ws || rows < 1 || rows > kFlashMaxRows || hpr == 0) return -1;
+    for (int r = 0; r < rows; ++r)
+        if (!same_launch(a[0], a[r]) || a[r].K != a[r].Kd || !O[r] || (a[r].mask && !cells[r])) return -1;
+    const size_t batch = static_cast<size_t>(rows) * hpr;
+    const size_t M = static_cast<size_t>(a[0].M), N = static_cast<size_t>(a[0].N);
+    // Workspace: dS of every entry, R where the caller keeps none, then the range partials.
     char* w = static_cast<char*>(ws);
-    const size_t M = static_cast<size_t>(a.M), N = static_cast<size_t>(a.N);
-    a.dS = reinterpret_cast<float*>(w);
+    float* dS = reinterpret_cast<float*>(w);
     w += align256(batch * M * N * sizeof(float));
-    if (!a.R) a.R = reinterpret_cast<float*>(w);   // R kept in the workspace unless the caller wants it
+    float* Rw = reinterpret_cast<float*>(w);
     w += align256(batch * M * sizeof(float));
-    a.g_do = 1;
-    const int KP = pad32(static_cast<size_t>(a.K));
-    const unsigned char* cl = a.mask ? cells : nullptr;
-    const bool pb = a.mask && a.mask_bs != 0;
-    FlashGeo gr = geo(batch, M, N, true, dq_pw(KP), cl, w, pb);
-    FlashGeo gc = geo(batch, M, N, false, cols_pw(KP), cl, w, pb);
-    if (a.mask && order)
+    FlashBwdArgs x[kFlashMaxRows];
+    RowdotSet rd{};
+    for (int r = 0; r < rows; ++r)
+    {
+        const size_t b0 = static_cast<size_t>(r) * hpr;
+        x[r] = a[r];
+        x[r].dS = dS + b0 * M * N;
+        if (!x[r].R) x[r].R = Rw + b0 * M;
+        x[r].g_do = 1;
+        rd.dO[r] = x[r].dO;
+        rd.O[r] = O[r];
+        rd.R[r] = x[r].R;
+    }
+    const int KP = pad32(static_cast<size_t>(x[0].K));
+    const unsigned char* cl0 = x[0].mask ? cells[0] : nullptr;
+    const bool pb = x[0].mask && x[0].mask_bs != 0;
+    FlashGeo gr = geo(batch, M, N, true, dq_pw(KP), cl0, w, pb);
+    FlashGeo gc = geo(batch, M, N, false, cols_pw(KP), cl0, w, pb);
+    if (x[0].mask && order)
     {
         gc.order = order;
         gr.order = reinterpret_cast<const int*>(reinterpret_cast<const char*>(order) + order_table_bytes(gc, batch));
     }
-    const long total = static_cast<long>(batch * M);
-    hipLaunchKernelGGL(k_flash_rowdot, dim3(static_cast<unsigned>((total + 63) / 64)), dim3(256), 0, s, a.dO, O,
-                       a.R, a.M, a.Kd, total, a.alpha2, o_qm ? 1 : 0);
+    const FlashBwdSet t = bwd_set(x, cells, rows, hpr, gr.cls_bs);
+    const long total = static_cast<long>(hpr * M);
+    hipLaunchKernelGGL(k_flash_rowdot, dim3(static_cast<unsigned>((total + 63) / 64), static_cast<unsigned>(rows)),
+                       dim3(256), 0, s, rd, x[0].M, x[0].Kd, total, x[0].alpha2, o_qm ? 1 : 0);
     if (int rc = launch_status()) return rc;
     auto run = [&](auto kp) -> int {
         constexpr int P = decltype(kp)::value;
-        if (a.S)
+        if (x[0].S)
             hipLaunchKernelGGL((k_flash_bwd_cols<P, true, true, true>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0,
-                               s, a, gc);
+                               s, t, gc);
         else
             hipLaunchKernelGGL((k_flash_bwd_cols<P, true, true>), dim3(grid_of(gc, batch)), dim3(64 * kWaves), 0, s,
-                               a, gc);
+                               t, gc);
         if (int rc = launch_status()) return rc;
         if (gc.NR > 1)
         {
             hipLaunchKernelGGL((k_flash_bwd_cols_combine<P>), dim3(static_cast<unsigned>(batch * gc.CT)), dim3(256),
-                               0, s, a, gc);
+                               0, s, t, gc);
             if (int rc = launch_status()) return rc;
         }
-        hipLaunchKernelGGL((k_flash_bwd_dq<P>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, a, gr);
+        hipLaunchKernelGGL((k_flash_bwd_dq<P>), dim3(grid_of(gr, batch)), dim3(64 * kWaves), 0, s, t, gr);
         if (int rc = launch_status()) return rc;
         if (gr.NR > 1)
         {
             hipLaunchKernelGGL((k_flash_bwd_dq_combine<P>), dim3(static_cast<unsigned>(batch * gr.RT)), dim3(256),
-                               0, s, a, gr);
+                               0, s, t, gr);
             if (int rc = launch_status()) return rc;
         }
         return 0;
     };
     return KP == 32 ? run(std::integral_constant<int, 32>{}) : run(std::integral_constant<int, 64>{});
+}
+
+int flash_backward_ds(const FlashBwdArgs& a, const float* O, int o_qm, const unsigned char* cells, size_t batch,
+                      void* ws, const int* order, hipStream_t s)
+{
+    return flash_backward_ds_rows(&a, &O, o_qm, &cells, 1, batch, ws, order, s);
 }
 
 } // namespace nnhip
@@ -1953,4 +2117,62 @@ extern "C" int nnhip_flash_build_order(const void* cells, size_t batch, size_t M
     if (!nnhip::flash_supported(batch, M, N, 1, 4)) return -3;
     return nnhip::flash_build_order(static_cast<const unsigned char*>(cells), batch, M, N, mask_batch_stride != 0,
                                     kind, order, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_flash_forward_rows(const nnhip_flash_fwd_row* rows, size_t nrows, size_t hpr, size_t M, size_t N,
+                                        size_t K, size_t D, float alpha, int v_dim_major, int o_dim_major,
+                                        const void* order, void* workspace, void* stream)
+{
+    if (!rows || nrows == 0 || nrows > static_cast<size_t>(nnhip::kFlashMaxRows) || hpr == 0) return -1;
+    if (!nnhip::flash_supported(nrows * hpr, M, N, K, D)) return -3;
+    nnhip::FlashFwdArgs a[nnhip::kFlashMaxRows];
+    const unsigned char* cells[nnhip::kFlashMaxRows];
+    for (size_t r = 0; r < nrows; ++r)
+    {
+        const nnhip_flash_fwd_row& x = rows[r];
+        if (!x.Q || !x.Kt || !x.m || !x.l || (x.O && !x.V) || (x.mask && !x.cells)) return -1;
+        a[r] = nnhip::FlashFwdArgs{x.Q, x.Kt, x.V, x.mask, x.m, x.l, x.O, static_cast<int>(M), static_cast<int>(N),
+                                   static_cast<int>(K), static_cast<int>(x.O ? D : 4), alpha};
+        a[r].v_dm = v_dim_major ? 1 : 0;
+        a[r].o_dm = o_dim_major ? 1 : 0;
+        a[r].S = x.scores;
+        cells[r] = static_cast<const unsigned char*>(x.cells);
+    }
+    return nnhip::flash_forward_rows(a, cells, static_cast<int>(nrows), hpr, workspace, static_cast<const int*>(order),
+                                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_flash_backward_ds_rows(const nnhip_flash_bwd_row* rows, size_t nrows, size_t hpr, size_t M,
+                                            size_t N, size_t K, float alpha, float alpha2, int o_query_major,
+                                            const void* order, void* workspace, void* stream)
+{
+    if (!rows || nrows == 0 || nrows > static_cast<size_t>(nnhip::kFlashMaxRows) || hpr == 0 || !workspace) return -1;
+    if (!nnhip::flash_supported(nrows * hpr, M, N, K, 4) || K % 4 != 0) return -3;
+    nnhip::FlashBwdArgs a[nnhip::kFlashMaxRows];
+    const float* O[nnhip::kFlashMaxRows];
+    const unsigned char* cells[nnhip::kFlashMaxRows];
+    for (size_t r = 0; r < nrows; ++r)
+    {
+        const nnhip_flash_bwd_row& x = rows[r];
+        if (!x.Q || !x.Kt || !x.dO || !x.Vp || !x.O || !x.m || !x.l || !x.dQ || !x.dK || !x.dV || (x.mask && !x.cells))
+            return -1;
+        a[r] = nnhip::FlashBwdArgs{x.Q, x.Kt, x.dO, x.Vp, nullptr, x.mask, x.m, x.l, x.R, x.dQ, x.dK, x.dV,
+                                   static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), static_cast<int>(K),
+                                   static_cast<int>(K), alpha, alpha2};
+        a[r].S = x.scores;
+        O[r] = x.O;
+        cells[r] = static_cast<const unsigned char*>(x.cells);
+    }
+    return nnhip::flash_backward_ds_rows(a, O, o_query_major, cells, static_cast<int>(nrows), hpr, workspace,
+                                         static_cast<const int*>(order), static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_flash_build_rows_order(const void* const* cells, size_t nrows, size_t hpr, size_t M, size_t N,
+                                            int kind, void* order, void* stream)
+{
+    if (!cells || !order || kind < 0 || kind > 2 || nrows == 0 || nrows > static_cast<size_t>(nnhip::kFlashMaxRows))
+        return -1;
+    if (!nnhip::flash_supported(nrows * hpr, M, N, 1, 4)) return -3;
+    return nnhip::flash_build_rows_order(reinterpret_cast<const unsigned char* const*>(cells), static_cast<int>(nrows),
+                                         hpr, M, N, false, kind, order, static_cast<hipStream_t>(stream));
 }

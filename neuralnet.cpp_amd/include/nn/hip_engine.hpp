@@ -149,6 +149,12 @@ public:
     // Same, plus one record per launch: {M, N, K, batch, transA, transB, ms}.
     Result<void> read_gemm_profile_records(std::vector<double>& records);
 
+    // Bytes of attention score blocks that the two-pass chain's recorded
+    // forward outputs may hold for their backward (default: 1/8 of the device
+    // memory free at start-up, at most 8 GiB). 0 keeps none: every backward
+    // then forms its scores again.
+    void set_score_budget(std::size_t bytes) noexcept { score_budget_ = bytes; }
+
 private:
     Result<Tensor> alloc_(std::size_t rows, std::size_t cols);
     // Row slices are views of their source's memory until the view or the
@@ -183,6 +189,31 @@ private:
         std::vector<OrderTable> orders;   // work orders of the launches over this table
     };
     std::vector<CellTable> cells_;
+    // Work orders of multi-row launches, keyed by the rows' cell tables (kept
+    // alive here, so a key never names a reused buffer), most recent last.
+    struct RowsOrder
+    {
+        std::vector<std::shared_ptr<DeviceBuffer>> cells;
+        std::size_t hpr, M, N;
+        int kind;
+        std::shared_ptr<DeviceBuffer> buf;
+    };
+    std::vector<RowsOrder> rows_orders_;
+    Result<std::shared_ptr<DeviceBuffer>> mask_cells_buf_(const Tensor* mask, std::size_t M, std::size_t N);
+    Result<const void*> rows_order_(const std::vector<std::shared_ptr<DeviceBuffer>>& cells, std::size_t hpr,
+                                    std::size_t M, std::size_t N, int kind);
+    // Fused two-pass attention launches (softmax_apply's forward; backward_kv's
+    // backward from the forward's output) recorded instead of launched. On
+    // demand all of them run: the forwards first, then the backwards, calls of
+    // one kind and shape (e.g. the packed rows of a document-masked batch, one
+    // call per row) together as multi-row launches.
+    struct PendingFlash;
+    std::vector<PendingFlash> pflash_;
+    bool flash_yields_(const float* p) const;
+    bool flash_uses_(const float* p) const;
+    Result<void> settle_flash_();
+    Result<void> launch_flash_(const std::vector<const PendingFlash*>& rows);
+    std::size_t score_budget_ = 0;
     std::vector<std::weak_ptr<DeviceBuffer>> views_;   // live row-slice views (HipView)
     // Every live aliased view and its root (may also hold buffers no longer
     // in that role): a write to any other buffer needs no unsharing.
@@ -265,7 +296,9 @@ private:
     // (yields or reads) them; the plain forms also launch the elementwise run.
     Result<void> settle_reads_(std::initializer_list<const Tensor*> ts);
     Result<void> settle_write_(const Tensor& t);
-    Result<void> settle_chain_reads_(std::initializer_list<const Tensor*> ts);
+    // keep_flash: recorded fused attention launches stay recorded even if they
+    // yield one of the tensors (the caller records work that runs after them).
+    Result<void> settle_chain_reads_(std::initializer_list<const Tensor*> ts, bool keep_flash = false);
     Result<void> settle_chain_write_(const Tensor& t, bool keep_swb = false);   // keep_swb: placed SwiGLU records stay
     Result<void> ew_push_(unsigned code, unsigned op, bool first, const Tensor& dst, const Tensor& a, const Tensor* b,
                           float s);

@@ -219,6 +219,13 @@ class Engine:
             fn.argtypes = [ctypes.c_void_p]
             self._check(fn(self._e))
 
+    def set_score_budget(self, nbytes: int) -> None:
+        """Bytes of attention score blocks the two-pass chain may keep from forward to backward
+        (HIP engine only; 0: every backward forms its scores again)."""
+        fn = self._lib.nnhip_engine_set_score_budget
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+        self._check(fn(self._e, nbytes))
+
     def tensor(self, a) -> Tensor:
         a = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
         if a.ndim == 1:

@@ -46,7 +46,8 @@ def test_oracle_mirrors_engine_abi():
     lib = ctypes.CDLL(ORACLE_LIB)
     names = [n for n in _declared(os.path.join(ROOT, "include", "nnhip_engine.h"))
              if not n.startswith("nnhip_engine_profile")
-             and n not in ("nnhip_engine_stream", "nnhip_engine_settle", "nnhip_engine_select")]
+             and n not in ("nnhip_engine_stream", "nnhip_engine_settle", "nnhip_engine_select",
+                           "nnhip_engine_set_score_budget")]
     missing = [n for n in names if not hasattr(lib, "nnoracle_" + n[len("nnhip_"):])]
     assert not missing, f"oracle lacks the mirror of {missing}"
 
