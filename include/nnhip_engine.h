@@ -105,6 +105,18 @@ int nnhip_engine_eval_expr(nnhip_engine* e, const uint8_t* instrs, size_t n_inst
                            uint32_t num_regs, nnhip_tensor* const* inputs, size_t n_inputs, size_t rows, size_t cols,
                            int vector_out, nnhip_tensor** out);
 
+/* The ExprSpec programs the GPT layers issue (include/nn/layer_exprs.hpp; reference compute_layer.hpp
+ * RMSNorm :733-795, SwiGLU backward :436-444, Softmax :840-860, RoPE :884-984), which HipEngine recognises
+ * structurally and runs as fused kernels, serialised as nnhip_engine_eval_expr takes them, so a host that
+ * builds the same programs can check that its copies match. name: rms_sum_sq, rms_normalize, rms_scale,
+ * rms_bwd_colsum, rms_bwd_dx, rms_bwd_rowsum, softmax_rows, softmax_rows_backward, swiglu_grad_gate,
+ * swiglu_grad_up, rope_forward, rope_backward (param: d_k). Capacities: instrs 8*64 bytes, view_kinds 2*8,
+ * view_params 8, consts 16, slot_args 8; slot_args[i] is the builder argument input slot i reads.
+ * Host-only. */
+int nnhip_layer_program(const char* name, uint32_t param, uint8_t* instrs, size_t* n_instrs, uint8_t* view_kinds,
+                        uint32_t* view_params, size_t* n_views, float* consts, size_t* n_consts, uint32_t* num_regs,
+                        int32_t* slot_args, size_t* n_slots);
+
 /* build_attention_mask (compute_layer.hpp:2081-2128): writes the (batch*heads*seq, seq) mask.
  * slopes: heads floats when alibi != 0; doc_ids: batch*seq ids or n_doc = 0. Host-only, no device use. */
 int nnhip_build_attention_mask(size_t batch, size_t seq, size_t heads, int alibi, const float* slopes,

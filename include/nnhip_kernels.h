@@ -51,8 +51,8 @@ int nnhip_gemm_heads(const float* W, const float* X, const float* row_bias, floa
                      size_t T, void* stream);
 
 /* Up to three such products of one X in one launch (the q, k and v projections): out[i] as
- * nnhip_gemm_heads(W[i], X, row_bias ? row_bias[i] : NULL, out[i], ...); count in 1..3, row_bias may be NULL
- * (no bias) or hold NULL entries. No CUDA counterpart. */
+ * nnhip_gemm_heads(W[i], X, row_bias ? row_bias[i] : NULL, out[i], ...); count in 1..3, count * B <= 65535,
+ * row_bias may be NULL (no bias) or hold NULL entries. No CUDA counterpart. */
 int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* const* row_bias, float* const* out,
                            size_t count, size_t M, size_t K, size_t B, size_t T, void* stream);
 

@@ -1826,8 +1826,9 @@ Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size
             r->heads = Tensor();
             return out;
         }
+        // A launch covers members x B sequences in grid z (at most 65535).
         auto fits = [&](const PendingMm& q) {
-            return !q.folded && !q.tA && !q.tB && q.M == M && q.N == B * N && q.K < 1024 &&
+            return !q.folded && !q.tA && !q.tB && q.M == M && q.N == B * N && q.K < 1024 && B <= 65535 &&
                    aligned16(q.A.dev_ptr()) && (!q.bias.size() || aligned16(q.bias.dev_ptr()));
         };
         if (r && fits(*r) && x.rows() == M)
@@ -1835,7 +1836,8 @@ Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size
             // The other recorded products of the same input (k and v after q) join the launch.
             std::vector<PendingMm*> grp{r};
             auto join = [&](PendingMm* q) {
-                if (q != r && grp.size() < 3 && fits(*q) && same_t(q->B, r->B) && q->K == r->K && live(q->C))
+                if (q != r && grp.size() < 3 && (grp.size() + 1) * B <= 65535 && fits(*q) && same_t(q->B, r->B) &&
+                    q->K == r->K && live(q->C))
                     grp.push_back(q);
             };
             for (auto& q : pmm_prev_) join(q.get());

@@ -906,7 +906,9 @@ extern "C" int nnhip_gemm_heads_group(const float* const* W, const float* X, con
                                       float* const* out, size_t count, size_t M, size_t K, size_t B, size_t T,
                                       void* stream)
 {
-    if (!W || !X || !out || count == 0 || count > 3 || B == 0 || T == 0 || M == 0 || K == 0 || B > 21845) return -1;
+    // grid z runs over count * B (member, sequence) pairs
+    if (!W || !X || !out || count == 0 || count > 3 || B == 0 || T == 0 || M == 0 || K == 0 || count * B > 65535)
+        return -1;
     GemmGroup g{};
     g.nb = static_cast<int>(B);
     for (size_t i = 0; i < count; ++i)

@@ -6,6 +6,7 @@
 #include <cstring>
 #include <iterator>
 #include <memory>
+#include <optional>
 #include <string>
 #include <vector>
 
@@ -13,6 +14,7 @@
 #include "compute_loss.hpp"
 #include "compute_optimizer.hpp"
 #include "model_file.hpp"
+#include "layer_exprs.hpp"
 #include "model.hpp"
 
 namespace nn::capi
@@ -648,6 +650,61 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
     return 0;
 }
 
+// The programs of layer_exprs.hpp by name (param: RoPE's head dim d_k),
+// serialised as eval_expr takes them, with the argument each input slot reads
+// (its position in the C++ builder's parameter list). Hosts that build the
+// same programs check theirs against these.
+inline int layer_program(const char* name, std::uint32_t param, std::uint8_t* instrs, std::size_t* n_instrs,
+                         std::uint8_t* vk, std::uint32_t* vp, std::size_t* n_views, float* consts,
+                         std::size_t* n_consts, std::uint32_t* num_regs, std::int32_t* slot_args, std::size_t* n_slots)
+{
+    namespace le = layer_exprs;
+    if (!name || !instrs || !n_instrs || !vk || !vp || !n_views || !consts || !n_consts || !num_regs || !slot_args ||
+        !n_slots)
+        return set_error("layer_program: null argument");
+    std::vector<Tensor> a;   // argument i is a placeholder with i + 1 rows
+    for (std::size_t i = 0; i < 6; ++i) a.push_back(Tensor::cpu(i + 1, 1));
+    const std::string n(name);
+    std::optional<std::pair<ExprSpec, std::vector<Tensor>>> r;
+    auto take = [&r](const auto& e) { r = dsl::to_expr_spec(e); };
+    if (n == "rms_sum_sq") take(le::rms_sum_sq(a[0]));
+    else if (n == "rms_normalize") take(le::rms_normalize(a[0], a[1]));
+    else if (n == "rms_scale") take(le::rms_scale(a[0], a[1]));
+    else if (n == "rms_bwd_colsum") take(le::rms_bwd_colsum(a[0], a[1], a[2]));
+    else if (n == "rms_bwd_dx") take(le::rms_bwd_dx(a[0], a[1], a[2], a[3], a[4]));
+    else if (n == "rms_bwd_rowsum") take(le::rms_bwd_rowsum(a[0], a[1], a[2]));
+    else if (n == "softmax_rows") take(le::softmax_rows(a[0]));
+    else if (n == "softmax_rows_backward") take(le::softmax_rows_backward(a[0], a[1]));
+    else if (n == "swiglu_grad_gate") take(le::swiglu_grad_gate(a[0], a[1], a[2], a[3]));
+    else if (n == "swiglu_grad_up") take(le::swiglu_grad_up(a[0], a[1], a[2]));
+    else if (n == "rope_forward") take(le::rope_forward(a[0], a[1], a[2], param));
+    else if (n == "rope_backward") take(le::rope_backward(a[0], a[1], a[2], param));
+    if (!r) return set_error("layer_program: unknown program " + n);
+    const ExprSpec& sp = r->first;
+    if (sp.instrs.size() > EXPR_MAX_INSTRS || sp.views.size() > EXPR_MAX_INPUTS || sp.consts.size() > EXPR_MAX_CONSTS)
+        return set_error("layer_program: program exceeds the ExprSpec limits");
+    for (std::size_t i = 0; i < sp.instrs.size(); ++i)
+    {
+        const ExprInstr& in = sp.instrs[i];
+        const std::uint8_t b[8] = {in.op, in.dst, in.a.kind, in.a.idx, in.b.kind, in.b.idx, in.c.kind, in.c.idx};
+        std::memcpy(instrs + 8 * i, b, 8);
+    }
+    for (std::size_t i = 0; i < sp.views.size(); ++i)
+    {
+        vk[2 * i] = sp.views[i].kind;
+        vk[2 * i + 1] = sp.views[i].negate_first_half;
+        vp[i] = sp.views[i].param;
+    }
+    for (std::size_t i = 0; i < sp.consts.size(); ++i) consts[i] = sp.consts[i];
+    for (std::size_t i = 0; i < r->second.size(); ++i) slot_args[i] = static_cast<std::int32_t>(r->second[i].rows()) - 1;
+    *n_instrs = sp.instrs.size();
+    *n_views = sp.views.size();
+    *n_consts = sp.consts.size();
+    *num_regs = sp.num_regs;
+    *n_slots = r->second.size();
+    return 0;
+}
+
 } // namespace nn::capi
 
 // Defines every symbol of include/nnhip_engine.h with the given prefix.
@@ -766,6 +823,12 @@ inline int attention_mask(std::size_t batch, std::size_t seq, std::size_t heads,
     int NN_CAPI_CAT(P, gpt_backward)(void* g) { return nn::capi::gpt_backward(static_cast<nn::capi::GptSession*>(g)); } \
     int NN_CAPI_CAT(P, gpt_optimizer_step)(void* g) { return nn::capi::gpt_step(static_cast<nn::capi::GptSession*>(g)); } \
     int NN_CAPI_CAT(P, gpt_zero_grad)(void* g) { return nn::capi::gpt_zero_grad(static_cast<nn::capi::GptSession*>(g)); } \
+    int NN_CAPI_CAT(P, layer_program)(const char* name, uint32_t param, uint8_t* ins, size_t* ni, uint8_t* vk,     \
+                                      uint32_t* vp, size_t* nv, float* cs, size_t* nc, uint32_t* nr,               \
+                                      int32_t* slot_args, size_t* ns)                                               \
+    {                                                                                                               \
+        return nn::capi::layer_program(name, param, ins, ni, vk, vp, nv, cs, nc, nr, slot_args, ns);              \
+    }                                                                                                               \
     int NN_CAPI_CAT(P, build_attention_mask)(size_t batch, size_t seq, size_t heads, int alibi, const float* slopes, \
                                              const uint64_t* doc_ids, size_t n_doc, float* out)                     \
     {                                                                                                               \

@@ -8,7 +8,11 @@ interpreter handles any other program and the shapes the fused kernels do
 not take.
 
 Each builder returns (spec, slots): `slots` names, per input slot, which
-argument the caller passes there.
+argument the caller passes there. ARGS lists each builder's arguments in the
+parameter order of its C++ counterpart in include/nn/layer_exprs.hpp, whose
+serialised programs the library exports (nnhip_layer_program): the tests
+check that every program here equals the engine's, instruction for
+instruction, so the fused-kernel tests cannot drift onto the interpreter.
 """
 from nnengine import ExprSpec, cst, inp, red, reg
 
@@ -128,6 +132,23 @@ def rope_tables(dk, T):
     c = np.concatenate([np.cos(ang)] * 2).astype(np.float32)
     sn = np.concatenate([np.sin(ang)] * 2).astype(np.float32)
     return c, sn
+
+
+# C++ name (include/nn/layer_exprs.hpp) and argument order of each builder.
+ARGS = {
+    "rms_sum_sq": ("rms_sum_sq", ("x",)),
+    "rms_normalize": ("rms_normalize", ("x", "rinv")),
+    "rms_scale": ("rms_scale", ("normed", "gamma")),
+    "rms_bwd_colsum": ("rms_bwd_colsum", ("g", "gamma", "normed")),
+    "rms_bwd_rowsum": ("rms_bwd_rowsum", ("g", "gamma", "normed")),
+    "rms_bwd_dx": ("rms_bwd_dx", ("g", "gamma", "m", "normed", "rinv")),
+    "swiglu_grad_gate": ("swiglu_grad_gate", ("g", "up", "s", "gate")),
+    "swiglu_grad_up": ("swiglu_grad_up", ("g", "gate", "s")),
+    "softmax_rows": ("softmax_rows", ("x",)),
+    "softmax_rows_backward": ("softmax_rows_backward", ("y", "g")),
+    "rope": ("rope_forward", ("q", "cos", "sin")),
+    "rope_backward": ("rope_backward", ("q", "cos", "sin")),
+}
 
 
 # (builder, reduced-vector output, closed form over float64 numpy arrays)

@@ -373,6 +373,31 @@ class Engine:
             pass
 
 
+def layer_program(lib: ctypes.CDLL, name: str, param: int = 0, prefix: str = "nnhip_") -> dict:
+    """A program of include/nn/layer_exprs.hpp as the library builds it (nnhip_layer_program):
+    instrs (8-tuples), views ((kind, negate, param)), consts, num_regs and slot_args (the C++
+    builder's argument each input slot reads)."""
+    fn = getattr(lib, prefix + "layer_program")
+    sz = ctypes.POINTER(ctypes.c_size_t)
+    fn.argtypes = [ctypes.c_char_p, ctypes.c_uint32, ctypes.c_void_p, sz, ctypes.c_void_p, ctypes.c_void_p, sz,
+                   ctypes.c_void_p, sz, ctypes.POINTER(ctypes.c_uint32), ctypes.c_void_p, sz]
+    ins = np.zeros((64, 8), np.uint8)
+    vk, vp = np.zeros(16, np.uint8), np.zeros(8, np.uint32)
+    cs, sa = np.zeros(16, np.float32), np.zeros(8, np.int32)
+    ni, nv, nc, ns = (ctypes.c_size_t() for _ in range(4))
+    nr = ctypes.c_uint32()
+    rc = fn(name.encode(), param, ins.ctypes.data, ctypes.byref(ni), vk.ctypes.data, vp.ctypes.data,
+            ctypes.byref(nv), cs.ctypes.data, ctypes.byref(nc), ctypes.byref(nr), sa.ctypes.data, ctypes.byref(ns))
+    if rc != 0:
+        err = getattr(lib, prefix + "last_error")
+        err.restype = ctypes.c_char_p
+        raise EngineError(err().decode())
+    return dict(instrs=[tuple(int(x) for x in r) for r in ins[:ni.value]],
+                views=[(int(vk[2 * i]), int(vk[2 * i + 1]), int(vp[i])) for i in range(nv.value)],
+                consts=[float(c) for c in cs[:nc.value]], num_regs=int(nr.value),
+                slot_args=[int(x) for x in sa[:ns.value]])
+
+
 # ExprSpec codes (expr_spec.hpp:30-62, 94-101, 116-159).
 EXPR_OP = dict(Neg=0, Exp=1, Log=2, Sqrt=3, Rsqrt=4, Abs=5, Tanh=6, Add=7, Sub=8, Mul=9, Div=10, Max=11, Min=12,
                Lt=13, Le=14, Gt=15, Ge=16, Eq=17, Ne=18, Select=19, ColSum=20, ColMax=21, RowSum=22, RowMax=23)
