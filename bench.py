@@ -540,10 +540,13 @@ def cpu_leg(seed, steps=3, warmup=1):
                 tflops=step_flops(CFG, 1) / mean / 1e12, min_s=best, mean_s=mean, host=host_info(threads))
 
 
-def cpu_legs_other(seed, iters=5):
-    """CPU legs of configs 2, 3 and 5 on the oracle, compute_bench's method: one warmup, then `iters`
-    timed calls (config 5: one packed row, timed once), min and mean. The fused attention primitives
-    are serial loops in the reference and in the oracle."""
+def cpu_legs_other(seed, iters=3, c2_heads=128, c5_heads=12, c5_iters=1):
+    """CPU legs of configs 2, 3 and 5 on the oracle, compute_bench's method (src/compute_bench.cpp:36-61):
+    one warmup, then timed calls, min and mean. The fused attention primitives are serial loops in the
+    reference and in the oracle, so their legs may run on a sample of the heads (c2_heads of config 2's
+    128 (batch x head) entries, c5_heads of a config-5 row's 12 heads); each head's work is the same, so
+    TFLOP/s carry over and the full call's time is the sample's scaled by the head count. Config 3 runs
+    its six GEMMs at full size."""
     eng, lib = _oracle(_cpu_threads())
     rng = np.random.default_rng(seed)
     out = {"host": host_info(int(lib.nnoracle_thread_count()))}
@@ -557,7 +560,7 @@ def cpu_legs_other(seed, iters=5):
             ts.append(time.perf_counter() - t0)
         return min(ts), sum(ts) / len(ts)
 
-    BH, T, d = 128, 512, 64
+    BH, T, d = c2_heads, 512, 64
     q, k = (eng.tensor(rng.standard_normal((BH * d, T), dtype=np.float32)) for _ in range(2))
     vt = eng.tensor(rng.standard_normal((BH * T, d), dtype=np.float32))
     mask = eng.tensor(eng.build_attention_mask(1, T, 1, False))
@@ -566,10 +569,13 @@ def cpu_legs_other(seed, iters=5):
         m = eng.batched_matmul_reduce(q, k, BH, "Max", True, False, 0.125, True, mask)
         lsum = eng.batched_matmul_softmax_denom(q, k, m, BH, True, False, 0.125, mask)
         return eng.batched_matmul_softmax_apply(q, k, vt, m, lsum, BH, True, False, 0.125, mask)
-    best, mean = bench(c2, 1)
+    best, mean = bench(c2, iters)
     flop = 4 * d * (T * (T + 1) // 2) * BH
-    out["config2_causal_forward"] = {"min_s": best, "mean_s": mean, "tflops": flop / mean / 1e12,
-                                     "iterations": 1, "warmup": 1}
+    out["config2_causal_forward"] = {
+        "tflops": flop / mean / 1e12, "min_s": best, "mean_s": mean, "full_call_s": mean * 128 / BH,
+        "iterations": iters, "warmup": 1,
+        "sample": f"{BH} of the 128 (batch x head) entries, T 512, d 64, causal: reduce + denom + apply"}
+    print(f"[bench] cpu config 2: {flop / mean / 1e12 * 1e3:.2f} GFLOP/s", file=sys.stderr, flush=True)
     del q, k, vt, mask
     sweep = []
     for name, M, K, N, tA, tB in GEMM_SWEEP[:6]:
@@ -577,10 +583,11 @@ def cpu_legs_other(seed, iters=5):
         b = eng.tensor(rng.uniform(-1, 1, (K, N)).astype(np.float32))
         best, mean = bench(lambda: eng.matmul(a, b), iters)
         fl = 2.0 * M * N * K
-        sweep.append({"shape": name, "min_s": best, "mean_s": mean, "gflops": fl / mean / 1e9, "iterations": iters})
+        sweep.append({"shape": name, "min_s": best, "mean_s": mean, "gflops": fl / mean / 1e9, "iterations": iters,
+                      "warmup": 1})
         print(f"[bench] cpu {name}: {fl / mean / 1e9:.1f} GFLOP/s", file=sys.stderr, flush=True)
     out["config3_gemm"] = sweep
-    H, T = 12, 2048
+    H, T = c5_heads, 2048
     lens, tot = [], 0
     while tot < T:
         L = min(int(rng.integers(64, 1025)), T - tot)
@@ -592,18 +599,38 @@ def cpu_legs_other(seed, iters=5):
     q, k, v, g = (eng.tensor(rng.standard_normal((H * d, T), dtype=np.float32)) for _ in range(4))
 
     def c5():
+        # the GPU leg's call sequence for one packed row (compute_layer.hpp:1196-1221, :1304-1327)
         m = eng.batched_matmul_reduce(q, k, H, "Max", True, False, 0.125, True, mk)
         lsum = eng.batched_matmul_softmax_denom(q, k, m, H, True, False, 0.125, mk)
+        vt5 = eng.rearrange_3d(eng.transpose(v), T, H, d)
+        o = eng.batched_matmul_softmax_apply(q, k, vt5, m, lsum, H, True, False, 0.125, mk)
         P = eng.batched_matmul(g, v, H, True, False)
         G = eng.rearrange_3d(eng.transpose(g), T, H, d)
         dq, r = eng.batched_matmul_softmax_backward_q(q, k, P, m, lsum, H, True, False, 0.125, mk)
-        return eng.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, lsum, H, True, False, 0.125, mk)
-    t0 = time.perf_counter()
-    c5()
-    dt = time.perf_counter() - t0
+        return o, dq, eng.batched_matmul_softmax_backward_kv(q, k, P, G, r, m, lsum, H, True, False, 0.125, mk)
+    best, mean = bench(c5, c5_iters)
     flop = 12 * d * pairs * H
-    out["config5_one_row_forward_backward"] = {"s": dt, "tflops": flop / dt / 1e12, "iterations": 1, "warmup": 0,
-                                               "allowed_pair_fraction": pairs / (T * T)}
+    out["config5_row_forward_backward"] = {
+        "tflops": flop / mean / 1e12, "min_s": best, "mean_s": mean, "full_row_s": mean * 12 / H,
+        "iterations": c5_iters, "warmup": 1, "allowed_pair_fraction": pairs / (T * T),
+        "sample": f"{H} of the 12 heads of one packed row (of 8), T 2048, d 64, documents U{{64..1024}}: "
+                  f"forward (reduce, denom, apply) + dP + backward_q + backward_kv"}
+    print(f"[bench] cpu config 5: {flop / mean / 1e12 * 1e3:.2f} GFLOP/s", file=sys.stderr, flush=True)
+    return out
+
+
+def cpu_configs_beside_gpu(cpu, attn, sweep):
+    """Per-config CPU figures (cpu_legs_other) next to the GPU figures of the same run."""
+    out = {"host": cpu["host"]}
+    if attn:
+        for key, gkey in (("config2_causal_forward", "causal_config2_forward"),
+                          ("config5_row_forward_backward", "doc_masked_config5_forward_backward")):
+            c, gt = cpu[key], attn[gkey]["tflops"]
+            out[key] = dict(c, gpu_tflops=gt, gpu_over_cpu=gt / c["tflops"])
+    gpu_by_shape = {r["shape"]: r["tflops"] for r in (sweep or [])}
+    out["config3_gemm"] = [dict(r, gpu_gflops=gpu_by_shape[r["shape"]] * 1e3,
+                                gpu_over_cpu=gpu_by_shape[r["shape"]] * 1e3 / r["gflops"])
+                           if r["shape"] in gpu_by_shape else r for r in cpu["config3_gemm"]]
     return out
 
 
@@ -706,6 +733,9 @@ def main():
         cpu = cpu_leg(args.seed)
         out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "tflops", "min_s",
                                                    "mean_s", "host")}
+        # configs 2, 3 and 5 on the same host in the same run, bounded samples (about 20 s)
+        others = cpu_legs_other(args.seed, iters=3, c2_heads=16, c5_heads=2, c5_iters=1)
+        out["cpu_baseline"]["configs"] = cpu_configs_beside_gpu(others, attn, sweep)
     print(json.dumps(out), flush=True)
 
 

@@ -4,7 +4,9 @@
   3072, RMSNorm, ALiBi, vocab 32000, context 1024) at batch 1 of 8, the same
   seeded weights and tokens on the HIP engine and on the CPU oracle: loss,
   logits, every parameter gradient and the AdamW-updated weights (reference
-  text_train.cpp:1181-1330 step; tolerances as in the small GPT tests).
+  text_train.cpp:1181-1330 step; tolerances as in the small GPT tests); and at
+  the full batch of 8, whose loss and gradients are the means of the 8
+  batch-1 rows' (rows are independent).
 * Config 3: the six GEMM sweep shapes NN, plus the GPT projection shapes in the
   reference's Linear orientation (W (out, in) times X (in, tokens)) and its two
   backward variants (TN for dX, NT for dW), against float64 with the a-priori
@@ -76,6 +78,45 @@ def test_config4_full_model_batch1(hip, cpu):
     flips = check_adam_params(h[3], c[3], c[2], lr=1e-3, got_grads=h[2], params0=params)
     print(f"[c4] grad max err {max(errs):.2e}, AdamW sign flips {flips} of {sum(p.size for p in params)}",
           flush=True)
+
+
+def test_config4_full_batch8_is_mean_of_rows(hip):
+    """Config 4 at its full batch of 8 (the step bench.py times: K = 8192 split-K weight gradients
+    with accumulate epilogues, B = 8 head layouts, per-sequence ALiBi masks). Rows are independent
+    (causal attention within a sequence; every other layer acts per token) and the loss is the mean
+    over all B*T tokens, so the batch-8 loss is the mean of the 8 batch-1 losses and every batch-8
+    gradient the mean of the per-row gradients; each batch-1 row is the path checked against the
+    oracle above. Loss relative 1e-5, gradients normwise 1e-3 per tensor."""
+    print("[c4b8] 12L d768 H12 ff3072 ALiBi V32000 T1024 B8 vs 8 x B1, seed 48", flush=True)
+    rng = np.random.default_rng(48)
+    T, B = C4["seq_len"], 8
+    g8 = hip.gpt(**C4)
+    params = _c4_params(g8.param_shapes(), C4, rng)
+    toks = rng.integers(0, C4["vocab_size"], size=(T + 1, B))
+    g8.set_params(params)
+    g8.load_batch(toks[:T].astype(np.float32), toks[1:].T.reshape(-1))
+    loss8 = g8.forward_loss()
+    g8.backward()
+    grads8 = g8.grads()
+    g8.close()
+    g1 = hip.gpt(**C4)
+    g1.set_params(params)
+    losses, mean_grads = [], None
+    for b in range(B):
+        g1.zero_grad()
+        g1.load_batch(toks[:T, b:b + 1].astype(np.float32), toks[1:, b])
+        losses.append(g1.forward_loss())
+        g1.backward()
+        gr = g1.grads()
+        mean_grads = [x.astype(np.float64) / B for x in gr] if mean_grads is None else \
+            [m + x.astype(np.float64) / B for m, x in zip(mean_grads, gr)]
+    g1.close()
+    ref = float(np.mean(np.float64(losses)))
+    print(f"[c4b8] batch-8 loss {loss8:.6f}, mean of rows {ref:.6f}", flush=True)
+    assert abs(loss8 - ref) <= 1e-5 * abs(ref), (loss8, ref)
+    errs = grad_errs(grads8, mean_grads)
+    print(f"[c4b8] gradient max err {max(errs):.2e}", flush=True)
+    assert max(errs) <= 1e-3, max(errs)
 
 
 def _check_gemm(hip, A, B, tA, tB):
