@@ -371,7 +371,9 @@ int nnhip_row_softmax_backward(const float* Y, const float* G, float* out, size_
  *   RMSNorm backward, compute_layer.hpp:772-795:  bwd_colsum  out[c] = sum_r G*gamma[r]*Nrm;
  *     bwd_dx  out = (G*gamma[r] - m[c]*Nrm) * rinv[c];  bwd_rowsum  out[r] = sum_c G*gamma[r]*Nrm.
  *   SwiGLU backward, compute_layer.hpp:436-444 (count % 4 == 0):
- *     grad_gate = G*up*(s*(1 + gate*(1 - s)));  grad_up = G*gate*s. */
+ *     grad_gate = G*up*(s*(1 + gate*(1 - s)));  grad_up = G*gate*s.
+ * sumsq, colbcast_mul and rmsnorm_forward also take narrow matrices (N % 4 != 0, 1 <= F <= 1024, N <= 65535,
+ * any alignment): one token's (F, 1) activations in incremental inference. */
 int nnhip_rmsnorm_sumsq(const float* X, float* out, size_t F, size_t N, void* stream);
 int nnhip_colbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream);
 int nnhip_rowbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream);

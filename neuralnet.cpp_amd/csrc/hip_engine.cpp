@@ -645,6 +645,9 @@ HipEngine::~HipEngine()
         (void)hipEventDestroy(static_cast<hipEvent_t>(r.stop));
     }
     for (void* e : event_pool_) (void)hipEventDestroy(static_cast<hipEvent_t>(e));
+    for (void* e : stage_ev_)
+        if (e) (void)hipEventDestroy(static_cast<hipEvent_t>(e));
+    if (stage_) (void)hipHostFree(stage_);
 }
 
 // ── GEMM event profile ──────────────────────────────────────────────────────
@@ -953,7 +956,9 @@ Result<void> HipEngine::launch_flash_(const std::vector<const PendingFlash*>& ro
 Result<const void*> HipEngine::flash_order_(const void* cells, std::size_t batch, std::size_t M, std::size_t N,
                                             std::size_t mask_bs, int kind)
 {
-    if (!cells) return static_cast<const void*>(nullptr);
+    // One query line per batch entry (a token of incremental inference, whose
+    // mask is new every call): every entry visits the same cells, nothing to balance.
+    if (!cells || M <= 32) return static_cast<const void*>(nullptr);
     for (CellTable& t : cells_)
     {
         if (t.cells->data() != cells) continue;
@@ -1568,11 +1573,52 @@ Tensor HipEngine::create_tensor(std::size_t rows, std::size_t cols)
     return *t;
 }
 
+// Host data up to kStageSlot bytes goes through a slot of a pinned staging
+// ring: the host copy lands in the slot at once and the upload is queued
+// behind the work before it, so the call does not wait for the stream (one
+// token of incremental inference uploads its ALiBi step bias in every layer).
+// A slot is reused only after its last upload has completed (an event per
+// slot). Larger data is uploaded and waited for.
+Result<bool> HipEngine::upload_(float* dst, const float* src, std::size_t n)
+{
+    const std::size_t bytes = n * sizeof(float);
+    if (bytes > kStageSlot) return false;
+    if (!stage_)
+    {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, kStageSlot * kStageSlots, hipHostMallocDefault) != hipSuccess)
+        {
+            (void)hipGetLastError();
+            return false;
+        }
+        stage_ = p;
+        stage_ev_.assign(kStageSlots, nullptr);
+        for (void*& e : stage_ev_)
+        {
+            hipEvent_t ev = nullptr;
+            if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+                return fail("HipEngine: hipEventCreate failed");
+            e = ev;
+        }
+    }
+    const std::size_t slot = stage_next_++ % kStageSlots;
+    const auto ev = static_cast<hipEvent_t>(stage_ev_[slot]);
+    if (hipEventSynchronize(ev) != hipSuccess) return fail("HipEngine: staging event wait failed");
+    char* at = static_cast<char*>(stage_) + slot * kStageSlot;
+    std::memcpy(at, src, bytes);
+    auto s = static_cast<hipStream_t>(stream_);
+    if (hipMemcpyAsync(dst, at, bytes, hipMemcpyHostToDevice, s) != hipSuccess || hipEventRecord(ev, s) != hipSuccess)
+        return fail("HipEngine: host to device copy failed");
+    return true;
+}
+
 Result<Tensor> HipEngine::from_matrix(const Matrix& m)
 {
     NN_TRY(t, alloc_(m.rows(), m.cols()));
     if (m.size())
     {
+        NN_TRY(queued, upload_(W(t), m.data(), m.size()));
+        if (queued) return t;
         auto s = static_cast<hipStream_t>(stream_);
         if (hipMemcpyAsync(W(t), m.data(), m.size() * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess)
             return fail("from_matrix: host to device copy failed");
@@ -1603,6 +1649,8 @@ Result<void> HipEngine::copy_from(Tensor& dst, const Matrix& src)
     NN_CHECK(settle_write_(dst));
     if (src.size())
     {
+        NN_TRY(queued, upload_(W(dst), src.data(), src.size()));
+        if (queued) return {};
         auto s = static_cast<hipStream_t>(stream_);
         if (hipMemcpyAsync(W(dst), src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess)
             return fail("copy_from: host to device copy failed");
@@ -2786,8 +2834,10 @@ Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std:
     {
         if (inputs.size() < 1 || !bind(canon(LayerProg::RmsSumSq), spec, inputs, a)) return R();
         const Tensor& x = inputs[0];
+        // float4 kernels for N % 4 == 0; narrow ones otherwise (one token's (F, 1) activations)
+        const bool narrow = cols % 4 != 0 && cols <= 65535;
         if (!x.is_gpu() || a[0] != x.dev_ptr() || x.rows() != rows || x.cols() != cols || rows == 0 ||
-            rows > 1024 || cols == 0 || cols % 4 != 0 || !aligned16(a[0]))
+            rows > 1024 || cols == 0 || (!narrow && (cols % 4 != 0 || !aligned16(a[0]))))
             return R();
         NN_CHECK(settle_rms_());
         NN_CHECK(settle_reads_({&x}));
@@ -2809,7 +2859,7 @@ Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std:
         return R(o);
     }
     if (r.stage == 5 && bind(canon(LayerProg::RmsScale), spec, inputs, a) && a[0] == r.normed.dev_ptr() &&
-        aligned16(a[1]))
+        (aligned16(a[1]) || cols % 4 != 0))
     {
         const Tensor* gamma = nullptr;
         for (const Tensor& t : inputs)

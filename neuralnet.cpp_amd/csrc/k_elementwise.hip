@@ -394,9 +394,19 @@ struct FillList
 };
 __global__ __launch_bounds__(kThreads) void k_fill_list(FillList f)
 {
+    // The block's tensor: the last t with first[t] <= b (binary search over the
+    // strictly increasing prefix sums; a scan of up to 96 kernel-argument
+    // loads per 16 KB block cost more than the block's stores).
     const unsigned b = blockIdx.x;
-    int t = 0;
-    while (t + 1 < f.count && f.first[t + 1] <= b) ++t;
+    int t = 0, hi = f.count - 1;
+    while (t < hi)
+    {
+        const int mid = (t + hi + 1) >> 1;
+        if (f.first[mid] <= b)
+            t = mid;
+        else
+            hi = mid - 1;
+    }
     const size_t base = static_cast<size_t>(b - f.first[t]) * kThreads * 16, n = f.n[t];
     float* p = f.p[t];
     const bool vec = (reinterpret_cast<uintptr_t>(p) & 15u) == 0;

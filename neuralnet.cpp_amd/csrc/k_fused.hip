@@ -434,6 +434,91 @@ __global__ __launch_bounds__(kColT) void k_rms_bwd(const float* __restrict__ g, 
     }
 }
 
+// ── narrow matrices (N % 4 != 0: one token's (F, 1) activations in incremental inference) ──
+// One workgroup of 256 threads per column. Thread t holds rows t, t + 256, ...
+// of the column (x^2 + acc as one fma, in row order); lane 0 of each wave
+// takes the wave's butterfly sum and the four waves are added in order. The
+// sum of squares and the one-pass forward share this order, so the forward
+// equals the separate calls bit for bit, as the float4 kernels do.
+constexpr unsigned kNarrowT = 256, kNarrowKM = 4;   // F <= 1024
+__device__ __forceinline__ float narrow_sumsq(const float* __restrict__ x, size_t N, unsigned F, unsigned c,
+                                              float (&xv)[kNarrowKM])
+{
+    __shared__ float part[kNarrowT / 64];
+#pragma unroll
+    for (unsigned k = 0; k < kNarrowKM; ++k)
+    {
+        const unsigned r = threadIdx.x + k * kNarrowT;
+        xv[k] = r < F ? x[size_t(r) * N + c] : 0.0f;
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (unsigned k = 0; k < kNarrowKM; ++k)
+        if (threadIdx.x + k * kNarrowT < F) acc = __builtin_fmaf(xv[k], xv[k], acc);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = acc;
+    __syncthreads();
+    float s = part[0];
+#pragma unroll
+    for (unsigned w = 1; w < kNarrowT / 64; ++w) s += part[w];
+    return s;
+}
+
+__global__ __launch_bounds__(kNarrowT) void k_sumsq_narrow(const float* __restrict__ x, float* __restrict__ out,
+                                                           unsigned F, size_t N)
+{
+    float xv[kNarrowKM];
+    const float s = narrow_sumsq(x, N, F, blockIdx.x, xv);
+    if (threadIdx.x == 0) out[blockIdx.x] = s;
+}
+
+// RMSNorm::forward's six calls on a narrow x, as k_rms_fwd.
+__global__ __launch_bounds__(kNarrowT) void k_rms_fwd_narrow(const float* __restrict__ x,
+                                                             const float* __restrict__ gamma, float inv_f, float eps,
+                                                             float* s_raw, float* scaled, float* var_eps,
+                                                             float* __restrict__ rinv, float* __restrict__ normed,
+                                                             float* __restrict__ out, unsigned F, size_t N)
+{
+    const unsigned c = blockIdx.x;
+    float xv[kNarrowKM];
+    const float s = narrow_sumsq(x, N, F, c, xv);
+    float ri;
+    {
+#pragma clang fp contract(off)
+        const float sc = s * inv_f, ve = sc + eps;
+        ri = 1.0f / sqrtf(ve);
+        if (threadIdx.x == 0)
+        {
+            if (s_raw) s_raw[c] = s;
+            if (scaled) scaled[c] = sc;
+            if (var_eps) var_eps[c] = ve;
+            rinv[c] = ri;
+        }
+    }
+#pragma unroll
+    for (unsigned k = 0; k < kNarrowKM; ++k)
+    {
+        const unsigned r = threadIdx.x + k * kNarrowT;
+        if (r < F)
+        {
+#pragma clang fp contract(off)
+            const float n = xv[k] * ri;
+            normed[size_t(r) * N + c] = n;
+            out[size_t(r) * N + c] = n * gamma[r];
+        }
+    }
+}
+
+// out = x * colbcast(v) on a narrow x.
+__global__ __launch_bounds__(kNarrowT) void k_colbcast_mul_narrow(const float* __restrict__ x,
+                                                                  const float* __restrict__ v, float* __restrict__ o,
+                                                                  size_t total, size_t N)
+{
+    const size_t i = size_t(blockIdx.x) * kNarrowT + threadIdx.x;
+    if (i < total) o[i] = x[i] * v[i % N];
+}
+
 // ── row sums: out[r] = sum_c g[r,c] * gamma[r] * normed[r,c], one workgroup per row ──
 __global__ __launch_bounds__(kT) void k_fused_rowsum_ggn(const float* g, const float* gamma, const float* n,
                                                          float* out, unsigned cols4, size_t cols, bool add)
@@ -507,8 +592,20 @@ int launch_flat(Op op, size_t count, hipStream_t s)
 
 using namespace nnhip;
 
+namespace
+{
+// Narrow shapes (N % 4 != 0) the narrow kernels take.
+bool narrow_ok(size_t F, size_t N) { return N % 4 != 0 && F >= 1 && F <= kNarrowT * kNarrowKM && N <= 65535; }
+} // namespace
+
 extern "C" int nnhip_rmsnorm_sumsq(const float* X, float* out, size_t F, size_t N, void* stream)
 {
+    if (X && out && narrow_ok(F, N))
+    {
+        hipLaunchKernelGGL(k_sumsq_narrow, dim3(unsigned(N)), dim3(kNarrowT), 0, static_cast<hipStream_t>(stream), X,
+                           out, unsigned(F), N);
+        return launch_status();
+    }
     if (!shape_ok(F, N, {X, out})) return kBadShape;
     return launch_colsum(SumSq{X, N}, out, F, N, static_cast<hipStream_t>(stream));
 }
@@ -518,11 +615,17 @@ extern "C" int nnhip_rmsnorm_forward(const float* X, const float* gamma, float i
                                      size_t N, void* stream)
 {
     if (!X || !gamma || !rinv || !normed || !out || F == 0 || F > 8 * kRowGroups) return kBadShape;
+    const auto s = static_cast<hipStream_t>(stream);
+    if (narrow_ok(F, N))
+    {
+        hipLaunchKernelGGL(k_rms_fwd_narrow, dim3(unsigned(N)), dim3(kNarrowT), 0, s, X, gamma, inv_f, eps, s_raw,
+                           scaled, var_eps, rinv, normed, out, unsigned(F), N);
+        return launch_status();
+    }
     if (!shape_ok(F, N, {X, rinv, normed, out, s_raw, scaled, var_eps})) return kBadShape;
     if (N == 0) return 0;
     const unsigned cols4 = unsigned(N / 4);
     const dim3 grid((cols4 + kColQuads - 1) / kColQuads), block(kColT);
-    const auto s = static_cast<hipStream_t>(stream);
     if (F <= 2 * kRowGroups)
         hipLaunchKernelGGL(k_rms_fwd<2>, grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
                            normed, out, unsigned(F), cols4, N);
@@ -559,6 +662,14 @@ extern "C" int nnhip_rmsnorm_backward(const float* G, const float* gamma, const 
 
 extern "C" int nnhip_colbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream)
 {
+    if (X && v && out && N % 4 != 0)
+    {
+        const size_t total = F * N;
+        if (total == 0) return 0;
+        hipLaunchKernelGGL(k_colbcast_mul_narrow, dim3(unsigned((total + kNarrowT - 1) / kNarrowT)), dim3(kNarrowT), 0,
+                           static_cast<hipStream_t>(stream), X, v, out, total, N);
+        return launch_status();
+    }
     if (!shape_ok(F, N, {X, v, out})) return kBadShape;
     return launch_ew(ColBcastMul{X, v, out, N}, F, N, static_cast<hipStream_t>(stream));
 }

@@ -260,6 +260,8 @@ extern "C" int nnhip_transpose(const float* A, float* out, size_t R, size_t C, v
 extern "C" int nnhip_transpose_batched(const float* A, float* out, size_t batch, size_t R, size_t C, void* stream)
 {
     if (batch == 0 || R == 0 || C == 0) return 0;
+    // A row or column vector's transpose holds the same floats in the same order.
+    if (R == 1 || C == 1) return nnhip_copy(A, out, batch * R * C, stream);
     if ((C + 63) / 64 > 0x7fffffff || (R + 63) / 64 > 65535 || batch > 65535) return -1;
     const dim3 grid(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>((R + 63) / 64),
                     static_cast<unsigned>(batch));

@@ -10,9 +10,10 @@
 //
 // Ordering: all work goes to one in-order stream, so a buffer released by a
 // Tensor can be handed to the next allocation immediately (stream-ordered
-// reuse). to_matrix / from_matrix / copy_from and end_batch / flush_batch
-// synchronise the stream, matching the reference's batch semantics
-// (compute_engine.hpp:93-118).
+// reuse). to_matrix and end_batch / flush_batch synchronise the stream,
+// matching the reference's batch semantics (compute_engine.hpp:93-118);
+// from_matrix / copy_from copy small host data into a pinned staging slot and
+// return once the upload is queued (larger data is uploaded and waited for).
 //
 // Deferred attention chains: the reference's two-pass attention calls
 // (compute_layer.hpp:1196-1221, :1304-1327) are recorded instead of launched
@@ -342,6 +343,15 @@ private:
     bool profile_ = false;
     std::vector<ProfRecord> prof_;
     std::vector<void*> event_pool_;
+
+    // Pinned staging ring for small uploads (from_matrix, copy_from): the
+    // call returns once its upload is queued. Returns false (nothing done)
+    // when the data does not fit a slot.
+    Result<bool> upload_(float* dst, const float* src, std::size_t n);
+    static constexpr std::size_t kStageSlot = std::size_t(256) << 10, kStageSlots = 64;
+    void* stage_ = nullptr;
+    std::vector<void*> stage_ev_;
+    std::size_t stage_next_ = 0;
 
     bool ok_ = false;
     std::string init_error_;

@@ -55,8 +55,11 @@ def chain(e, X, G, eps, cut=None):
     return res
 
 
-@pytest.mark.parametrize("F,N", [(768, 8192), (128, 36), (1024, 64), (1100, 40), (24, 10), (5, 4), (300, 100)])
+@pytest.mark.parametrize("F,N", [(768, 8192), (128, 36), (1024, 64), (1100, 40), (24, 10), (5, 4), (300, 100),
+                                 (768, 1), (1024, 1), (7, 2), (1025, 1), (200, 13)])
 def test_rmsnorm_forward_chain(hip, cpu, F, N):
+    """N % 4 != 0 with F <= 1024 (one token's (d_model, 1) activations in incremental inference) runs the
+    narrow kernels, whose one-pass forward and separate calls share one summation order."""
     rng = np.random.default_rng(F * 131 + N)
     X, G = normal(rng, (F, N)), uniform(rng, (F, 1), 0.5, 1.5)
     eps = 1e-5
