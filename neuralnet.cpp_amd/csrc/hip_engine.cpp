@@ -761,7 +761,6 @@ Result<void> HipEngine::need_gpu_(std::initializer_list<const Tensor*> ts, const
 // ── deferred work: launch on demand ─────────────────────────────────────────
 Result<void> HipEngine::settle_reads_(std::initializer_list<const Tensor*> ts)
 {
-    NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
     return settle_chain_reads_(ts);
 }
@@ -773,6 +772,7 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
         if (!t) continue;
         const float* p = t->dev_ptr();
         if (!p) continue;
+        NN_CHECK(settle_zero_for_(*t));
         if (!keep_flash && flash_yields_(p)) NN_CHECK(settle_flash_());
         if (pmm_ && has_buf(pmm_->C, p)) NN_CHECK(settle_mm_());
         if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, false));
@@ -977,16 +977,16 @@ Result<const void*> HipEngine::flash_order_(const void* cells, std::size_t batch
 
 Result<void> HipEngine::settle_write_(const Tensor& t)
 {
-    NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
     return settle_chain_write_(t);
 }
 
-Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb)
+Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb, bool keep_zero)
 {
     NN_CHECK(unshare_(t));
     const float* p = t.dev_ptr();
     if (!p) return {};
+    if (!keep_zero) NN_CHECK(settle_zero_for_(t));
     if (flash_uses_(p)) NN_CHECK(settle_flash_());
     if (pmm_ && pmm_->uses(p)) NN_CHECK(settle_mm_());
     if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, true));
@@ -1329,7 +1329,9 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
 Result<void> HipEngine::ew_push_(unsigned code, unsigned op, bool first, const Tensor& dst, const Tensor& a,
                                  const Tensor* b, float s)
 {
-    NN_CHECK(settle_zero_());
+    NN_CHECK(settle_zero_for_(dst));
+    NN_CHECK(settle_zero_for_(a));
+    if (b) NN_CHECK(settle_zero_for_(*b));
     const std::size_t n = dst.size();
     if (pew_ && (pew_->n != n || pew_->full())) NN_CHECK(settle_ew_(true));
     if (!pew_)
@@ -1791,7 +1793,7 @@ Result<void> HipEngine::insert_rows(Tensor& dst, std::size_t start, const Tensor
                 overlap = true;
         if (overlap) break;
         NN_CHECK(settle_ew_());
-        NN_CHECK(settle_chain_write_(dst, true));
+        NN_CHECK(settle_chain_write_(dst, true, true));
         for (auto& z : pzero_)
             if (same_t(z.t, dst)) z.covered.emplace_back(start, start + src.rows());
         PendingSwb& q = pswb_[i];
@@ -1810,8 +1812,9 @@ Result<void> HipEngine::insert_rows(Tensor& dst, std::size_t start, const Tensor
     {
         NN_CHECK(settle_ew_());
         NN_CHECK(settle_chain_reads_({&src}));
-        NN_CHECK(settle_chain_write_(dst));
-        z->covered.emplace_back(start, start + src.rows());
+        NN_CHECK(settle_chain_write_(dst, false, true));
+        for (auto& e : pzero_)   // (the settles above leave dst's zero record in place)
+            if (same_t(e.t, dst)) e.covered.emplace_back(start, start + src.rows());
     }
     else
     {
@@ -2215,7 +2218,6 @@ Result<Tensor> HipEngine::batched_matmul_softmax_backward_q(const Tensor& A, con
     {
         // m and l may still be results of a recorded forward: the backward
         // that consumes this record runs after it.
-        NN_CHECK(settle_zero_());
         NN_CHECK(settle_ew_());
         NN_CHECK(settle_chain_reads_({&A, &B, &row_max, &denom, mask}, true));
         NN_CHECK(settle_bwd_());
@@ -2420,26 +2422,33 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
     if (pmm_ && !pmm_->folded && !pmm_->bias.size() && same_t(B, pmm_->C) && !pmm_->uses(A.dev_ptr()))
     {
         // Linear backward: the weight-gradient accumulation becomes the
-        // product's epilogue (A += product); B stays recorded.
+        // product's epilogue (A += product); B stays recorded. A gradient
+        // still waiting for zero_grad's fill gets the product written
+        // instead (0 + x = x).
+        const bool fresh = take_zero_(A);
         NN_CHECK(settle_write_(A));
         if (pmm_ && same_t(B, pmm_->C))
         {
-            NN_CHECK(launch_mm_(*pmm_, A, nullptr, true));
+            NN_CHECK(launch_mm_(*pmm_, A, nullptr, !fresh));
             pmm_->folded = true;
             return {};
         }
+        if (fresh) NN_CHECK(zero_now_(A));
     }
     if (prsum_ && !prsum_->folded && same_t(B, prsum_->out) && !prsum_->uses(A.dev_ptr()))
     {
         // A bias / gamma gradient: the row-sum kernel adds its sums into A; B
-        // stays recorded.
+        // stays recorded. Into a gradient still waiting for its zero fill the
+        // sums are written.
+        const bool fresh = take_zero_(A);
         NN_CHECK(settle_write_(A));
         if (prsum_ && same_t(B, prsum_->out))
         {
-            NN_CHECK(launch_rsum_(*prsum_, W(A), true));
+            NN_CHECK(launch_rsum_(*prsum_, W(A), !fresh));
             prsum_->folded = true;
             return {};
         }
+        if (fresh) NN_CHECK(zero_now_(A));
     }
     NN_CHECK(settle_chain_reads_({&B}));
     NN_CHECK(settle_chain_write_(A));
@@ -2471,7 +2480,7 @@ Result<void> HipEngine::zero(Tensor& A)
     NN_CHECK(check_gpu_({&A}, "zero"));
     if (!A.size()) return {};
     NN_CHECK(settle_ew_());
-    NN_CHECK(settle_chain_write_(A));
+    NN_CHECK(settle_chain_write_(A, false, true));
     for (auto& e : pzero_)
         if (same_t(e.t, A))
         {
@@ -2483,11 +2492,54 @@ Result<void> HipEngine::zero(Tensor& A)
     return {};
 }
 
+// The recorded zero calls, or (settle_zero_for_) those whose memory overlaps
+// t's: one fill-list launch, rows inserted since the zero call left out.
 Result<void> HipEngine::settle_zero_()
 {
     if (pzero_.empty()) return {};
     std::vector<PendingZero> ts = std::move(pzero_);
     pzero_.clear();
+    return launch_zero_(ts);
+}
+
+Result<void> HipEngine::settle_zero_for_(const Tensor& t)
+{
+    if (pzero_.empty() || !t.dev_ptr() || !t.size()) return {};
+    const float *lo = t.dev_ptr(), *hi = lo + t.size();
+    std::vector<PendingZero> ts;
+    for (std::size_t i = pzero_.size(); i-- > 0;)
+    {
+        const float* zl = pzero_[i].t.dev_ptr();
+        if (zl < hi && lo < zl + pzero_[i].t.size())
+        {
+            ts.push_back(std::move(pzero_[i]));
+            pzero_.erase(pzero_.begin() + static_cast<std::ptrdiff_t>(i));
+        }
+    }
+    return ts.empty() ? Result<void>{} : launch_zero_(ts);
+}
+
+// True (and the record dropped) when t itself waits for its zero fill, whole:
+// the caller writes all of t instead of adding to it.
+bool HipEngine::take_zero_(const Tensor& t)
+{
+    for (std::size_t i = 0; i < pzero_.size(); ++i)
+        if (same_t(pzero_[i].t, t) && pzero_[i].covered.empty())
+        {
+            pzero_.erase(pzero_.begin() + static_cast<std::ptrdiff_t>(i));
+            return true;
+        }
+    return false;
+}
+
+Result<void> HipEngine::zero_now_(const Tensor& t)
+{
+    std::vector<PendingZero> ts{PendingZero{t, {}}};
+    return launch_zero_(ts);
+}
+
+Result<void> HipEngine::launch_zero_(std::vector<PendingZero>& ts)
+{
     std::vector<float*> ptrs;
     std::vector<std::size_t> counts;
     for (auto& z : ts)

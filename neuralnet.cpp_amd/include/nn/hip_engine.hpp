@@ -291,8 +291,15 @@ private:
         Tensor t;
         std::vector<std::pair<std::size_t, std::size_t>> covered;   // rows inserted since the zero call
     };
-    std::vector<PendingZero> pzero_;   // zero calls not yet launched
+    // zero calls not yet launched; each is launched when its memory is first
+    // read or written (or on settle), so zero_grad's fills wait for the
+    // backward, whose first accumulation into a gradient becomes a write.
+    std::vector<PendingZero> pzero_;
     Result<void> settle_zero_();
+    Result<void> settle_zero_for_(const Tensor& t);
+    bool take_zero_(const Tensor& t);
+    Result<void> zero_now_(const Tensor& t);
+    Result<void> launch_zero_(std::vector<PendingZero>& ts);
     // Before reading (writing) tensors: launch deferred work that yields
     // (yields or reads) them; the plain forms also launch the elementwise run.
     Result<void> settle_reads_(std::initializer_list<const Tensor*> ts);
@@ -300,7 +307,8 @@ private:
     // keep_flash: recorded fused attention launches stay recorded even if they
     // yield one of the tensors (the caller records work that runs after them).
     Result<void> settle_chain_reads_(std::initializer_list<const Tensor*> ts, bool keep_flash = false);
-    Result<void> settle_chain_write_(const Tensor& t, bool keep_swb = false);   // keep_swb: placed SwiGLU records stay
+    // keep_swb: placed SwiGLU records stay; keep_zero: t's own zero record stays
+    Result<void> settle_chain_write_(const Tensor& t, bool keep_swb = false, bool keep_zero = false);
     Result<void> ew_push_(unsigned code, unsigned op, bool first, const Tensor& dst, const Tensor& a, const Tensor* b,
                           float s);
     // keep_adam: recognised Adam chains stay collected in padam_ (the record

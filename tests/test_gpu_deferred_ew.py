@@ -204,6 +204,27 @@ def test_zero_list(hip):
     assert np.array_equal(keep.numpy(), arrs[0])
 
 
+def test_zero_folded_into_first_accumulation(hip):
+    """zero_grad then the Linear backward's grad_w += G X^T (and grad_b += row sums of G): a gradient
+    whose zero fill is still recorded gets the product (the sums) written instead of added; the
+    other zeroed tensors stay zero until read, including through a row slice of one of them."""
+    rng = np.random.default_rng(13)
+    G, X = uniform(rng, (96, 200)), uniform(rng, (64, 200))
+    gw, gb, other = (hip.tensor(uniform(rng, s, 1.0, 2.0)) for s in ((96, 64), (96, 1), (50, 7)))
+    for t in (gw, gb, other):
+        hip.zero(t)
+    g, x = hip.tensor(G), hip.tensor(X)
+    hip.add_inplace(gw, hip.matmul(g, x, False, True))     # Linear::backward's weight gradient
+    hip.add_inplace(gb, hip.row_reduce_sum(g))              # and its bias gradient
+    view = hip.slice_rows(other, 10, 5)
+    ref_w = G.astype(np.float64) @ X.astype(np.float64).T
+    assert np.abs(gw.numpy() - ref_w).max() <= 1e-5 * np.abs(ref_w).max()
+    assert np.abs(gb.numpy()[:, 0] - G.astype(np.float64).sum(1)).max() <= 1e-5 * np.abs(G).sum(1).max()
+    assert not view.numpy().any() and not other.numpy().any()
+    hip.add_inplace(gw, hip.matmul(g, x, False, True))     # second step: accumulates
+    assert np.abs(gw.numpy() - 2 * ref_w).max() <= 1e-5 * np.abs(2 * ref_w).max()
+
+
 def test_zero_then_inserts(hip):
     """SwiGLU::backward's zero + insert_rows pattern: inserted rows are not zeroed
     afterwards, rows no insert covers are, and a second zero call wins over earlier inserts."""
