@@ -56,6 +56,15 @@ int nnhip_gemm_heads(const float* W, const float* X, const float* row_bias, floa
 int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* const* row_bias, float* const* out,
                            size_t count, size_t M, size_t K, size_t B, size_t T, void* stream);
 
+/* C (M, N) = alpha * sum_i A_i^T B_i over count (1..3) products of one shape, one accumulator over
+ * K = count * K_each in segment order: A_i stored (K_each, M), B_i (K_each, N), all 16-byte aligned, M and N
+ * multiples of 4, K_each a multiple of 16. The attention's input gradient is three Linear backward products
+ * added in place (compute_layer.hpp:1397-1408: dx = Wq^T gQ; dx += Wk^T gK; dx += Wv^T gV); this computes it
+ * as one product, rounded once per output instead of after each add (within the GEMM tolerance of the
+ * separate calls, not bit-identical). Workspace as nnhip_gemm at K = count * K_each. No CUDA counterpart. */
+int nnhip_gemm_tn_sum(const float* const* A, const float* const* B, size_t count, float* C, size_t M, size_t N,
+                      size_t K_each, float alpha, void* workspace, size_t workspace_bytes, void* stream);
+
 /* One product with the epilogue of the call that follows it in the reference's Linear layer
  * (compute_layer.hpp Linear::forward / backward): C = alpha * op(A) op(B), then C[i][j] += row_bias[i]
  * (broadcast_row_inplace(C, bias, Add)) when row_bias is not null, and C = C_old + result

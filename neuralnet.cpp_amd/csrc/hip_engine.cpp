@@ -351,7 +351,15 @@ struct HipEngine::PendingMm
     Tensor bias;   // the Linear bias added by the call that followed (broadcast_row_inplace), if any
     Tensor heads;  // C already written in the heads' layout (B_h sequences of N_h) by a grouped launch
     std::size_t heads_B = 0, heads_N = 0;
-    bool uses(const float* p) const { return has_buf(A, p) || has_buf(B, p) || has_buf(C, p) || has_buf(bias, p); }
+    // Further products A^T B of the same shape added into C (add_inplace(C, their outputs)): C is their
+    // sum, computed as one product over the concatenated K (transposed A only).
+    std::vector<std::pair<Tensor, Tensor>> plus;
+    bool uses(const float* p) const
+    {
+        for (const auto& [a, b] : plus)
+            if (has_buf(a, p) || has_buf(b, p)) return true;
+        return has_buf(A, p) || has_buf(B, p) || has_buf(C, p) || has_buf(bias, p);
+    }
 };
 
 // Consecutive same-size elementwise calls (scale / axpy / add in place; unary,
@@ -1995,9 +2003,34 @@ Result<void> HipEngine::settle_mm_prev_(const float* p, bool write)
     return {};
 }
 
-// The recorded matmul into `out`: out = A B (+ bias per row) or out += A B.
+// The recorded matmul into `out`: out = A B (+ bias per row) or out += A B;
+// with added products, out = sum of A_i^T B_i in one launch.
 Result<void> HipEngine::launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate)
 {
+    if (!r.plus.empty())
+    {
+        if (bias || accumulate) return fail("matmul: a summed product takes no epilogue");
+        const std::size_t n = r.plus.size() + 1, Kt = n * r.K;
+        const float* As[3] = {D(r.A)};
+        const float* Bs[3] = {D(r.B)};
+        for (std::size_t i = 1; i < n; ++i)
+        {
+            As[i] = D(r.plus[i - 1].first);
+            Bs[i] = D(r.plus[i - 1].second);
+        }
+        const std::size_t wsb = nnhip_gemm_workspace_bytes(r.M, r.N, Kt, 1);
+        std::shared_ptr<DeviceBuffer> ws;
+        if (wsb)
+        {
+            NN_TRY(w, scratch_(wsb));
+            ws = w;
+        }
+        prof_begin_();
+        const int rc = nnhip_gemm_tn_sum(As, Bs, n, W(out), r.M, r.N, r.K, 1.0f, ws ? ws->data() : nullptr, wsb,
+                                         stream_);
+        prof_end_(r.M, r.N, Kt, 1, true, false);
+        return kernel_(rc, "matmul");
+    }
     const std::size_t wsb = nnhip_gemm_workspace_bytes(r.M, r.N, r.K, 1);
     std::shared_ptr<DeviceBuffer> ws;
     if (wsb)
@@ -2419,7 +2452,8 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
     NN_CHECK(check_gpu_({&A, &B}, "add_inplace"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("add_inplace: shape mismatch");
     if (!A.size()) return {};
-    if (pmm_ && !pmm_->folded && !pmm_->bias.size() && same_t(B, pmm_->C) && !pmm_->uses(A.dev_ptr()))
+    if (pmm_ && !pmm_->folded && !pmm_->bias.size() && pmm_->plus.empty() && same_t(B, pmm_->C) &&
+        !pmm_->uses(A.dev_ptr()))
     {
         // Linear backward: the weight-gradient accumulation becomes the
         // product's epilogue (A += product); B stays recorded. A gradient
@@ -2450,9 +2484,33 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
         }
         if (fresh) NN_CHECK(zero_now_(A));
     }
+    // The attention's input gradient (compute_layer.hpp:1397-1408): dx = Wq^T gQ, then dx += Wk^T gK and
+    // dx += Wv^T gV, all three products still recorded: dx becomes the sum over K = 3 d_model of one
+    // launch (within the GEMM tolerance of the separate products and adds). B stays recorded.
+    if (PendingMm *ra = pending_mm_(A), *rb = pending_mm_(B);
+        ra && rb && ra != rb && ra->tA && !ra->tB && rb->tA && !rb->tB && ra->M == rb->M && ra->N == rb->N &&
+        ra->K == rb->K && ra->K % 16 == 0 && ra->M % 4 == 0 && ra->N % 4 == 0 && rb->plus.empty() &&
+        ra->plus.size() < 2 && !ra->bias.size() && !rb->bias.size() && !rb->uses(A.dev_ptr()) &&
+        aligned16(rb->A.dev_ptr()) && aligned16(rb->B.dev_ptr()) && aligned16(ra->A.dev_ptr()) &&
+        aligned16(ra->B.dev_ptr()))
+    {
+        ra->plus.emplace_back(rb->A, rb->B);
+        rb->folded = true;
+        return {};
+    }
     NN_CHECK(settle_chain_reads_({&B}));
     NN_CHECK(settle_chain_write_(A));
     return ew_push_(kBin, static_cast<unsigned>(BinaryOp::Add), false, A, A, &B, 0.0f);
+}
+
+// The recorded, not yet folded plain product whose output is t, if any.
+HipEngine::PendingMm* HipEngine::pending_mm_(const Tensor& t)
+{
+    auto ok = [&](PendingMm* r) { return r && !r->folded && same_t(r->C, t) && !r->heads.size(); };
+    if (ok(pmm_.get())) return pmm_.get();
+    for (auto& q : pmm_prev_)
+        if (ok(q.get())) return q.get();
+    return nullptr;
 }
 
 Result<void> HipEngine::scale_inplace(Tensor& A, Scalar s)
@@ -2627,8 +2685,8 @@ Result<Tensor> HipEngine::col_reduce_max(const Tensor& A)
 Result<void> HipEngine::broadcast_row_inplace(Tensor& A, const Tensor& v, BinaryOp op)
 {
     NN_CHECK(check_gpu_({&A, &v}, "broadcast_row_inplace"));
-    if (op == BinaryOp::Add && pmm_ && !pmm_->folded && !pmm_->bias.size() && same_t(A, pmm_->C) &&
-        v.rows() == A.rows() && v.cols() == 1 && v.size() && !pmm_->uses(v.dev_ptr()))
+    if (op == BinaryOp::Add && pmm_ && !pmm_->folded && !pmm_->bias.size() && pmm_->plus.empty() &&
+        same_t(A, pmm_->C) && v.rows() == A.rows() && v.cols() == 1 && v.size() && !pmm_->uses(v.dev_ptr()))
     {
         // Linear forward: the bias add becomes the product's epilogue. The
         // product stays recorded: when the sparse cross-entropy reads it next

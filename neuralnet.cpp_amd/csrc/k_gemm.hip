@@ -55,12 +55,17 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 // Up to three products sharing B (the attention's q, k, v projections of one
 // input): workgroup batch z takes member z / nb, batch z % nb of that member.
+// With KSEG instead: up to three products of one shape summed into one C
+// (the q, k, v input gradients), k running through segment i = k / klen of
+// A[i] and B[i] in turn.
 struct GemmGroup
 {
     const float* A[3];
     float* C[3];
     const float* bias[3];
     int nb;
+    const float* B[3];
+    int klen;
 };
 
 // WM x WN waves; each wave owns (32*FM) x (32*FN) of C as FM x FN MFMA 32x32 blocks.
@@ -69,7 +74,8 @@ struct GemmGroup
 // rows, part[(tiles_m + tile_m) * N + n] = sum of exp(c - max) over them. The
 // sparse cross-entropy that follows the product (the GPT's lm_head logits)
 // merges these instead of reading C once more for them. Needs splits == 1.
-template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD, bool STATS = false, bool GRP = false>
+template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD, bool STATS = false, bool GRP = false,
+          bool KSEG = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K, long lda, long ldb,
                                                        long strideA, long strideB, long strideC, float alpha,
@@ -124,8 +130,22 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
 
     f4 ra[LA], rb[LB];   // native vectors: HIP's float4 struct kept these arrays in scratch
 
+    // KSEG: the operands of the segment holding stage k0 (a stage never
+    // straddles two: klen % BK == 0), addressed with k within the segment.
+    auto seg_of = [&](int k0, const float* const* ops, const float* whole, int& kb) {
+        if constexpr (KSEG)
+        {
+            const int sg = k0 / grp.klen;
+            kb = k0 - sg * grp.klen;
+            return ops[sg];
+        }
+        kb = k0;
+        return whole;
+    };
     // A_eff(m, k) = TA ? A[k*lda + m] : A[m*lda + k]
     auto load_a = [&](int k0) {
+        int kb;
+        const float* Ap = seg_of(k0, grp.A, A, kb);
 #pragma unroll
         for (int s = 0; s < LA; ++s)
         {
@@ -133,11 +153,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             int m, k;
             if constexpr (TA) { k = idx / (BM / 4); m = (idx % (BM / 4)) * 4; }
             else { m = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
-            const int gm = m0 + m, gk = k0 + k;
+            const int gm = m0 + m, gk = kb + k, dk = k0 - kb;   // gk + dk: k over the whole sum
             if constexpr (!GUARD)
             {
-                ra[s] = TA ? *reinterpret_cast<const f4*>(A + (long)gk * lda + gm)
-                           : *reinterpret_cast<const f4*>(A + (long)gm * lda + gk);
+                ra[s] = TA ? *reinterpret_cast<const f4*>(Ap + (long)gk * lda + gm)
+                           : *reinterpret_cast<const f4*>(Ap + (long)gm * lda + gk);
             }
             else
             {
@@ -146,7 +166,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
                 for (int q = 0; q < 4; ++q)
                 {
                     const int mm = TA ? gm + q : gm, kk = TA ? gk : gk + q;
-                    v[q] = (mm < M && kk < k_hi) ? (TA ? A[(long)kk * lda + mm] : A[(long)mm * lda + kk]) : 0.0f;
+                    v[q] = (mm < M && kk + dk < k_hi) ? (TA ? Ap[(long)kk * lda + mm] : Ap[(long)mm * lda + kk])
+                                                       : 0.0f;
                 }
                 ra[s] = f4{v[0], v[1], v[2], v[3]};
             }
@@ -154,6 +175,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     };
     // B_eff(k, n) = TB ? B[n*ldb + k] : B[k*ldb + n]
     auto load_b = [&](int k0) {
+        int kb;
+        const float* Bp = seg_of(k0, grp.B, B, kb);
 #pragma unroll
         for (int s = 0; s < LB; ++s)
         {
@@ -161,11 +184,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             int n, k;
             if constexpr (!TB) { k = idx / (BN / 4); n = (idx % (BN / 4)) * 4; }
             else { n = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
-            const int gn = n0 + n, gk = k0 + k;
+            const int gn = n0 + n, gk = kb + k, dk = k0 - kb;
             if constexpr (!GUARD)
             {
-                rb[s] = !TB ? *reinterpret_cast<const f4*>(B + (long)gk * ldb + gn)
-                            : *reinterpret_cast<const f4*>(B + (long)gn * ldb + gk);
+                rb[s] = !TB ? *reinterpret_cast<const f4*>(Bp + (long)gk * ldb + gn)
+                            : *reinterpret_cast<const f4*>(Bp + (long)gn * ldb + gk);
             }
             else
             {
@@ -174,7 +197,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
                 for (int q = 0; q < 4; ++q)
                 {
                     const int nn = !TB ? gn + q : gn, kk = !TB ? gk : gk + q;
-                    v[q] = (nn < N && kk < k_hi) ? (!TB ? B[(long)kk * ldb + nn] : B[(long)nn * ldb + kk]) : 0.0f;
+                    v[q] = (nn < N && kk + dk < k_hi) ? (!TB ? Bp[(long)kk * ldb + nn] : Bp[(long)nn * ldb + kk])
+                                                       : 0.0f;
                 }
                 rb[s] = f4{v[0], v[1], v[2], v[3]};
             }
@@ -580,6 +604,7 @@ struct Epi
     const float* bias;                  // per output row, or null
     int accum;                          // C += result
     const GemmGroup* grp = nullptr;     // members of a grouped launch (no split, NN only)
+    const GemmGroup* seg = nullptr;     // K segments summed into one C (TN only)
 };
 
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB>
@@ -592,6 +617,19 @@ void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, l
     const bool guard = !vec_ok || (M % BM) || (N % BN) || (K % BK) || (k_split % BK);
     const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits), static_cast<unsigned>(batch));
     const dim3 block(64 * WM * WN);
+    if constexpr (TA && !TB)
+        if (e.seg)
+        {
+            if (guard)
+                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, true, false, false, true>), grid, block, 0, s, A,
+                                   B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part, e.bias, e.accum,
+                                   *e.seg);
+            else
+                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, false, true>), grid, block, 0, s,
+                                   A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part, e.bias,
+                                   e.accum, *e.seg);
+            return;
+        }
     if constexpr (!TA && !TB)
         if (e.grp)
         {
@@ -793,8 +831,9 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
     if (M == 0 || N == 0 || batch == 0) return 0;
     if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || batch > 65535) return -1;
     if (e.grp && (tA || tB || workspace)) return -1;
+    if (e.seg && !(tA && !tB)) return -1;
     auto s = static_cast<hipStream_t>(stream);
-    if (int rc = 0; !e.grp && try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc))
+    if (int rc = 0; !e.grp && !e.seg && try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc))
         return rc;
     Plan p = plan_gemm(M, N, K, batch, workspace != nullptr);
     if (p.splits > 1 && static_cast<size_t>(p.splits) * batch * M * N * sizeof(float) > ws_bytes)
@@ -890,6 +929,29 @@ extern "C" int nnhip_gemm_epilogue(const float* A, const float* B, float* C, siz
     if (K != K2) return -2;
     return gemm_dispatch(A, B, C, M, N, K, A_cols, B_cols, A_rows * A_cols, B_rows * B_cols, M * N, transA != 0,
                          transB != 0, alpha, 1, workspace, workspace_bytes, stream, Epi{row_bias, accumulate ? 1 : 0});
+}
+
+extern "C" int nnhip_gemm_tn_sum(const float* const* A, const float* const* B, size_t count, float* C, size_t M,
+                                 size_t N, size_t K_each, float alpha, void* workspace, size_t workspace_bytes,
+                                 void* stream)
+{
+    if (!A || !B || !C || count == 0 || count > 3 || K_each == 0 || K_each % 16 != 0 || M % 4 != 0 || N % 4 != 0 ||
+        count * K_each > 0x7fffffff)
+        return -1;
+    GemmGroup g{};
+    g.klen = static_cast<int>(K_each);
+    for (size_t i = 0; i < count; ++i)
+    {
+        if (!A[i] || !B[i] || !aligned16(A[i]) || !aligned16(B[i])) return -1;
+        g.A[i] = A[i];
+        g.B[i] = B[i];
+    }
+    // A_i stored (K_each, M), B_i (K_each, N); the segment pointers come from the group, A[0] and B[0] here
+    // only give the launch its shape and alignment checks.
+    Epi e{nullptr, 0};
+    e.seg = &g;
+    return gemm_dispatch(A[0], B[0], C, M, N, count * K_each, M, N, 0, 0, M * N, true, false, alpha, 1, workspace,
+                         workspace_bytes, stream, e);
 }
 
 extern "C" int nnhip_gemm_heads(const float* W, const float* X, const float* row_bias, float* out, size_t M,

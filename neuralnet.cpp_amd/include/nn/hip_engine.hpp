@@ -238,6 +238,7 @@ private:
     Result<void> settle_mm_();
     Result<void> settle_mm_prev_(const float* p, bool write);
     Result<void> launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate);
+    PendingMm* pending_mm_(const Tensor& t);
     struct PendingMaskAdd;
     struct PendingAttn;
     struct PendingDv;

