@@ -362,6 +362,30 @@ struct HipEngine::PendingMm
     }
 };
 
+// Weight-gradient accumulations C_i += A_i op(B) (Linear::backward's
+// grad_w += G X^T, folded into the product) with one B, not launched yet: the
+// attention's q, k and v layers share their input X, so their three
+// accumulations run as one grouped launch (nnhip_gemm_group_acc).
+struct HipEngine::PendingAcc
+{
+    Tensor B;
+    bool tB;
+    std::size_t M, N, K;
+    std::vector<std::pair<Tensor, Tensor>> mem;   // (A_i, C_i)
+    bool yields(const float* p) const
+    {
+        for (const auto& m : mem)
+            if (has_buf(m.second, p)) return true;
+        return false;
+    }
+    bool uses(const float* p) const
+    {
+        for (const auto& m : mem)
+            if (has_buf(m.first, p)) return true;
+        return yields(p) || has_buf(B, p);
+    }
+};
+
 // Consecutive same-size elementwise calls (scale / axpy / add in place; unary,
 // binary, scalar and clone into new tensors), recorded in call order. Slots
 // are the distinct buffers the calls touch; every result is a real allocation
@@ -781,6 +805,7 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
         const float* p = t->dev_ptr();
         if (!p) continue;
         NN_CHECK(settle_zero_for_(*t));
+        if (pacc_ && pacc_->yields(p)) NN_CHECK(settle_acc_());
         if (!keep_flash && flash_yields_(p)) NN_CHECK(settle_flash_());
         if (pmm_ && has_buf(pmm_->C, p)) NN_CHECK(settle_mm_());
         if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, false));
@@ -995,6 +1020,7 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb, bool
     const float* p = t.dev_ptr();
     if (!p) return {};
     if (!keep_zero) NN_CHECK(settle_zero_for_(t));
+    if (pacc_ && pacc_->uses(p)) NN_CHECK(settle_acc_());
     if (flash_uses_(p)) NN_CHECK(settle_flash_());
     if (pmm_ && pmm_->uses(p)) NN_CHECK(settle_mm_());
     if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, true));
@@ -1041,6 +1067,7 @@ Result<void> HipEngine::settle()
     NN_CHECK(settle_zero_());
     NN_CHECK(settle_ew_());
     NN_CHECK(settle_flash_());
+    NN_CHECK(settle_acc_());
     NN_CHECK(settle_mm_());
     NN_CHECK(settle_mm_prev_(nullptr, false));
     NN_CHECK(settle_swb_());
@@ -2046,6 +2073,36 @@ Result<void> HipEngine::launch_mm_(const PendingMm& r, const Tensor& out, const 
     return kernel_(rc, "matmul");
 }
 
+// The recorded weight-gradient accumulations: one grouped launch (a single
+// member as its own product with the accumulating epilogue).
+Result<void> HipEngine::settle_acc_()
+{
+    if (!pacc_) return {};
+    std::unique_ptr<PendingAcc> r = std::move(pacc_);
+    const std::size_t n = r->mem.size();
+    const std::size_t wsb = nnhip_gemm_workspace_bytes(r->M, r->N, r->K, n);
+    std::shared_ptr<DeviceBuffer> ws;
+    if (wsb)
+    {
+        NN_TRY(w, scratch_(wsb));
+        ws = w;
+    }
+    const float* As[3] = {};
+    float* Cs[3] = {};
+    for (std::size_t i = 0; i < n; ++i)
+    {
+        As[i] = D(r->mem[i].first);
+        Cs[i] = W(r->mem[i].second);
+    }
+    prof_begin_();
+    const int rc = n == 1 ? nnhip_gemm_epilogue(As[0], D(r->B), Cs[0], r->M, r->K, r->B.rows(), r->B.cols(), 0,
+                                                r->tB, 1.0f, nullptr, 1, ws ? ws->data() : nullptr, wsb, stream_)
+                          : nnhip_gemm_group_acc(As, D(r->B), Cs, n, r->M, r->N, r->K, r->tB, 1,
+                                                 ws ? ws->data() : nullptr, wsb, stream_);
+    prof_end_(r->M, r->N, r->K, n, false, r->tB);
+    return kernel_(rc, "matmul");
+}
+
 Result<void> HipEngine::settle_mm_()
 {
     if (!pmm_) return {};
@@ -2463,8 +2520,25 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
         NN_CHECK(settle_write_(A));
         if (pmm_ && same_t(B, pmm_->C))
         {
-            NN_CHECK(launch_mm_(*pmm_, A, nullptr, !fresh));
-            pmm_->folded = true;
+            PendingMm& r = *pmm_;
+            r.folded = true;
+            // Accumulations sharing B wait to run together (the q, k, v weight gradients).
+            const bool group = !fresh && !r.tA && r.K >= 1024 && (r.M * r.N) % 4 == 0 && aligned16(A.dev_ptr());
+            if (group && pacc_ && same_t(pacc_->B, r.B) && pacc_->tB == r.tB && pacc_->M == r.M &&
+                pacc_->N == r.N && pacc_->K == r.K && pacc_->mem.size() < 3 && !pacc_->uses(A.dev_ptr()))
+            {
+                pacc_->mem.emplace_back(r.A, A);
+                if (pacc_->mem.size() == 3) NN_CHECK(settle_acc_());
+                return {};
+            }
+            NN_CHECK(settle_acc_());
+            if (group)
+            {
+                pacc_ = std::make_unique<PendingAcc>(PendingAcc{r.B, r.tB, r.M, r.N, r.K, {}});
+                pacc_->mem.emplace_back(r.A, A);
+                return {};
+            }
+            NN_CHECK(launch_mm_(r, A, nullptr, !fresh));
             return {};
         }
         if (fresh) NN_CHECK(zero_now_(A));

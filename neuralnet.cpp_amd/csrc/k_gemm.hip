@@ -450,6 +450,38 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_ep(const float* __restric
     }
 }
 
+// The split-K partials of a grouped launch (members of mn elements each,
+// part[s][member][mn]) into each member's C: C_i = alpha * sum_s part (+ C_i
+// when accum), summed in split order; mn % 4 == 0, every C_i 16-byte aligned.
+__global__ __launch_bounds__(256) void k_splitk_reduce_grp(const float* __restrict__ part, GemmGroup g, long mn,
+                                                           int members, int splits, float alpha, int accum)
+{
+#pragma clang fp contract(off)
+    const long n4 = (long)members * mn / 4, stride = (long)gridDim.x * 256;
+    const float4* p4 = reinterpret_cast<const float4*>(part);
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride)
+    {
+        float4 a = p4[i];
+        for (int s = 1; s < splits; ++s)
+        {
+            const float4 b = p4[(long)s * n4 + i];
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
+        const long e = 4 * i, mi = e / mn;
+        float4* c = reinterpret_cast<float4*>(g.C[mi] + (e - mi * mn));
+        float4 v = make_float4(alpha * a.x, alpha * a.y, alpha * a.z, alpha * a.w);
+        if (accum)
+        {
+            const float4 o = *c;
+            v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+        }
+        *c = v;
+    }
+}
+
 // C = alpha * sum_s part[s], summed in split order (deterministic).
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, float* __restrict__ C,
                                                        long n, int splits, float alpha, int vec)
@@ -630,7 +662,7 @@ void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, l
                                    e.accum, *e.seg);
             return;
         }
-    if constexpr (!TA && !TB)
+    if constexpr (!TA)
         if (e.grp)
         {
             if (guard)
@@ -830,7 +862,7 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
 {
     if (M == 0 || N == 0 || batch == 0) return 0;
     if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || batch > 65535) return -1;
-    if (e.grp && (tA || tB || workspace)) return -1;
+    if (e.grp && tA) return -1;
     if (e.seg && !(tA && !tB)) return -1;
     auto s = static_cast<hipStream_t>(stream);
     if (int rc = 0; !e.grp && !e.seg && try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc))
@@ -844,7 +876,14 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
     else if (!tA && tB) launch_trans<false, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
     else if (tA && !tB) launch_trans<true, false>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
     else launch_trans<true, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
-    if (p.splits > 1)
+    if (p.splits > 1 && e.grp)
+    {
+        // grouped members (nb == 1): each member's partials into its own C
+        const long mn = (long)M * (long)N;
+        hipLaunchKernelGGL(k_splitk_reduce_grp, dim3(grid_for(static_cast<size_t>(batch * mn / 4 + 1), 256, 256 * 16)),
+                           dim3(256), 0, s, part, *e.grp, mn, (int)batch, p.splits, alpha, e.accum);
+    }
+    else if (p.splits > 1)
     {
         const long total = (long)batch * (long)M * (long)N;
         const int vec = aligned16(C) && (e.bias || e.accum ? N % 4 == 0 : total % 4 == 0) ? 1 : 0;
@@ -929,6 +968,26 @@ extern "C" int nnhip_gemm_epilogue(const float* A, const float* B, float* C, siz
     if (K != K2) return -2;
     return gemm_dispatch(A, B, C, M, N, K, A_cols, B_cols, A_rows * A_cols, B_rows * B_cols, M * N, transA != 0,
                          transB != 0, alpha, 1, workspace, workspace_bytes, stream, Epi{row_bias, accumulate ? 1 : 0});
+}
+
+extern "C" int nnhip_gemm_group_acc(const float* const* A, const float* B, float* const* C, size_t count, size_t M,
+                                    size_t N, size_t K, int transB, int accumulate, void* workspace,
+                                    size_t workspace_bytes, void* stream)
+{
+    if (!A || !B || !C || count == 0 || count > 3 || M == 0 || N == 0 || K == 0 || (M * N) % 4 != 0) return -1;
+    GemmGroup g{};
+    g.nb = 1;
+    for (size_t i = 0; i < count; ++i)
+    {
+        if (!A[i] || !C[i] || !aligned16(C[i])) return -1;
+        g.A[i] = A[i];
+        g.C[i] = C[i];
+    }
+    // A_i stored (M, K), B (K, N) or, with transB, (N, K); batch z of the launch is member z.
+    Epi e{nullptr, accumulate ? 1 : 0};
+    e.grp = &g;
+    return gemm_dispatch(A[0], B, C[0], M, N, K, K, transB ? K : N, M * K, 0, M * N, false, transB != 0, 1.0f, count,
+                         workspace, workspace_bytes, stream, e);
 }
 
 extern "C" int nnhip_gemm_tn_sum(const float* const* A, const float* const* B, size_t count, float* C, size_t M,

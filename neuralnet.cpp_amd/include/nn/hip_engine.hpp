@@ -239,6 +239,9 @@ private:
     Result<void> settle_mm_prev_(const float* p, bool write);
     Result<void> launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate);
     PendingMm* pending_mm_(const Tensor& t);
+    struct PendingAcc;
+    std::unique_ptr<PendingAcc> pacc_;
+    Result<void> settle_acc_();
     struct PendingMaskAdd;
     struct PendingAttn;
     struct PendingDv;

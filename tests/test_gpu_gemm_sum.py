@@ -86,3 +86,70 @@ def test_entry_point(hip, count, M, N, K):
     _check(c.numpy(), As, Bs)
     assert lib.nnhip_gemm_tn_sum(pa, pb, 4, c.data_ptr(), M, N, K, 1.0, None, 0, None) == -1   # count > 3
     assert lib.nnhip_gemm_tn_sum(pa, pb, count, c.data_ptr(), M, N, 24, 1.0, None, 0, None) == -1   # K % 16
+
+
+# ── grouped weight-gradient accumulations (nnhip_gemm_group_acc) ──────────────
+def _acc_ref(W0, G, X):
+    return W0.astype(np.float64) + G.astype(np.float64) @ X.astype(np.float64).T
+
+
+def _check_acc(got, W0, G, X):
+    ref = _acc_ref(W0, G, X)
+    mag = np.abs(W0.astype(np.float64)) + np.abs(G.astype(np.float64)) @ np.abs(X.astype(np.float64)).T
+    assert nrm_err(got, ref) <= 1e-5
+    assert np.all(np.abs(got - ref) <= 2 * (X.shape[1] + 1) * 2.0 ** -24 * mag + 1e-30)
+
+
+@pytest.mark.parametrize("M,K,N,cut", [(768, 768, 8192, None), (96, 64, 2048, None), (96, 64, 2048, "read"),
+                                       (96, 64, 2048, "write_x")])
+def test_weight_gradients_sharing_input(hip, M, K, N, cut):
+    """Linear::backward's grad_w += G X^T for three layers with one input X (the q, k, v projections):
+    recorded and run as one grouped launch; `cut` reads the first gradient, or writes X in place, after
+    the second accumulation (the recorded ones run first)."""
+    rng = np.random.default_rng(M + K + N)
+    X = uniform(rng, (K, N))
+    Gs = [uniform(rng, (M, N)) for _ in range(3)]
+    W0 = [uniform(rng, (M, K)) for _ in range(3)]
+    x = hip.tensor(X)
+    gw = [hip.tensor(w) for w in W0]
+    early = None
+    for i in range(3):
+        hip.add_inplace(gw[i], hip.matmul(hip.tensor(Gs[i]), x, False, True))
+        if i == 1 and cut == "read":
+            early = gw[0].numpy()
+        if i == 1 and cut == "write_x":
+            hip.scale_inplace(x, 0.5)
+    X3 = X * (0.5 if cut == "write_x" else 1.0)
+    for i in range(3):
+        _check_acc(gw[i].numpy(), W0[i], Gs[i], X3 if i == 2 else X)
+    if early is not None:
+        _check_acc(early, W0[0], Gs[0], X)
+
+
+@pytest.mark.parametrize("count,M,N,K,tB", [(3, 768, 768, 8192, True), (2, 100, 36, 3000, True),
+                                            (3, 64, 128, 512, False), (1, 96, 64, 2048, True)])
+def test_group_acc_entry_point(hip, count, M, N, K, tB):
+    lib = nnengine.hip_library()
+    lib.nnhip_gemm_workspace_bytes.restype = SZ
+    lib.nnhip_gemm_workspace_bytes.argtypes = [SZ] * 4
+    lib.nnhip_gemm_group_acc.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, SZ, SZ, SZ, SZ,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p, SZ, ctypes.c_void_p]
+    lib.nnhip_engine_stream.restype = ctypes.c_void_p
+    lib.nnhip_engine_stream.argtypes = [ctypes.c_void_p]
+    rng = np.random.default_rng(count * M + K)
+    As = [uniform(rng, (M, K)) for _ in range(count)]
+    Bm = uniform(rng, (N, K) if tB else (K, N))
+    C0 = [uniform(rng, (M, N)) for _ in range(count)]
+    a, c = [hip.tensor(x) for x in As], [hip.tensor(x) for x in C0]
+    b = hip.tensor(Bm)
+    wsb = lib.nnhip_gemm_workspace_bytes(M, N, K, count)
+    ws = hip.create_tensor(max(1, wsb // 4), 1)
+    hip.sync()
+    pa = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in a])
+    pc = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in c])
+    print(f"[group_acc] count {count} M {M} N {N} K {K} tB {tB} ws {wsb}", flush=True)
+    assert lib.nnhip_gemm_group_acc(pa, b.data_ptr(), pc, count, M, N, K, int(tB), 1,
+                                    ws.data_ptr() if wsb else None, wsb, lib.nnhip_engine_stream(hip._e)) == 0
+    Xt = Bm if tB else Bm.T          # (N, K): C += A X^T
+    for i in range(count):
+        _check_acc(c[i].numpy(), C0[i], As[i], np.ascontiguousarray(Xt))
