@@ -83,6 +83,13 @@ int nnhip_gemm_epilogue(const float* A, const float* B, float* C, size_t A_rows,
                         size_t B_cols, int transA, int transB, float alpha, const float* row_bias, int accumulate,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Up to four products y_i (rows) = R_i (rows, K) x (+ bias_i) of one vector x in one launch, count in 1..4,
+ * bias NULL or with NULL entries: the q, k and v Linear forwards of one token in incremental inference
+ * (compute_layer.hpp:1426-1511 calls w_q, w_k, w_v on the same x_new). Each y_i is bit-identical to
+ * nnhip_gemm_epilogue(R_i, x, y_i, rows, K, K, 1, 0, 0, 1.0f, bias_i, 0, ...). No CUDA counterpart. */
+int nnhip_gemv_group(const float* const* R, const float* x, const float* const* bias, float* const* y, size_t count,
+                     size_t rows, size_t K, void* stream);
+
 /* nnhip_gemm that allocates nothing and takes no workspace. No counterpart in the reference: it is for
  * callers that cannot allocate device memory or hand in a workspace (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation). Split-K partial tiles go to a scratch array inside
@@ -348,6 +355,22 @@ int nnhip_flash_backward_ds_rows(const nnhip_flash_bwd_row* rows, size_t nrows, 
                                  void* workspace, void* stream);
 int nnhip_flash_build_rows_order(const void* const* cells, size_t nrows, size_t hpr, size_t M, size_t N, int kind,
                                  void* order, void* stream);
+
+/* One query per batch entry (incremental inference, compute_layer.hpp:1426-1511: scores =
+ * batched_matmul(q, K_T, transA, scale), + the ALiBi row, softmax, batched_matmul(V_T, attn, transB)),
+ * with keys and values read where they lie. For b < batch, j < N:
+ *   s_j = alpha * (q_b . k_bj) + mask[b*mask_bs + j]   (no mask term when mask is NULL)
+ *   m[b] = max_j s_j, l[b] = sum_j exp(s_j - m[b]), O[b*D + d] = sum_j exp(s_j - m[b]) v_bj[d] / l[b]
+ *   P[b*N + j] = exp(s_j - m[b]) / l[b]   (the probabilities, when P is not NULL)
+ * (m = lowest(), l = 0, O = 0 when every s_j is -inf, as nnhip_flash_forward leaves such rows), with
+ * q_b[k] = Q[b*K + k], k_bj[k] = Kp[b*kb + j*kj + k*kk], v_bj[d] = V[b*vb + j*vj + d*vd]: the rows of
+ * a (seq, heads*d) KV cache are read in place with kb = d, kj = heads*d, kk = 1. K, D <= 64. Workspace:
+ * nnhip_attn_query_workspace_bytes (0 up to 256 keys; longer rows are split and merged in key order).
+ * No CUDA counterpart. */
+size_t nnhip_attn_query_workspace_bytes(size_t batch, size_t N, size_t D);
+int nnhip_attn_query(const float* Q, const float* Kp, long kb, long kj, long kk, const float* V, long vb, long vj,
+                     long vd, const float* mask, long mask_bs, float* m, float* l, float* O, float* P, size_t batch,
+                     size_t N, size_t K, size_t D, float alpha, void* workspace, void* stream);
 
 /* ── column softmax / sparse cross-entropy (no CUDA counterpart) ─────────
  * cpu_engine.hpp:922-945 and :948-1006. Workspace from nnhip_col_softmax_workspace_bytes. */

@@ -1074,7 +1074,6 @@ Result<void> HipEngine::settle()
     NN_CHECK(settle_madd_());
     NN_CHECK(settle_rms_());
     NN_CHECK(settle_rsum_());
-    NN_CHECK(settle_layout_());
     NN_CHECK(settle_dv_());
     NN_CHECK(settle_ds_());
     if (pgrads_ && !live(pgrads_->dQ) && !live(pgrads_->dK)) pgrads_.reset();
@@ -1082,7 +1081,10 @@ Result<void> HipEngine::settle()
     forget_dead_two_();
     NN_CHECK(settle_bwd_());
     NN_CHECK(settle_gemm_());
-    return settle_fwd_();
+    NN_CHECK(settle_fwd_());
+    // Recorded transposes last: the records dropped above release the ones
+    // only they referenced (the one-query attention's key and value operands).
+    return settle_layout_();
 }
 
 // m (and l) of a deferred forward chain, in one pass over the scores.
@@ -1185,6 +1187,20 @@ const HipEngine::PendingLayout* HipEngine::layout_of_(const Tensor& t) const
     return nullptr;
 }
 
+// The copy of a recorded transpose whose result t is about to be read (a
+// no-op when t is not one).
+Result<void> HipEngine::settle_layout_for_(const Tensor& t)
+{
+    for (std::size_t i = 0; i < playout_.size(); ++i)
+        if (has_buf(playout_[i].out, t.dev_ptr()))
+        {
+            const PendingLayout r = std::move(playout_[i]);
+            playout_.erase(playout_.begin() + static_cast<std::ptrdiff_t>(i));
+            return materialise_layout_(r);
+        }
+    return {};
+}
+
 std::shared_ptr<HipEngine::PendingAttn> HipEngine::attn_of_(const Tensor& A) const
 {
     for (const auto& a : pattn_)
@@ -1274,8 +1290,10 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
     if (p && tB && !p->stats && alpha == 1.0f && A.rows() % batch == 0 && batch == p->batch && A.cols() == p->N)
     {
         const std::size_t Dv = A.rows() / batch;
+        if (p->M == 1 && Dv > 0 && Dv <= 64 && p->Kd <= 64) return attn_query_(*p, A, Dv);
         if (Dv == 0 || !nnhip_flash_supported(batch, p->M, p->N, p->Kd, Dv)) return R();
         NN_CHECK(settle_reads_({&A}));
+        NN_CHECK(settle_layout_for_(p->K));
         NN_TRY(out, alloc_(batch * Dv, p->M));
         NN_TRY(m, alloc_(batch * p->M, 1));
         NN_TRY(l, alloc_(batch * p->M, 1));
@@ -1327,6 +1345,7 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
         }
         NN_TRY(cells, mask_cells_(&q.mask, q.M, q.N));
         const std::size_t bs = q.mask.rows() == q.M ? 0 : q.M * q.N;
+        NN_CHECK(settle_layout_for_(q.K));
         if (q.O.dev_ptr() && same_t(pds_->Vp, q.V) && q.V.rows() == batch * q.Kd)
         {
             // R from the forward output (same V): one key-line pass plus dQ from the stored dS.
@@ -1355,6 +1374,47 @@ Result<std::optional<Tensor>> HipEngine::attn_bmm_(const Tensor& A, const Tensor
         return attn_bmm_(A, B, batch, tA, tB, alpha);
     }
     return R();
+}
+
+// O = V A^T for one query per batch entry (incremental inference): m, l and O
+// of the recorded chain in one launch, keys and values read where they lie
+// (the KV cache rows when K and V are recorded transposes of them).
+Result<std::optional<Tensor>> HipEngine::attn_query_(PendingAttn& p, const Tensor& V, std::size_t Dv)
+{
+    const std::size_t batch = p.batch, N = p.N, Kd = p.Kd;
+    // Source rows of a recorded transpose: (N, batch * d) for a (batch * d, N) operand.
+    auto rows_of = [&](const Tensor& t, std::size_t d) -> const Tensor* {
+        const PendingLayout* l = layout_of_(t);
+        return l && !l->per_batch && l->S.rows() == N && l->S.cols() == batch * d ? &l->S : nullptr;
+    };
+    const Tensor* ks = rows_of(p.K, Kd);
+    const Tensor* vs = rows_of(V, Dv);
+    if (!ks) NN_CHECK(settle_layout_for_(p.K));
+    if (!vs) NN_CHECK(settle_reads_({&V}));
+    const long kb = ks ? (long)Kd : (long)(Kd * N), kj = ks ? (long)ks->cols() : 1L, kk = ks ? 1L : (long)N;
+    const long vb = vs ? (long)Dv : (long)(Dv * N), vj = vs ? (long)vs->cols() : 1L, vd = vs ? 1L : (long)N;
+    const bool has_mask = p.mask.size() > 0;
+    const long mask_bs = has_mask && p.mask.rows() != 1 ? static_cast<long>(N) : 0L;
+    NN_TRY(out, alloc_(batch * Dv, 1));
+    NN_TRY(m, alloc_(batch, 1));
+    NN_TRY(l, alloc_(batch, 1));
+    const std::size_t wsb = nnhip_attn_query_workspace_bytes(batch, N, Dv);
+    std::shared_ptr<DeviceBuffer> ws;
+    if (wsb)
+    {
+        NN_TRY(w, scratch_(wsb));
+        ws = w;
+    }
+    // The probabilities go to the handed-out A as well (batch * N floats): the
+    // record is then complete and dropped, and with it the key and value
+    // operands, whose transposes are never made.
+    NN_CHECK(kernel_(nnhip_attn_query(D(p.Q), ks ? D(*ks) : D(p.K), kb, kj, kk, vs ? D(*vs) : D(V), vb, vj, vd,
+                                      has_mask ? D(p.mask) : nullptr, mask_bs, W(m), W(l), W(out), W(p.A), batch, N,
+                                      Kd, Dv, p.alpha, ws ? ws->data() : nullptr, stream_),
+                     "attention (one query)"));
+    p.materialised = true;
+    std::erase_if(pattn_, [&](const std::shared_ptr<PendingAttn>& q) { return q.get() == &p; });
+    return std::optional<Tensor>(out);
 }
 
 // ── deferred elementwise runs ───────────────────────────────────────────────
@@ -1596,7 +1656,11 @@ Result<void> HipEngine::sync_()
     return {};
 }
 
-Result<void> HipEngine::flush_batch() { return end_batch(); }
+// Submits the recorded work without waiting for it (the reference's CUDA
+// engine makes flush_batch a no-op; its Vulkan engine submits the command
+// buffer and records on): reads through the engine still wait for what they
+// read, and end_batch waits for everything.
+Result<void> HipEngine::flush_batch() { return settle(); }
 
 // ── factories and transfers (cpu_engine.hpp:40-72) ─────────────────────────
 Tensor HipEngine::create_tensor(std::size_t rows, std::size_t cols)
@@ -1837,27 +1901,32 @@ Result<void> HipEngine::insert_rows(Tensor& dst, std::size_t start, const Tensor
         q.placed = true;
         return {};
     }
+    // A recorded transpose of a vector holds its elements in the source's
+    // order: the row is copied from the source (a new KV-cache row in
+    // incremental inference, compute_layer.hpp:1426-1511).
+    const PendingLayout* sl = layout_of_(src);
+    const Tensor from = sl && !sl->per_batch && (sl->S.rows() == 1 || sl->S.cols() == 1) ? sl->S : src;
     PendingZero* z = nullptr;
     for (auto& e : pzero_)
         if (same_t(e.t, dst)) z = &e;
     bool src_zero = false;
     for (auto& e : pzero_)
-        if (has_buf(e.t, src.dev_ptr())) src_zero = true;
-    if (z && !src_zero && !has_buf(src, dst.dev_ptr()))
+        if (has_buf(e.t, from.dev_ptr())) src_zero = true;
+    if (z && !src_zero && !has_buf(from, dst.dev_ptr()))
     {
         NN_CHECK(settle_ew_());
-        NN_CHECK(settle_chain_reads_({&src}));
+        NN_CHECK(settle_chain_reads_({&from}));
         NN_CHECK(settle_chain_write_(dst, false, true));
         for (auto& e : pzero_)   // (the settles above leave dst's zero record in place)
             if (same_t(e.t, dst)) e.covered.emplace_back(start, start + src.rows());
     }
     else
     {
-        NN_CHECK(settle_reads_({&dst, &src}));
+        NN_CHECK(settle_reads_({&dst, &from}));
         NN_CHECK(settle_write_(dst));
     }
     if (src.size())
-        NN_CHECK(kernel_(nnhip_copy(D(src), W(dst) + start * dst.cols(), src.size(), stream_), "insert_rows"));
+        NN_CHECK(kernel_(nnhip_copy(D(from), W(dst) + start * dst.cols(), src.size(), stream_), "insert_rows"));
     return {};
 }
 
@@ -1999,9 +2068,9 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
         {
             std::unique_ptr<PendingMm> o = std::move(pmm_prev_.front());
             pmm_prev_.erase(pmm_prev_.begin());
-            if (live(o->C)) NN_CHECK(launch_mm_(*o, o->C, o->bias.size() ? &o->bias : nullptr, false));
+            NN_CHECK(launch_pending_mm_(std::move(o)));   // (may take pmm_ into its group)
         }
-        pmm_prev_.push_back(std::move(pmm_));
+        if (pmm_) pmm_prev_.push_back(std::move(pmm_));
     }
     else
         NN_CHECK(settle_mm_());
@@ -2025,9 +2094,60 @@ Result<void> HipEngine::settle_mm_prev_(const float* p, bool write)
         }
         std::unique_ptr<PendingMm> o = std::move(pmm_prev_[i]);
         pmm_prev_.erase(pmm_prev_.begin() + static_cast<std::ptrdiff_t>(i));
-        if (live(o->C)) NN_CHECK(launch_mm_(*o, o->C, o->bias.size() ? &o->bias : nullptr, false));
+        const std::size_t before = pmm_prev_.size();
+        NN_CHECK(launch_pending_mm_(std::move(o)));
+        if (pmm_prev_.size() != before) i = 0;   // partners of a grouped launch left the list
     }
     return {};
+}
+
+// A recorded matmul whose output is still referenced. A matrix-vector product
+// W x (+ bias) launches together with the other recorded ones of the same x
+// and shape (the q, k and v Linear forwards of one token in incremental
+// inference, compute_layer.hpp:1426-1511): one nnhip_gemv_group launch, the
+// same sums as separate launches.
+Result<void> HipEngine::launch_pending_mm_(std::unique_ptr<PendingMm> o)
+{
+    if (!live(o->C)) return {};
+    auto vec_form = [](const PendingMm& r) {
+        return r.N == 1 && r.M > 1 && !r.tA && !r.tB && r.plus.empty() && r.heads.size() == 0 &&
+               r.A.cols() == r.K && r.B.cols() == 1;
+    };
+    if (vec_form(*o))
+    {
+        std::vector<std::unique_ptr<PendingMm>> grp;
+        auto partner = [&](const std::unique_ptr<PendingMm>& q) {
+            return q && vec_form(*q) && same_t(q->B, o->B) && q->M == o->M && q->K == o->K && live(q->C) &&
+                   grp.size() < 3;
+        };
+        for (std::size_t i = 0; i < pmm_prev_.size();)
+            if (partner(pmm_prev_[i]))
+            {
+                grp.push_back(std::move(pmm_prev_[i]));
+                pmm_prev_.erase(pmm_prev_.begin() + static_cast<std::ptrdiff_t>(i));
+            }
+            else
+                ++i;
+        if (partner(pmm_)) grp.push_back(std::move(pmm_));
+        if (!grp.empty())
+        {
+            grp.insert(grp.begin(), std::move(o));
+            const float* R[4] = {};
+            const float* bias[4] = {};
+            float* y[4] = {};
+            for (std::size_t i = 0; i < grp.size(); ++i)
+            {
+                R[i] = D(grp[i]->A);
+                bias[i] = grp[i]->bias.size() ? D(grp[i]->bias) : nullptr;
+                y[i] = W(grp[i]->C);
+            }
+            prof_begin_();
+            const int rc = nnhip_gemv_group(R, D(grp[0]->B), bias, y, grp.size(), grp[0]->M, grp[0]->K, stream_);
+            prof_end_(grp[0]->M, 1, grp[0]->K, grp.size(), false, false);
+            return kernel_(rc, "matmul (vector group)");
+        }
+    }
+    return launch_mm_(*o, o->C, o->bias.size() ? &o->bias : nullptr, false);
 }
 
 // The recorded matmul into `out`: out = A B (+ bias per row) or out += A B;
@@ -2106,14 +2226,15 @@ Result<void> HipEngine::settle_acc_()
 Result<void> HipEngine::settle_mm_()
 {
     if (!pmm_) return {};
-    std::unique_ptr<PendingMm> r = std::move(pmm_);
-    if (!live(r->C)) return {};
-    return launch_mm_(*r, r->C, r->bias.size() ? &r->bias : nullptr, false);
+    return launch_pending_mm_(std::move(pmm_));
 }
 
 Result<void> HipEngine::launch_gemm_(const Tensor& A, const Tensor& B, Tensor& C, std::size_t batch, bool tA, bool tB,
                                      Scalar alpha, std::size_t M, std::size_t N, std::size_t K)
 {
+    // (a deferred scores product of one query may hold its key operand as a recorded transpose)
+    NN_CHECK(settle_layout_for_(A));
+    NN_CHECK(settle_layout_for_(B));
     const std::size_t wsb = nnhip_gemm_workspace_bytes(M, N, K, batch);
     std::shared_ptr<DeviceBuffer> ws;
     if (wsb)
@@ -2133,10 +2254,15 @@ Result<Tensor> HipEngine::batched_matmul(const Tensor& A, const Tensor& B, std::
 {
     NN_CHECK(check_gpu_({&A, &B}, "batched_matmul"));
     NN_TRY(d0, bdims(A, B, batch, tA, tB, "batched_matmul"));
-    (void)d0;
     NN_TRY(chained, attn_bmm_(A, B, batch, tA, tB, alpha));
     if (chained) return std::move(*chained);
-    NN_CHECK(need_gpu_({&A, &B}, "batched_matmul"));
+    // The scores of one query per batch entry (incremental inference,
+    // compute_layer.hpp:1426-1511) against keys given as a recorded transpose
+    // of the KV cache rows: the transpose stays recorded, since the one-query
+    // attention reads the cache rows in place; every other reader of the key
+    // operand (the GEMM launches, the one-pass kernels) copies it first.
+    const PendingLayout* kl = tA && !tB && d0.M == 1 ? layout_of_(B) : nullptr;
+    NN_CHECK(kl && !kl->per_batch ? need_gpu_({&A}, "batched_matmul") : need_gpu_({&A, &B}, "batched_matmul"));
     NN_TRY(d, bdims(A, B, batch, tA, tB, "batched_matmul"));
     NN_TRY(C, alloc_(batch * d.M, d.N));
     // The dP product of the attention backward (compute_layer.hpp:1306-1307) is

@@ -729,7 +729,49 @@ __device__ __forceinline__ float gemv_epilogue(float acc, float alpha, const flo
 }
 
 // y[i] = alpha * sum_k R[i][k] x[k] over rows of R (row stride ldr): one wave per output.
-template <bool VEC>
+// A row is short (a few KB) and each wave reads one, so the time is the memory
+// latency: a lane issues all its loads of up to U float4 pairs (K <= 256 U)
+// before the first multiply, and adds them in the order of k (lane q holds
+// float4 q, q + 64, ...; the wave then sums the lanes). U is the smallest of
+// 4, 8, 16 that covers K, to keep the registers (and so the waves resident
+// per SIMD) for many-row products such as the LM head.
+template <bool VEC, int U>
+__device__ __forceinline__ float gemv_row(const float* r, const float* xv, int K, unsigned lane)
+{
+    float acc = 0.0f;
+    int k = 0;
+    if constexpr (VEC)
+    {
+        const float4* r4 = reinterpret_cast<const float4*>(r);
+        const float4* x4 = reinterpret_cast<const float4*>(xv);
+        const int K4 = K / 4;
+        for (int q0 = static_cast<int>(lane); q0 < K4; q0 += 64 * U)
+        {
+            float4 a[U], v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (q0 + 64 * u < K4)
+                {
+                    a[u] = r4[q0 + 64 * u];
+                    v[u] = x4[q0 + 64 * u];
+                }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (q0 + 64 * u < K4)
+                {
+                    acc = __builtin_fmaf(a[u].x, v[u].x, acc);
+                    acc = __builtin_fmaf(a[u].y, v[u].y, acc);
+                    acc = __builtin_fmaf(a[u].z, v[u].z, acc);
+                    acc = __builtin_fmaf(a[u].w, v[u].w, acc);
+                }
+        }
+        k = 4 * K4;
+    }
+    for (int kk = k + static_cast<int>(lane); kk < K; kk += 64) acc = __builtin_fmaf(r[kk], xv[kk], acc);
+    return wave_sum(acc);
+}
+
+template <bool VEC, int U>
 __global__ __launch_bounds__(256) void k_gemv_rows(const float* __restrict__ R, long ldr, long sR,
                                                    const float* __restrict__ x, long sx, float* y, long sy, int rows,
                                                    int K, float alpha, const float* bias, int bias_each, int accum)
@@ -738,32 +780,31 @@ __global__ __launch_bounds__(256) void k_gemv_rows(const float* __restrict__ R, 
     const int i = blockIdx.x * 4 + static_cast<int>(wave);
     if (i >= rows) return;
     const long b = blockIdx.y;
-    const float* r = R + b * sR + (long)i * ldr;
-    const float* xv = x + b * sx;
-    float acc = 0.0f;
-    int k = 0;
-    if constexpr (VEC)
-    {
-        const float4* r4 = reinterpret_cast<const float4*>(r);
-        const float4* x4 = reinterpret_cast<const float4*>(xv);
-        const int K4 = K / 4;
-        for (int q = static_cast<int>(lane); q < K4; q += 64)
-        {
-            const float4 a = r4[q], v = x4[q];
-            acc = __builtin_fmaf(a.x, v.x, acc);
-            acc = __builtin_fmaf(a.y, v.y, acc);
-            acc = __builtin_fmaf(a.z, v.z, acc);
-            acc = __builtin_fmaf(a.w, v.w, acc);
-        }
-        k = 4 * K4;
-    }
-    for (int kk = k + static_cast<int>(lane); kk < K; kk += 64) acc = __builtin_fmaf(r[kk], xv[kk], acc);
-    acc = wave_sum(acc);
+    const float acc = gemv_row<VEC, U>(R + b * sR + (long)i * ldr, x + b * sx, K, lane);
     if (lane == 0)
     {
         float* out = y + b * sy + i;
         *out = gemv_epilogue(acc, alpha, bias, bias_each ? i : 0, out, accum);
     }
+}
+
+// Up to four such products of one vector x (the attention's q, k and v
+// projections of one token): member blockIdx.y, R_i (rows, K) row-major.
+struct GemvGroup
+{
+    const float* R[4];
+    const float* bias[4];
+    float* y[4];
+};
+template <bool VEC, int U>
+__global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __restrict__ x, int rows, int K)
+{
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int i = blockIdx.x * 4 + static_cast<int>(wave);
+    if (i >= rows) return;
+    const int m = blockIdx.y;
+    const float acc = gemv_row<VEC, U>(g.R[m] + (long)i * K, x, K, lane);
+    if (lane == 0) g.y[m][i] = gemv_epilogue(acc, 1.0f, g.bias[m], i, nullptr, 0);
 }
 
 // y[j] = alpha * sum_k x[k] Q[k][j] over rows of Q (row stride ldq), read along j: one thread per output,
@@ -839,12 +880,18 @@ int try_gemv(const float* A, const float* B, float* C, size_t M, size_t N, size_
     {
         const bool vec = ld % 4 == 0 && sR % 4 == 0 && sx % 4 == 0 && aligned16(R) && aligned16(x);
         const dim3 grid(static_cast<unsigned>((outs + 3) / 4), static_cast<unsigned>(batch));
-        if (vec)
-            hipLaunchKernelGGL(k_gemv_rows<true>, grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC, (int)outs,
-                               (int)K, alpha, e.bias, bias_each, e.accum);
+        if (vec && K <= 1024)
+            hipLaunchKernelGGL((k_gemv_rows<true, 4>), grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC,
+                               (int)outs, (int)K, alpha, e.bias, bias_each, e.accum);
+        else if (vec && K <= 2048)
+            hipLaunchKernelGGL((k_gemv_rows<true, 8>), grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC,
+                               (int)outs, (int)K, alpha, e.bias, bias_each, e.accum);
+        else if (vec)
+            hipLaunchKernelGGL((k_gemv_rows<true, 16>), grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC,
+                               (int)outs, (int)K, alpha, e.bias, bias_each, e.accum);
         else
-            hipLaunchKernelGGL(k_gemv_rows<false>, grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC, (int)outs,
-                               (int)K, alpha, e.bias, bias_each, e.accum);
+            hipLaunchKernelGGL((k_gemv_rows<false, 1>), grid, dim3(256), 0, s, R, ld, sR, x, sx, C, (long)sC,
+                               (int)outs, (int)K, alpha, e.bias, bias_each, e.accum);
     }
     else
     {
@@ -1115,4 +1162,36 @@ extern "C" int nnhip_batched_matmul(const float* A, const float* B, float* C, si
                                     void* stream)
 {
     return nnhip_gemm(A, B, C, A_rows, A_cols, B_rows, B_cols, batch, transA, transB, alpha, nullptr, 0, stream);
+}
+
+// Up to four matrix-vector products of one x: y_i = R_i x (+ bias_i), each
+// summed as the single product's gemv sums it (so bit-identical to
+// nnhip_gemm_epilogue of (rows, K) x (K, 1) with the same bias).
+extern "C" int nnhip_gemv_group(const float* const* R, const float* x, const float* const* bias, float* const* y,
+                                size_t count, size_t rows, size_t K, void* stream)
+{
+    if (count == 0 || rows == 0) return 0;
+    if (count > 4 || !R || !x || !y || K == 0 || K > 0x7fffffff || rows > 0x7fffffff) return -1;
+    GemvGroup g{};
+    bool vec = K % 4 == 0 && aligned16(x);
+    for (size_t i = 0; i < count; ++i)
+    {
+        if (!R[i] || !y[i]) return -1;
+        g.R[i] = R[i];
+        g.y[i] = y[i];
+        g.bias[i] = bias ? bias[i] : nullptr;
+        vec = vec && aligned16(R[i]);
+    }
+    auto s = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4), static_cast<unsigned>(count));
+    const int r = static_cast<int>(rows), k = static_cast<int>(K);
+    if (vec && K <= 1024)
+        hipLaunchKernelGGL((k_gemv_group<true, 4>), grid, dim3(256), 0, s, g, x, r, k);
+    else if (vec && K <= 2048)
+        hipLaunchKernelGGL((k_gemv_group<true, 8>), grid, dim3(256), 0, s, g, x, r, k);
+    else if (vec)
+        hipLaunchKernelGGL((k_gemv_group<true, 16>), grid, dim3(256), 0, s, g, x, r, k);
+    else
+        hipLaunchKernelGGL((k_gemv_group<false, 1>), grid, dim3(256), 0, s, g, x, r, k);
+    return launch_status();
 }

@@ -75,13 +75,27 @@ public:
     Result<Scalar> forward_sparse_resident(ComputeEngine& engine, const Tensor& logits, const Tensor& labels_t,
                                            const Tensor* mask_ptr, std::size_t vocab_size, std::size_t num_valid)
     {
+        NN_TRY(tot, forward_sparse_total(engine, logits, labels_t, mask_ptr, vocab_size, num_valid));
+        NN_TRY(host, engine.to_matrix(tot));
+        return loss_of_total(host, num_valid);
+    }
+
+    // Steps 3-4 without the host read: the (1,1) device sum of loss_vec, for a
+    // loop that reads the loss once its step's later work is queued (the value
+    // is the same; only the wait moves). loss_of_total finishes step 5.
+    Result<Tensor> forward_sparse_total(ComputeEngine& engine, const Tensor& logits, const Tensor& labels_t,
+                                        const Tensor* mask_ptr, std::size_t vocab_size, std::size_t num_valid)
+    {
         const Scalar inv = num_valid > 0 ? Scalar{1} / static_cast<Scalar>(num_valid) : Scalar{0};
         Tensor loss_vec;
         NN_TRY(grad, engine.col_softmax_sparse_forward(logits, labels_t, mask_ptr, vocab_size, inv, loss_vec));
         grad_ = grad;
-        NN_TRY(tot, engine.row_reduce_sum(loss_vec));
-        NN_TRY(host, engine.to_matrix(tot));
-        return num_valid > 0 ? -host.at_unchecked(0, 0) / static_cast<Scalar>(num_valid) : Scalar{0};
+        return engine.row_reduce_sum(loss_vec);
+    }
+
+    static Scalar loss_of_total(const Matrix& total, std::size_t num_valid)
+    {
+        return num_valid > 0 ? -total.at_unchecked(0, 0) / static_cast<Scalar>(num_valid) : Scalar{0};
     }
 
     Result<Tensor> backward() { return grad_; }

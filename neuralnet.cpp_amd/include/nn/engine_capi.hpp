@@ -368,36 +368,43 @@ inline int gpt_load_batch(GptSession* g, const float* tokens, std::size_t seq, s
     return 0;
 }
 
-inline int gpt_forward_loss(GptSession* g, float* loss)
+// Forward + CE of the loaded batch with the loss left on the device (the
+// (1,1) sum of loss_vec); flush_batch submits the work without waiting.
+inline int gpt_forward_total(GptSession* g, Tensor& total)
 {
     if (!g->has_batch) return set_error("gpt: no batch loaded");
     if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
     auto lg = g->model.forward(g->tokens);
     if (!lg) return set_error(lg.error().message);
     g->logits = *lg;
-    auto l = g->ce.forward_sparse_resident(*g->eng, g->logits, g->labels, g->has_mask ? &g->mask : nullptr, g->vocab,
-                                           g->num_valid);
-    if (!l) return set_error(l.error().message);
-    *loss = *l;
+    auto t = g->ce.forward_sparse_total(*g->eng, g->logits, g->labels, g->has_mask ? &g->mask : nullptr, g->vocab,
+                                        g->num_valid);
+    if (!t) return set_error(t.error().message);
+    total = *t;
     if (auto r = g->eng->flush_batch(); !r) return set_error(r.error().message);
     return 0;
 }
 
-inline int gpt_backward(GptSession* g)
+inline int gpt_read_loss(GptSession* g, const Tensor& total, float* loss)
 {
-    auto gr = g->ce.backward();
-    if (!gr) return set_error(gr.error().message);
-    auto b = g->model.backward(*gr);
-    if (!b) return set_error(b.error().message);
-    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
+    auto h = g->eng->to_matrix(total);
+    if (!h) return set_error(h.error().message);
+    *loss = CrossEntropyLoss::loss_of_total(*h, g->num_valid);
     return 0;
 }
 
-// Backward of one micro-batch when gradients are accumulated over several
-// (src/text_train.cpp:1242-1253): the loss gradient is scaled in place by
-// grad_scale (1 / accum_steps there) before the model backward, so the
-// accumulated gradients are the mean over the micro-batches.
-inline int gpt_backward_scaled(GptSession* g, float grad_scale)
+inline int gpt_forward_loss(GptSession* g, float* loss)
+{
+    Tensor total;
+    if (int rc = gpt_forward_total(g, total)) return rc;
+    return gpt_read_loss(g, total, loss);
+}
+
+// Backward of one micro-batch, submitted without waiting. When gradients are
+// accumulated over several (src/text_train.cpp:1242-1253) the loss gradient
+// is scaled in place by grad_scale (1 / accum_steps there) before the model
+// backward, so the accumulated gradients are the mean over the micro-batches.
+inline int gpt_backward_queued(GptSession* g, float grad_scale)
 {
     auto gr = g->ce.backward();
     if (!gr) return set_error(gr.error().message);
@@ -405,9 +412,18 @@ inline int gpt_backward_scaled(GptSession* g, float grad_scale)
         if (auto r = g->eng->scale_inplace(*gr, grad_scale); !r) return set_error(r.error().message);
     auto b = g->model.backward(*gr);
     if (!b) return set_error(b.error().message);
+    if (auto r = g->eng->flush_batch(); !r) return set_error(r.error().message);
+    return 0;
+}
+
+inline int gpt_backward_scaled(GptSession* g, float grad_scale)
+{
+    if (int rc = gpt_backward_queued(g, grad_scale)) return rc;
     if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
     return 0;
 }
+
+inline int gpt_backward(GptSession* g) { return gpt_backward_scaled(g, 1.0f); }
 
 // Global L2-norm gradient clipping (Optimizer::clip_grad_norm,
 // compute_optimizer.hpp:90-140); max_norm <= 0 leaves the gradients alone.
@@ -419,23 +435,28 @@ inline int gpt_clip_grad_norm(GptSession* g, float max_norm)
 
 // One iteration of the reference training loop (src/text_train.cpp:1181-1330):
 // forward + CE (flush), backward with the loss gradient scaled by
-// 1 / accum_steps when accum_steps > 1 (end_batch); then, when do_update,
+// 1 / accum_steps when accum_steps > 1; then, when do_update,
 // clip_grad_norm(max_norm) if max_norm > 0, and begin_batch, AdamW step,
-// zero_grad, end_batch.
+// zero_grad, end_batch. The work is submitted phase by phase and waited for
+// once, at the end, where the loss is read: the host records the backward
+// and the update while the GPU still runs the forward.
 inline int gpt_train_step_ex(GptSession* g, std::size_t accum_steps, float max_norm, int do_update, float* loss)
 {
     if (accum_steps == 0) return set_error("gpt: accum_steps must be at least 1");
-    if (int rc = gpt_forward_loss(g, loss)) return rc;
+    Tensor total;
+    if (int rc = gpt_forward_total(g, total)) return rc;
     const float scale = accum_steps > 1 ? 1.0f / static_cast<float>(accum_steps) : 1.0f;
-    if (int rc = gpt_backward_scaled(g, scale)) return rc;
-    if (!do_update) return 0;
-    if (max_norm > 0)
-        if (int rc = gpt_clip_grad_norm(g, max_norm)) return rc;
-    if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
-    if (auto r = g->opt->step(); !r) return set_error(r.error().message);
-    if (auto r = g->opt->zero_grad(); !r) return set_error(r.error().message);
+    if (int rc = gpt_backward_queued(g, scale)) return rc;
+    if (do_update)
+    {
+        if (max_norm > 0)
+            if (int rc = gpt_clip_grad_norm(g, max_norm)) return rc;
+        if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
+        if (auto r = g->opt->step(); !r) return set_error(r.error().message);
+        if (auto r = g->opt->zero_grad(); !r) return set_error(r.error().message);
+    }
     if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
-    return 0;
+    return gpt_read_loss(g, total, loss);
 }
 
 // The ModelSpec this session's model is built from (model_spec.hpp:58-77).
@@ -589,16 +610,7 @@ inline int gpt_zero_grad(GptSession* g)
     return 0;
 }
 
-inline int gpt_train_step(GptSession* g, float* loss)
-{
-    if (int rc = gpt_forward_loss(g, loss)) return rc;
-    if (int rc = gpt_backward(g)) return rc;
-    if (auto r = g->eng->begin_batch(); !r) return set_error(r.error().message);
-    if (auto r = g->opt->step(); !r) return set_error(r.error().message);
-    if (auto r = g->opt->zero_grad(); !r) return set_error(r.error().message);
-    if (auto r = g->eng->end_batch(); !r) return set_error(r.error().message);
-    return 0;
-}
+inline int gpt_train_step(GptSession* g, float* loss) { return gpt_train_step_ex(g, 1, 0.0f, 1, loss); }
 
 // One training batch cut from a token flow, as src/text_train.cpp:1137-1172
 // builds it: window b starts at flow offset starts[b] and holds

@@ -10,8 +10,9 @@
 //
 // Ordering: all work goes to one in-order stream, so a buffer released by a
 // Tensor can be handed to the next allocation immediately (stream-ordered
-// reuse). to_matrix and end_batch / flush_batch synchronise the stream,
-// matching the reference's batch semantics (compute_engine.hpp:93-118);
+// reuse). to_matrix and end_batch synchronise the stream, matching the
+// reference's batch semantics (compute_engine.hpp:93-118); flush_batch
+// submits the recorded work without waiting for it;
 // from_matrix / copy_from copy small host data into a pinned staging slot and
 // return once the upload is queued (larger data is uploaded and waited for).
 //
@@ -237,6 +238,7 @@ private:
     std::vector<std::unique_ptr<PendingMm>> pmm_prev_;
     Result<void> settle_mm_();
     Result<void> settle_mm_prev_(const float* p, bool write);
+    Result<void> launch_pending_mm_(std::unique_ptr<PendingMm> o);
     Result<void> launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate);
     PendingMm* pending_mm_(const Tensor& t);
     struct PendingAcc;
@@ -256,6 +258,7 @@ private:
     Result<void> settle_dv_();
     Result<void> settle_ds_();
     Result<void> materialise_attn_(PendingAttn& p);
+    Result<std::optional<Tensor>> attn_query_(PendingAttn& p, const Tensor& V, std::size_t Dv);
     void forget_dead_attn_();
     std::shared_ptr<PendingAttn> attn_of_(const Tensor& A) const;
     Result<void> scores_masked_(const Tensor& Q, const Tensor& K, const Tensor& mask, std::size_t batch, std::size_t M,
@@ -271,6 +274,7 @@ private:
     Result<void> materialise_layout_(const PendingLayout& r);
     Result<void> settle_layout_();
     const PendingLayout* layout_of_(const Tensor& t) const;
+    Result<void> settle_layout_for_(const Tensor& t);
     // A row sum not launched yet (a Linear bias gradient, RMSNorm's gamma gradient).
     struct PendingRowSum;
     std::unique_ptr<PendingRowSum> prsum_;
