@@ -83,12 +83,33 @@ int nnhip_gemm_epilogue(const float* A, const float* B, float* C, size_t A_rows,
                         size_t B_cols, int transA, int transB, float alpha, const float* row_bias, int accumulate,
                         void* workspace, size_t workspace_bytes, void* stream);
 
-/* Up to four products y_i (rows) = R_i (rows, K) x (+ bias_i) of one vector x in one launch, count in 1..4,
- * bias NULL or with NULL entries: the q, k and v Linear forwards of one token in incremental inference
- * (compute_layer.hpp:1426-1511 calls w_q, w_k, w_v on the same x_new). Each y_i is bit-identical to
- * nnhip_gemm_epilogue(R_i, x, y_i, rows, K, K, 1, 0, 0, 1.0f, bias_i, 0, ...). No CUDA counterpart. */
-int nnhip_gemv_group(const float* const* R, const float* x, const float* const* bias, float* const* y, size_t count,
-                     size_t rows, size_t K, void* stream);
+/* Up to four products v_i (rows) = R_i (rows, K) x (+ bias_i) of one vector x in one launch, count in 1..4:
+ * the q, k and v Linear forwards of one token in incremental inference (compute_layer.hpp:1426-1511 calls
+ * w_q, w_k, w_v on the same x_new). v_i goes to y_i and, when out_i is set, out_i = add_i + v_i (add_i set:
+ * the block's residual add, compute_layer.hpp:2413-2437) or out_i = v_i (a copy, e.g. into the KV cache row
+ * of insert_rows). bias, y, add, out: NULL or arrays with NULL entries; each member needs y_i or out_i.
+ * Each v_i is bit-identical to nnhip_gemm_epilogue(R_i, x, y_i, rows, K, K, 1, 0, 0, 1.0f, bias_i, 0, ...),
+ * and add_i + v_i to the separate add. No CUDA counterpart. */
+int nnhip_gemv_group(const float* const* R, const float* x, const float* const* bias, float* const* y,
+                     const float* const* add, float* const* out, size_t count, size_t rows, size_t K, void* stream);
+/* The same products of y = RMSNorm(x) instead of x (the block's norm before the q, k, v projections,
+ * compute_layer.hpp:2413-2437): y is what nnhip_rmsnorm_forward(x, gamma, inv_f, eps, ...) gives for the
+ * (K, 1) column x, bit for bit, and the RMSNorm outputs whose pointers are set here are written as that
+ * call writes them. K <= 1024. No CUDA counterpart. */
+typedef struct nnhip_gemv_rmsnorm
+{
+    const float* gamma;   /* (K) */
+    float inv_f, eps;
+    float* s_raw;         /* (1) each of these may be NULL */
+    float* scaled;
+    float* var_eps;
+    float* rinv;
+    float* normed;        /* (K) */
+    float* out;           /* (K): y */
+} nnhip_gemv_rmsnorm;
+int nnhip_gemv_group_rmsnorm(const float* const* R, const float* x, const nnhip_gemv_rmsnorm* rms,
+                             const float* const* bias, float* const* y, const float* const* add, float* const* out,
+                             size_t count, size_t rows, size_t K, void* stream);
 
 /* nnhip_gemm that allocates nothing and takes no workspace. No counterpart in the reference: it is for
  * callers that cannot allocate device memory or hand in a workspace (code under HIP graph capture, tight

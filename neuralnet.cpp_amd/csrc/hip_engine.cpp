@@ -354,12 +354,19 @@ struct HipEngine::PendingMm
     // Further products A^T B of the same shape added into C (add_inplace(C, their outputs)): C is their
     // sum, computed as one product over the concatenated K (transposed A only).
     std::vector<std::pair<Tensor, Tensor>> plus;
+    // A matrix-vector product's second destination: out2 (from element out2_off) = addx + C (the block's
+    // residual add) or, without addx, a copy of C (insert_rows of C's transpose into a KV cache).
+    Tensor out2, addx;
+    std::size_t out2_off = 0;
     bool uses(const float* p) const
     {
         for (const auto& [a, b] : plus)
             if (has_buf(a, p) || has_buf(b, p)) return true;
-        return has_buf(A, p) || has_buf(B, p) || has_buf(C, p) || has_buf(bias, p);
+        return has_buf(A, p) || has_buf(B, p) || has_buf(C, p) || has_buf(bias, p) || has_buf(out2, p) ||
+               has_buf(addx, p);
     }
+    bool yields(const float* p) const { return has_buf(C, p) || has_buf(out2, p); }
+    bool needed() const { return live(C) || (out2.size() && live(out2)); }
 };
 
 // Weight-gradient accumulations C_i += A_i op(B) (Linear::backward's
@@ -525,17 +532,19 @@ struct HipEngine::PendingRms
 {
     bool bwd = false;
     Tensor x, s, scaled, var_eps, rinv, normed;
-    Tensor gamma;   // bwd: with x = g and normed, an input
+    Tensor gamma;   // bwd: with x = g and normed, an input; forward stage 6: the scale
+    Tensor y;       // forward stage 6 (one column): the output, normed * gamma
     float inv_f = 0.0f, eps = 0.0f;
     int stage = 1;
     bool yields(const float* p) const
     {
         if (bwd) return has_buf(s, p) || has_buf(scaled, p);
-        return has_buf(s, p) || has_buf(scaled, p) || has_buf(var_eps, p) || has_buf(rinv, p) || has_buf(normed, p);
+        return has_buf(s, p) || has_buf(scaled, p) || has_buf(var_eps, p) || has_buf(rinv, p) || has_buf(normed, p) ||
+               has_buf(y, p);
     }
     bool uses(const float* p) const
     {
-        return has_buf(x, p) || yields(p) || (bwd && (has_buf(gamma, p) || has_buf(normed, p)));
+        return has_buf(x, p) || yields(p) || has_buf(gamma, p) || (bwd && has_buf(normed, p));
     }
 };
 
@@ -807,7 +816,7 @@ Result<void> HipEngine::settle_chain_reads_(std::initializer_list<const Tensor*>
         NN_CHECK(settle_zero_for_(*t));
         if (pacc_ && pacc_->yields(p)) NN_CHECK(settle_acc_());
         if (!keep_flash && flash_yields_(p)) NN_CHECK(settle_flash_());
-        if (pmm_ && has_buf(pmm_->C, p)) NN_CHECK(settle_mm_());
+        if (pmm_ && pmm_->yields(p)) NN_CHECK(settle_mm_());
         if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(p, false));
         for (const auto& r : pswb_)
             if (has_buf(r.out, p) || (r.placed && has_buf(r.dst, p)))
@@ -1165,6 +1174,12 @@ Result<void> HipEngine::push_layout_(PendingLayout r)
 
 Result<void> HipEngine::materialise_layout_(const PendingLayout& r)
 {
+    // (the source may be a recorded matrix-vector product, see transpose)
+    if (const float* sp = r.S.dev_ptr(); sp)
+    {
+        if (pmm_ && pmm_->yields(sp)) NN_CHECK(settle_mm_());
+        if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(sp, false));
+    }
     if (!r.per_batch)
         return kernel_(nnhip_transpose(D(r.S), W(r.out), r.S.rows(), r.S.cols(), stream_), "transpose");
     return kernel_(nnhip_transpose_batched(D(r.S), W(r.out), r.B, r.N, r.M, stream_), "rearrange_3d");
@@ -1389,8 +1404,10 @@ Result<std::optional<Tensor>> HipEngine::attn_query_(PendingAttn& p, const Tenso
     };
     const Tensor* ks = rows_of(p.K, Kd);
     const Tensor* vs = rows_of(V, Dv);
-    if (!ks) NN_CHECK(settle_layout_for_(p.K));
-    if (!vs) NN_CHECK(settle_reads_({&V}));
+    if (ks) NN_CHECK(settle_chain_reads_({ks}));
+    else NN_CHECK(settle_layout_for_(p.K));
+    if (vs) NN_CHECK(settle_chain_reads_({vs}));
+    else NN_CHECK(settle_reads_({&V}));
     const long kb = ks ? (long)Kd : (long)(Kd * N), kj = ks ? (long)ks->cols() : 1L, kk = ks ? 1L : (long)N;
     const long vb = vs ? (long)Dv : (long)(Dv * N), vj = vs ? (long)vs->cols() : 1L, vd = vs ? 1L : (long)N;
     const bool has_mask = p.mask.size() > 0;
@@ -1909,6 +1926,19 @@ Result<void> HipEngine::insert_rows(Tensor& dst, std::size_t start, const Tensor
     PendingZero* z = nullptr;
     for (auto& e : pzero_)
         if (same_t(e.t, dst)) z = &e;
+    // When that source is a recorded matrix-vector product (the k or v
+    // projection), the product writes the row itself when it runs.
+    if (!z && src.rows() == 1 && vec_record_(from) && !has_buf(from, dst.dev_ptr()))
+    {
+        NN_CHECK(settle_ew_());
+        NN_CHECK(settle_chain_write_(dst));
+        if (PendingMm* r = vec_record_(from); r && !r->uses(dst.dev_ptr()))
+        {
+            r->out2 = dst;
+            r->out2_off = start * dst.cols();
+            return {};
+        }
+    }
     bool src_zero = false;
     for (auto& e : pzero_)
         if (has_buf(e.t, from.dev_ptr())) src_zero = true;
@@ -1983,7 +2013,8 @@ Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size
         }
         // A launch covers members x B sequences in grid z (at most 65535).
         auto fits = [&](const PendingMm& q) {
-            return !q.folded && !q.tA && !q.tB && q.M == M && q.N == B * N && q.K < 1024 && B <= 65535 &&
+            return !q.folded && !q.out2.size() && !q.tA && !q.tB && q.M == M && q.N == B * N && q.K < 1024 &&
+                   B <= 65535 &&
                    aligned16(q.A.dev_ptr()) && (!q.bias.size() || aligned16(q.bias.dev_ptr()));
         };
         if (r && fits(*r) && x.rows() == M)
@@ -2037,7 +2068,10 @@ Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size
 // of the result launches the copy.
 Result<Tensor> HipEngine::transpose(const Tensor& A)
 {
-    NN_CHECK(need_gpu_({&A}, "transpose"));
+    // A recorded matrix-vector product stays recorded (its transpose is the
+    // same vector, which insert_rows may take as the product's second
+    // destination); making the copy runs it first.
+    NN_CHECK(vec_record_(A) ? check_gpu_({&A}, "transpose") : need_gpu_({&A}, "transpose"));
     NN_TRY(out, alloc_(A.cols(), A.rows()));
     if (out.size() == 0) return out;
     NN_CHECK(push_layout_(PendingLayout{A, out, false, 0, 0, 0}));
@@ -2047,7 +2081,11 @@ Result<Tensor> HipEngine::transpose(const Tensor& A)
 // ── GEMM (cpu_engine.hpp:293-419) ───────────────────────────────────────────
 Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool tB)
 {
-    NN_CHECK(need_gpu_({&A, &B}, "matmul"));
+    // A recorded RMSNorm column as the vector of W x stays recorded: the
+    // product normalises it itself when it runs (launch_pending_mm_).
+    const bool rms_x = !tA && !tB && B.cols() == 1 && prms_ && !prms_->bwd && prms_->stage == 6 && same_t(prms_->y, B);
+    NN_CHECK(rms_x ? need_gpu_({&A}, "matmul") : need_gpu_({&A, &B}, "matmul"));
+    NN_CHECK(check_gpu_({&B}, "matmul"));
     const std::size_t M = tA ? A.cols() : A.rows(), K = tA ? A.rows() : A.cols();
     const std::size_t K2 = tB ? B.cols() : B.rows(), N = tB ? B.rows() : B.cols();
     if (K != K2)
@@ -2060,9 +2098,9 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
     // product's epilogue; any other use launches the plain product.
     // An earlier record that this product does not read stays recorded (its
     // output may go straight into the heads' layout, see rearrange_3d).
-    std::erase_if(pmm_prev_, [](const std::unique_ptr<PendingMm>& r) { return !live(r->C); });
+    std::erase_if(pmm_prev_, [](const std::unique_ptr<PendingMm>& r) { return !r->needed(); });
     constexpr std::size_t kKeepPrev = 4;
-    if (pmm_ && !has_buf(pmm_->C, A.dev_ptr()) && !has_buf(pmm_->C, B.dev_ptr()))
+    if (pmm_ && !pmm_->yields(A.dev_ptr()) && !pmm_->yields(B.dev_ptr()))
     {
         if (pmm_prev_.size() >= kKeepPrev)
         {
@@ -2086,7 +2124,7 @@ Result<void> HipEngine::settle_mm_prev_(const float* p, bool write)
     for (std::size_t i = 0; i < pmm_prev_.size();)
     {
         PendingMm& r = *pmm_prev_[i];
-        const bool hit = !p || (write ? r.uses(p) : has_buf(r.C, p));
+        const bool hit = !p || (write ? r.uses(p) : r.yields(p));
         if (!hit)
         {
             ++i;
@@ -2108,7 +2146,7 @@ Result<void> HipEngine::settle_mm_prev_(const float* p, bool write)
 // same sums as separate launches.
 Result<void> HipEngine::launch_pending_mm_(std::unique_ptr<PendingMm> o)
 {
-    if (!live(o->C)) return {};
+    if (!o->needed()) return {};
     auto vec_form = [](const PendingMm& r) {
         return r.N == 1 && r.M > 1 && !r.tA && !r.tB && r.plus.empty() && r.heads.size() == 0 &&
                r.A.cols() == r.K && r.B.cols() == 1;
@@ -2117,7 +2155,7 @@ Result<void> HipEngine::launch_pending_mm_(std::unique_ptr<PendingMm> o)
     {
         std::vector<std::unique_ptr<PendingMm>> grp;
         auto partner = [&](const std::unique_ptr<PendingMm>& q) {
-            return q && vec_form(*q) && same_t(q->B, o->B) && q->M == o->M && q->K == o->K && live(q->C) &&
+            return q && vec_form(*q) && same_t(q->B, o->B) && q->M == o->M && q->K == o->K && q->needed() &&
                    grp.size() < 3;
         };
         for (std::size_t i = 0; i < pmm_prev_.size();)
@@ -2129,20 +2167,41 @@ Result<void> HipEngine::launch_pending_mm_(std::unique_ptr<PendingMm> o)
             else
                 ++i;
         if (partner(pmm_)) grp.push_back(std::move(pmm_));
-        if (!grp.empty())
+        const bool rms = prms_ && !prms_->bwd && prms_->stage == 6 && same_t(prms_->y, o->B) && o->K <= 1024 &&
+                         o->M <= 8192;
+        if (!grp.empty() || o->out2.size() || rms)
         {
             grp.insert(grp.begin(), std::move(o));
             const float* R[4] = {};
             const float* bias[4] = {};
+            const float* add[4] = {};
             float* y[4] = {};
+            float* out[4] = {};
             for (std::size_t i = 0; i < grp.size(); ++i)
             {
-                R[i] = D(grp[i]->A);
-                bias[i] = grp[i]->bias.size() ? D(grp[i]->bias) : nullptr;
-                y[i] = W(grp[i]->C);
+                const PendingMm& q = *grp[i];
+                R[i] = D(q.A);
+                bias[i] = q.bias.size() ? D(q.bias) : nullptr;
+                y[i] = live(q.C) ? W(q.C) : nullptr;
+                out[i] = q.out2.size() ? W(q.out2) + q.out2_off : nullptr;
+                add[i] = q.addx.size() ? D(q.addx) : nullptr;
             }
             prof_begin_();
-            const int rc = nnhip_gemv_group(R, D(grp[0]->B), bias, y, grp.size(), grp[0]->M, grp[0]->K, stream_);
+            int rc = 0;
+            if (rms)
+            {
+                // RMSNorm's outputs come from workgroup (0, 0) of the same launch.
+                std::unique_ptr<PendingRms> q = std::move(prms_);
+                const nnhip_gemv_rmsnorm rn{D(q->gamma), q->inv_f, q->eps, W(q->s), W(q->scaled), W(q->var_eps),
+                                            W(q->rinv), W(q->normed), W(q->y)};
+                rc = nnhip_gemv_group_rmsnorm(R, D(q->x), &rn, bias, y, add, out, grp.size(), grp[0]->M, grp[0]->K,
+                                              stream_);
+            }
+            else
+            {
+                NN_CHECK(settle_chain_reads_({&grp[0]->B}));
+                rc = nnhip_gemv_group(R, D(grp[0]->B), bias, y, add, out, grp.size(), grp[0]->M, grp[0]->K, stream_);
+            }
             prof_end_(grp[0]->M, 1, grp[0]->K, grp.size(), false, false);
             return kernel_(rc, "matmul (vector group)");
         }
@@ -2154,6 +2213,7 @@ Result<void> HipEngine::launch_pending_mm_(std::unique_ptr<PendingMm> o)
 // with added products, out = sum of A_i^T B_i in one launch.
 Result<void> HipEngine::launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate)
 {
+    NN_CHECK(settle_chain_reads_({&r.B}));   // (a recorded RMSNorm column, see matmul)
     if (!r.plus.empty())
     {
         if (bias || accumulate) return fail("matmul: a summed product takes no epilogue");
@@ -2578,7 +2638,8 @@ Result<Tensor> HipEngine::col_softmax_sparse_forward(const Tensor& logits, const
     NN_CHECK(check_gpu_({&logits, &labels, mask}, "col_softmax_sparse_forward"));
     // Logits still recorded as a product (the lm_head Linear): the product's
     // epilogue leaves per-tile column statistics, so the logits are read once.
-    if (pmm_ && !pmm_->folded && same_t(logits, pmm_->C) && !pmm_->uses(labels.dev_ptr()) &&
+    if (pmm_ && !pmm_->folded && !pmm_->out2.size() && same_t(logits, pmm_->C) &&
+        !pmm_->uses(labels.dev_ptr()) &&
         !(mask && pmm_->uses(mask->dev_ptr())) && vocab <= (std::size_t{1} << 24) && vocab <= logits.rows() &&
         labels.rows() == 1 && labels.cols() == logits.cols() && (!mask || (mask->rows() == 1 && mask->cols() == logits.cols())))
     {
@@ -2635,7 +2696,8 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
     NN_CHECK(check_gpu_({&A, &B}, "add_inplace"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("add_inplace: shape mismatch");
     if (!A.size()) return {};
-    if (pmm_ && !pmm_->folded && !pmm_->bias.size() && pmm_->plus.empty() && same_t(B, pmm_->C) &&
+    if (pmm_ && !pmm_->folded && !pmm_->bias.size() && pmm_->plus.empty() && !pmm_->out2.size() &&
+        same_t(B, pmm_->C) &&
         !pmm_->uses(A.dev_ptr()))
     {
         // Linear backward: the weight-gradient accumulation becomes the
@@ -2703,10 +2765,26 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
     return ew_push_(kBin, static_cast<unsigned>(BinaryOp::Add), false, A, A, &B, 0.0f);
 }
 
+// The recorded matrix-vector product W x (+ bias) whose output is t and that
+// has no second destination yet, if any.
+HipEngine::PendingMm* HipEngine::vec_record_(const Tensor& t)
+{
+    auto ok = [&](PendingMm* r) {
+        return r && !r->folded && same_t(r->C, t) && r->N == 1 && r->M > 1 && !r->tA && !r->tB && r->plus.empty() &&
+               !r->heads.size() && !r->out2.size() && r->A.cols() == r->K && r->B.cols() == 1;
+    };
+    if (ok(pmm_.get())) return pmm_.get();
+    for (auto& q : pmm_prev_)
+        if (ok(q.get())) return q.get();
+    return nullptr;
+}
+
 // The recorded, not yet folded plain product whose output is t, if any.
 HipEngine::PendingMm* HipEngine::pending_mm_(const Tensor& t)
 {
-    auto ok = [&](PendingMm* r) { return r && !r->folded && same_t(r->C, t) && !r->heads.size(); };
+    auto ok = [&](PendingMm* r) {
+        return r && !r->folded && same_t(r->C, t) && !r->heads.size() && !r->out2.size();
+    };
     if (ok(pmm_.get())) return pmm_.get();
     for (auto& q : pmm_prev_)
         if (ok(q.get())) return q.get();
@@ -2886,7 +2964,8 @@ Result<void> HipEngine::broadcast_row_inplace(Tensor& A, const Tensor& v, Binary
 {
     NN_CHECK(check_gpu_({&A, &v}, "broadcast_row_inplace"));
     if (op == BinaryOp::Add && pmm_ && !pmm_->folded && !pmm_->bias.size() && pmm_->plus.empty() &&
-        same_t(A, pmm_->C) && v.rows() == A.rows() && v.cols() == 1 && v.size() && !pmm_->uses(v.dev_ptr()))
+        !pmm_->out2.size() && same_t(A, pmm_->C) && v.rows() == A.rows() && v.cols() == 1 && v.size() &&
+        !pmm_->uses(v.dev_ptr()))
     {
         // Linear forward: the bias add becomes the product's epilogue. The
         // product stays recorded: when the sparse cross-entropy reads it next
@@ -2935,6 +3014,25 @@ Result<Tensor> HipEngine::elementwise_binary(BinaryOp op, const Tensor& A, const
     NN_CHECK(check_gpu_({&A, &B}, "elementwise_binary"));
     if (A.rows() != B.rows() || A.cols() != B.cols()) return fail("elementwise_binary: shape mismatch");
     if (static_cast<unsigned>(op) > static_cast<unsigned>(BinaryOp::Min)) return fail("elementwise_binary: bad op");
+    // x + (W v + bias) of a recorded matrix-vector product (the residual adds of
+    // a block in incremental inference, compute_layer.hpp:2413-2437): the
+    // product writes the sum as well when it runs (the same rounding).
+    if (op == BinaryOp::Add && A.cols() == 1 && A.size() && !has_buf(A, B.dev_ptr()) &&
+        (vec_record_(A) || vec_record_(B)))
+    {
+        const Tensor& X = vec_record_(B) ? A : B;
+        const Tensor& Cv = vec_record_(B) ? B : A;
+        NN_CHECK(settle_ew_());
+        NN_CHECK(settle_chain_reads_({&X}));
+        if (PendingMm* r = vec_record_(Cv); r && !r->uses(X.dev_ptr()))
+        {
+            NN_TRY(o, alloc_(A.rows(), 1));
+            r->addx = X;
+            r->out2 = o;
+            r->out2_off = 0;
+            return o;
+        }
+    }
     // scores + mask of a deferred scores product (materialised attention): recorded.
     if (op == BinaryOp::Add && pgemm_ && same_t(A, pgemm_->C) && !has_buf(B, A.dev_ptr()) && A.size() &&
         pgemm_->N == B.cols() && pgemm_->K <= 64)
@@ -3177,6 +3275,16 @@ Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std:
         if (!gamma || gamma->rows() != rows || gamma->cols() != 1 || prms_->uses(a[1])) return R();
         NN_CHECK(settle_reads_({gamma}));
         if (!prms_ || prms_->stage != 5) return R();
+        if (cols == 1 && rows <= 1024)
+        {
+            // One token's column: recorded, so that the matrix-vector products
+            // reading it can normalise it themselves (launch_pending_mm_).
+            NN_TRY(o, alloc_(rows, cols));
+            prms_->gamma = *gamma;
+            prms_->y = o;
+            prms_->stage = 6;
+            return R(o);
+        }
         std::unique_ptr<PendingRms> q = std::move(prms_);
         NN_TRY(o, alloc_(rows, cols));
         NN_CHECK(kernel_(nnhip_rmsnorm_forward(D(q->x), D(*gamma), q->inv_f, q->eps, W(q->s), W(q->scaled),
@@ -3203,6 +3311,10 @@ Result<void> HipEngine::settle_rms_()
                              "elementwise_binary_scalar"));
         return {};
     }
+    if (r->stage == 6)
+        return kernel_(nnhip_rmsnorm_forward(D(r->x), D(r->gamma), r->inv_f, r->eps, W(r->s), W(r->scaled),
+                                             W(r->var_eps), W(r->rinv), W(r->normed), W(r->y), F, N, stream_),
+                       "rmsnorm forward");
     NN_CHECK(kernel_(nnhip_rmsnorm_sumsq(D(r->x), W(r->s), F, N, stream_), "eval_expr_reduce(rmsnorm sum of squares)"));
     if (r->stage >= 2)
         NN_CHECK(kernel_(nnhip_elementwise_binary_scalar(D(r->s), W(r->scaled), N, static_cast<unsigned>(BinaryOp::Mul),

@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256) void k_attn_query(QueryArgs a)
         for (int u = 0; u < kQChunk / 16; ++u)
         {
             const int jj = g + 16 * u;
-            if (jj >= nk) break;
+            if (jj >= nk) continue;
             const float w = ps[jj];
             float4 v;
             if constexpr (VV)

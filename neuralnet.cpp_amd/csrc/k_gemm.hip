@@ -790,21 +790,94 @@ __global__ __launch_bounds__(256) void k_gemv_rows(const float* __restrict__ R, 
 
 // Up to four such products of one vector x (the attention's q, k and v
 // projections of one token): member blockIdx.y, R_i (rows, K) row-major.
+// Member m writes v = R_m x (+ bias) to y[m] (when set) and to out[m] (when
+// set; plus add[m], when set: the residual add x_new + v that follows a
+// projection, or a copy of v into a KV-cache row).
 struct GemvGroup
 {
     const float* R[4];
     const float* bias[4];
     float* y[4];
+    const float* add[4];
+    float* out[4];
 };
-template <bool VEC, int U>
-__global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __restrict__ x, int rows, int K)
+// RMS: x is first normalised as RMSNorm::forward's six calls on a (K, 1)
+// column do it (the narrow kernel of nnhip_rmsnorm_forward: the same sums in
+// the same order, so the same bits): y = x / sqrt(sum(x^2) inv_f + eps) *
+// gamma, into LDS for the products; workgroup (0, 0) also stores the
+// RMSNorm outputs that are asked for.
+template <bool VEC, int U, bool RMS>
+__global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __restrict__ x, int rows, int K,
+                                                    nnhip_gemv_rmsnorm rn)
 {
     const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const float* xv = x;
+    if constexpr (RMS)
+    {
+        __shared__ __align__(16) float xs[1024];
+        __shared__ float part[4];
+        const unsigned t = threadIdx.x;
+        float v[4];
+#pragma unroll
+        for (unsigned k = 0; k < 4; ++k)
+        {
+            const unsigned r = t + k * 256;
+            v[k] = r < static_cast<unsigned>(K) ? x[r] : 0.0f;
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (unsigned k = 0; k < 4; ++k)
+            if (t + k * 256 < static_cast<unsigned>(K)) acc = __builtin_fmaf(v[k], v[k], acc);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (lane == 0) part[wave] = acc;
+        __syncthreads();
+        float sum = part[0];
+#pragma unroll
+        for (unsigned w = 1; w < 4; ++w) sum += part[w];
+        const bool first = blockIdx.x == 0 && blockIdx.y == 0;
+        float ri;
+        {
+#pragma clang fp contract(off)
+            const float sc = sum * rn.inv_f, ve = sc + rn.eps;
+            ri = 1.0f / sqrtf(ve);
+            if (first && t == 0)
+            {
+                if (rn.s_raw) rn.s_raw[0] = sum;
+                if (rn.scaled) rn.scaled[0] = sc;
+                if (rn.var_eps) rn.var_eps[0] = ve;
+                if (rn.rinv) rn.rinv[0] = ri;
+            }
+        }
+#pragma unroll
+        for (unsigned k = 0; k < 4; ++k)
+        {
+            const unsigned r = t + k * 256;
+            if (r < static_cast<unsigned>(K))
+            {
+#pragma clang fp contract(off)
+                const float n = v[k] * ri, y = n * rn.gamma[r];
+                xs[r] = y;
+                if (first)
+                {
+                    if (rn.normed) rn.normed[r] = n;
+                    if (rn.out) rn.out[r] = y;
+                }
+            }
+        }
+        __syncthreads();
+        xv = xs;
+    }
     const int i = blockIdx.x * 4 + static_cast<int>(wave);
     if (i >= rows) return;
     const int m = blockIdx.y;
-    const float acc = gemv_row<VEC, U>(g.R[m] + (long)i * K, x, K, lane);
-    if (lane == 0) g.y[m][i] = gemv_epilogue(acc, 1.0f, g.bias[m], i, nullptr, 0);
+    const float acc = gemv_row<VEC, U>(g.R[m] + (long)i * K, xv, K, lane);
+    if (lane == 0)
+    {
+        const float v = gemv_epilogue(acc, 1.0f, g.bias[m], i, nullptr, 0);
+        if (g.y[m]) g.y[m][i] = v;
+        if (g.out[m]) g.out[m][i] = g.add[m] ? g.add[m][i] + v : v;
+    }
 }
 
 // y[j] = alpha * sum_k x[k] Q[k][j] over rows of Q (row stride ldq), read along j: one thread per output,
@@ -1164,34 +1237,63 @@ extern "C" int nnhip_batched_matmul(const float* A, const float* B, float* C, si
     return nnhip_gemm(A, B, C, A_rows, A_cols, B_rows, B_cols, batch, transA, transB, alpha, nullptr, 0, stream);
 }
 
-// Up to four matrix-vector products of one x: y_i = R_i x (+ bias_i), each
+// Up to four matrix-vector products of one x: v_i = R_i x (+ bias_i), each
 // summed as the single product's gemv sums it (so bit-identical to
-// nnhip_gemm_epilogue of (rows, K) x (K, 1) with the same bias).
-extern "C" int nnhip_gemv_group(const float* const* R, const float* x, const float* const* bias, float* const* y,
-                                size_t count, size_t rows, size_t K, void* stream)
+// nnhip_gemm_epilogue of (rows, K) x (K, 1) with the same bias), written to
+// y_i and / or out_i (= add_i + v_i when add_i is set).
+namespace
+{
+int gemv_group(const float* const* R, const float* x, const nnhip_gemv_rmsnorm* rms, const float* const* bias,
+               float* const* y, const float* const* add, float* const* out, size_t count, size_t rows, size_t K,
+               void* stream)
 {
     if (count == 0 || rows == 0) return 0;
-    if (count > 4 || !R || !x || !y || K == 0 || K > 0x7fffffff || rows > 0x7fffffff) return -1;
+    if (count > 4 || !R || !x || (!y && !out) || K == 0 || K > 0x7fffffff || rows > 0x7fffffff) return -1;
+    if (rms && (K > 1024 || !rms->gamma)) return -1;
     GemvGroup g{};
-    bool vec = K % 4 == 0 && aligned16(x);
+    bool vec = K % 4 == 0 && (rms || aligned16(x));
     for (size_t i = 0; i < count; ++i)
     {
-        if (!R[i] || !y[i]) return -1;
         g.R[i] = R[i];
-        g.y[i] = y[i];
+        g.y[i] = y ? y[i] : nullptr;
         g.bias[i] = bias ? bias[i] : nullptr;
+        g.out[i] = out ? out[i] : nullptr;
+        g.add[i] = add ? add[i] : nullptr;
+        if (!R[i] || (!g.y[i] && !g.out[i]) || (g.add[i] && !g.out[i])) return -1;
         vec = vec && aligned16(R[i]);
     }
     auto s = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>((rows + 3) / 4), static_cast<unsigned>(count));
     const int r = static_cast<int>(rows), k = static_cast<int>(K);
-    if (vec && K <= 1024)
-        hipLaunchKernelGGL((k_gemv_group<true, 4>), grid, dim3(256), 0, s, g, x, r, k);
+    const nnhip_gemv_rmsnorm rn = rms ? *rms : nnhip_gemv_rmsnorm{};
+    if (rms && vec)
+        hipLaunchKernelGGL((k_gemv_group<true, 4, true>), grid, dim3(256), 0, s, g, x, r, k, rn);
+    else if (rms)
+        hipLaunchKernelGGL((k_gemv_group<false, 1, true>), grid, dim3(256), 0, s, g, x, r, k, rn);
+    else if (vec && K <= 1024)
+        hipLaunchKernelGGL((k_gemv_group<true, 4, false>), grid, dim3(256), 0, s, g, x, r, k, rn);
     else if (vec && K <= 2048)
-        hipLaunchKernelGGL((k_gemv_group<true, 8>), grid, dim3(256), 0, s, g, x, r, k);
+        hipLaunchKernelGGL((k_gemv_group<true, 8, false>), grid, dim3(256), 0, s, g, x, r, k, rn);
     else if (vec)
-        hipLaunchKernelGGL((k_gemv_group<true, 16>), grid, dim3(256), 0, s, g, x, r, k);
+        hipLaunchKernelGGL((k_gemv_group<true, 16, false>), grid, dim3(256), 0, s, g, x, r, k, rn);
     else
-        hipLaunchKernelGGL((k_gemv_group<false, 1>), grid, dim3(256), 0, s, g, x, r, k);
+        hipLaunchKernelGGL((k_gemv_group<false, 1, false>), grid, dim3(256), 0, s, g, x, r, k, rn);
     return launch_status();
+}
+} // namespace
+
+extern "C" int nnhip_gemv_group(const float* const* R, const float* x, const float* const* bias, float* const* y,
+                                const float* const* add, float* const* out, size_t count, size_t rows, size_t K,
+                                void* stream)
+{
+    return gemv_group(R, x, nullptr, bias, y, add, out, count, rows, K, stream);
+}
+
+// The same products of RMSNorm(x) (a (K, 1) column, K <= 1024).
+extern "C" int nnhip_gemv_group_rmsnorm(const float* const* R, const float* x, const nnhip_gemv_rmsnorm* rms,
+                                        const float* const* bias, float* const* y, const float* const* add,
+                                        float* const* out, size_t count, size_t rows, size_t K, void* stream)
+{
+    if (!rms) return -1;
+    return gemv_group(R, x, rms, bias, y, add, out, count, rows, K, stream);
 }

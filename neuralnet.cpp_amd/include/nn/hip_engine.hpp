@@ -241,6 +241,7 @@ private:
     Result<void> launch_pending_mm_(std::unique_ptr<PendingMm> o);
     Result<void> launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate);
     PendingMm* pending_mm_(const Tensor& t);
+    PendingMm* vec_record_(const Tensor& t);
     struct PendingAcc;
     std::unique_ptr<PendingAcc> pacc_;
     Result<void> settle_acc_();
