@@ -616,6 +616,27 @@ Plan plan_gemm(size_t M, size_t N, size_t K, size_t batch, bool allow_split)
         p.cfg = kTall;
         p.bm = 256;
         p.bn = 128;
+        if (tiles(128, 128) < 128)
+        {
+            // Small outputs from long K (the 768 x 768 weight gradients over 8192
+            // tokens, alone or as the q, k, v group): 128 x 64 tiles split to
+            // about 1728 workgroups (q, k, v group 101 -> 111 TFLOP/s, the single
+            // one unchanged at 95-97, against 128 x 128 tiles split to 768).
+            p.cfg = kThinWaves;
+            p.bm = 128;
+            p.bn = 64;
+            const size_t t = tiles(128, 64);
+            size_t want = (1728 + t - 1) / t;
+            if (want > K / 256) want = K / 256;
+            if (want > 64) want = 64;
+            if (want > 1)
+            {
+                const size_t ks = ((K + want - 1) / want + 31) / 32 * 32;
+                p.k_split = static_cast<int>(ks);
+                p.splits = static_cast<int>((K + ks - 1) / ks);
+            }
+            return p;
+        }
         if (tiles(256, 128) < 128)
         {
             p.cfg = kSquare;
