@@ -668,6 +668,8 @@ def main():
                     help="run only the oracle's CPU legs of configs 2, 3 and 5 and print their JSON")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the attention leg (configs 2 and 5) and print its JSON (for kernel traces)")
+    ap.add_argument("--inference-only", action="store_true",
+                    help="run only the incremental-inference leg (config-4 model, batch 1) and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
@@ -679,6 +681,12 @@ def main():
         return
     if args.attention_only:
         print(json.dumps({"attention": attention_leg(args.seed)}), flush=True)
+        return
+    if args.inference_only:
+        import nnengine
+        eng = nnengine.Engine(nnengine.hip_library())
+        g = init_session(eng, CFG, 1, args.seed)
+        print(json.dumps({"inference": inference_leg(g, args.seed)}), flush=True)
         return
     if args.cpu_legs:
         print(json.dumps({"cpu_legs": cpu_legs_other(args.seed)}), flush=True)
