@@ -60,10 +60,14 @@ int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* c
  * them and one reduction; A_i stored (M, K), B (K, N) or (N, K) with transB, every C_i 16-byte aligned and
  * M*N % 4 == 0. The attention's q, k and v Linear backward each add G_i X^T into its weight gradient with
  * the same input X (compute_layer.hpp Linear::backward: grad_w += matmul(G, X, false, true)); this runs the
- * three accumulations together. Workspace: nnhip_gemm_workspace_bytes(M, N, K, count). Within the GEMM
- * tolerance of the separate products (the K split differs). No CUDA counterpart. */
+ * three accumulations together. row_sums (may be NULL): row_sums[i] (M) = [row_sums[i] +] the row sums of
+ * A_i over k (Linear::backward's grad_b += row_reduce_sum(G), G being A_i), computed from the A tiles the
+ * product stages (within float32 summation tolerance of row_reduce_sum: the order differs). Workspace:
+ * nnhip_gemm_workspace_bytes(M, N, K, count). Within the GEMM tolerance of the separate products (the K
+ * split differs). No CUDA counterpart. */
 int nnhip_gemm_group_acc(const float* const* A, const float* B, float* const* C, size_t count, size_t M, size_t N,
-                         size_t K, int transB, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+                         size_t K, int transB, int accumulate, float* const* row_sums, int row_sums_accumulate,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* C (M, N) = alpha * sum_i A_i^T B_i over count (1..3) products of one shape, one accumulator over
  * K = count * K_each in segment order: A_i stored (K_each, M), B_i (K_each, N), all 16-byte aligned, M and N

@@ -379,10 +379,17 @@ struct HipEngine::PendingAcc
     bool tB;
     std::size_t M, N, K;
     std::vector<std::pair<Tensor, Tensor>> mem;   // (A_i, C_i)
+    bool acc = true;                              // C_i += A_i op(B), else C_i = A_i op(B)
+    // Linear::backward's grad_b += row_reduce_sum(G) of a member (A_i = G): the
+    // row sums go to rs[i] (added when rs_acc), computed by the same launch.
+    std::vector<Tensor> rs;
+    int rs_acc = -1;
     bool yields(const float* p) const
     {
         for (const auto& m : mem)
             if (has_buf(m.second, p)) return true;
+        for (const auto& t : rs)
+            if (has_buf(t, p)) return true;
         return false;
     }
     bool uses(const float* p) const
@@ -2269,18 +2276,32 @@ Result<void> HipEngine::settle_acc_()
     }
     const float* As[3] = {};
     float* Cs[3] = {};
+    float* Rs[3] = {};
+    bool all_rs = r->rs_acc >= 0;
     for (std::size_t i = 0; i < n; ++i)
     {
         As[i] = D(r->mem[i].first);
         Cs[i] = W(r->mem[i].second);
+        Rs[i] = i < r->rs.size() && r->rs[i].size() ? W(r->rs[i]) : nullptr;
+        all_rs = all_rs && Rs[i];
     }
     prof_begin_();
-    const int rc = n == 1 ? nnhip_gemm_epilogue(As[0], D(r->B), Cs[0], r->M, r->K, r->B.rows(), r->B.cols(), 0,
-                                                r->tB, 1.0f, nullptr, 1, ws ? ws->data() : nullptr, wsb, stream_)
-                          : nnhip_gemm_group_acc(As, D(r->B), Cs, n, r->M, r->N, r->K, r->tB, 1,
-                                                 ws ? ws->data() : nullptr, wsb, stream_);
+    const int rc = nnhip_gemm_group_acc(As, D(r->B), Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
+                                        all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0, ws ? ws->data() : nullptr, wsb,
+                                        stream_);
     prof_end_(r->M, r->N, r->K, n, false, r->tB);
-    return kernel_(rc, "matmul");
+    NN_CHECK(kernel_(rc, "matmul"));
+    if (all_rs) return {};
+    // (row sums recorded for some members only: their own launches)
+    for (std::size_t i = 0; i < n; ++i)
+        if (Rs[i])
+        {
+            const std::size_t R = r->mem[i].first.rows(), C = r->mem[i].first.cols();
+            NN_CHECK(kernel_(r->rs_acc > 0 ? nnhip_reduce_row_sum_add(As[i], Rs[i], R, C, stream_)
+                                           : nnhip_reduce_row(As[i], Rs[i], R, C, 0u, stream_),
+                             "row_reduce_sum"));
+        }
+    return {};
 }
 
 Result<void> HipEngine::settle_mm_()
@@ -2710,19 +2731,23 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
         {
             PendingMm& r = *pmm_;
             r.folded = true;
-            // Accumulations sharing B wait to run together (the q, k, v weight gradients).
-            const bool group = !fresh && !r.tA && r.K >= 1024 && (r.M * r.N) % 4 == 0 && aligned16(A.dev_ptr());
-            if (group && pacc_ && same_t(pacc_->B, r.B) && pacc_->tB == r.tB && pacc_->M == r.M &&
-                pacc_->N == r.N && pacc_->K == r.K && pacc_->mem.size() < 3 && !pacc_->uses(A.dev_ptr()))
+            // Recorded until the layer's bias row sums of the same G arrive (the
+            // launch computes them too); accumulations sharing B run together
+            // (the q, k, v weight gradients).
+            const bool rec = !r.tA && r.plus.empty() && r.M > 1 && r.N > 1 && (r.M * r.N) % 4 == 0 &&
+                             aligned16(A.dev_ptr()) && A.size() == r.M * r.N;
+            if (rec && pacc_ && same_t(pacc_->B, r.B) && pacc_->tB == r.tB && pacc_->M == r.M &&
+                pacc_->N == r.N && pacc_->K == r.K && pacc_->acc == !fresh && pacc_->mem.size() < 3 &&
+                !pacc_->uses(A.dev_ptr()))
             {
                 pacc_->mem.emplace_back(r.A, A);
-                if (pacc_->mem.size() == 3) NN_CHECK(settle_acc_());
                 return {};
             }
             NN_CHECK(settle_acc_());
-            if (group)
+            if (rec)
             {
                 pacc_ = std::make_unique<PendingAcc>(PendingAcc{r.B, r.tB, r.M, r.N, r.K, {}});
+                pacc_->acc = !fresh;
                 pacc_->mem.emplace_back(r.A, A);
                 return {};
             }
@@ -2740,8 +2765,21 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
         NN_CHECK(settle_write_(A));
         if (prsum_ && same_t(B, prsum_->out))
         {
-            NN_CHECK(launch_rsum_(*prsum_, W(A), !fresh));
             prsum_->folded = true;
+            // The row sums of a recorded weight-gradient product's A (Linear's
+            // grad_b += row_reduce_sum(G) after grad_w += G Xᵀ): that launch
+            // computes them.
+            if (PendingAcc* q = pacc_.get(); q && prsum_->kind == 0 && (q->rs_acc < 0 || q->rs_acc == !fresh) &&
+                                             A.rows() == q->M && A.cols() == 1 && !q->uses(A.dev_ptr()))
+                for (std::size_t i = 0; i < q->mem.size(); ++i)
+                    if (same_t(q->mem[i].first, prsum_->src) && (i >= q->rs.size() || !q->rs[i].size()))
+                    {
+                        q->rs.resize(q->mem.size());
+                        q->rs[i] = A;
+                        q->rs_acc = fresh ? 0 : 1;
+                        return {};
+                    }
+            NN_CHECK(launch_rsum_(*prsum_, W(A), !fresh));
             return {};
         }
         if (fresh) NN_CHECK(zero_now_(A));

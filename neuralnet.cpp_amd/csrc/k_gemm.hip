@@ -68,6 +68,18 @@ struct GemmGroup
     int klen;
 };
 
+// RSUM: the row sums of A over k as well (Linear::backward's bias gradient
+// grad_b += row_reduce_sum(G) beside grad_w += G Xᵀ, whose A is G): the
+// workgroups of tile column 0 add up the A values they stage, per row, in the
+// order they stage them; member i's sums go to dst[i] (added to it when acc),
+// or, with split K, to part[(slice * members + i) * M + row] for the reduce.
+struct RowSums
+{
+    float* dst[3];
+    float* part;
+    int acc;
+};
+
 // WM x WN waves; each wave owns (32*FM) x (32*FN) of C as FM x FN MFMA 32x32 blocks.
 // STATS: besides C, each workgroup writes the column softmax statistics of its
 // BM rows of C (as stored, bias included): part[tile_m * N + n] = max over the
@@ -75,13 +87,15 @@ struct GemmGroup
 // sparse cross-entropy that follows the product (the GPT's lm_head logits)
 // merges these instead of reading C once more for them. Needs splits == 1.
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD, bool STATS = false, bool GRP = false,
-          bool KSEG = false>
+          bool KSEG = false, bool RSUM = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K, long lda, long ldb,
                                                        long strideA, long strideB, long strideC, float alpha,
                                                        int tiles_m, int tiles_n, int k_split, float* __restrict__ part,
-                                                       const float* __restrict__ bias, int accum, GemmGroup grp)
+                                                       const float* __restrict__ bias, int accum, GemmGroup grp,
+                                                       RowSums rs = {})
 {
+    static_assert(!RSUM || (GRP && !TA), "row sums of an untransposed A in grouped launches");
     constexpr int NT = 64 * WM * WN;
     constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
     constexpr int LA = BM * BK / 4 / NT;   // float4 per thread per stage for A
@@ -204,7 +218,15 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             }
         }
     };
+    float racc[RSUM ? LA : 1] = {};
+    const bool rsum_here = RSUM && tni == 0;
     auto store_a = [&](int buf) {
+        if constexpr (RSUM)
+            if (rsum_here)
+            {
+#pragma unroll
+                for (int s = 0; s < LA; ++s) racc[s] += (ra[s].x + ra[s].y) + (ra[s].z + ra[s].w);
+            }
 #pragma unroll
         for (int s = 0; s < LA; ++s)
         {
@@ -397,6 +419,30 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
                 }
             }
         }
+    if constexpr (RSUM)
+        if (rsum_here)
+        {
+            // the BK / 4 threads that stage one row's float4s of a stage are adjacent lanes
+            static_assert(BK / 4 == 4 && NT % 64 == 0, "row-sum lanes");
+            const long gi = bz / grp.nb;
+#pragma unroll
+            for (int s = 0; s < LA; ++s)
+            {
+                float v = racc[s];
+                v += __shfl_xor(v, 1, 64);
+                v += __shfl_xor(v, 2, 64);
+                const int gm = m0 + (tid + NT * s) / (BK / 4);
+                if ((tid & 3) != 0 || gm >= M) continue;
+                if (gridDim.y > 1)
+                    rs.part[((long)blockIdx.y * gridDim.z + bz) * M + gm] = v;
+                else
+                {
+#pragma clang fp contract(off)
+                    float* d = rs.dst[gi] + gm;
+                    *d = rs.acc ? *d + v : v;
+                }
+            }
+        }
 }
 
 // C = alpha * sum_s part[s], summed in split order (deterministic); then
@@ -454,10 +500,24 @@ __global__ __launch_bounds__(256) void k_splitk_reduce_ep(const float* __restric
 // part[s][member][mn]) into each member's C: C_i = alpha * sum_s part (+ C_i
 // when accum), summed in split order; mn % 4 == 0, every C_i 16-byte aligned.
 __global__ __launch_bounds__(256) void k_splitk_reduce_grp(const float* __restrict__ part, GemmGroup g, long mn,
-                                                           int members, int splits, float alpha, int accum)
+                                                           int members, int splits, float alpha, int accum, RowSums rs,
+                                                           int M)
 {
 #pragma clang fp contract(off)
     const long n4 = (long)members * mn / 4, stride = (long)gridDim.x * 256;
+    if (rs.part)
+    {
+        // the row sums (RowSums), summed in slice order
+        const long rows = (long)members * M;
+        for (long r = (long)blockIdx.x * 256 + threadIdx.x; r < rows; r += stride)
+        {
+            float a = rs.part[r];
+            for (int s = 1; s < splits; ++s) a += rs.part[(long)s * rows + r];
+            const long mi = r / M;
+            float* d = rs.dst[mi] + (r - mi * M);
+            *d = rs.acc ? *d + a : a;
+        }
+    }
     const float4* p4 = reinterpret_cast<const float4*>(part);
     for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride)
     {
@@ -658,6 +718,7 @@ struct Epi
     int accum;                          // C += result
     const GemmGroup* grp = nullptr;     // members of a grouped launch (no split, NN only)
     const GemmGroup* seg = nullptr;     // K segments summed into one C (TN only)
+    const RowSums* rs = nullptr;        // grouped launches: the row sums of each member's A as well
 };
 
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB>
@@ -681,6 +742,19 @@ void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, l
                 hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, false, true>), grid, block, 0, s,
                                    A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part, e.bias,
                                    e.accum, *e.seg);
+            return;
+        }
+    if constexpr (!TA)
+        if (e.grp && e.rs)
+        {
+            if (guard)
+                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, true, false, true, false, true>), grid, block, 0,
+                                   s, A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part, e.bias,
+                                   e.accum, *e.grp, *e.rs);
+            else
+                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, true, false, true>), grid, block,
+                                   0, s, A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part, e.bias,
+                                   e.accum, *e.grp, *e.rs);
             return;
         }
     if constexpr (!TA)
@@ -1009,9 +1083,17 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
     if (int rc = 0; !e.grp && !e.seg && try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc))
         return rc;
     Plan p = plan_gemm(M, N, K, batch, workspace != nullptr);
-    if (p.splits > 1 && static_cast<size_t>(p.splits) * batch * M * N * sizeof(float) > ws_bytes)
+    if (p.splits > 1 && static_cast<size_t>(p.splits) * batch * (M * N + (e.rs ? M : 0)) * sizeof(float) > ws_bytes)
         p = plan_gemm(M, N, K, batch, false);
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    RowSums rsl{};
+    if (e.rs)
+    {
+        // the row sums' slice partials follow the tiles' in the workspace
+        rsl = *e.rs;
+        rsl.part = part ? part + static_cast<size_t>(p.splits) * batch * M * N : nullptr;
+        e.rs = &rsl;
+    }
     const int m = (int)M, n = (int)N, k = (int)K, b = (int)batch;
     if (!tA && !tB) launch_trans<false, false>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
     else if (!tA && tB) launch_trans<false, true>(p, A, B, C, m, n, k, lda, ldb, sA, sB, sC, alpha, b, part, s, e);
@@ -1022,7 +1104,8 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
         // grouped members (nb == 1): each member's partials into its own C
         const long mn = (long)M * (long)N;
         hipLaunchKernelGGL(k_splitk_reduce_grp, dim3(grid_for(static_cast<size_t>(batch * mn / 4 + 1), 256, 256 * 16)),
-                           dim3(256), 0, s, part, *e.grp, mn, (int)batch, p.splits, alpha, e.accum);
+                           dim3(256), 0, s, part, *e.grp, mn, (int)batch, p.splits, alpha, e.accum,
+                           e.rs ? *e.rs : RowSums{}, (int)M);
     }
     else if (p.splits > 1)
     {
@@ -1082,8 +1165,9 @@ extern "C" int nnhip_gemm_colstats(const float* A, const float* B, float* C, siz
 
 extern "C" size_t nnhip_gemm_workspace_bytes(size_t M, size_t N, size_t K, size_t batch)
 {
+    // (split-K partial tiles, and the slices' row sums of nnhip_gemm_group_acc)
     const Plan p = plan_gemm(M, N, K, batch, true);
-    return p.splits > 1 ? static_cast<size_t>(p.splits) * batch * M * N * sizeof(float) : 0;
+    return p.splits > 1 ? static_cast<size_t>(p.splits) * batch * (M * N + M) * sizeof(float) : 0;
 }
 
 extern "C" int nnhip_gemm(const float* A, const float* B, float* C, size_t A_rows, size_t A_cols, size_t B_rows,
@@ -1112,21 +1196,25 @@ extern "C" int nnhip_gemm_epilogue(const float* A, const float* B, float* C, siz
 }
 
 extern "C" int nnhip_gemm_group_acc(const float* const* A, const float* B, float* const* C, size_t count, size_t M,
-                                    size_t N, size_t K, int transB, int accumulate, void* workspace,
-                                    size_t workspace_bytes, void* stream)
+                                    size_t N, size_t K, int transB, int accumulate, float* const* row_sums,
+                                    int row_sums_accumulate, void* workspace, size_t workspace_bytes, void* stream)
 {
     if (!A || !B || !C || count == 0 || count > 3 || M == 0 || N == 0 || K == 0 || (M * N) % 4 != 0) return -1;
     GemmGroup g{};
     g.nb = 1;
+    RowSums rs{};
     for (size_t i = 0; i < count; ++i)
     {
-        if (!A[i] || !C[i] || !aligned16(C[i])) return -1;
+        if (!A[i] || !C[i] || !aligned16(C[i]) || (row_sums && !row_sums[i])) return -1;
         g.A[i] = A[i];
         g.C[i] = C[i];
+        rs.dst[i] = row_sums ? row_sums[i] : nullptr;
     }
+    rs.acc = row_sums_accumulate ? 1 : 0;
     // A_i stored (M, K), B (K, N) or, with transB, (N, K); batch z of the launch is member z.
     Epi e{nullptr, accumulate ? 1 : 0};
     e.grp = &g;
+    if (row_sums) e.rs = &rs;
     return gemm_dispatch(A[0], B, C[0], M, N, K, K, transB ? K : N, M * K, 0, M * N, false, transB != 0, 1.0f, count,
                          workspace, workspace_bytes, stream, e);
 }

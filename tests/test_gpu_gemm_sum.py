@@ -5,7 +5,13 @@ order (include/nnhip_kernels.h). Bars: float64 with the GEMM tolerance (normwise
 elementwise a-priori bound |dC| <= 2K 2^-24 (sum |A_i|^T |B_i|)_ij) for the engine call pattern and
 the entry point directly, the folded products still readable afterwards, a write to an operand
 between the calls, and a GPT block whose backward takes this path against the oracle (the GPT
-parity tests cover the whole model)."""
+parity tests cover the whole model).
+
+Weight-gradient accumulations (Linear::backward's grad_w += G X^T) are recorded, the q, k, v ones
+with one X grouped into one launch (nnhip_gemm_group_acc), and the layer's bias row sums
+(grad_b += row_reduce_sum(G)) are computed by the same launch from the G tiles it stages: checked
+against float64 with the summation bound |d| <= 2K 2^-24 sum|G| per row, added or written (a bias
+gradient whose zero fill is still pending), with the row-sum tensors still readable."""
 import ctypes
 
 import numpy as np
@@ -126,14 +132,29 @@ def test_weight_gradients_sharing_input(hip, M, K, N, cut):
         _check_acc(early, W0[0], Gs[0], X)
 
 
-@pytest.mark.parametrize("count,M,N,K,tB", [(3, 768, 768, 8192, True), (2, 100, 36, 3000, True),
-                                            (3, 64, 128, 512, False), (1, 96, 64, 2048, True)])
-def test_group_acc_entry_point(hip, count, M, N, K, tB):
+def _rows_ref(r0, A, acc):
+    return (r0.astype(np.float64) if acc else 0.0) + A.astype(np.float64).sum(axis=1, keepdims=True)
+
+
+def _check_rows(got, r0, A, acc):
+    """Row sums of A over k (+ r0): normwise 1e-5 and |d| <= 2K 2^-24 sum |A| (+ |r0|) per row."""
+    ref = _rows_ref(r0, A, acc)
+    mag = np.abs(A.astype(np.float64)).sum(axis=1, keepdims=True) + (np.abs(r0) if acc else 0.0)
+    assert nrm_err(got, ref) <= 1e-5
+    assert np.all(np.abs(got - ref) <= 2 * (A.shape[1] + 1) * 2.0 ** -24 * mag + 1e-30)
+
+
+@pytest.mark.parametrize("count,M,N,K,tB,rows", [(3, 768, 768, 8192, True, 1), (2, 100, 36, 3000, True, 0),
+                                                 (3, 64, 128, 512, False, 1), (1, 96, 64, 2048, True, 2),
+                                                 (1, 100, 36, 300, True, 1), (3, 768, 3072, 8192, True, 2)])
+def test_group_acc_entry_point(hip, count, M, N, K, tB, rows):
+    """rows: 0 no row sums, 1 row sums added to their destination, 2 written."""
     lib = nnengine.hip_library()
     lib.nnhip_gemm_workspace_bytes.restype = SZ
     lib.nnhip_gemm_workspace_bytes.argtypes = [SZ] * 4
     lib.nnhip_gemm_group_acc.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, SZ, SZ, SZ, SZ,
-                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p, SZ, ctypes.c_void_p]
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                         SZ, ctypes.c_void_p]
     lib.nnhip_engine_stream.restype = ctypes.c_void_p
     lib.nnhip_engine_stream.argtypes = [ctypes.c_void_p]
     rng = np.random.default_rng(count * M + K)
@@ -145,11 +166,50 @@ def test_group_acc_entry_point(hip, count, M, N, K, tB):
     wsb = lib.nnhip_gemm_workspace_bytes(M, N, K, count)
     ws = hip.create_tensor(max(1, wsb // 4), 1)
     hip.sync()
+    R0 = [uniform(rng, (M, 1)) for _ in range(count)]
+    r = [hip.tensor(x) for x in R0]
+    hip.sync()
     pa = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in a])
     pc = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in c])
-    print(f"[group_acc] count {count} M {M} N {N} K {K} tB {tB} ws {wsb}", flush=True)
-    assert lib.nnhip_gemm_group_acc(pa, b.data_ptr(), pc, count, M, N, K, int(tB), 1,
-                                    ws.data_ptr() if wsb else None, wsb, lib.nnhip_engine_stream(hip._e)) == 0
+    pr = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in r])
+    print(f"[group_acc] count {count} M {M} N {N} K {K} tB {tB} rows {rows} ws {wsb}", flush=True)
+    assert lib.nnhip_gemm_group_acc(pa, b.data_ptr(), pc, count, M, N, K, int(tB), 1, pr if rows else None,
+                                    int(rows == 1), ws.data_ptr() if wsb else None, wsb,
+                                    lib.nnhip_engine_stream(hip._e)) == 0
     Xt = Bm if tB else Bm.T          # (N, K): C += A X^T
     for i in range(count):
         _check_acc(c[i].numpy(), C0[i], As[i], np.ascontiguousarray(Xt))
+        if rows:
+            _check_rows(r[i].numpy(), R0[i], As[i], rows == 1)
+        else:
+            assert np.array_equal(r[i].numpy(), R0[i])
+
+
+@pytest.mark.parametrize("fresh_b", [False, True])
+def test_linear_backward_bias_sums_with_weight_gradients(hip, fresh_b):
+    """Linear::backward's calls for the q, k, v layers (one X) and one more layer (another X):
+    grad_w += G X^T and grad_b += row_reduce_sum(G), recorded and launched with the products; the
+    bias gradients' zero fill still pending (fresh_b) makes the launch write the sums. The row-sum
+    tensors themselves stay readable."""
+    rng = np.random.default_rng(11 + fresh_b)
+    d, N = 256, 2048
+    X, X2 = uniform(rng, (d, N)), uniform(rng, (d, N))
+    Gs = [uniform(rng, (d, N)) for _ in range(4)]
+    W0 = [uniform(rng, (d, d)) for _ in range(4)]
+    B0 = [uniform(rng, (d, 1)) for _ in range(4)]
+    x, x2 = hip.tensor(X), hip.tensor(X2)
+    gw, gb = [hip.tensor(w) for w in W0], [hip.tensor(b) for b in B0]
+    if fresh_b:
+        for t in gb:
+            hip.zero(t)
+    sums = []
+    for i in range(4):
+        g = hip.tensor(Gs[i])
+        hip.add_inplace(gw[i], hip.matmul(g, x if i < 3 else x2, False, True))
+        rsum = hip.row_reduce_sum(g)
+        hip.add_inplace(gb[i], rsum)
+        sums.append(rsum)
+    for i in range(4):
+        _check_acc(gw[i].numpy(), W0[i], Gs[i], X if i < 3 else X2)
+        _check_rows(gb[i].numpy(), B0[i], Gs[i], not fresh_b)
+        _check_rows(sums[i].numpy(), B0[i], Gs[i], False)
