@@ -56,7 +56,7 @@ int nnhip_gemm_heads(const float* W, const float* X, const float* row_bias, floa
 int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* const* row_bias, float* const* out,
                            size_t count, size_t M, size_t K, size_t B, size_t T, void* stream);
 
-/* C_i (M, N) = [C_i +] A_i op(B), i < count (1..3): products sharing B in one launch, split-K over all of
+/* C_i (M, N) = [C_i +] A_i op(B), i < count (1..4): products sharing B in one launch, split-K over all of
  * them and one reduction; A_i stored (M, K), B (K, N) or (N, K) with transB, every C_i 16-byte aligned and
  * M*N % 4 == 0. The attention's q, k and v Linear backward each add G_i X^T into its weight gradient with
  * the same input X (compute_layer.hpp Linear::backward: grad_w += matmul(G, X, false, true)); this runs the
@@ -68,6 +68,15 @@ int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* c
 int nnhip_gemm_group_acc(const float* const* A, const float* B, float* const* C, size_t count, size_t M, size_t N,
                          size_t K, int transB, int accumulate, float* const* row_sums, int row_sums_accumulate,
                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* nnhip_gemm_group_acc with a B of each member: C_i = [C_i +] A_i op(B_i), i < count (1..4), every B_i of one
+ * shape. The attention's four Linears (output, q, k, v) have weight gradients of one shape, d_model x
+ * d_model over the batch's tokens (compute_layer.hpp:183-185 in each Linear::backward), the output
+ * projection's with its own input; they run as one launch. Same rounding and row sums as
+ * nnhip_gemm_group_acc. No CUDA counterpart. */
+int nnhip_gemm_group_acc_each(const float* const* A, const float* const* B, float* const* C, size_t count,
+                              size_t M, size_t N, size_t K, int transB, int accumulate, float* const* row_sums,
+                              int row_sums_accumulate, void* workspace, size_t workspace_bytes, void* stream);
 
 /* C (M, N) = alpha * sum_i A_i^T B_i over count (1..3) products of one shape, one accumulator over
  * K = count * K_each in segment order: A_i stored (K_each, M), B_i (K_each, N), all 16-byte aligned, M and N

@@ -369,16 +369,18 @@ struct HipEngine::PendingMm
     bool needed() const { return live(C) || (out2.size() && live(out2)); }
 };
 
-// Weight-gradient accumulations C_i += A_i op(B) (Linear::backward's
-// grad_w += G X^T, folded into the product) with one B, not launched yet: the
-// attention's q, k and v layers share their input X, so their three
-// accumulations run as one grouped launch (nnhip_gemm_group_acc).
+// Weight-gradient accumulations C_i += A_i op(B_i) (Linear::backward's
+// grad_w += G X^T, folded into the product) of one shape, not launched yet:
+// the attention's output, q, k and v layers have d_model x d_model weights
+// (q, k and v share their input X), so their four accumulations run as one
+// grouped launch (nnhip_gemm_group_acc[_each]).
 struct HipEngine::PendingAcc
 {
-    Tensor B;
+    Tensor B;   // member 0's
     bool tB;
     std::size_t M, N, K;
     std::vector<std::pair<Tensor, Tensor>> mem;   // (A_i, C_i)
+    std::vector<Tensor> mb;                       // B_i
     bool acc = true;                              // C_i += A_i op(B), else C_i = A_i op(B)
     // Linear::backward's grad_b += row_reduce_sum(G) of a member (A_i = G): the
     // row sums go to rs[i] (added when rs_acc), computed by the same launch.
@@ -396,6 +398,8 @@ struct HipEngine::PendingAcc
     {
         for (const auto& m : mem)
             if (has_buf(m.first, p)) return true;
+        for (const auto& t : mb)
+            if (has_buf(t, p)) return true;
         return yields(p) || has_buf(B, p);
     }
 };
@@ -2274,21 +2278,27 @@ Result<void> HipEngine::settle_acc_()
         NN_TRY(w, scratch_(wsb));
         ws = w;
     }
-    const float* As[3] = {};
-    float* Cs[3] = {};
-    float* Rs[3] = {};
-    bool all_rs = r->rs_acc >= 0;
+    const float* As[4] = {};
+    const float* Bs[4] = {};
+    float* Cs[4] = {};
+    float* Rs[4] = {};
+    bool all_rs = r->rs_acc >= 0, one_b = true;
     for (std::size_t i = 0; i < n; ++i)
     {
         As[i] = D(r->mem[i].first);
+        Bs[i] = D(r->mb[i]);
         Cs[i] = W(r->mem[i].second);
         Rs[i] = i < r->rs.size() && r->rs[i].size() ? W(r->rs[i]) : nullptr;
         all_rs = all_rs && Rs[i];
+        one_b = one_b && same_t(r->mb[i], r->B);
     }
     prof_begin_();
-    const int rc = nnhip_gemm_group_acc(As, D(r->B), Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
-                                        all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0, ws ? ws->data() : nullptr, wsb,
-                                        stream_);
+    const int rc = one_b ? nnhip_gemm_group_acc(As, D(r->B), Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
+                                                all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0,
+                                                ws ? ws->data() : nullptr, wsb, stream_)
+                         : nnhip_gemm_group_acc_each(As, Bs, Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
+                                                     all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0,
+                                                     ws ? ws->data() : nullptr, wsb, stream_);
     prof_end_(r->M, r->N, r->K, n, false, r->tB);
     NN_CHECK(kernel_(rc, "matmul"));
     if (all_rs) return {};
@@ -2732,15 +2742,16 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
             PendingMm& r = *pmm_;
             r.folded = true;
             // Recorded until the layer's bias row sums of the same G arrive (the
-            // launch computes them too); accumulations sharing B run together
-            // (the q, k, v weight gradients).
+            // launch computes them too); accumulations of one shape run together
+            // (the attention's output, q, k and v weight gradients).
             const bool rec = !r.tA && r.plus.empty() && r.M > 1 && r.N > 1 && (r.M * r.N) % 4 == 0 &&
                              aligned16(A.dev_ptr()) && A.size() == r.M * r.N;
-            if (rec && pacc_ && same_t(pacc_->B, r.B) && pacc_->tB == r.tB && pacc_->M == r.M &&
-                pacc_->N == r.N && pacc_->K == r.K && pacc_->acc == !fresh && pacc_->mem.size() < 3 &&
-                !pacc_->uses(A.dev_ptr()))
+            if (rec && pacc_ && pacc_->tB == r.tB && pacc_->M == r.M && pacc_->N == r.N && pacc_->K == r.K &&
+                r.B.rows() == pacc_->B.rows() && r.B.cols() == pacc_->B.cols() && pacc_->acc == !fresh &&
+                pacc_->mem.size() < 4 && !pacc_->uses(A.dev_ptr()))
             {
                 pacc_->mem.emplace_back(r.A, A);
+                pacc_->mb.push_back(r.B);
                 return {};
             }
             NN_CHECK(settle_acc_());
@@ -2749,6 +2760,7 @@ Result<void> HipEngine::add_inplace(Tensor& A, const Tensor& B)
                 pacc_ = std::make_unique<PendingAcc>(PendingAcc{r.B, r.tB, r.M, r.N, r.K, {}});
                 pacc_->acc = !fresh;
                 pacc_->mem.emplace_back(r.A, A);
+                pacc_->mb.push_back(r.B);
                 return {};
             }
             NN_CHECK(launch_mm_(r, A, nullptr, !fresh));

@@ -53,18 +53,20 @@ __device__ __forceinline__ void tile_coords(int bid, int nt, int tiles_m, int ti
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-// Up to three products sharing B (the attention's q, k, v projections of one
-// input): workgroup batch z takes member z / nb, batch z % nb of that member.
-// With KSEG instead: up to three products of one shape summed into one C
-// (the q, k, v input gradients), k running through segment i = k / klen of
-// A[i] and B[i] in turn.
+// Up to four products of one shape (the attention's q, k, v projections of
+// one input; the weight gradients of its four Linears): workgroup batch z takes
+// member z / nb, batch z % nb of that member, whose B is B[member] when set
+// and the launch's B otherwise. With KSEG instead: up to three products of one
+// shape summed into one C (the q, k, v input gradients), k running through
+// segment i = k / klen of A[i] and B[i] in turn.
+constexpr int kGroupMax = 4;
 struct GemmGroup
 {
-    const float* A[3];
-    float* C[3];
-    const float* bias[3];
+    const float* A[kGroupMax];
+    float* C[kGroupMax];
+    const float* bias[kGroupMax];
     int nb;
-    const float* B[3];
+    const float* B[kGroupMax];
     int klen;
 };
 
@@ -75,7 +77,7 @@ struct GemmGroup
 // or, with split K, to part[(slice * members + i) * M + row] for the reduce.
 struct RowSums
 {
-    float* dst[3];
+    float* dst[kGroupMax];
     float* part;
     int acc;
 };
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
         const int gi = static_cast<int>(bz / grp.nb);
         const long bb = bz % grp.nb;
         A = grp.A[gi];
-        B += bb * strideB;
+        B = (grp.B[gi] ? grp.B[gi] : B) + bb * strideB;
         C = grp.C[gi] + bb * strideC;
         bias = grp.bias[gi];
     }
@@ -1195,19 +1197,25 @@ extern "C" int nnhip_gemm_epilogue(const float* A, const float* B, float* C, siz
                          transB != 0, alpha, 1, workspace, workspace_bytes, stream, Epi{row_bias, accumulate ? 1 : 0});
 }
 
-extern "C" int nnhip_gemm_group_acc(const float* const* A, const float* B, float* const* C, size_t count, size_t M,
-                                    size_t N, size_t K, int transB, int accumulate, float* const* row_sums,
-                                    int row_sums_accumulate, void* workspace, size_t workspace_bytes, void* stream)
+namespace
 {
-    if (!A || !B || !C || count == 0 || count > 3 || M == 0 || N == 0 || K == 0 || (M * N) % 4 != 0) return -1;
+// The grouped accumulations: one B for every member (B_each null) or one each.
+int group_acc(const float* const* A, const float* B, const float* const* B_each, float* const* C, size_t count,
+              size_t M, size_t N, size_t K, int transB, int accumulate, float* const* row_sums,
+              int row_sums_accumulate, void* workspace, size_t workspace_bytes, void* stream)
+{
+    if (!A || !(B || B_each) || !C || count == 0 || count > kGroupMax || M == 0 || N == 0 || K == 0 ||
+        (M * N) % 4 != 0)
+        return -1;
     GemmGroup g{};
     g.nb = 1;
     RowSums rs{};
     for (size_t i = 0; i < count; ++i)
     {
-        if (!A[i] || !C[i] || !aligned16(C[i]) || (row_sums && !row_sums[i])) return -1;
+        if (!A[i] || !C[i] || !aligned16(C[i]) || (row_sums && !row_sums[i]) || (B_each && !B_each[i])) return -1;
         g.A[i] = A[i];
         g.C[i] = C[i];
+        g.B[i] = B_each ? B_each[i] : nullptr;
         rs.dst[i] = row_sums ? row_sums[i] : nullptr;
     }
     rs.acc = row_sums_accumulate ? 1 : 0;
@@ -1215,8 +1223,27 @@ extern "C" int nnhip_gemm_group_acc(const float* const* A, const float* B, float
     Epi e{nullptr, accumulate ? 1 : 0};
     e.grp = &g;
     if (row_sums) e.rs = &rs;
-    return gemm_dispatch(A[0], B, C[0], M, N, K, K, transB ? K : N, M * K, 0, M * N, false, transB != 0, 1.0f, count,
-                         workspace, workspace_bytes, stream, e);
+    return gemm_dispatch(A[0], B_each ? B_each[0] : B, C[0], M, N, K, K, transB ? K : N, M * K, 0, M * N, false,
+                         transB != 0, 1.0f, count, workspace, workspace_bytes, stream, e);
+}
+} // namespace
+
+extern "C" int nnhip_gemm_group_acc(const float* const* A, const float* B, float* const* C, size_t count, size_t M,
+                                    size_t N, size_t K, int transB, int accumulate, float* const* row_sums,
+                                    int row_sums_accumulate, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return group_acc(A, B, nullptr, C, count, M, N, K, transB, accumulate, row_sums, row_sums_accumulate, workspace,
+                     workspace_bytes, stream);
+}
+
+extern "C" int nnhip_gemm_group_acc_each(const float* const* A, const float* const* B, float* const* C,
+                                         size_t count, size_t M, size_t N, size_t K, int transB, int accumulate,
+                                         float* const* row_sums, int row_sums_accumulate, void* workspace,
+                                         size_t workspace_bytes, void* stream)
+{
+    if (!B) return -1;
+    return group_acc(A, nullptr, B, C, count, M, N, K, transB, accumulate, row_sums, row_sums_accumulate, workspace,
+                     workspace_bytes, stream);
 }
 
 extern "C" int nnhip_gemm_tn_sum(const float* const* A, const float* const* B, size_t count, float* C, size_t M,

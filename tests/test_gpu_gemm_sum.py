@@ -7,8 +7,9 @@ the entry point directly, the folded products still readable afterwards, a write
 between the calls, and a GPT block whose backward takes this path against the oracle (the GPT
 parity tests cover the whole model).
 
-Weight-gradient accumulations (Linear::backward's grad_w += G X^T) are recorded, the q, k, v ones
-with one X grouped into one launch (nnhip_gemm_group_acc), and the layer's bias row sums
+Weight-gradient accumulations (Linear::backward's grad_w += G X^T) are recorded, up to four of one
+shape grouped into one launch (the attention's output, q, k and v layers: nnhip_gemm_group_acc with
+one X, nnhip_gemm_group_acc_each with a B per member), and the layer's bias row sums
 (grad_b += row_reduce_sum(G)) are computed by the same launch from the G tiles it stages: checked
 against float64 with the summation bound |d| <= 2K 2^-24 sum|G| per row, added or written (a bias
 gradient whose zero fill is still pending), with the row-sum tensors still readable."""
@@ -169,9 +170,9 @@ def test_group_acc_entry_point(hip, count, M, N, K, tB, rows):
     R0 = [uniform(rng, (M, 1)) for _ in range(count)]
     r = [hip.tensor(x) for x in R0]
     hip.sync()
-    pa = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in a])
-    pc = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in c])
-    pr = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in r])
+    pa = (ctypes.c_void_p * count)(*[t.data_ptr() for t in a])
+    pc = (ctypes.c_void_p * count)(*[t.data_ptr() for t in c])
+    pr = (ctypes.c_void_p * count)(*[t.data_ptr() for t in r])
     print(f"[group_acc] count {count} M {M} N {N} K {K} tB {tB} rows {rows} ws {wsb}", flush=True)
     assert lib.nnhip_gemm_group_acc(pa, b.data_ptr(), pc, count, M, N, K, int(tB), 1, pr if rows else None,
                                     int(rows == 1), ws.data_ptr() if wsb else None, wsb,
@@ -183,6 +184,93 @@ def test_group_acc_entry_point(hip, count, M, N, K, tB, rows):
             _check_rows(r[i].numpy(), R0[i], As[i], rows == 1)
         else:
             assert np.array_equal(r[i].numpy(), R0[i])
+
+
+def _lib_each():
+    lib = nnengine.hip_library()
+    lib.nnhip_gemm_workspace_bytes.restype = SZ
+    lib.nnhip_gemm_workspace_bytes.argtypes = [SZ] * 4
+    P = ctypes.c_void_p
+    lib.nnhip_gemm_group_acc_each.argtypes = [P, P, P, SZ, SZ, SZ, SZ, ctypes.c_int, ctypes.c_int, P, ctypes.c_int,
+                                              P, SZ, P]
+    lib.nnhip_engine_stream.restype = ctypes.c_void_p
+    lib.nnhip_engine_stream.argtypes = [ctypes.c_void_p]
+    return lib
+
+
+@pytest.mark.parametrize("count,M,N,K,tB,rows", [(4, 768, 768, 8192, True, 1), (4, 96, 64, 2048, True, 2),
+                                                 (2, 100, 36, 3000, True, 0), (4, 64, 128, 512, False, 1),
+                                                 (3, 256, 256, 4096, True, 2)])
+def test_group_acc_each_entry_point(hip, count, M, N, K, tB, rows):
+    """nnhip_gemm_group_acc_each: C_i += A_i op(B_i) with a B of each member (the attention's output,
+    q, k and v weight gradients); rows: 0 no row sums, 1 added to their destination, 2 written."""
+    lib = _lib_each()
+    rng = np.random.default_rng(count * M + K + 5)
+    As = [uniform(rng, (M, K)) for _ in range(count)]
+    Bs = [uniform(rng, (N, K) if tB else (K, N)) for _ in range(count)]
+    C0 = [uniform(rng, (M, N)) for _ in range(count)]
+    R0 = [uniform(rng, (M, 1)) for _ in range(count)]
+    a, b = [hip.tensor(x) for x in As], [hip.tensor(x) for x in Bs]
+    c, r = [hip.tensor(x) for x in C0], [hip.tensor(x) for x in R0]
+    wsb = lib.nnhip_gemm_workspace_bytes(M, N, K, count)
+    ws = hip.create_tensor(max(1, wsb // 4), 1)
+    hip.sync()
+    arr = lambda ts: (ctypes.c_void_p * count)(*[t.data_ptr() for t in ts])
+    print(f"[group_acc_each] count {count} M {M} N {N} K {K} tB {tB} rows {rows} ws {wsb}", flush=True)
+    assert lib.nnhip_gemm_group_acc_each(arr(a), arr(b), arr(c), count, M, N, K, int(tB), 1,
+                                         arr(r) if rows else None, int(rows == 1), ws.data_ptr() if wsb else None,
+                                         wsb, lib.nnhip_engine_stream(hip._e)) == 0
+    for i in range(count):
+        Xt = np.ascontiguousarray(Bs[i] if tB else Bs[i].T)
+        _check_acc(c[i].numpy(), C0[i], As[i], Xt)
+        if rows:
+            _check_rows(r[i].numpy(), R0[i], As[i], rows == 1)
+        else:
+            assert np.array_equal(r[i].numpy(), R0[i])
+
+
+def test_group_acc_each_argument_errors(hip):
+    lib = _lib_each()
+    t = hip.create_tensor(64, 64)
+    p = t.data_ptr()
+    five = (ctypes.c_void_p * 5)(*([p] * 5))
+    assert lib.nnhip_gemm_group_acc_each(five, five, five, 5, 64, 64, 64, 1, 1, None, 0, None, 0, None) == -1
+    holes = (ctypes.c_void_p * 2)(p, None)
+    two = (ctypes.c_void_p * 2)(p, p)
+    assert lib.nnhip_gemm_group_acc_each(two, holes, two, 2, 64, 64, 64, 1, 1, None, 0, None, 0, None) == -1
+    assert lib.nnhip_gemm_group_acc_each(two, None, two, 2, 64, 64, 64, 1, 1, None, 0, None, 0, None) == -1
+
+
+@pytest.mark.parametrize("cut", [None, "read", "write_b0"])
+def test_attention_weight_gradients_grouped(hip, cut):
+    """The backward's order: the output projection's grad_w += G_o A^T (its own input A), then the q, k
+    and v layers' with the block input X, each with its bias row sums: one launch of four members. `cut`
+    reads the output projection's gradient, or writes its input A in place, after the q layer's calls
+    (the recorded members run first)."""
+    rng = np.random.default_rng(23)
+    d, N = 192, 1024
+    Xo, X = uniform(rng, (d, N)), uniform(rng, (d, N))
+    Gs = [uniform(rng, (d, N)) for _ in range(4)]
+    W0 = [uniform(rng, (d, d)) for _ in range(4)]
+    B0 = [uniform(rng, (d, 1)) for _ in range(4)]
+    xo, x = hip.tensor(Xo), hip.tensor(X)
+    gw, gb = [hip.tensor(w) for w in W0], [hip.tensor(b) for b in B0]
+    early = None
+    for i in range(4):
+        g = hip.tensor(Gs[i])
+        hip.add_inplace(gw[i], hip.matmul(g, xo if i == 0 else x, False, True))
+        hip.add_inplace(gb[i], hip.row_reduce_sum(g))
+        if i == 1 and cut == "read":
+            early = gw[0].numpy()
+        if i == 1 and cut == "write_b0":
+            hip.scale_inplace(xo, 0.5)
+    for i in range(4):
+        _check_acc(gw[i].numpy(), W0[i], Gs[i], Xo if i == 0 else X)
+        _check_rows(gb[i].numpy(), B0[i], Gs[i], True)
+    if early is not None:
+        _check_acc(early, W0[0], Gs[0], Xo)
+    if cut == "write_b0":
+        assert np.array_equal(xo.numpy(), Xo * np.float32(0.5))
 
 
 @pytest.mark.parametrize("fresh_b", [False, True])
