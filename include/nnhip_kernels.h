@@ -458,11 +458,24 @@ int nnhip_rowbcast_mul(const float* X, const float* v, float* out, size_t F, siz
  * NULL (not written). 1 <= F <= 1024. */
 int nnhip_rmsnorm_forward(const float* X, const float* gamma, float inv_f, float eps, float* s_raw, float* scaled,
                           float* var_eps, float* rinv, float* normed, float* out, size_t F, size_t N, void* stream);
+/* nnhip_rmsnorm_forward of X = A + B, X written as well: GPTBlock::forward's residual add followed by the next
+ * RMSNorm (compute_layer.hpp:2375-2379 and 2385 with the following block's norm, each add rounded as
+ * elementwise_binary(Add)), one pass reading A and B. N % 4 == 0, every matrix 16-byte aligned. Outputs equal
+ * elementwise_binary(Add, A, B) followed by nnhip_rmsnorm_forward bit for bit. No CUDA counterpart. */
+int nnhip_rmsnorm_forward_sum(const float* A, const float* B, float* X, const float* gamma, float inv_f, float eps,
+                              float* s_raw, float* scaled, float* var_eps, float* rinv, float* normed, float* out,
+                              size_t F, size_t N, void* stream);
 /* RMSNorm::backward's column sum, its scaling and dx in one pass (compute_layer.hpp:772-791; no CUDA
  * counterpart): m_raw = bwd_colsum(G, gamma, Nrm), m = m_raw * inv_f, dx = bwd_dx(G, gamma, m, Nrm, rinv),
  * equal bit for bit to the separate calls; m_raw may be NULL. 1 <= F <= 1024. */
 int nnhip_rmsnorm_backward(const float* G, const float* gamma, const float* Nrm, const float* rinv, float inv_f,
                            float* m_raw, float* m, float* dx, size_t F, size_t N, void* stream);
+/* nnhip_rmsnorm_backward that also writes out2 = addend + dx: GPTBlock::backward's residual adds of the layer
+ * gradients (compute_layer.hpp:2396 and 2404, elementwise_binary(Add, grad, dx)), in the same pass. dx, out2
+ * equal the separate calls bit for bit. No CUDA counterpart. */
+int nnhip_rmsnorm_backward_add(const float* G, const float* gamma, const float* Nrm, const float* rinv, float inv_f,
+                               float* m_raw, float* m, float* dx, const float* addend, float* out2, size_t F,
+                               size_t N, void* stream);
 int nnhip_rmsnorm_bwd_colsum(const float* G, const float* gamma, const float* Nrm, float* out, size_t F, size_t N,
                              void* stream);
 int nnhip_rmsnorm_bwd_dx(const float* G, const float* gamma, const float* m, const float* Nrm, const float* rinv,

@@ -545,17 +545,22 @@ struct HipEngine::PendingRms
     Tensor x, s, scaled, var_eps, rinv, normed;
     Tensor gamma;   // bwd: with x = g and normed, an input; forward stage 6: the scale
     Tensor y;       // forward stage 6 (one column): the output, normed * gamma
+    // forward: x = xa + xb, a recorded elementwise_binary(Add) taken into the
+    // launch (GPTBlock::forward's residual add before the layer); x is an output
+    Tensor xa, xb;
+    Tensor dx;      // bwd stage 3: dx, not launched yet (rinv is then an input)
     float inv_f = 0.0f, eps = 0.0f;
     int stage = 1;
     bool yields(const float* p) const
     {
-        if (bwd) return has_buf(s, p) || has_buf(scaled, p);
+        if (bwd) return has_buf(s, p) || has_buf(scaled, p) || has_buf(dx, p);
         return has_buf(s, p) || has_buf(scaled, p) || has_buf(var_eps, p) || has_buf(rinv, p) || has_buf(normed, p) ||
-               has_buf(y, p);
+               has_buf(y, p) || (xa.size() && has_buf(x, p));
     }
     bool uses(const float* p) const
     {
-        return has_buf(x, p) || yields(p) || has_buf(gamma, p) || (bwd && has_buf(normed, p));
+        return has_buf(x, p) || yields(p) || has_buf(gamma, p) || (bwd && (has_buf(normed, p) || has_buf(rinv, p))) ||
+               has_buf(xa, p) || has_buf(xb, p);
     }
 };
 
@@ -3083,6 +3088,30 @@ Result<Tensor> HipEngine::elementwise_binary(BinaryOp op, const Tensor& A, const
             return o;
         }
     }
+    // grad + dx of a recorded RMSNorm backward (the residual adds of
+    // GPTBlock::backward, compute_layer.hpp:2396, 2404): the layer's pass
+    // writes the sum as well (the same rounding).
+    if (op == BinaryOp::Add && prms_ && prms_->bwd && prms_->stage == 3 && !same_t(A, B) &&
+        (same_t(A, prms_->dx) || same_t(B, prms_->dx)))
+    {
+        const Tensor& E = same_t(B, prms_->dx) ? A : B;
+        if (E.size() && aligned16(E.dev_ptr()) && !prms_->yields(E.dev_ptr()) && !has_buf(E, prms_->dx.dev_ptr()))
+        {
+            NN_CHECK(settle_ew_());
+            NN_CHECK(settle_chain_reads_({&E}));
+            if (prms_ && prms_->bwd && prms_->stage == 3 && (same_t(A, prms_->dx) || same_t(B, prms_->dx)))
+            {
+                std::unique_ptr<PendingRms> q = std::move(prms_);
+                const std::size_t F = q->x.rows(), N = q->x.cols();
+                NN_TRY(o, alloc_(A.rows(), A.cols()));
+                NN_CHECK(kernel_(nnhip_rmsnorm_backward_add(D(q->x), D(q->gamma), D(q->normed), D(q->rinv), q->inv_f,
+                                                            W(q->s), W(q->scaled), W(q->dx), D(E), W(o), F, N,
+                                                            stream_),
+                                 "rmsnorm backward"));
+                return o;
+            }
+        }
+    }
     // scores + mask of a deferred scores product (materialised attention): recorded.
     if (op == BinaryOp::Add && pgemm_ && same_t(A, pgemm_->C) && !has_buf(B, A.dev_ptr()) && A.size() &&
         pgemm_->N == B.cols() && pgemm_->K <= 64)
@@ -3281,11 +3310,12 @@ Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std:
             return R();
         NN_CHECK(settle_reads_({rinv}));
         if (!prms_ || !prms_->bwd || prms_->stage != 2) return R();
-        std::unique_ptr<PendingRms> q = std::move(prms_);
+        // Recorded: the block's residual add of dx that usually follows
+        // (elementwise_binary) runs in the same pass.
         NN_TRY(o, alloc_(rows, cols));
-        NN_CHECK(kernel_(nnhip_rmsnorm_backward(D(q->x), D(q->gamma), D(q->normed), D(*rinv), q->inv_f, W(q->s),
-                                                W(q->scaled), W(o), rows, cols, stream_),
-                         "rmsnorm backward"));
+        prms_->rinv = *rinv;
+        prms_->dx = o;
+        prms_->stage = 3;
         return R(o);
     }
     if (vector_out)
@@ -3298,10 +3328,38 @@ Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std:
             rows > 1024 || cols == 0 || (!narrow && (cols % 4 != 0 || !aligned16(a[0]))))
             return R();
         NN_CHECK(settle_rms_());
-        NN_CHECK(settle_reads_({&x}));
+        // x = a + b still recorded as the last elementwise call (the block's
+        // residual add, GPTBlock::forward): the layer's pass forms and writes x.
+        Tensor xa, xb;
+        if (!narrow && pew_ && !pew_->ops.empty())
+        {
+            const PendingEw::Op& e = pew_->ops.back();
+            const Tensor& d = pew_->slots[e.dst];
+            std::size_t refs = 0;
+            for (const auto& op : pew_->ops)
+                refs += (op.dst == e.dst) + (op.a == e.dst) + (PendingEw::reads_b(op) && op.b == e.dst);
+            if (e.code == kBin && e.op == static_cast<std::uint8_t>(BinaryOp::Add) && same_t(d, x) && refs == 1 &&
+                e.a != e.dst && e.b != e.dst)
+            {
+                const Tensor &ta = pew_->slots[e.a], &tb = pew_->slots[e.b];
+                if (ta.rows() == rows && ta.cols() == cols && tb.rows() == rows && tb.cols() == cols &&
+                    aligned16(ta.dev_ptr()) && aligned16(tb.dev_ptr()) && !has_buf(ta, x.dev_ptr()) &&
+                    !has_buf(tb, x.dev_ptr()))
+                {
+                    xa = ta;
+                    xb = tb;
+                    pew_->ops.pop_back();
+                    if (pew_->ops.empty()) pew_.reset();
+                }
+            }
+        }
+        NN_CHECK(settle_reads_(xa.size() ? std::initializer_list<const Tensor*>{&xa, &xb}
+                                         : std::initializer_list<const Tensor*>{&x}));
         NN_TRY(o, alloc_(1, cols));
         prms_ = std::make_unique<PendingRms>();
         prms_->x = x;
+        prms_->xa = xa;
+        prms_->xb = xb;
         prms_->s = o;
         return R(o);
     }
@@ -3337,6 +3395,15 @@ Result<std::optional<Tensor>> HipEngine::rms_program_(const ExprSpec& spec, std:
         }
         std::unique_ptr<PendingRms> q = std::move(prms_);
         NN_TRY(o, alloc_(rows, cols));
+        if (q->xa.size())
+        {
+            NN_CHECK(settle_reads_({&q->xa, &q->xb}));
+            NN_CHECK(kernel_(nnhip_rmsnorm_forward_sum(D(q->xa), D(q->xb), W(q->x), D(*gamma), q->inv_f, q->eps,
+                                                       W(q->s), W(q->scaled), W(q->var_eps), W(q->rinv),
+                                                       W(q->normed), W(o), rows, cols, stream_),
+                             "rmsnorm forward"));
+            return R(o);
+        }
         NN_CHECK(kernel_(nnhip_rmsnorm_forward(D(q->x), D(*gamma), q->inv_f, q->eps, W(q->s), W(q->scaled),
                                                W(q->var_eps), W(q->rinv), W(q->normed), W(o), rows, cols, stream_),
                          "rmsnorm forward"));
@@ -3351,6 +3418,10 @@ Result<void> HipEngine::settle_rms_()
     if (!prms_) return {};
     std::unique_ptr<PendingRms> r = std::move(prms_);
     const std::size_t F = r->x.rows(), N = r->x.cols();
+    if (r->bwd && r->stage == 3)
+        return kernel_(nnhip_rmsnorm_backward(D(r->x), D(r->gamma), D(r->normed), D(r->rinv), r->inv_f, W(r->s),
+                                              W(r->scaled), W(r->dx), F, N, stream_),
+                       "rmsnorm backward");
     if (r->bwd)
     {
         NN_CHECK(kernel_(nnhip_rmsnorm_bwd_colsum(D(r->x), D(r->gamma), D(r->normed), W(r->s), F, N, stream_),
@@ -3360,6 +3431,14 @@ Result<void> HipEngine::settle_rms_()
                                                              static_cast<unsigned>(BinaryOp::Mul), r->inv_f, 0, stream_),
                              "elementwise_binary_scalar"));
         return {};
+    }
+    if (r->xa.size())
+    {
+        // the residual add first, then the calls recorded so far
+        NN_CHECK(settle_reads_({&r->xa, &r->xb}));
+        NN_CHECK(kernel_(nnhip_elementwise_binary(D(r->xa), D(r->xb), W(r->x), r->x.size(),
+                                                  static_cast<unsigned>(BinaryOp::Add), stream_),
+                         "elementwise_binary"));
     }
     if (r->stage == 6)
         return kernel_(nnhip_rmsnorm_forward(D(r->x), D(r->gamma), r->inv_f, r->eps, W(r->s), W(r->scaled),

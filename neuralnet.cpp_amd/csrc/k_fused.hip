@@ -245,12 +245,15 @@ __global__ __launch_bounds__(kColT) void k_fused_colsum(F f, float* out, unsigne
 // separate kernel, so the results equal the six calls' bit for bit. A thread
 // keeps its KM rows of x in registers between the sums and the products:
 // x is read once. s, scaled and var_eps are written when their pointer is set.
-template <unsigned KM>
+// SUM: x is formed as x + xb while it is read (the block's residual add that
+// precedes the layer, GPTBlock::forward, rounded as that add) and written to xs.
+template <unsigned KM, bool SUM = false>
 __global__ __launch_bounds__(kColT) void k_rms_fwd(const float* __restrict__ x, const float* __restrict__ gamma,
                                                    float inv_f, float eps, float* s_raw, float* scaled,
                                                    float* var_eps, float* __restrict__ rinv,
                                                    float* __restrict__ normed, float* __restrict__ out,
-                                                   unsigned rows, unsigned cols4, size_t cols)
+                                                   unsigned rows, unsigned cols4, size_t cols,
+                                                   const float* __restrict__ xb, float* __restrict__ xs)
 {
     __shared__ float4 part[kColWaves][kColQuads];
     __shared__ float4 rq[kColQuads];
@@ -266,6 +269,21 @@ __global__ __launch_bounds__(kColT) void k_rms_fwd(const float* __restrict__ x, 
         {
             const unsigned r = rg + k * kRowGroups;
             if (r < rows) xv[k] = ld4(x + size_t(r) * cols + 4u * q);
+        }
+        if constexpr (SUM)
+        {
+            float4 yv[KM];
+#pragma unroll
+            for (unsigned k = 0; k < KM; ++k)
+                if (rg + k * kRowGroups < rows) yv[k] = ld4(xb + size_t(rg + k * kRowGroups) * cols + 4u * q);
+#pragma unroll
+            for (unsigned k = 0; k < KM; ++k)
+                if (rg + k * kRowGroups < rows)
+                {
+#pragma clang fp contract(off)
+                    xv[k] = make_float4(xv[k].x + yv[k].x, xv[k].y + yv[k].y, xv[k].z + yv[k].z, xv[k].w + yv[k].w);
+                    st4(xs + size_t(rg + k * kRowGroups) * cols + 4u * q, xv[k]);
+                }
         }
 #pragma unroll
         for (unsigned k = 0; k < KM; ++k)
@@ -342,18 +360,21 @@ __global__ __launch_bounds__(kColT) void k_rms_fwd(const float* __restrict__ x, 
 // (g * gamma[r] - m * normed) * rinv, each with its separate kernel's
 // expression and k_fused_colsum's summation order, so equal bit for bit; g and
 // normed are read once.
-template <unsigned KM>
+// ADD: also out2 = addend + dx (the block's residual add of the gradient that
+// follows the layer, GPTBlock::backward, rounded as that add).
+template <unsigned KM, bool ADD = false>
 __global__ __launch_bounds__(kColT) void k_rms_bwd(const float* __restrict__ g, const float* __restrict__ gamma,
                                                    const float* __restrict__ nrm, const float* __restrict__ rinv,
                                                    float inv_f, float* m_raw, float* __restrict__ m,
-                                                   float* __restrict__ dx, unsigned rows, unsigned cols4, size_t cols)
+                                                   float* __restrict__ dx, unsigned rows, unsigned cols4, size_t cols,
+                                                   const float* __restrict__ addend, float* __restrict__ out2)
 {
     __shared__ float4 part[kColWaves][kColQuads];
     __shared__ float4 mq[kColQuads];
     const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const unsigned qi = lane % kColQuads, rg = threadIdx.x / kColQuads;
     const unsigned q = blockIdx.x * kColQuads + qi;
-    float4 gv[KM], nv[KM];
+    float4 gv[KM], nv[KM], av[ADD ? KM : 1];
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (q < cols4)
     {
@@ -366,6 +387,7 @@ __global__ __launch_bounds__(kColT) void k_rms_bwd(const float* __restrict__ g, 
                 const size_t i = size_t(r) * cols + 4u * q;
                 gv[k] = ld4(g + i);
                 nv[k] = ld4(nrm + i);
+                if constexpr (ADD) av[k] = ld4(addend + i);
             }
         }
 #pragma unroll
@@ -426,9 +448,16 @@ __global__ __launch_bounds__(kColT) void k_rms_bwd(const float* __restrict__ g, 
             {
                 const float gr = gamma[r];
                 const float4 a = gv[k], c = nv[k];
-                st4(dx + size_t(r) * cols + 4u * q,
-                    make_float4(RmsDx::one(a.x, gr, b.x, c.x, d.x), RmsDx::one(a.y, gr, b.y, c.y, d.y),
-                                RmsDx::one(a.z, gr, b.z, c.z, d.z), RmsDx::one(a.w, gr, b.w, c.w, d.w)));
+                const size_t i = size_t(r) * cols + 4u * q;
+                const float4 v = make_float4(RmsDx::one(a.x, gr, b.x, c.x, d.x), RmsDx::one(a.y, gr, b.y, c.y, d.y),
+                                             RmsDx::one(a.z, gr, b.z, c.z, d.z), RmsDx::one(a.w, gr, b.w, c.w, d.w));
+                st4(dx + i, v);
+                if constexpr (ADD)
+                {
+#pragma clang fp contract(off)   // dx rounded first, as the separate add reads it
+                    const float4 e = av[k];
+                    st4(out2 + i, make_float4(e.x + v.x, e.y + v.y, e.z + v.z, e.w + v.w));
+                }
             }
         }
     }
@@ -610,6 +639,51 @@ extern "C" int nnhip_rmsnorm_sumsq(const float* X, float* out, size_t F, size_t 
     return launch_colsum(SumSq{X, N}, out, F, N, static_cast<hipStream_t>(stream));
 }
 
+namespace
+{
+template <bool SUM>
+int rms_forward_wide(const float* X, const float* Xb, float* Xs, const float* gamma, float inv_f, float eps,
+                     float* s_raw, float* scaled, float* var_eps, float* rinv, float* normed, float* out, size_t F,
+                     size_t N, hipStream_t s)
+{
+    if (!shape_ok(F, N, {X, rinv, normed, out, s_raw, scaled, var_eps})) return kBadShape;
+    if (N == 0) return 0;
+    const unsigned cols4 = unsigned(N / 4);
+    const dim3 grid((cols4 + kColQuads - 1) / kColQuads), block(kColT);
+    if (F <= 2 * kRowGroups)
+        hipLaunchKernelGGL((k_rms_fwd<2, SUM>), grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
+                           normed, out, unsigned(F), cols4, N, Xb, Xs);
+    else if (F <= 6 * kRowGroups)
+        hipLaunchKernelGGL((k_rms_fwd<6, SUM>), grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
+                           normed, out, unsigned(F), cols4, N, Xb, Xs);
+    else
+        hipLaunchKernelGGL((k_rms_fwd<8, SUM>), grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
+                           normed, out, unsigned(F), cols4, N, Xb, Xs);
+    return launch_status();
+}
+
+template <bool ADD>
+int rms_backward_wide(const float* G, const float* gamma, const float* Nrm, const float* rinv, float inv_f,
+                      float* m_raw, float* m, float* dx, const float* addend, float* out2, size_t F, size_t N,
+                      hipStream_t s)
+{
+    if (!shape_ok(F, N, {G, Nrm, rinv, m, dx, m_raw})) return kBadShape;
+    if (N == 0) return 0;
+    const unsigned cols4 = unsigned(N / 4);
+    const dim3 grid((cols4 + kColQuads - 1) / kColQuads), block(kColT);
+    if (F <= 2 * kRowGroups)
+        hipLaunchKernelGGL((k_rms_bwd<2, ADD>), grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx,
+                           unsigned(F), cols4, N, addend, out2);
+    else if (F <= 6 * kRowGroups)
+        hipLaunchKernelGGL((k_rms_bwd<6, ADD>), grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx,
+                           unsigned(F), cols4, N, addend, out2);
+    else
+        hipLaunchKernelGGL((k_rms_bwd<8, ADD>), grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx,
+                           unsigned(F), cols4, N, addend, out2);
+    return launch_status();
+}
+} // namespace
+
 extern "C" int nnhip_rmsnorm_forward(const float* X, const float* gamma, float inv_f, float eps, float* s_raw,
                                      float* scaled, float* var_eps, float* rinv, float* normed, float* out, size_t F,
                                      size_t N, void* stream)
@@ -622,20 +696,18 @@ extern "C" int nnhip_rmsnorm_forward(const float* X, const float* gamma, float i
                            scaled, var_eps, rinv, normed, out, unsigned(F), N);
         return launch_status();
     }
-    if (!shape_ok(F, N, {X, rinv, normed, out, s_raw, scaled, var_eps})) return kBadShape;
-    if (N == 0) return 0;
-    const unsigned cols4 = unsigned(N / 4);
-    const dim3 grid((cols4 + kColQuads - 1) / kColQuads), block(kColT);
-    if (F <= 2 * kRowGroups)
-        hipLaunchKernelGGL(k_rms_fwd<2>, grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
-                           normed, out, unsigned(F), cols4, N);
-    else if (F <= 6 * kRowGroups)
-        hipLaunchKernelGGL(k_rms_fwd<6>, grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
-                           normed, out, unsigned(F), cols4, N);
-    else
-        hipLaunchKernelGGL(k_rms_fwd<8>, grid, block, 0, s, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv,
-                           normed, out, unsigned(F), cols4, N);
-    return launch_status();
+    return rms_forward_wide<false>(X, nullptr, nullptr, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv, normed, out,
+                                   F, N, s);
+}
+
+extern "C" int nnhip_rmsnorm_forward_sum(const float* A, const float* B, float* X, const float* gamma, float inv_f,
+                                         float eps, float* s_raw, float* scaled, float* var_eps, float* rinv,
+                                         float* normed, float* out, size_t F, size_t N, void* stream)
+{
+    if (!A || !B || !X || !gamma || !rinv || !normed || !out || F == 0 || F > 8 * kRowGroups) return kBadShape;
+    if (!shape_ok(F, N, {A, B, X})) return kBadShape;
+    return rms_forward_wide<true>(A, B, X, gamma, inv_f, eps, s_raw, scaled, var_eps, rinv, normed, out, F, N,
+                                  static_cast<hipStream_t>(stream));
 }
 
 extern "C" int nnhip_rmsnorm_backward(const float* G, const float* gamma, const float* Nrm, const float* rinv,
@@ -643,21 +715,19 @@ extern "C" int nnhip_rmsnorm_backward(const float* G, const float* gamma, const 
                                       void* stream)
 {
     if (!G || !gamma || !Nrm || !rinv || !m || !dx || F == 0 || F > 8 * kRowGroups) return kBadShape;
-    if (!shape_ok(F, N, {G, Nrm, rinv, m, dx, m_raw})) return kBadShape;
-    if (N == 0) return 0;
-    const unsigned cols4 = unsigned(N / 4);
-    const dim3 grid((cols4 + kColQuads - 1) / kColQuads), block(kColT);
-    const auto s = static_cast<hipStream_t>(stream);
-    if (F <= 2 * kRowGroups)
-        hipLaunchKernelGGL(k_rms_bwd<2>, grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx, unsigned(F),
-                           cols4, N);
-    else if (F <= 6 * kRowGroups)
-        hipLaunchKernelGGL(k_rms_bwd<6>, grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx, unsigned(F),
-                           cols4, N);
-    else
-        hipLaunchKernelGGL(k_rms_bwd<8>, grid, block, 0, s, G, gamma, Nrm, rinv, inv_f, m_raw, m, dx, unsigned(F),
-                           cols4, N);
-    return launch_status();
+    return rms_backward_wide<false>(G, gamma, Nrm, rinv, inv_f, m_raw, m, dx, nullptr, nullptr, F, N,
+                                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nnhip_rmsnorm_backward_add(const float* G, const float* gamma, const float* Nrm, const float* rinv,
+                                          float inv_f, float* m_raw, float* m, float* dx, const float* addend,
+                                          float* out2, size_t F, size_t N, void* stream)
+{
+    if (!G || !gamma || !Nrm || !rinv || !m || !dx || !addend || !out2 || F == 0 || F > 8 * kRowGroups)
+        return kBadShape;
+    if (!shape_ok(F, N, {addend, out2})) return kBadShape;
+    return rms_backward_wide<true>(G, gamma, Nrm, rinv, inv_f, m_raw, m, dx, addend, out2, F, N,
+                                   static_cast<hipStream_t>(stream));
 }
 
 extern "C" int nnhip_colbcast_mul(const float* X, const float* v, float* out, size_t F, size_t N, void* stream)

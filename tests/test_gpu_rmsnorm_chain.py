@@ -6,7 +6,9 @@ dx = (g * gamma - m * normed) * rinv.
 The HIP engine records these calls and, when the chain's last one arrives, runs
 them as one pass (nnhip_rmsnorm_forward / nnhip_rmsnorm_backward, the big inputs
 read once); any other use of an intermediate, or a write to an input, runs the
-calls so far with their separate kernels. Bars: every output of the one-pass run
+calls so far with their separate kernels. The GPT block's residual adds join
+these passes: x + a recorded before the forward's first call is formed by the
+forward pass, and grad + dx after the backward's dx call by the backward pass. Bars: every output of the one-pass run
 bit-identical to the separate kernels' (the chain cut right after its first
 call), every cut variant equal to it too, and all of them within 1e-5
 (normwise) of the oracle running the same calls.
@@ -140,3 +142,91 @@ def test_rmsnorm_backward_chain(hip, cpu, F, N):
     g64, n64, a64 = Gr.astype(np.float64), Nm.astype(np.float64), Ga.astype(np.float64)
     m = (g64 * a64 * n64).sum(0, keepdims=True) / F
     assert nrm_err(fused["dx"], (g64 * a64 - m * n64) * Ri.astype(np.float64)) <= 1e-5
+
+
+# ── the block's residual adds taken into the RMSNorm passes (GPTBlock, compute_layer.hpp:2366-2405) ──
+def residual_chain(e, X, A, G, eps, cut=None):
+    """y = x + a (GPTBlock::forward's residual add), then the layer's six calls on y; `cut`: "y" reads y
+    after the first call, "write_a" scales a in place before the scale call, "early" reads y right
+    after the add (the add then runs alone)."""
+    F, N = X.shape
+    x, a, g = e.tensor(X), e.tensor(A), e.tensor(G)
+    y = e.elementwise_binary("Add", x, a)
+    if cut == "early":
+        y.numpy()
+    s = e.eval_expr_reduce(SQ, [y, y], F, N)
+    if cut == "y":
+        y.numpy()
+    sc = e.elementwise_binary_scalar("Mul", s, 1.0 / F)
+    ve = e.elementwise_binary_scalar("Add", sc, eps)
+    ri = e.elementwise_unary("Rsqrt", ve)
+    nm = e.eval_expr(NORM, [y, ri], F, N)
+    if cut == "write_a":
+        e.scale_inplace(a, 2.0)
+    out = e.eval_expr(SCALE, [nm, g], F, N)
+    res = dict(zip(NAMES, (t.numpy() for t in (s, sc, ve, ri, nm, out))))
+    res["y"], res["a"] = y.numpy(), a.numpy()
+    return res
+
+
+@pytest.mark.parametrize("F,N", [(768, 8192), (128, 36), (1100, 40), (300, 100), (768, 1), (200, 13)])
+def test_residual_add_then_rmsnorm(hip, cpu, F, N):
+    """The recorded x + a is formed and written by the RMSNorm pass (nnhip_rmsnorm_forward_sum) when
+    N % 4 == 0: every output bit-identical to the add and the chain run apart ("early"), the cut
+    variants equal too, a written in place after y was recorded leaves y as it was."""
+    rng = np.random.default_rng(F * 17 + N)
+    X, A, G = normal(rng, (F, N)), normal(rng, (F, N)), uniform(rng, (F, 1), 0.5, 1.5)
+    eps = 1e-5
+    fused = residual_chain(hip, X, A, G, eps)
+    apart = residual_chain(hip, X, A, G, eps, "early")
+    ref = residual_chain(cpu, X, A, G, eps)
+    for n in NAMES + ("y",):
+        assert np.array_equal(bits(fused[n]), bits(apart[n])), n
+        assert nrm_err(fused[n], ref[n]) <= 1e-5, n
+    assert np.array_equal(bits(fused["y"]), bits(X + A))
+    for cut in ("y", "write_a"):
+        print(f"[rmsnorm residual] F{F} N{N} cut={cut}", flush=True)
+        other = residual_chain(hip, X, A, G, eps, cut)
+        for n in NAMES + ("y",):
+            assert np.array_equal(bits(fused[n]), bits(other[n])), (cut, n)
+        assert np.array_equal(bits(other["a"]), bits(A * (2.0 if cut == "write_a" else 1.0))), cut
+
+
+def residual_bwd_chain(e, Gr, Ga, Nm, Ri, E, cut=None, swap=False):
+    """The backward's calls, then out = e + dx (GPTBlock::backward's residual add; dx + e when
+    `swap`); `cut`: "dx" reads dx before the add (the add then runs alone), "write_e" scales e in
+    place before the add."""
+    F, N = Gr.shape
+    g, ga, nm, ri, ee = e.tensor(Gr), e.tensor(Ga), e.tensor(Nm), e.tensor(Ri), e.tensor(E)
+    m_raw = e.eval_expr_reduce(BCOL, [g, ga, nm], F, N)
+    m = e.elementwise_binary_scalar("Mul", m_raw, 1.0 / F)
+    dx = e.eval_expr(BDX, [g, ga, m, nm, ri], F, N)
+    gg = e.eval_expr_reduce(BROW, [g, ga, nm], F, N)
+    if cut == "dx":
+        dx.numpy()
+    if cut == "write_e":
+        e.scale_inplace(ee, 2.0)
+    out = e.elementwise_binary("Add", dx, ee) if swap else e.elementwise_binary("Add", ee, dx)
+    res = dict(zip(BNAMES, (t.numpy() for t in (m_raw, m, dx, gg))))
+    res["out"] = out.numpy()
+    return res
+
+
+@pytest.mark.parametrize("F,N", [(768, 8192), (128, 36), (1100, 40), (300, 100)])
+def test_rmsnorm_backward_then_residual_add(hip, cpu, F, N):
+    """The recorded dx and the add of the incoming gradient run as one pass
+    (nnhip_rmsnorm_backward_add): dx and the sum bit-identical to the calls run apart."""
+    rng = np.random.default_rng(F * 3 + N)
+    Gr, Nm, E = normal(rng, (F, N)), normal(rng, (F, N)), normal(rng, (F, N))
+    Ga, Ri = uniform(rng, (F, 1), 0.5, 1.5), uniform(rng, (1, N), 0.5, 2.0)
+    fused = residual_bwd_chain(hip, Gr, Ga, Nm, Ri, E)
+    apart = residual_bwd_chain(hip, Gr, Ga, Nm, Ri, E, "dx")
+    ref = residual_bwd_chain(cpu, Gr, Ga, Nm, Ri, E)
+    for n in BNAMES + ("out",):
+        assert np.array_equal(bits(fused[n]), bits(apart[n])), n
+        assert nrm_err(fused[n], ref[n]) <= 1e-5, n
+    assert np.array_equal(bits(fused["out"]), bits(E + fused["dx"]))
+    swapped = residual_bwd_chain(hip, Gr, Ga, Nm, Ri, E, swap=True)
+    assert np.array_equal(bits(swapped["out"]), bits(fused["out"]))
+    w = residual_bwd_chain(hip, Gr, Ga, Nm, Ri, E, "write_e")
+    assert np.array_equal(bits(w["out"]), bits(E * np.float32(2.0) + fused["dx"]))
