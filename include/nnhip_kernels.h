@@ -50,6 +50,13 @@ int nnhip_gemm(const float* A, const float* B, float* C, size_t A_rows, size_t A
 int nnhip_gemm_heads(const float* W, const float* X, const float* row_bias, float* out, size_t M, size_t K, size_t B,
                      size_t T, void* stream);
 
+/* nnhip_gemm_heads with W stored (K, M) when transW (out_b = W^T X_b): the attention's output projection
+ * backward, grad_concat = matmul(W_o, G, true, false) (compute_layer.hpp:179 in Linear::backward), followed
+ * by its head split rearrange_3d(grad_concat, H d_k, B, T) (:1281-1291), written in the heads' layout
+ * directly. No CUDA counterpart. */
+int nnhip_gemm_heads_ex(const float* W, const float* X, const float* row_bias, float* out, size_t M, size_t K,
+                        size_t B, size_t T, int transW, void* stream);
+
 /* Up to three such products of one X in one launch (the q, k and v projections): out[i] as
  * nnhip_gemm_heads(W[i], X, row_bias ? row_bias[i] : NULL, out[i], ...); count in 1..3, count * B <= 65535,
  * row_bias may be NULL (no bias) or hold NULL entries. No CUDA counterpart. */

@@ -507,6 +507,9 @@ struct HipEngine::PendingLayout
     Tensor S, out;
     bool per_batch;
     std::size_t M, B, N;   // per_batch: out (B*M, N) from S (B*N, M)
+    // merge: out (M, B*N) = rearrange_3d(S, M, B, N, inverse), S (B*M, N)
+    // holding the heads' rows (the attention's per-sequence layout)
+    bool merge = false;
     bool uses(const float* p) const { return has_buf(S, p) || has_buf(out, p); }
 };
 
@@ -1196,6 +1199,7 @@ Result<void> HipEngine::materialise_layout_(const PendingLayout& r)
         if (pmm_ && pmm_->yields(sp)) NN_CHECK(settle_mm_());
         if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(sp, false));
     }
+    if (r.merge) return kernel_(nnhip_rearrange_3d(D(r.S), W(r.out), r.M, r.B, r.N, 1u, stream_), "rearrange_3d");
     if (!r.per_batch)
         return kernel_(nnhip_transpose(D(r.S), W(r.out), r.S.rows(), r.S.cols(), stream_), "transpose");
     return kernel_(nnhip_transpose_batched(D(r.S), W(r.out), r.B, r.N, r.M, stream_), "rearrange_3d");
@@ -1214,7 +1218,14 @@ Result<void> HipEngine::settle_layout_()
 const HipEngine::PendingLayout* HipEngine::layout_of_(const Tensor& t) const
 {
     for (const PendingLayout& r : playout_)
-        if (same_t(r.out, t)) return &r;
+        if (!r.merge && same_t(r.out, t)) return &r;
+    return nullptr;
+}
+
+const HipEngine::PendingLayout* HipEngine::merge_of_(const Tensor& t) const
+{
+    for (const PendingLayout& r : playout_)
+        if (r.merge && same_t(r.out, t)) return &r;
     return nullptr;
 }
 
@@ -2026,6 +2037,35 @@ Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size
             Tensor out = r->heads;   // written by the group launch of an earlier head split
             r->heads = Tensor();
             return out;
+        }
+        // Of a recorded W^T G (the attention's output projection backward, then
+        // its head split, compute_layer.hpp:1281-1291): the product writes the
+        // heads' layout; its own output becomes a recorded merge of those rows,
+        // made only if something reads it.
+        if (r && !r->folded && r->tA && !r->tB && r->plus.empty() && !r->out2.size() && !r->bias.size() &&
+            !r->heads.size() && r->M == M && r->N == B * N && x.rows() == M && B <= 65535)
+        {
+            NN_CHECK(settle_reads_({&r->A, &r->B}));
+            // (settling may have launched the record)
+            PendingMm* q = nullptr;
+            if (pmm_ && same_t(x, pmm_->C)) q = pmm_.get();
+            for (auto& p : pmm_prev_)
+                if (same_t(x, p->C)) q = p.get();
+            if (q == r)
+            {
+                NN_TRY(h, alloc_(B * M, N));
+                prof_begin_();
+                const int rc = nnhip_gemm_heads_ex(D(r->A), D(r->B), nullptr, W(h), M, r->K, B, N, 1, stream_);
+                prof_end_(M, N, r->K, B, true, false);
+                NN_CHECK(kernel_(rc, "matmul into heads"));
+                const Tensor C = r->C;
+                if (pmm_ && pmm_.get() == r)
+                    pmm_.reset();
+                else
+                    std::erase_if(pmm_prev_, [r](const std::unique_ptr<PendingMm>& p) { return p.get() == r; });
+                NN_CHECK(push_layout_(PendingLayout{h, C, false, M, B, N, true}));
+                return h;
+            }
         }
         // A launch covers members x B sequences in grid z (at most 65535).
         auto fits = [&](const PendingMm& q) {

@@ -1279,6 +1279,15 @@ extern "C" int nnhip_gemm_heads(const float* W, const float* X, const float* row
                          Epi{row_bias, 0});
 }
 
+extern "C" int nnhip_gemm_heads_ex(const float* W, const float* X, const float* row_bias, float* out, size_t M,
+                                   size_t K, size_t B, size_t T, int transW, void* stream)
+{
+    // nnhip_gemm_heads with W stored (K, M) when transW: out_b = W^T X_b (+ bias)
+    if (!W || !X || !out || B == 0 || T == 0 || M == 0 || K == 0) return -1;
+    return gemm_dispatch(W, X, out, M, T, K, transW ? M : K, B * T, 0, T, M * T, transW != 0, false, 1.0f, B, nullptr,
+                         0, stream, Epi{row_bias, 0});
+}
+
 extern "C" int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* const* row_bias,
                                       float* const* out, size_t count, size_t M, size_t K, size_t B, size_t T,
                                       void* stream)

@@ -275,6 +275,7 @@ private:
     Result<void> materialise_layout_(const PendingLayout& r);
     Result<void> settle_layout_();
     const PendingLayout* layout_of_(const Tensor& t) const;
+    const PendingLayout* merge_of_(const Tensor& t) const;
     Result<void> settle_layout_for_(const Tensor& t);
     // A row sum not launched yet (a Linear bias gradient, RMSNorm's gamma gradient).
     struct PendingRowSum;

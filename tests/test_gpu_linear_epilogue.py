@@ -175,3 +175,38 @@ def test_projections_into_heads(hip, cpu, D, B, T):
     ref = _heads(cpu, Ws, bs, X, B, T, "read")
     for a, b in zip(fold, ref):
         assert nrm_err(a, b) <= 1e-5
+
+
+def _out_proj_bwd_heads(e, W, G, B, T, how):
+    """AttentionBase::backward's first steps: grad_concat = matmul(W_o, G, true, false) (Linear::backward),
+    then rearrange_3d(grad_concat, H_dk, B, T). "fold": as issued (the product writes the heads' layout,
+    grad_concat itself recorded as a merge of those rows); "read": grad_concat read first (the separate
+    calls); "write_h": the head split scaled in place before grad_concat is read (the merge must see
+    the rows as they were)."""
+    gc = e.matmul(e.tensor(W), e.tensor(G), True, False)
+    if how == "read":
+        gc.numpy()
+    h = e.rearrange_3d(gc, W.shape[1], B, T, False)
+    hv = h.numpy()
+    if how == "write_h":
+        e.scale_inplace(h, 2.0)
+    return [hv, gc.numpy()] + ([h.numpy()] if how == "write_h" else [])
+
+
+@pytest.mark.parametrize("D,B,T", [(768, 8, 1024), (64, 3, 40), (96, 2, 36)])
+def test_output_projection_backward_into_heads(hip, cpu, D, B, T):
+    """nnhip_gemm_heads_ex (transposed W): the output projection's input gradient written in the heads'
+    layout, bit-identical to the product then rearrange_3d; the product itself, read afterwards, comes
+    from those rows and is bit-identical too, also after the rows were overwritten."""
+    rng = np.random.default_rng(3 * D + B + T)
+    W, G = uniform(rng, (D, D)), uniform(rng, (D, B * T))
+    fold = _out_proj_bwd_heads(hip, W, G, B, T, "fold")
+    sep = _out_proj_bwd_heads(hip, W, G, B, T, "read")
+    for i, (a, b) in enumerate(zip(fold, sep)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+    w = _out_proj_bwd_heads(hip, W, G, B, T, "write_h")
+    assert np.array_equal(w[1].view(np.uint32), sep[1].view(np.uint32))
+    assert np.array_equal(w[2], sep[0] * np.float32(2.0))
+    ref = _out_proj_bwd_heads(cpu, W, G, B, T, "read")
+    for a, b in zip(fold, ref):
+        assert nrm_err(a, b) <= 1e-5
