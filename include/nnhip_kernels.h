@@ -63,6 +63,17 @@ int nnhip_gemm_heads_ex(const float* W, const float* X, const float* row_bias, f
 int nnhip_gemm_heads_group(const float* const* W, const float* X, const float* const* row_bias, float* const* out,
                            size_t count, size_t M, size_t K, size_t B, size_t T, void* stream);
 
+/* An operand stored by sequence, as the attention's heads' layout stores a (rows, B * T) matrix: its
+ * contiguous index c (k of an untransposed A, n of an untransposed B, k of a transposed B) lies at
+ * (c / len) * step + c % len and its rows len apart; len a multiple of 16 (of 128 for an untransposed B),
+ * step a multiple of 4 and >= len. The attention's rearrange_3d(x, H d_k, B, T, inverse) of such rows
+ * (compute_layer.hpp:1256-1259, :1377-1386) is then read in place: len = T, step = H d_k T. len 0: an
+ * ordinary operand. */
+typedef struct nnhip_by_seq
+{
+    size_t len, step;
+} nnhip_by_seq;
+
 /* C_i (M, N) = [C_i +] A_i op(B), i < count (1..4): products sharing B in one launch, split-K over all of
  * them and one reduction; A_i stored (M, K), B (K, N) or (N, K) with transB, every C_i 16-byte aligned and
  * M*N % 4 == 0. The attention's q, k and v Linear backward each add G_i X^T into its weight gradient with
@@ -85,6 +96,16 @@ int nnhip_gemm_group_acc_each(const float* const* A, const float* const* B, floa
                               size_t M, size_t N, size_t K, int transB, int accumulate, float* const* row_sums,
                               int row_sums_accumulate, void* workspace, size_t workspace_bytes, void* stream);
 
+/* nnhip_gemm_group_acc_each with transB, member i's A and / or B stored by sequence (a_seq[i], b_seq[i];
+ * either array may be NULL): the q, k and v layers' gradients G_i come from the attention backward as heads'
+ * rows (compute_layer.hpp:1377-1386 rearranges them back) and the output projection's input is the
+ * attention output as heads' rows (:1256-1259); the weight gradients read them in place. Returns -7 when
+ * the shapes do not give whole tiles (the caller rearranges instead). No CUDA counterpart. */
+int nnhip_gemm_group_acc_seq(const float* const* A, const float* const* B, float* const* C, size_t count, size_t M,
+                             size_t N, size_t K, int transB, int accumulate, float* const* row_sums,
+                             int row_sums_accumulate, const nnhip_by_seq* a_seq, const nnhip_by_seq* b_seq,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* C (M, N) = alpha * sum_i A_i^T B_i over count (1..3) products of one shape, one accumulator over
  * K = count * K_each in segment order: A_i stored (K_each, M), B_i (K_each, N), all 16-byte aligned, M and N
  * multiples of 4, K_each a multiple of 16. The attention's input gradient is three Linear backward products
@@ -93,6 +114,22 @@ int nnhip_gemm_group_acc_each(const float* const* A, const float* const* B, floa
  * separate calls, not bit-identical). Workspace as nnhip_gemm at K = count * K_each. No CUDA counterpart. */
 int nnhip_gemm_tn_sum(const float* const* A, const float* const* B, size_t count, float* C, size_t M, size_t N,
                       size_t K_each, float alpha, void* workspace, size_t workspace_bytes, void* stream);
+
+/* nnhip_gemm_tn_sum with every B_i stored by sequence along n (b_seq): the attention's input gradient
+ * Wq^T gQ + Wk^T gK + Wv^T gV (compute_layer.hpp:1397-1408) from gQ, gK, gV as the backward's heads' rows,
+ * without their rearrange (:1377-1386). Returns -7 when the shapes do not give whole tiles. No CUDA
+ * counterpart. */
+int nnhip_gemm_tn_sum_seq(const float* const* A, const float* const* B, size_t count, float* C, size_t M, size_t N,
+                          size_t K_each, float alpha, nnhip_by_seq b_seq, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* C (M, N) = [C +] alpha A B [+ row_bias], A (M, K) stored as it is, B (K, N) stored by sequence along n
+ * (b_seq), rounded as nnhip_gemm_epilogue: the attention's output projection of its output as heads' rows
+ * (compute_layer.hpp:1256-1259 rearranges them, then Linear::forward). Returns -7 when the shapes do not
+ * give whole tiles. No CUDA counterpart. */
+int nnhip_gemm_epilogue_seq(const float* A, const float* B, float* C, size_t M, size_t N, size_t K, float alpha,
+                            const float* row_bias, int accumulate, nnhip_by_seq b_seq, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* One product with the epilogue of the call that follows it in the reference's Linear layer
  * (compute_layer.hpp Linear::forward / backward): C = alpha * op(A) op(B), then C[i][j] += row_bias[i]

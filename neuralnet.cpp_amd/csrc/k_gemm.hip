@@ -59,6 +59,13 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // and the launch's B otherwise. With KSEG instead: up to three products of one
 // shape summed into one C (the q, k, v input gradients), k running through
 // segment i = k / klen of A[i] and B[i] in turn.
+//
+// SEG: operands stored by sequence, as the attention's heads' layout holds a
+// (rows, B * T) matrix: column c of the operand at (c / T) * step + c % T, its
+// rows T apart. Member i's A has its k columns so (aT[i] = T, aS[i] = step;
+// 0: plain), its B its n columns (untransposed B) or k columns (transposed).
+// A tile (n) or stage (k) never straddles two sequences (T a multiple of the
+// tile width and of BK), so this is an offset per tile or per stage.
 constexpr int kGroupMax = 4;
 struct GemmGroup
 {
@@ -68,6 +75,8 @@ struct GemmGroup
     int nb;
     const float* B[kGroupMax];
     int klen;
+    int aT[kGroupMax], bT[kGroupMax];
+    long aS[kGroupMax], bS[kGroupMax];
 };
 
 // RSUM: the row sums of A over k as well (Linear::backward's bias gradient
@@ -89,7 +98,7 @@ struct RowSums
 // sparse cross-entropy that follows the product (the GPT's lm_head logits)
 // merges these instead of reading C once more for them. Needs splits == 1.
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD, bool STATS = false, bool GRP = false,
-          bool KSEG = false, bool RSUM = false>
+          bool KSEG = false, bool RSUM = false, bool SEG = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K, long lda, long ldb,
                                                        long strideA, long strideB, long strideC, float alpha,
@@ -98,6 +107,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
                                                        RowSums rs = {})
 {
     static_assert(!RSUM || (GRP && !TA), "row sums of an untransposed A in grouped launches");
+    static_assert(!SEG || (!GUARD && !STATS), "operands by sequence in whole tiles only");
     constexpr int NT = 64 * WM * WN;
     constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
     constexpr int LA = BM * BK / 4 / NT;   // float4 per thread per stage for A
@@ -143,6 +153,20 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     const int k_lo = blockIdx.y * k_split;
     const int k_hi = min(K, k_lo + k_split);
     if (!STATS && gridDim.y > 1) C = part + ((long)blockIdx.y * gridDim.z + bz) * strideC;
+    // SEG: the member's sequence layouts (extra offset per sequence: step - T)
+    int sa_t = 0, sb_t = 0;
+    long sa_d = 0, sb_d = 0, b_off = 0;
+    if constexpr (SEG)
+    {
+        const int gi = GRP ? static_cast<int>(bz / grp.nb) : 0;
+        sa_t = grp.aT[gi];
+        sb_t = grp.bT[gi];
+        sa_d = grp.aS[gi] - sa_t;
+        sb_d = grp.bS[gi] - sb_t;
+        if (sa_t) lda = sa_t;   // rows of a sequence-stored operand are T apart
+        if (sb_t) ldb = sb_t;
+        if (!TB && sb_t) b_off = (long)(n0 / sb_t) * sb_d;
+    }
 
     f4 ra[LA], rb[LB];   // native vectors: HIP's float4 struct kept these arrays in scratch
 
@@ -162,6 +186,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     auto load_a = [&](int k0) {
         int kb;
         const float* Ap = seg_of(k0, grp.A, A, kb);
+        if constexpr (SEG && !TA)
+            if (sa_t) Ap += (long)(kb / sa_t) * sa_d;
 #pragma unroll
         for (int s = 0; s < LA; ++s)
         {
@@ -193,6 +219,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     auto load_b = [&](int k0) {
         int kb;
         const float* Bp = seg_of(k0, grp.B, B, kb);
+        if constexpr (SEG)
+        {
+            if (!TB) Bp += b_off;
+            else if (sb_t) Bp += (long)(kb / sb_t) * sb_d;
+        }
 #pragma unroll
         for (int s = 0; s < LB; ++s)
         {
@@ -721,6 +752,8 @@ struct Epi
     const GemmGroup* grp = nullptr;     // members of a grouped launch (no split, NN only)
     const GemmGroup* seg = nullptr;     // K segments summed into one C (TN only)
     const RowSums* rs = nullptr;        // grouped launches: the row sums of each member's A as well
+    const GemmGroup* sq = nullptr;      // plain launches: member 0 gives the operands' sequence layouts
+    bool by_seq = false;                // the group passed (grp, seg or sq) holds sequence layouts
 };
 
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB>
@@ -733,6 +766,32 @@ void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, l
     const bool guard = !vec_ok || (M % BM) || (N % BN) || (K % BK) || (k_split % BK);
     const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits), static_cast<unsigned>(batch));
     const dim3 block(64 * WM * WN);
+    if (e.by_seq)
+    {
+        if constexpr (TA && !TB)
+            if (e.seg && !guard)
+                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, false, true, false, true>), grid,
+                                   block, 0, s, A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part,
+                                   e.bias, e.accum, *e.seg);
+        if constexpr (!TA && TB)
+            if (e.grp && !guard)
+            {
+                if (e.rs)
+                    hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, true, false, true, true>), grid,
+                                       block, 0, s, A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split,
+                                       part, e.bias, e.accum, *e.grp, *e.rs);
+                else
+                    hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, true, false, false, true>),
+                                       grid, block, 0, s, A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split,
+                                       part, e.bias, e.accum, *e.grp, RowSums{});
+            }
+        if constexpr (!TA && !TB)
+            if (e.sq && !guard)
+                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, false, false, false, true>), grid,
+                                   block, 0, s, A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split, part,
+                                   e.bias, e.accum, *e.sq, RowSums{});
+        return;
+    }
     if constexpr (TA && !TB)
         if (e.seg)
         {
@@ -1081,12 +1140,30 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
     if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || batch > 65535) return -1;
     if (e.grp && tA) return -1;
     if (e.seg && !(tA && !tB)) return -1;
+    if (e.by_seq && !(tA && !tB ? e.seg != nullptr : !tA && tB ? e.grp != nullptr : !tA && !tB && e.sq != nullptr))
+        return -1;
     auto s = static_cast<hipStream_t>(stream);
-    if (int rc = 0; !e.grp && !e.seg && try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc))
+    if (int rc = 0; !e.grp && !e.seg && !e.by_seq &&
+                    try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc))
         return rc;
     Plan p = plan_gemm(M, N, K, batch, workspace != nullptr);
     if (p.splits > 1 && static_cast<size_t>(p.splits) * batch * (M * N + (e.rs ? M : 0)) * sizeof(float) > ws_bytes)
         p = plan_gemm(M, N, K, batch, false);
+    if (e.by_seq)
+    {
+        // whole tiles, 16-byte loads, and no tile or stage across two sequences
+        const GemmGroup& g = e.grp ? *e.grp : e.seg ? *e.seg : *e.sq;
+        const bool whole = M % p.bm == 0 && N % p.bn == 0 && K % 16 == 0 && p.k_split % 16 == 0 && lda % 4 == 0 &&
+                           ldb % 4 == 0 && sA % 4 == 0 && sB % 4 == 0 && aligned16(A) && aligned16(B);
+        if (!whole) return -7;
+        const int members = e.grp ? static_cast<int>(batch / g.nb) : 1;
+        for (int i = 0; i < members && i < kGroupMax; ++i)
+        {
+            if (g.aT[i] < 0 || g.bT[i] < 0 || g.aS[i] % 4 != 0 || g.bS[i] % 4 != 0) return -7;
+            if (g.aT[i] && (tA || g.aT[i] % 16 != 0 || g.aS[i] < g.aT[i])) return -7;
+            if (g.bT[i] && (g.bT[i] % (tB ? 16 : p.bn) != 0 || g.bS[i] < g.bT[i])) return -7;
+        }
+    }
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     RowSums rsl{};
     if (e.rs)
@@ -1199,17 +1276,28 @@ extern "C" int nnhip_gemm_epilogue(const float* A, const float* B, float* C, siz
 
 namespace
 {
-// The grouped accumulations: one B for every member (B_each null) or one each.
+bool seq_ok(const nnhip_by_seq* q, size_t n)
+{
+    if (!q) return true;
+    for (size_t i = 0; i < n; ++i)
+        if (q[i].len > 0x7fffffff || q[i].step > 0x7fffffffffffull) return false;
+    return true;
+}
+
+// The grouped accumulations: one B for every member (B_each null) or one each,
+// members' operands optionally stored by sequence.
 int group_acc(const float* const* A, const float* B, const float* const* B_each, float* const* C, size_t count,
               size_t M, size_t N, size_t K, int transB, int accumulate, float* const* row_sums,
-              int row_sums_accumulate, void* workspace, size_t workspace_bytes, void* stream)
+              int row_sums_accumulate, void* workspace, size_t workspace_bytes, void* stream,
+              const nnhip_by_seq* a_seq = nullptr, const nnhip_by_seq* b_seq = nullptr)
 {
     if (!A || !(B || B_each) || !C || count == 0 || count > kGroupMax || M == 0 || N == 0 || K == 0 ||
-        (M * N) % 4 != 0)
+        (M * N) % 4 != 0 || !seq_ok(a_seq, count) || !seq_ok(b_seq, count))
         return -1;
     GemmGroup g{};
     g.nb = 1;
     RowSums rs{};
+    bool by_seq = false;
     for (size_t i = 0; i < count; ++i)
     {
         if (!A[i] || !C[i] || !aligned16(C[i]) || (row_sums && !row_sums[i]) || (B_each && !B_each[i])) return -1;
@@ -1217,11 +1305,27 @@ int group_acc(const float* const* A, const float* B, const float* const* B_each,
         g.C[i] = C[i];
         g.B[i] = B_each ? B_each[i] : nullptr;
         rs.dst[i] = row_sums ? row_sums[i] : nullptr;
+        if (a_seq && a_seq[i].len)
+        {
+            g.aT[i] = static_cast<int>(a_seq[i].len);
+            g.aS[i] = static_cast<long>(a_seq[i].step);
+            by_seq = true;
+        }
+        if (b_seq && b_seq[i].len)
+        {
+            g.bT[i] = static_cast<int>(b_seq[i].len);
+            g.bS[i] = static_cast<long>(b_seq[i].step);
+            by_seq = true;
+        }
+        // members' loads are 16-byte loads when member 0's are
+        if (!aligned16(A[i]) || (B_each && !aligned16(B_each[i]))) return -1;
     }
     rs.acc = row_sums_accumulate ? 1 : 0;
     // A_i stored (M, K), B (K, N) or, with transB, (N, K); batch z of the launch is member z.
     Epi e{nullptr, accumulate ? 1 : 0};
     e.grp = &g;
+    e.by_seq = by_seq;
+    if (by_seq && !transB) return -1;
     if (row_sums) e.rs = &rs;
     return gemm_dispatch(A[0], B_each ? B_each[0] : B, C[0], M, N, K, K, transB ? K : N, M * K, 0, M * N, false,
                          transB != 0, 1.0f, count, workspace, workspace_bytes, stream, e);
@@ -1246,6 +1350,17 @@ extern "C" int nnhip_gemm_group_acc_each(const float* const* A, const float* con
                      workspace_bytes, stream);
 }
 
+extern "C" int nnhip_gemm_group_acc_seq(const float* const* A, const float* const* B, float* const* C, size_t count,
+                                        size_t M, size_t N, size_t K, int transB, int accumulate,
+                                        float* const* row_sums, int row_sums_accumulate, const nnhip_by_seq* a_seq,
+                                        const nnhip_by_seq* b_seq, void* workspace, size_t workspace_bytes,
+                                        void* stream)
+{
+    if (!B) return -1;
+    return group_acc(A, nullptr, B, C, count, M, N, K, transB, accumulate, row_sums, row_sums_accumulate, workspace,
+                     workspace_bytes, stream, a_seq, b_seq);
+}
+
 extern "C" int nnhip_gemm_tn_sum(const float* const* A, const float* const* B, size_t count, float* C, size_t M,
                                  size_t N, size_t K_each, float alpha, void* workspace, size_t workspace_bytes,
                                  void* stream)
@@ -1266,6 +1381,45 @@ extern "C" int nnhip_gemm_tn_sum(const float* const* A, const float* const* B, s
     Epi e{nullptr, 0};
     e.seg = &g;
     return gemm_dispatch(A[0], B[0], C, M, N, count * K_each, M, N, 0, 0, M * N, true, false, alpha, 1, workspace,
+                         workspace_bytes, stream, e);
+}
+
+extern "C" int nnhip_gemm_tn_sum_seq(const float* const* A, const float* const* B, size_t count, float* C, size_t M,
+                                     size_t N, size_t K_each, float alpha, nnhip_by_seq b_seq, void* workspace,
+                                     size_t workspace_bytes, void* stream)
+{
+    if (!A || !B || !C || count == 0 || count > 3 || K_each == 0 || K_each % 16 != 0 || M % 4 != 0 || N % 4 != 0 ||
+        count * K_each > 0x7fffffff || b_seq.len == 0 || !seq_ok(&b_seq, 1))
+        return -1;
+    GemmGroup g{};
+    g.klen = static_cast<int>(K_each);
+    g.bT[0] = static_cast<int>(b_seq.len);
+    g.bS[0] = static_cast<long>(b_seq.step);
+    for (size_t i = 0; i < count; ++i)
+    {
+        if (!A[i] || !B[i] || !aligned16(A[i]) || !aligned16(B[i])) return -1;
+        g.A[i] = A[i];
+        g.B[i] = B[i];
+    }
+    Epi e{nullptr, 0};
+    e.seg = &g;
+    e.by_seq = true;
+    return gemm_dispatch(A[0], B[0], C, M, N, count * K_each, M, b_seq.len, 0, 0, M * N, true, false, alpha, 1,
+                         workspace, workspace_bytes, stream, e);
+}
+
+extern "C" int nnhip_gemm_epilogue_seq(const float* A, const float* B, float* C, size_t M, size_t N, size_t K,
+                                       float alpha, const float* row_bias, int accumulate, nnhip_by_seq b_seq,
+                                       void* workspace, size_t workspace_bytes, void* stream)
+{
+    if (!A || !B || !C || b_seq.len == 0 || !seq_ok(&b_seq, 1)) return -1;
+    GemmGroup g{};
+    g.bT[0] = static_cast<int>(b_seq.len);
+    g.bS[0] = static_cast<long>(b_seq.step);
+    Epi e{row_bias, accumulate ? 1 : 0};
+    e.sq = &g;
+    e.by_seq = true;
+    return gemm_dispatch(A, B, C, M, N, K, K, b_seq.len, M * K, 0, M * N, false, false, alpha, 1, workspace,
                          workspace_bytes, stream, e);
 }
 
