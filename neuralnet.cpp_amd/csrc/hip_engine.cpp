@@ -1062,12 +1062,15 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb, bool
     if (prms_ && prms_->uses(p)) NN_CHECK(settle_rms_());
     if (prsum_ && prsum_->uses(p)) NN_CHECK(settle_rsum_());
     for (std::size_t i = playout_.size(); i-- > 0;)
+    {
+        if (i >= playout_.size()) continue;   // (a materialisation may settle others)
         if (playout_[i].uses(p))
         {
             const PendingLayout r = std::move(playout_[i]);
             playout_.erase(playout_.begin() + static_cast<std::ptrdiff_t>(i));
             if (live(r.out)) NN_CHECK(materialise_layout_(r));
         }
+    }
     std::erase_if(ptwo_, [p](const TwoPassOut& r) { return r.uses(p); });
     if (pdv_ && pdv_->uses(p)) NN_CHECK(settle_dv_());
     if (pds_ && pds_->uses(p)) NN_CHECK(settle_ds_());
@@ -1180,13 +1183,20 @@ void HipEngine::forget_dead_two_()
 Result<void> HipEngine::push_layout_(PendingLayout r)
 {
     std::erase_if(playout_, [](const PendingLayout& q) { return !live(q.out); });
-    constexpr std::size_t kKeep = 16;
-    if (playout_.size() >= kKeep)
-    {
-        const PendingLayout o = std::move(playout_.front());
-        playout_.erase(playout_.begin());
-        NN_CHECK(materialise_layout_(o));
-    }
+    // at most 16 transposes and 64 merges (the merges of a model's attention
+    // layers are kept from the forward to the backward) recorded
+    const std::size_t keep = r.merge ? 64 : 16;
+    std::size_t n = 0;
+    for (const PendingLayout& q : playout_) n += q.merge == r.merge;
+    if (n >= keep)
+        for (std::size_t i = 0; i < playout_.size(); ++i)
+            if (playout_[i].merge == r.merge)
+            {
+                const PendingLayout o = std::move(playout_[i]);
+                playout_.erase(playout_.begin() + static_cast<std::ptrdiff_t>(i));
+                NN_CHECK(materialise_layout_(o));
+                break;
+            }
     playout_.push_back(std::move(r));
     return {};
 }
@@ -1199,19 +1209,27 @@ Result<void> HipEngine::materialise_layout_(const PendingLayout& r)
         if (pmm_ && pmm_->yields(sp)) NN_CHECK(settle_mm_());
         if (!pmm_prev_.empty()) NN_CHECK(settle_mm_prev_(sp, false));
     }
-    if (r.merge) return kernel_(nnhip_rearrange_3d(D(r.S), W(r.out), r.M, r.B, r.N, 1u, stream_), "rearrange_3d");
+    if (r.merge)
+    {
+        NN_CHECK(settle_chain_reads_({&r.S}));
+        return kernel_(nnhip_rearrange_3d(D(r.S), W(r.out), r.M, r.B, r.N, 1u, stream_), "rearrange_3d");
+    }
     if (!r.per_batch)
         return kernel_(nnhip_transpose(D(r.S), W(r.out), r.S.rows(), r.S.cols(), stream_), "transpose");
     return kernel_(nnhip_transpose_batched(D(r.S), W(r.out), r.B, r.N, r.M, stream_), "rearrange_3d");
 }
 
-// Copies still referenced are made; the others are dropped.
+// Copies still referenced are made; the others are dropped. Merges stay
+// recorded (read in place by the products that take them, made when anything
+// else reads them or writes their rows).
 Result<void> HipEngine::settle_layout_()
 {
     std::vector<PendingLayout> rs = std::move(playout_);
     playout_.clear();
+    for (PendingLayout& r : rs)
+        if (r.merge && live(r.out)) playout_.push_back(std::move(r));
     for (const PendingLayout& r : rs)
-        if (live(r.out)) NN_CHECK(materialise_layout_(r));
+        if (!r.merge && r.out.dev_ptr() && live(r.out)) NN_CHECK(materialise_layout_(r));
     return {};
 }
 
@@ -2114,6 +2132,15 @@ Result<Tensor> HipEngine::rearrange_3d(const Tensor& x, std::size_t M, std::size
             return hs[0];
         }
     }
+    // The merge of the heads' rows (compute_layer.hpp:1256-1259, 1377-1386):
+    // recorded; the products taking it read the rows in place.
+    if (inverse && B > 1 && M > 0 && N % 16 == 0 && N > 0 && x.rows() == B * M && aligned16(x.dev_ptr()))
+    {
+        NN_CHECK(settle_ew_());
+        NN_TRY(out, alloc_(M, B * N));
+        NN_CHECK(push_layout_(PendingLayout{x, out, false, M, B, N, true}));
+        return out;
+    }
     NN_CHECK(settle_reads_({&x}));
     NN_TRY(out, alloc_(inverse ? M : B * M, inverse ? B * N : N));
     NN_CHECK(kernel_(nnhip_rearrange_3d(D(x), W(out), M, B, N, inverse ? 1u : 0u, stream_), "rearrange_3d"));
@@ -2140,8 +2167,16 @@ Result<Tensor> HipEngine::matmul(const Tensor& A, const Tensor& B, bool tA, bool
     // A recorded RMSNorm column as the vector of W x stays recorded: the
     // product normalises it itself when it runs (launch_pending_mm_).
     const bool rms_x = !tA && !tB && B.cols() == 1 && prms_ && !prms_->bwd && prms_->stage == 6 && same_t(prms_->y, B);
-    NN_CHECK(rms_x ? need_gpu_({&A}, "matmul") : need_gpu_({&A, &B}, "matmul"));
-    NN_CHECK(check_gpu_({&B}, "matmul"));
+    // A recorded merge of heads' rows as A (untransposed) or B stays recorded:
+    // the product reads the rows in place (settled here instead).
+    const PendingLayout* am = !tA ? merge_of_(A) : nullptr;
+    const PendingLayout* bm = merge_of_(B);
+    NN_CHECK(check_gpu_({&A, &B}, "matmul"));
+    {
+        // (copies: settling may change the recorded layouts)
+        const Tensor ra = am ? am->S : A, rb = bm ? bm->S : B;
+        NN_CHECK(settle_reads_({&ra, rms_x ? nullptr : &rb}));
+    }
     const std::size_t M = tA ? A.cols() : A.rows(), K = tA ? A.rows() : A.cols();
     const std::size_t K2 = tB ? B.cols() : B.rows(), N = tB ? B.rows() : B.cols();
     if (K != K2)
@@ -2236,6 +2271,7 @@ Result<void> HipEngine::launch_pending_mm_(std::unique_ptr<PendingMm> o)
             for (std::size_t i = 0; i < grp.size(); ++i)
             {
                 const PendingMm& q = *grp[i];
+                if (merge_of_(q.A)) NN_CHECK(settle_chain_reads_({&q.A}));
                 R[i] = D(q.A);
                 bias[i] = q.bias.size() ? D(q.bias) : nullptr;
                 y[i] = live(q.C) ? W(q.C) : nullptr;
@@ -2269,6 +2305,57 @@ Result<void> HipEngine::launch_pending_mm_(std::unique_ptr<PendingMm> o)
 // with added products, out = sum of A_i^T B_i in one launch.
 Result<void> HipEngine::launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate)
 {
+    if (merge_of_(r.A)) NN_CHECK(settle_chain_reads_({&r.A}));
+    // B as heads' rows read in place: the summed input gradient (every B a
+    // merge of one shape) and the plain product (the output projection).
+    if (const PendingLayout* bm = merge_of_(r.B); bm && !r.tB)
+    {
+        const PendingLayout l = *bm;
+        std::vector<Tensor> Ss{l.S};
+        bool all = true;
+        for (const auto& [pa, pb] : r.plus)
+        {
+            const PendingLayout* q = merge_of_(pb);
+            all = all && q && q->M == l.M && q->B == l.B && q->N == l.N;
+            if (all) Ss.push_back(q->S);
+        }
+        const bool sum = !r.plus.empty() && all && r.tA && !bias && !accumulate;
+        const bool plain = r.plus.empty() && !r.tA;
+        if (sum || plain)
+        {
+            for (const Tensor& t : Ss) NN_CHECK(settle_chain_reads_({&t}));
+            const std::size_t n = Ss.size(), Kt = n * r.K;
+            const std::size_t wsb = nnhip_gemm_workspace_bytes(r.M, r.N, Kt, 1);
+            std::shared_ptr<DeviceBuffer> ws;
+            if (wsb)
+            {
+                NN_TRY(w, scratch_(wsb));
+                ws = w;
+            }
+            int rc;
+            prof_begin_();
+            if (sum)
+            {
+                const float* As[3] = {D(r.A)};
+                const float* Bs[3] = {};
+                for (std::size_t i = 1; i < n; ++i) As[i] = D(r.plus[i - 1].first);
+                for (std::size_t i = 0; i < n; ++i) Bs[i] = D(Ss[i]);
+                rc = nnhip_gemm_tn_sum_seq(As, Bs, n, W(out), r.M, r.N, r.K, 1.0f, nnhip_by_seq{l.N, l.M * l.N},
+                                           ws ? ws->data() : nullptr, wsb, stream_);
+                prof_end_(r.M, r.N, Kt, 1, true, false);
+            }
+            else
+            {
+                rc = nnhip_gemm_epilogue_seq(D(r.A), D(Ss[0]), W(out), r.M, r.N, r.K, 1.0f, bias ? D(*bias) : nullptr,
+                                             accumulate ? 1 : 0, nnhip_by_seq{l.N, l.M * l.N}, ws ? ws->data() : nullptr, wsb,
+                                             stream_);
+                prof_end_(r.M, r.N, r.K, 1, false, false);
+            }
+            if (rc != -7) return kernel_(rc, "matmul");
+            // (not whole tiles: the merges are made and the product runs as usual)
+        }
+    }
+    for (const auto& [pa, pb] : r.plus) NN_CHECK(settle_chain_reads_({&pb}));
     NN_CHECK(settle_chain_reads_({&r.B}));   // (a recorded RMSNorm column, see matmul)
     if (!r.plus.empty())
     {
@@ -2330,30 +2417,83 @@ Result<void> HipEngine::settle_acc_()
     bool all_rs = r->rs_acc >= 0, one_b = true;
     for (std::size_t i = 0; i < n; ++i)
     {
-        As[i] = D(r->mem[i].first);
-        Bs[i] = D(r->mb[i]);
         Cs[i] = W(r->mem[i].second);
         Rs[i] = i < r->rs.size() && r->rs[i].size() ? W(r->rs[i]) : nullptr;
         all_rs = all_rs && Rs[i];
         one_b = one_b && same_t(r->mb[i], r->B);
     }
-    prof_begin_();
-    const int rc = one_b ? nnhip_gemm_group_acc(As, D(r->B), Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
-                                                all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0,
-                                                ws ? ws->data() : nullptr, wsb, stream_)
-                         : nnhip_gemm_group_acc_each(As, Bs, Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
-                                                     all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0,
-                                                     ws ? ws->data() : nullptr, wsb, stream_);
-    prof_end_(r->M, r->N, r->K, n, false, r->tB);
+    // Members' G (A) and input (transposed B) that are merges of heads' rows
+    // are read in place (the q, k, v gradients; the output projection's input).
+    nnhip_by_seq as[4] = {}, bs[4] = {};
+    bool by_seq = false;
+    if (r->tB)
+        for (std::size_t i = 0; i < n; ++i)
+        {
+            if (const PendingLayout* q = merge_of_(r->mem[i].first))
+            {
+                as[i] = nnhip_by_seq{q->N, q->M * q->N};   // rows of q->N per sequence
+                const Tensor S = q->S;
+                NN_CHECK(settle_chain_reads_({&S}));
+                by_seq = true;
+            }
+            if (const PendingLayout* q = merge_of_(r->mb[i]))
+            {
+                bs[i] = nnhip_by_seq{q->N, q->M * q->N};
+                const Tensor S = q->S;
+                NN_CHECK(settle_chain_reads_({&S}));
+                by_seq = true;
+            }
+        }
+    int rc = -7;
+    if (by_seq)
+    {
+        for (std::size_t i = 0; i < n; ++i)
+        {
+            const PendingLayout* qa = as[i].len ? merge_of_(r->mem[i].first) : nullptr;
+            const PendingLayout* qb = bs[i].len ? merge_of_(r->mb[i]) : nullptr;
+            if ((as[i].len && !qa) || (bs[i].len && !qb)) by_seq = false;   // (made meanwhile)
+            As[i] = qa ? D(qa->S) : D(r->mem[i].first);
+            Bs[i] = qb ? D(qb->S) : D(r->mb[i]);
+        }
+        if (by_seq)
+        {
+            prof_begin_();
+            rc = nnhip_gemm_group_acc_seq(As, Bs, Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
+                                          all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0, as, bs,
+                                          ws ? ws->data() : nullptr, wsb, stream_);
+            prof_end_(r->M, r->N, r->K, n, false, r->tB);
+        }
+    }
+    if (rc == -7)
+    {
+        // (no merges, or not whole tiles: the merges are made first)
+        for (std::size_t i = 0; i < n; ++i)
+        {
+            NN_CHECK(settle_chain_reads_({&r->mem[i].first, &r->mb[i]}));
+            As[i] = D(r->mem[i].first);
+            Bs[i] = D(r->mb[i]);
+        }
+        prof_begin_();
+        rc = one_b ? nnhip_gemm_group_acc(As, D(r->B), Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
+                                          all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0, ws ? ws->data() : nullptr,
+                                          wsb, stream_)
+                   : nnhip_gemm_group_acc_each(As, Bs, Cs, n, r->M, r->N, r->K, r->tB, r->acc ? 1 : 0,
+                                               all_rs ? Rs : nullptr, r->rs_acc > 0 ? 1 : 0,
+                                               ws ? ws->data() : nullptr, wsb, stream_);
+        prof_end_(r->M, r->N, r->K, n, false, r->tB);
+    }
     NN_CHECK(kernel_(rc, "matmul"));
     if (all_rs) return {};
-    // (row sums recorded for some members only: their own launches)
+    // (row sums recorded for some members only: their own launches, of G as a
+    // matrix, a merge of heads' rows made first)
     for (std::size_t i = 0; i < n; ++i)
         if (Rs[i])
         {
+            NN_CHECK(settle_chain_reads_({&r->mem[i].first}));
             const std::size_t R = r->mem[i].first.rows(), C = r->mem[i].first.cols();
-            NN_CHECK(kernel_(r->rs_acc > 0 ? nnhip_reduce_row_sum_add(As[i], Rs[i], R, C, stream_)
-                                           : nnhip_reduce_row(As[i], Rs[i], R, C, 0u, stream_),
+            const float* G = D(r->mem[i].first);
+            NN_CHECK(kernel_(r->rs_acc > 0 ? nnhip_reduce_row_sum_add(G, Rs[i], R, C, stream_)
+                                           : nnhip_reduce_row(G, Rs[i], R, C, 0u, stream_),
                              "row_reduce_sum"));
         }
     return {};
@@ -2725,6 +2865,11 @@ Result<Tensor> HipEngine::col_softmax_sparse_forward(const Tensor& logits, const
             NN_CHECK(settle_reads_({&labels, mask}));
             if (pmm_ && same_t(logits, pmm_->C))
             {
+                const Tensor a = pmm_->A, b = pmm_->B;   // (merges of heads' rows made)
+                NN_CHECK(settle_chain_reads_({&a, &b}));
+            }
+            if (pmm_ && same_t(logits, pmm_->C))
+            {
                 std::unique_ptr<PendingMm> r = std::move(pmm_);
                 const std::size_t C = logits.rows(), N = logits.cols();
                 NN_TRY(stats, scratch_(2 * tiles * N * sizeof(float)));
@@ -3001,7 +3146,14 @@ Result<void> HipEngine::launch_zero_(std::vector<PendingZero>& ts)
 // ── reductions (cpu_engine.hpp:1050-1086) ───────────────────────────────────
 Result<Tensor> HipEngine::row_reduce_sum(const Tensor& A)
 {
-    NN_CHECK(need_gpu_({&A}, "row_reduce_sum"));
+    if (const PendingLayout* am = merge_of_(A))
+    {
+        NN_CHECK(check_gpu_({&A}, "row_reduce_sum"));
+        const Tensor S = am->S;
+        NN_CHECK(settle_reads_({&S}));
+    }
+    else
+        NN_CHECK(need_gpu_({&A}, "row_reduce_sum"));
     NN_TRY(o, alloc_(A.rows(), 1));
     if (!A.rows()) return o;
     NN_CHECK(settle_rsum_());
@@ -3013,6 +3165,7 @@ Result<Tensor> HipEngine::row_reduce_sum(const Tensor& A)
 
 Result<void> HipEngine::launch_rsum_(const PendingRowSum& r, float* out, bool add)
 {
+    if (merge_of_(r.src)) NN_CHECK(settle_chain_reads_({&r.src}));
     const std::size_t R = r.src.rows(), C = r.src.cols();
     if (r.kind == 1)
         return kernel_(add ? nnhip_rmsnorm_bwd_rowsum_add(D(r.src), D(r.gamma), D(r.normed), out, R, C, stream_)

@@ -166,3 +166,93 @@ def test_partial_tiles_refused(hip):
     assert lib.nnhip_gemm_epilogue_seq(a.data_ptr(), bs.data_ptr(), c.data_ptr(), M, nb * T, K, 1.0, None, 0,
                                        BySeq(T, K * T), None, 0, st) == -7
     assert not c.numpy().any()
+
+
+# ── through the engine: rearrange_3d(., inverse) recorded, read in place ─────────
+def _fwd(e, W, bias, S, d, nb, T, how):
+    """AttentionBase::forward's end (compute_layer.hpp:1254-1267): concat = rearrange_3d(concat_out,
+    H d_k, B, T, true), then the output projection W concat + b. how: "fold" as issued; "read" concat
+    read before the product; "settle" a settle between the merge and the product (the merge stays
+    recorded); "write_s" concat_out scaled in place after the product was recorded."""
+    s = e.tensor(S)
+    concat = e.rearrange_3d(s, d, nb, T, True)
+    if how == "read":
+        concat.numpy()
+    if how == "settle":
+        e.settle()
+    y = e.matmul(e.tensor(W), concat)
+    e.broadcast_row_inplace(y, e.tensor(bias), "Add")
+    if how == "write_s":
+        e.scale_inplace(s, 2.0)
+    return [y.numpy(), concat.numpy()]
+
+
+@pytest.mark.parametrize("d,nb,T", [(768, 8, 1024), (128, 3, 256), (100, 2, 48)])
+def test_engine_output_projection_of_merge(hip, cpu, d, nb, T):
+    """(100, 2, 48): not whole tiles, the merge is made and the product runs as usual."""
+    rng = np.random.default_rng(d * nb + T)
+    W, bias = uniform(rng, (d, d)), uniform(rng, (d, 1))
+    S = uniform(rng, (nb * d, T))
+    fold = _fwd(hip, W, bias, S, d, nb, T, "fold")
+    for how in ("read", "settle", "write_s"):
+        print(f"[gemm_seq] engine fwd d {d} nb {nb} T {T} {how}", flush=True)
+        other = _fwd(hip, W, bias, S, d, nb, T, how)
+        for i in range(2):
+            assert np.array_equal(bits(fold[i]), bits(other[i])), (how, i)
+    ref = _fwd(cpu, W, bias, S, d, nb, T, "read")
+    for a, b in zip(fold, ref):
+        assert nrm_err(a, b) <= 1e-5
+
+
+def _bwd(e, Ws, Go, Xo_heads, X, dS, d, nb, T, how):
+    """AttentionBase::backward's Linear part (compute_layer.hpp:1377-1408 and Linear::backward):
+    the output projection's grad_w += G_o concat^T with concat a merge kept from the forward, then
+    gQ, gK, gV = merges of the attention's heads' rows, each Linear's dx = W^T g, grad_w += g X^T,
+    grad_b += row sums of g, the three dx summed. how: "fold" as issued; "read" every merge read
+    first."""
+    concat = e.rearrange_3d(e.tensor(Xo_heads), d, nb, T, True)
+    x = e.tensor(X)
+    gw = [e.tensor(np.zeros((d, d), np.float32)) for _ in range(4)]
+    gb = [e.tensor(np.zeros((d, 1), np.float32)) for _ in range(4)]
+    for t in gw + gb:
+        e.zero(t)
+    if how == "read":
+        concat.numpy()
+    go = e.tensor(Go)
+    e.add_inplace(gw[0], e.matmul(go, concat, False, True))
+    e.add_inplace(gb[0], e.row_reduce_sum(go))
+    gs = [e.rearrange_3d(e.tensor(h), d, nb, T, True) for h in dS]
+    if how == "read":
+        for g in gs:
+            g.numpy()
+    dx = None
+    for i, g in enumerate(gs):
+        p = e.matmul(e.tensor(Ws[i]), g, True, False)
+        if dx is None:
+            dx = p
+        else:
+            e.add_inplace(dx, p)
+        e.add_inplace(gw[i + 1], e.matmul(g, x, False, True))
+        e.add_inplace(gb[i + 1], e.row_reduce_sum(g))
+    return [dx.numpy()] + [t.numpy() for t in gw + gb]
+
+
+@pytest.mark.parametrize("d,nb,T", [(768, 8, 1024), (128, 4, 256)])
+def test_engine_attention_backward_linears_of_merges(hip, cpu, d, nb, T):
+    """The merges read in place by the summed input gradient (nnhip_gemm_tn_sum_seq) and the grouped
+    weight gradients with their row sums (nnhip_gemm_group_acc_seq): within the GEMM tolerance of the
+    calls on the made merges (the input-gradient sum differs from three products and two adds), the
+    weight gradients and row sums bit-identical (same grouped launch)."""
+    rng = np.random.default_rng(d + nb * T)
+    K = nb * T
+    Ws = [uniform(rng, (d, d)) for _ in range(3)]
+    Go, X = uniform(rng, (d, K)), uniform(rng, (d, K))
+    Xo_heads = uniform(rng, (nb * d, T))
+    dS = [uniform(rng, (nb * d, T)) for _ in range(3)]
+    fold = _bwd(hip, Ws, Go, Xo_heads, X, dS, d, nb, T, "fold")
+    sep = _bwd(hip, Ws, Go, Xo_heads, X, dS, d, nb, T, "read")
+    ref = _bwd(cpu, Ws, Go, Xo_heads, X, dS, d, nb, T, "read")
+    for i, (a, b, r) in enumerate(zip(fold, sep, ref)):
+        if i > 0:
+            assert np.array_equal(bits(a), bits(b)), i
+        assert nrm_err(a, r) <= 1e-5, i
