@@ -220,13 +220,6 @@ int nnhip_adam_update_list(float* const* p, float* const* m, float* const* v, co
  * No CUDA counterpart; HipEngine issues it when it recognises that chain among deferred calls. */
 int nnhip_swiglu_forward(const float* gate, const float* up, float* s_out, float* out, size_t count, float c_add,
                          float c_div, void* stream);
-/* The SwiGLU feed-forward's first Linear and its SwiGLU forward in one launch (FeedForward::forward: fc1,
- * then SwiGLU::forward on its gate rows [0, F) and up rows [F, 2F)): H (2F, N) = W (2F, K) X (K, N)
- * (+ row_bias), S (F, N) = c_div / (exp(-gate) + c_add) (when S is not null), out (F, N) = (gate * S) * up,
- * all bit-identical to nnhip_gemm_epilogue followed by nnhip_swiglu_forward. Returns -7 when the shapes do
- * not give the product's whole tiles (then run the two calls). No CUDA counterpart. */
-int nnhip_gemm_swiglu(const float* W, const float* X, const float* row_bias, float* H, float* S, float* out, size_t F,
-                      size_t N, size_t K, float c_add, float c_div, void* stream);
 /* dst[i] = src[i] for count floats (non-overlapping): slice_rows / insert_rows / clone (cpu_engine.hpp:75-114;
  * the CUDA engine uses cudaMemcpy). */
 int nnhip_copy(const float* src, float* dst, size_t count, void* stream);

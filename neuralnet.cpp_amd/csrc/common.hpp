@@ -113,15 +113,6 @@ inline int device_cus()
     return cus[dev];
 }
 
-// SwiGLU::forward's chain for one element (t = -gate, t = exp(t), t = t + c_add,
-// s = c_div / t, out = (gate * s) * up), shared by the element-wise pass and
-// the GEMM epilogue that runs the chain, so both round alike.
-__device__ __forceinline__ void swiglu_fwd_one(float g, float u, float c_add, float c_div, float& sv, float& o)
-{
-    sv = c_div / (expf(-g) + c_add);
-    o = (g * sv) * u;
-}
-
 inline int launch_status()
 {
     const hipError_t e = hipGetLastError();

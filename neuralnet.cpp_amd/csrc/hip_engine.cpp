@@ -1047,7 +1047,6 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb, bool
     NN_CHECK(unshare_(t));
     const float* p = t.dev_ptr();
     if (!p) return {};
-    if (up_last_.size() && t.device_buffer() == up_last_.device_buffer()) up_last_ = Tensor();   // (written)
     if (!keep_zero) NN_CHECK(settle_zero_for_(t));
     if (pacc_ && pacc_->uses(p)) NN_CHECK(settle_acc_());
     if (flash_uses_(p)) NN_CHECK(settle_flash_());
@@ -1778,25 +1777,10 @@ Result<bool> HipEngine::upload_(float* dst, const float* src, std::size_t n)
 
 Result<Tensor> HipEngine::from_matrix(const Matrix& m)
 {
-    // The same small matrix as the last upload (the ALiBi row every layer's
-    // attention uploads for one position, compute_layer.hpp:2267-2290): a view
-    // of that upload, copied only if either is written.
-    const std::size_t n = m.size();
-    if (n && n * sizeof(float) <= kStageSlot && up_last_.size() == n && up_last_.rows() == m.rows() &&
-        std::memcmp(up_host_.data(), m.data(), n * sizeof(float)) == 0)
-    {
-        const Tensor root = up_last_;
-        return slice_rows(root, 0, m.rows());
-    }
     NN_TRY(t, alloc_(m.rows(), m.cols()));
     if (m.size())
     {
         NN_TRY(queued, upload_(W(t), m.data(), m.size()));
-        if (queued && n * sizeof(float) <= kStageSlot)
-        {
-            up_last_ = t;
-            up_host_.assign(m.data(), m.data() + n);
-        }
         if (queued) return t;
         auto s = static_cast<hipStream_t>(stream_);
         if (hipMemcpyAsync(W(t), m.data(), m.size() * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess)

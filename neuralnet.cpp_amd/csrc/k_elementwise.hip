@@ -234,7 +234,10 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_fwd(const float* gate, cons
 {
     const size_t tid = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
     const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
-    auto one = [&](float g, float u, float& sv, float& o) { swiglu_fwd_one(g, u, c_add, c_div, sv, o); };
+    auto one = [&](float g, float u, float& sv, float& o) {
+        sv = c_div / (expf(-g) + c_add);
+        o = (g * sv) * u;
+    };
     size_t done = 0;
     if constexpr (VEC)
     {

@@ -91,20 +91,6 @@ struct RowSums
     int acc;
 };
 
-// GLU: the product is the SwiGLU layer's input h (2F rows: gate rows [0, F),
-// up rows [F, 2F); SwiGLU::forward's chain s = c_div / (exp(-gate) + c_add),
-// out = (gate * s) * up follows it). Each wave's two 32-row blocks take gate
-// row r and up row F + r (tile t holds gate rows t BM/2 .. (t + 1) BM/2), so
-// the epilogue writes h and also s and out (F rows each) from registers,
-// rounded as the separate chain. FM == 2, no split K.
-struct GluOut
-{
-    float* s;      // or nullptr when s is not kept
-    float* out;
-    int F;
-    float c_add, c_div;
-};
-
 // WM x WN waves; each wave owns (32*FM) x (32*FN) of C as FM x FN MFMA 32x32 blocks.
 // STATS: besides C, each workgroup writes the column softmax statistics of its
 // BM rows of C (as stored, bias included): part[tile_m * N + n] = max over the
@@ -112,17 +98,16 @@ struct GluOut
 // sparse cross-entropy that follows the product (the GPT's lm_head logits)
 // merges these instead of reading C once more for them. Needs splits == 1.
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB, bool GUARD, bool STATS = false, bool GRP = false,
-          bool KSEG = false, bool RSUM = false, bool SEG = false, bool GLU = false>
+          bool KSEG = false, bool RSUM = false, bool SEG = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K, long lda, long ldb,
                                                        long strideA, long strideB, long strideC, float alpha,
                                                        int tiles_m, int tiles_n, int k_split, float* __restrict__ part,
                                                        const float* __restrict__ bias, int accum, GemmGroup grp,
-                                                       RowSums rs = {}, GluOut glu = {})
+                                                       RowSums rs = {})
 {
     static_assert(!RSUM || (GRP && !TA), "row sums of an untransposed A in grouped launches");
     static_assert(!SEG || (!GUARD && !STATS), "operands by sequence in whole tiles only");
-    static_assert(!GLU || (!TA && !GUARD && !STATS && !GRP && !KSEG && !SEG && FM == 2), "GLU tiles");
     constexpr int NT = 64 * WM * WN;
     constexpr int BM = 32 * FM * WM, BN = 32 * FN * WN;
     constexpr int LA = BM * BK / 4 / NT;   // float4 per thread per stage for A
@@ -148,10 +133,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
     tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
     const long bz = blockIdx.z;
-    // GLU: local row m = 64 w + 32 i + r holds gate row t BM/2 + 32 w + r (i = 0) or F more (i = 1)
-    auto glu_row = [&](int m) {
-        return (((m >> 5) & 1) ? glu.F : 0) + tmi * (BM / 2) + (m >> 6) * 32 + (m & 31);
-    };
     if constexpr (GRP)
     {
         const int gi = static_cast<int>(bz / grp.nb);
@@ -214,7 +195,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             int m, k;
             if constexpr (TA) { k = idx / (BM / 4); m = (idx % (BM / 4)) * 4; }
             else { m = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
-            const int gm = GLU ? glu_row(m) : m0 + m, gk = kb + k, dk = k0 - kb;   // gk + dk: k over the whole sum
+            const int gm = m0 + m, gk = kb + k, dk = k0 - kb;   // gk + dk: k over the whole sum
             if constexpr (!GUARD)
             {
                 ra[s] = TA ? *reinterpret_cast<const f4*>(Ap + (long)gk * lda + gm)
@@ -444,38 +425,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             part[(long)tmi * N + gn] = m;
             part[(long)(tiles_m + tmi) * N + gn] = t;
         }
-    }
-    if constexpr (GLU)
-    {
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-        {
-            const int gn = n0 + wn * 32 * FN + j * 32 + col_l;
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-            {
-                const int lr = 8 * (r / 4) + row_l + (r % 4);
-                const int gr = tmi * (BM / 2) + wm * 32 + lr;   // gate row; up row F + gr
-                float g, u;
-                {
-#pragma clang fp contract(off)
-                    g = alpha * acc[0][j][r];
-                    u = alpha * acc[1][j][r];
-                    if (bias)
-                    {
-                        g = g + bias[gr];
-                        u = u + bias[glu.F + gr];
-                    }
-                }
-                C[(long)gr * N + gn] = g;
-                C[(long)(glu.F + gr) * N + gn] = u;
-                float sv, o;
-                swiglu_fwd_one(g, u, glu.c_add, glu.c_div, sv, o);
-                if (glu.s) glu.s[(long)gr * N + gn] = sv;
-                glu.out[(long)gr * N + gn] = o;
-            }
-        }
-        return;
     }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -805,7 +754,6 @@ struct Epi
     const RowSums* rs = nullptr;        // grouped launches: the row sums of each member's A as well
     const GemmGroup* sq = nullptr;      // plain launches: member 0 gives the operands' sequence layouts
     bool by_seq = false;                // the group passed (grp, seg or sq) holds sequence layouts
-    const GluOut* glu = nullptr;        // the SwiGLU chain in the epilogue (NN, whole tiles, no split)
 };
 
 template <int WM, int WN, int FM, int FN, int BK, bool TA, bool TB>
@@ -818,15 +766,6 @@ void launch_cfg(const float* A, const float* B, float* C, int M, int N, int K, l
     const bool guard = !vec_ok || (M % BM) || (N % BN) || (K % BK) || (k_split % BK);
     const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits), static_cast<unsigned>(batch));
     const dim3 block(64 * WM * WN);
-    if (e.glu)
-    {
-        if constexpr (!TA && !TB && FM == 2)
-            if (!guard && splits == 1)
-                hipLaunchKernelGGL((k_gemm<WM, WN, FM, FN, BK, TA, TB, false, false, false, false, false, false, true>),
-                                   grid, block, 0, s, A, B, C, M, N, K, lda, ldb, sA, sB, sC, alpha, tm, tn, k_split,
-                                   part, e.bias, e.accum, GemmGroup{}, RowSums{}, *e.glu);
-        return;
-    }
     if (e.by_seq)
     {
         if constexpr (TA && !TB)
@@ -1204,13 +1143,12 @@ int gemm_dispatch(const float* A, const float* B, float* C, size_t M, size_t N, 
     if (e.by_seq && !(tA && !tB ? e.seg != nullptr : !tA && tB ? e.grp != nullptr : !tA && !tB && e.sq != nullptr))
         return -1;
     auto s = static_cast<hipStream_t>(stream);
-    if (int rc = 0; !e.grp && !e.seg && !e.by_seq && !e.glu &&
+    if (int rc = 0; !e.grp && !e.seg && !e.by_seq &&
                     try_gemv(A, B, C, M, N, K, lda, ldb, sA, sB, sC, tA, tB, alpha, batch, s, e, rc))
         return rc;
     Plan p = plan_gemm(M, N, K, batch, workspace != nullptr);
     if (p.splits > 1 && static_cast<size_t>(p.splits) * batch * (M * N + (e.rs ? M : 0)) * sizeof(float) > ws_bytes)
         p = plan_gemm(M, N, K, batch, false);
-    if (e.glu && (p.splits != 1 || !(p.cfg == kTall || p.cfg == kSquare) || tA || tB || batch != 1)) return -7;
     if (e.by_seq)
     {
         // whole tiles, 16-byte loads, and no tile or stage across two sequences
@@ -1468,22 +1406,6 @@ extern "C" int nnhip_gemm_tn_sum_seq(const float* const* A, const float* const* 
     e.by_seq = true;
     return gemm_dispatch(A[0], B[0], C, M, N, count * K_each, M, b_seq.len, 0, 0, M * N, true, false, alpha, 1,
                          workspace, workspace_bytes, stream, e);
-}
-
-extern "C" int nnhip_gemm_swiglu(const float* W, const float* X, const float* row_bias, float* H, float* S,
-                                 float* out, size_t F, size_t N, size_t K, float c_add, float c_div, void* stream)
-{
-    // H (2F, N) = W (2F, K) X (K, N) (+ bias), then SwiGLU's chain on its halves, from the registers
-    if (!W || !X || !H || !out || F == 0 || N == 0 || K == 0 || F > 0x3fffffff) return -1;
-    const size_t M = 2 * F;
-    const Plan p = plan_gemm(M, N, K, 1, false);
-    const bool whole = (p.cfg == kTall || p.cfg == kSquare) && F % (p.bm / 2) == 0 && N % p.bn == 0 && K % 16 == 0 &&
-                       K % 4 == 0 && N % 4 == 0 && aligned16(W) && aligned16(X);
-    if (!whole) return -7;
-    GluOut g{S, out, static_cast<int>(F), c_add, c_div};
-    Epi e{row_bias, 0};
-    e.glu = &g;
-    return gemm_dispatch(W, X, H, M, N, K, K, N, M * K, K * N, M * N, false, false, 1.0f, 1, nullptr, 0, stream, e);
 }
 
 extern "C" int nnhip_gemm_epilogue_seq(const float* A, const float* B, float* C, size_t M, size_t N, size_t K,

@@ -370,11 +370,6 @@ private:
     void* stage_ = nullptr;
     std::vector<void*> stage_ev_;
     std::size_t stage_next_ = 0;
-    // The last small from_matrix upload and its host values: an equal upload
-    // returns a copy-on-write view of it (each layer's ALiBi row at one
-    // position in incremental inference); dropped when it is written.
-    Tensor up_last_;
-    std::vector<float> up_host_;
 
     bool ok_ = false;
     std::string init_error_;

@@ -9,12 +9,8 @@ calls launched one by one (an engine settle between them), the products within
 the GEMM bound of the float64 product, and the recorded product itself correct
 when read afterwards.
 """
-import ctypes
-
 import numpy as np
 import pytest
-
-import nnengine
 
 from helpers import nrm_err, uniform
 
@@ -214,49 +210,3 @@ def test_output_projection_backward_into_heads(hip, cpu, D, B, T):
     ref = _out_proj_bwd_heads(cpu, W, G, B, T, "read")
     for a, b in zip(fold, ref):
         assert nrm_err(a, b) <= 1e-5
-
-
-@pytest.mark.parametrize("F,N,K,keep_s", [(3072, 8192, 768, True), (768, 16384, 64, True), (384, 32768, 32, False),
-                                          (100, 64, 32, True), (128, 512, 64, True)])
-def test_gemm_swiglu_entry_point(hip, F, N, K, keep_s):
-    """nnhip_gemm_swiglu: fc1 (2F rows, bias) and SwiGLU::forward's chain on its halves in one launch,
-    every output bit-identical to nnhip_gemm_epilogue then nnhip_swiglu_forward; (100, 64, 32) does not
-    give whole tiles and (128, 512, 64) plans 128 x 64 tiles (one block per wave): -7, nothing written."""
-    P, SZ = ctypes.c_void_p, ctypes.c_size_t
-    lib = nnengine.hip_library()
-    lib.nnhip_engine_stream.restype = P
-    lib.nnhip_engine_stream.argtypes = [P]
-    lib.nnhip_gemm_swiglu.argtypes = [P, P, P, P, P, P, SZ, SZ, SZ, ctypes.c_float, ctypes.c_float, P]
-    lib.nnhip_gemm_epilogue.argtypes = [P, P, P, SZ, SZ, SZ, SZ, ctypes.c_int, ctypes.c_int, ctypes.c_float, P,
-                                        ctypes.c_int, P, SZ, P]
-    lib.nnhip_swiglu_forward.argtypes = [P, P, P, P, SZ, ctypes.c_float, ctypes.c_float, P]
-    rng = np.random.default_rng(F + N + K)
-    W, X, b = uniform(rng, (2 * F, K)), uniform(rng, (K, N)), uniform(rng, (2 * F, 1))
-    w, x, bb = hip.tensor(W), hip.tensor(X), hip.tensor(b)
-    h1, s1, o1 = hip.create_tensor(2 * F, N), hip.create_tensor(F, N), hip.create_tensor(F, N)
-    h2, s2, o2 = (hip.tensor(np.zeros(shape, np.float32)) for shape in ((2 * F, N), (F, N), (F, N)))
-    hip.sync()
-    st = lib.nnhip_engine_stream(hip._e)
-    print(f"[gemm_swiglu] F {F} N {N} K {K} keep_s {keep_s}", flush=True)
-    rc = lib.nnhip_gemm_swiglu(w.data_ptr(), x.data_ptr(), bb.data_ptr(), h2.data_ptr(),
-                               s2.data_ptr() if keep_s else None, o2.data_ptr(), F, N, K, 1.0, 1.0, st)
-    if F in (100, 128):
-        assert rc == -7
-        assert not h2.numpy().any() and not o2.numpy().any()
-        return
-    assert rc == 0
-    assert lib.nnhip_gemm_epilogue(w.data_ptr(), x.data_ptr(), h1.data_ptr(), 2 * F, K, K, N, 0, 0, 1.0,
-                                   bb.data_ptr(), 0, None, 0, st) == 0
-    gate, up = h1.data_ptr(), h1.data_ptr() + F * N * 4
-    assert lib.nnhip_swiglu_forward(gate, up, s1.data_ptr(), o1.data_ptr(), F * N, 1.0, 1.0, st) == 0
-    H1, H2 = h1.numpy(), h2.numpy()
-    assert np.array_equal(H1.view(np.uint32), H2.view(np.uint32))
-    assert np.array_equal(o1.numpy().view(np.uint32), o2.numpy().view(np.uint32))
-    if keep_s:
-        assert np.array_equal(s1.numpy().view(np.uint32), s2.numpy().view(np.uint32))
-    else:
-        assert not s2.numpy().any()
-    h64 = W.astype(np.float64) @ X.astype(np.float64) + b.astype(np.float64)
-    g64, u64 = h64[:F], h64[F:]
-    assert nrm_err(H2, h64) <= 1e-5
-    assert nrm_err(o2.numpy(), g64 / (1 + np.exp(-g64)) * u64) <= 1e-5

@@ -5,8 +5,7 @@ of a pinned staging ring and return once the upload is queued (no wait for the
 stream); larger data is uploaded and waited for. Checked: more uploads than the
 ring has slots, each read back after all of them, against the host data bit for
 bit; copy_from into a tensor that queued work still reads; the large path; and
-transposes of row and column vectors (plain copies of the same floats); an upload equal to
-the previous one shared copy-on-write.
+transposes of row and column vectors (plain copies of the same floats).
 """
 import numpy as np
 import pytest
@@ -50,25 +49,3 @@ def test_vector_transpose(hip, shape):
     rng = np.random.default_rng(4)
     X = normal(rng, shape)
     assert np.array_equal(hip.transpose(hip.tensor(X)).numpy().view(np.uint32), X.T.copy().view(np.uint32))
-
-
-def test_repeated_upload_shares_until_written(hip):
-    """An upload equal to the previous one (each layer's ALiBi row at one position) is a copy-on-write
-    view of it: both read the host values; writing either leaves the other as uploaded; a third equal
-    upload after the first was written is a new upload; a different matrix in between ends the
-    sharing."""
-    rng = np.random.default_rng(3)
-    H = normal(rng, (12, 73))
-    a, b = hip.tensor(H), hip.tensor(H)
-    assert np.array_equal(a.numpy(), H) and np.array_equal(b.numpy(), H)
-    hip.scale_inplace(b, 2.0)                      # the view gets its own copy
-    assert np.array_equal(a.numpy(), H) and np.array_equal(b.numpy(), H * np.float32(2.0))
-    c = hip.tensor(H)                              # still a view of a
-    hip.scale_inplace(a, 3.0)                      # the original written: c keeps the upload
-    assert np.array_equal(c.numpy(), H) and np.array_equal(a.numpy(), H * np.float32(3.0))
-    d = hip.tensor(H)                              # a new upload (a was written)
-    hip.add_inplace(d, d)
-    e = hip.tensor(normal(rng, (12, 73)))
-    f = hip.tensor(H)
-    assert np.array_equal(d.numpy(), H + H) and np.array_equal(f.numpy(), H) and np.array_equal(c.numpy(), H)
-    assert not np.array_equal(e.numpy(), H)
