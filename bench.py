@@ -76,6 +76,42 @@ def _gain_indices(cfg):
     return idx + [base + 14 * cfg["num_layers"]]
 
 
+# The config-4 step's main product shapes as C (M, N) = op(A) op(B) over K, with the engine's transposes.
+LIBRARY_SHAPES = [(6144, 8192, 768, False, False), (768, 8192, 3072, False, False), (768, 8192, 6144, True, False),
+                  (3072, 8192, 768, True, False), (6144, 768, 8192, False, True), (768, 3072, 8192, False, True),
+                  (768, 768, 8192, False, True), (768, 8192, 768, False, False), (32000, 8192, 768, False, False),
+                  (768, 8192, 32000, True, False), (4096, 4096, 4096, False, False)]
+
+
+def library_gemm_leg(reps=30):
+    """torch.mm in fp32 (TF32 off: ROCm's vendor GEMM) on the step's shapes, 10 untimed then `reps` timed
+    calls between torch.cuda events: a reference point for the engine's own kernels (roofline.by_shape)."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    out = []
+    for M, N, K, ta, tb in LIBRARY_SHAPES:
+        A = torch.randn((K, M) if ta else (M, K), device=dev, generator=gen)
+        B = torch.randn((N, K) if tb else (K, N), device=dev, generator=gen)
+        a, b = (A.t() if ta else A), (B.t() if tb else B)
+        C = torch.empty((M, N), device=dev)
+        for _ in range(10):
+            torch.mm(a, b, out=C)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            torch.mm(a, b, out=C)
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / reps
+        out.append(dict(M=M, N=N, K=K, transA=int(ta), transB=int(tb), ms=ms, tflops=2 * M * N * K / ms / 1e9,
+                        frac_of_fp32_mfma_peak=2 * M * N * K / ms / 1e9 / PEAK_FP32_MFMA_TFLOPS))
+        del A, B, C
+    return out
+
+
 def inference_leg(g, seed, tokens=64, warmup=8):
     """Incremental inference on the trained config-4 model (GPTModel::forward_step with KV caches,
     reference compute_layer.hpp:2906-2960): one token per call at positions 0..tokens-1, logits
@@ -670,6 +706,9 @@ def main():
                     help="run only the attention leg (configs 2 and 5) and print its JSON (for kernel traces)")
     ap.add_argument("--inference-only", action="store_true",
                     help="run only the incremental-inference leg (config-4 model, batch 1) and print its JSON")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="time the vendor fp32 GEMM (torch.mm, TF32 off) on the config-4 step's product shapes and "
+                         "print its JSON (a comparison, not part of the engine)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
@@ -681,6 +720,9 @@ def main():
         return
     if args.attention_only:
         print(json.dumps({"attention": attention_leg(args.seed)}), flush=True)
+        return
+    if args.library_gemm:
+        print(json.dumps({"library_gemm": library_gemm_leg()}), flush=True)
         return
     if args.inference_only:
         import nnengine
