@@ -962,31 +962,60 @@ struct GemvGroup
 // the same order, so the same bits): y = x / sqrt(sum(x^2) inv_f + eps) *
 // gamma, into LDS for the products; workgroup (0, 0) also stores the
 // RMSNorm outputs that are asked for.
+//
+// A launch is a few memory latencies long, so every load that does not depend
+// on another is issued before the first wait: the epilogue's bias and
+// residual, and with RMS (VEC, K <= 1024: one float4 trip per lane, U = 4)
+// x and gamma first, then the row. Waits on the vector-memory counter are in
+// issue order, so the prologue waits for x and gamma only while the row's
+// loads stay in flight.
 template <bool VEC, int U, bool RMS>
 __global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __restrict__ x, int rows, int K,
                                                     nnhip_gemv_rmsnorm rn)
 {
     const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    const float* xv = x;
+    const int i = blockIdx.x * 4 + static_cast<int>(wave);
+    const int m = blockIdx.y;
+    const bool live = i < rows;
+    const float* bias = g.bias[m];
+    const float* add = g.add[m];
+    float bv = 0.0f, av = 0.0f;
+    if (live && lane == 0)
+    {
+        if (bias) bv = bias[i];
+        if (add) av = add[i];
+    }
+    float acc;
     if constexpr (RMS)
     {
+        static_assert(!VEC || U == 4, "the RMS prologue's row covers K <= 1024 in one trip");
         __shared__ __align__(16) float xs[1024];
         __shared__ float part[4];
         const unsigned t = threadIdx.x;
-        float v[4];
+        float v[4], gm[4];
 #pragma unroll
         for (unsigned k = 0; k < 4; ++k)
         {
             const unsigned r = t + k * 256;
             v[k] = r < static_cast<unsigned>(K) ? x[r] : 0.0f;
+            gm[k] = r < static_cast<unsigned>(K) ? rn.gamma[r] : 0.0f;
         }
-        float acc = 0.0f;
+        const int K4 = K / 4;
+        const float4* r4 = reinterpret_cast<const float4*>(g.R[m] + (long)i * K);
+        float4 a[4];
+        if constexpr (VEC)
+        {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (live && static_cast<int>(lane) + 64 * u < K4) a[u] = r4[lane + 64 * u];
+        }
+        float ss = 0.0f;
 #pragma unroll
         for (unsigned k = 0; k < 4; ++k)
-            if (t + k * 256 < static_cast<unsigned>(K)) acc = __builtin_fmaf(v[k], v[k], acc);
+            if (t + k * 256 < static_cast<unsigned>(K)) ss = __builtin_fmaf(v[k], v[k], ss);
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
-        if (lane == 0) part[wave] = acc;
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) part[wave] = ss;
         __syncthreads();
         float sum = part[0];
 #pragma unroll
@@ -1012,7 +1041,7 @@ __global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __
             if (r < static_cast<unsigned>(K))
             {
 #pragma clang fp contract(off)
-                const float n = v[k] * ri, y = n * rn.gamma[r];
+                const float n = v[k] * ri, y = n * gm[k];
                 xs[r] = y;
                 if (first)
                 {
@@ -1022,17 +1051,39 @@ __global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __
             }
         }
         __syncthreads();
-        xv = xs;
+        if (!live) return;
+        if constexpr (VEC)
+        {
+            // gemv_row's sums for one trip: float4 lane + 64 u in the order of u, then the wave's sum.
+            const float4* x4 = reinterpret_cast<const float4*>(xs);
+            float d = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (static_cast<int>(lane) + 64 * u < K4)
+                {
+                    const float4 xv4 = x4[lane + 64 * u];
+                    d = __builtin_fmaf(a[u].x, xv4.x, d);
+                    d = __builtin_fmaf(a[u].y, xv4.y, d);
+                    d = __builtin_fmaf(a[u].z, xv4.z, d);
+                    d = __builtin_fmaf(a[u].w, xv4.w, d);
+                }
+            acc = wave_sum(d);
+        }
+        else
+            acc = gemv_row<VEC, U>(g.R[m] + (long)i * K, xs, K, lane);
     }
-    const int i = blockIdx.x * 4 + static_cast<int>(wave);
-    if (i >= rows) return;
-    const int m = blockIdx.y;
-    const float acc = gemv_row<VEC, U>(g.R[m] + (long)i * K, xv, K, lane);
+    else
+    {
+        if (!live) return;
+        acc = gemv_row<VEC, U>(g.R[m] + (long)i * K, x, K, lane);
+    }
     if (lane == 0)
     {
-        const float v = gemv_epilogue(acc, 1.0f, g.bias[m], i, nullptr, 0);
+#pragma clang fp contract(off)
+        float v = 1.0f * acc;
+        if (bias) v = v + bv;
         if (g.y[m]) g.y[m][i] = v;
-        if (g.out[m]) g.out[m][i] = g.add[m] ? g.add[m][i] + v : v;
+        if (g.out[m]) g.out[m][i] = add ? av + v : v;
     }
 }
 
