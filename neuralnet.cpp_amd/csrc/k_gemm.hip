@@ -426,6 +426,18 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
             part[(long)(tiles_m + tmi) * N + gn] = t;
         }
     }
+    // Global loads and stores share one in-order counter, so a bias load
+    // issued after a store would wait for the store as well: the tile's BM
+    // bias values are staged in LDS (free after the last stage's barrier) and
+    // read from there.
+    const float* bsh = nullptr;
+    if (!plain && bias)
+    {
+        float* bl = &As[0][0][0];
+        for (int m = tid; m < BM; m += NT) bl[m] = (!GUARD || m0 + m < M) ? bias[m0 + m] : 0.0f;
+        __syncthreads();
+        bsh = bl;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -435,7 +447,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
 #pragma unroll
             for (int r = 0; r < 16; ++r)
             {
-                const int gm = m0 + wm * 32 * FM + i * 32 + 8 * (r / 4) + row_l + (r % 4);
+                const int ml = wm * 32 * FM + i * 32 + 8 * (r / 4) + row_l + (r % 4), gm = m0 + ml;
                 if (GUARD && !(gm < M && gn < N)) continue;
                 float* c = C + (long)gm * N + gn;
                 if (plain)
@@ -446,7 +458,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(const float* __restrict__
                 {
 #pragma clang fp contract(off)
                     float v = alpha * acc[i][j][r];
-                    if (bias) v = v + bias[gm];
+                    if (bias) v = v + bsh[ml];
                     if (accum) v = *c + v;
                     *c = v;
                 }
