@@ -713,6 +713,16 @@ protected:
     return s;
 }
 
+// The ALiBi bias of one incremental-inference position (H, new_len), uploaded
+// once and read by every attention layer of a model that shares the cache:
+// the layers' slopes are equal (they depend on the head count only), so at one
+// position their biases are equal too and one upload serves them all.
+struct StepBiasCache
+{
+    std::size_t heads = 0, len = 0;
+    Tensor bias;
+};
+
 // ── CausalSelfAttention (reference compute_layer.hpp:2156-2304) ───────────
 // Pure causal -> two-pass path with a shared (seq,seq) mask; ALiBi or
 // document ids -> materialised path with a (BH*seq, seq) mask added to S.
@@ -754,13 +764,24 @@ protected:
     {
         if (!use_alibi_) return std::move(scores);
         const std::size_t new_len = cur_len + 1;
-        Matrix bias(num_heads_, new_len);
-        for (std::size_t h = 0; h < num_heads_; ++h)
-            for (std::size_t j = 0; j < new_len; ++j)
-                bias.set_value_unchecked(h, j, -slopes_[h] * static_cast<Scalar>(cur_len - j));
-        NN_TRY(bt, engine.from_matrix(bias));
-        return engine.elementwise_binary(BinaryOp::Add, scores, bt);
+        StepBiasCache& c = *step_bias_;
+        if (c.heads != num_heads_ || c.len != new_len || c.bias.size() != num_heads_ * new_len)
+        {
+            Matrix bias(num_heads_, new_len);
+            for (std::size_t h = 0; h < num_heads_; ++h)
+                for (std::size_t j = 0; j < new_len; ++j)
+                    bias.set_value_unchecked(h, j, -slopes_[h] * static_cast<Scalar>(cur_len - j));
+            NN_TRY(bt, engine.from_matrix(bias));
+            c = StepBiasCache{num_heads_, new_len, bt};
+        }
+        return engine.elementwise_binary(BinaryOp::Add, scores, c.bias);
     }
+
+public:
+    // Layers of one model (same engine, same head count) share one cache.
+    void share_step_bias(std::shared_ptr<StepBiasCache> c) { step_bias_ = std::move(c); }
+
+protected:
 
     Result<TwoPassMask> two_pass_mask_(ComputeEngine& engine, std::size_t, std::size_t seq) override
     {
@@ -782,6 +803,7 @@ protected:
 private:
     bool use_alibi_;
     std::vector<Scalar> slopes_;
+    std::shared_ptr<StepBiasCache> step_bias_ = std::make_shared<StepBiasCache>();
     std::vector<std::size_t> doc_ids_;
     Tensor mask_;
     std::size_t mask_batch_ = 0, mask_seq_ = 0;
@@ -910,6 +932,8 @@ public:
         NN_TRY(f, ff_.forward(engine, n2));
         return engine.elementwise_binary(BinaryOp::Add, r2, f);
     }
+
+    void share_step_bias(std::shared_ptr<StepBiasCache> c) { attn_.share_step_bias(std::move(c)); }
 
 private:
     CausalSelfAttention attn_;
@@ -1052,9 +1076,13 @@ public:
         else
             pos_ = std::make_unique<NoPositionEncoder>();
         blocks_.reserve(layers);
+        auto step_bias = std::make_shared<StepBiasCache>();
         for (std::size_t i = 0; i < layers; ++i)
+        {
             blocks_.push_back(
                 std::make_unique<GPTBlock>(engine, d_model, heads, d_ff, seq_len, pos_enc, activation, norm_type));
+            blocks_.back()->share_step_bias(step_bias);
+        }
     }
 
     std::vector<TensorRef> parameters() override
