@@ -88,8 +88,9 @@ int nnhip_tensor_to_host(nnhip_engine* e, const nnhip_tensor* t, float* out);   
 int nnhip_tensor_copy_from_host(nnhip_engine* e, nnhip_tensor* t, const float* data);
 size_t nnhip_tensor_rows(const nnhip_tensor* t);
 size_t nnhip_tensor_cols(const nnhip_tensor* t);
-/* Device pointer (host pointer for the CPU oracle). Results of the deferred attention calls hold their
- * values only after nnhip_engine_settle (or any engine call that reads them) on the HIP engine. */
+/* Device pointer (host pointer for the CPU oracle), as it is: results of deferred calls may not be queued
+ * yet, and the materialised attention's probability tensor holds score blocks until it is read through the
+ * engine. A raw reader takes nnhip_tensor_device_ptr below instead. */
 void* nnhip_tensor_data_ptr(const nnhip_tensor* t);
 void nnhip_tensor_release(nnhip_tensor* t);
 
@@ -208,6 +209,13 @@ void* nnhip_engine_stream(nnhip_engine* e);
  * none, and every backward forms its scores again. The blocks only save work: results are the same
  * either way, and an allocation that fails leaves them out. No reference counterpart. */
 int nnhip_engine_set_score_budget(nnhip_engine* e, size_t bytes);
+/* The device pointer of t for a raw reader (an FFI host handing it to its own kernels): everything t's
+ * values depend on is queued first, as a read through the engine would (the deferred producers; for the
+ * materialised attention's probability tensor, which holds the forward's score blocks across
+ * flush_batch, the probabilities), without waiting; t holds its values once nnhip_engine_stream reaches
+ * this point (nnhip_engine_sync, or work ordered after it on that stream). 0 or an error code. No
+ * reference counterpart (the reference's host reads go through to_matrix, compute_engine.hpp). */
+int nnhip_tensor_device_ptr(nnhip_engine* e, const nnhip_tensor* t, void** out);
 /* Launches every deferred attention call (HipEngine defers the reference's two-pass attention chains
  * and runs each as one fused launch) whose results are still referenced, without waiting. */
 int nnhip_engine_settle(nnhip_engine* e);

@@ -1093,6 +1093,12 @@ Result<void> HipEngine::settle_chain_write_(const Tensor& t, bool keep_swb, bool
     return {};
 }
 
+Result<void> HipEngine::settle_for_read(const Tensor& t)
+{
+    if (!t.is_gpu()) return {};
+    return settle_reads_({&t});
+}
+
 Result<void> HipEngine::settle()
 {
     NN_CHECK(settle_zero_());

@@ -140,6 +140,15 @@ public:
         (void)cols;
         return fail("eval_expr_reduce: not supported by this engine");
     }
+
+    // Queues everything t's values depend on, as a read through the engine
+    // would, without waiting (engines that defer work; others have nothing
+    // to do). No reference counterpart: the reference reads through to_matrix.
+    [[nodiscard]] virtual Result<void> settle_for_read(const Tensor& t)
+    {
+        (void)t;
+        return {};
+    }
 };
 
 } // namespace nn

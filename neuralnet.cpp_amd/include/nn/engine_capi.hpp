@@ -83,6 +83,16 @@ inline void* tensor_data_ptr(const void* h)
     return t->dev_ptr();
 }
 
+// The pointer for a raw reader, once the engine has queued what t's values depend on.
+inline int tensor_device_ptr(EngineHandle* e, const void* h, void** out)
+{
+    if (!e || !h || !out) return set_error("tensor_device_ptr: null argument");
+    auto r = e->eng->settle_for_read(*T(h));
+    if (!r) return set_error(r.error().message);
+    *out = tensor_data_ptr(h);
+    return 0;
+}
+
 inline int engine_op(EngineHandle* e, int op, void* const* in, std::size_t n_in, void** out, std::size_t n_out,
                      const double* a, std::size_t n_args)
 {
@@ -765,6 +775,10 @@ inline int layer_program(const char* name, std::uint32_t param, std::uint8_t* in
     size_t NN_CAPI_CAT(P, tensor_rows)(const void* t) { return nn::capi::T(t)->rows(); }                          \
     size_t NN_CAPI_CAT(P, tensor_cols)(const void* t) { return nn::capi::T(t)->cols(); }                          \
     void* NN_CAPI_CAT(P, tensor_data_ptr)(const void* t) { return nn::capi::tensor_data_ptr(t); }                 \
+    int NN_CAPI_CAT(P, tensor_device_ptr)(void* e, const void* t, void** out)                                      \
+    {                                                                                                               \
+        return nn::capi::tensor_device_ptr(static_cast<nn::capi::EngineHandle*>(e), t, out);                      \
+    }                                                                                                               \
     void NN_CAPI_CAT(P, tensor_release)(void* t) { delete nn::capi::T(t); }                                        \
     int NN_CAPI_CAT(P, engine_op)(void* e, int op, void* const* in, size_t n_in, void** out, size_t n_out,        \
                                   const double* args, size_t n_args)                                                \

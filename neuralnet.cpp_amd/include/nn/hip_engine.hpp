@@ -136,6 +136,11 @@ public:
 
     // Launches every deferred call whose results are still referenced (no wait).
     Result<void> settle();
+    // Queues everything t's values depend on, as a read through the engine
+    // would (the deferred producers, and for an attention probability tensor
+    // that holds the forward's score blocks, the probabilities), without
+    // waiting: t's memory holds its values once the stream reaches this point.
+    Result<void> settle_for_read(const Tensor& t) override;
 
     // Bytes currently cached (free) and held by live tensors in the pool.
     [[nodiscard]] std::size_t pool_cached_bytes() const;

@@ -164,6 +164,16 @@ class Tensor:
     def data_ptr(self) -> int:
         return self._eng._f["tensor_data_ptr"](self._h) or 0
 
+    def device_ptr(self) -> int:
+        """The pointer for a raw reader: everything the values depend on is queued first
+        (nnhip_tensor_device_ptr); the memory holds them once the engine's stream gets there."""
+        f = getattr(self._eng._lib, self._eng._prefix + "tensor_device_ptr")
+        f.restype = ctypes.c_int
+        f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+        out = ctypes.c_void_p()
+        self._eng._check(f(self._eng._e, self._h, ctypes.byref(out)))
+        return out.value or 0
+
     def numpy(self) -> np.ndarray:
         out = np.empty(self.shape, dtype=np.float32)
         self._eng._check(self._eng._f["tensor_to_host"](self._eng._e, self._h, _fptr(out)))
@@ -187,6 +197,7 @@ class Engine:
 
     def __init__(self, lib: Optional[ctypes.CDLL] = None, prefix: str = "nnhip_", handle: Optional[int] = None):
         self._lib = lib if lib is not None else hip_library()
+        self._prefix = prefix
         self._f = _bind(self._lib, prefix)
         if handle is not None:   # an engine already created (create_engine)
             self._e = ctypes.c_void_p(handle)
