@@ -1474,17 +1474,6 @@ __global__ __launch_bounds__(256) void k_flash_rowdot(RowdotSet set, int M, int 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const long t0 = (long)blockIdx.x * 64, t = t0 + lane;
     const int q = Kd / 4, d0 = wave * q;
-    // dO's loads go out first, so that they are in flight with the staging of
-    // O (one memory round trip, not two).
-    const bool live = t < total;
-    const long b = live ? t / M : 0, i = live ? t % M : 0;
-    float pv[16];
-    if (live)
-    {
-        const float* p = dO + (b * Kd + d0) * M + i;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) pv[k] = p[(long)min(k, q - 1) * M];
-    }
     if (o_qm)
     {
         // 64 rows x Kd floats, Kd / 4 per thread; past the last row reads 0.
@@ -1503,14 +1492,17 @@ __global__ __launch_bounds__(256) void k_flash_rowdot(RowdotSet set, int M, int 
         __syncthreads();
     }
     float acc[2] = {0.0f, 0.0f};
-    if (live)
+    if (t < total)
     {
+        const long b = t / M, i = t % M;
+        const float* p = dO + (b * Kd + d0) * M + i;
         const float* od = O + (b * Kd + d0) * M + i;
-        float ov[16];
+        float pv[16], ov[16];
 #pragma unroll
         for (int k = 0; k < 16; ++k)
         {
             const int kc = min(k, q - 1);
+            pv[k] = p[(long)kc * M];
             ov[k] = o_qm ? Ot[lane][d0 + kc] : od[(long)kc * M];
         }
 #pragma unroll
