@@ -164,6 +164,16 @@ typedef struct nnhip_gemv_rmsnorm
     float* normed;        /* (K) */
     float* out;           /* (K): y */
 } nnhip_gemv_rmsnorm;
+/* A token's SwiGLU feed-forward input in one launch (incremental inference; no CUDA counterpart): the
+ * Linear fc1 of 2*half rows on x, or on RMSNorm(x) when rms is set (K <= 1024; the RMSNorm outputs as
+ * nnhip_gemv_group_rmsnorm writes them), v = R x (+ bias), written to y (2*half, may be NULL), then
+ * SwiGLU::forward's chain on gate = v[0, half), up = v[half, 2*half) (compute_layer.hpp:143-154 on a
+ * (2*d_ff, 1) input; its scalar constants c_add = 1 and c_div = 1 as the chain passes them):
+ * s = c_div / (exp(-gate) + c_add) to s_out (may be NULL) and out = (gate * s) * up. Bit-identical to
+ * nnhip_gemv_group[_rmsnorm] of the 2*half rows followed by nnhip_swiglu_forward(y, y + half, s_out, out).
+ * With rms, K % 4 == 0 and R 16-byte aligned. */
+int nnhip_gemv_swiglu(const float* R, const float* x, const nnhip_gemv_rmsnorm* rms, const float* bias, float* y,
+                      float* s_out, float* out, size_t half, size_t K, float c_add, float c_div, void* stream);
 int nnhip_gemv_group_rmsnorm(const float* const* R, const float* x, const nnhip_gemv_rmsnorm* rms,
                              const float* const* bias, float* const* y, const float* const* add, float* const* out,
                              size_t count, size_t rows, size_t K, void* stream);

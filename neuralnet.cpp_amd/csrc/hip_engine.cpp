@@ -257,6 +257,11 @@ bool same_t(const Tensor& a, const Tensor& b)
 }
 bool same_mask(const Tensor* a, const std::optional<Tensor>& b) { return a ? (b && same_t(*a, *b)) : !b; }
 bool has_buf(const Tensor& t, const float* p) { return p && t.dev_ptr() == p; }
+bool in_buf(const Tensor& t, const float* p)
+{
+    const float* b = t.dev_ptr();
+    return p && b && p >= b && p < b + (t.size() ? t.size() : 1);
+}
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 // True when a tensor held by a deferred record is also referenced elsewhere.
 bool live(const Tensor& t) { return t.device_buffer().use_count() > 1; }
@@ -362,10 +367,12 @@ struct HipEngine::PendingMm
     {
         for (const auto& [a, b] : plus)
             if (has_buf(a, p) || has_buf(b, p)) return true;
-        return has_buf(A, p) || has_buf(B, p) || has_buf(C, p) || has_buf(bias, p) || has_buf(out2, p) ||
+        return has_buf(A, p) || has_buf(B, p) || in_buf(C, p) || has_buf(bias, p) || has_buf(out2, p) ||
                has_buf(addx, p);
     }
-    bool yields(const float* p) const { return has_buf(C, p) || has_buf(out2, p); }
+    // Anywhere in C: a row slice of a recorded matrix-vector product (slice_rows
+    // leaves it recorded) is read through a pointer into it.
+    bool yields(const float* p) const { return in_buf(C, p) || has_buf(out2, p); }
     bool needed() const { return live(C) || (out2.size() && live(out2)); }
 };
 
@@ -421,6 +428,10 @@ struct HipEngine::PendingEw
     std::size_t n = 0;   // elements of every tensor in the record
     std::vector<Tensor> slots;
     std::vector<Op> ops;
+    // Some slots are row slices of a recorded matrix-vector product that was
+    // left unlaunched (SwiGLU's gate and up halves of a token's fc1): the
+    // product runs before the record, or with it (swiglu_vec_run_).
+    bool vec_reads = false;
 
     std::uint8_t slot(const Tensor& t)
     {
@@ -1530,7 +1541,16 @@ Result<void> HipEngine::settle_ew_(bool keep_adam)
     }
     const auto st = static_cast<hipStream_t>(stream_);
     const std::size_t n = g->n;
-    for (std::size_t i = 0; i < ops.size();)
+    std::size_t i0 = 0;
+    if (g->vec_reads)
+    {
+        NN_TRY(k, swiglu_vec_run_(*g, last_read));
+        i0 = k;
+        // Any product still recorded whose rows the record reads runs first.
+        for (const Tensor& t : g->slots)
+            if (std::size_t off = 0; vec_slice_of_(t, off)) NN_CHECK(settle_chain_reads_({&t}));
+    }
+    for (std::size_t i = i0; i < ops.size();)
     {
         NN_TRY(k, adam_run_(*g, i, last_read));
         if (k)
@@ -1688,6 +1708,70 @@ Result<std::size_t> HipEngine::swiglu_run_(const PendingEw& g, std::size_t i,
     return kSwigluLen;
 }
 
+// SwiGLU::forward's chain at the start of a record whose gate and up are the
+// two halves of one recorded matrix-vector product (a token's fc1, and its
+// RMSNorm when that is recorded too): both in one nnhip_gemv_swiglu launch,
+// bit-identical to the product's launch followed by nnhip_swiglu_forward.
+Result<std::size_t> HipEngine::swiglu_vec_run_(const PendingEw& g, const std::vector<std::ptrdiff_t>& last_read)
+{
+    int slot_of[kSwigluRoles];
+    if (!match_run_(g, 0, kSwigluSteps, kSwigluLen, kSwigluRoles, slot_of)) return std::size_t{0};
+    const auto end = static_cast<std::ptrdiff_t>(kSwigluLen);
+    for (int r : {sT1, sT2, sT3, sSW})
+        if (live(g.slots[slot_of[r]]) || last_read[slot_of[r]] >= end) return std::size_t{0};
+    const Tensor& G = g.slots[slot_of[sG]];
+    const Tensor& U = g.slots[slot_of[sU]];
+    std::size_t og = 0, ou = 0;
+    PendingMm* r = vec_slice_of_(G, og);
+    if (!r || vec_slice_of_(U, ou) != r || og != 0 || ou != G.size() || r->M != 2 * G.size() || g.n != G.size())
+        return std::size_t{0};
+    // Products of the same input launch together (launch_pending_mm_): not folded then.
+    auto partner = [&](const std::unique_ptr<PendingMm>& q) {
+        return q && q.get() != r && q->N == 1 && same_t(q->B, r->B);
+    };
+    if (partner(pmm_)) return std::size_t{0};
+    for (const auto& q : pmm_prev_)
+        if (partner(q)) return std::size_t{0};
+    const bool rms = prms_ && !prms_->bwd && prms_->stage == 6 && same_t(prms_->y, r->B) && r->K <= 1024 &&
+                     r->K % 4 == 0 && aligned16(D(r->A));
+    std::unique_ptr<PendingMm> o;
+    if (pmm_.get() == r)
+        o = std::move(pmm_);
+    else
+        for (std::size_t i = 0; i < pmm_prev_.size(); ++i)
+            if (pmm_prev_[i].get() == r)
+            {
+                o = std::move(pmm_prev_[i]);
+                pmm_prev_.erase(pmm_prev_.begin() + static_cast<std::ptrdiff_t>(i));
+                break;
+            }
+    if (merge_of_(o->A)) NN_CHECK(settle_chain_reads_({&o->A}));
+    const Tensor& S = g.slots[slot_of[sS]];
+    const bool keep_s = live(S) || last_read[slot_of[sS]] >= end;
+    float* y = live(o->C) ? W(o->C) : nullptr;
+    const float* bias = o->bias.size() ? D(o->bias) : nullptr;
+    const auto st = static_cast<hipStream_t>(stream_);
+    prof_begin_();
+    int rc = 0;
+    if (rms)
+    {
+        std::unique_ptr<PendingRms> q = std::move(prms_);
+        const nnhip_gemv_rmsnorm rn{D(q->gamma), q->inv_f, q->eps, W(q->s), W(q->scaled), W(q->var_eps),
+                                    W(q->rinv), W(q->normed), W(q->y)};
+        rc = nnhip_gemv_swiglu(D(o->A), D(q->x), &rn, bias, y, keep_s ? W(S) : nullptr, W(g.slots[slot_of[sO]]),
+                               G.size(), o->K, g.ops[2].s, g.ops[3].s, st);
+    }
+    else
+    {
+        NN_CHECK(settle_chain_reads_({&o->B}));
+        rc = nnhip_gemv_swiglu(D(o->A), D(o->B), nullptr, bias, y, keep_s ? W(S) : nullptr,
+                               W(g.slots[slot_of[sO]]), G.size(), o->K, g.ops[2].s, g.ops[3].s, st);
+    }
+    prof_end_(o->M, 1, o->K, 1, false, false);
+    NN_CHECK(kernel_(rc, "matmul + swiglu (vector)"));
+    return kSwigluLen;
+}
+
 Result<Tensor> HipEngine::alloc_(std::size_t rows, std::size_t cols)
 {
     const std::size_t n = rows * cols;
@@ -1841,7 +1925,16 @@ Result<Tensor> HipEngine::clone(const Tensor& src)
 // Returns a view of src's rows (see unshare_); views of views share the root.
 Result<Tensor> HipEngine::slice_rows(const Tensor& src, std::size_t start, std::size_t count)
 {
-    NN_CHECK(need_gpu_({&src}, "slice_rows"));
+    // A recorded matrix-vector product stays recorded (a read through the
+    // slice launches it: PendingMm::yields covers its whole output), so that
+    // SwiGLU's chain on a token's fc1 halves can run with it (swiglu_vec_run_).
+    if (vec_record_(src))
+    {
+        NN_CHECK(check_gpu_({&src}, "slice_rows"));
+        NN_CHECK(settle_ew_());
+    }
+    else
+        NN_CHECK(need_gpu_({&src}, "slice_rows"));
     if (start + count > src.rows()) return fail("slice_rows: range out of bounds");
     const std::size_t n = count * src.cols();
     if (!n) return alloc_(count, src.cols());
@@ -1879,6 +1972,9 @@ Result<void> HipEngine::unshare_(const Tensor& t)
     if (views_.empty()) return {};
     const DeviceBuffer* b = t.device_buffer().get();
     if (!b || !view_keys_.count(b)) return {};   // neither a view nor the memory of one
+    // A recorded matrix-vector product may still produce the memory (slice_rows
+    // leaves it recorded): it runs before the copies are taken.
+    NN_CHECK(settle_chain_reads_({&t}));
     auto take_copy = [&](HipView& v) -> Result<void> {
         const std::size_t n = v.capacity();
         NN_TRY(own, alloc_(1, n));
@@ -3025,6 +3121,24 @@ HipEngine::PendingMm* HipEngine::vec_record_(const Tensor& t)
     return nullptr;
 }
 
+// The recorded matrix-vector product (as vec_record_) whose output t is a row
+// slice of, with t's offset in it (in floats).
+HipEngine::PendingMm* HipEngine::vec_slice_of_(const Tensor& t, std::size_t& off)
+{
+    const auto* v = dynamic_cast<const HipView*>(t.device_buffer().get());
+    if (!v || !v->aliased() || t.cols() != 1) return nullptr;
+    auto ok = [&](PendingMm* r) {
+        return r && !r->folded && r->N == 1 && r->M > 1 && !r->tA && !r->tB && r->plus.empty() && !r->heads.size() &&
+               !r->out2.size() && r->A.cols() == r->K && r->B.cols() == 1 &&
+               r->C.device_buffer().get() == v->root();
+    };
+    PendingMm* r = ok(pmm_.get()) ? pmm_.get() : nullptr;
+    for (std::size_t i = 0; !r && i < pmm_prev_.size(); ++i)
+        if (ok(pmm_prev_[i].get())) r = pmm_prev_[i].get();
+    if (r) off = v->offset();
+    return r;
+}
+
 // The recorded, not yet folded plain product whose output is t, if any.
 HipEngine::PendingMm* HipEngine::pending_mm_(const Tensor& t)
 {
@@ -3258,6 +3372,17 @@ Result<Tensor> HipEngine::elementwise_unary(UnaryOp op, const Tensor& A)
         prms_->stage = 4;
         return o;
     }
+    // SwiGLU::forward's first call on the gate half of a token's recorded fc1
+    // product: the product stays recorded (swiglu_vec_run_ may run it with
+    // the chain); the record starts here.
+    if (std::size_t off = 1; op == UnaryOp::Neg && A.size() && vec_slice_of_(A, off) && off == 0)
+    {
+        if (pew_) NN_CHECK(settle_ew_(true));
+        NN_TRY(o, alloc_(A.rows(), A.cols()));
+        NN_CHECK(ew_push_(kUnary, static_cast<unsigned>(op), false, o, A, nullptr, 0.0f));
+        pew_->vec_reads = true;
+        return o;
+    }
     NN_CHECK(settle_chain_reads_({&A}));
     NN_TRY(o, alloc_(A.rows(), A.cols()));
     if (A.size()) NN_CHECK(ew_push_(kUnary, static_cast<unsigned>(op), false, o, A, nullptr, 0.0f));
@@ -3322,6 +3447,21 @@ Result<Tensor> HipEngine::elementwise_binary(BinaryOp op, const Tensor& A, const
             const PendingGemm& g = *pgemm_;
             NN_TRY(o, alloc_(A.rows(), A.cols()));
             pmadd_ = std::make_unique<PendingMaskAdd>(PendingMaskAdd{g.A, g.B, B, o, g.batch, g.M, g.N, g.K, g.alpha});
+            return o;
+        }
+    }
+    // The chain's products with the gate or up half (see elementwise_unary).
+    if (op == BinaryOp::Mul && A.size() && pew_ && pew_->vec_reads)
+    {
+        std::size_t off = 0;
+        const bool va = vec_slice_of_(A, off) != nullptr, vb = vec_slice_of_(B, off) != nullptr;
+        if (va || vb)
+        {
+            if (!va) NN_CHECK(settle_chain_reads_({&A}));
+            if (!vb) NN_CHECK(settle_chain_reads_({&B}));
+            NN_TRY(o, alloc_(A.rows(), A.cols()));
+            NN_CHECK(ew_push_(kBin, static_cast<unsigned>(op), false, o, A, &B, 0.0f));
+            pew_->vec_reads = true;
             return o;
         }
     }

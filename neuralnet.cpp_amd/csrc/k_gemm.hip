@@ -978,9 +978,98 @@ struct GemvGroup
 // A launch is a few memory latencies long, so every load that does not depend
 // on another is issued before the first wait: the epilogue's bias and
 // residual, and with RMS (VEC, K <= 1024: one float4 trip per lane, U = 4)
-// x and gamma first, then the row. Waits on the vector-memory counter are in
-// issue order, so the prologue waits for x and gamma only while the row's
+// x and gamma first, then the rows. Waits on the vector-memory counter are in
+// issue order, so the prologue waits for x and gamma only while the rows'
 // loads stay in flight.
+struct RmsLoads
+{
+    float v[4], gm[4];
+};
+__device__ __forceinline__ void rms_load(const float* __restrict__ x, const float* __restrict__ gamma, int K,
+                                         RmsLoads& r)
+{
+    const unsigned t = threadIdx.x;
+#pragma unroll
+    for (unsigned k = 0; k < 4; ++k)
+    {
+        const unsigned i = t + k * 256;
+        r.v[k] = i < static_cast<unsigned>(K) ? x[i] : 0.0f;
+        r.gm[k] = i < static_cast<unsigned>(K) ? gamma[i] : 0.0f;
+    }
+}
+// The normalised vector into xs (LDS, K <= 1024 floats); ends with a barrier.
+__device__ __forceinline__ void rms_finish(const RmsLoads& r, int K, const nnhip_gemv_rmsnorm& rn, float* xs,
+                                           float* part, bool first)
+{
+    const unsigned t = threadIdx.x, lane = t % 64, wave = t / 64;
+    float ss = 0.0f;
+#pragma unroll
+    for (unsigned k = 0; k < 4; ++k)
+        if (t + k * 256 < static_cast<unsigned>(K)) ss = __builtin_fmaf(r.v[k], r.v[k], ss);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    float sum = part[0];
+#pragma unroll
+    for (unsigned w = 1; w < 4; ++w) sum += part[w];
+    float ri;
+    {
+#pragma clang fp contract(off)
+        const float sc = sum * rn.inv_f, ve = sc + rn.eps;
+        ri = 1.0f / sqrtf(ve);
+        if (first && t == 0)
+        {
+            if (rn.s_raw) rn.s_raw[0] = sum;
+            if (rn.scaled) rn.scaled[0] = sc;
+            if (rn.var_eps) rn.var_eps[0] = ve;
+            if (rn.rinv) rn.rinv[0] = ri;
+        }
+    }
+#pragma unroll
+    for (unsigned k = 0; k < 4; ++k)
+    {
+        const unsigned i = t + k * 256;
+        if (i < static_cast<unsigned>(K))
+        {
+#pragma clang fp contract(off)
+            const float n = r.v[k] * ri, y = n * r.gm[k];
+            xs[i] = y;
+            if (first)
+            {
+                if (rn.normed) rn.normed[i] = n;
+                if (rn.out) rn.out[i] = y;
+            }
+        }
+    }
+    __syncthreads();
+}
+// One row's float4s for the RMS path's single trip (lane + 64 u, u < 4).
+__device__ __forceinline__ void row_load4(const float* __restrict__ row, int K4, unsigned lane, bool live, float4* a)
+{
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (live && static_cast<int>(lane) + 64 * u < K4) a[u] = r4[lane + 64 * u];
+}
+// gemv_row's sums for that trip: float4 lane + 64 u in the order of u, then the wave's sum.
+__device__ __forceinline__ float row_dot4(const float4* a, const float* xs, int K4, unsigned lane)
+{
+    const float4* x4 = reinterpret_cast<const float4*>(xs);
+    float d = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (static_cast<int>(lane) + 64 * u < K4)
+        {
+            const float4 xv4 = x4[lane + 64 * u];
+            d = __builtin_fmaf(a[u].x, xv4.x, d);
+            d = __builtin_fmaf(a[u].y, xv4.y, d);
+            d = __builtin_fmaf(a[u].z, xv4.z, d);
+            d = __builtin_fmaf(a[u].w, xv4.w, d);
+        }
+    return wave_sum(d);
+}
+
 template <bool VEC, int U, bool RMS>
 __global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __restrict__ x, int rows, int K,
                                                     nnhip_gemv_rmsnorm rn)
@@ -1003,84 +1092,15 @@ __global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __
         static_assert(!VEC || U == 4, "the RMS prologue's row covers K <= 1024 in one trip");
         __shared__ __align__(16) float xs[1024];
         __shared__ float part[4];
-        const unsigned t = threadIdx.x;
-        float v[4], gm[4];
-#pragma unroll
-        for (unsigned k = 0; k < 4; ++k)
-        {
-            const unsigned r = t + k * 256;
-            v[k] = r < static_cast<unsigned>(K) ? x[r] : 0.0f;
-            gm[k] = r < static_cast<unsigned>(K) ? rn.gamma[r] : 0.0f;
-        }
+        RmsLoads rl;
+        rms_load(x, rn.gamma, K, rl);
         const int K4 = K / 4;
-        const float4* r4 = reinterpret_cast<const float4*>(g.R[m] + (long)i * K);
         float4 a[4];
-        if constexpr (VEC)
-        {
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (live && static_cast<int>(lane) + 64 * u < K4) a[u] = r4[lane + 64 * u];
-        }
-        float ss = 0.0f;
-#pragma unroll
-        for (unsigned k = 0; k < 4; ++k)
-            if (t + k * 256 < static_cast<unsigned>(K)) ss = __builtin_fmaf(v[k], v[k], ss);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if (lane == 0) part[wave] = ss;
-        __syncthreads();
-        float sum = part[0];
-#pragma unroll
-        for (unsigned w = 1; w < 4; ++w) sum += part[w];
-        const bool first = blockIdx.x == 0 && blockIdx.y == 0;
-        float ri;
-        {
-#pragma clang fp contract(off)
-            const float sc = sum * rn.inv_f, ve = sc + rn.eps;
-            ri = 1.0f / sqrtf(ve);
-            if (first && t == 0)
-            {
-                if (rn.s_raw) rn.s_raw[0] = sum;
-                if (rn.scaled) rn.scaled[0] = sc;
-                if (rn.var_eps) rn.var_eps[0] = ve;
-                if (rn.rinv) rn.rinv[0] = ri;
-            }
-        }
-#pragma unroll
-        for (unsigned k = 0; k < 4; ++k)
-        {
-            const unsigned r = t + k * 256;
-            if (r < static_cast<unsigned>(K))
-            {
-#pragma clang fp contract(off)
-                const float n = v[k] * ri, y = n * gm[k];
-                xs[r] = y;
-                if (first)
-                {
-                    if (rn.normed) rn.normed[r] = n;
-                    if (rn.out) rn.out[r] = y;
-                }
-            }
-        }
-        __syncthreads();
+        if constexpr (VEC) row_load4(g.R[m] + (long)i * K, K4, lane, live, a);
+        rms_finish(rl, K, rn, xs, part, blockIdx.x == 0 && blockIdx.y == 0);
         if (!live) return;
         if constexpr (VEC)
-        {
-            // gemv_row's sums for one trip: float4 lane + 64 u in the order of u, then the wave's sum.
-            const float4* x4 = reinterpret_cast<const float4*>(xs);
-            float d = 0.0f;
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (static_cast<int>(lane) + 64 * u < K4)
-                {
-                    const float4 xv4 = x4[lane + 64 * u];
-                    d = __builtin_fmaf(a[u].x, xv4.x, d);
-                    d = __builtin_fmaf(a[u].y, xv4.y, d);
-                    d = __builtin_fmaf(a[u].z, xv4.z, d);
-                    d = __builtin_fmaf(a[u].w, xv4.w, d);
-                }
-            acc = wave_sum(d);
-        }
+            acc = row_dot4(a, xs, K4, lane);
         else
             acc = gemv_row<VEC, U>(g.R[m] + (long)i * K, xs, K, lane);
     }
@@ -1096,6 +1116,80 @@ __global__ __launch_bounds__(256) void k_gemv_group(GemvGroup g, const float* __
         if (bias) v = v + bv;
         if (g.y[m]) g.y[m][i] = v;
         if (g.out[m]) g.out[m][i] = add ? av + v : v;
+    }
+}
+
+// A Linear of 2h rows whose output feeds SwiGLU (a token's fc1, then
+// SwiGLU::forward's chain on its gate rows [0, h) and up rows [h, 2h)): wave
+// i forms rows i and h + i as k_gemv_group does (the same sums, bias added
+// the same way; y = both rows when set) and then the chain's values from
+// them as k_swiglu_fwd forms them, s = c_div / (exp(-gate) + c_add) (when
+// s_out is set) and out = (gate * s) * up. K % 4 == 0, K <= 1024 with RMS.
+struct GemvSwiglu
+{
+    const float* R;
+    const float* bias;
+    float* y;
+    float* s_out;
+    float* out;
+    int half, K;
+    float c_add, c_div;
+};
+template <bool VEC, int U, bool RMS>
+__global__ __launch_bounds__(256) void k_gemv_swiglu(GemvSwiglu g, const float* __restrict__ x, nnhip_gemv_rmsnorm rn)
+{
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int i = blockIdx.x * 4 + static_cast<int>(wave);
+    const bool live = i < g.half;
+    const int K = g.K;
+    const float* rg = g.R + (long)i * K;
+    const float* ru = g.R + (long)(g.half + i) * K;
+    float bg = 0.0f, bu = 0.0f;
+    if (live && lane == 0 && g.bias)
+    {
+        bg = g.bias[i];
+        bu = g.bias[g.half + i];
+    }
+    float accg, accu;
+    if constexpr (RMS)
+    {
+        static_assert(VEC && U == 4, "the RMS prologue's rows cover K <= 1024 in one trip");
+        __shared__ __align__(16) float xs[1024];
+        __shared__ float part[4];
+        RmsLoads rl;
+        rms_load(x, rn.gamma, K, rl);
+        const int K4 = K / 4;
+        float4 a[4], b[4];
+        row_load4(rg, K4, lane, live, a);
+        row_load4(ru, K4, lane, live, b);
+        rms_finish(rl, K, rn, xs, part, blockIdx.x == 0);
+        if (!live) return;
+        accg = row_dot4(a, xs, K4, lane);
+        accu = row_dot4(b, xs, K4, lane);
+    }
+    else
+    {
+        if (!live) return;
+        accg = gemv_row<VEC, U>(rg, x, K, lane);
+        accu = gemv_row<VEC, U>(ru, x, K, lane);
+    }
+    if (lane == 0)
+    {
+#pragma clang fp contract(off)
+        float vg = 1.0f * accg, vu = 1.0f * accu;
+        if (g.bias)
+        {
+            vg = vg + bg;
+            vu = vu + bu;
+        }
+        if (g.y)
+        {
+            g.y[i] = vg;
+            g.y[g.half + i] = vu;
+        }
+        const float sv = g.c_div / (expf(-vg) + g.c_add);
+        if (g.s_out) g.s_out[i] = sv;
+        g.out[i] = (vg * sv) * vu;
     }
 }
 
@@ -1649,6 +1743,35 @@ extern "C" int nnhip_gemv_group(const float* const* R, const float* x, const flo
                                 void* stream)
 {
     return gemv_group(R, x, nullptr, bias, y, add, out, count, rows, K, stream);
+}
+
+// fc1 (2 half rows) of x or of RMSNorm(x), and SwiGLU::forward's chain on its
+// two halves, in one launch: bit-identical to nnhip_gemv_group[_rmsnorm] of
+// the 2 half rows followed by nnhip_swiglu_forward(y, y + half, s, out).
+extern "C" int nnhip_gemv_swiglu(const float* R, const float* x, const nnhip_gemv_rmsnorm* rms, const float* bias,
+                                 float* y, float* s_out, float* out, size_t half, size_t K, float c_add, float c_div,
+                                 void* stream)
+{
+    if (half == 0) return 0;
+    if (!R || !x || !out || K == 0 || K > 0x7fffffff || half > 0x3fffffff) return -1;
+    if (rms && (K > 1024 || !rms->gamma)) return -1;
+    const bool vec = K % 4 == 0 && (rms || aligned16(x)) && aligned16(R);
+    if (rms && !vec) return -1;
+    GemvSwiglu g{R, bias, y, s_out, out, static_cast<int>(half), static_cast<int>(K), c_add, c_div};
+    const nnhip_gemv_rmsnorm rn = rms ? *rms : nnhip_gemv_rmsnorm{};
+    auto s = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>((half + 3) / 4));
+    if (rms)
+        hipLaunchKernelGGL((k_gemv_swiglu<true, 4, true>), grid, dim3(256), 0, s, g, x, rn);
+    else if (vec && K <= 1024)
+        hipLaunchKernelGGL((k_gemv_swiglu<true, 4, false>), grid, dim3(256), 0, s, g, x, rn);
+    else if (vec && K <= 2048)
+        hipLaunchKernelGGL((k_gemv_swiglu<true, 8, false>), grid, dim3(256), 0, s, g, x, rn);
+    else if (vec)
+        hipLaunchKernelGGL((k_gemv_swiglu<true, 16, false>), grid, dim3(256), 0, s, g, x, rn);
+    else
+        hipLaunchKernelGGL((k_gemv_swiglu<false, 1, false>), grid, dim3(256), 0, s, g, x, rn);
+    return launch_status();
 }
 
 // The same products of RMSNorm(x) (a (K, 1) column, K <= 1024).

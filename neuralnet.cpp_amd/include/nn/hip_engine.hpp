@@ -247,6 +247,7 @@ private:
     Result<void> launch_mm_(const PendingMm& r, const Tensor& out, const Tensor* bias, bool accumulate);
     PendingMm* pending_mm_(const Tensor& t);
     PendingMm* vec_record_(const Tensor& t);
+    PendingMm* vec_slice_of_(const Tensor& t, std::size_t& off);
     struct PendingAcc;
     std::unique_ptr<PendingAcc> pacc_;
     Result<void> settle_acc_();
@@ -341,6 +342,7 @@ private:
     Result<void> flush_adam_();
     Result<std::size_t> adam_run_(const PendingEw& g, std::size_t i, const std::vector<std::ptrdiff_t>& last_read);
     Result<std::size_t> swiglu_run_(const PendingEw& g, std::size_t i, const std::vector<std::ptrdiff_t>& last_read);
+    Result<std::size_t> swiglu_vec_run_(const PendingEw& g, const std::vector<std::ptrdiff_t>& last_read);
     static bool match_run_(const PendingEw& g, std::size_t i, const RunStep* steps, std::size_t len, int nroles,
                            int* slot_of);
     Result<void> settle_fwd_();
